@@ -1,0 +1,184 @@
+/*
+ * lrq.h — C ABI of the MI355X (gfx950) compressed-activation library (liblrq.so).
+ *
+ * The reference (Ther-nullptr/Triton-Kernel-Test) exposes this path as Python functions
+ * over torch CUDA tensors that launch Triton kernels.  Each entry point below replaces one
+ * of those launches; the reference function it stands in for is cited beside it.  The
+ * Python package `triton-kernel-test_amd` keeps the reference's function names and
+ * calls these through ctypes.
+ *
+ * Conventions (every entry point):
+ *   - Pointers are device pointers (HBM) unless stated; dimensions and leading
+ *     dimensions are int64 element counts; matrices are row-major.
+ *   - bf16 / fp16 tensors are passed as raw 16-bit storage.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream).  Work is enqueued
+ *     asynchronously; nothing synchronises the host.
+ *   - No entry point allocates device memory.  Outputs and workspaces come from the
+ *     caller.  No global mutable state is kept: calls are reentrant and thread-safe.
+ *   - Return value: LRQ_OK (0) on success; a negative LRQ_ERR_* when an argument is
+ *     invalid — always detected on the host BEFORE any HIP call, so these paths can be
+ *     exercised without a GPU; a positive hipError_t if a launch fails.
+ *
+ * Compressed format ("group mode", the north-star format).  An activation X[rows, hidden]
+ * (bf16) is stored as
+ *     L      bf16  [rows, rank]          projection coefficients, L = bf16(Y V)
+ *     codes  uint8 [rows, hidden*bits/8] residual codes, row-planar packing: byte j of a
+ *                                        row holds column j + i*hidden*bits/8 in bits
+ *                                        [bits*i, bits*i + bits)
+ *     scale  fp16  [rows, hidden/group]  per-group step
+ *     zero   fp16  [rows, hidden/group]  per-group minimum
+ *     side   fp16  [rows, n_outlier]     outlier channels kept dense (optional)
+ *     idx    int32 [n_outlier]           their column indices, ascending (optional)
+ * where Y = X (or its blockwise 128-point Walsh-Hadamard rotation) and V[hidden, rank] is
+ * an orthonormal basis supplied by the caller.
+ */
+#ifndef LRQ_H
+#define LRQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LRQ_OK 0
+#define LRQ_ERR_NULL (-1)        /* a required pointer is NULL                         */
+#define LRQ_ERR_SHAPE (-2)       /* a dimension or leading dimension is invalid        */
+#define LRQ_ERR_UNSUPPORTED (-3) /* bits / group / rank / flag combination not built    */
+#define LRQ_ERR_ALIGN (-4)       /* pointer or leading dimension misaligned             */
+#define LRQ_ERR_WORKSPACE (-5)   /* caller workspace too small                          */
+
+#define LRQ_FLAG_HADAMARD 1 /* rotate by the blockwise normalised WHT-128 before compression */
+
+/* Descriptor of one compressed activation.  Encode writes L/codes/scale/zero/side;
+ * decode-side entry points read them.  Unused fields may be NULL / 0. */
+typedef struct lrq_tensors {
+  int64_t rows, hidden;
+  int32_t rank;  /* 0, 16 or 32 */
+  int32_t bits;  /* 4 or 8 */
+  int32_t group; /* 64 or 128 (multiple of 32) */
+  int32_t flags; /* LRQ_FLAG_* */
+  void* L;
+  int64_t ld_L;
+  const void* V;  /* bf16 [hidden, rank] */
+  const void* Vt; /* bf16 [rank, hidden] (encode only; lrq_transpose_bf16 builds it) */
+  void* codes;
+  int64_t ld_codes;
+  void* scale;
+  void* zero;
+  int64_t ld_sz;
+  const int32_t* outlier_idx;
+  int32_t n_outlier;
+  void* side;
+  int64_t ld_side;
+} lrq_tensors;
+
+/* ------------------------------------------------------------------ group mode */
+
+/* Encode X[rows, hidden] (bf16, leading dim ldx) into `t`.
+ * Replaces low_rank_addition_fuse_compression_quantization
+ * (low_rank_extraction_fuse_compression_quantization.py:118-150, kernel :13-115) in the
+ * north-star format: projection, residual, per-group quantisation and packing in one pass
+ * over X when hidden has a single-pass kernel, otherwise two passes. */
+int lrq_encode(const lrq_tensors* t, const void* x, int64_t ldx, void* stream);
+
+/* Same result as lrq_encode, always through the two-pass kernels (projection pass, then
+ * residual/quantisation pass).  Diagnostic and test hook; no reference counterpart. */
+int lrq_encode_twopass(const lrq_tensors* t, const void* x, int64_t ldx, void* stream);
+
+/* Decode `t` into out[rows, hidden] bf16.
+ * Replaces low_rank_addition_fuse_decompression_dequantization
+ * (low_rank_extraction_fuse_decompression_dequantization.py:116-152, kernel :13-113). */
+int lrq_decode(const lrq_tensors* t, void* out, int64_t ldo, void* stream);
+
+/* dx = dy * s(x)(1 + x(1 - s(x))), s = sigmoid, x = decode(t), fused.
+ * Replaces triton_silu_backward_fuse_extraction (extraction_fuse_silu_backward.py:192-216). */
+int lrq_silu_bwd(const lrq_tensors* t, const void* dy, int64_t lddy, void* dx, int64_t lddx, void* stream);
+
+/* dx = tanh-GELU'(x) * dy, x = decode(t), fused (gelu_backward.py:14-21 formula; the reference
+ * has only the uncompressed triton_gelu_backward, gelu_backward.py:73-88). */
+int lrq_gelu_bwd(const lrq_tensors* t, const void* dy, int64_t lddy, void* dx, int64_t lddx, void* stream);
+
+/* out = decode(t) * y elementwise.
+ * Replaces triton_hadamard_fuse_extraction (extraction_fuse_hadamard.py:185-209). */
+int lrq_mul(const lrq_tensors* t, const void* y, int64_t ldy, void* out, int64_t ldo, void* stream);
+
+/* ds = p * (dp - rowsum(dp * p)), p = decode(t) (rows = softmax rows), fused with the row sum
+ * (softmax_backward.py:6-7 formula; the reference has only the uncompressed
+ * triton_softmax_backward, softmax_backward.py:45-61). */
+int lrq_softmax_bwd(const lrq_tensors* t, const void* dp, int64_t lddp, void* ds, int64_t ldds,
+                    void* stream);
+
+/* out[rows, n_out] = decode(t) @ a[hidden, n_out] (a bf16 row-major), fp32 accumulate;
+ * out is fp32 when out_fp32 != 0, else bf16.
+ * Replaces triton_matmul_decompress (extraction_fuse_matmul.py:224-249). */
+int lrq_dequant_gemm(const lrq_tensors* t, const void* a, int32_t n_out, void* out, int64_t ldo,
+                     int32_t out_fp32, void* stream);
+
+/* colmax[c] = max_r |x[r, c]| (fp32).  First half of the outlier-channel split
+ * (no reference counterpart; the reference's channel split takes caller indices,
+ * extraction_outlier_channel.py:11-14). */
+int lrq_colmax(const void* x, int64_t ldx, int64_t rows, int64_t hidden, float* colmax, void* stream);
+
+/* idx = the k columns with the largest colmax, ascending; ties toward the lower index. */
+int lrq_topk(const float* colmax, int64_t hidden, int32_t k, int32_t* idx, void* stream);
+
+/* dst[cols, rows] = src[rows, cols]^T for bf16 (builds Vt from V, and V-layout from the
+ * reference's r[K, N] factor). */
+int lrq_transpose_bf16(const void* src, int64_t rows, int64_t cols, void* dst, void* stream);
+
+/* ------------------------------------------------------------------ legacy mode
+ * The reference's own formulation: caller-supplied factors l[M, K] (bf16) and r as
+ * rt[N, K] (= r^T, bf16), per-column symmetric scale s[S, N] (bf16; batch b uses row
+ * b % S), threshold outliers kept as a dense bf16 tensor, row-planar packing.  x is
+ * [B, M, N] bf16 with leading dims (ldx_b, ldx_m); row-major in N.  Arithmetic follows
+ * the reference's torch forms, bf16 rounding after each op. */
+
+/* Replaces low_rank_addition_fuse_compression_quantization
+ * (low_rank_extraction_fuse_compression_quantization.py:118-150; torch form :153-171).
+ * o[B, M, N] receives the dense outliers (bf16), q[B, M, N*bits/8] the codes. */
+int lrq_legacy_encode(const void* l, const void* rt, int32_t K, const void* x, int64_t B, int64_t M,
+                      int64_t N, int64_t ldx_b, int64_t ldx_m, const void* s, int64_t s_rows,
+                      int32_t bits, float outlier, void* o, void* q, void* stream);
+
+/* Replaces low_rank_addition_fuse_decompression_dequantization
+ * (low_rank_extraction_fuse_decompression_dequantization.py:116-152; torch form :155-165).
+ * o may be NULL (no outliers).  out[B, M, N] bf16. */
+int lrq_legacy_decode(const void* l, const void* rt, int32_t K, const void* q, const void* o,
+                      const void* s, int64_t s_rows, int64_t B, int64_t M, int64_t N, int32_t bits,
+                      void* out, void* stream);
+
+/* Fused legacy consumers (no outliers): op = 0 store x_hat, 1 SiLU backward with y as dy
+ * (extraction_fuse_silu_backward.py:192-216), 2 elementwise product with y
+ * (extraction_fuse_hadamard.py:185-209).  y, out: [B, M, N] bf16 contiguous. */
+int lrq_legacy_fused(const void* l, const void* rt, int32_t K, const void* q, const void* s,
+                     int64_t s_rows, int64_t B, int64_t M, int64_t N, int32_t bits, int32_t op,
+                     const void* y, void* out, void* stream);
+
+/* out = x + l @ r (bf16 semantics of torch_low_rank_addition).
+ * Replaces low_rank_addition (low_rank_extraction_speed.py:77-103). */
+int lrq_lowrank_add(const void* l, const void* rt, int32_t K, const void* x, int64_t B, int64_t M,
+                    int64_t N, void* out, void* stream);
+
+/* ------------------------------------------------------------------ dense consumers
+ * Uncompressed elementwise kernels over n contiguous bf16 elements.
+ * op: 0 SiLU bwd (triton_silu_backward, silu_backward.py:54-69),
+ *     1 GELU bwd (triton_gelu_backward, gelu_backward.py:73-88),
+ *     2 product  (triton_hadamard, extraction_fuse_hadamard.py:62-73). */
+int lrq_dense_elementwise(int32_t op, const void* x, const void* y, void* out, int64_t n, void* stream);
+
+/* ds = y * (g - rowsum(g * y)) over rows of length n_cols, contiguous bf16.
+ * Replaces triton_softmax_backward (softmax_backward.py:45-61). */
+int lrq_dense_softmax_bwd(const void* y, const void* g, void* out, int64_t rows, int64_t n_cols,
+                          void* stream);
+
+/* ------------------------------------------------------------------ misc */
+const char* lrq_status_string(int status);
+int32_t lrq_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LRQ_H */

@@ -1,0 +1,80 @@
+"""Comparators for HIP-vs-oracle parity (test infrastructure).
+
+Bars:
+  * packed codes, scales, zeros, index sets: bit-exact, except rounding-tie flips, which
+    must stay under 1e-4 of codes;
+  * fused floating-point outputs: max-abs <= 1e-2 and relative-L2 <= 1e-3 against the
+    oracle's decompress-then-op result (formula in float64 on the bf16 x_hat, rounded
+    once to bf16).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+import oracle as O
+
+TIE_BUDGET = 1e-4
+MAX_ABS = 1e-2
+REL_L2 = 1e-3
+
+
+def bits16(t: torch.Tensor) -> np.ndarray:
+    """bf16/fp16 tensor -> uint16 bit patterns (numpy)."""
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def f16(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().numpy().astype(np.float16)
+
+
+def from_bits(a: np.ndarray, device) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).to(device)
+
+
+def ulp_diff_bf16(a_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
+    """|a - b| in bf16 ulps via the ordered integer mapping of the bit patterns."""
+    def ordered(u):
+        u = u.astype(np.int32)
+        return np.where(u & 0x8000, 0x8000 - (u & 0x7FFF), u + 0x8000)
+    return np.abs(ordered(a_bits) - ordered(b_bits))
+
+
+def code_mismatch_report(gpu_packed: np.ndarray, ref: dict, bits: int) -> dict:
+    """Compare packed codes with the oracle's; classify mismatches.
+
+    A mismatch is a tie flip when the codes differ by one and the oracle's pre-rounding
+    value t lies within 1e-3 of the half-integer between them (fp32 reassociation inside
+    the MFMA can move t by a few ulps)."""
+    g = O.unpack_rowplanar(gpu_packed, bits).astype(np.int32)
+    r = ref["codes_unpacked"].astype(np.int32)
+    mism = g != r
+    n = mism.sum()
+    t = ref["t"]
+    near_tie = np.abs(np.abs(t - np.floor(t)) - 0.5) < 1e-3
+    tie = mism & (np.abs(g - r) == 1) & (near_tie | (t < 0) | (t > (1 << bits) - 1))
+    return dict(n=int(g.size), mismatches=int(n), tie_flips=int(tie.sum()), other=int((mism & ~tie).sum()),
+                frac=float(n) / g.size)
+
+
+def assert_codes(gpu_packed, ref, bits, budget=TIE_BUDGET, what="codes"):
+    rep = code_mismatch_report(np.asarray(gpu_packed), ref, bits)
+    assert rep["frac"] <= budget, f"{what}: {rep}"
+    return rep
+
+
+def assert_fp_close(gpu_bits: np.ndarray, ref_f64: np.ndarray, what: str,
+                    max_abs=MAX_ABS, rel_l2=REL_L2) -> dict:
+    """Fused output (bf16 bits) vs the float64 oracle result: max-abs and rel-L2 bars, plus
+    the bf16 ulp-flip count against the once-rounded oracle."""
+    g = O.bf16_to_f32(gpu_bits).astype(np.float64)
+    ref_rounded = O.bf16_to_f32(O.round_out(ref_f64)).astype(np.float64)
+    diff = g - ref_rounded
+    mx = float(np.abs(diff).max()) if diff.size else 0.0
+    den = float(np.linalg.norm(ref_rounded)) or 1.0
+    rl2 = float(np.linalg.norm(diff)) / den
+    flips = int((ulp_diff_bf16(gpu_bits, O.round_out(ref_f64)) > 0).sum())
+    rep = dict(max_abs=mx, rel_l2=rl2, ulp_flips=flips, n=int(g.size))
+    assert mx <= max_abs and rl2 <= rel_l2, f"{what}: {rep}"
+    return rep

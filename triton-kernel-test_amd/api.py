@@ -1,0 +1,294 @@
+"""Python operator API over liblrq.so (group mode — the north-star compressed format).
+
+Functions take and return torch tensors on a ROCm device and launch the HIP kernels on
+torch's current stream.  There is no CPU path: host tensors raise ``ValueError`` and a
+missing library raises ``RuntimeError``.
+
+Reference call surface this mirrors (file:line in Ther-nullptr/Triton-Kernel-Test):
+  encode                      <- low_rank_addition_fuse_compression_quantization
+                                 (low_rank_extraction_fuse_compression_quantization.py:118)
+  decode                      <- low_rank_addition_fuse_decompression_dequantization
+                                 (low_rank_extraction_fuse_decompression_dequantization.py:116)
+  silu_backward_compressed    <- triton_silu_backward_fuse_extraction (extraction_fuse_silu_backward.py:192)
+  mul_compressed              <- triton_hadamard_fuse_extraction (extraction_fuse_hadamard.py:185)
+  dequant_gemm                <- triton_matmul_decompress (extraction_fuse_matmul.py:224)
+  gelu_backward_compressed    <- triton_gelu_backward formula (gelu_backward.py:14-21), fused
+  softmax_backward_compressed <- triton_softmax_backward formula (softmax_backward.py:6-7), fused
+  outlier_channels            <- torch_extract_channel (extraction_outlier_channel.py:11-14), with
+                                 the channel set chosen by column abs-max instead of given
+The reference-named legacy functions live in ``legacy.py``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import LrqTensors, call
+
+__all__ = [
+    "LowRankBasis", "CompressedActivation", "encode", "decode", "silu_backward_compressed",
+    "gelu_backward_compressed", "mul_compressed", "softmax_backward_compressed", "dequant_gemm",
+    "outlier_channels", "column_absmax", "topk_channels",
+]
+
+
+def _p(t: Optional[torch.Tensor]):
+    return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_device(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("liblrq works on ROCm device tensors only (there is no CPU path); got a "
+                             f"tensor on {t.device}")
+
+
+def _rows_view(x: torch.Tensor) -> tuple[torch.Tensor, int, int, int]:
+    """View x[..., N] as a 2-D [rows, N] operand with unit inner stride; returns (x2, rows, N, ld)."""
+    if x.dim() < 1:
+        raise ValueError("activation must have at least one dimension")
+    n = x.shape[-1]
+    if x.dim() == 2 and x.stride(1) == 1:
+        return x, x.shape[0], n, x.stride(0)
+    x2 = x.reshape(-1, n)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    return x2, x2.shape[0], n, x2.stride(0)
+
+
+class LowRankBasis:
+    """An orthonormal basis V[N, r] (bf16, device) used for the projection.
+
+    ``Vt`` (the [r, N] transpose the projection operand wants) is built once on the
+    device by ``lrq_transpose_bf16`` and cached, like a pre-packed weight.
+    """
+
+    def __init__(self, V: torch.Tensor):
+        _require_device(V)
+        if V.dtype != torch.bfloat16 or V.dim() != 2:
+            raise ValueError("basis V must be a bf16 [N, r] tensor")
+        self.V = V.contiguous()
+        self._vt: Optional[torch.Tensor] = None
+
+    @property
+    def hidden(self) -> int:
+        return self.V.shape[0]
+
+    @property
+    def rank(self) -> int:
+        return self.V.shape[1]
+
+    @property
+    def Vt(self) -> torch.Tensor:
+        if self._vt is None:
+            vt = torch.empty((self.rank, self.hidden), dtype=torch.bfloat16, device=self.V.device)
+            with torch.cuda.device(self.V.device):
+                call("lrq_transpose_bf16", _p(self.V), self.hidden, self.rank, _p(vt), _stream(self.V.device))
+            self._vt = vt
+        return self._vt
+
+
+@dataclass
+class CompressedActivation:
+    """The compressed form of an activation x[..., N]; see include/lrq.h for the layout."""
+
+    codes: torch.Tensor                 # uint8 [rows, N*bits/8], row-planar
+    scale: torch.Tensor                 # fp16 [rows, N/group]
+    zero: torch.Tensor                  # fp16 [rows, N/group]
+    L: Optional[torch.Tensor]           # bf16 [rows, r]
+    basis: Optional[LowRankBasis]
+    side: Optional[torch.Tensor]        # fp16 [rows, k]
+    idx: Optional[torch.Tensor]         # int32 [k], ascending
+    shape: tuple
+    bits: int
+    group: int
+    hadamard: bool = False
+
+    @property
+    def rows(self) -> int:
+        return self.codes.shape[0]
+
+    @property
+    def hidden(self) -> int:
+        return self.shape[-1]
+
+    @property
+    def rank(self) -> int:
+        return 0 if self.basis is None else self.basis.rank
+
+    @property
+    def device(self) -> torch.device:
+        return self.codes.device
+
+    def nbytes(self) -> int:
+        n = self.codes.numel() + 2 * (self.scale.numel() + self.zero.numel())
+        if self.L is not None:
+            n += 2 * self.L.numel()
+        if self.side is not None:
+            n += 2 * self.side.numel() + 4 * self.idx.numel()
+        return n
+
+    def descriptor(self, for_encode: bool = False) -> LrqTensors:
+        t = LrqTensors()
+        t.rows, t.hidden = self.rows, self.hidden
+        t.rank, t.bits, t.group = self.rank, self.bits, self.group
+        t.flags = _lib.LRQ_FLAG_HADAMARD if self.hadamard else 0
+        if self.rank:
+            t.L, t.ld_L = self.L.data_ptr(), self.L.stride(0)
+            t.V = self.basis.V.data_ptr()
+            if for_encode:
+                t.Vt = self.basis.Vt.data_ptr()
+        t.codes, t.ld_codes = self.codes.data_ptr(), self.codes.stride(0)
+        t.scale, t.zero, t.ld_sz = self.scale.data_ptr(), self.zero.data_ptr(), self.scale.stride(0)
+        if self.idx is not None and self.idx.numel() > 0:
+            t.outlier_idx, t.n_outlier = self.idx.data_ptr(), self.idx.numel()
+            t.side, t.ld_side = self.side.data_ptr(), self.side.stride(0)
+        return t
+
+
+def _alloc(rows: int, n: int, bits: int, group: int, rank: int, k: int, device) -> dict:
+    # 8-byte aligned code rows: every supported shape gives N*bits/8 divisible by 8.
+    return dict(
+        codes=torch.empty((rows, n * bits // 8), dtype=torch.uint8, device=device),
+        scale=torch.empty((rows, n // group), dtype=torch.float16, device=device),
+        zero=torch.empty((rows, n // group), dtype=torch.float16, device=device),
+        L=torch.empty((rows, rank), dtype=torch.bfloat16, device=device) if rank else None,
+        side=torch.empty((rows, k), dtype=torch.float16, device=device) if k else None,
+    )
+
+
+def encode(x: torch.Tensor, basis: Optional[LowRankBasis | torch.Tensor] = None, *, bits: int = 4,
+           group_size: int = 64, hadamard: bool = False, outlier_idx: Optional[torch.Tensor] = None,
+           _twopass: bool = False) -> CompressedActivation:
+    """Compress a bf16 activation x[..., N].
+
+    ``basis``: the rank-r orthonormal V[N, r] (or a ``LowRankBasis``); None for rank 0.
+    ``outlier_idx``: int32 column indices kept as fp16 side columns (see ``outlier_channels``).
+    """
+    _require_device(x)
+    if x.dtype != torch.bfloat16:
+        raise ValueError("activation must be bf16")
+    if isinstance(basis, torch.Tensor):
+        basis = LowRankBasis(basis)
+    x2, rows, n, ldx = _rows_view(x)
+    if basis is not None and basis.hidden != n:
+        raise ValueError(f"basis has {basis.hidden} rows, activation hidden size is {n}")
+    rank = 0 if basis is None else basis.rank
+    if outlier_idx is not None:
+        _require_device(outlier_idx)
+        outlier_idx = outlier_idx.to(torch.int32).contiguous()
+    k = 0 if outlier_idx is None else outlier_idx.numel()
+    bufs = _alloc(rows, n, bits, group_size, rank, k, x.device)
+    c = CompressedActivation(codes=bufs["codes"], scale=bufs["scale"], zero=bufs["zero"], L=bufs["L"],
+                             basis=basis, side=bufs["side"], idx=outlier_idx if k else None,
+                             shape=tuple(x.shape), bits=bits, group=group_size, hadamard=hadamard)
+    t = c.descriptor(for_encode=True)
+    with torch.cuda.device(x.device):
+        call("lrq_encode_twopass" if _twopass else "lrq_encode", ctypes.byref(t), _p(x2), ldx,
+             _stream(x.device))
+    return c
+
+
+def _out_like(c: CompressedActivation, out: Optional[torch.Tensor]) -> torch.Tensor:
+    if out is None:
+        return torch.empty(c.shape, dtype=torch.bfloat16, device=c.device)
+    if out.shape != torch.Size(c.shape) or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous bf16 tensor of the activation's shape")
+    return out
+
+
+def _operand(c: CompressedActivation, y: torch.Tensor, name: str) -> tuple[torch.Tensor, int]:
+    _require_device(y)
+    if tuple(y.shape) != tuple(c.shape) or y.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bf16 with the activation's shape {c.shape}")
+    y2, _, _, ld = _rows_view(y)
+    return y2, ld
+
+
+def decode(c: CompressedActivation, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Reconstruct x_hat (bf16, the activation's shape)."""
+    o = _out_like(c, out)
+    t = c.descriptor()
+    with torch.cuda.device(c.device):
+        call("lrq_decode", ctypes.byref(t), _p(o), c.hidden, _stream(c.device))
+    return o
+
+
+def _fused(name: str, c: CompressedActivation, y: torch.Tensor, argname: str) -> torch.Tensor:
+    y2, ldy = _operand(c, y, argname)
+    o = _out_like(c, None)
+    t = c.descriptor()
+    with torch.cuda.device(c.device):
+        call(name, ctypes.byref(t), _p(y2), ldy, _p(o), c.hidden, _stream(c.device))
+    return o
+
+
+def silu_backward_compressed(c: CompressedActivation, grad_output: torch.Tensor) -> torch.Tensor:
+    """dX = dY * s(x)(1 + x(1 - s(x))) with x = decode(c), decompressed in-kernel."""
+    return _fused("lrq_silu_bwd", c, grad_output, "grad_output")
+
+
+def gelu_backward_compressed(c: CompressedActivation, grad_output: torch.Tensor) -> torch.Tensor:
+    """tanh-approximate GELU backward on x = decode(c), decompressed in-kernel."""
+    return _fused("lrq_gelu_bwd", c, grad_output, "grad_output")
+
+
+def mul_compressed(c: CompressedActivation, y: torch.Tensor) -> torch.Tensor:
+    """decode(c) * y elementwise (the reference's "hadamard" consumer)."""
+    return _fused("lrq_mul", c, y, "y")
+
+
+def softmax_backward_compressed(c: CompressedActivation, grad_p: torch.Tensor) -> torch.Tensor:
+    """dS = P (dP - rowsum(dP P)) with P = decode(c); rows are the softmax rows."""
+    return _fused("lrq_softmax_bwd", c, grad_p, "grad_p")
+
+
+def dequant_gemm(c: CompressedActivation, a: torch.Tensor, out_dtype=torch.float32) -> torch.Tensor:
+    """decode(c) @ a with a[N, n] bf16; fp32 accumulate, output fp32 or bf16."""
+    _require_device(a)
+    if a.dtype != torch.bfloat16 or a.dim() != 2 or a.shape[0] != c.hidden:
+        raise ValueError("a must be bf16 [N, n]")
+    a = a.contiguous()
+    n_out = a.shape[1]
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("out_dtype must be float32 or bfloat16")
+    o = torch.empty((c.rows, n_out), dtype=out_dtype, device=c.device)
+    t = c.descriptor()
+    with torch.cuda.device(c.device):
+        call("lrq_dequant_gemm", ctypes.byref(t), _p(a), n_out, _p(o), n_out,
+             1 if out_dtype == torch.float32 else 0, _stream(c.device))
+    return o.reshape(tuple(c.shape[:-1]) + (n_out,))
+
+
+def column_absmax(x: torch.Tensor) -> torch.Tensor:
+    """max over rows of |x[..., c]| as fp32 [N]."""
+    _require_device(x)
+    x2, rows, n, ldx = _rows_view(x)
+    out = torch.empty((n,), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        call("lrq_colmax", _p(x2), ldx, rows, n, _p(out), _stream(x.device))
+    return out
+
+
+def topk_channels(colmax: torch.Tensor, k: int) -> torch.Tensor:
+    """Indices of the k largest entries, ascending (ties toward the lower index)."""
+    _require_device(colmax)
+    colmax = colmax.to(torch.float32).contiguous()
+    idx = torch.empty((k,), dtype=torch.int32, device=colmax.device)
+    with torch.cuda.device(colmax.device):
+        call("lrq_topk", _p(colmax), colmax.numel(), k, _p(idx), _stream(colmax.device))
+    return idx
+
+
+def outlier_channels(x: torch.Tensor, k: int) -> torch.Tensor:
+    """The k hidden channels with the largest column abs-max (int32, ascending)."""
+    return topk_channels(column_absmax(x), k)

@@ -1,0 +1,66 @@
+// Host-side argument validation shared by the C-ABI entry points.  Every check here runs
+// before any HIP call, so an invalid argument returns a negative status without touching
+// the GPU (the CPU test-suite drives these paths with no device present).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/lrq.h"
+
+namespace lrq {
+
+static inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+static constexpr int format_key(int bits, int group, int rank) { return bits * 100000 + group * 100 + rank; }
+
+static inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? LRQ_OK : (int)e;
+}
+
+// Validates a group-mode descriptor.  `encode` additionally requires Vt (projection
+// operand) when rank > 0.
+static inline int validate_tensors(const lrq_tensors* t, int encode) {
+  if (t == nullptr) return LRQ_ERR_NULL;
+  if (t->rows < 0 || t->hidden <= 0 || t->rows > INT32_MAX || t->hidden > INT32_MAX) return LRQ_ERR_SHAPE;
+  if (t->bits != 4 && t->bits != 8) return LRQ_ERR_UNSUPPORTED;
+  if (t->group != 64 && t->group != 128) return LRQ_ERR_UNSUPPORTED;
+  if (t->rank != 0 && t->rank != 16 && t->rank != 32) return LRQ_ERR_UNSUPPORTED;
+  if ((t->flags & ~LRQ_FLAG_HADAMARD) != 0) return LRQ_ERR_UNSUPPORTED;
+  const int64_t np = 8 / t->bits;
+  if (t->hidden % (t->group * np) != 0) return LRQ_ERR_SHAPE;
+  if (t->flags & LRQ_FLAG_HADAMARD) {
+    if (t->hidden % 128 != 0) return LRQ_ERR_SHAPE;
+    if (t->n_outlier != 0) return LRQ_ERR_UNSUPPORTED;
+  }
+  if (t->rank > 0) {
+    if (t->L == nullptr || t->V == nullptr) return LRQ_ERR_NULL;
+    if (encode && t->Vt == nullptr) return LRQ_ERR_NULL;
+    if (t->ld_L < t->rank) return LRQ_ERR_SHAPE;
+    if ((t->ld_L % 4) != 0 || !aligned(t->L, 8) || !aligned(t->V, 8)) return LRQ_ERR_ALIGN;
+    if (encode && !aligned(t->Vt, 16)) return LRQ_ERR_ALIGN;
+  }
+  if (t->codes == nullptr || t->scale == nullptr || t->zero == nullptr) return LRQ_ERR_NULL;
+  if (t->ld_codes < t->hidden * t->bits / 8 || t->ld_sz < t->hidden / t->group) return LRQ_ERR_SHAPE;
+  if ((t->ld_codes % 8) != 0 || !aligned(t->codes, 8)) return LRQ_ERR_ALIGN;
+  if (!aligned(t->scale, 2) || !aligned(t->zero, 2)) return LRQ_ERR_ALIGN;
+  if (t->n_outlier < 0 || t->n_outlier > t->hidden) return LRQ_ERR_SHAPE;
+  if (t->n_outlier > 0) {
+    if (t->rank != 0) return LRQ_ERR_UNSUPPORTED;
+    if (t->outlier_idx == nullptr || t->side == nullptr) return LRQ_ERR_NULL;
+    if (t->ld_side < t->n_outlier) return LRQ_ERR_SHAPE;
+    if (!aligned(t->side, 2) || !aligned(t->outlier_idx, 4)) return LRQ_ERR_ALIGN;
+  }
+  return LRQ_OK;
+}
+
+// A bf16 [rows, >= cols] operand with 16-byte aligned rows.
+static inline int validate_rows16(const void* p, int64_t ld, int64_t cols) {
+  if (p == nullptr) return LRQ_ERR_NULL;
+  if (ld < cols) return LRQ_ERR_SHAPE;
+  if ((ld % 8) != 0 || !aligned(p, 16)) return LRQ_ERR_ALIGN;
+  return LRQ_OK;
+}
+
+}  // namespace lrq

@@ -1,0 +1,106 @@
+"""Seeded synthetic inputs for the five BASELINE.json configurations.
+
+Parity inputs are drawn on the CPU with ``torch.Generator().manual_seed(seed)`` in fp32 and
+cast to bf16, so the HIP path and the CPU oracle see identical bits.  Full-size benchmark
+inputs may instead be drawn on the device (``device="cuda"``): same recipe, different
+random stream, much faster.
+
+Recipes (BASELINE.json "configs"):
+  c1 / north_star  X[rows, 4096] ~ N(0,1), 8 seeded channels x20; V = QR(randn(4096, 16)).Q;
+                   rank 16, int4, group 64 (c1: 2048 rows, north star: 16384 rows)
+  c2               X[8192, 11008] ~ N(0,1); V[11008, 32]; int4/g64; dY = 0.02 N(0,1)  (SiLU bwd)
+  c3               X[16384, 4096] ~ N(0,1), 41 channels x50; top-41 channels to fp16 side columns;
+                   rest int8/g128, rank 0; dY = 0.02 N(0,1)                              (GELU bwd)
+  c4               X[16384, 5120] ~ N(0,1), 16 channels x30; WHT-128 rotation; V[5120, 16]; int4/g64
+  c5               P = softmax(N(0,1)/sqrt(128)) over [2, 32, 2048, 2048] (rows of 2048);
+                   V[2048, 16]; int4/g64 per row; dP = 0.02 N(0,1)                       (softmax bwd)
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+__all__ = ["Config", "CONFIGS", "activation", "basis", "gradient", "softmax_probs", "make"]
+
+
+@dataclass(frozen=True)
+class Config:
+    name: str
+    rows: int
+    hidden: int
+    rank: int
+    bits: int
+    group: int
+    n_outlier: int = 0          # channels scaled to act as outliers
+    outlier_scale: float = 1.0
+    keep_channels: int = 0      # channels kept dense as fp16 side columns (top-k by abs-max)
+    hadamard: bool = False
+    consumer: str = "decode"    # decode | silu | gelu | softmax
+    grad_std: float = 0.02
+    seed: int = 0
+    softmax_shape: tuple = field(default=())
+
+
+CONFIGS = {
+    "north_star": Config("north_star", 16384, 4096, 16, 4, 64, n_outlier=8, outlier_scale=20.0, seed=0),
+    "c1": Config("c1", 2048, 4096, 16, 4, 64, n_outlier=8, outlier_scale=20.0, seed=1),
+    "c2": Config("c2", 8192, 11008, 32, 4, 64, consumer="silu", seed=2),
+    "c3": Config("c3", 16384, 4096, 0, 8, 128, n_outlier=41, outlier_scale=50.0, keep_channels=41,
+                 consumer="gelu", seed=3),
+    "c4": Config("c4", 16384, 5120, 16, 4, 64, n_outlier=16, outlier_scale=30.0, hadamard=True, seed=4),
+    "c5": Config("c5", 2 * 32 * 2048, 2048, 16, 4, 64, consumer="softmax", seed=5,
+                 softmax_shape=(2, 32, 2048, 2048)),
+}
+
+
+def _gen(seed: int, device) -> torch.Generator:
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def activation(rows: int, hidden: int, n_outlier: int = 0, outlier_scale: float = 1.0, seed: int = 0,
+               device="cpu") -> torch.Tensor:
+    """X ~ N(0,1) [rows, hidden] with ``n_outlier`` seeded channels scaled; bf16."""
+    g = _gen(seed, device)
+    x = torch.randn((rows, hidden), generator=g, device=device, dtype=torch.float32)
+    if n_outlier:
+        ch = torch.randperm(hidden, generator=g, device=device)[:n_outlier]
+        x[:, ch] *= outlier_scale
+    return x.to(torch.bfloat16)
+
+
+def basis(hidden: int, rank: int, seed: int = 0) -> torch.Tensor:
+    """Orthonormal V[hidden, rank] = QR(randn).Q, drawn on the CPU, cast to bf16."""
+    g = _gen(seed + 1_000_003, "cpu")
+    q, _ = torch.linalg.qr(torch.randn((hidden, rank), generator=g, dtype=torch.float32))
+    return q.to(torch.bfloat16)
+
+
+def gradient(shape, std: float = 0.02, seed: int = 0, device="cpu") -> torch.Tensor:
+    g = _gen(seed + 2_000_003, device)
+    return (torch.randn(shape, generator=g, device=device, dtype=torch.float32) * std).to(torch.bfloat16)
+
+
+def softmax_probs(shape, seed: int = 0, device="cpu") -> torch.Tensor:
+    """P = softmax(N(0,1)/sqrt(128)) along the last axis, computed in fp32, cast to bf16."""
+    g = _gen(seed, device)
+    logits = torch.randn(shape, generator=g, device=device, dtype=torch.float32) / math.sqrt(128.0)
+    return torch.softmax(logits, dim=-1).to(torch.bfloat16)
+
+
+def make(cfg: Config, rows: int | None = None, device="cpu") -> dict:
+    """Inputs for ``cfg`` with the row count optionally reduced (parity sizes)."""
+    rows = cfg.rows if rows is None else rows
+    out = {}
+    if cfg.consumer == "softmax":
+        out["x"] = softmax_probs((rows, cfg.hidden), seed=cfg.seed, device=device)
+    else:
+        out["x"] = activation(rows, cfg.hidden, cfg.n_outlier, cfg.outlier_scale, cfg.seed, device)
+    out["V"] = basis(cfg.hidden, cfg.rank, cfg.seed) if cfg.rank else None
+    if cfg.consumer != "decode":
+        out["dy"] = gradient((rows, cfg.hidden), cfg.grad_std, cfg.seed, device)
+    return out

@@ -1,0 +1,239 @@
+"""The reference's own operator names and signatures ("legacy mode"), on liblrq.so.
+
+Same positional signatures, argument meanings and assertion messages as the reference's
+Python wrappers; the arithmetic follows the reference's torch forms (bf16 rounding after
+every op, row-planar packing, per-batch scale rows) rather than its Triton kernels, whose
+defects (s[0] only, tile-planar packing, unmasked scratch stores) are not reproduced.
+
+  low_rank_addition_fuse_compression_quantization      low_rank_extraction_fuse_compression_quantization.py:118
+  low_rank_addition_fuse_decompression_dequantization  low_rank_extraction_fuse_decompression_dequantization.py:116
+  low_rank_addition                                    low_rank_extraction_speed.py:77
+  triton_silu_backward_fuse_extraction                 extraction_fuse_silu_backward.py:192
+  triton_silu_backward_add_extraction                  extraction_fuse_silu_backward.py:324 (returns the result)
+  triton_hadamard_fuse_extraction                      extraction_fuse_hadamard.py:185
+  triton_hadamard_add_extraction                       extraction_fuse_hadamard.py:317 (returns the result)
+  triton_matmul_decompress                             extraction_fuse_matmul.py:224
+  triton_silu_backward                                 silu_backward.py:54
+  triton_gelu_backward                                 gelu_backward.py:73
+  triton_softmax_backward                              softmax_backward.py:45
+  triton_hadamard                                      extraction_fuse_hadamard.py:62
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ._lib import call
+from .api import _p, _require_device, _stream
+
+__all__ = [
+    "low_rank_addition_fuse_compression_quantization",
+    "low_rank_addition_fuse_decompression_dequantization",
+    "low_rank_addition",
+    "triton_silu_backward_fuse_extraction",
+    "triton_silu_backward_add_extraction",
+    "triton_hadamard_fuse_extraction",
+    "triton_hadamard_add_extraction",
+    "triton_matmul_decompress",
+    "triton_silu_backward",
+    "triton_gelu_backward",
+    "triton_softmax_backward",
+    "triton_hadamard",
+]
+
+_OP_STORE, _OP_SILU, _OP_MUL = 0, 1, 2
+
+
+def _factors(l: torch.Tensor, r: torch.Tensor):
+    """Zero-pad the rank to 16 or 32 (as the reference pads K < 16 to 16,
+    low_rank_extraction_fuse_compression_quantization.py:126-129) and build rt = r^T [N, K]."""
+    _require_device(l, r)
+    M, K = l.shape
+    K2, N = r.shape
+    if K2 != K:
+        raise AssertionError("Incompatible dimensions")
+    if K > 32:
+        raise ValueError("liblrq supports low-rank factors of rank <= 32")
+    kp = 16 if K <= 16 else 32
+    if kp != K:
+        l = torch.cat([l, torch.zeros((M, kp - K), device=l.device, dtype=l.dtype)], dim=1)
+        r = torch.cat([r, torch.zeros((kp - K, N), device=r.device, dtype=r.dtype)], dim=0)
+    l = l.to(torch.bfloat16).contiguous()
+    r = r.to(torch.bfloat16).contiguous()
+    rt = torch.empty((N, kp), dtype=torch.bfloat16, device=r.device)
+    call("lrq_transpose_bf16", _p(r), kp, N, _p(rt), _stream(r.device))
+    return l, rt, kp
+
+
+def _scale(s: torch.Tensor, B: int, N: int) -> torch.Tensor:
+    _require_device(s)
+    if s.dim() == 1:
+        s = s.unsqueeze(0)
+    if s.shape[-1] != N or s.shape[0] not in (1, B):
+        raise ValueError(f"s must be [B or 1, N] = [{B} or 1, {N}], got {tuple(s.shape)}")
+    return s.to(torch.bfloat16).contiguous()
+
+
+def _bits(quantize_bit: int) -> int:
+    if quantize_bit not in (1, 2, 4, 8):
+        raise ValueError("quantize_bit must be 1, 2, 4 or 8")
+    return int(quantize_bit)
+
+
+def low_rank_addition_fuse_compression_quantization(l, r, x, s, quantize_bit=8, outlier=5.):
+    """Encode x[B, M, N] - l@r: threshold outliers (returned sparse COO, like the reference) and
+    symmetric per-column quantisation with row-planar packing.  Returns (o, q)."""
+    assert l.shape[1] == r.shape[0], "Incompatible dimensions"
+    assert l.is_contiguous(), "Matrix A must be contiguous"
+    assert r.is_contiguous(), "Matrix B must be contiguous"
+    bits = _bits(quantize_bit)
+    _require_device(x)
+    M, _ = l.shape
+    _, N = r.shape
+    B = x.shape[0]
+    if tuple(x.shape) != (B, M, N):
+        raise ValueError(f"x must be [B, {M}, {N}]")
+    if x.stride(2) != 1:
+        x = x.contiguous()
+    with torch.cuda.device(x.device):
+        l2, rt, K = _factors(l, r)
+        s2 = _scale(s, B, N)
+        o = torch.empty((B, M, N), device=x.device, dtype=torch.bfloat16)
+        q = torch.empty((B, M, N // (8 // bits)), device=x.device, dtype=torch.uint8)
+        call("lrq_legacy_encode", _p(l2), _p(rt), K, _p(x), B, M, N, x.stride(0), x.stride(1), _p(s2),
+             s2.shape[0], bits, float(outlier), _p(o), _p(q), _stream(x.device))
+    return o.to_sparse(), q
+
+
+def low_rank_addition_fuse_decompression_dequantization(l, r, q, o, s, quantize_bit=8, outlier=5.):
+    """Decode: bf16(bf16(bf16(c*s) + o) + bf16(l@r)).  ``o`` may be sparse COO, dense or None."""
+    assert l.shape[1] == r.shape[0], "Incompatible dimensions"
+    assert l.is_contiguous(), "Matrix A must be contiguous"
+    assert r.is_contiguous(), "Matrix B must be contiguous"
+    bits = _bits(quantize_bit)
+    _require_device(q)
+    M, _ = l.shape
+    _, N = r.shape
+    B = q.shape[0]
+    q = q.contiguous()
+    if o is not None:
+        _require_device(o)
+        o = (o.to_dense() if o.is_sparse else o).to(torch.bfloat16).contiguous()
+    with torch.cuda.device(q.device):
+        l2, rt, K = _factors(l, r)
+        s2 = _scale(s, B, N)
+        x = torch.empty((B, M, N), device=q.device, dtype=torch.bfloat16)
+        call("lrq_legacy_decode", _p(l2), _p(rt), K, _p(q), _p(o), _p(s2), s2.shape[0], B, M, N, bits,
+             _p(x), _stream(q.device))
+    return x
+
+
+def low_rank_addition(l, r, x):
+    """x + l @ r with the torch form's bf16 rounding (low_rank_extraction_speed.py:106-107)."""
+    assert l.shape[1] == r.shape[0], "Incompatible dimensions"
+    assert l.is_contiguous(), "Matrix A must be contiguous"
+    assert r.is_contiguous(), "Matrix B must be contiguous"
+    _require_device(x)
+    M, _ = l.shape
+    _, N = r.shape
+    B = x.shape[0]
+    x = x.contiguous()
+    with torch.cuda.device(x.device):
+        l2, rt, K = _factors(l, r)
+        o = torch.empty((B, M, N), device=x.device, dtype=torch.bfloat16)
+        call("lrq_lowrank_add", _p(l2), _p(rt), K, _p(x), B, M, N, _p(o), _stream(x.device))
+    return o
+
+
+def _legacy_fused(op, l, r, q, s, b, quantize_bit):
+    bits = _bits(quantize_bit)
+    _require_device(q)
+    M, _ = l.shape
+    _, N = r.shape
+    B = q.shape[0]
+    q = q.contiguous()
+    if b is not None:
+        _require_device(b)
+        if tuple(b.shape) != (B, M, N):
+            raise ValueError(f"second operand must be [{B}, {M}, {N}]")
+        b = b.to(torch.bfloat16).contiguous()
+    with torch.cuda.device(q.device):
+        l2, rt, K = _factors(l, r)
+        s2 = _scale(s, B, N)
+        c = torch.empty((B, M, N), device=q.device, dtype=torch.bfloat16)
+        call("lrq_legacy_fused", _p(l2), _p(rt), K, _p(q), _p(s2), s2.shape[0], B, M, N, bits, op, _p(b),
+             _p(c), _stream(q.device))
+    return c
+
+
+def triton_silu_backward_fuse_extraction(l, r, q, s, b, quantize_bit=2):
+    """SiLU backward of the decompressed activation, decompression fused in-kernel."""
+    return _legacy_fused(_OP_SILU, l, r, q, s, b, quantize_bit)
+
+
+def triton_hadamard_fuse_extraction(l, r, q, s, b, quantize_bit=2):
+    """Elementwise product of the decompressed activation with b, fused in-kernel."""
+    return _legacy_fused(_OP_MUL, l, r, q, s, b, quantize_bit)
+
+
+def triton_silu_backward_add_extraction(l, r, q, s, b, quantize_bit=2):
+    """Unfused: decode kernel, then the SiLU-backward kernel (the reference returns None here)."""
+    a = _legacy_fused(_OP_STORE, l, r, q, s, None, quantize_bit)
+    return triton_silu_backward(a, b)
+
+
+def triton_hadamard_add_extraction(l, r, q, s, b, quantize_bit=2):
+    """Unfused: decode kernel, then the elementwise-product kernel (the reference returns None)."""
+    a = _legacy_fused(_OP_STORE, l, r, q, s, None, quantize_bit)
+    return triton_hadamard(a, b)
+
+
+def triton_matmul_decompress(q, l, r, s, y, quantize_bit=2):
+    """(decode(q) ) @ y per batch: x_hat[B, M, N] @ y[B, N, n] -> bf16 [B, M, n].
+
+    The legacy per-column format is decoded by the HIP decode kernel and multiplied by the
+    library GEMM; the fused dequant-GEMM kernel serves the group-mode format
+    (``api.dequant_gemm``)."""
+    a = _legacy_fused(_OP_STORE, l, r, q, s, None, quantize_bit)
+    _require_device(y)
+    return torch.matmul(a, y.to(torch.bfloat16).contiguous())
+
+
+def _dense(op, x, y):
+    _require_device(x, y)
+    if x.shape != y.shape:
+        raise AssertionError("shape mismatch")
+    x = x.to(torch.bfloat16).contiguous()
+    y = y.to(torch.bfloat16).contiguous()
+    o = torch.empty_like(x)
+    with torch.cuda.device(x.device):
+        call("lrq_dense_elementwise", op, _p(x), _p(y), _p(o), x.numel(), _stream(x.device))
+    return o
+
+
+def triton_silu_backward(x, g):
+    """g * s(x)(1 + x(1 - s(x))) in fp32, rounded once (silu_backward.py:54-69)."""
+    return _dense(0, x, g)
+
+
+def triton_gelu_backward(x, g):
+    """tanh-GELU backward in fp32, rounded once (gelu_backward.py:73-88)."""
+    return _dense(1, x, g)
+
+
+def triton_hadamard(a, b):
+    """a * b (extraction_fuse_hadamard.py:62-73)."""
+    return _dense(2, a, b)
+
+
+def triton_softmax_backward(y, grad_y):
+    """(g - rowsum(g * y)) * y over the last axis (softmax_backward.py:45-61)."""
+    _require_device(y, grad_y)
+    assert grad_y.shape == y.shape
+    n = y.shape[-1]
+    y2 = y.to(torch.bfloat16).contiguous()
+    g2 = grad_y.to(torch.bfloat16).contiguous()
+    o = torch.empty_like(y2)
+    with torch.cuda.device(y.device):
+        call("lrq_dense_softmax_bwd", _p(y2), _p(g2), _p(o), y2.numel() // n, n, _stream(y.device))
+    return o
