@@ -21,14 +21,16 @@
  *
  * Compressed format ("group mode", the north-star format).  An activation X[rows, hidden]
  * (bf16) is stored as
- *     L      bf16  [rows, rank]          projection coefficients, L = bf16(Y V)
- *     codes  uint8 [rows, hidden*bits/8] residual codes, row-planar packing: byte j of a
- *                                        row holds column j + i*hidden*bits/8 in bits
- *                                        [bits*i, bits*i + bits)
- *     scale  fp16  [rows, hidden/group]  per-group step
- *     zero   fp16  [rows, hidden/group]  per-group minimum
- *     side   fp16  [rows, n_outlier]     outlier channels kept dense (optional)
- *     idx    int32 [n_outlier]           their column indices, ascending (optional)
+ *     L       bf16  [rows, rank]          projection coefficients, L = bf16(Y V)
+ *     codes   uint8 [rows, hidden*bits/8] residual codes, row-planar packing: byte j of a
+ *                                         row holds column j + i*hidden*bits/8 in bits
+ *                                         [bits*i, bits*i + bits), i < NP = 8/bits
+ *     qparams fp16  [rows, U, NP, 2]      U = hidden/(group*NP) units per row; entry
+ *                                         [r, u, i] is (scale, zero) of the group of columns
+ *                                         i*hidden/NP + u*group .. + group - 1 (the groups
+ *                                         whose codes share bytes u*group .. + group - 1)
+ *     side    fp16  [rows, n_outlier]     outlier channels kept dense (optional)
+ *     idx     int32 [n_outlier]           their column indices, ascending (optional)
  * where Y = X (or its blockwise 128-point Walsh-Hadamard rotation) and V[hidden, rank] is
  * an orthonormal basis supplied by the caller.
  */
@@ -62,12 +64,12 @@ typedef struct lrq_tensors {
   void* L;
   int64_t ld_L;
   const void* V;  /* bf16 [hidden, rank] */
-  const void* Vt; /* bf16 [rank, hidden] (encode only; lrq_transpose_bf16 builds it) */
+  const void* Vt; /* bf16 [rank, hidden]; read only by the two-pass encode (rank 32 and hidden
+                     sizes without a single-pass kernel); lrq_transpose_bf16 builds it */
   void* codes;
   int64_t ld_codes;
-  void* scale;
-  void* zero;
-  int64_t ld_sz;
+  void* qparams;  /* fp16 [rows, U, NP, 2], see above */
+  int64_t ld_qp;  /* row stride of qparams in fp16 elements (>= 2*hidden/group) */
   const int32_t* outlier_idx;
   int32_t n_outlier;
   void* side;

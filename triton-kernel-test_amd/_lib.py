@@ -32,7 +32,7 @@ class LrqTensors(ctypes.Structure):
         ("L", c_void_p), ("ld_L", c_int64),
         ("V", c_void_p), ("Vt", c_void_p),
         ("codes", c_void_p), ("ld_codes", c_int64),
-        ("scale", c_void_p), ("zero", c_void_p), ("ld_sz", c_int64),
+        ("qparams", c_void_p), ("ld_qp", c_int64),
         ("outlier_idx", c_void_p), ("n_outlier", c_int32),
         ("side", c_void_p), ("ld_side", c_int64),
     ]

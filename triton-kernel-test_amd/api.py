@@ -102,8 +102,7 @@ class CompressedActivation:
     """The compressed form of an activation x[..., N]; see include/lrq.h for the layout."""
 
     codes: torch.Tensor                 # uint8 [rows, N*bits/8], row-planar
-    scale: torch.Tensor                 # fp16 [rows, N/group]
-    zero: torch.Tensor                  # fp16 [rows, N/group]
+    qparams: torch.Tensor               # fp16 [rows, U, NP, 2]: per unit, (scale, zero) of each plane
     L: Optional[torch.Tensor]           # bf16 [rows, r]
     basis: Optional[LowRankBasis]
     side: Optional[torch.Tensor]        # fp16 [rows, k]
@@ -129,8 +128,23 @@ class CompressedActivation:
     def device(self) -> torch.device:
         return self.codes.device
 
+    def _per_group(self, which: int) -> torch.Tensor:
+        # qparams[r, u, i] belongs to group i*U + u of the row (plane i, unit u)
+        q = self.qparams[..., which]                      # [rows, U, NP]
+        return q.permute(0, 2, 1).reshape(self.rows, -1)  # [rows, N/group], column order
+
+    @property
+    def scale(self) -> torch.Tensor:
+        """Per-group scale, fp16 [rows, N/group] in column order (a copy)."""
+        return self._per_group(0)
+
+    @property
+    def zero(self) -> torch.Tensor:
+        """Per-group zero point (group minimum), fp16 [rows, N/group] in column order (a copy)."""
+        return self._per_group(1)
+
     def nbytes(self) -> int:
-        n = self.codes.numel() + 2 * (self.scale.numel() + self.zero.numel())
+        n = self.codes.numel() + 2 * self.qparams.numel()
         if self.L is not None:
             n += 2 * self.L.numel()
         if self.side is not None:
@@ -148,7 +162,7 @@ class CompressedActivation:
             if for_encode:
                 t.Vt = self.basis.Vt.data_ptr()
         t.codes, t.ld_codes = self.codes.data_ptr(), self.codes.stride(0)
-        t.scale, t.zero, t.ld_sz = self.scale.data_ptr(), self.zero.data_ptr(), self.scale.stride(0)
+        t.qparams, t.ld_qp = self.qparams.data_ptr(), self.qparams.stride(0)
         if self.idx is not None and self.idx.numel() > 0:
             t.outlier_idx, t.n_outlier = self.idx.data_ptr(), self.idx.numel()
             t.side, t.ld_side = self.side.data_ptr(), self.side.stride(0)
@@ -156,11 +170,13 @@ class CompressedActivation:
 
 
 def _alloc(rows: int, n: int, bits: int, group: int, rank: int, k: int, device) -> dict:
-    # 8-byte aligned code rows: every supported shape gives N*bits/8 divisible by 8.
+    # Code rows are N*bits/8 bytes: a multiple of the group (>= 64), so 16-byte aligned.
+    np_ = 8 // bits
+    if n % (group * np_) != 0:
+        raise ValueError(f"hidden size {n} must be a multiple of group*8/bits = {group * np_}")
     return dict(
         codes=torch.empty((rows, n * bits // 8), dtype=torch.uint8, device=device),
-        scale=torch.empty((rows, n // group), dtype=torch.float16, device=device),
-        zero=torch.empty((rows, n // group), dtype=torch.float16, device=device),
+        qparams=torch.empty((rows, n // (group * np_), np_, 2), dtype=torch.float16, device=device),
         L=torch.empty((rows, rank), dtype=torch.bfloat16, device=device) if rank else None,
         side=torch.empty((rows, k), dtype=torch.float16, device=device) if k else None,
     )
@@ -188,7 +204,7 @@ def encode(x: torch.Tensor, basis: Optional[LowRankBasis | torch.Tensor] = None,
         outlier_idx = outlier_idx.to(torch.int32).contiguous()
     k = 0 if outlier_idx is None else outlier_idx.numel()
     bufs = _alloc(rows, n, bits, group_size, rank, k, x.device)
-    c = CompressedActivation(codes=bufs["codes"], scale=bufs["scale"], zero=bufs["zero"], L=bufs["L"],
+    c = CompressedActivation(codes=bufs["codes"], qparams=bufs["qparams"], L=bufs["L"],
                              basis=basis, side=bufs["side"], idx=outlier_idx if k else None,
                              shape=tuple(x.shape), bits=bits, group=group_size, hadamard=hadamard)
     t = c.descriptor(for_encode=True)

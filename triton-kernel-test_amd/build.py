@@ -29,6 +29,8 @@ HIPFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-ffp-contract=off",
+    # MFMA results straight into VGPRs (no v_accvgpr_read round trips in the epilogues)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

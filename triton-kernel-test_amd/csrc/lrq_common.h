@@ -1,14 +1,28 @@
 // Shared device helpers for the compressed-activation kernels (gfx950 / CDNA4, wave64).
 //
-// Lane conventions used by every kernel in this library.  A wave works on a block of
-// 16 rows; lane l has j = l & 15 (row inside the block) and g = l >> 4 (0..3).  For a
-// "chunk" of 32 consecutive columns starting at c0, lane (j, g) holds the 8 columns
-// c0 + 8g .. c0 + 8g + 7 of row j as one 16-byte vector (4 dwords, two bf16 each,
-// even column in the low half).  That is exactly the B operand of
-// v_mfma_f32_16x16x32_bf16 with B = X^T, and — by choosing which V rows feed the A
-// operand — the output layout of two v_mfma_f32_16x16x16_bf16 that compute L V^T for
-// the same 32 columns.  So projection, residual and reconstruction never move
-// activation data between lanes.
+// Layout conventions used by every group-mode kernel in this library.
+//
+//  * A wave works on a block of 16 rows.  Lane l has j = l & 15 (row inside the block)
+//    and g = l >> 4 (0..3).
+//  * Columns are split into NP = 8/bits packing planes (plane p holds columns
+//    [p*N/NP, (p+1)*N/NP)); byte c of a packed code row holds column c of every plane.
+//  * A "unit" u is group-column u of every plane: columns base_p = p*N/NP + u*G .. +G-1.
+//    Lane (j, g) owns the G/4 consecutive columns base_p + (G/4)*g + e, e < G/4, of row j,
+//    for every plane; they sit in G/32 16-byte vectors x[p][k] (columns 8k .. 8k+7 of the
+//    lane's quarter, two bf16 per dword, even column low).  The lane's codes for the unit
+//    are the G/4 contiguous bytes u*G + (G/4)*g .. of the packed row.
+//  * Reconstruction L V^T: v_mfma_f32_16x16x16_bf16 number q (q < G/16) of a unit-plane
+//    feeds A row i with V row base_p + (G/4)*(i/4) + 4q + (i%4) (ranks 4g..4g+3 of the
+//    rank tile in lane (i, g)) and B = L^T; its output lands in lane (j, g) as columns
+//    base_p + (G/4)*g + 4q + v, v < 4 — exactly elements 4q..4q+3 of the lane's quarter.
+//  * Projection L = Y V: the same operand, multiplied by the identity on MFMA, comes out
+//    transposed (lane (rank, g) holding V at columns base_p + (G/4)g + 4q + v), which is
+//    the A operand of a 16x16x16 MFMA whose B operand is the lane's own x elements
+//    4q..4q+3.  Its output is L[row j][16t + 4g + v] in lane (j, g): the B operand the
+//    reconstruction needs.  No activation data ever moves between lanes.
+//  * Group statistics: the four lanes of a row (j, j+16, j+32, j+48) hold the whole group;
+//    two xor-shuffles finish min/max.
+//  * qparams: fp16 [rows, N/(G*NP), NP, 2] — per unit, (scale, zero) of each plane's group.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -29,23 +43,38 @@ static constexpr int kWave = 64;
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// fp32 -> bf16 bits, round to nearest even (finite inputs; NaN becomes a quiet NaN).
-__device__ __forceinline__ uint32_t bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
-}
+// fp32 -> 2 x bf16 in one dword (lo in bits 0..15), round to nearest even, on the gfx950
+// conversion unit (v_cvt_pk_bf16_f32).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return bf16_bits(lo) | (bf16_bits(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
-__device__ __forceinline__ float bf16_roundtrip(float f) { return __uint_as_float(bf16_bits(f) << 16); }
+__device__ __forceinline__ float bf16_roundtrip(float f) { return __uint_as_float(pack_bf16x2(f, 0.f) << 16); }
+// Pack two fp32 values that are already exactly representable in bf16 (no rounding).
+__device__ __forceinline__ uint32_t pack_bf16x2_exact(float lo, float hi) {
+  return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
+}
+
+// Byte K of w as fp32 (v_cvt_f32_ubyteK).  Written as asm so the compiler keeps one
+// masked dword feeding four conversions instead of splitting it into per-byte extracts.
+template <int K>
+__device__ __forceinline__ float ubyte_f32(uint32_t w) {
+  float f;
+  if constexpr (K == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(w));
+  else if constexpr (K == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(w));
+  else if constexpr (K == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(w));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(w));
+  return f;
+}
 
 // fp32 -> fp16 bits (RNE) and back.
 __device__ __forceinline__ uint16_t f16_bits(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
-__device__ __forceinline__ float f16_val(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ float f16_val(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
 
 // ---------------------------------------------------------------- MFMA wrappers
 // D(16x16) += A(16x32) * B(32x16), bf16 inputs, fp32 accumulate.
@@ -58,10 +87,12 @@ __device__ __forceinline__ f32x4 mfma_16x16x16(u32x2 a, u32x2 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
                                                    __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
 }
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
 // ---------------------------------------------------------------- memory helpers
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ u32x2 ld8(const void* p) { return *reinterpret_cast<const u32x2*>(p); }
+__device__ __forceinline__ uint32_t ld4(const void* p) { return *reinterpret_cast<const uint32_t*>(p); }
 __device__ __forceinline__ u32x4 ld16_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
@@ -70,6 +101,7 @@ __device__ __forceinline__ u32x2 ld8_stream(const void* p) {
 }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ __forceinline__ void st8(void* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }
+__device__ __forceinline__ void st4(void* p, uint32_t v) { *reinterpret_cast<uint32_t*>(p) = v; }
 __device__ __forceinline__ void st16_stream(void* p, u32x4 v) {
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
@@ -89,27 +121,66 @@ __device__ __forceinline__ u32x4 pack8(const float* f) {
   return v;
 }
 
-// ---------------------------------------------------------------- low-rank reconstruction
-// P[j][c0 + 8g + e], e = 0..7, for the lane's row j, using the residual-operand trick:
-// MFMA h (h = 0, 1) feeds A row i = j with V row c0 + 8*(i/4) + 4h + (i%4), so its output
-// lands in lane (j, g) as columns c0 + 8g + 4h + v.  `lop[t]` is the B operand of rank
-// tile t: L[j][16t + 4g .. 16t + 4g + 3] as 4 packed bf16.  V is [N][R] bf16, row-major.
-template <int R>
-__device__ __forceinline__ void lowrank_chunk(const uint16_t* __restrict__ V, int c0, int j, int g,
-                                              const u32x2* lop, float* p) {
+// ---------------------------------------------------------------- unit geometry
+// First column of unit u in plane p.
+__device__ __forceinline__ int unit_base(int p, int u, int N, int NP, int G) { return p * (N / NP) + u * G; }
+
+// V row feeding A row j of reconstruction MFMA q (see the header comment).
+template <int G>
+__device__ __forceinline__ int vrow_res(int base, int j, int q) {
+  return base + (G / 4) * (j >> 2) + 4 * q + (j & 3);
+}
+
+// Load the reconstruction A operands of one unit-plane: vop[q][t] for q < G/16, t < R/16.
+template <int G, int R>
+__device__ __forceinline__ void load_vops(const uint16_t* __restrict__ V, int base, int j, int g,
+                                          u32x2 (&vop)[G / 16][R / 16]) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int vrow = c0 + 8 * (j >> 2) + 4 * h + (j & 3);
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < G / 16; ++q)
+#pragma unroll
+    for (int t = 0; t < R / 16; ++t)
+      vop[q][t] = ld8(V + (int64_t)vrow_res<G>(base, j, q) * R + 16 * t + 4 * g);
+}
+
+// P = L V^T for the lane's G/4 columns of one unit-plane: p[4q + v].
+template <int G, int R>
+__device__ __forceinline__ void lowrank_unit(const u32x2 (&vop)[G / 16][R / 16], const u32x2* lop, float* p) {
+#pragma unroll
+  for (int q = 0; q < G / 16; ++q) {
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int t = 0; t < R / 16; ++t) acc = mfma_16x16x16(vop[q][t], lop[t], acc);
+    p[4 * q + 0] = acc[0];
+    p[4 * q + 1] = acc[1];
+    p[4 * q + 2] = acc[2];
+    p[4 * q + 3] = acc[3];
+  }
+}
+
+// B operand of the identity: lane (j, g) holds I[4g + e][j], e < 4, as bf16.
+__device__ __forceinline__ u32x2 identity_bop(int j, int g) {
+  const uint32_t one = 0x3f80u;
+  uint32_t h[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) h[e] = (4 * g + e == j) ? one : 0u;
+  return u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+}
+
+// Projection partial for one unit-plane: acc[t] += V_t^T(block q) * X^T(block q), with the
+// V^T operand obtained by multiplying the reconstruction operand by the identity (exact).
+template <int G, int R>
+__device__ __forceinline__ void project_unit(const u32x2 (&vop)[G / 16][R / 16], const u32x4* x, u32x2 ident,
+                                             f32x4* acc) {
+#pragma unroll
+  for (int q = 0; q < G / 16; ++q) {
+    const u32x4 xv = x[q >> 1];
+    const u32x2 xb = (q & 1) ? u32x2{xv[2], xv[3]} : u32x2{xv[0], xv[1]};
 #pragma unroll
     for (int t = 0; t < R / 16; ++t) {
-      u32x2 a = ld8(V + (int64_t)vrow * R + 16 * t + 4 * g);
-      acc = mfma_16x16x16(a, lop[t], acc);
+      const f32x4 vt = mfma_16x16x16(vop[q][t], ident, zero4());
+      const u32x2 a = u32x2{pack_bf16x2_exact(vt[0], vt[1]), pack_bf16x2_exact(vt[2], vt[3])};
+      acc[t] = mfma_16x16x16(a, xb, acc[t]);
     }
-    p[4 * h + 0] = acc[0];
-    p[4 * h + 1] = acc[1];
-    p[4 * h + 2] = acc[2];
-    p[4 * h + 3] = acc[3];
   }
 }
 
@@ -130,13 +201,21 @@ __device__ __forceinline__ float wave_sum4(float v) {
   return v;
 }
 
+// Workgroup barrier that waits for LDS traffic only (outstanding global loads — e.g. a
+// prefetch of the next row block — stay in flight across it).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt, expcnt untouched
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // ---------------------------------------------------------------- group quantiser
 // Per-group parameters from min/max, exactly as the CPU oracle defines them:
 //   scale_h = fp16(min((mx - mn) / qmax, 65504)), 1 when that is 0; zero_h = fp16(clamp(mn));
 //   inv = 1 / fp32(scale_h).  Division is IEEE correctly rounded (HIP default).
 struct GroupParams {
   float inv, zf;
-  uint16_t sh, zh;
+  uint32_t sh, zh;
 };
 template <int BITS>
 __device__ __forceinline__ GroupParams group_params(float mn, float mx) {
@@ -144,9 +223,9 @@ __device__ __forceinline__ GroupParams group_params(float mn, float mx) {
   GroupParams gp;
   float s = (mx - mn) / qmax;
   s = fminf(s, 65504.f);
-  uint16_t sh = f16_bits(s);
+  uint32_t sh = f16_bits(s);
   if ((sh & 0x7fffu) == 0) sh = 0x3c00u;  // 1.0
-  float z = fminf(fmaxf(mn, -65504.f), 65504.f);
+  const float z = fminf(fmaxf(mn, -65504.f), 65504.f);
   gp.sh = sh;
   gp.zh = f16_bits(z);
   gp.zf = f16_val(gp.zh);
@@ -154,13 +233,25 @@ __device__ __forceinline__ GroupParams group_params(float mn, float mx) {
   return gp;
 }
 // code = clamp(rint((r - zf) * inv), 0, qmax); the subtract and the multiply round separately.
+// Returned as the bit pattern of 1.5*2^23 + code: clamping before rounding gives the same
+// code for every t, and adding 1.5*2^23 to t in [0, qmax] rounds it to an integer (half to
+// even) in the low mantissa bits, so the code is the low BITS bits of the result.
 template <int BITS>
-__device__ __forceinline__ uint32_t quant_code(float r, const GroupParams& gp) {
+__device__ __forceinline__ uint32_t quant_code_bits(float r, const GroupParams& gp) {
   constexpr float qmax = (float)((1 << BITS) - 1);
   float t = __fmul_rn(__fsub_rn(r, gp.zf), gp.inv);
-  t = __builtin_rintf(t);
-  t = fminf(fmaxf(t, 0.f), qmax);
-  return (uint32_t)t;
+  t = __builtin_amdgcn_fmed3f(t, 0.f, qmax);
+  return __float_as_uint(__fadd_rn(t, 12582912.0f));
+}
+template <int BITS>
+__device__ __forceinline__ uint32_t quant_code(float r, const GroupParams& gp) {
+  return quant_code_bits<BITS>(r, gp) & ((1u << BITS) - 1u);
+}
+// Gather byte 0 of four dwords into one dword (b0 in bits 0..7).
+__device__ __forceinline__ uint32_t gather_bytes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
+  const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u);  // [b0.0, b1.0, 0, 0]
+  const uint32_t hi = __builtin_amdgcn_perm(b3, b2, 0x04000c0cu);  // [0, 0, b2.0, b3.0]
+  return lo | hi;
 }
 
 }  // namespace lrq

@@ -1,22 +1,37 @@
 // Group-mode decode and the fused elementwise consumers (SiLU backward, GELU backward,
-// elementwise product).  One streaming pass: codes, scales and L are read once, the
+// elementwise product).  One streaming pass: codes, qparams and L are read once, the
 // low-rank term L V^T is rebuilt on MFMA in the lanes that own the columns, and the
-// epilogue either stores x_hat (bf16, non-temporal) or applies the consumer with the
-// upstream gradient so the full-precision activation never goes back to HBM.
+// epilogue either stores x_hat (bf16) or applies the consumer with the
+// upstream gradient, so the full-precision activation never goes back to HBM.
+//
+// Work split: a workgroup is NW waves on NW consecutive units (G columns of every packing
+// plane, see lrq_common.h) of the same rows; each wave keeps its unit's V operands in
+// registers and walks its row blocks, prefetching the next block's codes, qparams and L
+// while it computes the current.
 #include "lrq_common.h"
 #include "lrq_host.h"
 
 namespace lrq {
 
 // ------------------------------------------------------------------ epilogues
-// Each receives 8 consecutive reconstructed values (fp32, before the bf16 rounding that
-// defines x_hat) for row `row`, columns col .. col + 7.
+// An epilogue binds its row pointers once per row block (`row(r)`), then receives 8
+// consecutive reconstructed values (fp32, before the bf16 rounding that defines x_hat)
+// for columns col .. col + 7 of that row.
 struct EpiStore {
   uint16_t* out;
   int64_t ld;
-  __device__ __forceinline__ void operator()(int64_t row, int col, const float* xh, bool rv) const {
-    if (rv) st16_stream(out + row * ld + col, pack8(xh));
+  struct Row {
+    uint16_t* o;
+  };
+  __device__ __forceinline__ Row row(int64_t r) const { return Row{out + r * ld}; }
+  __device__ __forceinline__ void operator()(const Row& r, int col, const float* xh, bool rv) const {
+    if (rv) st16(r.o + col, pack8(xh));
   }
+};
+
+struct RowIO {
+  const uint16_t* in;
+  uint16_t* o;
 };
 
 // silu_backward.py:6-8: dy * (s * (1 + x * (1 - s))), s = sigmoid(x), x = bf16(x_hat); fp32.
@@ -25,17 +40,19 @@ struct EpiSilu {
   int64_t lddy;
   uint16_t* dx;
   int64_t lddx;
-  __device__ __forceinline__ void operator()(int64_t row, int col, const float* xh, bool rv) const {
+  using Row = RowIO;
+  __device__ __forceinline__ Row row(int64_t r) const { return Row{dy + r * lddy, dx + r * lddx}; }
+  __device__ __forceinline__ void operator()(const Row& r, int col, const float* xh, bool rv) const {
     if (!rv) return;
     float d[8], o[8];
-    unpack8(ld16_stream(dy + row * lddy + col), d);
+    unpack8(ld16_stream(r.in + col), d);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float x = bf16_roundtrip(xh[e]);
       const float s = __builtin_amdgcn_rcpf(1.f + __expf(-x));
       o[e] = d[e] * (s * (1.f + x * (1.f - s)));
     }
-    st16_stream(dx + row * lddx + col, pack8(o));
+    st16(r.o + col, pack8(o));
   }
 };
 
@@ -45,11 +62,13 @@ struct EpiGelu {
   int64_t lddy;
   uint16_t* dx;
   int64_t lddx;
-  __device__ __forceinline__ void operator()(int64_t row, int col, const float* xh, bool rv) const {
+  using Row = RowIO;
+  __device__ __forceinline__ Row row(int64_t r) const { return Row{dy + r * lddy, dx + r * lddx}; }
+  __device__ __forceinline__ void operator()(const Row& r, int col, const float* xh, bool rv) const {
     if (!rv) return;
     constexpr float kGamma = 0.7978845608028654f, kKappa = 0.044715f;
     float d[8], o[8];
-    unpack8(ld16_stream(dy + row * lddy + col), d);
+    unpack8(ld16_stream(r.in + col), d);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float x = bf16_roundtrip(xh[e]);
@@ -59,7 +78,7 @@ struct EpiGelu {
       const float th = 1.f - 2.f * __builtin_amdgcn_rcpf(__expf(2.f * u) + 1.f);
       o[e] = 0.5f * ((1.f + th) + x * ((1.f - th * th) * kGamma * (1.f + 3.f * kKappa * x2))) * d[e];
     }
-    st16_stream(dx + row * lddx + col, pack8(o));
+    st16(r.o + col, pack8(o));
   }
 };
 
@@ -69,33 +88,44 @@ struct EpiMul {
   int64_t ldy;
   uint16_t* out;
   int64_t ldo;
-  __device__ __forceinline__ void operator()(int64_t row, int col, const float* xh, bool rv) const {
+  using Row = RowIO;
+  __device__ __forceinline__ Row row(int64_t r) const { return Row{y + r * ldy, out + r * ldo}; }
+  __device__ __forceinline__ void operator()(const Row& r, int col, const float* xh, bool rv) const {
     if (!rv) return;
     float a[8], o[8];
-    unpack8(ld16_stream(y + row * ldy + col), a);
+    unpack8(ld16_stream(r.in + col), a);
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = bf16_roundtrip(xh[e]) * a[e];
-    st16_stream(out + row * ldo + col, pack8(o));
+    st16(r.o + col, pack8(o));
   }
 };
 
 // ------------------------------------------------------------------ kernel
-// Grid: (ceil(rows / 64), ceil(units / upb)), 256 threads = 4 waves x 16 rows.  A unit is
-// CPG = G/32 consecutive chunks of every packing plane (see lrq_quant.h); the 8 bytes lane
-// (j, g) reads for chunk k hold the codes of columns c0 + 8g + e of all NP planes.
-template <int BITS, int G, int R, bool OUTL, class EPI>
-__global__ __launch_bounds__(256) void k_decode(
-    const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ scale,
-    const uint16_t* __restrict__ zero, int64_t ldsz, const uint16_t* __restrict__ Lin, int64_t ldl,
-    const uint16_t* __restrict__ V, int M, int N, const int32_t* __restrict__ oidx, int nout,
-    const uint16_t* __restrict__ side, int64_t ldside, int upb, EPI epi) {
-  constexpr int NP = 8 / BITS, CPG = G / 32, RT = R > 0 ? R / 16 : 1;
+// Per-row-block inputs of one lane: its G/4 code bytes, the unit's NP (scale, zero) pairs
+// and the L operand of its row.
+template <int BITS, int G, int R>
+struct DecIn {
+  u32x4 cb[G / 64];
+  uint32_t qp[8 / BITS];
+  u32x2 lop[R > 0 ? R / 16 : 1];
+};
+
+// Grid: (ceil(row blocks / rbw), ceil(units / NW)); NW waves; wave w owns unit
+// blockIdx.y * NW + w and walks row blocks blockIdx.x * rbw + b, b < rbw.  The waves of a
+// workgroup work on consecutive units of the same rows, so at any time a workgroup writes
+// NW * G * 2 contiguous bytes per row and plane (DRAM-page friendly), while each wave
+// reuses its unit's V operands for all its row blocks.
+template <int BITS, int G, int R, bool OUTL, int NW, class EPI>
+__global__ __launch_bounds__(NW * 64) void k_decode(
+    const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
+    const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
+    const int32_t* __restrict__ oidx, int nout, const uint16_t* __restrict__ side, int64_t ldside, int rbw,
+    EPI epi) {
+  constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, E = G / 4;
   constexpr uint32_t kMask = (1u << BITS) - 1u;
   extern __shared__ uint32_t smem[];
-  uint32_t* colmask = smem;                               // N/32 words
+  uint32_t* colmask = smem;                                    // N/32 words
   int16_t* slot = reinterpret_cast<int16_t*>(smem + N / 32);  // N entries
-  const int PC = N / (32 * NP);
-  const int units = PC / CPG;
   if constexpr (OUTL) {
     for (int i = threadIdx.x; i < N / 32; i += blockDim.x) colmask[i] = 0u;
     for (int i = threadIdx.x; i < N; i += blockDim.x) slot[i] = -1;
@@ -111,75 +141,115 @@ __global__ __launch_bounds__(256) void k_decode(
   }
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
-  const int row = blockIdx.x * 64 + w * 16 + j;
-  const bool rv = row < M;
-  const int64_t rr = rv ? row : 0;
-  u32x2 lop[RT];
+  const int u = blockIdx.y * NW + w;
+  if (u >= N / (G * NP)) return;  // tail workgroup of a row: idle wave (no barrier follows)
+  const int nrb = (M + 15) / 16;
+
+  u32x2 vop[NP][G / 16][RT];
   if constexpr (R > 0) {
 #pragma unroll
-    for (int t = 0; t < RT; ++t) lop[t] = rv ? ld8(Lin + rr * ldl + 16 * t + 4 * g) : u32x2{0u, 0u};
+    for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, u, N, NP, G), j, g, vop[p]);
   }
-  const uint8_t* crow = codes + rr * ldc;
-  for (int ui = 0; ui < upb; ++ui) {
-    const int u = blockIdx.y * upb + ui;
-    if (u >= units) break;
-    const int cu = u * CPG;
-    u32x2 cb[CPG];
+
+  auto load = [&](DecIn<BITS, G, R>& in, int rb, bool valid) {
+    const int64_t row = valid ? min(rb * 16 + j, M - 1) : 0;
+    const uint8_t* cp = codes + row * ldc + u * G + E * g;
 #pragma unroll
-    for (int k = 0; k < CPG; ++k) cb[k] = rv ? ld8_stream(crow + (cu + k) * 32 + 8 * g) : u32x2{0u, 0u};
+    for (int i = 0; i < G / 64; ++i) in.cb[i] = ld16_stream(cp + 16 * i);
+    const uint16_t* qpp = qparams + row * ldq + u * NP * 2;
+    if constexpr (NP == 2) {
+      const u32x2 v = ld8(qpp);
+      in.qp[0] = v[0];
+      in.qp[1] = v[1];
+    } else {
+      in.qp[0] = ld4(qpp);
+    }
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t) in.lop[t] = ld8(Lin + row * ldl + 16 * t + 4 * g);
+    }
+  };
+
+  auto compute = [&](const DecIn<BITS, G, R>& in, int rb) {
+    const int row = rb * 16 + j;
+    const bool rv = row < M;
+    const int64_t rr = rv ? row : M - 1;
+    const typename EPI::Row erow = epi.row(rr);
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-      const int gi = ((p * PC + cu) * 32) / G;
-      const float sf = f16_val(scale[rr * ldsz + gi]);
-      const float zf = f16_val(zero[rr * ldsz + gi]);
+      const float sf = f16_val(in.qp[p] & 0xffffu);
+      const float zf = f16_val(in.qp[p] >> 16);
+      float xh[E];
 #pragma unroll
-      for (int k = 0; k < CPG; ++k) {
-        const int c0 = (p * PC + cu + k) * 32;
-        float xh[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t code = (cb[k][e >> 2] >> (8 * (e & 3) + BITS * p)) & kMask;
-          xh[e] = __builtin_fmaf((float)code, sf, zf);  // code * scale is exact
-        }
-        if constexpr (R > 0) {
-          float pl[8];
-          lowrank_chunk<R>(V, c0, j, g, lop, pl);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) xh[e] = __fadd_rn(xh[e], pl[e]);
-        }
-        if constexpr (OUTL) {
-          const uint32_t mbits = (colmask[c0 >> 5] >> (8 * g)) & 0xffu;
-          if (mbits && rv) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-              if ((mbits >> e) & 1u) xh[e] = f16_val(side[rr * ldside + slot[c0 + 8 * g + e]]);
-          }
-        }
-        epi(rr, c0 + 8 * g, xh, rv);
+      for (int d = 0; d < E / 4; ++d) {
+        // the codes of plane p for elements 4d .. 4d+3, one per byte
+        const uint32_t wd = in.cb[d >> 2][d & 3];
+        const uint32_t wq = NP == 1 ? wd : ((wd >> (BITS * p)) & (0x01010101u * kMask));
+        // code * scale is exact, so the fma rounds once, like the oracle's mul + add
+        xh[4 * d + 0] = __builtin_fmaf(ubyte_f32<0>(wq), sf, zf);
+        xh[4 * d + 1] = __builtin_fmaf(ubyte_f32<1>(wq), sf, zf);
+        xh[4 * d + 2] = __builtin_fmaf(ubyte_f32<2>(wq), sf, zf);
+        xh[4 * d + 3] = __builtin_fmaf(ubyte_f32<3>(wq), sf, zf);
       }
+      if constexpr (R > 0) {
+        float pl[E];
+        lowrank_unit<G, R>(vop[p], in.lop, pl);
+#pragma unroll
+        for (int e = 0; e < E; ++e) xh[e] = __fadd_rn(xh[e], pl[e]);
+      }
+      const int c0 = unit_base(p, u, N, NP, G) + E * g;
+      if constexpr (OUTL) {
+        const uint32_t mbits = colmask[c0 >> 5] >> (c0 & 31);
+        if (mbits != 0u && rv) {
+#pragma unroll
+          for (int e = 0; e < E; ++e)
+            if ((mbits >> e) & 1u) xh[e] = f16_val(side[rr * ldside + slot[c0 + e]]);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < E / 8; ++k) epi(erow, c0 + 8 * k, xh + 8 * k, rv);
     }
+  };
+
+  const int rb0 = blockIdx.x * rbw;
+  if (rb0 >= nrb) return;
+  DecIn<BITS, G, R> cur, nxt;
+  load(cur, rb0, true);
+  for (int b = 0; b < rbw; ++b) {
+    const int rb = rb0 + b;
+    const int rbn = rb + 1;
+    const bool more = (b + 1 < rbw) && (rbn < nrb);
+    load(nxt, rbn, more);
+    compute(cur, rb);
+    if (!more) break;
+    cur = nxt;
   }
 }
 
 // ------------------------------------------------------------------ host side
 template <int BITS, int G, int R, class EPI>
 static int decode_launch(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
-  constexpr int NP = 8 / BITS, CPG = G / 32;
+  constexpr int NP = 8 / BITS, NW = 8;
   const int M = (int)t->rows, N = (int)t->hidden;
-  const int units = N / (32 * NP) / CPG;
-  const int upb = units >= 16 ? 4 : 1;
-  dim3 grid((M + 63) / 64, (units + upb - 1) / upb);
+  const int units = N / (G * NP);
+  const int nrb = (M + 15) / 16;
+  const int ugroups = (units + NW - 1) / NW;
+  // as many row blocks per wave as keeps >= 512 workgroups (2 per CU), at most 8: the unit's
+  // V operands are loaded once per wave
+  int rbw = 8;
+  while (rbw > 1 && (int64_t)((nrb + rbw - 1) / rbw) * ugroups < 512) rbw >>= 1;
+  dim3 grid((nrb + rbw - 1) / rbw, ugroups);
   if (t->n_outlier > 0) {
     const size_t shm = (size_t)(N / 32) * 4 + (size_t)N * 2;
-    hipLaunchKernelGGL((k_decode<BITS, G, R, true, EPI>), grid, dim3(256), shm, s, (const uint8_t*)t->codes,
-                       t->ld_codes, (const uint16_t*)t->scale, (const uint16_t*)t->zero, t->ld_sz,
-                       (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, t->outlier_idx,
-                       t->n_outlier, (const uint16_t*)t->side, t->ld_side, upb, epi);
+    hipLaunchKernelGGL((k_decode<BITS, G, R, true, NW, EPI>), grid, dim3(NW * 64), shm, s,
+                       (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
+                       (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, t->outlier_idx, t->n_outlier,
+                       (const uint16_t*)t->side, t->ld_side, rbw, epi);
   } else {
-    hipLaunchKernelGGL((k_decode<BITS, G, R, false, EPI>), grid, dim3(256), 0, s, (const uint8_t*)t->codes,
-                       t->ld_codes, (const uint16_t*)t->scale, (const uint16_t*)t->zero, t->ld_sz,
+    hipLaunchKernelGGL((k_decode<BITS, G, R, false, NW, EPI>), grid, dim3(NW * 64), 0, s,
+                       (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
                        (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, nullptr, 0, nullptr,
-                       (int64_t)0, upb, epi);
+                       (int64_t)0, rbw, epi);
   }
   return launch_status();
 }
@@ -201,8 +271,9 @@ static int decode_dispatch(const lrq_tensors* t, hipStream_t s, const EPI& epi) 
   }
 }
 
-static int check_io(const lrq_tensors* t, const void* in, int64_t ldin, const void* out, int64_t ldout, bool need_in) {
-  int st = validate_tensors(t, 0);
+static int check_io(const lrq_tensors* t, const void* in, int64_t ldin, const void* out, int64_t ldout,
+                    bool need_in) {
+  int st = validate_tensors(t);
   if (st) return st;
   if (need_in) {
     st = validate_rows16(in, ldin, t->hidden);

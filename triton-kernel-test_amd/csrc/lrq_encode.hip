@@ -1,101 +1,173 @@
 // Group-mode encode: projection L = bf16(X V), residual R = X - L V^T, per-group
 // asymmetric quantisation and row-planar packing.
 //
-// Two implementations, chosen per call by lrq_encode():
-//   * k_encode_fused — one pass over X.  A workgroup owns 16 full rows; its NW waves
-//     split the hidden dimension and keep their share of X in registers (the row is
-//     needed twice: once for the projection, once for the residual, and only a whole
-//     row gives L).  Partial L tiles are reduced across waves through LDS.  Instantiated
-//     for the hidden sizes listed in encode_fused_dispatch().
-//   * k_project + k_quant — two passes for any other hidden size (and rank 0 without
-//     the projection): X is read twice.
+// Implementations, chosen per call by lrq_encode():
+//   * k_encode_persist — one pass over X, persistent (one workgroup per CU).  The NW waves
+//     split the hidden dimension into units; each wave keeps the reconstruction operands of
+//     its units (V rows) in registers for the whole kernel, and its share of the current
+//     16-row block of X in registers while the next block streams in (double buffer).  The
+//     projection's V^T operand is regenerated from the register-resident V operand with an
+//     identity MFMA, so V is read from memory once per workgroup.  Partial L tiles are
+//     reduced across waves through LDS behind a barrier that does not wait for the prefetch.
+//   * k_project + k_quant — two passes for other shapes (rank 32, hidden sizes without a
+//     persistent instantiation); X is read twice.  k_quant alone is the whole rank-0 encode
+//     (with optional outlier channels).
 #include "lrq_common.h"
-#include "lrq_quant.h"
 #include "lrq_host.h"
+#include "lrq_quant.h"
 
 namespace lrq {
 
 // -------------------------------------------------------------------------------------
-// Single-pass encode.  Grid: ceil(rows / 16) workgroups of NW waves.  Wave w owns chunks
-// [w*CPW, (w+1)*CPW) of every packing plane; the host guarantees hidden == NW*CPW*32*NP.
-template <int BITS, int G, int R, int NW, int CPW>
-__global__ __launch_bounds__(NW * 64) void k_encode_fused(
+// Persistent single-pass encode.  Grid: min(row blocks, CUs) workgroups of NW waves; wave w
+// owns units [w*UPW, (w+1)*UPW).  The host guarantees N == NW*UPW*G*NP and R == 16*RT.
+// VLDS: the waves' V operands live in LDS (read right before each use) instead of registers,
+// which leaves room for the double-buffered X tile.
+template <int BITS, int G, int R, int NW, int UPW>
+struct PersistLds {
+  static constexpr int kVopPerWave = UPW * (8 / BITS) * (G / 16) * (R / 16);  // u32x2 per lane
+  static constexpr size_t kVopBytes = (size_t)NW * kVopPerWave * 64 * 8;
+  static constexpr size_t kRedBytes = (size_t)2 * NW * (R / 16) * 64 * 16;
+};
+
+template <int BITS, int G, int R, int NW, int UPW, bool DB, bool VLDS>
+__global__ __launch_bounds__(NW * 64) void k_encode_persist(
     const uint16_t* __restrict__ X, int64_t ldx, int M, int N, const uint16_t* __restrict__ V,
-    const uint16_t* __restrict__ Vt, uint16_t* __restrict__ Lout, int64_t ldl,
-    uint8_t* __restrict__ codes, int64_t ldc, uint16_t* __restrict__ scale,
-    uint16_t* __restrict__ zero, int64_t ldsz) {
-  constexpr int NP = 8 / BITS, CPG = G / 32, RT = R / 16;
-  static_assert(CPW % CPG == 0, "a wave must own whole groups");
-  constexpr int PC = NW * CPW;  // chunks per plane
-  __shared__ f32x4 red[NW * RT * 64];
+    uint16_t* __restrict__ Lout, int64_t ldl, uint8_t* __restrict__ codes, int64_t ldc,
+    uint16_t* __restrict__ qparams, int64_t ldq) {
+  constexpr int NP = 8 / BITS, CPG = G / 32, RT = R / 16, E = G / 4;
+  using Lds = PersistLds<BITS, G, R, NW, UPW>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char shm[];
+  f32x4* red = reinterpret_cast<f32x4*>(shm);                          // [2][NW*RT*64]
+  u32x2* vlds = reinterpret_cast<u32x2*>(shm + Lds::kRedBytes);        // [NW][kVopPerWave][64]
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
-  const int row = blockIdx.x * 16 + j;
-  const bool rv = row < M;
-  const uint16_t* xrow = X + (int64_t)(rv ? row : 0) * ldx;
+  const int nrb = (M + 15) / 16;
+  const int stride = gridDim.x;
 
-  u32x4 xr[NP][CPW];
+  u32x2 vreg[VLDS ? 1 : UPW][NP][G / 16][RT];
 #pragma unroll
-  for (int p = 0; p < NP; ++p)
+  for (int uu = 0; uu < UPW; ++uu)
 #pragma unroll
-    for (int k = 0; k < CPW; ++k) {
-      const int col = (p * PC + w * CPW + k) * 32 + 8 * g;
-      xr[p][k] = rv ? ld16_stream(xrow + col) : u32x4{0u, 0u, 0u, 0u};
+    for (int p = 0; p < NP; ++p) {
+      u32x2 tmp[G / 16][RT];
+      load_vops<G, R>(V, unit_base(p, w * UPW + uu, N, NP, G), j, g, tmp);
+#pragma unroll
+      for (int q = 0; q < G / 16; ++q)
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+          if constexpr (VLDS)
+            vlds[(w * Lds::kVopPerWave + ((uu * NP + p) * (G / 16) + q) * RT + t) * 64 + lane] = tmp[q][t];
+          else
+            vreg[uu][p][q][t] = tmp[q][t];
+        }
     }
-
-  // Projection, transposed: D(rank, row) += Vt(rank, cols) * X^T(cols, row).  Lane (j, g)
-  // ends up with L[row j][16t + 4g + v], v = 0..3 — the B-operand layout of the residual.
-  f32x4 acc[RT];
+  // V operands of unit uu, plane p (from registers, or LDS where this wave wrote them)
+  auto vops = [&](int uu, int p, u32x2 (&out)[G / 16][RT]) {
 #pragma unroll
-  for (int t = 0; t < RT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int p = 0; p < NP; ++p)
-#pragma unroll
-    for (int k = 0; k < CPW; ++k) {
-      const int col = (p * PC + w * CPW + k) * 32 + 8 * g;
+    for (int q = 0; q < G / 16; ++q)
 #pragma unroll
       for (int t = 0; t < RT; ++t) {
-        const u32x4 a = ld16(Vt + (int64_t)(16 * t + j) * N + col);
-        acc[t] = mfma_16x16x32(a, xr[p][k], acc[t]);
+        if constexpr (VLDS)
+          out[q][t] = vlds[(w * Lds::kVopPerWave + ((uu * NP + p) * (G / 16) + q) * RT + t) * 64 + lane];
+        else
+          out[q][t] = vreg[VLDS ? 0 : uu][p][q][t];
       }
-    }
-#pragma unroll
-  for (int t = 0; t < RT; ++t) red[(w * RT + t) * 64 + lane] = acc[t];
-  __syncthreads();
-  u32x2 lop[RT];
-#pragma unroll
-  for (int t = 0; t < RT; ++t) {
-    f32x4 s = red[t * 64 + lane];
-#pragma unroll
-    for (int w2 = 1; w2 < NW; ++w2) {
-      const f32x4 o = red[(w2 * RT + t) * 64 + lane];
-      s[0] += o[0];
-      s[1] += o[1];
-      s[2] += o[2];
-      s[3] += o[3];
-    }
-    lop[t] = u32x2{pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3])};
-    if (w == 0 && rv) st8(Lout + (int64_t)row * ldl + 16 * t + 4 * g, lop[t]);
-  }
+  };
+  const u32x2 ident = identity_bop(j, g);
 
-  uint8_t* crow = codes + (int64_t)row * ldc;
-  uint16_t* srow = scale + (int64_t)row * ldsz;
-  uint16_t* zrow = zero + (int64_t)row * ldsz;
+  // Load the lane's share of row block rb; when !valid every lane reads X[0..15] instead
+  // (one cached line) so the instruction stream — and the wait counts — stay uniform.
+  auto load = [&](u32x4 (&x)[UPW][NP][CPG], int rb, bool valid) {
+    const int row = min(rb * 16 + j, M - 1);
+    const uint16_t* xr = X + (int64_t)row * ldx + E * g;
 #pragma unroll
-  for (int u = 0; u < CPW / CPG; ++u) {
-    u32x4 xu[NP][CPG];
+    for (int uu = 0; uu < UPW; ++uu)
 #pragma unroll
-    for (int p = 0; p < NP; ++p)
+      for (int p = 0; p < NP; ++p)
 #pragma unroll
-      for (int k = 0; k < CPG; ++k) xu[p][k] = xr[p][u * CPG + k];
-    quant_unit<BITS, G, R>(xu, w * CPW + u * CPG, PC, V, lop, nullptr, j, g, rv, crow, srow, zrow);
+        for (int k = 0; k < CPG; ++k) {
+          const uint16_t* a = xr + unit_base(p, w * UPW + uu, N, NP, G) + 8 * k;
+          x[uu][p][k] = ld16_stream(valid ? a : X);
+        }
+  };
+
+  auto process = [&](const u32x4 (&x)[UPW][NP][CPG], int rb, int parity) {
+    const int row = rb * 16 + j;
+    const bool rv = row < M;
+    f32x4 acc[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) acc[t] = zero4();
+#pragma unroll
+    for (int uu = 0; uu < UPW; ++uu)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        u32x2 v[G / 16][RT];
+        vops(uu, p, v);
+        project_unit<G, R>(v, x[uu][p], ident, acc);
+      }
+    f32x4* rp = red + parity * (NW * RT * 64);
+#pragma unroll
+    for (int t = 0; t < RT; ++t) rp[(w * RT + t) * 64 + lane] = acc[t];
+    lds_barrier();
+    u32x2 lop[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      f32x4 s = rp[t * 64 + lane];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; ++w2) {
+        const f32x4 o = rp[(w2 * RT + t) * 64 + lane];
+        s[0] += o[0];
+        s[1] += o[1];
+        s[2] += o[2];
+        s[3] += o[3];
+      }
+      lop[t] = u32x2{pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3])};
+      if (w == 0 && rv) st8(Lout + (int64_t)row * ldl + 16 * t + 4 * g, lop[t]);
+    }
+    uint8_t* crow = codes + (int64_t)row * ldc;
+    uint16_t* qrow = qparams + (int64_t)row * ldq;
+#pragma unroll
+    for (int uu = 0; uu < UPW; ++uu) {
+      u32x2 v[NP][G / 16][RT];
+#pragma unroll
+      for (int p = 0; p < NP; ++p) vops(uu, p, v[p]);
+      quant_unit<BITS, G, R>(x[uu], v, lop, nullptr, w * UPW + uu, N, g, rv, crow, qrow);
+    }
+  };
+
+  u32x4 xa[UPW][NP][CPG];
+  int rb = blockIdx.x;
+  load(xa, rb, true);
+  if constexpr (DB) {
+    u32x4 xb[UPW][NP][CPG];
+    for (;;) {
+      const int rb1 = rb + stride;
+      load(xb, rb1, rb1 < nrb);
+      process(xa, rb, 0);
+      if (rb1 >= nrb) break;
+      const int rb2 = rb1 + stride;
+      load(xa, rb2, rb2 < nrb);
+      process(xb, rb1, 1);
+      if (rb2 >= nrb) break;
+      rb = rb2;
+    }
+  } else {
+    int parity = 0;
+    for (;;) {
+      process(xa, rb, parity);
+      rb += stride;
+      if (rb >= nrb) break;
+      load(xa, rb, true);
+      parity ^= 1;
+    }
   }
 }
 
 // -------------------------------------------------------------------------------------
 // Projection only (first pass of the two-pass encode).  Grid: ceil(rows / 16) workgroups
-// of 4 waves; wave w sums chunks w, w + 4, ... of the row.
+// of 4 waves; wave w sums 32-column chunks w, w + 4, ... of the row.  Uses V^T [R, N].
 template <int R>
 __global__ __launch_bounds__(256) void k_project(const uint16_t* __restrict__ X, int64_t ldx, int M,
                                                  int N, const uint16_t* __restrict__ Vt,
@@ -110,7 +182,7 @@ __global__ __launch_bounds__(256) void k_project(const uint16_t* __restrict__ X,
   const int NC = N / 32;
   f32x4 acc[RT];
 #pragma unroll
-  for (int t = 0; t < RT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < RT; ++t) acc[t] = zero4();
   for (int c = w; c < NC; c += NWV * U) {
     u32x4 xv[U];
 #pragma unroll
@@ -153,19 +225,17 @@ __global__ __launch_bounds__(256) void k_project(const uint16_t* __restrict__ X,
 }
 
 // -------------------------------------------------------------------------------------
-// Streaming residual + quantisation (second pass; also the whole encode at rank 0).
-// Grid: (ceil(rows / 64), ceil(units / upb)); a workgroup is 4 waves x 16 rows and walks
-// `upb` units.  With OUTL, outlier columns are zeroed before the group statistics.
-template <int BITS, int G, int R, bool OUTL>
+// Streaming residual + quantisation given L (second pass; the whole encode at rank 0).
+// Grid: (ceil(rows / (64*RB)), units); a workgroup is 4 waves on the same unit, each wave
+// walking RB row blocks, so the unit's V operands are loaded once per wave.  With OUTL,
+// outlier columns are zeroed before the group statistics.
+template <int BITS, int G, int R, int RB, bool OUTL>
 __global__ __launch_bounds__(256) void k_quant(
     const uint16_t* __restrict__ X, int64_t ldx, int M, int N, const uint16_t* __restrict__ V,
     const uint16_t* __restrict__ Lin, int64_t ldl, uint8_t* __restrict__ codes, int64_t ldc,
-    uint16_t* __restrict__ scale, uint16_t* __restrict__ zero, int64_t ldsz,
-    const int32_t* __restrict__ oidx, int nout, int upb) {
-  constexpr int NP = 8 / BITS, CPG = G / 32, RT = R > 0 ? R / 16 : 1;
+    uint16_t* __restrict__ qparams, int64_t ldq, const int32_t* __restrict__ oidx, int nout) {
+  constexpr int NP = 8 / BITS, CPG = G / 32, RT = R > 0 ? R / 16 : 1, E = G / 4;
   extern __shared__ uint32_t colmask[];
-  const int PC = N / (32 * NP);
-  const int units = PC / CPG;
   if constexpr (OUTL) {
     for (int i = threadIdx.x; i < N / 32; i += blockDim.x) colmask[i] = 0u;
     __syncthreads();
@@ -177,30 +247,29 @@ __global__ __launch_bounds__(256) void k_quant(
   }
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
-  const int row = blockIdx.x * 64 + w * 16 + j;
-  const bool rv = row < M;
-  const int64_t rr = rv ? row : 0;
-  const uint16_t* xrow = X + rr * ldx;
-  u32x2 lop[RT];
+  const int u = blockIdx.y;
+  u32x2 vop[NP][G / 16][RT];
   if constexpr (R > 0) {
 #pragma unroll
-    for (int t = 0; t < RT; ++t)
-      lop[t] = rv ? ld8(Lin + rr * ldl + 16 * t + 4 * g) : u32x2{0u, 0u};
+    for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, u, N, NP, G), j, g, vop[p]);
   }
-  uint8_t* crow = codes + rr * ldc;
-  uint16_t* srow = scale + rr * ldsz;
-  uint16_t* zrow = zero + rr * ldsz;
-  for (int ui = 0; ui < upb; ++ui) {
-    const int u = blockIdx.y * upb + ui;
-    if (u >= units) break;
-    const int cu = u * CPG;
-    u32x4 xu[NP][CPG];
+  for (int b = 0; b < RB; ++b) {
+    const int row = (blockIdx.x * RB + b) * 64 + w * 16 + j;
+    if (row - j >= M) break;  // whole 16-row block past the end (uniform per wave)
+    const bool rv = row < M;
+    const int64_t rr = rv ? row : M - 1;
+    u32x2 lop[RT];
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t) lop[t] = ld8(Lin + rr * ldl + 16 * t + 4 * g);
+    }
+    u32x4 x[NP][CPG];
 #pragma unroll
     for (int p = 0; p < NP; ++p)
 #pragma unroll
-      for (int k = 0; k < CPG; ++k)
-        xu[p][k] = rv ? ld16_stream(xrow + (p * PC + cu + k) * 32 + 8 * g) : u32x4{0u, 0u, 0u, 0u};
-    quant_unit<BITS, G, R>(xu, cu, PC, V, lop, OUTL ? colmask : nullptr, j, g, rv, crow, srow, zrow);
+      for (int k = 0; k < CPG; ++k) x[p][k] = ld16_stream(X + rr * ldx + unit_base(p, u, N, NP, G) + E * g + 8 * k);
+    quant_unit<BITS, G, R>(x, vop, lop, OUTL ? colmask : nullptr, u, N, g, rv, codes + rr * ldc,
+                           qparams + rr * ldq);
   }
 }
 
@@ -220,92 +289,107 @@ __global__ __launch_bounds__(256) void k_gather_side(const uint16_t* __restrict_
 // -------------------------------------------------------------------------------------
 // host side
 
-template <int BITS, int G, int R, int NW, int CPW>
-static int launch_fused(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s) {
-  dim3 grid((unsigned)((t->rows + 15) / 16));
-  hipLaunchKernelGGL((k_encode_fused<BITS, G, R, NW, CPW>), grid, dim3(NW * 64), 0, s,
-                     (const uint16_t*)x, ldx, (int)t->rows, (int)t->hidden, (const uint16_t*)t->V,
-                     (const uint16_t*)t->Vt, (uint16_t*)t->L, t->ld_L, (uint8_t*)t->codes, t->ld_codes,
-                     (uint16_t*)t->scale, (uint16_t*)t->zero, t->ld_sz);
+static int cu_count() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+  return n;
+}
+
+template <int BITS, int G, int R, int NW, int UPW, bool DB>
+static int launch_persist(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s) {
+  using Lds = PersistLds<BITS, G, R, NW, UPW>;
+  // Wide waves keep their V operands in LDS so the double-buffered X tile fits in registers.
+  constexpr bool VLDS = DB && UPW * G * (8 / BITS) >= 512 && Lds::kVopBytes + Lds::kRedBytes <= 160 * 1024;
+  const size_t shm = Lds::kRedBytes + (VLDS ? Lds::kVopBytes : 0);
+  auto kern = k_encode_persist<BITS, G, R, NW, UPW, DB, VLDS>;
+  if (shm > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+  const int nrb = (int)((t->rows + 15) / 16);
+  const int grid = nrb < cu_count() ? nrb : cu_count();
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), shm, s, (const uint16_t*)x, ldx, (int)t->rows,
+                     (int)t->hidden, (const uint16_t*)t->V, (uint16_t*)t->L, t->ld_L, (uint8_t*)t->codes,
+                     t->ld_codes, (uint16_t*)t->qparams, t->ld_qp);
   return launch_status();
 }
 
-template <int BITS, int G, int R, int NW, int CPW>
-static int try_fused(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s, int* status) {
-  if constexpr (CPW % (G / 32) == 0) {
-    *status = launch_fused<BITS, G, R, NW, CPW>(t, x, ldx, s);
-    return 1;
-  } else {
-    return 0;
-  }
-}
-
 // Returns 1 and launches when a single-pass kernel exists for this shape, else 0.
-// Chunks per plane (pc) = hidden / (32 * NP) is split over NW waves of CPW chunks.
 template <int BITS, int G, int R>
-static int encode_fused_dispatch(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s,
-                                 int* status) {
-  constexpr int NP = 8 / BITS;
-  const int64_t pc = t->hidden / (32 * NP);
-  switch (pc) {
-    case 16: return try_fused<BITS, G, R, 4, 4>(t, x, ldx, s, status);
-    case 32: return try_fused<BITS, G, R, 4, 8>(t, x, ldx, s, status);
-    case 64: return try_fused<BITS, G, R, 8, 8>(t, x, ldx, s, status);
-    case 80: return try_fused<BITS, G, R, 8, 10>(t, x, ldx, s, status);
-    default: return 0;
+static int encode_persist_dispatch(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s,
+                                   int* status) {
+  if constexpr (R != 16) {
+    return 0;
+  } else {
+    constexpr int NP = 8 / BITS;
+    // wide instantiations only where a wave's columns per unit (G*NP) keep it spill-free
+    constexpr bool wide_ok = G * NP <= 128;
+    const int64_t units = t->hidden / ((int64_t)G * NP);
+    switch (units) {
+      case 8: *status = launch_persist<BITS, G, R, 4, 2, true>(t, x, ldx, s); return 1;
+      case 16: *status = launch_persist<BITS, G, R, 8, 2, true>(t, x, ldx, s); return 1;
+      case 32:
+        if constexpr (wide_ok) {
+          *status = launch_persist<BITS, G, R, 8, 4, true>(t, x, ldx, s);
+          return 1;
+        }
+        return 0;
+      case 40:
+        if constexpr (wide_ok) {
+          *status = launch_persist<BITS, G, R, 8, 5, false>(t, x, ldx, s);
+          return 1;
+        }
+        return 0;
+      default: return 0;
+    }
   }
 }
 
 template <int BITS, int G, int R>
 static int encode_twopass(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s) {
   const int M = (int)t->rows, N = (int)t->hidden;
-  constexpr int NP = 8 / BITS, CPG = G / 32;
+  constexpr int NP = 8 / BITS, RB = 4;
   if constexpr (R > 0) {
-    hipLaunchKernelGGL((k_project<R>), dim3((M + 15) / 16), dim3(256), 0, s, (const uint16_t*)x, ldx, M,
-                       N, (const uint16_t*)t->Vt, (uint16_t*)t->L, t->ld_L);
+    hipLaunchKernelGGL((k_project<R>), dim3((M + 15) / 16), dim3(256), 0, s, (const uint16_t*)x, ldx, M, N,
+                       (const uint16_t*)t->Vt, (uint16_t*)t->L, t->ld_L);
     int st = launch_status();
     if (st) return st;
   }
-  const int units = N / (32 * NP) / CPG;
-  const int upb = 4;
-  dim3 grid((M + 63) / 64, (units + upb - 1) / upb);
-  const bool outl = t->n_outlier > 0;
-  if (outl) {
-    hipLaunchKernelGGL((k_quant<BITS, G, R, true>), grid, dim3(256), (size_t)(N / 32) * 4, s,
+  const int units = N / (G * NP);
+  dim3 grid((M + 64 * RB - 1) / (64 * RB), units);
+  if (t->n_outlier > 0) {
+    hipLaunchKernelGGL((k_quant<BITS, G, R, RB, true>), grid, dim3(256), (size_t)(N / 32) * 4, s,
                        (const uint16_t*)x, ldx, M, N, (const uint16_t*)t->V, (const uint16_t*)t->L, t->ld_L,
-                       (uint8_t*)t->codes, t->ld_codes, (uint16_t*)t->scale, (uint16_t*)t->zero, t->ld_sz,
-                       t->outlier_idx, t->n_outlier, upb);
+                       (uint8_t*)t->codes, t->ld_codes, (uint16_t*)t->qparams, t->ld_qp, t->outlier_idx,
+                       t->n_outlier);
     int st = launch_status();
     if (st) return st;
     const int64_t n = (int64_t)M * t->n_outlier;
     hipLaunchKernelGGL(k_gather_side, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const uint16_t*)x,
                        ldx, M, N, t->outlier_idx, t->n_outlier, (uint16_t*)t->side, t->ld_side);
   } else {
-    hipLaunchKernelGGL((k_quant<BITS, G, R, false>), grid, dim3(256), 0, s, (const uint16_t*)x, ldx, M, N,
-                       (const uint16_t*)t->V, (const uint16_t*)t->L, t->ld_L, (uint8_t*)t->codes,
-                       t->ld_codes, (uint16_t*)t->scale, (uint16_t*)t->zero, t->ld_sz, nullptr, 0, upb);
+    hipLaunchKernelGGL((k_quant<BITS, G, R, RB, false>), grid, dim3(256), 0, s, (const uint16_t*)x, ldx, M, N,
+                       (const uint16_t*)t->V, (const uint16_t*)t->L, t->ld_L, (uint8_t*)t->codes, t->ld_codes,
+                       (uint16_t*)t->qparams, t->ld_qp, nullptr, 0);
   }
   return launch_status();
 }
 
 template <int BITS, int G, int R>
 static int encode_impl(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s, int force_twopass) {
-  if constexpr (R > 0) {
-    int st = 0;
-    if (!force_twopass && t->n_outlier == 0 && encode_fused_dispatch<BITS, G, R>(t, x, ldx, s, &st)) return st;
-  }
+  int st = 0;
+  if (!force_twopass && t->n_outlier == 0 && encode_persist_dispatch<BITS, G, R>(t, x, ldx, s, &st)) return st;
+  if (R > 0 && t->Vt == nullptr) return LRQ_ERR_NULL;  // the two-pass projection reads V^T
   return encode_twopass<BITS, G, R>(t, x, ldx, s);
 }
 
 static int encode_entry(const lrq_tensors* t, const void* x, int64_t ldx, void* stream, int force_twopass) {
-  int st = validate_tensors(t, /*encode=*/1);
+  int st = validate_tensors(t);
   if (st) return st;
   if (x == nullptr) return LRQ_ERR_NULL;
-  if (ldx < t->hidden || (ldx % 8) != 0 || !aligned(x, 16)) return ldx < t->hidden ? LRQ_ERR_SHAPE : LRQ_ERR_ALIGN;
+  if (ldx < t->hidden) return LRQ_ERR_SHAPE;
+  if ((ldx % 8) != 0 || !aligned(x, 16)) return LRQ_ERR_ALIGN;
   if (t->rows == 0) return LRQ_OK;
   hipStream_t s = (hipStream_t)stream;
-  const int key = format_key(t->bits, t->group, t->rank);
-  switch (key) {
+  switch (format_key(t->bits, t->group, t->rank)) {
     case format_key(4, 64, 0): return encode_impl<4, 64, 0>(t, x, ldx, s, force_twopass);
     case format_key(4, 64, 16): return encode_impl<4, 64, 16>(t, x, ldx, s, force_twopass);
     case format_key(4, 64, 32): return encode_impl<4, 64, 32>(t, x, ldx, s, force_twopass);
@@ -325,7 +409,6 @@ extern "C" int lrq_encode(const lrq_tensors* t, const void* x, int64_t ldx, void
   return lrq::encode_entry(t, x, ldx, stream, 0);
 }
 
-// Test hook: the two-pass path for shapes that also have a single-pass kernel.
 extern "C" int lrq_encode_twopass(const lrq_tensors* t, const void* x, int64_t ldx, void* stream) {
   return lrq::encode_entry(t, x, ldx, stream, 1);
 }

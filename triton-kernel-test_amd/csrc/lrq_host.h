@@ -19,9 +19,8 @@ static inline int launch_status() {
   return e == hipSuccess ? LRQ_OK : (int)e;
 }
 
-// Validates a group-mode descriptor.  `encode` additionally requires Vt (projection
-// operand) when rank > 0.
-static inline int validate_tensors(const lrq_tensors* t, int encode) {
+// Validates a group-mode descriptor (Vt is checked by the two-pass encode, its only reader).
+static inline int validate_tensors(const lrq_tensors* t) {
   if (t == nullptr) return LRQ_ERR_NULL;
   if (t->rows < 0 || t->hidden <= 0 || t->rows > INT32_MAX || t->hidden > INT32_MAX) return LRQ_ERR_SHAPE;
   if (t->bits != 4 && t->bits != 8) return LRQ_ERR_UNSUPPORTED;
@@ -36,15 +35,14 @@ static inline int validate_tensors(const lrq_tensors* t, int encode) {
   }
   if (t->rank > 0) {
     if (t->L == nullptr || t->V == nullptr) return LRQ_ERR_NULL;
-    if (encode && t->Vt == nullptr) return LRQ_ERR_NULL;
     if (t->ld_L < t->rank) return LRQ_ERR_SHAPE;
     if ((t->ld_L % 4) != 0 || !aligned(t->L, 8) || !aligned(t->V, 8)) return LRQ_ERR_ALIGN;
-    if (encode && !aligned(t->Vt, 16)) return LRQ_ERR_ALIGN;
+    if (t->Vt != nullptr && !aligned(t->Vt, 16)) return LRQ_ERR_ALIGN;
   }
-  if (t->codes == nullptr || t->scale == nullptr || t->zero == nullptr) return LRQ_ERR_NULL;
-  if (t->ld_codes < t->hidden * t->bits / 8 || t->ld_sz < t->hidden / t->group) return LRQ_ERR_SHAPE;
-  if ((t->ld_codes % 8) != 0 || !aligned(t->codes, 8)) return LRQ_ERR_ALIGN;
-  if (!aligned(t->scale, 2) || !aligned(t->zero, 2)) return LRQ_ERR_ALIGN;
+  if (t->codes == nullptr || t->qparams == nullptr) return LRQ_ERR_NULL;
+  if (t->ld_codes < t->hidden * t->bits / 8 || t->ld_qp < 2 * (t->hidden / t->group)) return LRQ_ERR_SHAPE;
+  if ((t->ld_codes % 16) != 0 || !aligned(t->codes, 16)) return LRQ_ERR_ALIGN;
+  if ((t->ld_qp % 4) != 0 || !aligned(t->qparams, 8)) return LRQ_ERR_ALIGN;
   if (t->n_outlier < 0 || t->n_outlier > t->hidden) return LRQ_ERR_SHAPE;
   if (t->n_outlier > 0) {
     if (t->rank != 0) return LRQ_ERR_UNSUPPORTED;

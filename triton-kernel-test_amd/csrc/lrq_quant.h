@@ -1,76 +1,72 @@
-// Residual + per-group quantisation of one "unit" of columns, shared by the fused
-// single-pass encode and the streaming (second-pass / rank-0) encode.
-//
-// A unit is, for every packing plane p (NP = 8/BITS planes; plane p holds columns
-// [p*N/NP, (p+1)*N/NP)), the CPG = G/32 consecutive chunks starting at chunk `cu` of that
-// plane.  Lane (j, g) holds 8 columns of each chunk, so it holds 8*CPG elements of each
-// of the NP groups the unit covers; the other three lanes of row j hold the rest, and a
-// two-step xor-shuffle finishes the group min/max.
+// Residual + per-group quantisation of one unit (see lrq_common.h for the layout), shared
+// by the persistent single-pass encode and the streaming second-pass / rank-0 encode.
 #pragma once
 
 #include "lrq_common.h"
 
 namespace lrq {
 
+// x[p][k]: the lane's G/4 columns of plane p (bf16); vop[p]: reconstruction operands of the
+// unit-plane (unused when R == 0); lop: L operands of the lane's row; colmask: optional LDS
+// bitmap of outlier columns (zeroed before the statistics).  Writes the lane's G/4 code bytes
+// and, from lane g == 0, the unit's NP (scale, zero) pairs.
 template <int BITS, int G, int R>
-__device__ __forceinline__ void quant_unit(const u32x4 (&x)[8 / BITS][G / 32], int cu, int PC,
-                                           const uint16_t* __restrict__ V, const u32x2* lop,
-                                           const uint32_t* colmask, int j, int g, bool rv,
-                                           uint8_t* __restrict__ crow, uint16_t* __restrict__ srow,
-                                           uint16_t* __restrict__ zrow) {
-  constexpr int NP = 8 / BITS, CPG = G / 32;
-  uint32_t word[CPG][2];
-#pragma unroll
-  for (int k = 0; k < CPG; ++k) word[k][0] = word[k][1] = 0u;
+__device__ __forceinline__ void quant_unit(const u32x4 (&x)[8 / BITS][G / 32],
+                                           const u32x2 (&vop)[8 / BITS][G / 16][R > 0 ? R / 16 : 1],
+                                           const u32x2* lop, const uint32_t* colmask, int u, int N, int g,
+                                           bool rv, uint8_t* __restrict__ crow, uint16_t* __restrict__ qrow) {
+  constexpr int NP = 8 / BITS, E = G / 4;
+  static_assert(NP == 1 || NP == 2, "group mode packs 4- or 8-bit codes");
+  // byte[e]: the packed code byte of element e in bits 0..7 (higher bits are don't-care)
+  uint32_t byte[E];
+  uint32_t qp[NP];
 
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
-    float r[CPG][8];
-    float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+    float r[E];
 #pragma unroll
-    for (int k = 0; k < CPG; ++k) {
-      const int c0 = (p * PC + cu + k) * 32;
-      unpack8(x[p][k], r[k]);
-      if constexpr (R > 0) {
-        float pl[8];
-        lowrank_chunk<R>(V, c0, j, g, lop, pl);
+    for (int k = 0; k < G / 32; ++k) unpack8(x[p][k], r + 8 * k);
+    if constexpr (R > 0) {
+      float pl[E];
+      lowrank_unit<G, R>(vop[p], lop, pl);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) r[k][e] = __fsub_rn(r[k][e], pl[e]);
-      }
-      if (colmask != nullptr) {
-        const uint32_t mbits = colmask[c0 >> 5] >> (8 * g);
+      for (int e = 0; e < E; ++e) r[e] = __fsub_rn(r[e], pl[e]);
+    }
+    if (colmask != nullptr) {
+      const int c0 = unit_base(p, u, N, NP, G) + E * g;  // E consecutive columns in one mask word
+      const uint32_t mbits = colmask[c0 >> 5] >> (c0 & 31);
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if ((mbits >> e) & 1u) r[k][e] = 0.f;
-      }
+      for (int e = 0; e < E; ++e)
+        if ((mbits >> e) & 1u) r[e] = 0.f;
+    }
+    float mn = r[0], mx = r[0];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        mn = fminf(mn, r[k][e]);
-        mx = fmaxf(mx, r[k][e]);
-      }
+    for (int e = 1; e < E; ++e) {
+      mn = fminf(mn, r[e]);
+      mx = fmaxf(mx, r[e]);
     }
     mn = wave_min4(mn);
     mx = wave_max4(mx);
     const GroupParams gp = group_params<BITS>(mn, mx);
-    if (rv && g == 0) {
-      const int gi = ((p * PC + cu) * 32) / G;
-      srow[gi] = gp.sh;
-      zrow[gi] = gp.zh;
-    }
+    qp[p] = gp.sh | (gp.zh << 16);
 #pragma unroll
-    for (int k = 0; k < CPG; ++k) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t c = quant_code<BITS>(r[k][e], gp);
-        word[k][e >> 2] |= c << (8 * (e & 3) + BITS * p);
-      }
+    for (int e = 0; e < E; ++e) {
+      const uint32_t b = quant_code_bits<BITS>(r[e], gp);  // code in the low BITS bits
+      if constexpr (NP == 1) byte[e] = b;
+      else if (p == 0) byte[e] = b & 0xfu;
+      else byte[e] = (b << 4) | byte[e];
     }
   }
+  uint32_t word[E / 4];
+#pragma unroll
+  for (int i = 0; i < E / 4; ++i) word[i] = gather_bytes(byte[4 * i], byte[4 * i + 1], byte[4 * i + 2], byte[4 * i + 3]);
   if (rv) {
 #pragma unroll
-    for (int k = 0; k < CPG; ++k) {
-      u32x2 w2 = {word[k][0], word[k][1]};
-      st8(crow + (cu + k) * 32 + 8 * g, w2);
+    for (int i = 0; i < E / 16; ++i)
+      st16(crow + u * G + E * g + 16 * i, u32x4{word[4 * i], word[4 * i + 1], word[4 * i + 2], word[4 * i + 3]});
+    if (g == 0) {
+      if constexpr (NP == 2) st8(qrow + u * 4, u32x2{qp[0], qp[1]});
+      else if constexpr (NP == 1) st4(qrow + u * 2, qp[0]);
     }
   }
 }
