@@ -42,7 +42,7 @@ __all__ = [
     # Walsh-Hadamard
     "sylvester", "WHT_SCALE", "wht128_rows",
     # group mode
-    "projection", "lowrank_product", "quant_groups", "dequant_groups",
+    "projection", "lowrank_product", "fma32", "rcp32", "quant_groups", "dequant_groups",
     "encode", "decode", "reconstruct_f32",
     # outlier channels
     "colmax_abs", "topk_channels",
@@ -188,7 +188,8 @@ def projection(y: np.ndarray, v_bits: np.ndarray):
 
 
 def lowrank_product(l_bits: np.ndarray, v_bits: np.ndarray, row_index=None) -> np.ndarray:
-    """``P = fp32(exact(L @ V^T))`` with bf16 L [M', r] and V [N, r]; float32 [M, N].
+    """``L @ V^T`` with bf16 L [M', r] and V [N, r], exact in float64 (products of bf16 are
+    exact; the r-term sums are exact for ordinary exponent ranges).  float64 [M, N].
 
     ``row_index`` optionally maps output rows to rows of L (legacy batched form).
     """
@@ -196,7 +197,36 @@ def lowrank_product(l_bits: np.ndarray, v_bits: np.ndarray, row_index=None) -> n
     if row_index is not None:
         l = l[row_index]
     v = bf16_to_f32(v_bits).astype(np.float64)
-    return (l @ v.T).astype(np.float32)
+    return l @ v.T
+
+
+def fma32(a, b, c) -> np.ndarray:
+    """Correctly rounded float32 fused multiply-add ``round32(a*b + c)``.
+
+    a*b is exact in float64; the float64 sum is corrected with the exact TwoSum error, so
+    the one case where rounding the float64 sum to float32 could differ from rounding the
+    exact value (the sum landing exactly on a float32 midpoint) is resolved by the error's sign.
+    """
+    a = np.asarray(a, dtype=np.float32).astype(np.float64)
+    b = np.asarray(b, dtype=np.float32).astype(np.float64)
+    c = np.asarray(c, dtype=np.float32).astype(np.float64)
+    p = a * b
+    s = p + c
+    bp = s - c
+    e = (p - (s - bp)) + (c - bp)          # s + e == p + c exactly
+    r = s.astype(np.float32)
+    d = s - r.astype(np.float64)
+    away = np.nextafter(r, np.where(d >= 0, np.float32(np.inf), np.float32(-np.inf))).astype(np.float32)
+    half = np.abs(away.astype(np.float64) - r.astype(np.float64)) * 0.5
+    tie = (d != 0) & (np.abs(d) == half) & (e != 0)
+    flip = tie & (np.sign(e) == np.sign(d))
+    return np.where(flip, away, r).astype(np.float32)
+
+
+def rcp32(x) -> np.ndarray:
+    """Correctly rounded float32 reciprocal (what the kernels' rcp + Newton step returns for
+    every positive finite fp16 input)."""
+    return (np.float32(1.0) / np.asarray(x, dtype=np.float32)).astype(np.float32)
 
 
 def quant_groups(r: np.ndarray, bits: int, group: int):
@@ -204,11 +234,12 @@ def quant_groups(r: np.ndarray, bits: int, group: int):
 
     For each group of ``group`` consecutive columns of a row:
       mn, mx   = min, max of R (fp32)
-      scale_h  = fp16_rne(min((mx - mn) / (2^bits - 1), 65504)), replaced by 1 when 0
+      scale_h  = fp16_rne(min((mx - mn) * fp32(1/qmax), 65504)), replaced by 1 when 0
       zero_h   = fp16_rne(clamp(mn, +-65504))
-      inv      = 1 / fp32(scale_h)                       (fp32, correctly rounded)
-      t        = (R - fp32(zero_h)) * inv                (two fp32 roundings, no fma)
-      code     = clamp(rint(t), 0, 2^bits - 1)           (round half to even)
+      inv      = 1 / fp32(scale_h)              (fp32, correctly rounded)
+      nzi      = fp32(-fp32(zero_h) * inv)
+      t        = fma(R, inv, nzi)               (one rounding)
+      code     = clamp(rint(t), 0, qmax)        (round half to even), qmax = 2^bits - 1
     Returns (codes uint8 [.., N], scale fp16 [.., N/G], zero fp16 [.., N/G], t float32 [.., N]).
     Pinned by: codes in range, min/max map to the end codes, constant groups decode
     exactly, |decode - R| <= scale/2 (tests/test_oracle.py).
@@ -220,14 +251,14 @@ def quant_groups(r: np.ndarray, bits: int, group: int):
     rg = r.reshape(lead + (n // group, group))
     mn = rg.min(axis=-1)
     mx = rg.max(axis=-1)
-    scale_f = (mx - mn) / np.float32(qmax)
+    scale_f = (mx - mn) * np.float32(1.0 / qmax)
     scale_f = np.minimum(scale_f, np.float32(65504.0))
     scale_h = scale_f.astype(np.float16)
     scale_h = np.where(scale_h == 0, np.float16(1.0), scale_h)
     zero_h = f16_sat(mn)
-    inv = np.float32(1.0) / scale_h.astype(np.float32)
-    zf = zero_h.astype(np.float32)
-    t = (rg - zf[..., None]) * inv[..., None]
+    inv = rcp32(scale_h.astype(np.float32))
+    nzi = (-zero_h.astype(np.float32) * inv).astype(np.float32)
+    t = fma32(rg, inv[..., None], nzi[..., None])
     codes = np.clip(np.rint(t), 0, qmax).astype(np.uint8)
     return (codes.reshape(lead + (n,)), scale_h, zero_h, t.reshape(lead + (n,)).astype(np.float32))
 
@@ -248,7 +279,11 @@ def encode(x_bits: np.ndarray, v_bits, bits: int = 4, group: int = 64, hadamard:
       Y  = wht128_rows(x) if hadamard else fp32(x)
       side[:, k] = fp16(x[:, idx[k]]); Y[:, idx] = 0            (outlier channels, if any)
       L  = bf16(fp32(exact(Y @ V)))                              (if rank > 0)
-      P  = fp32(exact(L @ V^T)); R = Y - P                        (if rank > 0, else R = Y)
+      P  = fp32(exact(L @ V^T))                                  (if rank > 0)
+      R  = fp32(Y - P)                (the product is rounded first, then the difference,
+                                       as ``accumulator -= tl.dot(a, b)`` in
+                                       low_rank_extraction_fuse_compression_quantization.py:72
+                                       does; else R = Y)
       R[:, idx] = 0
       codes, scale, zero = quant_groups(R)
       packed = pack_rowplanar(codes)
@@ -274,7 +309,7 @@ def encode(x_bits: np.ndarray, v_bits, bits: int = 4, group: int = 64, hadamard:
             l_bits, l32 = projection(y, v_bits)
         else:
             l_bits, l32 = np.asarray(l_override, dtype=np.uint16), None
-        p = lowrank_product(l_bits, v_bits)
+        p = lowrank_product(l_bits, v_bits).astype(np.float32)  # the fp32 MMA result
         r = (y - p).astype(np.float32)
     else:
         l_bits, l32, p = None, None, None
@@ -288,11 +323,14 @@ def encode(x_bits: np.ndarray, v_bits, bits: int = 4, group: int = 64, hadamard:
 
 def reconstruct_f32(l_bits, v_bits, packed, scale, zero, bits: int, group: int, hadamard=False,
                     side=None, idx=None) -> np.ndarray:
-    """fp32 reconstruction before the final bf16 rounding (see ``decode``)."""
+    """fp32 reconstruction before the final bf16 rounding (see ``decode``).  The low-rank
+    term is added inside the accumulation (one rounding): ``accumulator += tl.dot(a, b)`` in
+    low_rank_extraction_fuse_decompression_dequantization.py:107 is an MMA with the
+    dequantised values as its accumulator input."""
     codes = unpack_rowplanar(np.asarray(packed, dtype=np.uint8), bits)
     y = dequant_groups(codes, scale, zero, group)
     if l_bits is not None and v_bits is not None and np.asarray(v_bits).shape[1] > 0:
-        y = (y + lowrank_product(l_bits, v_bits)).astype(np.float32)
+        y = (y.astype(np.float64) + lowrank_product(l_bits, v_bits)).astype(np.float32)  # one rounding
     if idx is not None and len(idx) > 0:
         y[:, np.asarray(idx)] = np.asarray(side, dtype=np.float16).astype(np.float32)
     if hadamard:
@@ -305,7 +343,7 @@ def decode(l_bits, v_bits, packed, scale, zero, bits: int, group: int, hadamard=
     """Group-mode decode: ``x_hat = bf16(reconstruct_f32(...))`` where
 
       d  = fp32(code) * scale + zero
-      Y' = d + P            (P = fp32(exact(L @ V^T)), rank > 0)
+      Y' = fp32(exact(d + L @ V^T))   (one rounding; rank > 0)
       Y'[:, idx] = side     (outlier channels)
       X' = wht128_rows(Y')  (rotation is its own inverse)
     Returns bf16 bits [M, N].

@@ -51,9 +51,10 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
 __device__ __forceinline__ float bf16_roundtrip(float f) { return __uint_as_float(pack_bf16x2(f, 0.f) << 16); }
-// Pack two fp32 values that are already exactly representable in bf16 (no rounding).
+// Pack two fp32 values that are already exactly representable in bf16 (no rounding): the
+// high halves of both, one v_perm_b32.
 __device__ __forceinline__ uint32_t pack_bf16x2_exact(float lo, float hi) {
-  return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
 // Byte K of w as fp32 (v_cvt_f32_ubyteK).  Written as asm so the compiler keeps one
@@ -106,6 +107,16 @@ __device__ __forceinline__ void st16_stream(void* p, u32x4 v) {
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
 
+// Predicated 8-byte store without a branch: a raw buffer store over the `len`-byte region at
+// the wave-uniform `base`; lanes with !keep use an offset past the region, which the
+// hardware drops.  (A branch around a store would make the compiler drain every
+// outstanding memory operation at the next use of a load — gfx9 counts loads and stores
+// in one in-order counter.)
+__device__ __forceinline__ void st8_pred(void* base, uint32_t len, uint32_t off, u32x2 v, bool keep) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)len, 0x00020000);
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, keep ? off : 0x7ffffff0u, 0, 0);
+}
+
 // Unpack the 8 bf16 of a 16-byte vector into fp32.
 __device__ __forceinline__ void unpack8(u32x4 v, float* f) {
 #pragma unroll
@@ -142,20 +153,34 @@ __device__ __forceinline__ void load_vops(const uint16_t* __restrict__ V, int ba
       vop[q][t] = ld8(V + (int64_t)vrow_res<G>(base, j, q) * R + 16 * t + 4 * g);
 }
 
-// P = L V^T for the lane's G/4 columns of one unit-plane: p[4q + v].
+// out[4q + v] = fp32(c[4q + v] + sum_rank V[col][rank] * L[row][rank]) for the lane's G/4
+// columns of one unit-plane, rounded once: the MFMA adds its C operand and all products
+// exactly before rounding (checked on gfx950).  Rank 16 is one 16x16x16 step; rank 32 is one
+// 16x16x32 step whose K order puts ranks 4g..4g+3 and 16+4g..16+4g+3 in lane group g, so
+// the two 16-rank operands are simply concatenated.  Pass L negated to subtract.
 template <int G, int R>
-__device__ __forceinline__ void lowrank_unit(const u32x2 (&vop)[G / 16][R / 16], const u32x2* lop, float* p) {
+__device__ __forceinline__ void residual_unit(const u32x2 (&vop)[G / 16][R / 16], const u32x2* lop,
+                                              const float* c, float* out) {
+  static_assert(R == 16 || R == 32, "rank 16 or 32");
 #pragma unroll
   for (int q = 0; q < G / 16; ++q) {
-    f32x4 acc = zero4();
-#pragma unroll
-    for (int t = 0; t < R / 16; ++t) acc = mfma_16x16x16(vop[q][t], lop[t], acc);
-    p[4 * q + 0] = acc[0];
-    p[4 * q + 1] = acc[1];
-    p[4 * q + 2] = acc[2];
-    p[4 * q + 3] = acc[3];
+    f32x4 acc = f32x4{c[4 * q], c[4 * q + 1], c[4 * q + 2], c[4 * q + 3]};
+    if constexpr (R == 16) {
+      acc = mfma_16x16x16(vop[q][0], lop[0], acc);
+    } else {
+      const u32x4 a = u32x4{vop[q][0][0], vop[q][0][1], vop[q][1][0], vop[q][1][1]};
+      const u32x4 b = u32x4{lop[0][0], lop[0][1], lop[1][0], lop[1][1]};
+      acc = mfma_16x16x32(a, b, acc);
+    }
+    out[4 * q + 0] = acc[0];
+    out[4 * q + 1] = acc[1];
+    out[4 * q + 2] = acc[2];
+    out[4 * q + 3] = acc[3];
   }
 }
+
+// Negate packed bf16 operands (exact).
+__device__ __forceinline__ u32x2 neg_bf16x4(u32x2 v) { return u32x2{v[0] ^ 0x80008000u, v[1] ^ 0x80008000u}; }
 
 // B operand of the identity: lane (j, g) holds I[4g + e][j], e < 4, as bf16.
 __device__ __forceinline__ u32x2 identity_bop(int j, int g) {
@@ -166,20 +191,22 @@ __device__ __forceinline__ u32x2 identity_bop(int j, int g) {
   return u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
 }
 
-// Projection partial for one unit-plane: acc[t] += V_t^T(block q) * X^T(block q), with the
-// V^T operand obtained by multiplying the reconstruction operand by the identity (exact).
+// Projection partial for one unit-plane: acc[t] += V_t^T(cols) * X^T(cols) over the lane
+// quarter's G/4 columns.  The V^T operand comes from multiplying the reconstruction operand
+// by the identity (exact): operands q and q+1 transpose to lane (rank, g) holding V at the
+// 8 consecutive columns 8*(q/2) .. +7 of quarter g, which pair with x[q/2] as a 16x16x32 step.
 template <int G, int R>
 __device__ __forceinline__ void project_unit(const u32x2 (&vop)[G / 16][R / 16], const u32x4* x, u32x2 ident,
                                              f32x4* acc) {
 #pragma unroll
-  for (int q = 0; q < G / 16; ++q) {
-    const u32x4 xv = x[q >> 1];
-    const u32x2 xb = (q & 1) ? u32x2{xv[2], xv[3]} : u32x2{xv[0], xv[1]};
+  for (int k = 0; k < G / 32; ++k) {
 #pragma unroll
     for (int t = 0; t < R / 16; ++t) {
-      const f32x4 vt = mfma_16x16x16(vop[q][t], ident, zero4());
-      const u32x2 a = u32x2{pack_bf16x2_exact(vt[0], vt[1]), pack_bf16x2_exact(vt[2], vt[3])};
-      acc[t] = mfma_16x16x16(a, xb, acc[t]);
+      const f32x4 v0 = mfma_16x16x16(vop[2 * k][t], ident, zero4());
+      const f32x4 v1 = mfma_16x16x16(vop[2 * k + 1][t], ident, zero4());
+      const u32x4 a = u32x4{pack_bf16x2_exact(v0[0], v0[1]), pack_bf16x2_exact(v0[2], v0[3]),
+                            pack_bf16x2_exact(v1[0], v1[1]), pack_bf16x2_exact(v1[2], v1[3])};
+      acc[t] = mfma_16x16x32(a, x[k], acc[t]);
     }
   }
 }
@@ -211,35 +238,38 @@ __device__ __forceinline__ void lds_barrier() {
 
 // ---------------------------------------------------------------- group quantiser
 // Per-group parameters from min/max, exactly as the CPU oracle defines them:
-//   scale_h = fp16(min((mx - mn) / qmax, 65504)), 1 when that is 0; zero_h = fp16(clamp(mn));
-//   inv = 1 / fp32(scale_h).  Division is IEEE correctly rounded (HIP default).
+//   scale_h = fp16(min((mx - mn) * fp32(1/qmax), 65504)), 1 when that is 0;
+//   zero_h  = fp16(clamp(mn)); inv = 1 / fp32(scale_h) correctly rounded; nzi = -zf * inv.
+// The reciprocal is rcp + one Newton step, which equals the correctly rounded 1/x for every
+// positive finite fp16 x (checked exhaustively on gfx950).
 struct GroupParams {
-  float inv, zf;
+  float inv, nzi;
   uint32_t sh, zh;
 };
 template <int BITS>
 __device__ __forceinline__ GroupParams group_params(float mn, float mx) {
-  constexpr float qmax = (float)((1 << BITS) - 1);
+  constexpr float kInvQmax = 1.0f / (float)((1 << BITS) - 1);
   GroupParams gp;
-  float s = (mx - mn) / qmax;
-  s = fminf(s, 65504.f);
+  const float s = fminf(__fmul_rn(__fsub_rn(mx, mn), kInvQmax), 65504.f);
   uint32_t sh = f16_bits(s);
   if ((sh & 0x7fffu) == 0) sh = 0x3c00u;  // 1.0
   const float z = fminf(fmaxf(mn, -65504.f), 65504.f);
   gp.sh = sh;
   gp.zh = f16_bits(z);
-  gp.zf = f16_val(gp.zh);
-  gp.inv = 1.0f / f16_val(sh);
+  const float sf = f16_val(sh);
+  const float r0 = __builtin_amdgcn_rcpf(sf);
+  gp.inv = __builtin_fmaf(__builtin_fmaf(-sf, r0, 1.0f), r0, r0);
+  gp.nzi = __fmul_rn(-f16_val(gp.zh), gp.inv);
   return gp;
 }
-// code = clamp(rint((r - zf) * inv), 0, qmax); the subtract and the multiply round separately.
-// Returned as the bit pattern of 1.5*2^23 + code: clamping before rounding gives the same
-// code for every t, and adding 1.5*2^23 to t in [0, qmax] rounds it to an integer (half to
-// even) in the low mantissa bits, so the code is the low BITS bits of the result.
+// code = clamp(rint(fma(r, inv, nzi)), 0, qmax), returned as the bit pattern of
+// 1.5*2^23 + code: clamping before rounding gives the same code for every t, and adding
+// 1.5*2^23 to t in [0, qmax] rounds it to an integer (half to even) in the low mantissa
+// bits, so the code is the low BITS bits of the result.
 template <int BITS>
 __device__ __forceinline__ uint32_t quant_code_bits(float r, const GroupParams& gp) {
   constexpr float qmax = (float)((1 << BITS) - 1);
-  float t = __fmul_rn(__fsub_rn(r, gp.zf), gp.inv);
+  float t = __builtin_fmaf(r, gp.inv, gp.nzi);
   t = __builtin_amdgcn_fmed3f(t, 0.f, qmax);
   return __float_as_uint(__fadd_rn(t, 12582912.0f));
 }

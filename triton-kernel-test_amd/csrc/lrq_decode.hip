@@ -16,7 +16,10 @@ namespace lrq {
 // ------------------------------------------------------------------ epilogues
 // An epilogue binds its row pointers once per row block (`row(r)`), then receives 8
 // consecutive reconstructed values (fp32, before the bf16 rounding that defines x_hat)
-// for columns col .. col + 7 of that row.
+// for columns col .. col + 7 of that row.  Stores are unconditional: lanes of rows past the
+// end are clamped to the last row and store the same bytes as its own lanes, which keeps
+// the instruction stream branch-free (on gfx9 a conditional store makes the compiler drain
+// every outstanding memory operation at the next load use, prefetches included).
 struct EpiStore {
   uint16_t* out;
   int64_t ld;
@@ -24,8 +27,8 @@ struct EpiStore {
     uint16_t* o;
   };
   __device__ __forceinline__ Row row(int64_t r) const { return Row{out + r * ld}; }
-  __device__ __forceinline__ void operator()(const Row& r, int col, const float* xh, bool rv) const {
-    if (rv) st16(r.o + col, pack8(xh));
+  __device__ __forceinline__ void operator()(const Row& r, int col, const float* xh) const {
+    st16(r.o + col, pack8(xh));
   }
 };
 
@@ -42,8 +45,7 @@ struct EpiSilu {
   int64_t lddx;
   using Row = RowIO;
   __device__ __forceinline__ Row row(int64_t r) const { return Row{dy + r * lddy, dx + r * lddx}; }
-  __device__ __forceinline__ void operator()(const Row& r, int col, const float* xh, bool rv) const {
-    if (!rv) return;
+  __device__ __forceinline__ void operator()(const Row& r, int col, const float* xh) const {
     float d[8], o[8];
     unpack8(ld16_stream(r.in + col), d);
 #pragma unroll
@@ -64,8 +66,7 @@ struct EpiGelu {
   int64_t lddx;
   using Row = RowIO;
   __device__ __forceinline__ Row row(int64_t r) const { return Row{dy + r * lddy, dx + r * lddx}; }
-  __device__ __forceinline__ void operator()(const Row& r, int col, const float* xh, bool rv) const {
-    if (!rv) return;
+  __device__ __forceinline__ void operator()(const Row& r, int col, const float* xh) const {
     constexpr float kGamma = 0.7978845608028654f, kKappa = 0.044715f;
     float d[8], o[8];
     unpack8(ld16_stream(r.in + col), d);
@@ -90,8 +91,7 @@ struct EpiMul {
   int64_t ldo;
   using Row = RowIO;
   __device__ __forceinline__ Row row(int64_t r) const { return Row{y + r * ldy, out + r * ldo}; }
-  __device__ __forceinline__ void operator()(const Row& r, int col, const float* xh, bool rv) const {
-    if (!rv) return;
+  __device__ __forceinline__ void operator()(const Row& r, int col, const float* xh) const {
     float a[8], o[8];
     unpack8(ld16_stream(r.in + col), a);
 #pragma unroll
@@ -110,16 +110,16 @@ struct DecIn {
   u32x2 lop[R > 0 ? R / 16 : 1];
 };
 
-// Grid: (ceil(row blocks / rbw), ceil(units / NW)); NW waves; wave w owns unit
-// blockIdx.y * NW + w and walks row blocks blockIdx.x * rbw + b, b < rbw.  The waves of a
+// Grid: (ceil(row blocks / RBW), ceil(units / NW)); NW waves; wave w owns unit
+// blockIdx.y * NW + w and walks row blocks blockIdx.x * RBW + b, b < RBW.  The waves of a
 // workgroup work on consecutive units of the same rows, so at any time a workgroup writes
 // NW * G * 2 contiguous bytes per row and plane (DRAM-page friendly), while each wave
 // reuses its unit's V operands for all its row blocks.
-template <int BITS, int G, int R, bool OUTL, int NW, class EPI>
+template <int BITS, int G, int R, bool OUTL, int NW, int RBW, class EPI>
 __global__ __launch_bounds__(NW * 64) void k_decode(
     const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
     const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
-    const int32_t* __restrict__ oidx, int nout, const uint16_t* __restrict__ side, int64_t ldside, int rbw,
+    const int32_t* __restrict__ oidx, int nout, const uint16_t* __restrict__ side, int64_t ldside,
     EPI epi) {
   constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, E = G / 4;
   constexpr uint32_t kMask = (1u << BITS) - 1u;
@@ -171,9 +171,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode(
   };
 
   auto compute = [&](const DecIn<BITS, G, R>& in, int rb) {
-    const int row = rb * 16 + j;
-    const bool rv = row < M;
-    const int64_t rr = rv ? row : M - 1;
+    const int64_t rr = min(rb * 16 + j, M - 1);
     const typename EPI::Row erow = epi.row(rr);
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
@@ -191,67 +189,67 @@ __global__ __launch_bounds__(NW * 64) void k_decode(
         xh[4 * d + 2] = __builtin_fmaf(ubyte_f32<2>(wq), sf, zf);
         xh[4 * d + 3] = __builtin_fmaf(ubyte_f32<3>(wq), sf, zf);
       }
-      if constexpr (R > 0) {
-        float pl[E];
-        lowrank_unit<G, R>(vop[p], in.lop, pl);
-#pragma unroll
-        for (int e = 0; e < E; ++e) xh[e] = __fadd_rn(xh[e], pl[e]);
-      }
+      if constexpr (R > 0) residual_unit<G, R>(vop[p], in.lop, xh, xh);  // d + L V^T, one rounding
       const int c0 = unit_base(p, u, N, NP, G) + E * g;
       if constexpr (OUTL) {
         const uint32_t mbits = colmask[c0 >> 5] >> (c0 & 31);
-        if (mbits != 0u && rv) {
+        if (mbits != 0u) {
 #pragma unroll
           for (int e = 0; e < E; ++e)
             if ((mbits >> e) & 1u) xh[e] = f16_val(side[rr * ldside + slot[c0 + e]]);
         }
       }
 #pragma unroll
-      for (int k = 0; k < E / 8; ++k) epi(erow, c0 + 8 * k, xh + 8 * k, rv);
+      for (int k = 0; k < E / 8; ++k) epi(erow, c0 + 8 * k, xh + 8 * k);
     }
   };
 
-  const int rb0 = blockIdx.x * rbw;
+  const int rb0 = blockIdx.x * RBW;
   if (rb0 >= nrb) return;
-  DecIn<BITS, G, R> cur, nxt;
-  load(cur, rb0, true);
-  for (int b = 0; b < rbw; ++b) {
-    const int rb = rb0 + b;
-    const int rbn = rb + 1;
-    const bool more = (b + 1 < rbw) && (rbn < nrb);
-    load(nxt, rbn, more);
-    compute(cur, rb);
-    if (!more) break;
-    cur = nxt;
-  }
+  // All of the wave's row-block inputs are requested up front (codes, qparams and L are a
+  // quarter of the traffic); blocks are then reconstructed and stored in order.  With RBW a
+  // compile-time constant and no branch in the body every wait count is exact and no load
+  // is issued after a store.  Blocks past the end (tail workgroup only) repeat the last row
+  // block, rewriting the same bytes.
+  DecIn<BITS, G, R> in[RBW];
+#pragma unroll
+  for (int b = 0; b < RBW; ++b) load(in[b], min(rb0 + b, nrb - 1), true);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int b = 0; b < RBW; ++b) compute(in[b], min(rb0 + b, nrb - 1));
 }
 
 // ------------------------------------------------------------------ host side
-template <int BITS, int G, int R, class EPI>
-static int decode_launch(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
+template <int BITS, int G, int R, int RBW, class EPI>
+static int decode_launch_rbw(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
   constexpr int NP = 8 / BITS, NW = 8;
   const int M = (int)t->rows, N = (int)t->hidden;
   const int units = N / (G * NP);
   const int nrb = (M + 15) / 16;
-  const int ugroups = (units + NW - 1) / NW;
-  // as many row blocks per wave as keeps >= 512 workgroups (2 per CU), at most 8: the unit's
-  // V operands are loaded once per wave
-  int rbw = 8;
-  while (rbw > 1 && (int64_t)((nrb + rbw - 1) / rbw) * ugroups < 512) rbw >>= 1;
-  dim3 grid((nrb + rbw - 1) / rbw, ugroups);
+  dim3 grid((nrb + RBW - 1) / RBW, (units + NW - 1) / NW);
   if (t->n_outlier > 0) {
     const size_t shm = (size_t)(N / 32) * 4 + (size_t)N * 2;
-    hipLaunchKernelGGL((k_decode<BITS, G, R, true, NW, EPI>), grid, dim3(NW * 64), shm, s,
+    hipLaunchKernelGGL((k_decode<BITS, G, R, true, NW, RBW, EPI>), grid, dim3(NW * 64), shm, s,
                        (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
                        (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, t->outlier_idx, t->n_outlier,
-                       (const uint16_t*)t->side, t->ld_side, rbw, epi);
+                       (const uint16_t*)t->side, t->ld_side, epi);
   } else {
-    hipLaunchKernelGGL((k_decode<BITS, G, R, false, NW, EPI>), grid, dim3(NW * 64), 0, s,
+    hipLaunchKernelGGL((k_decode<BITS, G, R, false, NW, RBW, EPI>), grid, dim3(NW * 64), 0, s,
                        (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
                        (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, nullptr, 0, nullptr,
-                       (int64_t)0, rbw, epi);
+                       (int64_t)0, epi);
   }
   return launch_status();
+}
+
+// 8 row blocks per wave when that still leaves >= 512 workgroups (2 per CU), else 2.
+template <int BITS, int G, int R, class EPI>
+static int decode_launch(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
+  constexpr int NP = 8 / BITS, NW = 8;
+  const int64_t units = t->hidden / (G * NP), nrb = (t->rows + 15) / 16;
+  const int64_t wgs8 = ((nrb + 7) / 8) * ((units + NW - 1) / NW);
+  if (wgs8 >= 512) return decode_launch_rbw<BITS, G, R, 8>(t, s, epi);
+  return decode_launch_rbw<BITS, G, R, 2>(t, s, epi);
 }
 
 template <class EPI>

@@ -2,7 +2,7 @@
 // asymmetric quantisation and row-planar packing.
 //
 // Implementations, chosen per call by lrq_encode():
-//   * k_encode_persist — one pass over X, persistent (one workgroup per CU).  The NW waves
+//   * k_encode_persist — one pass over X (about one workgroup per CU).  The NW waves
 //     split the hidden dimension into units; each wave keeps the reconstruction operands of
 //     its units (V rows) in registers for the whole kernel, and its share of the current
 //     16-row block of X in registers while the next block streams in (double buffer).  The
@@ -19,8 +19,9 @@
 namespace lrq {
 
 // -------------------------------------------------------------------------------------
-// Persistent single-pass encode.  Grid: min(row blocks, CUs) workgroups of NW waves; wave w
-// owns units [w*UPW, (w+1)*UPW).  The host guarantees N == NW*UPW*G*NP and R == 16*RT.
+// Single-pass encode.  Grid: ceil(row blocks / RBW) workgroups of NW waves (about one per
+// CU); wave w owns units [w*UPW, (w+1)*UPW).  The host guarantees N == NW*UPW*G*NP and
+// R == 16*RT.
 // VLDS: the waves' V operands live in LDS (read right before each use) instead of registers,
 // which leaves room for the double-buffered X tile.
 template <int BITS, int G, int R, int NW, int UPW>
@@ -30,7 +31,7 @@ struct PersistLds {
   static constexpr size_t kRedBytes = (size_t)2 * NW * (R / 16) * 64 * 16;
 };
 
-template <int BITS, int G, int R, int NW, int UPW, bool DB, bool VLDS>
+template <int BITS, int G, int R, int NW, int UPW, bool DB, bool VLDS, int RBW>
 __global__ __launch_bounds__(NW * 64) void k_encode_persist(
     const uint16_t* __restrict__ X, int64_t ldx, int M, int N, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ Lout, int64_t ldl, uint8_t* __restrict__ codes, int64_t ldc,
@@ -44,7 +45,6 @@ __global__ __launch_bounds__(NW * 64) void k_encode_persist(
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int nrb = (M + 15) / 16;
-  const int stride = gridDim.x;
 
   u32x2 vreg[VLDS ? 1 : UPW][NP][G / 16][RT];
 #pragma unroll
@@ -77,8 +77,7 @@ __global__ __launch_bounds__(NW * 64) void k_encode_persist(
   };
   const u32x2 ident = identity_bop(j, g);
 
-  // Load the lane's share of row block rb; when !valid every lane reads X[0..15] instead
-  // (one cached line) so the instruction stream — and the wait counts — stay uniform.
+  // Load the lane's share of row block rb (when !valid every lane reads X[0..15] instead).
   auto load = [&](u32x4 (&x)[UPW][NP][CPG], int rb, bool valid) {
     const int row = min(rb * 16 + j, M - 1);
     const uint16_t* xr = X + (int64_t)row * ldx + E * g;
@@ -91,25 +90,35 @@ __global__ __launch_bounds__(NW * 64) void k_encode_persist(
           const uint16_t* a = xr + unit_base(p, w * UPW + uu, N, NP, G) + 8 * k;
           x[uu][p][k] = ld16_stream(valid ? a : X);
         }
+    // keep the prefetch where it is issued (the scheduler would sink it next to its use,
+    // behind the previous block's stores)
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   auto process = [&](const u32x4 (&x)[UPW][NP][CPG], int rb, int parity) {
-    const int row = rb * 16 + j;
-    const bool rv = row < M;
-    f32x4 acc[RT];
+    const int row = min(rb * 16 + j, M - 1);  // rows past the end repeat the last row (see load)
+    // two accumulator chains (even / odd unit-plane) to halve the dependent MFMA sequence
+    f32x4 acc[2][RT];
 #pragma unroll
-    for (int t = 0; t < RT; ++t) acc[t] = zero4();
+    for (int t = 0; t < RT; ++t) acc[0][t] = acc[1][t] = zero4();
 #pragma unroll
     for (int uu = 0; uu < UPW; ++uu)
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
         u32x2 v[G / 16][RT];
         vops(uu, p, v);
-        project_unit<G, R>(v, x[uu][p], ident, acc);
+        project_unit<G, R>(v, x[uu][p], ident, acc[(uu * NP + p) & 1]);
       }
     f32x4* rp = red + parity * (NW * RT * 64);
 #pragma unroll
-    for (int t = 0; t < RT; ++t) rp[(w * RT + t) * 64 + lane] = acc[t];
+    for (int t = 0; t < RT; ++t) {
+      f32x4 a = acc[0][t];
+      a[0] += acc[1][t][0];
+      a[1] += acc[1][t][1];
+      a[2] += acc[1][t][2];
+      a[3] += acc[1][t][3];
+      rp[(w * RT + t) * 64 + lane] = a;
+    }
     lds_barrier();
     u32x2 lop[RT];
 #pragma unroll
@@ -124,7 +133,9 @@ __global__ __launch_bounds__(NW * 64) void k_encode_persist(
         s[3] += o[3];
       }
       lop[t] = u32x2{pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3])};
-      if (w == 0 && rv) st8(Lout + (int64_t)row * ldl + 16 * t + 4 * g, lop[t]);
+      // every wave holds the reduced tile; wave w stores rows j with j % NW == w
+      st8_pred(Lout + (int64_t)rb * 16 * ldl, (uint32_t)(16 * ldl * 2), (uint32_t)((j * ldl + 16 * t + 4 * g) * 2),
+               lop[t], (j % NW) == w && rb * 16 + j < M);
     }
     uint8_t* crow = codes + (int64_t)row * ldc;
     uint16_t* qrow = qparams + (int64_t)row * ldq;
@@ -133,34 +144,25 @@ __global__ __launch_bounds__(NW * 64) void k_encode_persist(
       u32x2 v[NP][G / 16][RT];
 #pragma unroll
       for (int p = 0; p < NP; ++p) vops(uu, p, v[p]);
-      quant_unit<BITS, G, R>(x[uu], v, lop, nullptr, w * UPW + uu, N, g, rv, crow, qrow);
+      quant_unit<BITS, G, R>(x[uu], v, lop, nullptr, w * UPW + uu, N, g, crow, qrow);
     }
+    __builtin_amdgcn_sched_barrier(0);  // keep row blocks from interleaving (register pressure)
   };
 
-  u32x4 xa[UPW][NP][CPG];
-  int rb = blockIdx.x;
-  load(xa, rb, true);
-  if constexpr (DB) {
-    u32x4 xb[UPW][NP][CPG];
-    for (;;) {
-      const int rb1 = rb + stride;
-      load(xb, rb1, rb1 < nrb);
-      process(xa, rb, 0);
-      if (rb1 >= nrb) break;
-      const int rb2 = rb1 + stride;
-      load(xa, rb2, rb2 < nrb);
-      process(xb, rb1, 1);
-      if (rb2 >= nrb) break;
-      rb = rb2;
-    }
-  } else {
-    int parity = 0;
-    for (;;) {
-      process(xa, rb, parity);
-      rb += stride;
-      if (rb >= nrb) break;
-      load(xa, rb, true);
-      parity ^= 1;
+  // RBW row blocks per workgroup, straight-line: block b+1 is requested before block b is
+  // processed (two register buffers, indices fixed after unrolling).  Blocks past the end
+  // (tail workgroup only) repeat the last block and rewrite the same bytes.
+  const int rb0 = blockIdx.x * RBW;
+  u32x4 xs[DB ? 2 : 1][UPW][NP][CPG];
+  load(xs[0], min(rb0, nrb - 1), true);
+#pragma unroll
+  for (int b = 0; b < RBW; ++b) {
+    if constexpr (DB) {
+      if (b + 1 < RBW) load(xs[(b + 1) & 1], min(rb0 + b + 1, nrb - 1), true);
+      process(xs[b & 1], min(rb0 + b, nrb - 1), b & 1);
+    } else {
+      if (b > 0) load(xs[0], min(rb0 + b, nrb - 1), true);
+      process(xs[0], min(rb0 + b, nrb - 1), b & 1);
     }
   }
 }
@@ -256,8 +258,7 @@ __global__ __launch_bounds__(256) void k_quant(
   for (int b = 0; b < RB; ++b) {
     const int row = (blockIdx.x * RB + b) * 64 + w * 16 + j;
     if (row - j >= M) break;  // whole 16-row block past the end (uniform per wave)
-    const bool rv = row < M;
-    const int64_t rr = rv ? row : M - 1;
+    const int64_t rr = min(row, M - 1);
     u32x2 lop[RT];
     if constexpr (R > 0) {
 #pragma unroll
@@ -268,7 +269,7 @@ __global__ __launch_bounds__(256) void k_quant(
     for (int p = 0; p < NP; ++p)
 #pragma unroll
       for (int k = 0; k < CPG; ++k) x[p][k] = ld16_stream(X + rr * ldx + unit_base(p, u, N, NP, G) + E * g + 8 * k);
-    quant_unit<BITS, G, R>(x, vop, lop, OUTL ? colmask : nullptr, u, N, g, rv, codes + rr * ldc,
+    quant_unit<BITS, G, R>(x, vop, lop, OUTL ? colmask : nullptr, u, N, g, codes + rr * ldc,
                            qparams + rr * ldq);
   }
 }
@@ -296,20 +297,28 @@ static int cu_count() {
   return n;
 }
 
-template <int BITS, int G, int R, int NW, int UPW, bool DB>
-static int launch_persist(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s) {
+template <int BITS, int G, int R, int NW, int UPW, bool DB, int RBW>
+static int launch_persist_rbw(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s) {
   using Lds = PersistLds<BITS, G, R, NW, UPW>;
   // Wide waves keep their V operands in LDS so the double-buffered X tile fits in registers.
-  constexpr bool VLDS = DB && UPW * G * (8 / BITS) >= 512 && Lds::kVopBytes + Lds::kRedBytes <= 160 * 1024;
+  constexpr bool VLDS = DB && (NW >= 16 || UPW * G * (8 / BITS) >= 512) && Lds::kVopBytes + Lds::kRedBytes <= 160 * 1024;
   const size_t shm = Lds::kRedBytes + (VLDS ? Lds::kVopBytes : 0);
-  auto kern = k_encode_persist<BITS, G, R, NW, UPW, DB, VLDS>;
+  auto kern = k_encode_persist<BITS, G, R, NW, UPW, DB, VLDS, RBW>;
   if (shm > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
   const int nrb = (int)((t->rows + 15) / 16);
-  const int grid = nrb < cu_count() ? nrb : cu_count();
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), shm, s, (const uint16_t*)x, ldx, (int)t->rows,
-                     (int)t->hidden, (const uint16_t*)t->V, (uint16_t*)t->L, t->ld_L, (uint8_t*)t->codes,
-                     t->ld_codes, (uint16_t*)t->qparams, t->ld_qp);
+  hipLaunchKernelGGL(kern, dim3((nrb + RBW - 1) / RBW), dim3(NW * 64), shm, s, (const uint16_t*)x, ldx,
+                     (int)t->rows, (int)t->hidden, (const uint16_t*)t->V, (uint16_t*)t->L, t->ld_L,
+                     (uint8_t*)t->codes, t->ld_codes, (uint16_t*)t->qparams, t->ld_qp);
   return launch_status();
+}
+
+// Row blocks per workgroup: 4 when that still gives every CU a workgroup, else 1 (one
+// workgroup of NW waves fits per CU).
+template <int BITS, int G, int R, int NW, int UPW, bool DB>
+static int launch_persist(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s) {
+  const int64_t nrb = (t->rows + 15) / 16;
+  if (nrb >= 4 * (int64_t)cu_count()) return launch_persist_rbw<BITS, G, R, NW, UPW, DB, 4>(t, x, ldx, s);
+  return launch_persist_rbw<BITS, G, R, NW, UPW, DB, 1>(t, x, ldx, s);
 }
 
 // Returns 1 and launches when a single-pass kernel exists for this shape, else 0.
@@ -326,12 +335,7 @@ static int encode_persist_dispatch(const lrq_tensors* t, const void* x, int64_t 
     switch (units) {
       case 8: *status = launch_persist<BITS, G, R, 4, 2, true>(t, x, ldx, s); return 1;
       case 16: *status = launch_persist<BITS, G, R, 8, 2, true>(t, x, ldx, s); return 1;
-      case 32:
-        if constexpr (wide_ok) {
-          *status = launch_persist<BITS, G, R, 8, 4, true>(t, x, ldx, s);
-          return 1;
-        }
-        return 0;
+      case 32: *status = launch_persist<BITS, G, R, 16, 2, true>(t, x, ldx, s); return 1;
       case 40:
         if constexpr (wide_ok) {
           *status = launch_persist<BITS, G, R, 8, 5, false>(t, x, ldx, s);
