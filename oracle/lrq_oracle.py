@@ -237,10 +237,14 @@ def quant_groups(r: np.ndarray, bits: int, group: int):
       scale_h  = fp16_rne(min((mx - mn) * fp32(1/qmax), 65504)), replaced by 1 when 0
       zero_h   = fp16_rne(clamp(mn, +-65504))
       inv      = 1 / fp32(scale_h)              (fp32, correctly rounded)
-      nzi      = fp32(-fp32(zero_h) * inv)
-      t        = fma(R, inv, nzi)               (one rounding)
-      code     = clamp(rint(t), 0, qmax)        (round half to even), qmax = 2^bits - 1
-    Returns (codes uint8 [.., N], scale fp16 [.., N/G], zero fp16 [.., N/G], t float32 [.., N]).
+      a        = fp32(inv * fp32(1/qmax))
+      b        = fp32(-fp32(zero_h) * a)
+      u        = clamp(fma(R, a, b), 0, 1)      (one rounding; NaN -> 0)
+      code     = rint(u * qmax)                 (exact product, round half to even),
+    qmax = 2^bits - 1.  The kernels evaluate u with one clamped fma and the rounding as
+    fma(u, qmax, 1.5 * 2^23), whose low mantissa bits are the code.
+    Returns (codes uint8 [.., N], scale fp16 [.., N/G], zero fp16 [.., N/G],
+    t = u * qmax float64 [.., N], the value that was rounded).
     Pinned by: codes in range, min/max map to the end codes, constant groups decode
     exactly, |decode - R| <= scale/2 (tests/test_oracle.py).
     """
@@ -257,10 +261,13 @@ def quant_groups(r: np.ndarray, bits: int, group: int):
     scale_h = np.where(scale_h == 0, np.float16(1.0), scale_h)
     zero_h = f16_sat(mn)
     inv = rcp32(scale_h.astype(np.float32))
-    nzi = (-zero_h.astype(np.float32) * inv).astype(np.float32)
-    t = fma32(rg, inv[..., None], nzi[..., None])
-    codes = np.clip(np.rint(t), 0, qmax).astype(np.uint8)
-    return (codes.reshape(lead + (n,)), scale_h, zero_h, t.reshape(lead + (n,)).astype(np.float32))
+    a = (inv * np.float32(1.0 / qmax)).astype(np.float32)
+    b = (-zero_h.astype(np.float32) * a).astype(np.float32)
+    u = fma32(rg, a[..., None], b[..., None])
+    u = np.where(np.isnan(u), np.float32(0.0), np.clip(u, np.float32(0.0), np.float32(1.0)))
+    t = u.astype(np.float64) * qmax
+    codes = np.rint(t).astype(np.uint8)
+    return (codes.reshape(lead + (n,)), scale_h, zero_h, t.reshape(lead + (n,)))
 
 
 def dequant_groups(codes: np.ndarray, scale_h: np.ndarray, zero_h: np.ndarray, group: int) -> np.ndarray:
@@ -279,11 +286,9 @@ def encode(x_bits: np.ndarray, v_bits, bits: int = 4, group: int = 64, hadamard:
       Y  = wht128_rows(x) if hadamard else fp32(x)
       side[:, k] = fp16(x[:, idx[k]]); Y[:, idx] = 0            (outlier channels, if any)
       L  = bf16(fp32(exact(Y @ V)))                              (if rank > 0)
-      P  = fp32(exact(L @ V^T))                                  (if rank > 0)
-      R  = fp32(Y - P)                (the product is rounded first, then the difference,
-                                       as ``accumulator -= tl.dot(a, b)`` in
-                                       low_rank_extraction_fuse_compression_quantization.py:72
-                                       does; else R = Y)
+      R  = fp32(exact(Y - L @ V^T))   (one rounding: the kernels form it as an MFMA whose
+                                       accumulator input is Y, the same form the decode
+                                       uses for Y'; else R = Y)
       R[:, idx] = 0
       codes, scale, zero = quant_groups(R)
       packed = pack_rowplanar(codes)
@@ -309,8 +314,8 @@ def encode(x_bits: np.ndarray, v_bits, bits: int = 4, group: int = 64, hadamard:
             l_bits, l32 = projection(y, v_bits)
         else:
             l_bits, l32 = np.asarray(l_override, dtype=np.uint16), None
-        p = lowrank_product(l_bits, v_bits).astype(np.float32)  # the fp32 MMA result
-        r = (y - p).astype(np.float32)
+        p = lowrank_product(l_bits, v_bits)
+        r = (y.astype(np.float64) - p).astype(np.float32)  # one rounding
     else:
         l_bits, l32, p = None, None, None
         r = y

@@ -31,6 +31,9 @@ HIPFLAGS = [
     "-ffp-contract=off",
     # MFMA results straight into VGPRs (no v_accvgpr_read round trips in the epilogues)
     "-mllvm", "-amdgpu-mfma-vgpr-form",
+    # IEEE mode off: v_min/v_max of MFMA results need no canonicalising moves.  The kernels
+    # assume finite inputs (NaN / Inf activations give unspecified codes, never a fault).
+    "-fno-honor-nans", "-mno-amdgpu-ieee",
 ]
 
 

@@ -21,7 +21,9 @@
 //    4q..4q+3.  Its output is L[row j][16t + 4g + v] in lane (j, g): the B operand the
 //    reconstruction needs.  No activation data ever moves between lanes.
 //  * Group statistics: the four lanes of a row (j, j+16, j+32, j+48) hold the whole group;
-//    two xor-shuffles finish min/max.
+//    two permlane swaps finish min/max.  With two planes the two groups of a unit are
+//    reduce-scattered (lanes 0..31 finish plane 0, 32..63 plane 1), their parameters are
+//    computed once and swapped back.
 //  * qparams: fp16 [rows, N/(G*NP), NP, 2] — per unit, (scale, zero) of each plane's group.
 #pragma once
 
@@ -211,16 +213,65 @@ __device__ __forceinline__ void project_unit(const u32x2 (&vop)[G / 16][R / 16],
   }
 }
 
-// Cross-lane reductions over the 4 lanes that share a row (lanes j, j+16, j+32, j+48).
-__device__ __forceinline__ float wave_min4(float v) {
-  v = fminf(v, __shfl_xor(v, 16));
-  v = fminf(v, __shfl_xor(v, 32));
-  return v;
+// ---------------------------------------------------------------- row-quad exchanges
+// The four lanes of a row (j, j+16, j+32, j+48) are one lane of each 16-lane row of the
+// wave.  v_permlane32_swap exchanges lanes 32..63 of its first operand with lanes 0..31 of
+// its second; v_permlane16_swap exchanges the odd 16-lane rows of its first operand with the
+// even rows of its second.  Both are plain VALU moves (no LDS round trip).
+__device__ __forceinline__ void swap32(float& a, float& b) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  a = __uint_as_float(s[0]);
+  b = __uint_as_float(s[1]);
 }
-__device__ __forceinline__ float wave_max4(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+__device__ __forceinline__ void swap16(float& a, float& b) {
+  const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  a = __uint_as_float(s[0]);
+  b = __uint_as_float(s[1]);
+}
+// min / max as v_med3 against -inf / +inf: the same result as fminf / fmaxf for non-NaN
+// inputs, without the canonicalising moves the compiler adds around fminf of values it
+// cannot prove canonical (such as permlane results).
+__device__ __forceinline__ float min_nc(float a, float b) { return __builtin_amdgcn_fmed3f(a, b, -__builtin_inff()); }
+__device__ __forceinline__ float max_nc(float a, float b) { return __builtin_amdgcn_fmed3f(a, b, __builtin_inff()); }
+
+// Reductions over the four lanes of a row; every lane receives the result.
+__device__ __forceinline__ float row_min4(float v) {
+  float a = v, b = v;
+  swap32(a, b);  // a = v of lanes 0..31 repeated, b = v of lanes 32..63 repeated
+  v = min_nc(a, b);
+  a = v, b = v;
+  swap16(a, b);
+  return min_nc(a, b);
+}
+__device__ __forceinline__ float row_max4(float v) {
+  float a = v, b = v;
+  swap32(a, b);
+  v = max_nc(a, b);
+  a = v, b = v;
+  swap16(a, b);
+  return max_nc(a, b);
+}
+// Reduce-scatter of two per-lane partials over the row: lanes 0..31 receive the min of
+// `va` over the row's four lanes, lanes 32..63 the min of `vb`.
+__device__ __forceinline__ float row_min4_pair(float va, float vb) {
+  swap32(va, vb);  // va = [a(l), b(l)], vb = [a(l+32), b(l+32)] for lanes l < 32 | l >= 32
+  float v = min_nc(va, vb);
+  float a = v, b = v;
+  swap16(a, b);
+  return min_nc(a, b);
+}
+__device__ __forceinline__ float row_max4_pair(float va, float vb) {
+  swap32(va, vb);
+  float v = max_nc(va, vb);
+  float a = v, b = v;
+  swap16(a, b);
+  return max_nc(a, b);
+}
+// Inverse of the pair scatter: `v` holds one value in lanes 0..31 and another in 32..63;
+// returns the first in lo and the second in hi, in every lane.
+__device__ __forceinline__ void halves_broadcast(float v, float& lo, float& hi) {
+  lo = v, hi = v;
+  swap32(lo, hi);
 }
 __device__ __forceinline__ float wave_sum4(float v) {
   v += __shfl_xor(v, 16);
@@ -239,12 +290,13 @@ __device__ __forceinline__ void lds_barrier() {
 // ---------------------------------------------------------------- group quantiser
 // Per-group parameters from min/max, exactly as the CPU oracle defines them:
 //   scale_h = fp16(min((mx - mn) * fp32(1/qmax), 65504)), 1 when that is 0;
-//   zero_h  = fp16(clamp(mn)); inv = 1 / fp32(scale_h) correctly rounded; nzi = -zf * inv.
+//   zero_h  = fp16(clamp(mn)); inv = 1 / fp32(scale_h) correctly rounded;
+//   a = fp32(inv * fp32(1/qmax)); b = fp32(-fp32(zero_h) * a).
 // The reciprocal is rcp + one Newton step, which equals the correctly rounded 1/x for every
 // positive finite fp16 x (checked exhaustively on gfx950).
 struct GroupParams {
-  float inv, nzi;
-  uint32_t sh, zh;
+  float a, b;
+  uint32_t qp;  // scale_h | zero_h << 16, the qparams pair as stored
 };
 template <int BITS>
 __device__ __forceinline__ GroupParams group_params(float mn, float mx) {
@@ -253,29 +305,24 @@ __device__ __forceinline__ GroupParams group_params(float mn, float mx) {
   const float s = fminf(__fmul_rn(__fsub_rn(mx, mn), kInvQmax), 65504.f);
   uint32_t sh = f16_bits(s);
   if ((sh & 0x7fffu) == 0) sh = 0x3c00u;  // 1.0
-  const float z = fminf(fmaxf(mn, -65504.f), 65504.f);
-  gp.sh = sh;
-  gp.zh = f16_bits(z);
+  const uint32_t zh = f16_bits(__builtin_amdgcn_fmed3f(mn, -65504.f, 65504.f));
+  gp.qp = sh | (zh << 16);
   const float sf = f16_val(sh);
   const float r0 = __builtin_amdgcn_rcpf(sf);
-  gp.inv = __builtin_fmaf(__builtin_fmaf(-sf, r0, 1.0f), r0, r0);
-  gp.nzi = __fmul_rn(-f16_val(gp.zh), gp.inv);
+  const float inv = __builtin_fmaf(__builtin_fmaf(-sf, r0, 1.0f), r0, r0);
+  gp.a = __fmul_rn(inv, kInvQmax);
+  gp.b = __fmul_rn(-f16_val(zh), gp.a);
   return gp;
 }
-// code = clamp(rint(fma(r, inv, nzi)), 0, qmax), returned as the bit pattern of
-// 1.5*2^23 + code: clamping before rounding gives the same code for every t, and adding
-// 1.5*2^23 to t in [0, qmax] rounds it to an integer (half to even) in the low mantissa
-// bits, so the code is the low BITS bits of the result.
+// code = rint(qmax * clamp(fma(r, a, b), 0, 1)), returned as the bit pattern of
+// 1.5*2^23 + code: the clamp folds into the fma (clamp modifier; NaN gives 0), and
+// fma(u, qmax, 1.5*2^23) rounds u*qmax to an integer (half to even) in the low mantissa
+// bits, so the code is the low BITS bits of the result and bits BITS..7 are zero.
 template <int BITS>
 __device__ __forceinline__ uint32_t quant_code_bits(float r, const GroupParams& gp) {
   constexpr float qmax = (float)((1 << BITS) - 1);
-  float t = __builtin_fmaf(r, gp.inv, gp.nzi);
-  t = __builtin_amdgcn_fmed3f(t, 0.f, qmax);
-  return __float_as_uint(__fadd_rn(t, 12582912.0f));
-}
-template <int BITS>
-__device__ __forceinline__ uint32_t quant_code(float r, const GroupParams& gp) {
-  return quant_code_bits<BITS>(r, gp) & ((1u << BITS) - 1u);
+  const float u = __builtin_amdgcn_fmed3f(__builtin_fmaf(r, gp.a, gp.b), 0.f, 1.f);
+  return __float_as_uint(__builtin_fmaf(u, qmax, 12582912.0f));
 }
 // Gather byte 0 of four dwords into one dword (b0 in bits 0..7).
 __device__ __forceinline__ uint32_t gather_bytes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {

@@ -7,8 +7,10 @@
 //     its units (V rows) in registers for the whole kernel, and its share of the current
 //     16-row block of X in registers while the next block streams in (double buffer).  The
 //     projection's V^T operand is regenerated from the register-resident V operand with an
-//     identity MFMA, so V is read from memory once per workgroup.  Partial L tiles are
-//     reduced across waves through LDS behind a barrier that does not wait for the prefetch.
+//     identity MFMA, so V is read from memory once per workgroup.  Partial L tiles go
+//     through LDS; each wave sums a 1/NW slice of the tile and writes it as bf16, and every
+//     wave reads back its rows of L (two barriers per row block, neither of which waits for
+//     the prefetch).
 //   * k_project + k_quant — two passes for other shapes (rank 32, hidden sizes without a
 //     persistent instantiation); X is read twice.  k_quant alone is the whole rank-0 encode
 //     (with optional outlier channels).
@@ -28,7 +30,9 @@ template <int BITS, int G, int R, int NW, int UPW>
 struct PersistLds {
   static constexpr int kVopPerWave = UPW * (8 / BITS) * (G / 16) * (R / 16);  // u32x2 per lane
   static constexpr size_t kVopBytes = (size_t)NW * kVopPerWave * 64 * 8;
-  static constexpr size_t kRedBytes = (size_t)2 * NW * (R / 16) * 64 * 16;
+  static constexpr size_t kPartBytes = (size_t)NW * (R / 16) * 64 * 16;  // per-wave partial L tiles
+  static constexpr size_t kLBytes = (size_t)16 * R * 2;                  // reduced L tile, bf16
+  static constexpr size_t kRedBytes = kPartBytes + kLBytes;
 };
 
 template <int BITS, int G, int R, int NW, int UPW, bool DB, bool VLDS, int RBW>
@@ -39,9 +43,9 @@ __global__ __launch_bounds__(NW * 64) void k_encode_persist(
   constexpr int NP = 8 / BITS, CPG = G / 32, RT = R / 16, E = G / 4;
   using Lds = PersistLds<BITS, G, R, NW, UPW>;
   extern __shared__ __attribute__((aligned(16))) unsigned char shm[];
-  f32x4* red = reinterpret_cast<f32x4*>(shm);                          // [2][NW*RT*64]
-  u32x2* vlds = reinterpret_cast<u32x2*>(shm + Lds::kRedBytes);        // [NW][kVopPerWave][64]
-
+  f32x4* part = reinterpret_cast<f32x4*>(shm);                              // [NW][RT][64]
+  uint16_t* ltile = reinterpret_cast<uint16_t*>(shm + Lds::kPartBytes);     // [16][R]
+  u32x2* vlds = reinterpret_cast<u32x2*>(shm + Lds::kRedBytes);             // [NW][kVopPerWave][64]
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int nrb = (M + 15) / 16;
@@ -95,7 +99,14 @@ __global__ __launch_bounds__(NW * 64) void k_encode_persist(
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  auto process = [&](const u32x4 (&x)[UPW][NP][CPG], int rb, int parity) {
+  // The L tile of a row block is RT*256 fp32 sums over NW partials; wave w reduces floats
+  // [w*F, (w+1)*F): lane l adds partials (l/F)*PPL .. +PPL-1 of float l%F, and the S lanes
+  // holding the same float combine with xor-shuffles.
+  constexpr int F = RT * 256 / NW, S = 64 / F, PPL = NW / S;
+  static_assert(F >= 1 && F <= 64 && 64 % F == 0 && NW % S == 0, "L reduction split");
+  const float* partf = reinterpret_cast<const float*>(part);
+
+  auto process = [&](const u32x4 (&x)[UPW][NP][CPG], int rb) {
     const int row = min(rb * 16 + j, M - 1);  // rows past the end repeat the last row (see load)
     // two accumulator chains (even / odd unit-plane) to halve the dependent MFMA sequence
     f32x4 acc[2][RT];
@@ -109,7 +120,6 @@ __global__ __launch_bounds__(NW * 64) void k_encode_persist(
         vops(uu, p, v);
         project_unit<G, R>(v, x[uu][p], ident, acc[(uu * NP + p) & 1]);
       }
-    f32x4* rp = red + parity * (NW * RT * 64);
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
       f32x4 a = acc[0][t];
@@ -117,25 +127,30 @@ __global__ __launch_bounds__(NW * 64) void k_encode_persist(
       a[1] += acc[1][t][1];
       a[2] += acc[1][t][2];
       a[3] += acc[1][t][3];
-      rp[(w * RT + t) * 64 + lane] = a;
+      part[(w * RT + t) * 64 + lane] = a;
     }
     lds_barrier();
-    u32x2 lop[RT];
+    {
+      const int f = lane % F, pg = lane / F;
+      const int fi = w * F + f;                          // float of the tile: (t, source lane, v)
+      const int t = fi >> 8, src = (fi >> 2) & 63, v = fi & 3;
+      float sum = 0.f;
+#pragma unroll
+      for (int i = 0; i < PPL; ++i) sum += partf[(((pg * PPL + i) * RT + t) * 64 + src) * 4 + v];
+#pragma unroll
+      for (int m = F; m < 64; m <<= 1) sum += __shfl_xor(sum, m);
+      // source lane (j', g') of partial tile t holds L[row j'][16t + 4g' + v]
+      if (pg == 0) ltile[(src & 15) * R + 16 * t + 4 * (src >> 4) + v] = (uint16_t)pack_bf16x2(sum, 0.f);
+    }
+    lds_barrier();
+    u32x2 lop[RT], lopn[RT];
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
-      f32x4 s = rp[t * 64 + lane];
-#pragma unroll
-      for (int w2 = 1; w2 < NW; ++w2) {
-        const f32x4 o = rp[(w2 * RT + t) * 64 + lane];
-        s[0] += o[0];
-        s[1] += o[1];
-        s[2] += o[2];
-        s[3] += o[3];
-      }
-      lop[t] = u32x2{pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3])};
-      // every wave holds the reduced tile; wave w stores rows j with j % NW == w
-      st8_pred(Lout + (int64_t)rb * 16 * ldl, (uint32_t)(16 * ldl * 2), (uint32_t)((j * ldl + 16 * t + 4 * g) * 2),
-               lop[t], (j % NW) == w && rb * 16 + j < M);
+      lop[t] = *reinterpret_cast<const u32x2*>(ltile + j * R + 16 * t + 4 * g);
+      lopn[t] = neg_bf16x4(lop[t]);
+      // wave 0 stores the tile (rows past the end rewrite the last row's L)
+      st8_pred(Lout + (int64_t)rb * 16 * ldl, (uint32_t)(16 * ldl * 2),
+               (uint32_t)(((row - rb * 16) * ldl + 16 * t + 4 * g) * 2), lop[t], w == 0);
     }
     uint8_t* crow = codes + (int64_t)row * ldc;
     uint16_t* qrow = qparams + (int64_t)row * ldq;
@@ -144,7 +159,7 @@ __global__ __launch_bounds__(NW * 64) void k_encode_persist(
       u32x2 v[NP][G / 16][RT];
 #pragma unroll
       for (int p = 0; p < NP; ++p) vops(uu, p, v[p]);
-      quant_unit<BITS, G, R>(x[uu], v, lop, nullptr, w * UPW + uu, N, g, crow, qrow);
+      quant_unit<BITS, G, R>(x[uu], v, lopn, nullptr, w * UPW + uu, N, g, crow, qrow);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep row blocks from interleaving (register pressure)
   };
@@ -159,10 +174,10 @@ __global__ __launch_bounds__(NW * 64) void k_encode_persist(
   for (int b = 0; b < RBW; ++b) {
     if constexpr (DB) {
       if (b + 1 < RBW) load(xs[(b + 1) & 1], min(rb0 + b + 1, nrb - 1), true);
-      process(xs[b & 1], min(rb0 + b, nrb - 1), b & 1);
+      process(xs[b & 1], min(rb0 + b, nrb - 1));
     } else {
       if (b > 0) load(xs[0], min(rb0 + b, nrb - 1), true);
-      process(xs[0], min(rb0 + b, nrb - 1), b & 1);
+      process(xs[0], min(rb0 + b, nrb - 1));
     }
   }
 }
@@ -259,17 +274,17 @@ __global__ __launch_bounds__(256) void k_quant(
     const int row = (blockIdx.x * RB + b) * 64 + w * 16 + j;
     if (row - j >= M) break;  // whole 16-row block past the end (uniform per wave)
     const int64_t rr = min(row, M - 1);
-    u32x2 lop[RT];
+    u32x2 lopn[RT];  // -L
     if constexpr (R > 0) {
 #pragma unroll
-      for (int t = 0; t < RT; ++t) lop[t] = ld8(Lin + rr * ldl + 16 * t + 4 * g);
+      for (int t = 0; t < RT; ++t) lopn[t] = neg_bf16x4(ld8(Lin + rr * ldl + 16 * t + 4 * g));
     }
     u32x4 x[NP][CPG];
 #pragma unroll
     for (int p = 0; p < NP; ++p)
 #pragma unroll
       for (int k = 0; k < CPG; ++k) x[p][k] = ld16_stream(X + rr * ldx + unit_base(p, u, N, NP, G) + E * g + 8 * k);
-    quant_unit<BITS, G, R>(x, vop, lop, OUTL ? colmask : nullptr, u, N, g, codes + rr * ldc,
+    quant_unit<BITS, G, R>(x, vop, lopn, OUTL ? colmask : nullptr, u, N, g, codes + rr * ldc,
                            qparams + rr * ldq);
   }
 }
