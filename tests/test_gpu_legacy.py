@@ -1,0 +1,165 @@
+"""GPU parity of the reference-format ("legacy") operators and the dense consumers.
+
+Each reference entry point (legacy.py) runs on the HIP kernels and is compared with the CPU
+restatement of the reference's torch form (oracle/lrq_oracle.py legacy_* functions).  The
+torch forms round to bf16 after every op; the kernels reproduce those roundings, and l @ r
+is the fp32 rounding of the exact sum in both, so codes, outliers and bf16 outputs are
+expected to match bit for bit (the assertion allows the north-star tie budget of 1e-4).
+Shapes cover both kernel paths: the MFMA path (every plane a multiple of 64 columns,
+16-byte aligned operands) and the scalar path (the reference's 32 x 32 smoke shape, odd
+widths, unaligned row strides), K below 16 and between 16 and 32 (zero-padded, R14),
+batch-shared and per-batch scales, 1/2/4/8-bit codes.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from parity import TIE_BUDGET, assert_fp_close, bits16, from_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(seed, B, M, N, K, s_rows, scale_lo=0.05, scale_hi=0.4, outlier_cols=4):
+    g = torch.Generator().manual_seed(seed)
+    l = (torch.randn(M, K, generator=g) * 0.5).to(torch.bfloat16)
+    r = (torch.randn(K, N, generator=g) * 0.5).to(torch.bfloat16)
+    x = torch.randn(B, M, N, generator=g)
+    cols = torch.randperm(N, generator=g)[:outlier_cols]
+    x[:, :, cols] *= 12.0
+    x = x.to(torch.bfloat16)
+    s = (scale_lo + (scale_hi - scale_lo) * torch.rand(s_rows, N, generator=g)).to(torch.bfloat16)
+    return l, r, x, s
+
+
+def _frac_mismatch(a: np.ndarray, b: np.ndarray) -> float:
+    return float((a != b).sum()) / max(1, a.size)
+
+
+CASES = [
+    # (B, M, N, K, bits, s_rows, tau) — path noted
+    (1, 32, 32, 16, 4, 1, 5.0),      # reference smoke shape: scalar path
+    (2, 100, 1024, 16, 4, 2, 5.0),   # MFMA, per-batch scales, ragged rows
+    (1, 64, 2048, 32, 8, 1, 5.0),    # MFMA, K = 32
+    (1, 48, 1024, 8, 2, 1, 4.0),     # MFMA, K = 8 padded to 16
+    (1, 40, 1024, 16, 1, 1, 12.0),   # MFMA, 1-bit (8 planes), tau = 12 as the encode speed test
+    (3, 17, 96, 20, 4, 3, 5.0),      # scalar, K = 20 padded to 32
+]
+
+
+@pytest.mark.parametrize("B,M,N,K,bits,s_rows,tau", CASES)
+def test_legacy_encode_decode(pkg, dev, B, M, N, K, bits, s_rows, tau):
+    l, r, x, s = _inputs(1000 + N + bits, B, M, N, K, s_rows)
+    lb, rb, xb, sb = bits16(l), bits16(r), bits16(x), bits16(s)
+    o_sp, q = pkg.low_rank_addition_fuse_compression_quantization(l.to(dev), r.to(dev), x.to(dev), s.to(dev),
+                                                                  quantize_bit=bits, outlier=tau)
+    torch.cuda.synchronize()
+    assert o_sp.is_sparse
+    o_ref, q_ref = O.legacy_encode(lb, rb, xb, sb, bits, tau)
+    qg = q.cpu().numpy()
+    assert qg.shape == q_ref.shape
+    fq = _frac_mismatch(qg, q_ref)
+    assert fq <= TIE_BUDGET, f"code bytes differ: {fq}"
+    og = bits16(o_sp.to_dense())
+    # outliers: values equal; the sign of non-outlier zeros is not part of the format
+    nz = (O.bf16_to_f32(o_ref) != 0) | (O.bf16_to_f32(og) != 0)
+    assert _frac_mismatch(og[nz], o_ref[nz]) <= TIE_BUDGET
+    assert int(nz.sum()) > 0, "test data should contain outliers"
+
+    # decode of the oracle's own (q, o): bf16 bit parity
+    xh = pkg.low_rank_addition_fuse_decompression_dequantization(
+        l.to(dev), r.to(dev), torch.from_numpy(q_ref).to(dev), from_bits(o_ref, dev), s.to(dev), quantize_bit=bits)
+    xh_ref = O.legacy_decode(lb, rb, q_ref, o_ref, sb, bits)
+    assert _frac_mismatch(bits16(xh), xh_ref) <= TIE_BUDGET
+
+    # round trip through the device's own encode == the unpacked naive round trip (R5)
+    xh2 = pkg.low_rank_addition_fuse_decompression_dequantization(l.to(dev), r.to(dev), q, o_sp, s.to(dev),
+                                                                  quantize_bit=bits)
+    naive = O.naive_roundtrip(lb, rb, xb, sb, bits, tau)
+    assert _frac_mismatch(bits16(xh2), naive) <= TIE_BUDGET
+
+    # decode without outliers
+    xh3 = pkg.low_rank_addition_fuse_decompression_dequantization(l.to(dev), r.to(dev), q, None, s.to(dev),
+                                                                  quantize_bit=bits)
+    assert _frac_mismatch(bits16(xh3), O.legacy_decode(lb, rb, qg, None, sb, bits)) <= TIE_BUDGET
+
+
+def test_legacy_encode_strided_input(pkg, dev):
+    """x rows with a padded stride (the reference passes x's strides to its kernel): an
+    8-aligned stride stays on the MFMA path, an odd one takes the scalar path."""
+    B, M, N, K, bits = 2, 40, 1024, 16, 4
+    l, r, x, s = _inputs(77, B, M, N, K, 1)
+    for pad in (8, 3):
+        wide = torch.zeros(B, M, N + pad, dtype=torch.bfloat16)
+        wide[:, :, :N] = x
+        xs = wide.to(dev)[:, :, :N]
+        assert xs.stride(1) == N + pad
+        o_sp, q = pkg.low_rank_addition_fuse_compression_quantization(l.to(dev), r.to(dev), xs, s.to(dev),
+                                                                      quantize_bit=bits)
+        o_ref, q_ref = O.legacy_encode(bits16(l), bits16(r), bits16(x), bits16(s), bits, 5.0)
+        assert _frac_mismatch(q.cpu().numpy(), q_ref) <= TIE_BUDGET, f"pad {pad}"
+
+
+FUSED = [
+    (1, 64, 1024, 16, 2),   # the fused wrappers' default 2-bit codes, MFMA path
+    (2, 33, 1024, 16, 4),   # ragged rows, batch 2
+    (1, 32, 32, 16, 2),     # scalar path
+]
+
+
+@pytest.mark.parametrize("B,M,N,K,bits", FUSED)
+def test_legacy_fused_consumers(pkg, dev, B, M, N, K, bits):
+    l, r, x, s = _inputs(5000 + N, B, M, N, K, 1, outlier_cols=0)
+    lb, rb, xb, sb = bits16(l), bits16(r), bits16(x), bits16(s)
+    _, q_ref = O.legacy_encode(lb, rb, xb, sb, bits, 1e9)
+    xh = O.bf16_to_f32(O.legacy_decode(lb, rb, q_ref, None, sb, bits))
+    g = torch.Generator().manual_seed(99)
+    dy = (torch.randn(B, M, N, generator=g) * 0.02).to(torch.bfloat16)
+    yb = bits16(dy)
+    yf = O.bf16_to_f32(yb)
+    q = torch.from_numpy(q_ref).to(dev)
+    args = (l.to(dev), r.to(dev), q, s.to(dev), dy.to(dev))
+    out = pkg.triton_silu_backward_fuse_extraction(*args, quantize_bit=bits)
+    assert_fp_close(bits16(out), O.silu_bwd(xh, yf), "legacy fused SiLU bwd")
+    out = pkg.triton_silu_backward_add_extraction(*args, quantize_bit=bits)
+    assert_fp_close(bits16(out), O.silu_bwd(xh, yf), "legacy unfused SiLU bwd")
+    out = pkg.triton_hadamard_fuse_extraction(*args, quantize_bit=bits)
+    assert _frac_mismatch(bits16(out), O.round_out(O.mul(xh, yf))) <= TIE_BUDGET
+    out = pkg.triton_hadamard_add_extraction(*args, quantize_bit=bits)
+    assert _frac_mismatch(bits16(out), O.round_out(O.mul(xh, yf))) <= TIE_BUDGET
+    # dequant-matmul (R12, legacy format): x_hat @ y with y [B, N, 32]
+    yk = (torch.randn(B, N, 32, generator=g) * 0.1).to(torch.bfloat16)
+    mm = pkg.triton_matmul_decompress(q, l.to(dev), r.to(dev), s.to(dev), yk.to(dev), quantize_bit=bits)
+    ref = np.stack([O.gemm(xh[b], O.bf16_to_f32(bits16(yk[b]))) for b in range(B)])
+    assert_fp_close(bits16(mm), ref, "legacy dequant matmul", max_abs=2e-2, rel_l2=1e-2)
+
+
+@pytest.mark.parametrize("B,M,N,K", [(2, 100, 1024, 16), (1, 32, 32, 8), (1, 16, 96, 32)])
+def test_low_rank_addition(pkg, dev, B, M, N, K):
+    l, r, x, _ = _inputs(300 + N, B, M, N, K, 1)
+    out = pkg.low_rank_addition(l.to(dev), r.to(dev), x.to(dev))
+    ref = O.lowrank_add(bits16(l), bits16(r), bits16(x))
+    assert _frac_mismatch(bits16(out), ref) <= TIE_BUDGET
+
+
+@pytest.mark.parametrize("shape", [(2, 64, 1024), (1, 7, 333)])
+def test_dense_elementwise(pkg, dev, shape):
+    g = torch.Generator().manual_seed(11)
+    x = (torch.randn(*shape, generator=g) * 2).to(torch.bfloat16)
+    y = (torch.randn(*shape, generator=g) * 0.02).to(torch.bfloat16)
+    xf, yf = O.bf16_to_f32(bits16(x)), O.bf16_to_f32(bits16(y))
+    assert_fp_close(bits16(pkg.triton_silu_backward(x.to(dev), y.to(dev))), O.silu_bwd(xf, yf), "dense SiLU bwd")
+    assert_fp_close(bits16(pkg.triton_gelu_backward(x.to(dev), y.to(dev))), O.gelu_bwd(xf, yf), "dense GELU bwd")
+    assert _frac_mismatch(bits16(pkg.triton_hadamard(x.to(dev), y.to(dev))), O.round_out(O.mul(xf, yf))) == 0
+
+
+@pytest.mark.parametrize("shape", [(2, 4, 64, 64), (1, 2, 8, 2048), (1, 1, 5, 2050), (1, 1, 3, 10000)])
+def test_dense_softmax_bwd(pkg, dev, shape):
+    g = torch.Generator().manual_seed(12)
+    logits = torch.randn(*shape, generator=g) / np.sqrt(128)
+    p = torch.softmax(logits, dim=-1).to(torch.bfloat16)
+    dp = (torch.randn(*shape, generator=g) * 0.02).to(torch.bfloat16)
+    pf, dpf = O.bf16_to_f32(bits16(p)), O.bf16_to_f32(bits16(dp))
+    out = pkg.triton_softmax_backward(p.to(dev), dp.to(dev))
+    assert_fp_close(bits16(out), O.softmax_bwd(pf, dpf), "dense softmax bwd", max_abs=1e-3)

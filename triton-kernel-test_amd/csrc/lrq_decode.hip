@@ -10,112 +10,98 @@
 // while it computes the current.
 #include "lrq_common.h"
 #include "lrq_host.h"
+#include "lrq_math.h"
 
 namespace lrq {
 
 // ------------------------------------------------------------------ epilogues
-// An epilogue binds its row pointers once per row block (`row(r)`), then receives 8
-// consecutive reconstructed values (fp32, before the bf16 rounding that defines x_hat)
-// for columns col .. col + 7 of that row.  Stores are unconditional: lanes of rows past the
-// end are clamped to the last row and store the same bytes as its own lanes, which keeps
-// the instruction stream branch-free (on gfx9 a conditional store makes the compiler drain
-// every outstanding memory operation at the next load use, prefetches included).
+// An epilogue maps 8 consecutive reconstructed values of a row (fp32, before the bf16
+// rounding that defines x_hat) to the 8 bf16 it stores.  Consumers that read a second
+// tensor (kIn) get its 8 matching bf16 as a vector that the kernel prefetched together with
+// the codes: on gfx9 one in-order counter tracks loads and stores, so a load issued after
+// a row block's stores could only be consumed once those stores had completed.
 struct EpiStore {
+  static constexpr bool kIn = false;
   uint16_t* out;
   int64_t ld;
-  struct Row {
-    uint16_t* o;
-  };
-  __device__ __forceinline__ Row row(int64_t r) const { return Row{out + r * ld}; }
-  __device__ __forceinline__ void operator()(const Row& r, int col, const float* xh) const {
-    st16(r.o + col, pack8(xh));
-  }
+  __device__ __forceinline__ const uint16_t* in_row(int64_t) const { return nullptr; }
+  __device__ __forceinline__ uint16_t* out_row(int64_t r) const { return out + r * ld; }
+  __device__ __forceinline__ u32x4 apply(const float* xh, u32x4) const { return pack8(xh); }
 };
 
-struct RowIO {
-  const uint16_t* in;
-  uint16_t* o;
-};
-
-// silu_backward.py:6-8: dy * (s * (1 + x * (1 - s))), s = sigmoid(x), x = bf16(x_hat); fp32.
+// silu_backward.py:6-8 on x = bf16(x_hat), fp32 (lrq_math.h).
 struct EpiSilu {
+  static constexpr bool kIn = true;
   const uint16_t* dy;
   int64_t lddy;
   uint16_t* dx;
   int64_t lddx;
-  using Row = RowIO;
-  __device__ __forceinline__ Row row(int64_t r) const { return Row{dy + r * lddy, dx + r * lddx}; }
-  __device__ __forceinline__ void operator()(const Row& r, int col, const float* xh) const {
+  __device__ __forceinline__ const uint16_t* in_row(int64_t r) const { return dy + r * lddy; }
+  __device__ __forceinline__ uint16_t* out_row(int64_t r) const { return dx + r * lddx; }
+  __device__ __forceinline__ u32x4 apply(const float* xh, u32x4 dyv) const {
     float d[8], o[8];
-    unpack8(ld16_stream(r.in + col), d);
+    unpack8(dyv, d);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float x = bf16_roundtrip(xh[e]);
-      const float s = __builtin_amdgcn_rcpf(1.f + __expf(-x));
-      o[e] = d[e] * (s * (1.f + x * (1.f - s)));
-    }
-    st16(r.o + col, pack8(o));
+    for (int e = 0; e < 8; ++e) o[e] = silu_bwd_f32(bf16_roundtrip(xh[e]), d[e]);
+    return pack8(o);
   }
 };
 
-// gelu_backward.py:14-21 (tanh approximation), fp32 on x = bf16(x_hat).
+// gelu_backward.py:14-21 (tanh approximation) on x = bf16(x_hat), fp32 (lrq_math.h).
 struct EpiGelu {
+  static constexpr bool kIn = true;
   const uint16_t* dy;
   int64_t lddy;
   uint16_t* dx;
   int64_t lddx;
-  using Row = RowIO;
-  __device__ __forceinline__ Row row(int64_t r) const { return Row{dy + r * lddy, dx + r * lddx}; }
-  __device__ __forceinline__ void operator()(const Row& r, int col, const float* xh) const {
-    constexpr float kGamma = 0.7978845608028654f, kKappa = 0.044715f;
+  __device__ __forceinline__ const uint16_t* in_row(int64_t r) const { return dy + r * lddy; }
+  __device__ __forceinline__ uint16_t* out_row(int64_t r) const { return dx + r * lddx; }
+  __device__ __forceinline__ u32x4 apply(const float* xh, u32x4 dyv) const {
     float d[8], o[8];
-    unpack8(ld16_stream(r.in + col), d);
+    unpack8(dyv, d);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float x = bf16_roundtrip(xh[e]);
-      const float x2 = x * x;
-      const float u = kGamma * (x + kKappa * x2 * x);
-      // tanh(u) = 1 - 2 / (exp(2u) + 1); saturates correctly at +-1.
-      const float th = 1.f - 2.f * __builtin_amdgcn_rcpf(__expf(2.f * u) + 1.f);
-      o[e] = 0.5f * ((1.f + th) + x * ((1.f - th * th) * kGamma * (1.f + 3.f * kKappa * x2))) * d[e];
-    }
-    st16(r.o + col, pack8(o));
+    for (int e = 0; e < 8; ++e) o[e] = gelu_bwd_f32(bf16_roundtrip(xh[e]), d[e]);
+    return pack8(o);
   }
 };
 
 // extraction_fuse_hadamard.py:5-6: x * y.
 struct EpiMul {
+  static constexpr bool kIn = true;
   const uint16_t* y;
   int64_t ldy;
   uint16_t* out;
   int64_t ldo;
-  using Row = RowIO;
-  __device__ __forceinline__ Row row(int64_t r) const { return Row{y + r * ldy, out + r * ldo}; }
-  __device__ __forceinline__ void operator()(const Row& r, int col, const float* xh) const {
+  __device__ __forceinline__ const uint16_t* in_row(int64_t r) const { return y + r * ldy; }
+  __device__ __forceinline__ uint16_t* out_row(int64_t r) const { return out + r * ldo; }
+  __device__ __forceinline__ u32x4 apply(const float* xh, u32x4 yv) const {
     float a[8], o[8];
-    unpack8(ld16_stream(r.in + col), a);
+    unpack8(yv, a);
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = bf16_roundtrip(xh[e]) * a[e];
-    st16(r.o + col, pack8(o));
+    return pack8(o);
   }
 };
 
 // ------------------------------------------------------------------ kernel
-// Per-row-block inputs of one lane: its G/4 code bytes, the unit's NP (scale, zero) pairs
-// and the L operand of its row.
-template <int BITS, int G, int R>
+// Per-row-block inputs of one lane: its G/4 code bytes, the unit's NP (scale, zero) pairs,
+// the L operand of its row and, for consumers that read a second tensor, its G/4 columns of
+// that tensor in every plane.
+template <int BITS, int G, int R, bool IN>
 struct DecIn {
   u32x4 cb[G / 64];
   uint32_t qp[8 / BITS];
   u32x2 lop[R > 0 ? R / 16 : 1];
+  u32x4 ein[IN ? 8 / BITS : 1][IN ? G / 32 : 1];
 };
 
 // Grid: (ceil(row blocks / RBW), ceil(units / NW)); NW waves; wave w owns unit
-// blockIdx.y * NW + w and walks row blocks blockIdx.x * RBW + b, b < RBW.  The waves of a
+// blockIdx.y * NW + w and walks row blocks blockIdx.x * RBW + b, b < RBW, keeping the
+// inputs of the next PD blocks in flight while it reconstructs and stores block b.  The waves of a
 // workgroup work on consecutive units of the same rows, so at any time a workgroup writes
 // NW * G * 2 contiguous bytes per row and plane (DRAM-page friendly), while each wave
 // reuses its unit's V operands for all its row blocks.
-template <int BITS, int G, int R, bool OUTL, int NW, int RBW, class EPI>
+template <int BITS, int G, int R, bool OUTL, int NW, int RBW, int PD, class EPI>
 __global__ __launch_bounds__(NW * 64) void k_decode(
     const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
     const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
@@ -151,8 +137,9 @@ __global__ __launch_bounds__(NW * 64) void k_decode(
     for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, u, N, NP, G), j, g, vop[p]);
   }
 
-  auto load = [&](DecIn<BITS, G, R>& in, int rb, bool valid) {
-    const int64_t row = valid ? min(rb * 16 + j, M - 1) : 0;
+  using In = DecIn<BITS, G, R, EPI::kIn>;
+  auto load = [&](In& in, int rb) {
+    const int64_t row = min(rb * 16 + j, M - 1);
     const uint8_t* cp = codes + row * ldc + u * G + E * g;
 #pragma unroll
     for (int i = 0; i < G / 64; ++i) in.cb[i] = ld16_stream(cp + 16 * i);
@@ -168,11 +155,18 @@ __global__ __launch_bounds__(NW * 64) void k_decode(
 #pragma unroll
       for (int t = 0; t < RT; ++t) in.lop[t] = ld8(Lin + row * ldl + 16 * t + 4 * g);
     }
+    if constexpr (EPI::kIn) {
+      const uint16_t* ir = epi.in_row(row);
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int k = 0; k < G / 32; ++k) in.ein[p][k] = ld16_stream(ir + unit_base(p, u, N, NP, G) + E * g + 8 * k);
+    }
   };
 
-  auto compute = [&](const DecIn<BITS, G, R>& in, int rb) {
+  auto compute = [&](const In& in, int rb) {
     const int64_t rr = min(rb * 16 + j, M - 1);
-    const typename EPI::Row erow = epi.row(rr);
+    uint16_t* orow = epi.out_row(rr);
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       const float sf = f16_val(in.qp[p] & 0xffffu);
@@ -200,41 +194,48 @@ __global__ __launch_bounds__(NW * 64) void k_decode(
         }
       }
 #pragma unroll
-      for (int k = 0; k < E / 8; ++k) epi(erow, c0 + 8 * k, xh + 8 * k);
+      for (int k = 0; k < E / 8; ++k) st16(orow + c0 + 8 * k, epi.apply(xh + 8 * k, in.ein[EPI::kIn ? p : 0][EPI::kIn ? k : 0]));
     }
   };
 
   const int rb0 = blockIdx.x * RBW;
   if (rb0 >= nrb) return;
-  // All of the wave's row-block inputs are requested up front (codes, qparams and L are a
-  // quarter of the traffic); blocks are then reconstructed and stored in order.  With RBW a
-  // compile-time constant and no branch in the body every wait count is exact and no load
-  // is issued after a store.  Blocks past the end (tail workgroup only) repeat the last row
-  // block, rewriting the same bytes.
-  DecIn<BITS, G, R> in[RBW];
+  // The inputs of the first PD blocks are requested up front; block b + PD is requested
+  // before block b is reconstructed and stored (PD + 1 register buffers, indices fixed after
+  // unrolling).  On gfx9 one in-order counter tracks loads and stores, so waiting for a load
+  // issued after a store also waits for that store: PD >= RBW (every load issued before the
+  // first store) is the fastest form measured on MI355X.  With RBW and PD compile-time
+  // constants and no branch in the body every wait count is exact.  Blocks past the end
+  // (tail workgroup only) repeat the last row block, rewriting the same bytes.
+  In in[PD < RBW ? PD + 1 : RBW];
+  constexpr int NB = PD < RBW ? PD + 1 : RBW;
 #pragma unroll
-  for (int b = 0; b < RBW; ++b) load(in[b], min(rb0 + b, nrb - 1), true);
-  __builtin_amdgcn_sched_barrier(0);
+  for (int b = 0; b < PD && b < RBW; ++b) load(in[b % NB], min(rb0 + b, nrb - 1));
 #pragma unroll
-  for (int b = 0; b < RBW; ++b) compute(in[b], min(rb0 + b, nrb - 1));
+  for (int b = 0; b < RBW; ++b) {
+    if (b + PD < RBW) load(in[(b + PD) % NB], min(rb0 + b + PD, nrb - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    compute(in[b % NB], min(rb0 + b, nrb - 1));
+    __builtin_amdgcn_sched_barrier(0);
+  }
 }
 
 // ------------------------------------------------------------------ host side
 template <int BITS, int G, int R, int RBW, class EPI>
 static int decode_launch_rbw(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
-  constexpr int NP = 8 / BITS, NW = 8;
+  constexpr int NP = 8 / BITS, NW = 8, PD = RBW;  // every load before the first store
   const int M = (int)t->rows, N = (int)t->hidden;
   const int units = N / (G * NP);
   const int nrb = (M + 15) / 16;
   dim3 grid((nrb + RBW - 1) / RBW, (units + NW - 1) / NW);
   if (t->n_outlier > 0) {
     const size_t shm = (size_t)(N / 32) * 4 + (size_t)N * 2;
-    hipLaunchKernelGGL((k_decode<BITS, G, R, true, NW, RBW, EPI>), grid, dim3(NW * 64), shm, s,
+    hipLaunchKernelGGL((k_decode<BITS, G, R, true, NW, RBW, PD, EPI>), grid, dim3(NW * 64), shm, s,
                        (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
                        (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, t->outlier_idx, t->n_outlier,
                        (const uint16_t*)t->side, t->ld_side, epi);
   } else {
-    hipLaunchKernelGGL((k_decode<BITS, G, R, false, NW, RBW, EPI>), grid, dim3(NW * 64), 0, s,
+    hipLaunchKernelGGL((k_decode<BITS, G, R, false, NW, RBW, PD, EPI>), grid, dim3(NW * 64), 0, s,
                        (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
                        (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, nullptr, 0, nullptr,
                        (int64_t)0, epi);
@@ -242,13 +243,14 @@ static int decode_launch_rbw(const lrq_tensors* t, hipStream_t s, const EPI& epi
   return launch_status();
 }
 
-// 8 row blocks per wave when that still leaves >= 512 workgroups (2 per CU), else 2.
+// 8 row blocks per wave (4 when the consumer also streams a second tensor in) when that
+// still leaves >= 512 workgroups (2 per CU), else 2.
 template <int BITS, int G, int R, class EPI>
 static int decode_launch(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
-  constexpr int NP = 8 / BITS, NW = 8;
+  constexpr int NP = 8 / BITS, NW = 8, BIG = EPI::kIn ? 4 : 8;
   const int64_t units = t->hidden / (G * NP), nrb = (t->rows + 15) / 16;
-  const int64_t wgs8 = ((nrb + 7) / 8) * ((units + NW - 1) / NW);
-  if (wgs8 >= 512) return decode_launch_rbw<BITS, G, R, 8>(t, s, epi);
+  const int64_t wgs = ((nrb + BIG - 1) / BIG) * ((units + NW - 1) / NW);
+  if (wgs >= 512) return decode_launch_rbw<BITS, G, R, BIG>(t, s, epi);
   return decode_launch_rbw<BITS, G, R, 2>(t, s, epi);
 }
 

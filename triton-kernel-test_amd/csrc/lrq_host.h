@@ -6,11 +6,29 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <cstring>
+#include <initializer_list>
+
 #include "../../include/lrq.h"
 
 namespace lrq {
 
 static inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+// fp32 -> bf16 (round to nearest even) on the host, and back.
+static inline uint16_t bf16_bits_host(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+static inline float bf16_value_host(uint16_t h) {
+  const uint32_t u = (uint32_t)h << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
 
 static constexpr int format_key(int bits, int group, int rank) { return bits * 100000 + group * 100 + rank; }
 

@@ -1,0 +1,343 @@
+// Legacy (reference-format) kernels: the arithmetic of the reference's torch forms.
+//
+//   encode  torch_low_rank_addition_fuse_compression_quantization
+//           (low_rank_extraction_fuse_compression_quantization.py:153-171)
+//             xr = bf16(x - bf16(l @ r));  o = xr if |xr| > bf16(tau) else 0;
+//             c  = clamp(rint(bf16((xr - o) / s)), -2^(b-1), 2^(b-1)-1) + 2^(b-1)
+//             q  = row-planar packing: byte j of a row holds column j + p*N/NP in bits
+//                  p*b .. p*b+b-1 of plane p (NP = 8/b planes)
+//   decode  torch_low_rank_addition_fuse_decompression_dequantization
+//           (low_rank_extraction_fuse_decompression_dequantization.py:155-165)
+//             x_hat = bf16(bf16(bf16((c - 2^(b-1)) * s) + o) + bf16(l @ r))
+//   fused   decode without outliers, then store / SiLU backward / product with y
+//           (extraction_fuse_silu_backward.py:192-216, extraction_fuse_hadamard.py:185-209)
+//   add     torch_low_rank_addition (low_rank_extraction_speed.py:106-107): bf16(x + bf16(l @ r))
+//
+// l is [M, K] and rt = r^T is [N, K] (K = 16 or 32, zero-padded by the caller as the reference
+// pads K < 16); s is [1 or B, N].  bf16(l @ r) is the fp32 rounding of the exact sum, then bf16
+// (what an fp32-accumulating GEMM returns up to the order of its additions).
+//
+// Two implementations with identical results:
+//   * k_legacy_mfma — when every plane is a whole number of 64-column units and the operands
+//     are 16-byte aligned.  The unit layout of lrq_common.h (lane (j, g) owns 16 consecutive
+//     columns of its row in every plane) with l @ r rebuilt on MFMA exactly like the
+//     group-mode reconstruction (V = rt).
+//   * k_legacy_scalar — any shape: one thread per packed byte, l @ r summed in fp64 (the
+//     products of bf16 values are exact and so is their fp64 sum for K <= 32).
+#include "lrq_common.h"
+#include "lrq_host.h"
+#include "lrq_math.h"
+
+namespace lrq {
+
+enum LegacyMode : int { kEncode = 0, kDecode = 1, kFusedStore = 2, kFusedSilu = 3, kFusedMul = 4, kAdd = 5 };
+
+struct LegacyArgs {
+  const uint16_t* l;    // [M, K]
+  const uint16_t* rt;   // [N, K]
+  const uint16_t* x;    // encode / add input [B, M, N] with strides (ldx_b, ldx_m, 1)
+  int64_t ldx_b, ldx_m;
+  const uint16_t* s;    // [s_rows, N]
+  int64_t s_rows;
+  const uint8_t* qin;   // decode / fused codes [B, M, N/NP]
+  const uint16_t* oin;  // decode outliers, dense [B, M, N], or null
+  const uint16_t* y;    // fused SiLU dy / product operand [B, M, N]
+  uint16_t* out;        // decode / fused / add output [B, M, N]
+  uint16_t* oout;       // encode outliers, dense [B, M, N]
+  uint8_t* qout;        // encode codes [B, M, N/NP]
+  int64_t M, N;
+  float tau;            // outlier threshold, already rounded to bf16
+};
+
+// Encode of one element given its bf16 input x, bf16(l @ r) lr and scale sc: returns the code
+// (0 .. 2^b - 1) and writes the outlier value (0 unless an outlier).
+template <int BITS>
+__device__ __forceinline__ uint32_t legacy_code(float x, float lr, float sc, float tau, float& o) {
+  constexpr float half = (float)(1 << (BITS - 1));
+  const float xr = bf16r(x - lr);
+  o = fabsf(xr) > tau ? xr : 0.f;
+  const float d = bf16r((xr - o) / sc);  // IEEE division, then the bf16 rounding of the torch op
+  const float c = __builtin_amdgcn_fmed3f(rintf(d), -half, half - 1.f);
+  return (uint32_t)(int)(c + half);
+}
+
+// Decode of one element: bf16(bf16(bf16((code - 2^(b-1)) * s) + o) + lr); with !HAS_O the add
+// of o (exact zero) is skipped.
+template <int BITS, bool HAS_O>
+__device__ __forceinline__ float legacy_value(uint32_t code, float sc, float o, float lr) {
+  float a = bf16r((float)((int)code - (1 << (BITS - 1))) * sc);
+  if constexpr (HAS_O) a = bf16r(a + o);
+  return bf16r(a + lr);
+}
+
+template <int MODE>
+__device__ __forceinline__ float legacy_consume(float xh, float yv) {
+  if constexpr (MODE == kFusedSilu) return silu_bwd_f32(xh, yv);
+  else if constexpr (MODE == kFusedMul) return xh * yv;
+  else return xh;
+}
+
+// ------------------------------------------------------------------ MFMA path
+// Grid: (ceil(M / (64 * RB)), N / (64 * NP), B); 4 waves; wave w walks row blocks
+// (blockIdx.x * RB + i) * 64 + w * 16, i < RB, of unit blockIdx.y.
+template <int MODE, int BITS, int K, int RB, bool HAS_O>
+__global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
+  constexpr int NP = (MODE == kAdd) ? 1 : 8 / BITS, G = 64, E = 16, RT = K / 16;
+  constexpr uint32_t kMask = BITS == 8 ? 0xffu : (1u << BITS) - 1u;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int u = blockIdx.y, b = blockIdx.z;
+  const int M = (int)a.M, N = (int)a.N;
+  const int64_t NB = N / NP;  // bytes per code row
+  const uint16_t* srow = a.s + (a.s_rows == 1 ? 0 : (int64_t)b * N);
+
+  u32x2 vop[NP][G / 16][RT];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) load_vops<G, K>(a.rt, unit_base(p, u, N, NP, G), j, g, vop[p]);
+  const float zero[E] = {};
+
+  for (int i = 0; i < RB; ++i) {
+    const int row = (blockIdx.x * RB + i) * 64 + w * 16 + j;
+    if (row - j >= M) break;  // whole 16-row block past the end (uniform per wave)
+    const int64_t rr = min(row, M - 1);
+    const int64_t erow = ((int64_t)b * M + rr) * N;  // element offset of the row in [B, M, N] outputs
+    u32x2 lop[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) lop[t] = ld8(a.l + rr * K + 16 * t + 4 * g);
+    u32x4 qb = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (MODE == kDecode || MODE == kFusedStore || MODE == kFusedSilu || MODE == kFusedMul)
+      qb = ld16(a.qin + ((int64_t)b * M + rr) * NB + u * G + E * g);
+    uint32_t byte[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) byte[e] = 0u;
+
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int c0 = unit_base(p, u, N, NP, G) + E * g;
+      float lr[E];
+      residual_unit<G, K>(vop[p], lop, zero, lr);
+#pragma unroll
+      for (int e = 0; e < E; ++e) lr[e] = bf16r(lr[e]);
+      float sc[E];
+      if constexpr (MODE != kAdd) {
+        unpack8(ld16(srow + c0), sc);
+        unpack8(ld16(srow + c0 + 8), sc + 8);
+      }
+      if constexpr (MODE == kEncode || MODE == kAdd) {
+        float xv[E];
+        const uint16_t* xp = a.x + (int64_t)b * a.ldx_b + rr * a.ldx_m + c0;
+        unpack8(ld16(xp), xv);
+        unpack8(ld16(xp + 8), xv + 8);
+        if constexpr (MODE == kEncode) {
+          float ov[E];
+#pragma unroll
+          for (int e = 0; e < E; ++e) byte[e] |= legacy_code<BITS>(xv[e], lr[e], sc[e], a.tau, ov[e]) << (BITS * p);
+          st16(a.oout + erow + c0, pack8(ov));
+          st16(a.oout + erow + c0 + 8, pack8(ov + 8));
+        } else {
+          float ov[E];
+#pragma unroll
+          for (int e = 0; e < E; ++e) ov[e] = xv[e] + lr[e];  // fp32 add, then bf16 (pack8), as torch
+          st16(a.out + erow + c0, pack8(ov));
+          st16(a.out + erow + c0 + 8, pack8(ov + 8));
+        }
+      } else {
+        float ov[E], oo[E], yv[E];
+        if constexpr (MODE == kDecode && HAS_O) {
+          unpack8(ld16(a.oin + erow + c0), oo);
+          unpack8(ld16(a.oin + erow + c0 + 8), oo + 8);
+        }
+        if constexpr (MODE == kFusedSilu || MODE == kFusedMul) {
+          unpack8(ld16(a.y + erow + c0), yv);
+          unpack8(ld16(a.y + erow + c0 + 8), yv + 8);
+        }
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const uint32_t code = (qb[e >> 2] >> (8 * (e & 3) + BITS * p)) & kMask;
+          const float xh = legacy_value<BITS, MODE == kDecode && HAS_O>(code, sc[e], oo[e], lr[e]);
+          ov[e] = legacy_consume<MODE>(xh, yv[e]);
+        }
+        st16(a.out + erow + c0, pack8(ov));
+        st16(a.out + erow + c0 + 8, pack8(ov + 8));
+      }
+    }
+    if constexpr (MODE == kEncode) {
+      uint32_t word[E / 4];
+#pragma unroll
+      for (int k = 0; k < E / 4; ++k) word[k] = gather_bytes(byte[4 * k], byte[4 * k + 1], byte[4 * k + 2], byte[4 * k + 3]);
+      st16(a.qout + ((int64_t)b * M + rr) * NB + u * G + E * g, u32x4{word[0], word[1], word[2], word[3]});
+    }
+  }
+}
+
+// ------------------------------------------------------------------ scalar path
+// One thread per packed byte position c of one row; grid.x enumerates (b, m, 256-byte chunk).
+template <int MODE, int BITS, bool HAS_O>
+__global__ __launch_bounds__(256) void k_legacy_scalar(LegacyArgs a, int K, int64_t chunks) {
+  constexpr int NP = (MODE == kAdd) ? 1 : 8 / BITS;
+  constexpr uint32_t kMask = BITS == 8 ? 0xffu : (1u << BITS) - 1u;
+  const int64_t M = a.M, N = a.N, NB = N / NP;
+  const int64_t blk = blockIdx.x;
+  const int64_t bm = blk / chunks;
+  const int64_t c = (blk - bm * chunks) * 256 + threadIdx.x;
+  if (c >= NB) return;
+  const int64_t b = bm / M, m = bm - b * M;
+  const uint16_t* srow = a.s + (a.s_rows == 1 ? 0 : b * N);
+  const uint16_t* lrow = a.l + m * K;
+  const int64_t erow = bm * N;
+  uint32_t byte = 0u;
+  if constexpr (MODE == kDecode || MODE == kFusedStore || MODE == kFusedSilu || MODE == kFusedMul)
+    byte = a.qin[bm * NB + c];
+  uint32_t qout = 0u;
+  for (int p = 0; p < NP; ++p) {
+    const int64_t col = p * NB + c;
+    const uint16_t* rrow = a.rt + col * K;
+    double acc = 0.0;
+    for (int k = 0; k < K; ++k)
+      acc = __builtin_fma((double)__uint_as_float((uint32_t)lrow[k] << 16),
+                          (double)__uint_as_float((uint32_t)rrow[k] << 16), acc);
+    const float lr = bf16r((float)acc);
+    if constexpr (MODE == kEncode) {
+      const float xv = __uint_as_float((uint32_t)a.x[b * a.ldx_b + m * a.ldx_m + col] << 16);
+      const float sc = __uint_as_float((uint32_t)srow[col] << 16);
+      float o;
+      qout |= legacy_code<BITS>(xv, lr, sc, a.tau, o) << (BITS * p);
+      a.oout[erow + col] = (uint16_t)pack_bf16x2(o, 0.f);
+    } else if constexpr (MODE == kAdd) {
+      const float xv = __uint_as_float((uint32_t)a.x[b * a.ldx_b + m * a.ldx_m + col] << 16);
+      a.out[erow + col] = (uint16_t)pack_bf16x2(xv + lr, 0.f);
+    } else {
+      const float sc = __uint_as_float((uint32_t)srow[col] << 16);
+      const uint32_t code = (byte >> (BITS * p)) & kMask;
+      float o = 0.f, yv = 0.f;
+      if constexpr (MODE == kDecode && HAS_O) o = __uint_as_float((uint32_t)a.oin[erow + col] << 16);
+      if constexpr (MODE == kFusedSilu || MODE == kFusedMul) yv = __uint_as_float((uint32_t)a.y[erow + col] << 16);
+      const float xh = legacy_value<BITS, MODE == kDecode && HAS_O>(code, sc, o, lr);
+      a.out[erow + col] = (uint16_t)pack_bf16x2(legacy_consume<MODE>(xh, yv), 0.f);
+    }
+  }
+  if constexpr (MODE == kEncode) a.qout[bm * NB + c] = (uint8_t)qout;
+}
+
+// ------------------------------------------------------------------ host side
+template <int MODE, int BITS, bool HAS_O>
+static int legacy_launch(const LegacyArgs& a, int K, int64_t B, bool mfma_ok, hipStream_t st) {
+  constexpr int NP = (MODE == kAdd) ? 1 : 8 / BITS;
+  const int64_t NB = a.N / NP;
+  if (mfma_ok && NB % 64 == 0 && NB / 64 <= 65535 && B <= 65535) {
+    constexpr int RB = 4;
+    dim3 grid((unsigned)((a.M + 64 * RB - 1) / (64 * RB)), (unsigned)(NB / 64), (unsigned)B);
+    if (K == 16) hipLaunchKernelGGL((k_legacy_mfma<MODE, BITS, 16, RB, HAS_O>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((k_legacy_mfma<MODE, BITS, 32, RB, HAS_O>), grid, dim3(256), 0, st, a);
+  } else {
+    const int64_t chunks = (NB + 255) / 256;
+    if (B * a.M * chunks > INT32_MAX) return LRQ_ERR_SHAPE;
+    hipLaunchKernelGGL((k_legacy_scalar<MODE, BITS, HAS_O>), dim3((unsigned)(B * a.M * chunks)), dim3(256), 0, st, a,
+                       K, chunks);
+  }
+  return launch_status();
+}
+
+template <int MODE, bool HAS_O>
+static int legacy_bits(const LegacyArgs& a, int K, int64_t B, int bits, bool mfma_ok, hipStream_t st) {
+  switch (bits) {
+    case 1: return legacy_launch<MODE, 1, HAS_O>(a, K, B, mfma_ok, st);
+    case 2: return legacy_launch<MODE, 2, HAS_O>(a, K, B, mfma_ok, st);
+    case 4: return legacy_launch<MODE, 4, HAS_O>(a, K, B, mfma_ok, st);
+    case 8: return legacy_launch<MODE, 8, HAS_O>(a, K, B, mfma_ok, st);
+    default: return LRQ_ERR_UNSUPPORTED;
+  }
+}
+
+// Shape / argument checks common to every legacy entry point.
+static int legacy_check(const void* l, const void* rt, int32_t K, int64_t B, int64_t M, int64_t N, int32_t bits,
+                        const void* s, int64_t s_rows, bool need_s) {
+  if (l == nullptr || rt == nullptr) return LRQ_ERR_NULL;
+  if (need_s && s == nullptr) return LRQ_ERR_NULL;
+  if (K != 16 && K != 32) return LRQ_ERR_UNSUPPORTED;
+  if (bits != 1 && bits != 2 && bits != 4 && bits != 8) return LRQ_ERR_UNSUPPORTED;
+  if (B < 0 || M < 0 || N <= 0 || M > INT32_MAX || N > INT32_MAX) return LRQ_ERR_SHAPE;
+  if (N % (8 / bits) != 0) return LRQ_ERR_SHAPE;
+  if (need_s && s_rows != 1 && s_rows != B) return LRQ_ERR_SHAPE;
+  if (!aligned(l, 2) || !aligned(rt, 2) || (need_s && !aligned(s, 2))) return LRQ_ERR_ALIGN;
+  return LRQ_OK;
+}
+
+// The MFMA path reads and writes 16-byte vectors and 8-byte L / V operands.
+static bool vec_ok(std::initializer_list<const void*> ptrs) {
+  for (const void* p : ptrs)
+    if (p != nullptr && !aligned(p, 16)) return false;
+  return true;
+}
+
+}  // namespace lrq
+
+using namespace lrq;
+
+extern "C" int lrq_legacy_encode(const void* l, const void* rt, int32_t K, const void* x, int64_t B, int64_t M,
+                                 int64_t N, int64_t ldx_b, int64_t ldx_m, const void* s, int64_t s_rows,
+                                 int32_t bits, float outlier, void* o, void* q, void* stream) {
+  int st = legacy_check(l, rt, K, B, M, N, bits, s, s_rows, true);
+  if (st) return st;
+  if (x == nullptr || o == nullptr || q == nullptr) return LRQ_ERR_NULL;
+  if (ldx_m < N || (M > 1 && B > 1 && ldx_b < ldx_m * (M - 1) + N)) return LRQ_ERR_SHAPE;
+  if (!aligned(x, 2) || !aligned(o, 2)) return LRQ_ERR_ALIGN;
+  if (B == 0 || M == 0) return LRQ_OK;
+  LegacyArgs a{};
+  a.l = (const uint16_t*)l, a.rt = (const uint16_t*)rt, a.x = (const uint16_t*)x, a.ldx_b = ldx_b, a.ldx_m = ldx_m;
+  a.s = (const uint16_t*)s, a.s_rows = s_rows, a.oout = (uint16_t*)o, a.qout = (uint8_t*)q, a.M = M, a.N = N;
+  a.tau = bf16_value_host(bf16_bits_host(outlier));
+  const bool mfma_ok = vec_ok({l, rt, x, s, o, q}) && ldx_b % 8 == 0 && ldx_m % 8 == 0 && N % 8 == 0;
+  return legacy_bits<kEncode, false>(a, K, B, bits, mfma_ok, (hipStream_t)stream);
+}
+
+extern "C" int lrq_legacy_decode(const void* l, const void* rt, int32_t K, const void* q, const void* o,
+                                 const void* s, int64_t s_rows, int64_t B, int64_t M, int64_t N, int32_t bits,
+                                 void* out, void* stream) {
+  int st = legacy_check(l, rt, K, B, M, N, bits, s, s_rows, true);
+  if (st) return st;
+  if (q == nullptr || out == nullptr) return LRQ_ERR_NULL;
+  if (!aligned(out, 2) || (o != nullptr && !aligned(o, 2))) return LRQ_ERR_ALIGN;
+  if (B == 0 || M == 0) return LRQ_OK;
+  LegacyArgs a{};
+  a.l = (const uint16_t*)l, a.rt = (const uint16_t*)rt, a.s = (const uint16_t*)s, a.s_rows = s_rows;
+  a.qin = (const uint8_t*)q, a.oin = (const uint16_t*)o, a.out = (uint16_t*)out, a.M = M, a.N = N;
+  const bool mfma_ok = vec_ok({l, rt, q, o, s, out}) && N % 8 == 0;
+  if (o != nullptr) return legacy_bits<kDecode, true>(a, K, B, bits, mfma_ok, (hipStream_t)stream);
+  return legacy_bits<kDecode, false>(a, K, B, bits, mfma_ok, (hipStream_t)stream);
+}
+
+extern "C" int lrq_legacy_fused(const void* l, const void* rt, int32_t K, const void* q, const void* s,
+                                int64_t s_rows, int64_t B, int64_t M, int64_t N, int32_t bits, int32_t op,
+                                const void* y, void* out, void* stream) {
+  int st = legacy_check(l, rt, K, B, M, N, bits, s, s_rows, true);
+  if (st) return st;
+  if (op < 0 || op > 2) return LRQ_ERR_UNSUPPORTED;
+  if (q == nullptr || out == nullptr || (op != 0 && y == nullptr)) return LRQ_ERR_NULL;
+  if (!aligned(out, 2) || (y != nullptr && !aligned(y, 2))) return LRQ_ERR_ALIGN;
+  if (B == 0 || M == 0) return LRQ_OK;
+  LegacyArgs a{};
+  a.l = (const uint16_t*)l, a.rt = (const uint16_t*)rt, a.s = (const uint16_t*)s, a.s_rows = s_rows;
+  a.qin = (const uint8_t*)q, a.y = (const uint16_t*)y, a.out = (uint16_t*)out, a.M = M, a.N = N;
+  const bool mfma_ok = vec_ok({l, rt, q, s, y, out}) && N % 8 == 0;
+  hipStream_t hs = (hipStream_t)stream;
+  switch (op) {
+    case 0: return legacy_bits<kFusedStore, false>(a, K, B, bits, mfma_ok, hs);
+    case 1: return legacy_bits<kFusedSilu, false>(a, K, B, bits, mfma_ok, hs);
+    default: return legacy_bits<kFusedMul, false>(a, K, B, bits, mfma_ok, hs);
+  }
+}
+
+extern "C" int lrq_lowrank_add(const void* l, const void* rt, int32_t K, const void* x, int64_t B, int64_t M,
+                               int64_t N, void* out, void* stream) {
+  int st = legacy_check(l, rt, K, B, M, N, 8, nullptr, 1, false);
+  if (st) return st;
+  if (x == nullptr || out == nullptr) return LRQ_ERR_NULL;
+  if (!aligned(x, 2) || !aligned(out, 2)) return LRQ_ERR_ALIGN;
+  if (B == 0 || M == 0) return LRQ_OK;
+  LegacyArgs a{};
+  a.l = (const uint16_t*)l, a.rt = (const uint16_t*)rt, a.x = (const uint16_t*)x, a.ldx_b = M * N, a.ldx_m = N;
+  a.out = (uint16_t*)out, a.M = M, a.N = N;
+  const bool mfma_ok = vec_ok({l, rt, x, out}) && N % 8 == 0;
+  return legacy_launch<kAdd, 8, false>(a, K, B, mfma_ok, (hipStream_t)stream);
+}
