@@ -10,6 +10,7 @@
 // while it computes the current.
 #include "lrq_common.h"
 #include "lrq_host.h"
+#include "lrq_dequant.h"
 #include "lrq_math.h"
 
 namespace lrq {
@@ -108,7 +109,6 @@ __global__ __launch_bounds__(NW * 64) void k_decode(
     const int32_t* __restrict__ oidx, int nout, const uint16_t* __restrict__ side, int64_t ldside,
     EPI epi) {
   constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, E = G / 4;
-  constexpr uint32_t kMask = (1u << BITS) - 1u;
   extern __shared__ uint32_t smem[];
   uint32_t* colmask = smem;                                    // N/32 words
   int16_t* slot = reinterpret_cast<int16_t*>(smem + N / 32);  // N entries
@@ -169,21 +169,8 @@ __global__ __launch_bounds__(NW * 64) void k_decode(
     uint16_t* orow = epi.out_row(rr);
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-      const float sf = f16_val(in.qp[p] & 0xffffu);
-      const float zf = f16_val(in.qp[p] >> 16);
       float xh[E];
-#pragma unroll
-      for (int d = 0; d < E / 4; ++d) {
-        // the codes of plane p for elements 4d .. 4d+3, one per byte
-        const uint32_t wd = in.cb[d >> 2][d & 3];
-        const uint32_t wq = NP == 1 ? wd : ((wd >> (BITS * p)) & (0x01010101u * kMask));
-        // code * scale is exact, so the fma rounds once, like the oracle's mul + add
-        xh[4 * d + 0] = __builtin_fmaf(ubyte_f32<0>(wq), sf, zf);
-        xh[4 * d + 1] = __builtin_fmaf(ubyte_f32<1>(wq), sf, zf);
-        xh[4 * d + 2] = __builtin_fmaf(ubyte_f32<2>(wq), sf, zf);
-        xh[4 * d + 3] = __builtin_fmaf(ubyte_f32<3>(wq), sf, zf);
-      }
-      if constexpr (R > 0) residual_unit<G, R>(vop[p], in.lop, xh, xh);  // d + L V^T, one rounding
+      reconstruct_plane<BITS, G, R>(in.cb, in.qp[p], p, vop[p], in.lop, xh);
       const int c0 = unit_base(p, u, N, NP, G) + E * g;
       if constexpr (OUTL) {
         const uint32_t mbits = colmask[c0 >> 5] >> (c0 & 31);

@@ -1,0 +1,309 @@
+// Consumers that reduce along the hidden dimension, decompressing in-kernel:
+//
+//   k_softmax_bwd   dS = P (dP - rowsum(dP P)), P = bf16(decode(c)), one pass: the workgroup
+//                   holds whole rows, so the row sum is finished in LDS between the
+//                   reconstruction and the output (softmax_backward.py:6-7 formula; the
+//                   reference has only the uncompressed triton_softmax_backward, :45-61).
+//   k_dequant_gemm  out = bf16(decode(c)) @ A, A [N, n] bf16, fp32 accumulate on MFMA
+//                   (extraction_fuse_matmul.py:224-249 intends this; its kernel reads wrong
+//                   addresses, so the torch form :5-6 defines it).
+#include "lrq_common.h"
+#include "lrq_dequant.h"
+#include "lrq_host.h"
+
+namespace lrq {
+
+// ------------------------------------------------------------------ softmax backward
+// Grid: ceil(row blocks / RBW); NW waves; wave w owns units w*UPW .. +UPW-1 and the host
+// guarantees NW*UPW units per row.  Every input of the workgroup's RBW row blocks is
+// requested up front (no load is issued after a store; see lrq_decode.hip).
+template <int BITS, int G, int R, int NW, int UPW, int RBW>
+__global__ __launch_bounds__(NW * 64) void k_softmax_bwd(
+    const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
+    const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
+    const uint16_t* __restrict__ dp, int64_t lddp, uint16_t* __restrict__ ds, int64_t ldds) {
+  constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, E = G / 4;
+  __shared__ float red[2][NW][16];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int nrb = (M + 15) / 16;
+  const int rb0 = blockIdx.x * RBW;
+
+  u32x2 vop[UPW][NP][G / 16][RT];
+  if constexpr (R > 0) {
+#pragma unroll
+    for (int uu = 0; uu < UPW; ++uu)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, w * UPW + uu, N, NP, G), j, g, vop[uu][p]);
+  }
+  struct In {
+    u32x4 cb[UPW][G / 64];
+    uint32_t qp[UPW][NP];
+    u32x2 lop[RT];
+    u32x4 d[UPW][NP][G / 32];
+  };
+  In in[RBW];
+#pragma unroll
+  for (int b = 0; b < RBW; ++b) {
+    const int64_t row = min(min(rb0 + b, nrb - 1) * 16 + j, M - 1);
+#pragma unroll
+    for (int uu = 0; uu < UPW; ++uu) {
+      const int u = w * UPW + uu;
+#pragma unroll
+      for (int i = 0; i < G / 64; ++i) in[b].cb[uu][i] = ld16_stream(codes + row * ldc + u * G + E * g + 16 * i);
+      if constexpr (NP == 2) {
+        const u32x2 q = ld8(qparams + row * ldq + u * 4);
+        in[b].qp[uu][0] = q[0];
+        in[b].qp[uu][1] = q[1];
+      } else {
+        in[b].qp[uu][0] = ld4(qparams + row * ldq + u * 2);
+      }
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int k = 0; k < G / 32; ++k)
+          in[b].d[uu][p][k] = ld16_stream(dp + row * lddp + unit_base(p, u, N, NP, G) + E * g + 8 * k);
+    }
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t) in[b].lop[t] = ld8(Lin + row * ldl + 16 * t + 4 * g);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+  for (int b = 0; b < RBW; ++b) {
+    const int64_t row = min(min(rb0 + b, nrb - 1) * 16 + j, M - 1);
+    float pv[UPW][NP][E];
+    float part = 0.f;
+#pragma unroll
+    for (int uu = 0; uu < UPW; ++uu)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        reconstruct_plane<BITS, G, R>(in[b].cb[uu], in[b].qp[uu][p], p, vop[uu][p], in[b].lop, pv[uu][p]);
+        float dv[E];
+#pragma unroll
+        for (int k = 0; k < G / 32; ++k) unpack8(in[b].d[uu][p][k], dv + 8 * k);
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          pv[uu][p][e] = bf16_roundtrip(pv[uu][p][e]);
+          part = __builtin_fmaf(pv[uu][p][e], dv[e], part);
+        }
+      }
+    // the row's four lanes, then the NW waves (through LDS)
+    {
+      float a = part, c = part;
+      swap32(a, c);
+      part = a + c;
+      a = part, c = part;
+      swap16(a, c);
+      part = a + c;
+    }
+    if (g == 0) red[b & 1][w][j] = part;
+    lds_barrier();
+    float sum = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2) sum += red[b & 1][w2][j];
+#pragma unroll
+    for (int uu = 0; uu < UPW; ++uu)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const int c0 = unit_base(p, w * UPW + uu, N, NP, G) + E * g;
+        float dv[E], o[E];
+#pragma unroll
+        for (int k = 0; k < G / 32; ++k) unpack8(in[b].d[uu][p][k], dv + 8 * k);
+#pragma unroll
+        for (int e = 0; e < E; ++e) o[e] = pv[uu][p][e] * (dv[e] - sum);
+#pragma unroll
+        for (int k = 0; k < G / 32; ++k) st16(ds + row * ldds + c0 + 8 * k, pack8(o + 8 * k));
+      }
+  }
+}
+
+// ------------------------------------------------------------------ dequant-GEMM
+// Grid: ceil(row blocks / RBW); NW waves; wave w takes units w, w + NW, ...; for each unit
+// it decodes the RBW row blocks and multiplies them into its partial out tiles (A's MFMA
+// operand is regenerated per unit with the identity-MFMA transpose of lrq_common.h).  The NW
+// partial tiles of a row block are then summed through LDS, each wave summing 1/NW of it.
+template <int BITS, int G, int R, int NOUT, int NW, int RBW, bool OUT_F32>
+__global__ __launch_bounds__(NW * 64) void k_dequant_gemm(
+    const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
+    const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
+    const uint16_t* __restrict__ A, void* __restrict__ out, int64_t ldo) {
+  constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, TO = NOUT / 16, E = G / 4;
+  __shared__ f32x4 part[NW][TO][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int nrb = (M + 15) / 16;
+  const int rb0 = blockIdx.x * RBW;
+  const int units = N / (G * NP);
+  const u32x2 ident = identity_bop(j, g);
+
+  f32x4 acc[RBW][TO];
+#pragma unroll
+  for (int b = 0; b < RBW; ++b)
+#pragma unroll
+    for (int t = 0; t < TO; ++t) acc[b][t] = zero4();
+
+  for (int u = w; u < units; u += NW) {
+    u32x2 vop[NP][G / 16][RT];
+    u32x2 va[NP][G / 16][TO];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      if constexpr (R > 0) load_vops<G, R>(V, unit_base(p, u, N, NP, G), j, g, vop[p]);
+      load_vops<G, NOUT>(A, unit_base(p, u, N, NP, G), j, g, va[p]);
+    }
+    u32x4 cb[RBW][G / 64];
+    uint32_t qp[RBW][NP];
+    u32x2 lop[RBW][RT];
+#pragma unroll
+    for (int b = 0; b < RBW; ++b) {
+      const int64_t row = min(min(rb0 + b, nrb - 1) * 16 + j, M - 1);
+#pragma unroll
+      for (int i = 0; i < G / 64; ++i) cb[b][i] = ld16_stream(codes + row * ldc + u * G + E * g + 16 * i);
+      if constexpr (NP == 2) {
+        const u32x2 q = ld8(qparams + row * ldq + u * 4);
+        qp[b][0] = q[0];
+        qp[b][1] = q[1];
+      } else {
+        qp[b][0] = ld4(qparams + row * ldq + u * 2);
+      }
+      if constexpr (R > 0) {
+#pragma unroll
+        for (int t = 0; t < RT; ++t) lop[b][t] = ld8(Lin + row * ldl + 16 * t + 4 * g);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < RBW; ++b)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        float xh[E];
+        reconstruct_plane<BITS, G, R>(cb[b], qp[b][p], p, vop[p], lop[b], xh);
+        u32x4 xb[G / 32];
+#pragma unroll
+        for (int k = 0; k < G / 32; ++k) xb[k] = pack8(xh + 8 * k);  // x_hat = bf16(reconstruction)
+        project_unit<G, NOUT>(va[p], xb, ident, acc[b]);
+      }
+  }
+
+  // acc[b][t] in lane (j, g), component v: out[row j][16t + 4g + v] (partial over this wave's units)
+  constexpr int F = TO * 256 / NW, S = 64 / F, PPL = NW / S;
+  static_assert(F >= 1 && F <= 64 && 64 % F == 0 && NW % S == 0, "out reduction split");
+  const float* partf = reinterpret_cast<const float*>(&part[0][0][0]);
+#pragma unroll
+  for (int b = 0; b < RBW; ++b) {
+    if (rb0 + b >= nrb) break;  // uniform
+#pragma unroll
+    for (int t = 0; t < TO; ++t) part[w][t][lane] = acc[b][t];
+    __syncthreads();
+    const int f = lane % F, pg = lane / F;
+    const int fi = w * F + f;
+    const int t = fi >> 8, src = (fi >> 2) & 63, v = fi & 3;
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) s += partf[(((pg * PPL + i) * TO + t) * 64 + src) * 4 + v];
+#pragma unroll
+    for (int m = F; m < 64; m <<= 1) s += __shfl_xor(s, m);
+    const int row = (rb0 + b) * 16 + (src & 15);
+    const int col = 16 * t + 4 * (src >> 4) + v;
+    if (pg == 0 && row < M) {
+      if constexpr (OUT_F32) reinterpret_cast<float*>(out)[(int64_t)row * ldo + col] = s;
+      else reinterpret_cast<uint16_t*>(out)[(int64_t)row * ldo + col] = (uint16_t)pack_bf16x2(s, 0.f);
+    }
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------------------------ host side
+template <int BITS, int G, int R, int NW, int UPW>
+static int softmax_launch(const lrq_tensors* t, const void* dp, int64_t lddp, void* ds, int64_t ldds, hipStream_t s) {
+  constexpr int RBW = 2;
+  const int M = (int)t->rows, N = (int)t->hidden;
+  const int nrb = (M + 15) / 16;
+  hipLaunchKernelGGL((k_softmax_bwd<BITS, G, R, NW, UPW, RBW>), dim3((nrb + RBW - 1) / RBW), dim3(NW * 64), 0, s,
+                     (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
+                     (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)dp, lddp,
+                     (uint16_t*)ds, ldds);
+  return launch_status();
+}
+
+// One pass needs the whole row in one workgroup: 4, 8 or 16 units (one per wave).
+template <int BITS, int G, int R>
+static int softmax_units(const lrq_tensors* t, const void* dp, int64_t lddp, void* ds, int64_t ldds, hipStream_t s) {
+  const int64_t units = t->hidden / ((int64_t)G * (8 / BITS));
+  switch (units) {
+    case 4: return softmax_launch<BITS, G, R, 4, 1>(t, dp, lddp, ds, ldds, s);
+    case 8: return softmax_launch<BITS, G, R, 8, 1>(t, dp, lddp, ds, ldds, s);
+    case 16: return softmax_launch<BITS, G, R, 16, 1>(t, dp, lddp, ds, ldds, s);
+    default: return LRQ_ERR_UNSUPPORTED;
+  }
+}
+
+template <int BITS, int G, int R, int NOUT, bool F32>
+static int gemm_launch(const lrq_tensors* t, const void* a, void* out, int64_t ldo, hipStream_t s) {
+  constexpr int NW = 8, RBW = 4;
+  const int M = (int)t->rows, N = (int)t->hidden;
+  const int nrb = (M + 15) / 16;
+  hipLaunchKernelGGL((k_dequant_gemm<BITS, G, R, NOUT, NW, RBW, F32>), dim3((nrb + RBW - 1) / RBW), dim3(NW * 64), 0,
+                     s, (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
+                     (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)a, out, ldo);
+  return launch_status();
+}
+
+template <int BITS, int G, int R>
+static int gemm_nout(const lrq_tensors* t, const void* a, int n_out, void* out, int64_t ldo, bool f32, hipStream_t s) {
+  switch (n_out * 2 + (f32 ? 1 : 0)) {
+    case 16 * 2 + 1: return gemm_launch<BITS, G, R, 16, true>(t, a, out, ldo, s);
+    case 16 * 2: return gemm_launch<BITS, G, R, 16, false>(t, a, out, ldo, s);
+    case 32 * 2 + 1: return gemm_launch<BITS, G, R, 32, true>(t, a, out, ldo, s);
+    case 32 * 2: return gemm_launch<BITS, G, R, 32, false>(t, a, out, ldo, s);
+    default: return LRQ_ERR_UNSUPPORTED;
+  }
+}
+
+#define LRQ_FORMATS(F, ...)                                   \
+  switch (format_key(t->bits, t->group, t->rank)) {           \
+    case format_key(4, 64, 0): return F<4, 64, 0>(__VA_ARGS__);    \
+    case format_key(4, 64, 16): return F<4, 64, 16>(__VA_ARGS__);  \
+    case format_key(4, 64, 32): return F<4, 64, 32>(__VA_ARGS__);  \
+    case format_key(4, 128, 0): return F<4, 128, 0>(__VA_ARGS__);  \
+    case format_key(4, 128, 16): return F<4, 128, 16>(__VA_ARGS__); \
+    case format_key(8, 64, 0): return F<8, 64, 0>(__VA_ARGS__);    \
+    case format_key(8, 64, 16): return F<8, 64, 16>(__VA_ARGS__);  \
+    case format_key(8, 128, 0): return F<8, 128, 0>(__VA_ARGS__);  \
+    case format_key(8, 128, 16): return F<8, 128, 16>(__VA_ARGS__); \
+    default: return LRQ_ERR_UNSUPPORTED;                      \
+  }
+
+}  // namespace lrq
+
+using namespace lrq;
+
+extern "C" int lrq_softmax_bwd(const lrq_tensors* t, const void* dp, int64_t lddp, void* ds, int64_t ldds,
+                               void* stream) {
+  int st = validate_tensors(t);
+  if (st) return st;
+  st = validate_rows16(dp, lddp, t->hidden);
+  if (st) return st;
+  st = validate_rows16(ds, ldds, t->hidden);
+  if (st) return st;
+  if ((t->flags & LRQ_FLAG_HADAMARD) || t->n_outlier > 0) return LRQ_ERR_UNSUPPORTED;
+  if (t->rows == 0) return LRQ_OK;
+  hipStream_t s = (hipStream_t)stream;
+  LRQ_FORMATS(softmax_units, t, dp, lddp, ds, ldds, s)
+}
+
+extern "C" int lrq_dequant_gemm(const lrq_tensors* t, const void* a, int32_t n_out, void* out, int64_t ldo,
+                                int32_t out_fp32, void* stream) {
+  int st = validate_tensors(t);
+  if (st) return st;
+  if (a == nullptr || out == nullptr) return LRQ_ERR_NULL;
+  if (n_out != 16 && n_out != 32) return LRQ_ERR_UNSUPPORTED;
+  if (ldo < n_out) return LRQ_ERR_SHAPE;
+  if (!aligned(a, 8) || !aligned(out, out_fp32 ? 4 : 2)) return LRQ_ERR_ALIGN;
+  if ((t->flags & LRQ_FLAG_HADAMARD) || t->n_outlier > 0) return LRQ_ERR_UNSUPPORTED;
+  if (t->rows == 0) return LRQ_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const bool f32 = out_fp32 != 0;
+  LRQ_FORMATS(gemm_nout, t, a, n_out, out, ldo, f32, s)
+}
