@@ -51,7 +51,11 @@ extern "C" {
 #define LRQ_ERR_ALIGN (-4)       /* pointer or leading dimension misaligned             */
 #define LRQ_ERR_WORKSPACE (-5)   /* caller workspace too small                          */
 
-#define LRQ_FLAG_HADAMARD 1 /* rotate by the blockwise normalised WHT-128 before compression */
+/* The rotated format (config 4) is composed by the caller from lrq_wht128 and the plain
+ * entry points: encode(bf16(WHT(x))), then WHT(bf16(decode)).  The flag marks a descriptor
+ * as rotated; the fused entry points refuse it (LRQ_ERR_UNSUPPORTED) rather than return
+ * unrotated values. */
+#define LRQ_FLAG_HADAMARD 1
 
 /* Descriptor of one compressed activation.  Encode writes L/codes/scale/zero/side;
  * decode-side entry points read them.  Unused fields may be NULL / 0. */
@@ -129,6 +133,12 @@ int lrq_topk(const float* colmax, int64_t hidden, int32_t k, int32_t* idx, void*
 /* dst[cols, rows] = src[rows, cols]^T for bf16 (builds Vt from V, and V-layout from the
  * reference's r[K, N] factor). */
 int lrq_transpose_bf16(const void* src, int64_t rows, int64_t cols, void* dst, void* stream);
+
+/* y = bf16(WHT128(x)) per 128-column block of every row: the normalised Walsh-Hadamard
+ * rotation (its own inverse), sums accumulated on MFMA in four 32-column steps.  x, y:
+ * bf16 [rows, hidden] with 16-byte aligned rows, hidden % 128 == 0; y may equal x (in place).
+ * No reference function (north-star config 4). */
+int lrq_wht128(const void* x, int64_t ldx, int64_t rows, int64_t hidden, void* y, int64_t ldy, void* stream);
 
 /* ------------------------------------------------------------------ legacy mode
  * The reference's own formulation: caller-supplied factors l[M, K] (bf16) and r as

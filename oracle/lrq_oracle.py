@@ -40,7 +40,7 @@ __all__ = [
     # packing
     "pack_rowplanar", "unpack_rowplanar",
     # Walsh-Hadamard
-    "sylvester", "WHT_SCALE", "wht128_rows",
+    "sylvester", "WHT_SCALE", "wht128_chunks", "wht128_rows", "wht128_bf16",
     # group mode
     "projection", "lowrank_product", "fma32", "rcp32", "quant_groups", "dequant_groups",
     "encode", "decode", "reconstruct_f32",
@@ -151,14 +151,23 @@ def sylvester(n: int) -> np.ndarray:
 _H128 = None
 
 
-def wht128_rows(y: np.ndarray) -> np.ndarray:
-    """Blockwise normalised WHT along the last axis: per 128-column block b,
-    ``out[:, 128b + i] = fp32(sum_j H[i, j] * y[:, 128b + j]) * fp32(1/sqrt(128))``.
+def wht128_chunks():
+    """Column order of the rotation's accumulation: step c (0..3) adds the 32 columns
+    32g + 8c + e (g < 4, e < 8) of the block, one rounding to fp32 per step."""
+    return [np.array([32 * g + 8 * c + e for g in range(4) for e in range(8)]) for c in range(4)]
 
-    The sum is formed in float64 (exact for bf16-valued inputs of ordinary range) and
-    rounded once to fp32; the scale is one fp32 multiply.  The normalised H is
-    symmetric and its own inverse, so the same function undoes itself up to rounding.
-    Pinned by: H H = 128 I, WHT(e_k) = column k / sqrt(128), norm preservation.
+
+def wht128_rows(y: np.ndarray) -> np.ndarray:
+    """Blockwise normalised WHT along the last axis (config 4; no reference function).
+    Per 128-column block b and output column o:
+
+      acc = 0;  for c in 0..3:  acc = fp32(acc + sum_{k in chunk c} H[o, k] * y[128b + k])
+      out[128b + o] = fp32(acc * fp32(1/sqrt(128)))
+
+    (chunks from ``wht128_chunks``; each step's sum is exact, as one MFMA forms it).  The
+    normalised H is symmetric and its own inverse, so the function undoes itself up to
+    rounding.  Pinned by: H H = 128 I, WHT(e_k) = column k / sqrt(128), norm preservation,
+    agreement with the exact matrix product to fp32 rounding (tests/test_oracle.py).
     """
     global _H128
     if _H128 is None:
@@ -167,8 +176,16 @@ def wht128_rows(y: np.ndarray) -> np.ndarray:
     lead, n = y.shape[:-1], y.shape[-1]
     assert n % 128 == 0, "hidden size must be a multiple of 128 for the rotation"
     yb = y.astype(np.float64).reshape(-1, n // 128, 128)
-    s = (yb @ _H128).astype(np.float32)  # H symmetric: row-vector times H == H times column
-    return (s * WHT_SCALE).reshape(lead + (n,))
+    acc = np.zeros(yb.shape, dtype=np.float32)
+    for cols in wht128_chunks():
+        part = yb[..., cols] @ _H128[cols, :]  # H symmetric: row-vector times H == H times column
+        acc = (acc.astype(np.float64) + part).astype(np.float32)
+    return (acc * WHT_SCALE).astype(np.float32).reshape(lead + (n,))
+
+
+def wht128_bf16(x_bits: np.ndarray) -> np.ndarray:
+    """The rotation as the kernels apply it to a bf16 tensor: bf16(wht128_rows(x))."""
+    return bf16_round(wht128_rows(bf16_to_f32(x_bits)))
 
 
 # ---------------------------------------------------------------------------
@@ -283,7 +300,7 @@ def encode(x_bits: np.ndarray, v_bits, bits: int = 4, group: int = 64, hadamard:
     """Group-mode encode of a bf16 activation x [M, N] (no reference function; north-star format).
 
     Steps (all on the CPU, float32 unless stated):
-      Y  = wht128_rows(x) if hadamard else fp32(x)
+      Y  = bf16(wht128_rows(x)) if hadamard else fp32(x)   (the rotated activation is bf16)
       side[:, k] = fp16(x[:, idx[k]]); Y[:, idx] = 0            (outlier channels, if any)
       L  = bf16(fp32(exact(Y @ V)))                              (if rank > 0)
       R  = fp32(exact(Y - L @ V^T))   (one rounding: the kernels form it as an MFMA whose
@@ -300,7 +317,7 @@ def encode(x_bits: np.ndarray, v_bits, bits: int = 4, group: int = 64, hadamard:
     x_bits = np.asarray(x_bits, dtype=np.uint16)
     m, n = x_bits.shape
     x = bf16_to_f32(x_bits)
-    y = wht128_rows(x) if hadamard else x.copy()
+    y = bf16_to_f32(wht128_bf16(x_bits)) if hadamard else x.copy()
     idx = None
     side = None
     if outlier_idx is not None and len(outlier_idx) > 0:
@@ -339,7 +356,7 @@ def reconstruct_f32(l_bits, v_bits, packed, scale, zero, bits: int, group: int, 
     if idx is not None and len(idx) > 0:
         y[:, np.asarray(idx)] = np.asarray(side, dtype=np.float16).astype(np.float32)
     if hadamard:
-        y = wht128_rows(y)
+        y = wht128_rows(bf16_to_f32(bf16_round(y)))
     return y
 
 
@@ -350,7 +367,7 @@ def decode(l_bits, v_bits, packed, scale, zero, bits: int, group: int, hadamard=
       d  = fp32(code) * scale + zero
       Y' = fp32(exact(d + L @ V^T))   (one rounding; rank > 0)
       Y'[:, idx] = side     (outlier channels)
-      X' = wht128_rows(Y')  (rotation is its own inverse)
+      X' = wht128_rows(bf16(Y'))  (rotation is its own inverse; it takes bf16 input)
     Returns bf16 bits [M, N].
     """
     return bf16_round(reconstruct_f32(l_bits, v_bits, packed, scale, zero, bits, group, hadamard,

@@ -1,0 +1,70 @@
+"""GPU parity of the blockwise WHT-128 rotation (N4) and of the rotated compressed format
+(config 4 recipe at reduced rows).  The rotation sums in the order the oracle defines
+(wht128_rows), so its bf16 output must match bit for bit; the rotated encode is checked like
+the plain one (codes conditional on the device's L, then end to end), and decode against the
+oracle's decode of the device's codes.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from parity import TIE_BUDGET, assert_codes, assert_fp_close, bits16, f16, ulp_diff_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("rows,n", [(50, 1024), (16, 5120), (3, 128)])
+def test_wht128_bitexact(pkg, dev, rows, n):
+    g = torch.Generator().manual_seed(rows + n)
+    x = (torch.randn(rows, n, generator=g) * 3).to(torch.bfloat16)
+    xb = bits16(x)
+    y = pkg.wht128(x.to(dev))
+    torch.cuda.synchronize()
+    ref = O.wht128_bf16(xb)
+    assert np.array_equal(bits16(y), ref), int((bits16(y) != ref).sum())
+    # in place, and the rotation undoes itself to within bf16 rounding
+    xd = x.to(dev).clone()
+    pkg.wht128(xd, out=xd)
+    assert np.array_equal(bits16(xd), ref)
+    back = bits16(pkg.wht128(y))
+    assert np.array_equal(back, O.wht128_bf16(ref))
+    err = np.abs(O.bf16_to_f32(back) - O.bf16_to_f32(xb))
+    assert err.max() <= 0.05 * np.abs(O.bf16_to_f32(xb)).max()
+
+
+def test_rotated_format_c4_recipe(pkg, dev):
+    """Config 4: X [rows, 5120], 16 outlier channels x30, rotation, rank 16, int4/g64."""
+    rows, n, rank = 64, 5120, 16
+    print("[c4] inputs", flush=True)
+    x = pkg.inputs.activation(rows, n, 16, 30.0, seed=4)
+    V = pkg.inputs.basis(n, rank, seed=4)
+    xb, vb = bits16(x), bits16(V)
+    c = pkg.encode(x.to(dev), V.to(dev), bits=4, group_size=64, hadamard=True)
+    torch.cuda.synchronize()
+    lg = bits16(c.L)
+    ref_full = O.encode(xb, vb, 4, 64, hadamard=True)
+    d = ulp_diff_bf16(lg, ref_full["L"])
+    assert d.max() <= 1 and (d > 0).sum() <= max(2, 1e-3 * d.size)
+    ref = O.encode(xb, vb, 4, 64, hadamard=True, l_override=lg)
+    codes = c.codes.cpu().numpy()
+    rep = assert_codes(codes, ref, 4, what="rotated codes | device L")
+    assert_codes(codes, ref_full, 4, what="rotated codes end-to-end")
+    print(f"[c4] codes {rep}", flush=True)
+    xh = pkg.decode(c)
+    torch.cuda.synchronize()
+    ref_xh = O.decode(lg, vb, codes, f16(c.scale), f16(c.zero), 4, 64, hadamard=True)
+    flips = int((bits16(xh) != ref_xh).sum())
+    assert flips <= TIE_BUDGET * ref_xh.size + 1, flips
+    # round-trip error of the rotated format stays at the quantiser's scale
+    x32 = O.bf16_to_f32(xb).astype(np.float64)
+    e = O.bf16_to_f32(bits16(xh)).astype(np.float64) - x32
+    rel = np.linalg.norm(e) / np.linalg.norm(x32)
+    print(f"[c4] round-trip rel-L2 {rel:.4f}", flush=True)
+    assert rel < 0.1
+    # consumers on the rotated format compose decode + dense op
+    dy = pkg.inputs.gradient((rows, n), 0.02, seed=4)
+    out = pkg.silu_backward_compressed(c, dy.to(dev))
+    xhf = O.bf16_to_f32(ref_xh)
+    assert_fp_close(bits16(out), O.silu_bwd(xhf, O.bf16_to_f32(bits16(dy))), "rotated SiLU bwd")

@@ -53,6 +53,7 @@ SIGNATURES = {
     "lrq_colmax": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     "lrq_topk": (c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p]),
     "lrq_transpose_bf16": (c_int32, [c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+    "lrq_wht128": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p]),
     "lrq_legacy_encode": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_int64, c_int64,
                                     c_int64, c_int64, c_void_p, c_int64, c_int32, c_float, c_void_p,
                                     c_void_p, c_void_p]),

@@ -33,7 +33,7 @@ from ._lib import LrqTensors, call
 __all__ = [
     "LowRankBasis", "CompressedActivation", "encode", "decode", "silu_backward_compressed",
     "gelu_backward_compressed", "mul_compressed", "softmax_backward_compressed", "dequant_gemm",
-    "outlier_channels", "column_absmax", "topk_channels",
+    "outlier_channels", "column_absmax", "topk_channels", "wht128",
 ]
 
 
@@ -155,7 +155,9 @@ class CompressedActivation:
         t = LrqTensors()
         t.rows, t.hidden = self.rows, self.hidden
         t.rank, t.bits, t.group = self.rank, self.bits, self.group
-        t.flags = _lib.LRQ_FLAG_HADAMARD if self.hadamard else 0
+        # encode takes the already-rotated activation (see ``encode``); every other entry
+        # point sees the flag
+        t.flags = _lib.LRQ_FLAG_HADAMARD if (self.hadamard and not for_encode) else 0
         if self.rank:
             t.L, t.ld_L = self.L.data_ptr(), self.L.stride(0)
             t.V = self.basis.V.data_ptr()
@@ -209,9 +211,29 @@ def encode(x: torch.Tensor, basis: Optional[LowRankBasis | torch.Tensor] = None,
                              shape=tuple(x.shape), bits=bits, group=group_size, hadamard=hadamard)
     t = c.descriptor(for_encode=True)
     with torch.cuda.device(x.device):
+        if hadamard:
+            # rotated format: y = bf16(WHT128(x)) into a temporary, then the plain encode of y
+            y = torch.empty((rows, n), dtype=torch.bfloat16, device=x.device)
+            call("lrq_wht128", _p(x2), ldx, rows, n, _p(y), n, _stream(x.device))
+            x2, ldx = y, n
         call("lrq_encode_twopass" if _twopass else "lrq_encode", ctypes.byref(t), _p(x2), ldx,
              _stream(x.device))
     return c
+
+
+def wht128(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """bf16(normalised blockwise WHT-128(x)) along the last axis (its own inverse up to
+    rounding).  ``out`` may be ``x`` (in place)."""
+    _require_device(x)
+    if x.dtype != torch.bfloat16:
+        raise ValueError("wht128 takes bf16")
+    x2, rows, n, ldx = _rows_view(x)
+    o = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device) if out is None else out
+    if o.shape != x.shape or o.dtype != torch.bfloat16 or not o.is_contiguous():
+        raise ValueError("out must be a contiguous bf16 tensor of x's shape")
+    with torch.cuda.device(x.device):
+        call("lrq_wht128", _p(x2), ldx, rows, n, _p(o), n, _stream(x.device))
+    return o
 
 
 def _out_like(c: CompressedActivation, out: Optional[torch.Tensor]) -> torch.Tensor:
@@ -239,8 +261,24 @@ def decode(c: CompressedActivation, out: Optional[torch.Tensor] = None) -> torch
     return o
 
 
+_DENSE_OP = {"lrq_silu_bwd": 0, "lrq_gelu_bwd": 1, "lrq_mul": 2}
+
+
 def _fused(name: str, c: CompressedActivation, y: torch.Tensor, argname: str) -> torch.Tensor:
     y2, ldy = _operand(c, y, argname)
+    if c.hadamard:
+        # rotated format: the inverse rotation needs whole 128-column blocks, so decode (which
+        # rotates back) and apply the consumer on the result
+        xh = decode(c)
+        o = torch.empty_like(xh)
+        y3 = y.contiguous()
+        with torch.cuda.device(c.device):
+            if name == "lrq_softmax_bwd":
+                call("lrq_dense_softmax_bwd", _p(xh), _p(y3), _p(o), c.rows, c.hidden, _stream(c.device))
+            else:
+                call("lrq_dense_elementwise", _DENSE_OP[name], _p(xh), _p(y3), _p(o), xh.numel(),
+                     _stream(c.device))
+        return o
     o = _out_like(c, None)
     t = c.descriptor()
     with torch.cuda.device(c.device):
@@ -277,6 +315,9 @@ def dequant_gemm(c: CompressedActivation, a: torch.Tensor, out_dtype=torch.float
     n_out = a.shape[1]
     if out_dtype not in (torch.float32, torch.bfloat16):
         raise ValueError("out_dtype must be float32 or bfloat16")
+    if c.hadamard:
+        xh = decode(c).reshape(c.rows, c.hidden)
+        return torch.matmul(xh.float(), a.float()).to(out_dtype).reshape(tuple(c.shape[:-1]) + (n_out,))
     o = torch.empty((c.rows, n_out), dtype=out_dtype, device=c.device)
     t = c.descriptor()
     with torch.cuda.device(c.device):

@@ -277,6 +277,14 @@ extern "C" int lrq_decode(const lrq_tensors* t, void* out, int64_t ldo, void* st
   int st = check_io(t, nullptr, 0, out, ldo, false);
   if (st) return st;
   if (t->rows == 0) return LRQ_OK;
+  if (t->flags & LRQ_FLAG_HADAMARD) {
+    // rotated format: decode, then undo the rotation in place (the rotation is its own inverse)
+    lrq_tensors plain = *t;
+    plain.flags &= ~LRQ_FLAG_HADAMARD;
+    st = decode_dispatch(&plain, (hipStream_t)stream, EpiStore{(uint16_t*)out, ldo});
+    if (st) return st;
+    return lrq_wht128(out, ldo, t->rows, t->hidden, out, ldo, stream);
+  }
   return decode_dispatch(t, (hipStream_t)stream, EpiStore{(uint16_t*)out, ldo});
 }
 

@@ -403,6 +403,9 @@ static int encode_impl(const lrq_tensors* t, const void* x, int64_t ldx, hipStre
 static int encode_entry(const lrq_tensors* t, const void* x, int64_t ldx, void* stream, int force_twopass) {
   int st = validate_tensors(t);
   if (st) return st;
+  // the rotated format needs a rotated copy of x (lrq_wht128 into a caller buffer, then
+  // encode that without the flag); refusing beats silently encoding unrotated data
+  if (t->flags & LRQ_FLAG_HADAMARD) return LRQ_ERR_UNSUPPORTED;
   if (x == nullptr) return LRQ_ERR_NULL;
   if (ldx < t->hidden) return LRQ_ERR_SHAPE;
   if ((ldx % 8) != 0 || !aligned(x, 16)) return LRQ_ERR_ALIGN;

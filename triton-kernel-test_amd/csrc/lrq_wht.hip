@@ -1,0 +1,113 @@
+// Blockwise normalised Walsh-Hadamard rotation, 128 points (config 4's rotation, its own
+// inverse): for every 128-column block b of a row,
+//
+//   y[128b + o] = bf16( fp32(S_o) * fp32(1/sqrt(128)) ),   S_o = sum_k H128[o, k] x[128b + k],
+//
+// with S_o accumulated on MFMA in four chained 32-term steps (each step adds 32 exact
+// products to the running fp32 sum and rounds once).  Step c covers the columns
+// 32g + 8c + e (g < 4, e < 8); the CPU oracle (wht128_rows) sums in the same order.
+//
+// Layout: a wave owns one 128-column block of 16 rows; lane (j, g) holds columns
+// 32g .. 32g+31 of row j, which are both its B operands (step c = columns 32g + 8c ..) and,
+// with output column o = 32g' + 4q + v assigned to MFMA tile q, lane (j, g') and element v,
+// exactly where its outputs land, so no data moves between lanes.
+//
+// H128[o, k] = (-1)^popcount(o & k).  With o = (v, q, g') and k = (e, c, kg) in bit fields
+// (2, 3, 2) and (3, 2, 2), the sign splits into a factor that depends on (v, g', e, kg, q0)
+// (the lane's A operand for tile parity q0) and a wave-uniform factor (-1)^((q1&c0)^(q2&c1)):
+// two register operands and their negations serve all 32 MFMAs of a block.
+#include "lrq_common.h"
+#include "lrq_host.h"
+
+namespace lrq {
+
+// A operand of tile parity q0 for lane (i, kg): 8 bf16 signs for e = 0..7.
+__device__ __forceinline__ u32x4 wht_base_operand(int i, int kg, int q0, bool neg) {
+  const int v = i & 3, gp = i >> 2;
+  uint32_t w[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    uint32_t pair = 0;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int e = 2 * h + s;
+      const int par = (__builtin_popcount(v & e & 3) + (q0 & (e >> 2)) + __builtin_popcount(gp & kg) + (neg ? 1 : 0)) & 1;
+      pair |= (par ? 0xbf80u : 0x3f80u) << (16 * s);
+    }
+    w[h] = pair;
+  }
+  return u32x4{w[0], w[1], w[2], w[3]};
+}
+
+// Grid: (ceil(row blocks / RBW), ceil(blocks per row / 4)); 4 waves, wave w on 128-column block
+// blockIdx.y * 4 + w (idle past the end; no barrier follows).  In-place (x == y) is safe: a
+// wave reads all of its rows' block before writing it.
+template <int RBW>
+__global__ __launch_bounds__(256) void k_wht128(const uint16_t* x, int64_t ldx, int M, int N, uint16_t* y,
+                                                int64_t ldy) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int blk = blockIdx.y * 4 + w;
+  if (blk >= N / 128) return;
+  const int nrb = (M + 15) / 16;
+  u32x4 op[2][2];  // [q0][negated]
+#pragma unroll
+  for (int q0 = 0; q0 < 2; ++q0)
+#pragma unroll
+    for (int n = 0; n < 2; ++n) op[q0][n] = wht_base_operand(j, g, q0, n != 0);
+  const float kScale = 0.08838834764831845f;  // fp32(1/sqrt(128))
+
+#pragma unroll 1
+  for (int b = 0; b < RBW; ++b) {
+    const int rb = blockIdx.x * RBW + b;
+    if (rb >= nrb) break;  // uniform
+    const int64_t row = min(rb * 16 + j, M - 1);
+    const uint16_t* xr = x + row * ldx + 128 * blk + 32 * g;
+    u32x4 xv[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) xv[c] = ld16(xr + 8 * c);
+    float out[32];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int flip = (((q >> 1) & c & 1) ^ ((q >> 2) & (c >> 1) & 1));
+        acc = mfma_16x16x32(op[q & 1][flip], xv[c], acc);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) out[4 * q + v] = acc[v] * kScale;
+    }
+    uint16_t* yr = y + row * ldy + 128 * blk + 32 * g;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) st16(yr + 8 * k, pack8(out + 8 * k));
+  }
+}
+
+}  // namespace lrq
+
+using namespace lrq;
+
+extern "C" int lrq_wht128(const void* x, int64_t ldx, int64_t rows, int64_t hidden, void* y, int64_t ldy,
+                          void* stream) {
+  if (x == nullptr || y == nullptr) return LRQ_ERR_NULL;
+  if (rows < 0 || hidden <= 0 || rows > INT32_MAX || hidden > INT32_MAX) return LRQ_ERR_SHAPE;
+  if (hidden % 128 != 0 || ldx < hidden || ldy < hidden) return LRQ_ERR_SHAPE;
+  if ((ldx % 8) != 0 || (ldy % 8) != 0 || !aligned(x, 16) || !aligned(y, 16)) return LRQ_ERR_ALIGN;
+  if (x != y) {  // partial overlap would race
+    const uintptr_t xa = (uintptr_t)x, ya = (uintptr_t)y;
+    const uintptr_t xe = xa + (uintptr_t)((rows > 0 ? rows - 1 : 0) * ldx + hidden) * 2;
+    const uintptr_t ye = ya + (uintptr_t)((rows > 0 ? rows - 1 : 0) * ldy + hidden) * 2;
+    if (rows > 0 && xa < ye && ya < xe) return LRQ_ERR_SHAPE;
+  } else if (ldx != ldy) {
+    return LRQ_ERR_SHAPE;
+  }
+  if (rows == 0) return LRQ_OK;
+  constexpr int RBW = 4;
+  const int nrb = (int)((rows + 15) / 16);
+  const int nblk = (int)(hidden / 128);
+  dim3 grid((nrb + RBW - 1) / RBW, (nblk + 3) / 4);
+  hipLaunchKernelGGL((k_wht128<RBW>), grid, dim3(256), 0, (hipStream_t)stream, (const uint16_t*)x, ldx, (int)rows,
+                     (int)hidden, (uint16_t*)y, ldy);
+  return launch_status();
+}
