@@ -1,0 +1,141 @@
+"""The C ABI boundary without a GPU: the library loads, exports every function that
+include/lrq.h declares (and the ctypes table binds exactly those), and argument errors are
+reported as negative status codes before any HIP call, so no compute runs here.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "lrq.h"
+
+
+@pytest.fixture(scope="module")
+def L(pkg):
+    return pkg._lib
+
+
+@pytest.fixture(scope="module")
+def lib(L):
+    return L.load()
+
+
+def header_functions() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"^\s*(?:const\s+)?(?:int|int32_t|char\s*\*|const\s+char\s*\*)\s*\**\s*(lrq_\w+)\s*\(",
+                          text, flags=re.M)) | set(re.findall(r"\b(lrq_\w+)\s*\(", text))
+
+
+def test_header_parses():
+    names = header_functions()
+    assert {"lrq_encode", "lrq_decode", "lrq_legacy_encode", "lrq_wht128", "lrq_abi_version"} <= names
+
+
+def test_every_declared_function_is_exported(L, lib):
+    names = header_functions()
+    missing = sorted(n for n in names if not hasattr(lib, n))
+    assert not missing, missing
+    assert not L.missing_symbols()
+
+
+def test_ctypes_table_matches_header(L):
+    assert set(L.SIGNATURES) == header_functions()
+
+
+def test_abi_version_and_status_strings(lib, L):
+    assert lib.lrq_abi_version() == 1
+    for code in (L.LRQ_OK, L.LRQ_ERR_NULL, L.LRQ_ERR_SHAPE, L.LRQ_ERR_UNSUPPORTED, L.LRQ_ERR_ALIGN,
+                 L.LRQ_ERR_WORKSPACE):
+        s = L.status_string(code)
+        assert s and s != "unknown status"
+
+
+def _desc(L, **kw):
+    t = L.LrqTensors()
+    t.rows, t.hidden, t.rank, t.bits, t.group, t.flags = 32, 4096, 0, 4, 64, 0
+    t.codes, t.ld_codes = 4096, 2048
+    t.qparams, t.ld_qp = 8192, 128
+    for k, v in kw.items():
+        setattr(t, k, v)
+    return t
+
+
+def _encode(L, t, x=0x10000, ldx=4096):
+    return L.call_raw("lrq_encode", ctypes.byref(t), ctypes.c_void_p(x), ldx, None)
+
+
+@pytest.mark.parametrize("change,code", [
+    (dict(codes=0), "NULL"),
+    (dict(bits=3), "UNSUPPORTED"),
+    (dict(group=32), "UNSUPPORTED"),
+    (dict(rank=8), "UNSUPPORTED"),
+    (dict(hidden=4000), "SHAPE"),
+    (dict(rows=-1), "SHAPE"),
+    (dict(ld_codes=1000), "SHAPE"),
+    (dict(ld_codes=2056), "ALIGN"),
+    (dict(codes=4097), "ALIGN"),
+    (dict(rank=16), "NULL"),                   # rank 16 needs L and V
+    (dict(flags=1), "UNSUPPORTED"),            # encode takes the rotated copy, never the flag
+    (dict(flags=4), "UNSUPPORTED"),
+    (dict(n_outlier=3), "NULL"),               # outliers need idx and side
+])
+def test_encode_argument_errors(L, change, code):
+    t = _desc(L, **change)
+    assert _encode(L, t) == getattr(L, "LRQ_ERR_" + code)
+
+
+def test_encode_input_errors(L):
+    t = _desc(L)
+    assert _encode(L, t, x=0) == L.LRQ_ERR_NULL
+    assert _encode(L, t, ldx=100) == L.LRQ_ERR_SHAPE
+    assert _encode(L, t, x=0x10002) == L.LRQ_ERR_ALIGN
+
+
+def test_decode_and_consumer_argument_errors(L):
+    t = _desc(L)
+    assert L.call_raw("lrq_decode", ctypes.byref(t), None, 4096, None) == L.LRQ_ERR_NULL
+    assert L.call_raw("lrq_decode", ctypes.byref(t), ctypes.c_void_p(0x10000), 100, None) == L.LRQ_ERR_SHAPE
+    for fn in ("lrq_silu_bwd", "lrq_gelu_bwd", "lrq_mul", "lrq_softmax_bwd"):
+        assert L.call_raw(fn, ctypes.byref(t), None, 4096, ctypes.c_void_p(0x10000), 4096, None) == L.LRQ_ERR_NULL
+    assert L.call_raw("lrq_dequant_gemm", ctypes.byref(t), ctypes.c_void_p(0x10000), 24,
+                      ctypes.c_void_p(0x20000), 24, 1, None) == L.LRQ_ERR_UNSUPPORTED
+
+
+def test_legacy_argument_errors(L):
+    p = ctypes.c_void_p(0x10000)
+    enc = lambda K, bits, N=1024, s_rows=1: L.call_raw(  # noqa: E731
+        "lrq_legacy_encode", p, p, K, p, 1, 64, N, 64 * N, N, p, s_rows, bits, 5.0, p, p, None)
+    assert enc(8, 4) == L.LRQ_ERR_UNSUPPORTED         # K is padded to 16 / 32 by the caller
+    assert enc(16, 3) == L.LRQ_ERR_UNSUPPORTED
+    assert enc(16, 4, N=1023) == L.LRQ_ERR_SHAPE      # N % (8 / bits)
+    assert enc(16, 4, s_rows=2) == L.LRQ_ERR_SHAPE    # s rows must be 1 or B
+    assert L.call_raw("lrq_legacy_decode", None, p, 16, p, None, p, 1, 1, 64, 1024, 4, p, None) == L.LRQ_ERR_NULL
+    assert L.call_raw("lrq_legacy_fused", p, p, 16, p, p, 1, 1, 64, 1024, 4, 3, p, p, None) == L.LRQ_ERR_UNSUPPORTED
+    assert L.call_raw("lrq_legacy_fused", p, p, 16, p, p, 1, 1, 64, 1024, 4, 1, None, p, None) == L.LRQ_ERR_NULL
+    assert L.call_raw("lrq_lowrank_add", p, p, 20, p, 1, 64, 1024, p, None) == L.LRQ_ERR_UNSUPPORTED
+
+
+def test_misc_argument_errors(L):
+    p = ctypes.c_void_p(0x10000)
+    assert L.call_raw("lrq_wht128", p, 1000, 4, 1000, p, 1000, None) == L.LRQ_ERR_SHAPE      # hidden % 128
+    assert L.call_raw("lrq_wht128", ctypes.c_void_p(0x10002), 1024, 4, 1024, p, 1024, None) == L.LRQ_ERR_ALIGN
+    assert L.call_raw("lrq_wht128", p, 1024, 4, 1024, ctypes.c_void_p(0x10000 + 64), 1024, None) == L.LRQ_ERR_SHAPE
+    assert L.call_raw("lrq_dense_elementwise", 7, p, p, p, 100, None) == L.LRQ_ERR_UNSUPPORTED
+    assert L.call_raw("lrq_dense_elementwise", 0, None, p, p, 100, None) == L.LRQ_ERR_NULL
+    assert L.call_raw("lrq_dense_softmax_bwd", p, p, p, 4, 0, None) == L.LRQ_ERR_SHAPE
+    assert L.call_raw("lrq_topk", None, 10, 3, p, None) == L.LRQ_ERR_NULL
+    assert L.call_raw("lrq_colmax", p, 10, 4, 100, None, None) == L.LRQ_ERR_NULL
+
+
+def test_empty_inputs_are_no_ops(L):
+    """Zero rows succeed without launching anything (no GPU needed)."""
+    t = _desc(L, rows=0)
+    assert _encode(L, t) == L.LRQ_OK
+    assert L.call_raw("lrq_decode", ctypes.byref(t), ctypes.c_void_p(0x10000), 4096, None) == L.LRQ_OK
+    p = ctypes.c_void_p(0x10000)
+    assert L.call_raw("lrq_dense_elementwise", 0, p, p, p, 0, None) == L.LRQ_OK
+    assert L.call_raw("lrq_wht128", p, 1024, 0, 1024, p, 1024, None) == L.LRQ_OK

@@ -114,12 +114,17 @@ def check(code: int, what: str) -> None:
     raise RuntimeError(msg)
 
 
-def call(name: str, *args) -> None:
+def call_raw(name: str, *args) -> int:
+    """Call an entry point and return its status without raising."""
     lib = load()
     if name in _missing:
         raise RuntimeError(f"{name} is not exported by {LIB_PATH}")
-    check(getattr(lib, name)(*args), name)
+    return int(getattr(lib, name)(*args))
 
 
-__all__ = ["LrqTensors", "load", "call", "check", "status_string", "missing_symbols", "SIGNATURES",
+def call(name: str, *args) -> None:
+    check(call_raw(name, *args), name)
+
+
+__all__ = ["LrqTensors", "load", "call", "call_raw", "check", "status_string", "missing_symbols", "SIGNATURES",
            "LIB_PATH", "LRQ_FLAG_HADAMARD", "c_size_t"]
