@@ -9,9 +9,11 @@ serve them.  Prints ONE JSON line (driver contract).
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config north_star|c1|c2|c3|c4|c5]
                   [--no-cpu-baseline]
 
-value       = activation GB/s = 2*rows*hidden bytes / (encode + decode time per step)
+value       = activation GB/s = 2*rows*hidden bytes / (encode + decode time per step);
+              fused-consumer configs: / (consumer time)
 roofline    = dominant kernel's algorithmic HBM bytes per launch / its mean duration
-              (HIP events on the launch stream), against 8 TB/s
+              (K back-to-back launches between HIP events on the launch stream), against
+              8 TB/s; traffic = rocprofv3 FETCH_SIZE/WRITE_SIZE bytes per launch from profiles/
 cpu_baseline= the CPU oracle (numpy, 1 thread) on a bounded row sample of the same workload
 """
 
@@ -66,8 +68,11 @@ def traffic_from_profiles(name: str):
 
 
 def cpu_baseline(cfg, seconds: float):
-    """Time the numpy oracle's encode+decode on a row sample sized to ~`seconds` of work."""
+    """Time the numpy CPU oracle on a row sample of the same workload, sized to ~`seconds`:
+    encode + decode for the round-trip configs, decode + consumer for the fused ones (the
+    encode is the producer there and is not timed).  One thread."""
     import numpy as np
+    import torch
     try:
         from threadpoolctl import threadpool_limits
     except Exception:  # pragma: no cover
@@ -75,33 +80,114 @@ def cpu_baseline(cfg, seconds: float):
     import oracle as O
     pkg = importlib.import_module("triton-kernel-test_amd")
     ctx = threadpool_limits(1) if threadpool_limits else None
+    as_bits = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
     try:
-        rows = 64
         V = pkg.inputs.basis(cfg.hidden, cfg.rank, cfg.seed) if cfg.rank else None
-        vb = V.view(__import__("torch").int16).numpy().view(np.uint16) if V is not None else None
+        vb = as_bits(V) if V is not None else None
 
         def run(r):
-            x = pkg.inputs.activation(r, cfg.hidden, cfg.n_outlier, cfg.outlier_scale, cfg.seed)
-            xb = x.view(__import__("torch").int16).numpy().view(np.uint16)
+            inp = pkg.inputs.make(cfg, rows=r)
+            xb = as_bits(inp["x"])
+            idx = None
+            if cfg.keep_channels:
+                idx = O.topk_channels(O.colmax_abs(xb), cfg.keep_channels)
             t0 = time.perf_counter()
-            e = O.encode(xb, vb, cfg.bits, cfg.group)
-            O.decode(e["L"], vb, e["codes"], e["scale"], e["zero"], cfg.bits, cfg.group)
+            e = O.encode(xb, vb, cfg.bits, cfg.group, hadamard=cfg.hadamard, outlier_idx=idx)
+            if cfg.consumer != "decode":
+                t0 = time.perf_counter()
+            xh = O.decode(e["L"], vb, e["codes"], e["scale"], e["zero"], cfg.bits, cfg.group,
+                          hadamard=cfg.hadamard, side=e["side"], idx=e["idx"])
+            if cfg.consumer != "decode":
+                f = {"silu": O.silu_bwd, "gelu": O.gelu_bwd, "softmax": O.softmax_bwd}[cfg.consumer]
+                O.round_out(f(O.bf16_to_f32(xh), O.bf16_to_f32(as_bits(inp["dy"]))))
             return time.perf_counter() - t0
 
+        rows = 32
         t = run(rows)
         while t < seconds / 8 and rows < cfg.rows:
             rows = min(cfg.rows, rows * 2)
             t = run(rows)
-        if t < seconds and rows < cfg.rows:
-            rows = min(cfg.rows, max(rows, int(rows * seconds / max(t, 1e-3))))
-            t = run(rows)
+        for _ in range(2):  # two refinements: the first runs carry one-time setup costs
+            if t < 0.8 * seconds and rows < cfg.rows:
+                rows = min(cfg.rows, max(rows, int(rows * seconds / max(t, 1e-3))))
+                t = run(rows)
         gbs = 2 * rows * cfg.hidden / t / 1e9
+        what = "encode+decode" if cfg.consumer == "decode" else f"decode+{cfg.consumer} backward"
         return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-                "sample": f"numpy oracle encode+decode of {rows} of {cfg.rows} rows x {cfg.hidden} "
+                "sample": f"numpy CPU oracle {what} of {rows} of {cfg.rows} rows x {cfg.hidden} "
                           f"(same recipe), {t:.1f} s, 1 thread"}
     finally:
         if ctx is not None:
             ctx.__exit__(None, None, None)
+
+
+def consumer_bytes(rows, hidden, rank, bits, group, n_side=0):
+    """Fused consumer bytes = M N (b/8 + 4/G + 2 + 2) + 2 M r + 2 N r (+ 2 M k side columns)."""
+    b = rows * hidden * (bits / 8 + 4 / group + 4) + 2 * rows * rank + 2 * hidden * rank
+    return b + 2 * rows * n_side
+
+
+def build_plan(cfg, pkg, lib, dev, nbuf):
+    """Per-config step: a list of (name, launch(k) -> status, algorithmic bytes, mfma flops) run
+    in order on buffer set k, plus the step's activation bytes and how `value` is formed."""
+    import torch
+    c_void_p = ctypes.c_void_p
+    sp = c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    M, N, r = cfg.rows, cfg.hidden, cfg.rank
+    V = pkg.inputs.basis(N, r, cfg.seed).to(dev) if r else None
+    basis = pkg.LowRankBasis(V) if r else None
+    if basis is not None:
+        _ = basis.Vt
+    sets = []
+    for i in range(nbuf):
+        if cfg.consumer == "softmax":
+            x = pkg.inputs.softmax_probs((M, N), seed=cfg.seed + i, device=dev)
+        else:
+            x = pkg.inputs.activation(M, N, cfg.n_outlier, cfg.outlier_scale, cfg.seed + i, dev)
+        idx = None
+        if cfg.keep_channels:
+            idx = pkg.topk_channels(pkg.column_absmax(x), cfg.keep_channels)
+        c = pkg.encode(x, basis, bits=cfg.bits, group_size=cfg.group, hadamard=cfg.hadamard, outlier_idx=idx)
+        st = dict(x=x, c=c, out=torch.empty_like(x), enc=c.descriptor(for_encode=True), dec=c.descriptor())
+        if cfg.hadamard:
+            st["y"] = torch.empty_like(x)
+        if cfg.keep_channels:
+            st["cm"] = torch.empty((N,), dtype=torch.float32, device=dev)
+        if cfg.consumer != "decode":
+            st["dy"] = pkg.inputs.gradient((M, N), cfg.grad_std, cfg.seed + i, dev)
+        sets.append(st)
+    torch.cuda.synchronize()
+    P = lambda t: c_void_p(t.data_ptr())  # noqa: E731
+    B = lambda d: ctypes.byref(d)  # noqa: E731
+    side = cfg.keep_channels
+    enc_b = algorithmic_bytes(M, N, r, cfg.bits, cfg.group, side)
+    entries = []
+    if cfg.keep_channels:
+        entries.append(("colmax", lambda k: lib.lrq_colmax(P(sets[k]["x"]), N, M, N, P(sets[k]["cm"]), sp),
+                        2 * M * N, 0))
+        entries.append(("topk", lambda k: lib.lrq_topk(P(sets[k]["cm"]), N, side, c_void_p(sets[k]["c"].idx.data_ptr()),
+                                                       sp), 4 * N, 0))
+    if cfg.hadamard:
+        entries.append(("wht128", lambda k: lib.lrq_wht128(P(sets[k]["x"]), N, M, N, P(sets[k]["y"]), N, sp),
+                        4 * M * N, 2 * M * N * 128))
+        src = "y"
+    else:
+        src = "x"
+    entries.append(("encode", lambda k: lib.lrq_encode(B(sets[k]["enc"]), P(sets[k][src]), N, sp), enc_b,
+                    4 * M * N * r))
+    if cfg.consumer == "decode":
+        dec_flops = 2 * M * N * r + (2 * M * N * 128 if cfg.hadamard else 0)
+        dec_bytes = enc_b + (4 * M * N if cfg.hadamard else 0)
+        entries.append(("decode", lambda k: lib.lrq_decode(B(sets[k]["dec"]), P(sets[k]["out"]), N, sp),
+                        dec_bytes, dec_flops))
+        timed = None  # value over the whole step (round trip)
+    else:
+        fn = {"silu": lib.lrq_silu_bwd, "gelu": lib.lrq_gelu_bwd, "softmax": lib.lrq_softmax_bwd}[cfg.consumer]
+        name = f"{cfg.consumer}_bwd"
+        entries.append((name, lambda k: fn(B(sets[k]["dec"]), P(sets[k]["dy"]), N, P(sets[k]["out"]), N, sp),
+                        consumer_bytes(M, N, r, cfg.bits, cfg.group, side), 2 * M * N * r))
+        timed = name  # value over the fused consumer (the encode is the producer)
+    return entries, 2 * M * N, timed, sets
 
 
 def main():
@@ -117,38 +203,21 @@ def main():
     lib_mod = import_module("triton-kernel-test_amd._lib")
     lib = lib_mod.load()
     cfg = pkg.inputs.CONFIGS[args.config]
-    if cfg.consumer != "decode" or cfg.hadamard or cfg.keep_channels:
-        raise SystemExit(f"config {args.config} is not benchmarked by this script yet")
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-
-    # ---- inputs: nbuf HBM-resident sets (device RNG: same recipe, fast)
-    V = pkg.inputs.basis(cfg.hidden, cfg.rank, cfg.seed).to(dev)
-    basis = pkg.LowRankBasis(V)
-    _ = basis.Vt
-    xs, comps, outs = [], [], []
-    for i in range(args.nbuf):
-        x = pkg.inputs.activation(cfg.rows, cfg.hidden, cfg.n_outlier, cfg.outlier_scale, cfg.seed + i, dev)
-        xs.append(x)
-        comps.append(pkg.encode(x, basis, bits=cfg.bits, group_size=cfg.group))
-        outs.append(torch.empty_like(x))
-    torch.cuda.synchronize()
-    descs = [c.descriptor(for_encode=True) for c in comps]
     stream = torch.cuda.current_stream(dev)
-    sp = ctypes.c_void_p(stream.cuda_stream)
-    enc, dec = lib.lrq_encode, lib.lrq_decode
+
+    entries, act_bytes, timed, _sets = build_plan(cfg, pkg, lib, dev, args.nbuf)
 
     def step(i, ev=None):
         k = i % args.nbuf
-        d = ctypes.byref(descs[k])
+        st = 0
+        for e, (name, fn, _, _) in enumerate(entries):
+            if ev is not None:
+                ev[e].record(stream)
+            st |= fn(k)
         if ev is not None:
-            ev[0].record(stream)
-        st = enc(d, ctypes.c_void_p(xs[k].data_ptr()), cfg.hidden, sp)
-        if ev is not None:
-            ev[1].record(stream)
-        st |= dec(d, ctypes.c_void_p(outs[k].data_ptr()), cfg.hidden, sp)
-        if ev is not None:
-            ev[2].record(stream)
+            ev[len(entries)].record(stream)
         if st:
             raise RuntimeError(f"launch failed: {lib_mod.status_string(st)}")
 
@@ -157,7 +226,8 @@ def main():
     torch.cuda.synchronize()
 
     # ---- timed region: K steps, per-kernel HIP events on the launch stream
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    ne = len(entries)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(ne + 1)] for _ in range(args.steps)]
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -168,24 +238,48 @@ def main():
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
     ms_step = total_ms / args.steps
-    enc_ms = [e[0].elapsed_time(e[1]) for e in evs]
-    dec_ms = [e[1].elapsed_time(e[2]) for e in evs]
-    enc_mean, dec_mean = statistics.mean(enc_ms), statistics.mean(dec_ms)
-    enc_med, dec_med = statistics.median(enc_ms), statistics.median(dec_ms)
 
-    act_bytes = 2 * cfg.rows * cfg.hidden
-    alg = algorithmic_bytes(cfg.rows, cfg.hidden, cfg.rank, cfg.bits, cfg.group)
-    value = act_bytes / (ms_step * 1e-3) / 1e9
-    dominant = "encode" if enc_mean >= dec_mean else "decode"
-    dom_ms = max(enc_mean, dec_mean)
-    achieved = alg / (dom_ms * 1e-3) / 1e9
-    traffic = traffic_from_profiles(f"{dominant}_{args.config}")
-    # MFMA work: encode = projection (2 M N r) + residual (2 M N r); decode = 2 M N r
-    enc_tf = 4 * cfg.rows * cfg.hidden * cfg.rank / (enc_mean * 1e-3) / 1e12
-    dec_tf = 2 * cfg.rows * cfg.hidden * cfg.rank / (dec_mean * 1e-3) / 1e12
+    # ---- per-kernel duration: K back-to-back launches of that kernel alone between two
+    # events on its stream (dispatch latency overlaps, as in a rocprofv3 kernel trace)
+    solo = []
+    for e, (name, fn, _, _) in enumerate(entries):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for i in range(args.steps):
+            fn(i % args.nbuf)
+        b.record(stream)
+        torch.cuda.synchronize()
+        solo.append(a.elapsed_time(b) / args.steps)
+
+    kernels = {}
+    for e, (name, _, alg, flops) in enumerate(entries):
+        ms = [ev[e].elapsed_time(ev[e + 1]) for ev in evs]
+        in_step, med = statistics.mean(ms), statistics.median(ms)
+        mean = solo[e]
+        kernels[name] = {"mean_us": round(mean * 1e3, 2), "in_step_mean_us": round(in_step * 1e3, 2),
+                         "in_step_median_us": round(med * 1e3, 2),
+                         "alg_GBs": round(alg / (mean * 1e-3) / 1e9, 1),
+                         "hbm_frac": round(alg / (mean * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        if flops:
+            tf = flops / (mean * 1e-3) / 1e12
+            kernels[name].update(mfma_tflops=round(tf, 2), mfma_util=round(tf / BF16_DENSE_TFLOPS, 5))
+    if timed is None:
+        value = act_bytes / (ms_step * 1e-3) / 1e9  # whole step, kernels interleaved as in use
+        workload = "encode+decode" + (" with WHT-128 rotation" if cfg.hadamard else "")
+    else:
+        value = act_bytes / (kernels[timed]["mean_us"] * 1e-6) / 1e9
+        workload = f"fused {timed} on the compressed activation (encode timed alongside)"
+    dom_name, dom_alg, dom_us = None, 0, -1.0
+    for name, _, alg, _ in entries:
+        if kernels[name]["mean_us"] > dom_us:
+            dom_name, dom_alg, dom_us = name, alg, kernels[name]["mean_us"]
+    achieved = dom_alg / (dom_us * 1e-6) / 1e9
+    traffic = traffic_from_profiles(f"{dom_name}_{args.config}")
+    step_alg = sum(e[2] for e in entries)
 
     line = {
-        "metric": METRIC,
+        "metric": METRIC if args.config == "north_star" else f"{args.config}: activation GB/s and % of HBM peak",
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -197,18 +291,11 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) with scaled outlier channels; orthonormal QR basis)",
-        "config": {"workload": f"{args.config}: encode+decode", "rows": cfg.rows, "hidden": cfg.hidden,
+        "config": {"workload": f"{args.config}: {workload}", "rows": cfg.rows, "hidden": cfg.hidden,
                    "rank": cfg.rank, "bits": cfg.bits, "group": cfg.group, "buffers": args.nbuf},
-        "hbm_frac_step": round(2 * alg / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "kernels": {
-            "encode": {"mean_us": round(enc_mean * 1e3, 2), "median_us": round(enc_med * 1e3, 2),
-                       "alg_GBs": round(alg / (enc_mean * 1e-3) / 1e9, 1),
-                       "mfma_tflops": round(enc_tf, 2), "mfma_util": round(enc_tf / BF16_DENSE_TFLOPS, 5)},
-            "decode": {"mean_us": round(dec_mean * 1e3, 2), "median_us": round(dec_med * 1e3, 2),
-                       "alg_GBs": round(alg / (dec_mean * 1e-3) / 1e9, 1),
-                       "mfma_tflops": round(dec_tf, 2), "mfma_util": round(dec_tf / BF16_DENSE_TFLOPS, 5)},
-        },
-        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+        "hbm_frac_step": round(step_alg / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "kernels": kernels,
+        "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": (traffic or {}).get("bytes_per_launch")},
     }
