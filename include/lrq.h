@@ -185,6 +185,17 @@ int lrq_dense_elementwise(int32_t op, const void* x, const void* y, void* out, i
 int lrq_dense_softmax_bwd(const void* y, const void* g, void* out, int64_t rows, int64_t n_cols,
                           void* stream);
 
+/* outlier = x * (|x| > bf16(threshold)), rest = x - outlier over n contiguous bf16.
+ * Replaces torch_extract_unstructured (extraction_outlier_channel.py:5-8); the caller makes
+ * the sparse COO tensor of outlier, as the reference does. */
+int lrq_threshold_split(const void* x, int64_t n, float threshold, void* outlier, void* rest, void* stream);
+
+/* out[b, i, :] = x[b, idx[i], :] and x[b, idx[i], :] = 0 (in place) for x [B, M, N] bf16
+ * contiguous, k distinct indices along dim 1 (the reference's axis).
+ * Replaces torch_extract_channel (extraction_outlier_channel.py:11-14). */
+int lrq_gather_rows_zero(void* x, int64_t B, int64_t M, int64_t N, const int32_t* idx, int32_t k, void* out,
+                         void* stream);
+
 /* ------------------------------------------------------------------ misc */
 const char* lrq_status_string(int status);
 int32_t lrq_abi_version(void);

@@ -163,3 +163,25 @@ def test_dense_softmax_bwd(pkg, dev, shape):
     pf, dpf = O.bf16_to_f32(bits16(p)), O.bf16_to_f32(bits16(dp))
     out = pkg.triton_softmax_backward(p.to(dev), dp.to(dev))
     assert_fp_close(bits16(out), O.softmax_bwd(pf, dpf), "dense softmax bwd", max_abs=1e-3)
+
+
+def test_outlier_extraction_forms(pkg, dev):
+    """torch_extract_unstructured / torch_extract_channel (extraction_outlier_channel.py:5-14)."""
+    g = torch.Generator().manual_seed(13)
+    x = (torch.randn(2, 64, 96, generator=g) * 2).to(torch.bfloat16)
+    xb = bits16(x)
+    xf = O.bf16_to_f32(xb)
+    thr = torch.tensor(2.3)  # as the reference passes a kthvalue result
+    o_sp, rest = pkg.torch_extract_unstructured(x.to(dev), thr.to(dev))
+    tau = O.bf16_to_f32(O.bf16_round(np.float32(2.3)))
+    mask = np.abs(xf) > tau
+    assert np.array_equal(bits16(o_sp.to_dense()), np.where(mask, xb, 0).astype(np.uint16))
+    assert np.array_equal(bits16(rest), np.where(mask, 0, xb).astype(np.uint16))
+    idx = [3, 10, 40, 63]
+    xd = x.to(dev).contiguous()
+    out, x2 = pkg.torch_extract_channel(xd, idx)
+    assert x2.data_ptr() == xd.data_ptr()  # in place, like the reference
+    assert np.array_equal(bits16(out), xb[:, idx, :])
+    ref = xb.copy()
+    ref[:, idx, :] = 0
+    assert np.array_equal(bits16(x2), ref)

@@ -65,6 +65,9 @@ SIGNATURES = {
                                   c_void_p, c_void_p]),
     "lrq_dense_elementwise": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
     "lrq_dense_softmax_bwd": (c_int32, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
+    "lrq_threshold_split": (c_int32, [c_void_p, c_int64, c_float, c_void_p, c_void_p, c_void_p]),
+    "lrq_gather_rows_zero": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int32, c_void_p,
+                                       c_void_p]),
     "lrq_status_string": (ctypes.c_char_p, [c_int32]),
     "lrq_abi_version": (c_int32, []),
 }

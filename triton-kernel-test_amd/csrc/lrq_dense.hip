@@ -111,6 +111,37 @@ __global__ __launch_bounds__(256) void k_dense_softmax_bwd(const uint16_t* __res
   }
 }
 
+// extraction_outlier_channel.py:5-8: o = x * (|x| > tau), rest = x - o (tau rounded to bf16, as
+// the comparison of a bf16 tensor with a scalar is evaluated).  Both exact: o is x or 0.
+__global__ __launch_bounds__(256) void k_threshold_split(const uint16_t* __restrict__ x, int64_t n, float tau,
+                                                         uint16_t* __restrict__ o, uint16_t* __restrict__ rest) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; k < n; k += stride) {
+    const uint16_t h = x[k];
+    const bool out = fabsf(__uint_as_float((uint32_t)h << 16)) > tau;
+    o[k] = out ? h : (uint16_t)0;
+    rest[k] = out ? (uint16_t)0 : h;
+  }
+}
+
+// extraction_outlier_channel.py:11-14 (the reference indexes dim 1 of [B, M, N]):
+// out[b, i, :] = x[b, idx[i], :], then x[b, idx[i], :] = 0 in place.  One workgroup per (b, i);
+// indices must be distinct (a repeated index would read a row another workgroup zeroes).
+__global__ __launch_bounds__(256) void k_gather_rows_zero(uint16_t* __restrict__ x, int64_t M, int64_t N,
+                                                          const int32_t* __restrict__ idx, int k,
+                                                          uint16_t* __restrict__ out) {
+  const int64_t b = blockIdx.x / k;
+  const int i = (int)(blockIdx.x - b * k);
+  const int64_t m = idx[i];
+  if (m < 0 || m >= M) return;
+  uint16_t* src = x + (b * M + m) * N;
+  uint16_t* dst = out + (b * k + i) * N;
+  for (int64_t c = threadIdx.x; c < N; c += 256) {
+    dst[c] = src[c];
+    src[c] = 0;
+  }
+}
+
 static int grid_for(int64_t work) {
   const int64_t blocks = (work + 255) / 256;
   return (int)(blocks < 1 ? 1 : (blocks > 8192 ? 8192 : blocks));
@@ -159,5 +190,28 @@ extern "C" int lrq_dense_softmax_bwd(const void* y, const void* g, void* out, in
   else
     hipLaunchKernelGGL((k_dense_softmax_bwd<false>), dim3((unsigned)rows), dim3(256), 0, s, (const uint16_t*)y,
                        (const uint16_t*)g, (uint16_t*)out, n_cols);
+  return launch_status();
+}
+
+extern "C" int lrq_threshold_split(const void* x, int64_t n, float threshold, void* outlier, void* rest,
+                                   void* stream) {
+  if (x == nullptr || outlier == nullptr || rest == nullptr) return LRQ_ERR_NULL;
+  if (n < 0) return LRQ_ERR_SHAPE;
+  if (!aligned(x, 2) || !aligned(outlier, 2) || !aligned(rest, 2)) return LRQ_ERR_ALIGN;
+  if (n == 0) return LRQ_OK;
+  const float tau = bf16_value_host(bf16_bits_host(threshold));
+  hipLaunchKernelGGL(k_threshold_split, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)x, n, tau,
+                     (uint16_t*)outlier, (uint16_t*)rest);
+  return launch_status();
+}
+
+extern "C" int lrq_gather_rows_zero(void* x, int64_t B, int64_t M, int64_t N, const int32_t* idx, int32_t k,
+                                    void* out, void* stream) {
+  if (x == nullptr || (k > 0 && (idx == nullptr || out == nullptr))) return LRQ_ERR_NULL;
+  if (B < 0 || M < 0 || N < 0 || k < 0 || B * (int64_t)k > INT32_MAX) return LRQ_ERR_SHAPE;
+  if (!aligned(x, 2) || (out != nullptr && !aligned(out, 2)) || (idx != nullptr && !aligned(idx, 4))) return LRQ_ERR_ALIGN;
+  if (B == 0 || k == 0 || N == 0) return LRQ_OK;
+  hipLaunchKernelGGL(k_gather_rows_zero, dim3((unsigned)(B * k)), dim3(256), 0, (hipStream_t)stream, (uint16_t*)x, M, N,
+                     idx, (int)k, (uint16_t*)out);
   return launch_status();
 }

@@ -17,6 +17,8 @@ defects (s[0] only, tile-planar packing, unmasked scratch stores) are not reprod
   triton_gelu_backward                                 gelu_backward.py:73
   triton_softmax_backward                              softmax_backward.py:45
   triton_hadamard                                      extraction_fuse_hadamard.py:62
+  torch_extract_unstructured                           extraction_outlier_channel.py:5
+  torch_extract_channel                                extraction_outlier_channel.py:11
 """
 
 from __future__ import annotations
@@ -39,6 +41,8 @@ __all__ = [
     "triton_gelu_backward",
     "triton_softmax_backward",
     "triton_hadamard",
+    "torch_extract_unstructured",
+    "torch_extract_channel",
 ]
 
 _OP_STORE, _OP_SILU, _OP_MUL = 0, 1, 2
@@ -237,3 +241,33 @@ def triton_softmax_backward(y, grad_y):
     with torch.cuda.device(y.device):
         call("lrq_dense_softmax_bwd", _p(y2), _p(g2), _p(o), y2.numel() // n, n, _stream(y.device))
     return o
+
+
+def torch_extract_unstructured(x, threshold):
+    """(x * (|x| > threshold)).to_sparse() and the remainder x - that, on the HIP kernel
+    (the comparison is made in bf16, as for a bf16 tensor against a scalar)."""
+    _require_device(x)
+    x2 = x.to(torch.bfloat16).contiguous()
+    o = torch.empty_like(x2)
+    rest = torch.empty_like(x2)
+    tau = float(threshold.item() if isinstance(threshold, torch.Tensor) else threshold)
+    with torch.cuda.device(x2.device):
+        call("lrq_threshold_split", _p(x2), x2.numel(), tau, _p(o), _p(rest), _stream(x2.device))
+    return o.to_sparse(), rest
+
+
+def torch_extract_channel(x, channel_index):
+    """Returns (x[:, channel_index, :], x) after zeroing those rows of x in place — the
+    reference's axis (dim 1) and in-place behaviour, kept for drop-in use.  For hidden-channel
+    outliers of the compressed format see ``outlier_channels`` / ``encode(outlier_idx=...)``."""
+    _require_device(x)
+    if x.dim() != 3 or x.dtype != torch.bfloat16 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous bf16 [B, M, N] tensor")
+    idx = torch.as_tensor(channel_index, device=x.device).to(torch.int32).contiguous()
+    if idx.numel() != torch.unique(idx).numel():
+        raise ValueError("channel_index must not repeat")
+    B, M, N = x.shape
+    out = torch.empty((B, idx.numel(), N), dtype=x.dtype, device=x.device)
+    with torch.cuda.device(x.device):
+        call("lrq_gather_rows_zero", _p(x), B, M, N, _p(idx), idx.numel(), _p(out), _stream(x.device))
+    return out, x
