@@ -13,6 +13,8 @@
 #include "lrq_dequant.h"
 #include "lrq_math.h"
 
+#include <type_traits>
+
 namespace lrq {
 
 // ------------------------------------------------------------------ epilogues
@@ -352,7 +354,197 @@ __global__ __launch_bounds__(NW * 64) void k_decode_staged(
   }
 }
 
+// ------------------------------------------------------------------ row-persistent kernel
+// The plain decode (x_hat stored), about one workgroup per CU.  Same per-block arithmetic and
+// input staging as k_decode_staged; the difference is on the store side.  Each wave writes its
+// reconstructed unit (16 rows x NP planes x G columns, MFMA layout) into an LDS output tile, and
+// after the next barrier the workgroup stores the tile as whole row segments: one 16-byte
+// vector per lane, NW*G*2 contiguous bytes per row and plane.  The MFMA layout stores 4 x 16 B
+// pieces of 16 rows per instruction; on MI355X these partial-line writes, and a second
+// workgroup interleaving its own traffic on the CU, cost about a third of the decode's time.
+//
+// Pipeline (one barrier per row block b): write the staged codes/qparams/L of block b into
+// input slot b&1 -> barrier -> store the output tile of block b-1 (slot (b-1)&1) -> reconstruct
+// block b into output slot b&1.  A slot is rewritten two blocks later, after a barrier that
+// every wave reaches only once its reads of that slot have returned.  All input loads of the
+// workgroup's RBW blocks are issued before the first store (loads and stores share one
+// in-order counter on gfx9).  Requires units % NW == 0 (every wave active).
+template <int BITS, int G, int NW>
+struct RowsOut {
+  static constexpr int NP = 8 / BITS;
+  static constexpr int OROW = NW * G * 2;           // output bytes per row and plane
+  static constexpr int OPAD = OROW + 16;            // LDS row pitch (spreads the 16 rows over banks)
+  static constexpr int OSLOT = 16 * NP * OPAD;      // one block's output tile
+  static constexpr int OCH = 16 * NP * (OROW / 16); // 16-byte chunks per tile
+  static_assert(OROW % 16 == 0, "row segment of whole vectors");
+};
+
+template <int BITS, int G, int R, int NW, int RBW>
+__global__ __launch_bounds__(NW * 64) void k_decode_rows(
+    const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
+    const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
+    uint16_t* __restrict__ out, int64_t ldo) {
+  using Tl = StagedTile<BITS, G, R, NW>;
+  using Ro = RowsOut<BITS, G, NW>;
+  constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, E = G / 4, T = Tl::T;
+  extern __shared__ __attribute__((aligned(16))) unsigned char sm[];  // [2][SLOT] inputs, [2][OSLOT] outputs
+  unsigned char* osm = sm + 2 * Tl::SLOT;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int u0 = blockIdx.y * NW, u = u0 + w;
+  const int nrb = (M + 15) / 16;
+  const int rb0 = blockIdx.x * RBW;
+  if (rb0 >= nrb) return;  // whole workgroup (no barrier reached)
+
+  u32x2 vop[NP][G / 16][RT];
+  if constexpr (R > 0) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, u, N, NP, G), j, g, vop[p]);
+  }
+
+  struct In {
+    u32x4 c[Tl::CPT];
+    u32x2 ql;
+  };
+  const int qk = tid, lk = tid - Tl::QCH;
+  const bool has_q = qk < Tl::QCH;
+  const bool has_l = R > 0 && lk >= 0 && lk < Tl::LCH;
+  auto load = [&](In& in, int rb) {
+#pragma unroll
+    for (int i = 0; i < Tl::CPT; ++i) {
+      const int k = tid + T * i, r = k / (Tl::CROW / 16), c16 = k % (Tl::CROW / 16);
+      const int64_t row = min(rb * 16 + r, M - 1);
+      in.c[i] = ld16_stream(codes + row * ldc + (int64_t)u0 * G + c16 * 16);
+    }
+    if (has_q) {
+      const int r = qk / (Tl::QROW / 8), c8 = qk % (Tl::QROW / 8);
+      const int64_t row = min(rb * 16 + r, M - 1);
+      in.ql = ld8(reinterpret_cast<const uint8_t*>(qparams) + (row * ldq + (int64_t)u0 * NP * 2) * 2 + c8 * 8);
+    } else if (has_l) {
+      const int r = lk / (Tl::LROW / 8), c8 = lk % (Tl::LROW / 8);
+      const int64_t row = min(rb * 16 + r, M - 1);
+      in.ql = ld8(reinterpret_cast<const uint8_t*>(Lin) + row * ldl * 2 + c8 * 8);
+    }
+  };
+  // Store the output tile of block rb from slot s: chunk k -> plane, row, 16-byte column chunk.
+  auto store_tile = [&](int rb, int s) {
+    const unsigned char* os = osm + s * Ro::OSLOT;
+#pragma unroll
+    for (int i = 0; i < (Ro::OCH + T - 1) / T; ++i) {
+      const int k = tid + T * i;
+      if (Ro::OCH % T == 0 || k < Ro::OCH) {
+        const int c16 = k % (Ro::OROW / 16), pr = k / (Ro::OROW / 16), p = pr / 16, r = pr % 16;
+        const int64_t row = min(rb * 16 + r, M - 1);
+        const u32x4 v = *reinterpret_cast<const u32x4*>(os + (p * 16 + r) * Ro::OPAD + c16 * 16);
+        st16(reinterpret_cast<unsigned char*>(out + row * ldo + unit_base(p, u0, N, NP, G)) + c16 * 16, v);
+      }
+    }
+  };
+
+  In in[RBW];
+#pragma unroll
+  for (int b = 0; b < RBW; ++b) load(in[b], min(rb0 + b, nrb - 1));
+  __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+  for (int b = 0; b < RBW; ++b) {
+    const int rb = min(rb0 + b, nrb - 1);
+    unsigned char* slot = sm + (b & 1) * Tl::SLOT;
+#pragma unroll
+    for (int i = 0; i < Tl::CPT; ++i) {
+      const int k = tid + T * i, r = k / (Tl::CROW / 16), c16 = k % (Tl::CROW / 16);
+      *reinterpret_cast<u32x4*>(slot + r * Tl::CROW + c16 * 16) = in[b].c[i];
+    }
+    if (has_q) {
+      const int r = qk / (Tl::QROW / 8), c8 = qk % (Tl::QROW / 8);
+      *reinterpret_cast<u32x2*>(slot + Tl::QOFF + r * Tl::QROW + c8 * 8) = in[b].ql;
+    } else if (has_l) {
+      const int r = lk / (Tl::LROW / 8), c8 = lk % (Tl::LROW / 8);
+      *reinterpret_cast<u32x2*>(slot + Tl::LOFF + r * Tl::LROW + c8 * 8) = in[b].ql;
+    }
+    lds_barrier();
+    if (b > 0) store_tile(min(rb0 + b - 1, nrb - 1), (b - 1) & 1);
+    u32x4 cb[G / 64];
+#pragma unroll
+    for (int i = 0; i < G / 64; ++i)
+      cb[i] = *reinterpret_cast<const u32x4*>(slot + j * Tl::CROW + w * G + E * g + 16 * i);
+    uint32_t qp[NP];
+    if constexpr (NP == 2) {
+      const u32x2 q = *reinterpret_cast<const u32x2*>(slot + Tl::QOFF + j * Tl::QROW + w * 8);
+      qp[0] = q[0];
+      qp[1] = q[1];
+    } else {
+      qp[0] = *reinterpret_cast<const uint32_t*>(slot + Tl::QOFF + j * Tl::QROW + w * 4);
+    }
+    u32x2 lop[RT];
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t)
+        lop[t] = *reinterpret_cast<const u32x2*>(slot + Tl::LOFF + j * Tl::LROW + 32 * t + 8 * g);
+    }
+    unsigned char* os = osm + (b & 1) * Ro::OSLOT;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      float xh[E];
+      reconstruct_plane<BITS, G, R>(cb, qp[p], p, vop[p], lop, xh);
+#pragma unroll
+      for (int k = 0; k < E / 8; ++k)
+        *reinterpret_cast<u32x4*>(os + (p * 16 + j) * Ro::OPAD + (w * G + E * g + 8 * k) * 2) = pack8(xh + 8 * k);
+    }
+  }
+  lds_barrier();
+  store_tile(min(rb0 + RBW - 1, nrb - 1), (RBW - 1) & 1);
+}
+
 // ------------------------------------------------------------------ host side
+// Waves per workgroup for k_decode_rows: NW * G = 512 columns, so each output row segment is 1 KB
+// (one 16-byte vector per lane) and two tiles plus two input slots fit in LDS.
+template <int G>
+constexpr int rows_nw() { return 512 / G; }
+
+template <int BITS, int G, int R, int RBW>
+static int decode_rows_launch_rbw(const lrq_tensors* t, hipStream_t s, uint16_t* out, int64_t ldo) {
+  constexpr int NW = rows_nw<G>();
+  const int M = (int)t->rows, N = (int)t->hidden;
+  const int units = N / (G * (8 / BITS));
+  const int nrb = (M + 15) / 16;
+  const size_t shm = 2 * (size_t)StagedTile<BITS, G, R, NW>::SLOT + 2 * (size_t)RowsOut<BITS, G, NW>::OSLOT;
+  auto kern = k_decode_rows<BITS, G, R, NW, RBW>;
+  if (shm > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+  hipLaunchKernelGGL(kern, dim3((nrb + RBW - 1) / RBW, units / NW), dim3(NW * 64), shm, s, (const uint8_t*)t->codes,
+                     t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp, (const uint16_t*)t->L, t->ld_L,
+                     (const uint16_t*)t->V, M, N, out, ldo);
+  return launch_status();
+}
+
+// Row blocks per workgroup: the choice that minimises (workgroup rounds) x (blocks + 2), where
+// a round is one workgroup per CU (the LDS tile keeps it at one) and the 2 stands for the
+// per-workgroup fixed cost (V operands, pipeline fill).
+template <int BITS, int G, int R>
+static int decode_rows_launch(const lrq_tensors* t, hipStream_t s, uint16_t* out, int64_t ldo) {
+  constexpr int NW = rows_nw<G>();
+  const int64_t ug = t->hidden / (G * (8 / BITS)) / NW, nrb = (t->rows + 15) / 16, cus = cu_count();
+  // 16 blocks of G = 128 codes with a rank term exceed the register budget (spills)
+  constexpr int kMax = (G == 128 && R > 0) ? 12 : 16;
+  const int cand[] = {16, 12, 8, 4, 2, 1};
+  int best = 1;
+  int64_t best_cost = INT64_MAX;
+  for (int rbw : cand) {
+    if (rbw > kMax) continue;
+    const int64_t wgs = ((nrb + rbw - 1) / rbw) * ug;
+    const int64_t cost = ((wgs + cus - 1) / cus) * (rbw + 2);
+    if (cost < best_cost) best_cost = cost, best = rbw;
+  }
+  switch (best) {
+    case 16: return decode_rows_launch_rbw<BITS, G, R, kMax>(t, s, out, ldo);
+    case 12: return decode_rows_launch_rbw<BITS, G, R, 12>(t, s, out, ldo);
+    case 8: return decode_rows_launch_rbw<BITS, G, R, 8>(t, s, out, ldo);
+    case 4: return decode_rows_launch_rbw<BITS, G, R, 4>(t, s, out, ldo);
+    case 2: return decode_rows_launch_rbw<BITS, G, R, 2>(t, s, out, ldo);
+    default: return decode_rows_launch_rbw<BITS, G, R, 1>(t, s, out, ldo);
+  }
+}
+
 template <int BITS, int G, int R, int RBW, class EPI>
 static int decode_launch_rbw(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
   constexpr int NP = 8 / BITS, NW = 8, PD = RBW;  // every load before the first store
@@ -380,6 +572,10 @@ static int decode_launch_rbw(const lrq_tensors* t, hipStream_t s, const EPI& epi
 template <int BITS, int G, int R, class EPI>
 static int decode_launch(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
   constexpr int NP = 8 / BITS, NW = 8, BIG = EPI::kIn ? 4 : 8;
+  if constexpr (std::is_same_v<EPI, EpiStore>) {
+    if (t->n_outlier == 0 && (t->hidden / (G * NP)) % rows_nw<G>() == 0)
+      return decode_rows_launch<BITS, G, R>(t, s, epi.out, epi.ld);
+  }
   const int64_t units = t->hidden / (G * NP), nrb = (t->rows + 15) / 16;
   const int64_t wgs = ((nrb + BIG - 1) / BIG) * ((units + NW - 1) / NW);
   if (wgs >= 512) return decode_launch_rbw<BITS, G, R, BIG>(t, s, epi);

@@ -305,13 +305,6 @@ __global__ __launch_bounds__(256) void k_gather_side(const uint16_t* __restrict_
 // -------------------------------------------------------------------------------------
 // host side
 
-static int cu_count() {
-  int dev = 0, n = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 256;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
-  return n;
-}
-
 template <int BITS, int G, int R, int NW, int UPW, bool DB, int RBW>
 static int launch_persist_rbw(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s) {
   using Lds = PersistLds<BITS, G, R, NW, UPW>;

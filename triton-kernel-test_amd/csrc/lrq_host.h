@@ -32,6 +32,14 @@ static inline float bf16_value_host(uint16_t h) {
 
 static constexpr int format_key(int bits, int group, int rank) { return bits * 100000 + group * 100 + rank; }
 
+// Compute units of the current device (256 on MI355X); launch shapes are sized from it.
+static inline int cu_count() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+  return n;
+}
+
 static inline int launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? LRQ_OK : (int)e;
