@@ -225,19 +225,24 @@ def main():
         step(i)
     torch.cuda.synchronize()
 
-    # ---- timed region: K steps, per-kernel HIP events on the launch stream
-    ne = len(entries)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(ne + 1)] for _ in range(args.steps)]
+    # ---- timed region: exactly K steps, nothing else on the stream
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_start.record(stream)
     for i in range(args.steps):
-        step(i, evs[i])
+        step(i)
     t_end.record(stream)
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
     ms_step = total_ms / args.steps
+
+    # ---- in-step breakdown (a separate pass): HIP events between the kernels of each step
+    ne = len(entries)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(ne + 1)] for _ in range(args.steps)]
+    for i in range(args.steps):
+        step(i, evs[i])
+    torch.cuda.synchronize()
 
     # ---- per-kernel duration: K back-to-back launches of that kernel alone between two
     # events on its stream (dispatch latency overlaps, as in a rocprofv3 kernel trace)

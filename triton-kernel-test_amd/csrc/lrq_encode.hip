@@ -18,6 +18,8 @@
 #include "lrq_host.h"
 #include "lrq_quant.h"
 
+#include <type_traits>
+
 namespace lrq {
 
 // -------------------------------------------------------------------------------------
@@ -183,6 +185,194 @@ __global__ __launch_bounds__(NW * 64) void k_encode_persist(
 }
 
 // -------------------------------------------------------------------------------------
+// Row-staged single-pass encode (about one workgroup per CU, NW waves of UPW units each).
+//
+// On MI355X a CU has a small budget of loads in flight (about its L1 size) and serves its
+// memory instructions in issue order; loads in the MFMA layout (16 rows x 4 x 16 B per
+// instruction) reach far less bandwidth than contiguous ones.  Here each wave streams its own
+// slice of the next row block (16 rows x NP pieces of UPW*G*2 contiguous bytes) into a private
+// LDS region, in NR rounds interleaved with the current block's work, and reads it back in the
+// MFMA layout.  The region is private, so the only barrier per block is the one that publishes
+// the projection partials (double-buffered; every lane sums the NW partials of its own lane
+// position in a fixed order, so L is deterministic).  V operands stay in registers for the
+// whole kernel.  Rows past the end repeat the last row (no predicated stores).
+template <int BITS, int G, int R, int NW, int UPW>
+struct RowsEnc {
+  static constexpr int NP = 8 / BITS, RT = R / 16;
+  static constexpr int PIECE = UPW * G * 2;         // bytes of one (row, plane) piece of a slice
+  static constexpr int PITCH = NP * PIECE + 16;      // LDS row pitch of a region (bank spread)
+  static constexpr int REGION = 16 * PITCH;          // bytes per wave
+  static constexpr int PPL = 1024 / PIECE;           // pieces per 1 KB load instruction
+  static constexpr int LPL = 64 / PPL;               // lanes per piece
+  static constexpr int NLD = 16 * NP / PPL;          // load instructions per wave and block
+  static constexpr int NR = 4, RL = NLD / NR;        // rounds per block, loads per round
+  static constexpr int PART = NW * RT * 64 * 16;     // one partial slot
+  static constexpr size_t LDS = (size_t)NW * REGION + 2 * (size_t)PART;
+  static_assert(1024 % PIECE == 0 && NLD % NR == 0 && NR == 4, "slice pieces per load; the round schedule is written for 4");
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+};
+
+template <int BITS, int G, int R, int NW, int UPW, int RBW>
+__global__ __launch_bounds__(NW * 64) void k_encode_rows(
+    const uint16_t* __restrict__ X, int64_t ldx, int M, int N, const uint16_t* __restrict__ V,
+    uint16_t* __restrict__ Lout, int64_t ldl, uint8_t* __restrict__ codes, int64_t ldc,
+    uint16_t* __restrict__ qparams, int64_t ldq) {
+  using Re = RowsEnc<BITS, G, R, NW, UPW>;
+  constexpr int NP = Re::NP, CPG = G / 32, RT = Re::RT, E = G / 4;
+  static_assert(NP == 2 && UPW == 4, "the qparams gather below is written for 4 units x 2 planes");
+  extern __shared__ __attribute__((aligned(16))) unsigned char shm[];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  unsigned char* region = shm + (size_t)w * Re::REGION;
+  f32x4* part = reinterpret_cast<f32x4*>(shm + (size_t)NW * Re::REGION);  // [2][NW][RT][64]
+  const int nrb = (M + 15) / 16;
+  const int rb0 = blockIdx.x * RBW;
+  const int ub = w * UPW;  // first unit of this wave
+
+  // V operands of the wave's units, requested before any X so they are first in the queue.
+  u32x2 vop[UPW][NP][G / 16][RT];
+#pragma unroll
+  for (int uu = 0; uu < UPW; ++uu)
+#pragma unroll
+    for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, ub + uu, N, NP, G), j, g, vop[uu][p]);
+  const u32x2 ident = identity_bop(j, g);
+
+  // Load instruction i of block rb: pieces i*PPL .. +PPL-1 (piece pc = row pc/NP, plane pc%NP);
+  // lane l carries 16 bytes of piece i*PPL + l/LPL at byte (l % LPL) * 16.
+  const int lpc = lane / Re::LPL, loff = (lane % Re::LPL) * 16;
+  auto gaddr = [&](int rb, int i) {
+    const int pc = i * Re::PPL + lpc, r = pc / NP, p = pc % NP;
+    const int64_t row = min(rb * 16 + r, M - 1);
+    return reinterpret_cast<const unsigned char*>(X + row * ldx + unit_base(p, ub, N, NP, G)) + loff;
+  };
+  auto laddr = [&](int i) {
+    const int pc = i * Re::PPL + lpc, r = pc / NP, p = pc % NP;
+    return region + r * Re::PITCH + p * Re::PIECE + loff;
+  };
+  u32x4 pf[2][Re::RL];
+  auto issue = [&](int buf, int rb, int round) {
+#pragma unroll
+    for (int i = 0; i < Re::RL; ++i) pf[buf][i] = ld16_stream(gaddr(rb, round * Re::RL + i));
+  };
+  auto land = [&](int buf, int round) {
+#pragma unroll
+    for (int i = 0; i < Re::RL; ++i) *reinterpret_cast<u32x4*>(laddr(round * Re::RL + i)) = pf[buf][i];
+  };
+
+  // Prologue: block rb0 into the region, two rounds in flight.
+  {
+    const int rb = min(rb0, nrb - 1);
+    issue(0, rb, 0);
+    issue(1, rb, 1);
+#pragma unroll
+    for (int rd = 0; rd < Re::NR; ++rd) {
+      land(rd & 1, rd);
+      if (rd + 2 < Re::NR) issue(rd & 1, rb, rd + 2);
+    }
+  }
+
+  // One row block; NEXT: stream the next block's slice into the region meanwhile.  The block
+  // loop is not unrolled (unrolled, the compiler's schedule across blocks spills registers).
+  auto block = [&](auto next_tag, int b) {
+    constexpr bool next = decltype(next_tag)::value;
+    const int rb = min(rb0 + b, nrb - 1);
+    const int row = min(rb * 16 + j, M - 1);
+    const int rbn = min(rb0 + b + 1, nrb - 1);
+    // this block's slice, MFMA layout (lane (j, g): row j, columns E*g .. of each unit-plane)
+    u32x4 x[UPW][NP][CPG];
+#pragma unroll
+    for (int uu = 0; uu < UPW; ++uu)
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int k = 0; k < CPG; ++k)
+          x[uu][p][k] = *reinterpret_cast<const u32x4*>(region + j * Re::PITCH + p * Re::PIECE + (uu * G + E * g + 8 * k) * 2);
+    if (next) issue(0, rbn, 0);
+    __builtin_amdgcn_sched_barrier(0);
+
+    f32x4 acc[2][RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) acc[0][t] = acc[1][t] = zero4();
+#pragma unroll
+    for (int uu = 0; uu < UPW; ++uu)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) project_unit<G, R>(vop[uu][p], x[uu][p], ident, acc[(uu * NP + p) & 1]);
+    f32x4* slot = part + (size_t)(b & 1) * NW * RT * 64;
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      f32x4 a = acc[0][t];
+      a[0] += acc[1][t][0];
+      a[1] += acc[1][t][1];
+      a[2] += acc[1][t][2];
+      a[3] += acc[1][t][3];
+      slot[(w * RT + t) * 64 + lane] = a;
+    }
+    lds_barrier();
+    u32x2 lop[RT], lopn[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      f32x4 s = slot[t * 64 + lane];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; ++w2) {
+        const f32x4 o = slot[(w2 * RT + t) * 64 + lane];
+        s[0] += o[0];
+        s[1] += o[1];
+        s[2] += o[2];
+        s[3] += o[3];
+      }
+      // lane (j, g) holds L[row j][16t + 4g + v]
+      lop[t] = u32x2{pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3])};
+      lopn[t] = neg_bf16x4(lop[t]);
+    }
+    // the region's rows of the next block arrive round by round between the quantised units
+    // (at most two rounds in flight: round 0 overlaps the projection, 1 and 2 the first two
+    // units, 3 the last two)
+    if (next) {
+      land(0, 0);
+      issue(1, rbn, 1);
+      issue(0, rbn, 2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint8_t* crow = codes + (int64_t)row * ldc;
+    uint32_t qp[UPW];
+#pragma unroll
+    for (int uu = 0; uu < UPW; ++uu) {
+      qp[uu] = quant_unit_regs<BITS, G, R>(x[uu], vop[uu], lopn, ub + uu, g, crow);
+      if (uu == 1 && next) {
+        __builtin_amdgcn_sched_barrier(0);
+        land(1, 1);
+        issue(1, rbn, 3);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // qparams of the wave's 4 units as one 16-byte store per row half: lanes 0..31 hold the
+    // plane-0 pairs, lanes 32..63 the plane-1 pairs; two half-swaps interleave them.
+    {
+      float a = __uint_as_float(qp[0]), bq = __uint_as_float(qp[2]);
+      float c = __uint_as_float(qp[1]), d = __uint_as_float(qp[3]);
+      swap32(a, bq);
+      swap32(c, d);
+      const u32x4 v = u32x4{__float_as_uint(a), __float_as_uint(bq), __float_as_uint(c), __float_as_uint(d)};
+      st16_pred(qparams + (int64_t)rb * 16 * ldq, (uint32_t)(16 * ldq * 2),
+                (uint32_t)(((row - rb * 16) * ldq + ub * NP * 2) * 2 + (g >> 1) * 16), v, (g & 1) == 0);
+    }
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+      st8_pred(Lout + (int64_t)rb * 16 * ldl, (uint32_t)(16 * ldl * 2),
+               (uint32_t)(((row - rb * 16) * ldl + 16 * t + 4 * g) * 2), lop[t], w == 0);
+    if (next) {
+      __builtin_amdgcn_sched_barrier(0);
+      land(0, 2);
+      land(1, 3);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+#pragma unroll 1
+  for (int b = 0; b < RBW - 1; ++b) block(std::true_type{}, b);
+  block(std::false_type{}, RBW - 1);
+}
+
+// -------------------------------------------------------------------------------------
 // Projection only (first pass of the two-pass encode).  Grid: ceil(rows / 16) workgroups
 // of 4 waves; wave w sums 32-column chunks w, w + 4, ... of the row.  Uses V^T [R, N].
 template <int R>
@@ -329,6 +519,41 @@ static int launch_persist(const lrq_tensors* t, const void* x, int64_t ldx, hipS
   return launch_persist_rbw<BITS, G, R, NW, UPW, DB, 1>(t, x, ldx, s);
 }
 
+template <int BITS, int G, int R, int RBW>
+static int launch_rows_rbw(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s) {
+  constexpr int NW = 8, UPW = 4;
+  using Re = RowsEnc<BITS, G, R, NW, UPW>;
+  auto kern = k_encode_rows<BITS, G, R, NW, UPW, RBW>;
+  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)Re::LDS);
+  const int nrb = (int)((t->rows + 15) / 16);
+  hipLaunchKernelGGL(kern, dim3((nrb + RBW - 1) / RBW), dim3(NW * 64), Re::LDS, s, (const uint16_t*)x, ldx,
+                     (int)t->rows, (int)t->hidden, (const uint16_t*)t->V, (uint16_t*)t->L, t->ld_L,
+                     (uint8_t*)t->codes, t->ld_codes, (uint16_t*)t->qparams, t->ld_qp);
+  return launch_status();
+}
+
+// Row blocks per workgroup for k_encode_rows (one workgroup per CU): the choice minimising
+// (workgroup rounds) x (2 * blocks + 3), the 3 standing for the per-workgroup V operands and
+// the first block's unoverlapped load.
+template <int BITS, int G, int R>
+static int launch_rows(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s) {
+  const int64_t nrb = (t->rows + 15) / 16, cus = cu_count();
+  int best = 1;
+  int64_t best_cost = INT64_MAX;
+  // (2 is not offered: its one-iteration block loop is folded and the two blocks' schedules
+  // merge into a spilling one)
+  for (int rbw : {8, 4, 1}) {
+    const int64_t wgs = (nrb + rbw - 1) / rbw;
+    const int64_t cost = ((wgs + cus - 1) / cus) * (2 * rbw + 3);
+    if (cost < best_cost) best_cost = cost, best = rbw;
+  }
+  switch (best) {
+    case 8: return launch_rows_rbw<BITS, G, R, 8>(t, x, ldx, s);
+    case 4: return launch_rows_rbw<BITS, G, R, 4>(t, x, ldx, s);
+    default: return launch_rows_rbw<BITS, G, R, 1>(t, x, ldx, s);
+  }
+}
+
 // Returns 1 and launches when a single-pass kernel exists for this shape, else 0.
 template <int BITS, int G, int R>
 static int encode_persist_dispatch(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s,
@@ -343,7 +568,16 @@ static int encode_persist_dispatch(const lrq_tensors* t, const void* x, int64_t 
     switch (units) {
       case 8: *status = launch_persist<BITS, G, R, 4, 2, true>(t, x, ldx, s); return 1;
       case 16: *status = launch_persist<BITS, G, R, 8, 2, true>(t, x, ldx, s); return 1;
-      case 32: *status = launch_persist<BITS, G, R, 16, 2, true>(t, x, ldx, s); return 1;
+      case 32:
+        // row-staged kernel (4 units x 2 planes per wave; 16-byte qparams stores per row)
+        if constexpr (BITS == 4 && G == 64) {
+          if (t->ld_qp % 8 == 0 && aligned(t->qparams, 16)) {
+            *status = launch_rows<BITS, G, R>(t, x, ldx, s);
+            return 1;
+          }
+        }
+        *status = launch_persist<BITS, G, R, 16, 2, true>(t, x, ldx, s);
+        return 1;
       case 40:
         if constexpr (wide_ok) {
           *status = launch_persist<BITS, G, R, 8, 5, false>(t, x, ldx, s);

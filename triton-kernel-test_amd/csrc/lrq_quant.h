@@ -48,11 +48,13 @@ __device__ __forceinline__ void local_minmax(const float* r, float& mn, float& m
 // stores repeat its bytes, so no store is predicated (on gfx9 a predicated store makes the
 // compiler drain all outstanding memory operations, prefetches included, at the next use
 // of a load).
+// Core of quant_unit: stores the lane's code bytes and returns the (scale, zero) pair this lane
+// computed (with two planes: plane 0's in lanes 0..31, plane 1's in lanes 32..63).
 template <int BITS, int G, int R>
-__device__ __forceinline__ void quant_unit(const u32x4 (&x)[8 / BITS][G / 32],
-                                           const u32x2 (&vop)[8 / BITS][G / 16][R > 0 ? R / 16 : 1],
-                                           const u32x2* lopn, const uint32_t* colmask, int u, int N, int g,
-                                           uint8_t* __restrict__ crow, uint16_t* __restrict__ qrow) {
+__device__ __forceinline__ uint32_t quant_unit_core(const u32x4 (&x)[8 / BITS][G / 32],
+                                                    const u32x2 (&vop)[8 / BITS][G / 16][R > 0 ? R / 16 : 1],
+                                                    const u32x2* lopn, const uint32_t* colmask, int u, int N,
+                                                    int g, uint8_t* __restrict__ crow) {
   constexpr int NP = 8 / BITS, E = G / 4;
   static_assert(NP == 1 || NP == 2, "group mode packs 4- or 8-bit codes");
   float r[NP][E];
@@ -71,15 +73,16 @@ __device__ __forceinline__ void quant_unit(const u32x4 (&x)[8 / BITS][G / 32],
   }
 
   GroupParams gp[NP];
+  uint32_t qp;
   if constexpr (NP == 2) {
     // lanes 0..31 hold plane 0's statistics, lanes 32..63 plane 1's
     const GroupParams own = group_params<BITS>(row_min4_pair(mn[0], mn[1]), row_max4_pair(mx[0], mx[1]));
     halves_broadcast(own.a, gp[0].a, gp[1].a);
     halves_broadcast(own.b, gp[0].b, gp[1].b);
-    st4(qrow + u * 4 + (g >> 1) * 2, own.qp);  // lanes g, g^1 write the same pair
+    qp = own.qp;
   } else {
     gp[0] = group_params<BITS>(row_min4(mn[0]), row_max4(mx[0]));
-    st4(qrow + u * 2, gp[0].qp);
+    qp = gp[0].qp;
   }
 
   // byte[e]: the packed code byte of element e in bits 0..7 (higher bits are don't-care).
@@ -97,6 +100,27 @@ __device__ __forceinline__ void quant_unit(const u32x4 (&x)[8 / BITS][G / 32],
 #pragma unroll
   for (int i = 0; i < E / 16; ++i)
     st16(crow + u * G + E * g + 16 * i, u32x4{word[4 * i], word[4 * i + 1], word[4 * i + 2], word[4 * i + 3]});
+  return qp;
+}
+
+template <int BITS, int G, int R>
+__device__ __forceinline__ void quant_unit(const u32x4 (&x)[8 / BITS][G / 32],
+                                           const u32x2 (&vop)[8 / BITS][G / 16][R > 0 ? R / 16 : 1],
+                                           const u32x2* lopn, const uint32_t* colmask, int u, int N, int g,
+                                           uint8_t* __restrict__ crow, uint16_t* __restrict__ qrow) {
+  const uint32_t qp = quant_unit_core<BITS, G, R>(x, vop, lopn, colmask, u, N, g, crow);
+  if constexpr (8 / BITS == 2)
+    st4(qrow + u * 4 + (g >> 1) * 2, qp);  // lanes g, g^1 write the same pair
+  else
+    st4(qrow + u * 2, qp);
+}
+
+// quant_unit without the qparams store: the caller gathers the pairs of several units.
+template <int BITS, int G, int R>
+__device__ __forceinline__ uint32_t quant_unit_regs(const u32x4 (&x)[8 / BITS][G / 32],
+                                                    const u32x2 (&vop)[8 / BITS][G / 16][R > 0 ? R / 16 : 1],
+                                                    const u32x2* lopn, int u, int g, uint8_t* __restrict__ crow) {
+  return quant_unit_core<BITS, G, R>(x, vop, lopn, nullptr, u, 0, g, crow);
 }
 
 }  // namespace lrq
