@@ -436,7 +436,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
         const int c16 = k % (Ro::OROW / 16), pr = k / (Ro::OROW / 16), p = pr / 16, r = pr % 16;
         const int64_t row = min(rb * 16 + r, M - 1);
         const u32x4 v = *reinterpret_cast<const u32x4*>(os + (p * 16 + r) * Ro::OPAD + c16 * 16);
-        st16(reinterpret_cast<unsigned char*>(out + row * ldo + unit_base(p, u0, N, NP, G)) + c16 * 16, v);
+        st16_stream(reinterpret_cast<unsigned char*>(out + row * ldo + unit_base(p, u0, N, NP, G)) + c16 * 16, v);
       }
     }
   };

@@ -229,12 +229,7 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
   const int rb0 = blockIdx.x * RBW;
   const int ub = w * UPW;  // first unit of this wave
 
-  // V operands of the wave's units, requested before any X so they are first in the queue.
   u32x2 vop[UPW][NP][G / 16][RT];
-#pragma unroll
-  for (int uu = 0; uu < UPW; ++uu)
-#pragma unroll
-    for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, ub + uu, N, NP, G), j, g, vop[uu][p]);
   const u32x2 ident = identity_bop(j, g);
 
   // Load instruction i of block rb: pieces i*PPL .. +PPL-1 (piece pc = row pc/NP, plane pc%NP);
@@ -259,11 +254,42 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
     for (int i = 0; i < Re::RL; ++i) *reinterpret_cast<u32x4*>(laddr(round * Re::RL + i)) = pf[buf][i];
   };
 
-  // Prologue: block rb0 into the region, two rounds in flight.
+  // Prologue: block rb0 into the region, two rounds in flight.  The first two rounds are
+  // requested before the V operands (L2-resident after the first workgroups), so HBM is busy
+  // from the start.  V arrives as whole 1 KB pieces (the wave's V rows are NP contiguous ranges
+  // of UPW*G rows), passes through the region, and is read back in the operand layout before
+  // the region receives block rb0.
   {
     const int rb = min(rb0, nrb - 1);
     issue(0, rb, 0);
     issue(1, rb, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    constexpr int VB = UPW * G * R * 2;  // bytes of the wave's V rows in one plane
+    constexpr int VLD = NP * VB / 1024;   // 1 KB loads
+    static_assert(VB % 1024 == 0 && NP * VB <= Re::REGION, "V staging through the region");
+    u32x4 vraw[VLD];
+#pragma unroll
+    for (int i = 0; i < VLD; ++i) {
+      const int p = i / (VB / 1024);
+      vraw[i] = ld16(reinterpret_cast<const unsigned char*>(V + (int64_t)unit_base(p, ub, N, NP, G) * R) +
+                     (i % (VB / 1024)) * 1024 + lane * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < VLD; ++i) *reinterpret_cast<u32x4*>(region + i * 1024 + lane * 16) = vraw[i];
+#pragma unroll
+    for (int uu = 0; uu < UPW; ++uu)
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int q = 0; q < G / 16; ++q)
+#pragma unroll
+          for (int t = 0; t < RT; ++t) {
+            const int vr = uu * G + vrow_res<G>(0, j, q);  // V row within the plane's range
+            vop[uu][p][q][t] = *reinterpret_cast<const u32x2*>(region + p * VB + vr * R * 2 + 32 * t + 8 * g);
+          }
+    // the region is rewritten below: every read above must have returned
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int rd = 0; rd < Re::NR; ++rd) {
       land(rd & 1, rd);
