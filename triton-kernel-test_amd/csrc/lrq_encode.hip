@@ -154,7 +154,7 @@ __global__ __launch_bounds__(NW * 64) void k_encode_persist(
       st8_pred(Lout + (int64_t)rb * 16 * ldl, (uint32_t)(16 * ldl * 2),
                (uint32_t)(((row - rb * 16) * ldl + 16 * t + 4 * g) * 2), lop[t], w == 0);
     }
-    uint8_t* crow = codes + (int64_t)row * ldc;
+    uint8_t* crow = codes + (int64_t)rb * 16 * ldc + (uint32_t)(row - rb * 16) * (uint32_t)ldc;
     uint16_t* qrow = qparams + (int64_t)row * ldq;
 #pragma unroll
     for (int uu = 0; uu < UPW; ++uu) {
@@ -232,13 +232,15 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
   u32x2 vop[UPW][NP][G / 16][RT];
   const u32x2 ident = identity_bop(j, g);
 
-  // Load instruction i of block rb: pieces i*PPL .. +PPL-1 (piece pc = row pc/NP, plane pc%NP);
-  // lane l carries 16 bytes of piece i*PPL + l/LPL at byte (l % LPL) * 16.
+  // Load instruction i of block rb covers row i of the block, every plane: lane l carries
+  // 16 bytes of plane l/LPL at byte (l % LPL) * 16 of the wave's piece.  The row address is
+  // wave-uniform (scalar), the lane part a fixed 32-bit offset.
+  static_assert(Re::PPL == NP, "one row (all planes) per load instruction");
   const int lpc = lane / Re::LPL, loff = (lane % Re::LPL) * 16;
+  const uint32_t xlane = (uint32_t)unit_base(lpc, ub, N, NP, G) * 2u + (uint32_t)loff;
   auto gaddr = [&](int rb, int i) {
-    const int pc = i * Re::PPL + lpc, r = pc / NP, p = pc % NP;
-    const int64_t row = min(rb * 16 + r, M - 1);
-    return reinterpret_cast<const unsigned char*>(X + row * ldx + unit_base(p, ub, N, NP, G)) + loff;
+    const int64_t row = min(rb * 16 + i, M - 1);
+    return reinterpret_cast<const unsigned char*>(X + row * ldx) + xlane;
   };
   auto laddr = [&](int i) {
     const int pc = i * Re::PPL + lpc, r = pc / NP, p = pc % NP;
@@ -301,9 +303,9 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
   // loop is not unrolled (unrolled, the compiler's schedule across blocks spills registers).
   auto block = [&](auto next_tag, int b) {
     constexpr bool next = decltype(next_tag)::value;
-    const int rb = min(rb0 + b, nrb - 1);
+    const int rb = __builtin_amdgcn_readfirstlane(min(rb0 + b, nrb - 1));  // wave-uniform
     const int row = min(rb * 16 + j, M - 1);
-    const int rbn = min(rb0 + b + 1, nrb - 1);
+    const int rbn = __builtin_amdgcn_readfirstlane(min(rb0 + b + 1, nrb - 1));
     // this block's slice, MFMA layout (lane (j, g): row j, columns E*g .. of each unit-plane)
     u32x4 x[UPW][NP][CPG];
 #pragma unroll
@@ -359,7 +361,7 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
       issue(0, rbn, 2);
     }
     __builtin_amdgcn_sched_barrier(0);
-    uint8_t* crow = codes + (int64_t)row * ldc;
+    uint8_t* crow = codes + (int64_t)rb * 16 * ldc + (uint32_t)(row - rb * 16) * (uint32_t)ldc;
     uint32_t qp[UPW];
 #pragma unroll
     for (int uu = 0; uu < UPW; ++uu) {
