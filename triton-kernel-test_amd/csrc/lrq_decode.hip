@@ -355,66 +355,123 @@ __global__ __launch_bounds__(NW * 64) void k_decode_staged(
 }
 
 // ------------------------------------------------------------------ row-persistent kernel
-// The plain decode (x_hat stored), about one workgroup per CU.  Same per-block arithmetic and
-// input staging as k_decode_staged; the difference is on the store side.  Each wave writes its
-// reconstructed unit (16 rows x NP planes x G columns, MFMA layout) into an LDS output tile, and
-// after the next barrier the workgroup stores the tile as whole row segments: one 16-byte
-// vector per lane, NW*G*2 contiguous bytes per row and plane.  The MFMA layout stores 4 x 16 B
-// pieces of 16 rows per instruction; on MI355X these partial-line writes, and a second
-// workgroup interleaving its own traffic on the CU, cost about a third of the decode's time.
+// Decode and the fused elementwise consumers at about one workgroup per CU.  Same per-block
+// arithmetic and input staging as k_decode_staged; the difference is the full-precision side.
+// Each wave writes its reconstructed (or consumed) unit, 16 rows x NP planes x G columns in
+// the MFMA layout, into an LDS output tile, and after the next barrier the workgroup stores the
+// tile as whole row segments: one 16-byte vector per lane, nu*G*2 contiguous bytes per row and
+// plane (nu = units of the workgroup).  A consumer's second tensor (dY) comes the opposite way:
+// whole row segments into an LDS input tile, read back in the MFMA layout.  The MFMA layout
+// moves 4 x 16 B pieces of 16 rows per instruction; on MI355X such partial-line traffic, and a
+// second workgroup interleaving its own on the CU, cost about a third of the decode's time.
 //
-// Pipeline (one barrier per row block b): write the staged codes/qparams/L of block b into
-// input slot b&1 -> barrier -> store the output tile of block b-1 (slot (b-1)&1) -> reconstruct
-// block b into output slot b&1.  A slot is rewritten two blocks later, after a barrier that
-// every wave reaches only once its reads of that slot have returned.  All input loads of the
-// workgroup's RBW blocks are issued before the first store (loads and stores share one
-// in-order counter on gfx9).  Requires units % NW == 0 (every wave active).
+// Pipeline (one barrier per row block b): write block b's staged inputs into slot b&1 ->
+// barrier -> store the output tile of block b-1 (slot (b-1)&1) -> compute block b into output
+// slot b&1.  A slot is rewritten two blocks later, after a barrier that every wave reaches only
+// once its reads of that slot have returned.  All input loads of the workgroup's RBW blocks are
+// issued before the first store (loads and stores share one in-order counter on gfx9).  Waves
+// past the last unit of the row take part in the loads, barriers and stores only.
+//
+// OUTL (rank 0, at most kSideMax outlier channels): the fp16 side columns of each block are
+// staged with the codes, and reconstructed values of outlier columns are replaced by them.
+static constexpr int kSideMax = 64;
+
 template <int BITS, int G, int NW>
 struct RowsOut {
   static constexpr int NP = 8 / BITS;
-  static constexpr int OROW = NW * G * 2;           // output bytes per row and plane
+  static constexpr int OROW = NW * G * 2;           // full-precision bytes per row and plane
   static constexpr int OPAD = OROW + 16;            // LDS row pitch (spreads the 16 rows over banks)
-  static constexpr int OSLOT = 16 * NP * OPAD;      // one block's output tile
+  static constexpr int OSLOT = 16 * NP * OPAD;      // one block's tile
   static constexpr int OCH = 16 * NP * (OROW / 16); // 16-byte chunks per tile
   static_assert(OROW % 16 == 0, "row segment of whole vectors");
 };
 
-template <int BITS, int G, int R, int NW, int RBW>
+template <int BITS, int G, int R, int NW, bool IN, bool OUTL>
+struct RowsLayout {
+  using Tl = StagedTile<BITS, G, R, NW>;
+  using Ro = RowsOut<BITS, G, NW>;
+  static constexpr int T = NW * 64;
+  static constexpr int DPT = (Ro::OCH + T - 1) / T;           // input-tile chunks per thread
+  static constexpr int SIDE = OUTL ? 16 * kSideMax * 2 : 0;    // side columns per block
+  static constexpr int SPT = OUTL ? (16 * kSideMax + T - 1) / T : 0;
+  static constexpr int ISLOT = Tl::SLOT + SIDE;                // staged inputs per block
+  static constexpr size_t FIXED = 2 * (size_t)ISLOT + (IN ? 2 : 0) * (size_t)Ro::OSLOT + 2 * (size_t)Ro::OSLOT;
+  static size_t bytes(int N) { return FIXED + (OUTL ? (size_t)(N / 32) * 4 + (size_t)N * 2 : 0); }
+  // registers a block's prefetched inputs take per lane (drives the largest RBW)
+  static constexpr int kRegsPerBlock = 4 * Tl::CPT + 2 + (IN ? 4 * DPT : 0) + SPT;
+};
+
+template <int BITS, int G, int R, int NW, int RBW, bool OUTL, class EPI>
 __global__ __launch_bounds__(NW * 64) void k_decode_rows(
     const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
     const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
-    uint16_t* __restrict__ out, int64_t ldo) {
-  using Tl = StagedTile<BITS, G, R, NW>;
-  using Ro = RowsOut<BITS, G, NW>;
-  constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, E = G / 4, T = Tl::T;
-  extern __shared__ __attribute__((aligned(16))) unsigned char sm[];  // [2][SLOT] inputs, [2][OSLOT] outputs
-  unsigned char* osm = sm + 2 * Tl::SLOT;
+    const int32_t* __restrict__ oidx, int nout, const uint16_t* __restrict__ side, int64_t ldside, EPI epi) {
+  constexpr bool IN = EPI::kIn;
+  using Lay = RowsLayout<BITS, G, R, NW, IN, OUTL>;
+  using Tl = typename Lay::Tl;
+  using Ro = typename Lay::Ro;
+  constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, E = G / 4, T = Lay::T;
+  extern __shared__ __attribute__((aligned(16))) unsigned char sm[];
+  unsigned char* ism = sm;                                   // [2][ISLOT] staged codes/qparams/L/side
+  unsigned char* dsm = sm + 2 * Lay::ISLOT;                  // [2][OSLOT] input tiles (IN)
+  unsigned char* osm = dsm + (IN ? 2 : 0) * Ro::OSLOT;       // [2][OSLOT] output tiles
+  uint32_t* colmask = reinterpret_cast<uint32_t*>(osm + 2 * Ro::OSLOT);  // OUTL: N/32 words
+  int16_t* oslot = reinterpret_cast<int16_t*>(colmask + N / 32);         // OUTL: N entries
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int j = lane & 15, g = lane >> 4;
+  const int units = N / (G * NP);
   const int u0 = blockIdx.y * NW, u = u0 + w;
+  const int nu = min(NW, units - u0);  // units present in this workgroup
+  const bool active = w < nu;
+  const int vbytes = nu * G * 2;       // valid bytes of a row segment
   const int nrb = (M + 15) / 16;
   const int rb0 = blockIdx.x * RBW;
   if (rb0 >= nrb) return;  // whole workgroup (no barrier reached)
 
+  if constexpr (OUTL) {
+    for (int i = tid; i < N / 32; i += T) colmask[i] = 0u;
+    for (int i = tid; i < N; i += T) oslot[i] = -1;
+    __syncthreads();
+    for (int k = tid; k < nout; k += T) {
+      const int c = oidx[k];
+      if (c >= 0 && c < N) {
+        atomicOr(&colmask[c >> 5], 1u << (c & 31));
+        oslot[c] = (int16_t)k;
+      }
+    }
+    // made visible by the first block's barrier
+  }
+
   u32x2 vop[NP][G / 16][RT];
   if constexpr (R > 0) {
+    if (active) {
 #pragma unroll
-    for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, u, N, NP, G), j, g, vop[p]);
+      for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, u, N, NP, G), j, g, vop[p]);
+    }
   }
 
   struct In {
     u32x4 c[Tl::CPT];
     u32x2 ql;
+    u32x4 d[IN ? Lay::DPT : 1];
+    uint32_t sd[OUTL ? Lay::SPT : 1];
   };
   const int qk = tid, lk = tid - Tl::QCH;
-  const bool has_q = qk < Tl::QCH;
+  const bool has_q = qk < Tl::QCH && (qk % (Tl::QROW / 8)) * 8 < nu * NP * 4;
   const bool has_l = R > 0 && lk >= 0 && lk < Tl::LCH;
+  // tile chunk k -> (plane, row, 16-byte column chunk)
+  auto chunk = [](int k, int& p, int& r, int& c16) {
+    c16 = k % (Ro::OROW / 16);
+    const int pr = k / (Ro::OROW / 16);
+    p = pr / 16;
+    r = pr % 16;
+  };
   auto load = [&](In& in, int rb) {
 #pragma unroll
     for (int i = 0; i < Tl::CPT; ++i) {
       const int k = tid + T * i, r = k / (Tl::CROW / 16), c16 = k % (Tl::CROW / 16);
       const int64_t row = min(rb * 16 + r, M - 1);
-      in.c[i] = ld16_stream(codes + row * ldc + (int64_t)u0 * G + c16 * 16);
+      if (c16 * 16 < nu * G) in.c[i] = ld16_stream(codes + row * ldc + (int64_t)u0 * G + c16 * 16);
     }
     if (has_q) {
       const int r = qk / (Tl::QROW / 8), c8 = qk % (Tl::QROW / 8);
@@ -425,18 +482,72 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
       const int64_t row = min(rb * 16 + r, M - 1);
       in.ql = ld8(reinterpret_cast<const uint8_t*>(Lin) + row * ldl * 2 + c8 * 8);
     }
+    if constexpr (IN) {
+#pragma unroll
+      for (int i = 0; i < Lay::DPT; ++i) {
+        const int k = tid + T * i;
+        int p, r, c16;
+        chunk(k, p, r, c16);
+        if ((Ro::OCH % T == 0 || k < Ro::OCH) && c16 * 16 < vbytes) {
+          const int64_t row = min(rb * 16 + r, M - 1);
+          in.d[i] = ld16_stream(reinterpret_cast<const unsigned char*>(epi.in_row(row) + unit_base(p, u0, N, NP, G)) +
+                                c16 * 16);
+        }
+      }
+    }
+    if constexpr (OUTL) {
+#pragma unroll
+      for (int i = 0; i < Lay::SPT; ++i) {
+        const int k = tid + T * i, r = k / kSideMax, c = k % kSideMax;
+        if (k < 16 * kSideMax && c < nout) in.sd[i] = side[min(rb * 16 + r, M - 1) * ldside + c];
+      }
+    }
   };
-  // Store the output tile of block rb from slot s: chunk k -> plane, row, 16-byte column chunk.
-  auto store_tile = [&](int rb, int s) {
-    const unsigned char* os = osm + s * Ro::OSLOT;
+  auto stage = [&](const In& in, int b) {
+    unsigned char* slot = ism + (b & 1) * Lay::ISLOT;
+#pragma unroll
+    for (int i = 0; i < Tl::CPT; ++i) {
+      const int k = tid + T * i, r = k / (Tl::CROW / 16), c16 = k % (Tl::CROW / 16);
+      if (c16 * 16 < nu * G) *reinterpret_cast<u32x4*>(slot + r * Tl::CROW + c16 * 16) = in.c[i];
+    }
+    if (has_q) {
+      const int r = qk / (Tl::QROW / 8), c8 = qk % (Tl::QROW / 8);
+      *reinterpret_cast<u32x2*>(slot + Tl::QOFF + r * Tl::QROW + c8 * 8) = in.ql;
+    } else if (has_l) {
+      const int r = lk / (Tl::LROW / 8), c8 = lk % (Tl::LROW / 8);
+      *reinterpret_cast<u32x2*>(slot + Tl::LOFF + r * Tl::LROW + c8 * 8) = in.ql;
+    }
+    if constexpr (IN) {
+      unsigned char* ds = dsm + (b & 1) * Ro::OSLOT;
+#pragma unroll
+      for (int i = 0; i < Lay::DPT; ++i) {
+        const int k = tid + T * i;
+        int p, r, c16;
+        chunk(k, p, r, c16);
+        if ((Ro::OCH % T == 0 || k < Ro::OCH) && c16 * 16 < vbytes)
+          *reinterpret_cast<u32x4*>(ds + (p * 16 + r) * Ro::OPAD + c16 * 16) = in.d[i];
+      }
+    }
+    if constexpr (OUTL) {
+      uint16_t* ss = reinterpret_cast<uint16_t*>(slot + Tl::SLOT);
+#pragma unroll
+      for (int i = 0; i < Lay::SPT; ++i) {
+        const int k = tid + T * i;
+        if (k < 16 * kSideMax && (k % kSideMax) < nout) ss[k] = (uint16_t)in.sd[i];
+      }
+    }
+  };
+  auto store_tile = [&](int rb, int b) {
+    const unsigned char* os = osm + (b & 1) * Ro::OSLOT;
 #pragma unroll
     for (int i = 0; i < (Ro::OCH + T - 1) / T; ++i) {
       const int k = tid + T * i;
-      if (Ro::OCH % T == 0 || k < Ro::OCH) {
-        const int c16 = k % (Ro::OROW / 16), pr = k / (Ro::OROW / 16), p = pr / 16, r = pr % 16;
+      int p, r, c16;
+      chunk(k, p, r, c16);
+      if ((Ro::OCH % T == 0 || k < Ro::OCH) && c16 * 16 < vbytes) {
         const int64_t row = min(rb * 16 + r, M - 1);
         const u32x4 v = *reinterpret_cast<const u32x4*>(os + (p * 16 + r) * Ro::OPAD + c16 * 16);
-        st16_stream(reinterpret_cast<unsigned char*>(out + row * ldo + unit_base(p, u0, N, NP, G)) + c16 * 16, v);
+        st16_stream(reinterpret_cast<unsigned char*>(epi.out_row(row) + unit_base(p, u0, N, NP, G)) + c16 * 16, v);
       }
     }
   };
@@ -449,99 +560,112 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
 #pragma unroll
   for (int b = 0; b < RBW; ++b) {
     const int rb = min(rb0 + b, nrb - 1);
-    unsigned char* slot = sm + (b & 1) * Tl::SLOT;
-#pragma unroll
-    for (int i = 0; i < Tl::CPT; ++i) {
-      const int k = tid + T * i, r = k / (Tl::CROW / 16), c16 = k % (Tl::CROW / 16);
-      *reinterpret_cast<u32x4*>(slot + r * Tl::CROW + c16 * 16) = in[b].c[i];
-    }
-    if (has_q) {
-      const int r = qk / (Tl::QROW / 8), c8 = qk % (Tl::QROW / 8);
-      *reinterpret_cast<u32x2*>(slot + Tl::QOFF + r * Tl::QROW + c8 * 8) = in[b].ql;
-    } else if (has_l) {
-      const int r = lk / (Tl::LROW / 8), c8 = lk % (Tl::LROW / 8);
-      *reinterpret_cast<u32x2*>(slot + Tl::LOFF + r * Tl::LROW + c8 * 8) = in[b].ql;
-    }
+    stage(in[b], b);
     lds_barrier();
-    if (b > 0) store_tile(min(rb0 + b - 1, nrb - 1), (b - 1) & 1);
-    u32x4 cb[G / 64];
+    if (b > 0) store_tile(min(rb0 + b - 1, nrb - 1), b - 1);
+    if (active) {
+      const unsigned char* slot = ism + (b & 1) * Lay::ISLOT;
+      u32x4 cb[G / 64];
 #pragma unroll
-    for (int i = 0; i < G / 64; ++i)
-      cb[i] = *reinterpret_cast<const u32x4*>(slot + j * Tl::CROW + w * G + E * g + 16 * i);
-    uint32_t qp[NP];
-    if constexpr (NP == 2) {
-      const u32x2 q = *reinterpret_cast<const u32x2*>(slot + Tl::QOFF + j * Tl::QROW + w * 8);
-      qp[0] = q[0];
-      qp[1] = q[1];
-    } else {
-      qp[0] = *reinterpret_cast<const uint32_t*>(slot + Tl::QOFF + j * Tl::QROW + w * 4);
-    }
-    u32x2 lop[RT];
-    if constexpr (R > 0) {
+      for (int i = 0; i < G / 64; ++i)
+        cb[i] = *reinterpret_cast<const u32x4*>(slot + j * Tl::CROW + w * G + E * g + 16 * i);
+      uint32_t qp[NP];
+      if constexpr (NP == 2) {
+        const u32x2 q = *reinterpret_cast<const u32x2*>(slot + Tl::QOFF + j * Tl::QROW + w * 8);
+        qp[0] = q[0];
+        qp[1] = q[1];
+      } else {
+        qp[0] = *reinterpret_cast<const uint32_t*>(slot + Tl::QOFF + j * Tl::QROW + w * 4);
+      }
+      u32x2 lop[RT];
+      if constexpr (R > 0) {
 #pragma unroll
-      for (int t = 0; t < RT; ++t)
-        lop[t] = *reinterpret_cast<const u32x2*>(slot + Tl::LOFF + j * Tl::LROW + 32 * t + 8 * g);
-    }
-    unsigned char* os = osm + (b & 1) * Ro::OSLOT;
+        for (int t = 0; t < RT; ++t)
+          lop[t] = *reinterpret_cast<const u32x2*>(slot + Tl::LOFF + j * Tl::LROW + 32 * t + 8 * g);
+      }
+      const unsigned char* ds = dsm + (b & 1) * Ro::OSLOT;
+      unsigned char* os = osm + (b & 1) * Ro::OSLOT;
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      float xh[E];
-      reconstruct_plane<BITS, G, R>(cb, qp[p], p, vop[p], lop, xh);
+      for (int p = 0; p < NP; ++p) {
+        float xh[E];
+        reconstruct_plane<BITS, G, R>(cb, qp[p], p, vop[p], lop, xh);
+        if constexpr (OUTL) {
+          const int c0 = unit_base(p, u, N, NP, G) + E * g;  // E consecutive columns in one mask word
+          const uint32_t mbits = colmask[c0 >> 5] >> (c0 & 31);
+          if (mbits != 0u) {
+            const uint16_t* ss = reinterpret_cast<const uint16_t*>(slot + Tl::SLOT) + j * kSideMax;
 #pragma unroll
-      for (int k = 0; k < E / 8; ++k)
-        *reinterpret_cast<u32x4*>(os + (p * 16 + j) * Ro::OPAD + (w * G + E * g + 8 * k) * 2) = pack8(xh + 8 * k);
+            for (int e = 0; e < E; ++e)
+              if ((mbits >> e) & 1u) xh[e] = f16_val(ss[oslot[c0 + e]]);
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < E / 8; ++k) {
+          const int off = (p * 16 + j) * Ro::OPAD + (w * G + E * g + 8 * k) * 2;
+          u32x4 dv = u32x4{0u, 0u, 0u, 0u};
+          if constexpr (IN) dv = *reinterpret_cast<const u32x4*>(ds + off);
+          *reinterpret_cast<u32x4*>(os + off) = epi.apply(xh + 8 * k, dv);
+        }
+      }
     }
   }
   lds_barrier();
-  store_tile(min(rb0 + RBW - 1, nrb - 1), (RBW - 1) & 1);
+  store_tile(min(rb0 + RBW - 1, nrb - 1), RBW - 1);
 }
 
 // ------------------------------------------------------------------ host side
-// Waves per workgroup for k_decode_rows: NW * G = 512 columns, so each output row segment is 1 KB
-// (one 16-byte vector per lane) and two tiles plus two input slots fit in LDS.
+// Waves per workgroup for k_decode_rows: NW * G = 512 columns, so each row segment is 1 KB (one
+// 16-byte vector per lane) and the tiles plus two input slots fit in LDS.
 template <int G>
 constexpr int rows_nw() { return 512 / G; }
 
-template <int BITS, int G, int R, int RBW>
-static int decode_rows_launch_rbw(const lrq_tensors* t, hipStream_t s, uint16_t* out, int64_t ldo) {
+template <int BITS, int G, int R, int RBW, bool OUTL, class EPI>
+static int decode_rows_launch_rbw(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
   constexpr int NW = rows_nw<G>();
+  using Lay = RowsLayout<BITS, G, R, NW, EPI::kIn, OUTL>;
   const int M = (int)t->rows, N = (int)t->hidden;
   const int units = N / (G * (8 / BITS));
   const int nrb = (M + 15) / 16;
-  const size_t shm = 2 * (size_t)StagedTile<BITS, G, R, NW>::SLOT + 2 * (size_t)RowsOut<BITS, G, NW>::OSLOT;
-  auto kern = k_decode_rows<BITS, G, R, NW, RBW>;
+  const size_t shm = Lay::bytes(N);
+  if (shm > 160 * 1024) return LRQ_ERR_UNSUPPORTED;
+  auto kern = k_decode_rows<BITS, G, R, NW, RBW, OUTL, EPI>;
   if (shm > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-  hipLaunchKernelGGL(kern, dim3((nrb + RBW - 1) / RBW, units / NW), dim3(NW * 64), shm, s, (const uint8_t*)t->codes,
-                     t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp, (const uint16_t*)t->L, t->ld_L,
-                     (const uint16_t*)t->V, M, N, out, ldo);
+  hipLaunchKernelGGL(kern, dim3((nrb + RBW - 1) / RBW, (units + NW - 1) / NW), dim3(NW * 64), shm, s,
+                     (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
+                     (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, t->outlier_idx, (int)t->n_outlier,
+                     (const uint16_t*)t->side, t->ld_side, epi);
   return launch_status();
 }
 
 // Row blocks per workgroup: the choice that minimises (workgroup rounds) x (blocks + 2), where
-// a round is one workgroup per CU (the LDS tile keeps it at one) and the 2 stands for the
-// per-workgroup fixed cost (V operands, pipeline fill).
-template <int BITS, int G, int R>
-static int decode_rows_launch(const lrq_tensors* t, hipStream_t s, uint16_t* out, int64_t ldo) {
+// a round is one workgroup per CU (the LDS tiles keep it at one) and the 2 stands for the
+// per-workgroup fixed cost (V operands, pipeline fill).  Every block's inputs are held in
+// registers until it is staged, which bounds the blocks per workgroup.
+template <int BITS, int G, int R, bool OUTL, class EPI>
+static int decode_rows_launch(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
   constexpr int NW = rows_nw<G>();
-  const int64_t ug = t->hidden / (G * (8 / BITS)) / NW, nrb = (t->rows + 15) / 16, cus = cu_count();
-  // 16 blocks of G = 128 codes with a rank term exceed the register budget (spills)
-  constexpr int kMax = (G == 128 && R > 0) ? 12 : 16;
-  const int cand[] = {16, 12, 8, 4, 2, 1};
+  using Lay = RowsLayout<BITS, G, R, NW, EPI::kIn, OUTL>;
+  constexpr int kBudget = R == 32 ? 160 : 180;  // VGPRs for prefetched inputs (rank 32: larger V operands)
+  constexpr int kMax = kBudget / Lay::kRegsPerBlock >= 16 ? 16
+                       : kBudget / Lay::kRegsPerBlock >= 12 ? 12
+                       : kBudget / Lay::kRegsPerBlock >= 8 ? 8
+                       : kBudget / Lay::kRegsPerBlock >= 4 ? 4 : 2;
+  const int64_t ug = (t->hidden / (G * (8 / BITS)) + NW - 1) / NW, nrb = (t->rows + 15) / 16, cus = cu_count();
   int best = 1;
   int64_t best_cost = INT64_MAX;
-  for (int rbw : cand) {
+  for (int rbw : {16, 12, 8, 4, 2, 1}) {
     if (rbw > kMax) continue;
     const int64_t wgs = ((nrb + rbw - 1) / rbw) * ug;
     const int64_t cost = ((wgs + cus - 1) / cus) * (rbw + 2);
     if (cost < best_cost) best_cost = cost, best = rbw;
   }
   switch (best) {
-    case 16: return decode_rows_launch_rbw<BITS, G, R, kMax>(t, s, out, ldo);
-    case 12: return decode_rows_launch_rbw<BITS, G, R, 12>(t, s, out, ldo);
-    case 8: return decode_rows_launch_rbw<BITS, G, R, 8>(t, s, out, ldo);
-    case 4: return decode_rows_launch_rbw<BITS, G, R, 4>(t, s, out, ldo);
-    case 2: return decode_rows_launch_rbw<BITS, G, R, 2>(t, s, out, ldo);
-    default: return decode_rows_launch_rbw<BITS, G, R, 1>(t, s, out, ldo);
+    case 16: return decode_rows_launch_rbw<BITS, G, R, (kMax >= 16 ? 16 : 1), OUTL>(t, s, epi);
+    case 12: return decode_rows_launch_rbw<BITS, G, R, (kMax >= 12 ? 12 : 1), OUTL>(t, s, epi);
+    case 8: return decode_rows_launch_rbw<BITS, G, R, (kMax >= 8 ? 8 : 1), OUTL>(t, s, epi);
+    case 4: return decode_rows_launch_rbw<BITS, G, R, 4, OUTL>(t, s, epi);
+    case 2: return decode_rows_launch_rbw<BITS, G, R, 2, OUTL>(t, s, epi);
+    default: return decode_rows_launch_rbw<BITS, G, R, 1, OUTL>(t, s, epi);
   }
 }
 
@@ -572,9 +696,13 @@ static int decode_launch_rbw(const lrq_tensors* t, hipStream_t s, const EPI& epi
 template <int BITS, int G, int R, class EPI>
 static int decode_launch(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
   constexpr int NP = 8 / BITS, NW = 8, BIG = EPI::kIn ? 4 : 8;
-  if constexpr (std::is_same_v<EPI, EpiStore>) {
-    if (t->n_outlier == 0 && (t->hidden / (G * NP)) % rows_nw<G>() == 0)
-      return decode_rows_launch<BITS, G, R>(t, s, epi.out, epi.ld);
+  // Consumers of G = 128 groups keep the two-workgroups-per-CU kernels: at NW = 4 the row kernel
+  // would run four waves per CU.
+  if constexpr (!(EPI::kIn && G == 128)) {
+    if (t->n_outlier == 0) return decode_rows_launch<BITS, G, R, false>(t, s, epi);
+    if constexpr (R == 0) {
+      if (t->n_outlier <= kSideMax) return decode_rows_launch<BITS, G, R, true>(t, s, epi);
+    }
   }
   const int64_t units = t->hidden / (G * NP), nrb = (t->rows + 15) / 16;
   const int64_t wgs = ((nrb + BIG - 1) / BIG) * ((units + NW - 1) / NW);
