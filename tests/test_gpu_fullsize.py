@@ -18,13 +18,7 @@ import torch
 import oracle as O
 from parity import assert_codes, bits16, f16
 
-pytestmark = [
-    pytest.mark.gpu,
-    pytest.mark.skip(reason="these checks were in the first GPU run of an encode variant that "
-                            "staged X through direct global-to-LDS loads; that run faulted the GPU "
-                            "before any test reported, and no cause has been shown. The variant "
-                            "is removed; these tests stay off the GPU until the fault is explained."),
-]
+pytestmark = pytest.mark.gpu
 
 
 def _codes_unpacked(c):
@@ -63,10 +57,15 @@ def test_fullsize_roundtrip_properties(pkg, dev, name):
     frac_ok = float((err <= bound).float().mean())
     print(f"[full {name}] within half-step: {frac_ok:.7f}", flush=True)
     assert frac_ok >= 1 - 1e-6
-    # decode error relative to the input stays at the quantiser's level
+    # decode error relative to the input stays at the quantiser's level: every element of
+    # x_hat - x is within half its group's step (plus the bf16 rounding of x_hat, and of the
+    # rotation for the rotated format), so the relative L2 error is bounded by those steps
     rel = float((xh.float() - x.float()).norm() / x.float().norm())
-    print(f"[full {name}] round-trip rel-L2 {rel:.4f}", flush=True)
-    assert rel < 0.1
+    half = (0.5 * step * (1 + 2e-3)).expand(-1, -1, G).reshape(cfg.rows, -1)
+    slack = x.float().abs() * 2.0 ** -7 + 1e-6
+    rel_bound = float((half + slack).norm() / x.float().norm())
+    print(f"[full {name}] round-trip rel-L2 {rel:.4f} (bound {rel_bound:.4f})", flush=True)
+    assert rel <= rel_bound
     # re-encode the decoded activation: same codes up to ties
     c2 = pkg.encode(xh, V.to(dev), bits=cfg.bits, group_size=cfg.group, hadamard=cfg.hadamard)
     same = float((c2.codes == c.codes).float().mean())
