@@ -212,14 +212,14 @@ struct RowsEnc {
   static_assert(LDS <= 160 * 1024, "LDS budget");
 };
 
-template <int BITS, int G, int R, int NW, int UPW, int RBW>
+template <int BITS, int G, int R, int NW, int UPW>
 __global__ __launch_bounds__(NW * 64) void k_encode_rows(
     const uint16_t* __restrict__ X, int64_t ldx, int M, int N, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ Lout, int64_t ldl, uint8_t* __restrict__ codes, int64_t ldc,
-    uint16_t* __restrict__ qparams, int64_t ldq) {
+    uint16_t* __restrict__ qparams, int64_t ldq, int RBW) {
   using Re = RowsEnc<BITS, G, R, NW, UPW>;
   constexpr int NP = Re::NP, CPG = G / 32, RT = Re::RT, E = G / 4;
-  static_assert(NP == 2 && UPW == 4, "the qparams gather below is written for 4 units x 2 planes");
+  static_assert(NP == 2 && (UPW == 2 || UPW == 4), "the qparams gather below is written for 2 planes x 2 or 4 units");
   extern __shared__ __attribute__((aligned(16))) unsigned char shm[];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
@@ -227,24 +227,32 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
   f32x4* part = reinterpret_cast<f32x4*>(shm + (size_t)NW * Re::REGION);  // [2][NW][RT][64]
   const int nrb = (M + 15) / 16;
   const int rb0 = blockIdx.x * RBW;
+  if (rb0 >= nrb) return;  // whole workgroup (no barrier reached)
+  const int nblk = min(RBW, nrb - rb0);
   const int ub = w * UPW;  // first unit of this wave
 
   u32x2 vop[UPW][NP][G / 16][RT];
   const u32x2 ident = identity_bop(j, g);
 
-  // Load instruction i of block rb covers row i of the block, every plane: lane l carries
-  // 16 bytes of plane l/LPL at byte (l % LPL) * 16 of the wave's piece.  The row address is
-  // wave-uniform (scalar), the lane part a fixed 32-bit offset.
-  static_assert(Re::PPL == NP, "one row (all planes) per load instruction");
+  // Load instruction i of block rb covers rows RPL*i .. RPL*i + RPL-1 of the block (RPL = PPL/NP
+  // rows), every plane: lane l carries 16 bytes of piece i*PPL + l/LPL (row RPL*i + (l/LPL)/NP,
+  // plane (l/LPL)%NP) at byte (l % LPL) * 16 of the wave's piece.  The first row's address is
+  // wave-uniform (scalar); the lane part is a fixed 32-bit offset.  Rows past the end are
+  // clamped to the last row, which only the last block can reach.
+  static_assert(Re::PPL % NP == 0, "whole rows per load instruction");
+  constexpr int RPL = Re::PPL / NP;
   const int lpc = lane / Re::LPL, loff = (lane % Re::LPL) * 16;
-  const uint32_t xlane = (uint32_t)unit_base(lpc, ub, N, NP, G) * 2u + (uint32_t)loff;
+  const int lrow = lpc / NP;  // row within the instruction's RPL rows
+  const uint32_t xlane = (uint32_t)unit_base(lpc % NP, ub, N, NP, G) * 2u + (uint32_t)loff;
   auto gaddr = [&](int rb, int i) {
-    const int64_t row = min(rb * 16 + i, M - 1);
+    const int64_t r0 = rb * 16 + RPL * i;
+    if (r0 + RPL <= M)  // every row of the instruction present (all but possibly the last block)
+      return reinterpret_cast<const unsigned char*>(X + r0 * ldx) + (uint32_t)(lrow * ldx * 2) + xlane;
+    const int64_t row = min(r0 + lrow, (int64_t)M - 1);
     return reinterpret_cast<const unsigned char*>(X + row * ldx) + xlane;
   };
   auto laddr = [&](int i) {
-    const int pc = i * Re::PPL + lpc, r = pc / NP, p = pc % NP;
-    return region + r * Re::PITCH + p * Re::PIECE + loff;
+    return region + (RPL * i + lrow) * Re::PITCH + (lpc % NP) * Re::PIECE + loff;
   };
   u32x4 pf[2][Re::RL];
   auto issue = [&](int buf, int rb, int round) {
@@ -373,16 +381,26 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // qparams of the wave's 4 units as one 16-byte store per row half: lanes 0..31 hold the
-    // plane-0 pairs, lanes 32..63 the plane-1 pairs; two half-swaps interleave them.
+    // qparams of the wave's units as 16-byte stores per row: lanes 0..31 hold the plane-0
+    // pairs, lanes 32..63 the plane-1 pairs, and the row's memory order is (unit, plane).
+    // Four units: two half-swaps leave units 0-1 in the low lanes and units 2-3 in the high
+    // lanes.  Two units: the half-swaps pair each plane-0 value with its plane-1 partner in the
+    // low lanes, which store.
     {
-      float a = __uint_as_float(qp[0]), bq = __uint_as_float(qp[2]);
-      float c = __uint_as_float(qp[1]), d = __uint_as_float(qp[3]);
+      float a, bq, c, d;
+      if constexpr (UPW == 4) {
+        a = __uint_as_float(qp[0]), bq = __uint_as_float(qp[2]);
+        c = __uint_as_float(qp[1]), d = __uint_as_float(qp[3]);
+      } else {
+        a = bq = __uint_as_float(qp[0]);
+        c = d = __uint_as_float(qp[1]);
+      }
       swap32(a, bq);
       swap32(c, d);
       const u32x4 v = u32x4{__float_as_uint(a), __float_as_uint(bq), __float_as_uint(c), __float_as_uint(d)};
+      const bool keep = UPW == 4 ? (g & 1) == 0 : g == 0;
       st16_pred(qparams + (int64_t)rb * 16 * ldq, (uint32_t)(16 * ldq * 2),
-                (uint32_t)(((row - rb * 16) * ldq + ub * NP * 2) * 2 + (g >> 1) * 16), v, (g & 1) == 0);
+                (uint32_t)(((row - rb * 16) * ldq + ub * NP * 2) * 2 + (g >> 1) * 16), v, keep);
     }
 #pragma unroll
     for (int t = 0; t < RT; ++t)
@@ -396,8 +414,8 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
     __builtin_amdgcn_sched_barrier(0);
   };
 #pragma unroll 1
-  for (int b = 0; b < RBW - 1; ++b) block(std::true_type{}, b);
-  block(std::false_type{}, RBW - 1);
+  for (int b = 0; b < nblk - 1; ++b) block(std::true_type{}, b);
+  block(std::false_type{}, nblk - 1);
 }
 
 // -------------------------------------------------------------------------------------
@@ -547,39 +565,20 @@ static int launch_persist(const lrq_tensors* t, const void* x, int64_t ldx, hipS
   return launch_persist_rbw<BITS, G, R, NW, UPW, DB, 1>(t, x, ldx, s);
 }
 
-template <int BITS, int G, int R, int RBW>
-static int launch_rows_rbw(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s) {
-  constexpr int NW = 8, UPW = 4;
-  using Re = RowsEnc<BITS, G, R, NW, UPW>;
-  auto kern = k_encode_rows<BITS, G, R, NW, UPW, RBW>;
-  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)Re::LDS);
-  const int nrb = (int)((t->rows + 15) / 16);
-  hipLaunchKernelGGL(kern, dim3((nrb + RBW - 1) / RBW), dim3(NW * 64), Re::LDS, s, (const uint16_t*)x, ldx,
-                     (int)t->rows, (int)t->hidden, (const uint16_t*)t->V, (uint16_t*)t->L, t->ld_L,
-                     (uint8_t*)t->codes, t->ld_codes, (uint16_t*)t->qparams, t->ld_qp);
-  return launch_status();
-}
-
-// Row blocks per workgroup for k_encode_rows (one workgroup per CU): the choice minimising
-// (workgroup rounds) x (2 * blocks + 3), the 3 standing for the per-workgroup V operands and
-// the first block's unoverlapped load.
-template <int BITS, int G, int R>
+// k_encode_rows: one workgroup per CU, each walking ceil(row blocks / CUs) consecutive blocks.
+template <int BITS, int G, int R, int UPW>
 static int launch_rows(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s) {
+  constexpr int NW = 8;
+  using Re = RowsEnc<BITS, G, R, NW, UPW>;
+  auto kern = k_encode_rows<BITS, G, R, NW, UPW>;
+  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)Re::LDS);
   const int64_t nrb = (t->rows + 15) / 16, cus = cu_count();
-  int best = 1;
-  int64_t best_cost = INT64_MAX;
-  // (2 is not offered: its one-iteration block loop is folded and the two blocks' schedules
-  // merge into a spilling one)
-  for (int rbw : {8, 4, 1}) {
-    const int64_t wgs = (nrb + rbw - 1) / rbw;
-    const int64_t cost = ((wgs + cus - 1) / cus) * (2 * rbw + 3);
-    if (cost < best_cost) best_cost = cost, best = rbw;
-  }
-  switch (best) {
-    case 8: return launch_rows_rbw<BITS, G, R, 8>(t, x, ldx, s);
-    case 4: return launch_rows_rbw<BITS, G, R, 4>(t, x, ldx, s);
-    default: return launch_rows_rbw<BITS, G, R, 1>(t, x, ldx, s);
-  }
+  const int rbw = (int)((nrb + cus - 1) / cus);
+  const int64_t wgs = (nrb + rbw - 1) / rbw;
+  hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(NW * 64), Re::LDS, s, (const uint16_t*)x, ldx, (int)t->rows,
+                     (int)t->hidden, (const uint16_t*)t->V, (uint16_t*)t->L, t->ld_L, (uint8_t*)t->codes,
+                     t->ld_codes, (uint16_t*)t->qparams, t->ld_qp, rbw);
+  return launch_status();
 }
 
 // Returns 1 and launches when a single-pass kernel exists for this shape, else 0.
@@ -595,12 +594,21 @@ static int encode_persist_dispatch(const lrq_tensors* t, const void* x, int64_t 
     const int64_t units = t->hidden / ((int64_t)G * NP);
     switch (units) {
       case 8: *status = launch_persist<BITS, G, R, 4, 2, true>(t, x, ldx, s); return 1;
-      case 16: *status = launch_persist<BITS, G, R, 8, 2, true>(t, x, ldx, s); return 1;
-      case 32:
-        // row-staged kernel (4 units x 2 planes per wave; 16-byte qparams stores per row)
+      case 16:
+        // row-staged kernel (8 waves x 2 units; 16-byte qparams stores per row)
         if constexpr (BITS == 4 && G == 64) {
           if (t->ld_qp % 8 == 0 && aligned(t->qparams, 16)) {
-            *status = launch_rows<BITS, G, R>(t, x, ldx, s);
+            *status = launch_rows<BITS, G, R, 2>(t, x, ldx, s);
+            return 1;
+          }
+        }
+        *status = launch_persist<BITS, G, R, 8, 2, true>(t, x, ldx, s);
+        return 1;
+      case 32:
+        // row-staged kernel (8 waves x 4 units)
+        if constexpr (BITS == 4 && G == 64) {
+          if (t->ld_qp % 8 == 0 && aligned(t->qparams, 16)) {
+            *status = launch_rows<BITS, G, R, 4>(t, x, ldx, s);
             return 1;
           }
         }
