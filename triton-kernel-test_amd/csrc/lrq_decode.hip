@@ -13,6 +13,7 @@
 #include "lrq_dequant.h"
 #include "lrq_math.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace lrq {
@@ -29,6 +30,8 @@ struct EpiStore {
   int64_t ld;
   __device__ __forceinline__ const uint16_t* in_row(int64_t) const { return nullptr; }
   __device__ __forceinline__ uint16_t* out_row(int64_t r) const { return out + r * ld; }
+  __host__ __device__ __forceinline__ int64_t in_ld() const { return 0; }
+  __host__ __device__ __forceinline__ int64_t out_ld() const { return ld; }
   __device__ __forceinline__ u32x4 apply(const float* xh, u32x4) const { return pack8(xh); }
 };
 
@@ -41,6 +44,8 @@ struct EpiSilu {
   int64_t lddx;
   __device__ __forceinline__ const uint16_t* in_row(int64_t r) const { return dy + r * lddy; }
   __device__ __forceinline__ uint16_t* out_row(int64_t r) const { return dx + r * lddx; }
+  __host__ __device__ __forceinline__ int64_t in_ld() const { return lddy; }
+  __host__ __device__ __forceinline__ int64_t out_ld() const { return lddx; }
   __device__ __forceinline__ u32x4 apply(const float* xh, u32x4 dyv) const {
     float d[8], o[8];
     unpack8(dyv, d);
@@ -59,6 +64,8 @@ struct EpiGelu {
   int64_t lddx;
   __device__ __forceinline__ const uint16_t* in_row(int64_t r) const { return dy + r * lddy; }
   __device__ __forceinline__ uint16_t* out_row(int64_t r) const { return dx + r * lddx; }
+  __host__ __device__ __forceinline__ int64_t in_ld() const { return lddy; }
+  __host__ __device__ __forceinline__ int64_t out_ld() const { return lddx; }
   __device__ __forceinline__ u32x4 apply(const float* xh, u32x4 dyv) const {
     float d[8], o[8];
     unpack8(dyv, d);
@@ -77,6 +84,8 @@ struct EpiMul {
   int64_t ldo;
   __device__ __forceinline__ const uint16_t* in_row(int64_t r) const { return y + r * ldy; }
   __device__ __forceinline__ uint16_t* out_row(int64_t r) const { return out + r * ldo; }
+  __host__ __device__ __forceinline__ int64_t in_ld() const { return ldy; }
+  __host__ __device__ __forceinline__ int64_t out_ld() const { return ldo; }
   __device__ __forceinline__ u32x4 apply(const float* xh, u32x4 yv) const {
     float a[8], o[8];
     unpack8(yv, a);
@@ -401,11 +410,12 @@ struct RowsLayout {
   static constexpr int kRegsPerBlock = 4 * Tl::CPT + 2 + (IN ? 4 * DPT : 0) + SPT;
 };
 
-template <int BITS, int G, int R, int NW, int RBW, bool OUTL, class EPI>
+template <int BITS, int G, int R, int NW, int PD, bool OUTL, class EPI>
 __global__ __launch_bounds__(NW * 64) void k_decode_rows(
     const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
     const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
-    const int32_t* __restrict__ oidx, int nout, const uint16_t* __restrict__ side, int64_t ldside, EPI epi) {
+    const int32_t* __restrict__ oidx, int nout, const uint16_t* __restrict__ side, int64_t ldside, EPI epi,
+    int RBW) {
   constexpr bool IN = EPI::kIn;
   using Lay = RowsLayout<BITS, G, R, NW, IN, OUTL>;
   using Tl = typename Lay::Tl;
@@ -427,6 +437,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
   const int nrb = (M + 15) / 16;
   const int rb0 = blockIdx.x * RBW;
   if (rb0 >= nrb) return;  // whole workgroup (no barrier reached)
+  const int nblk = min(RBW, nrb - rb0);
 
   if constexpr (OUTL) {
     for (int i = tid; i < N / 32; i += T) colmask[i] = 0u;
@@ -466,33 +477,39 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
     p = pr / 16;
     r = pr % 16;
   };
+  // Addresses: a chunk's column bytes are fixed per thread; its row enters as
+  // min(r, last row of the matrix - first row of the block) times the row stride, added to the
+  // wave-uniform base of the block (rows past the end repeat the last row).
+  const uint32_t ccol = (uint32_t)u0 * G;
+  const int64_t ldc_b = ldc, ldq_b = ldq * 2, ldl_b = ldl * 2;
+  const int64_t ldi_b = epi.in_ld() * 2, ldo_b = epi.out_ld() * 2;
+  auto rowclamp = [&](int rb, int r) { return (uint32_t)min(r, M - 1 - rb * 16); };
   auto load = [&](In& in, int rb) {
+    const unsigned char* cb0 = codes + (int64_t)rb * 16 * ldc_b;
 #pragma unroll
     for (int i = 0; i < Tl::CPT; ++i) {
       const int k = tid + T * i, r = k / (Tl::CROW / 16), c16 = k % (Tl::CROW / 16);
-      const int64_t row = min(rb * 16 + r, M - 1);
-      if (c16 * 16 < nu * G) in.c[i] = ld16_stream(codes + row * ldc + (int64_t)u0 * G + c16 * 16);
+      if (c16 * 16 < nu * G) in.c[i] = ld16_stream(cb0 + rowclamp(rb, r) * (uint32_t)ldc_b + ccol + c16 * 16);
     }
     if (has_q) {
       const int r = qk / (Tl::QROW / 8), c8 = qk % (Tl::QROW / 8);
-      const int64_t row = min(rb * 16 + r, M - 1);
-      in.ql = ld8(reinterpret_cast<const uint8_t*>(qparams) + (row * ldq + (int64_t)u0 * NP * 2) * 2 + c8 * 8);
+      const unsigned char* qb0 = reinterpret_cast<const unsigned char*>(qparams) + (int64_t)rb * 16 * ldq_b;
+      in.ql = ld8(qb0 + rowclamp(rb, r) * (uint32_t)ldq_b + (uint32_t)u0 * NP * 4 + c8 * 8);
     } else if (has_l) {
       const int r = lk / (Tl::LROW / 8), c8 = lk % (Tl::LROW / 8);
-      const int64_t row = min(rb * 16 + r, M - 1);
-      in.ql = ld8(reinterpret_cast<const uint8_t*>(Lin) + row * ldl * 2 + c8 * 8);
+      const unsigned char* lb0 = reinterpret_cast<const unsigned char*>(Lin) + (int64_t)rb * 16 * ldl_b;
+      in.ql = ld8(lb0 + rowclamp(rb, r) * (uint32_t)ldl_b + c8 * 8);
     }
     if constexpr (IN) {
+      const unsigned char* ib0 = reinterpret_cast<const unsigned char*>(epi.in_row((int64_t)rb * 16));
 #pragma unroll
       for (int i = 0; i < Lay::DPT; ++i) {
         const int k = tid + T * i;
         int p, r, c16;
         chunk(k, p, r, c16);
-        if ((Ro::OCH % T == 0 || k < Ro::OCH) && c16 * 16 < vbytes) {
-          const int64_t row = min(rb * 16 + r, M - 1);
-          in.d[i] = ld16_stream(reinterpret_cast<const unsigned char*>(epi.in_row(row) + unit_base(p, u0, N, NP, G)) +
+        if ((Ro::OCH % T == 0 || k < Ro::OCH) && c16 * 16 < vbytes)
+          in.d[i] = ld16_stream(ib0 + rowclamp(rb, r) * (uint32_t)ldi_b + (uint32_t)unit_base(p, u0, N, NP, G) * 2 +
                                 c16 * 16);
-        }
       }
     }
     if constexpr (OUTL) {
@@ -539,30 +556,44 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
   };
   auto store_tile = [&](int rb, int b) {
     const unsigned char* os = osm + (b & 1) * Ro::OSLOT;
+    unsigned char* ob0 = reinterpret_cast<unsigned char*>(epi.out_row((int64_t)rb * 16));
 #pragma unroll
     for (int i = 0; i < (Ro::OCH + T - 1) / T; ++i) {
       const int k = tid + T * i;
       int p, r, c16;
       chunk(k, p, r, c16);
       if ((Ro::OCH % T == 0 || k < Ro::OCH) && c16 * 16 < vbytes) {
-        const int64_t row = min(rb * 16 + r, M - 1);
         const u32x4 v = *reinterpret_cast<const u32x4*>(os + (p * 16 + r) * Ro::OPAD + c16 * 16);
-        st16_stream(reinterpret_cast<unsigned char*>(epi.out_row(row) + unit_base(p, u0, N, NP, G)) + c16 * 16, v);
+        st16_stream(ob0 + rowclamp(rb, r) * (uint32_t)ldo_b + (uint32_t)unit_base(p, u0, N, NP, G) * 2 + c16 * 16, v);
       }
     }
   };
 
-  In in[RBW];
+  // Ring of PD prefetched blocks.  Block b + PD is requested right after block b - 1's
+  // stores (a store queued behind loads waits for them), so each iteration's traffic is
+  // [stores of b - 1, loads of b + PD].  With PD >= the workgroup's blocks every load is issued
+  // before the first store.
+  In in[PD];
 #pragma unroll
-  for (int b = 0; b < RBW; ++b) load(in[b], min(rb0 + b, nrb - 1));
+  for (int b = 0; b < PD; ++b)
+    if (b < nblk) load(in[b], rb0 + b);
   __builtin_amdgcn_sched_barrier(0);
 
+#pragma unroll 1
+  for (int bb = 0; bb < nblk; bb += PD) {
 #pragma unroll
-  for (int b = 0; b < RBW; ++b) {
-    const int rb = min(rb0 + b, nrb - 1);
-    stage(in[b], b);
+  for (int k = 0; k < PD; ++k) {
+    const int b = bb + k;
+    if (b >= nblk) break;
+    const int rb = rb0 + b;
+    stage(in[k], b);
     lds_barrier();
-    if (b > 0) store_tile(min(rb0 + b - 1, nrb - 1), b - 1);
+    if (b > 0) store_tile(rb - 1, b - 1);
+    if (b + PD < nblk) {
+      __builtin_amdgcn_sched_barrier(0);
+      load(in[k], rb + PD);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     if (active) {
       const unsigned char* slot = ism + (b & 1) * Lay::ISLOT;
       u32x4 cb[G / 64];
@@ -600,17 +631,18 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
           }
         }
 #pragma unroll
-        for (int k = 0; k < E / 8; ++k) {
-          const int off = (p * 16 + j) * Ro::OPAD + (w * G + E * g + 8 * k) * 2;
+        for (int kk = 0; kk < E / 8; ++kk) {
+          const int off = (p * 16 + j) * Ro::OPAD + (w * G + E * g + 8 * kk) * 2;
           u32x4 dv = u32x4{0u, 0u, 0u, 0u};
           if constexpr (IN) dv = *reinterpret_cast<const u32x4*>(ds + off);
-          *reinterpret_cast<u32x4*>(os + off) = epi.apply(xh + 8 * k, dv);
+          *reinterpret_cast<u32x4*>(os + off) = epi.apply(xh + 8 * kk, dv);
         }
       }
     }
   }
+  }
   lds_barrier();
-  store_tile(min(rb0 + RBW - 1, nrb - 1), RBW - 1);
+  store_tile(rb0 + nblk - 1, nblk - 1);
 }
 
 // ------------------------------------------------------------------ host side
@@ -619,54 +651,32 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
 template <int G>
 constexpr int rows_nw() { return 512 / G; }
 
-template <int BITS, int G, int R, int RBW, bool OUTL, class EPI>
-static int decode_rows_launch_rbw(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
-  constexpr int NW = rows_nw<G>();
-  using Lay = RowsLayout<BITS, G, R, NW, EPI::kIn, OUTL>;
-  const int M = (int)t->rows, N = (int)t->hidden;
-  const int units = N / (G * (8 / BITS));
-  const int nrb = (M + 15) / 16;
-  const size_t shm = Lay::bytes(N);
-  if (shm > 160 * 1024) return LRQ_ERR_UNSUPPORTED;
-  auto kern = k_decode_rows<BITS, G, R, NW, RBW, OUTL, EPI>;
-  if (shm > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-  hipLaunchKernelGGL(kern, dim3((nrb + RBW - 1) / RBW, (units + NW - 1) / NW), dim3(NW * 64), shm, s,
-                     (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
-                     (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, t->outlier_idx, (int)t->n_outlier,
-                     (const uint16_t*)t->side, t->ld_side, epi);
-  return launch_status();
-}
-
-// Row blocks per workgroup: the choice that minimises (workgroup rounds) x (blocks + 2), where
-// a round is one workgroup per CU (the LDS tiles keep it at one) and the 2 stands for the
-// per-workgroup fixed cost (V operands, pipeline fill).  Every block's inputs are held in
-// registers until it is staged, which bounds the blocks per workgroup.
+// One workgroup per CU: the workgroups of a unit group split its row blocks into runs of RBW
+// consecutive blocks, RBW being the smallest run that keeps the grid within one round.  The ring
+// holds up to 16 blocks of staged inputs within a register budget of about 180 VGPRs (rank 32:
+// 160, its V operands are twice as large; consumers: 100, their epilogue and the streamed loop
+// need the rest).
 template <int BITS, int G, int R, bool OUTL, class EPI>
 static int decode_rows_launch(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
   constexpr int NW = rows_nw<G>();
   using Lay = RowsLayout<BITS, G, R, NW, EPI::kIn, OUTL>;
-  constexpr int kBudget = R == 32 ? 160 : 180;  // VGPRs for prefetched inputs (rank 32: larger V operands)
-  constexpr int kMax = kBudget / Lay::kRegsPerBlock >= 16 ? 16
-                       : kBudget / Lay::kRegsPerBlock >= 12 ? 12
-                       : kBudget / Lay::kRegsPerBlock >= 8 ? 8
-                       : kBudget / Lay::kRegsPerBlock >= 4 ? 4 : 2;
-  const int64_t ug = (t->hidden / (G * (8 / BITS)) + NW - 1) / NW, nrb = (t->rows + 15) / 16, cus = cu_count();
-  int best = 1;
-  int64_t best_cost = INT64_MAX;
-  for (int rbw : {16, 12, 8, 4, 2, 1}) {
-    if (rbw > kMax) continue;
-    const int64_t wgs = ((nrb + rbw - 1) / rbw) * ug;
-    const int64_t cost = ((wgs + cus - 1) / cus) * (rbw + 2);
-    if (cost < best_cost) best_cost = cost, best = rbw;
-  }
-  switch (best) {
-    case 16: return decode_rows_launch_rbw<BITS, G, R, (kMax >= 16 ? 16 : 1), OUTL>(t, s, epi);
-    case 12: return decode_rows_launch_rbw<BITS, G, R, (kMax >= 12 ? 12 : 1), OUTL>(t, s, epi);
-    case 8: return decode_rows_launch_rbw<BITS, G, R, (kMax >= 8 ? 8 : 1), OUTL>(t, s, epi);
-    case 4: return decode_rows_launch_rbw<BITS, G, R, 4, OUTL>(t, s, epi);
-    case 2: return decode_rows_launch_rbw<BITS, G, R, 2, OUTL>(t, s, epi);
-    default: return decode_rows_launch_rbw<BITS, G, R, 1, OUTL>(t, s, epi);
-  }
+  constexpr int kBudget = EPI::kIn ? 100 : R == 32 ? 160 : 180;
+  constexpr int kFit = kBudget / Lay::kRegsPerBlock;
+  constexpr int PD = kFit >= 16 ? 16 : kFit >= 8 ? 8 : kFit >= 4 ? 4 : 2;
+  const int M = (int)t->rows, N = (int)t->hidden;
+  const int units = N / (G * (8 / BITS));
+  const int64_t ug = (units + NW - 1) / NW, nrb = (M + 15) / 16, cus = cu_count();
+  const int64_t per = std::max<int64_t>(1, cus / ug);  // workgroups per unit group
+  const int rbw = (int)((nrb + per - 1) / per);
+  const size_t shm = Lay::bytes(N);
+  if (shm > 160 * 1024) return LRQ_ERR_UNSUPPORTED;
+  auto kern = k_decode_rows<BITS, G, R, NW, PD, OUTL, EPI>;
+  if (shm > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+  hipLaunchKernelGGL(kern, dim3((unsigned)((nrb + rbw - 1) / rbw), (unsigned)ug), dim3(NW * 64), shm, s,
+                     (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
+                     (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, t->outlier_idx, (int)t->n_outlier,
+                     (const uint16_t*)t->side, t->ld_side, epi, rbw);
+  return launch_status();
 }
 
 template <int BITS, int G, int R, int RBW, class EPI>
@@ -698,10 +708,15 @@ static int decode_launch(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
   constexpr int NP = 8 / BITS, NW = 8, BIG = EPI::kIn ? 4 : 8;
   // Consumers of G = 128 groups keep the two-workgroups-per-CU kernels: at NW = 4 the row kernel
   // would run four waves per CU.
+  // The row kernel addresses a block's rows by 32-bit offsets: 16 rows of every operand must
+  // stay below 2^31 bytes (always true for real hidden sizes; the others take the tile kernels).
+  bool off32 = true;
+  for (int64_t ldb : {t->ld_codes, 2 * t->ld_qp, 2 * t->ld_L, 2 * epi.in_ld(), 2 * epi.out_ld()})
+    off32 = off32 && 16 * ldb < ((int64_t)1 << 31);
   if constexpr (!(EPI::kIn && G == 128)) {
-    if (t->n_outlier == 0) return decode_rows_launch<BITS, G, R, false>(t, s, epi);
+    if (off32 && t->n_outlier == 0) return decode_rows_launch<BITS, G, R, false>(t, s, epi);
     if constexpr (R == 0) {
-      if (t->n_outlier <= kSideMax) return decode_rows_launch<BITS, G, R, true>(t, s, epi);
+      if (off32 && t->n_outlier <= kSideMax) return decode_rows_launch<BITS, G, R, true>(t, s, epi);
     }
   }
   const int64_t units = t->hidden / (G * NP), nrb = (t->rows + 15) / 16;
