@@ -219,6 +219,38 @@ __device__ __forceinline__ void project_unit(const u32x2 (&vop)[G / 16][R / 16],
   }
 }
 
+// The V^T operands of project_unit, computed once: vt[k][t] is the A operand that pairs with
+// x[k] (see project_unit) for rank tile t.
+template <int G, int R>
+__device__ __forceinline__ void transpose_vops(const u32x2 (&vop)[G / 16][R / 16], u32x2 ident,
+                                               u32x4 (&vt)[G / 32][R / 16]) {
+#pragma unroll
+  for (int k = 0; k < G / 32; ++k) {
+#pragma unroll
+    for (int t = 0; t < R / 16; ++t) {
+      const f32x4 v0 = mfma_16x16x16(vop[2 * k][t], ident, zero4());
+      const f32x4 v1 = mfma_16x16x16(vop[2 * k + 1][t], ident, zero4());
+      vt[k][t] = u32x4{pack_bf16x2_exact(v0[0], v0[1]), pack_bf16x2_exact(v0[2], v0[3]),
+                       pack_bf16x2_exact(v1[0], v1[1]), pack_bf16x2_exact(v1[2], v1[3])};
+    }
+  }
+}
+// project_unit with the V^T operands already transposed.
+template <int G, int R>
+__device__ __forceinline__ void project_unit_vt(const u32x4 (&vt)[G / 32][R / 16], const u32x4* x, f32x4* acc) {
+#pragma unroll
+  for (int k = 0; k < G / 32; ++k)
+#pragma unroll
+    for (int t = 0; t < R / 16; ++t) acc[t] = mfma_16x16x32(vt[k][t], x[k], acc[t]);
+}
+
+// 16 bytes per lane from global memory straight into LDS (no VGPRs): lane l's bytes land at
+// lds + 16 * l, so `lds` must be wave-uniform.  Non-temporal (streamed once).  Completion is
+// counted by vmcnt.
+__device__ __forceinline__ void ld16_to_lds(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 2);
+}
+
 // ---------------------------------------------------------------- row-quad exchanges
 // The four lanes of a row (j, j+16, j+32, j+48) are one lane of each 16-lane row of the
 // wave.  v_permlane32_swap exchanges lanes 32..63 of its first operand with lanes 0..31 of
@@ -234,11 +266,19 @@ __device__ __forceinline__ void swap16(float& a, float& b) {
   a = __uint_as_float(s[0]);
   b = __uint_as_float(s[1]);
 }
-// min / max as v_med3 against -inf / +inf: the same result as fminf / fmaxf for non-NaN
-// inputs, without the canonicalising moves the compiler adds around fminf of values it
-// cannot prove canonical (such as permlane results).
-__device__ __forceinline__ float min_nc(float a, float b) { return __builtin_amdgcn_fmed3f(a, b, -__builtin_inff()); }
-__device__ __forceinline__ float max_nc(float a, float b) { return __builtin_amdgcn_fmed3f(a, b, __builtin_inff()); }
+// min / max of non-NaN values without the canonicalising moves the compiler adds around
+// fminf / fmaxf (and around v_med3 against an infinity, which it folds into min / max) of
+// values it cannot prove canonical, such as permlane results.
+__device__ __forceinline__ float min_nc(float a, float b) {
+  float r;
+  asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float max_nc(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 
 // Reductions over the four lanes of a row; every lane receives the result.
 __device__ __forceinline__ float row_min4(float v) {

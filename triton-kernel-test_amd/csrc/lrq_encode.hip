@@ -221,7 +221,7 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
   constexpr int NP = Re::NP, CPG = G / 32, RT = Re::RT, E = G / 4;
   static_assert(NP == 2 && (UPW == 2 || UPW == 4), "the qparams gather below is written for 2 planes x 2 or 4 units");
   extern __shared__ __attribute__((aligned(16))) unsigned char shm[];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int j = lane & 15, g = lane >> 4;
   unsigned char* region = shm + (size_t)w * Re::REGION;
   f32x4* part = reinterpret_cast<f32x4*>(shm + (size_t)NW * Re::REGION);  // [2][NW][RT][64]
@@ -231,7 +231,12 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
   const int nblk = min(RBW, nrb - rb0);
   const int ub = w * UPW;  // first unit of this wave
 
+  // With one row per load instruction (RPL == 1) a load's 1 KB lands contiguously in the
+  // region, so it goes straight from HBM to LDS (no staging registers); the registers saved
+  // hold the projection's V^T operands for the whole kernel.
+  constexpr bool DMA = Re::PPL == NP;
   u32x2 vop[UPW][NP][G / 16][RT];
+  u32x4 vt[DMA ? UPW : 1][NP][CPG][RT];
   const u32x2 ident = identity_bop(j, g);
 
   // Load instruction i of block rb covers rows RPL*i .. RPL*i + RPL-1 of the block (RPL = PPL/NP
@@ -254,14 +259,21 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
   auto laddr = [&](int i) {
     return region + (RPL * i + lrow) * Re::PITCH + (lpc % NP) * Re::PIECE + loff;
   };
-  u32x4 pf[2][Re::RL];
+  u32x4 pf[DMA ? 1 : 2][Re::RL];
   auto issue = [&](int buf, int rb, int round) {
 #pragma unroll
-    for (int i = 0; i < Re::RL; ++i) pf[buf][i] = ld16_stream(gaddr(rb, round * Re::RL + i));
+    for (int i = 0; i < Re::RL; ++i) {
+      if constexpr (DMA)
+        ld16_to_lds(gaddr(rb, round * Re::RL + i), region + (round * Re::RL + i) * Re::PITCH);
+      else
+        pf[buf][i] = ld16_stream(gaddr(rb, round * Re::RL + i));
+    }
   };
   auto land = [&](int buf, int round) {
+    if constexpr (!DMA) {
 #pragma unroll
-    for (int i = 0; i < Re::RL; ++i) *reinterpret_cast<u32x4*>(laddr(round * Re::RL + i)) = pf[buf][i];
+      for (int i = 0; i < Re::RL; ++i) *reinterpret_cast<u32x4*>(laddr(round * Re::RL + i)) = pf[buf][i];
+    }
   };
 
   // Prologue: block rb0 into the region, two rounds in flight.  The first two rounds are
@@ -269,7 +281,23 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
   // from the start.  V arrives as whole 1 KB pieces (the wave's V rows are NP contiguous ranges
   // of UPW*G rows), passes through the region, and is read back in the operand layout before
   // the region receives block rb0.
-  {
+  if constexpr (DMA) {
+    // V operands straight from global memory (L2-resident after the first workgroups) in the
+    // residual layout, transposed once for the projection; then the whole of block rb0.
+    const int rb = min(rb0, nrb - 1);
+#pragma unroll
+    for (int uu = 0; uu < UPW; ++uu)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, ub + uu, N, NP, G), j, g, vop[uu][p]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int rd = 0; rd < Re::NR; ++rd) issue(0, rb, rd);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int uu = 0; uu < UPW; ++uu)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) transpose_vops<G, R>(vop[uu][p], ident, vt[uu][p]);
+  } else {
     const int rb = min(rb0, nrb - 1);
     issue(0, rb, 0);
     issue(1, rb, 1);
@@ -314,6 +342,19 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
     const int rb = __builtin_amdgcn_readfirstlane(min(rb0 + b, nrb - 1));  // wave-uniform
     const int row = min(rb * 16 + j, M - 1);
     const int rbn = __builtin_amdgcn_readfirstlane(min(rb0 + b + 1, nrb - 1));
+    if constexpr (DMA) {
+      // Wait until the slice's loads have written the region.  vmcnt retires in issue order
+      // on gfx9 (loads and stores alike); after the last round of a block's loads this wave
+      // issues exactly kAfter stores (the codes of units 2.., the qparams and L rows), which
+      // need not complete here.  Block 0's loads are the prologue's last memory operations.
+      constexpr int kAfter = (UPW - 2) * (E / 16) + 1 + RT;
+      static_assert(kAfter < 16, "vmcnt immediate");
+      if (b == 0)
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+      else
+        __builtin_amdgcn_s_waitcnt(0x0f70 | kAfter);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     // this block's slice, MFMA layout (lane (j, g): row j, columns E*g .. of each unit-plane)
     u32x4 x[UPW][NP][CPG];
 #pragma unroll
@@ -323,6 +364,11 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
 #pragma unroll
         for (int k = 0; k < CPG; ++k)
           x[uu][p][k] = *reinterpret_cast<const u32x4*>(region + j * Re::PITCH + p * Re::PIECE + (uu * G + E * g + 8 * k) * 2);
+    if constexpr (DMA) {
+      // the region may be overwritten once every read of the slice has returned
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      __builtin_amdgcn_sched_barrier(0);
+    }
     if (next) issue(0, rbn, 0);
     __builtin_amdgcn_sched_barrier(0);
 
@@ -332,7 +378,12 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
 #pragma unroll
     for (int uu = 0; uu < UPW; ++uu)
 #pragma unroll
-      for (int p = 0; p < NP; ++p) project_unit<G, R>(vop[uu][p], x[uu][p], ident, acc[(uu * NP + p) & 1]);
+      for (int p = 0; p < NP; ++p) {
+        if constexpr (DMA)
+          project_unit_vt<G, R>(vt[uu][p], x[uu][p], acc[(uu * NP + p) & 1]);
+        else
+          project_unit<G, R>(vop[uu][p], x[uu][p], ident, acc[(uu * NP + p) & 1]);
+      }
     f32x4* slot = part + (size_t)(b & 1) * NW * RT * 64;
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
