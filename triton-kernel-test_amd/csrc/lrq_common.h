@@ -124,6 +124,11 @@ __device__ __forceinline__ void st16_pred(void* base, uint32_t len, uint32_t off
   const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)len, 0x00020000);
   __builtin_amdgcn_raw_buffer_store_b128(v, r, keep ? off : 0x7ffffff0u, 0, 0);
 }
+// st16_pred as a non-temporal (streaming) store.
+__device__ __forceinline__ void st16_pred_stream(void* base, uint32_t len, uint32_t off, u32x4 v, bool keep) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)len, 0x00020000);
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, keep ? off : 0x7ffffff0u, 0, 2);
+}
 
 // Unpack the 8 bf16 of a 16-byte vector into fp32.
 __device__ __forceinline__ void unpack8(u32x4 v, float* f) {

@@ -393,6 +393,7 @@ struct RowsOut {
   static constexpr int OSLOT = 16 * NP * OPAD;      // one block's tile
   static constexpr int OCH = 16 * NP * (OROW / 16); // 16-byte chunks per tile
   static_assert(OROW % 16 == 0, "row segment of whole vectors");
+  static_assert(OCH % (NW * 64) == 0, "tile chunks split evenly over the workgroup");
 };
 
 template <int BITS, int G, int R, int NW, bool IN, bool OUTL>
@@ -427,7 +428,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
   unsigned char* osm = dsm + (IN ? 2 : 0) * Ro::OSLOT;       // [2][OSLOT] output tiles
   uint32_t* colmask = reinterpret_cast<uint32_t*>(osm + 2 * Ro::OSLOT);  // OUTL: N/32 words
   int16_t* oslot = reinterpret_cast<int16_t*>(colmask + N / 32);         // OUTL: N entries
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int j = lane & 15, g = lane >> 4;
   const int units = N / (G * NP);
   const int u0 = blockIdx.y * NW, u = u0 + w;
@@ -455,10 +456,9 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
 
   u32x2 vop[NP][G / 16][RT];
   if constexpr (R > 0) {
-    if (active) {
+    // unconditional (see below); waves past the last unit load the last unit's operands
 #pragma unroll
-      for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, u, N, NP, G), j, g, vop[p]);
-    }
+    for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, min(u, units - 1), N, NP, G), j, g, vop[p]);
   }
 
   struct In {
@@ -467,8 +467,17 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
     u32x4 d[IN ? Lay::DPT : 1];
     uint32_t sd[OUTL ? Lay::SPT : 1];
   };
-  const int qk = tid, lk = tid - Tl::QCH;
-  const bool has_q = qk < Tl::QCH && (qk % (Tl::QROW / 8)) * 8 < nu * NP * 4;
+  // Every global load and store of the block loop is issued by every lane, unconditionally:
+  // a load or store under a per-lane branch makes the compiler drain all outstanding memory
+  // operations (the prefetched blocks included) before the next use of any load.  Lanes whose
+  // chunk lies past the workgroup's units load a clamped (valid) address and stage the value
+  // where nothing reads it; their stores are dropped by the buffer range check.
+  // qparams move as one 4-byte pair per lane (QROW / 4 per row, waves 0.. of the block), L as
+  // 8-byte chunks (the next waves); both splits are whole waves.
+  constexpr int QCH4 = 4 * Tl::QROW;
+  static_assert(QCH4 % 64 == 0 && Tl::LCH % 64 == 0 && QCH4 + Tl::LCH <= T, "qparam / L split in whole waves");
+  const int qk = tid, lk = tid - QCH4;
+  const bool has_q = qk < QCH4;
   const bool has_l = R > 0 && lk >= 0 && lk < Tl::LCH;
   // tile chunk k -> (plane, row, 16-byte column chunk)
   auto chunk = [](int k, int& p, int& r, int& c16) {
@@ -488,13 +497,13 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
     const unsigned char* cb0 = codes + (int64_t)rb * 16 * ldc_b;
 #pragma unroll
     for (int i = 0; i < Tl::CPT; ++i) {
-      const int k = tid + T * i, r = k / (Tl::CROW / 16), c16 = k % (Tl::CROW / 16);
-      if (c16 * 16 < nu * G) in.c[i] = ld16_stream(cb0 + rowclamp(rb, r) * (uint32_t)ldc_b + ccol + c16 * 16);
+      const int k = tid + T * i, r = k / (Tl::CROW / 16), c16 = min(k % (Tl::CROW / 16), nu * (G / 16) - 1);
+      in.c[i] = ld16_stream(cb0 + rowclamp(rb, r) * (uint32_t)ldc_b + ccol + c16 * 16);
     }
     if (has_q) {
-      const int r = qk / (Tl::QROW / 8), c8 = qk % (Tl::QROW / 8);
+      const int r = qk / (Tl::QROW / 4), c4 = min(qk % (Tl::QROW / 4), nu * NP - 1);
       const unsigned char* qb0 = reinterpret_cast<const unsigned char*>(qparams) + (int64_t)rb * 16 * ldq_b;
-      in.ql = ld8(qb0 + rowclamp(rb, r) * (uint32_t)ldq_b + (uint32_t)u0 * NP * 4 + c8 * 8);
+      in.ql[0] = ld4(qb0 + rowclamp(rb, r) * (uint32_t)ldq_b + (uint32_t)u0 * NP * 4 + c4 * 4);
     } else if (has_l) {
       const int r = lk / (Tl::LROW / 8), c8 = lk % (Tl::LROW / 8);
       const unsigned char* lb0 = reinterpret_cast<const unsigned char*>(Lin) + (int64_t)rb * 16 * ldl_b;
@@ -507,16 +516,16 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
         const int k = tid + T * i;
         int p, r, c16;
         chunk(k, p, r, c16);
-        if ((Ro::OCH % T == 0 || k < Ro::OCH) && c16 * 16 < vbytes)
-          in.d[i] = ld16_stream(ib0 + rowclamp(rb, r) * (uint32_t)ldi_b + (uint32_t)unit_base(p, u0, N, NP, G) * 2 +
-                                c16 * 16);
+        c16 = min(c16, vbytes / 16 - 1);
+        in.d[i] = ld16_stream(ib0 + rowclamp(rb, r) * (uint32_t)ldi_b + (uint32_t)unit_base(p, u0, N, NP, G) * 2 +
+                              c16 * 16);
       }
     }
     if constexpr (OUTL) {
 #pragma unroll
       for (int i = 0; i < Lay::SPT; ++i) {
-        const int k = tid + T * i, r = k / kSideMax, c = k % kSideMax;
-        if (k < 16 * kSideMax && c < nout) in.sd[i] = side[min(rb * 16 + r, M - 1) * ldside + c];
+        const int k = tid + T * i, r = k / kSideMax, c = min(k % kSideMax, nout - 1);
+        in.sd[i] = side[min(rb * 16 + r, M - 1) * ldside + c];
       }
     }
   };
@@ -525,11 +534,11 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
 #pragma unroll
     for (int i = 0; i < Tl::CPT; ++i) {
       const int k = tid + T * i, r = k / (Tl::CROW / 16), c16 = k % (Tl::CROW / 16);
-      if (c16 * 16 < nu * G) *reinterpret_cast<u32x4*>(slot + r * Tl::CROW + c16 * 16) = in.c[i];
+      *reinterpret_cast<u32x4*>(slot + r * Tl::CROW + c16 * 16) = in.c[i];
     }
     if (has_q) {
-      const int r = qk / (Tl::QROW / 8), c8 = qk % (Tl::QROW / 8);
-      *reinterpret_cast<u32x2*>(slot + Tl::QOFF + r * Tl::QROW + c8 * 8) = in.ql;
+      const int r = qk / (Tl::QROW / 4), c4 = qk % (Tl::QROW / 4);
+      *reinterpret_cast<uint32_t*>(slot + Tl::QOFF + r * Tl::QROW + c4 * 4) = in.ql[0];
     } else if (has_l) {
       const int r = lk / (Tl::LROW / 8), c8 = lk % (Tl::LROW / 8);
       *reinterpret_cast<u32x2*>(slot + Tl::LOFF + r * Tl::LROW + c8 * 8) = in.ql;
@@ -541,8 +550,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
         const int k = tid + T * i;
         int p, r, c16;
         chunk(k, p, r, c16);
-        if ((Ro::OCH % T == 0 || k < Ro::OCH) && c16 * 16 < vbytes)
-          *reinterpret_cast<u32x4*>(ds + (p * 16 + r) * Ro::OPAD + c16 * 16) = in.d[i];
+        *reinterpret_cast<u32x4*>(ds + (p * 16 + r) * Ro::OPAD + c16 * 16) = in.d[i];
       }
     }
     if constexpr (OUTL) {
@@ -558,14 +566,14 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
     const unsigned char* os = osm + (b & 1) * Ro::OSLOT;
     unsigned char* ob0 = reinterpret_cast<unsigned char*>(epi.out_row((int64_t)rb * 16));
 #pragma unroll
-    for (int i = 0; i < (Ro::OCH + T - 1) / T; ++i) {
+    for (int i = 0; i < Ro::OCH / T; ++i) {
       const int k = tid + T * i;
       int p, r, c16;
       chunk(k, p, r, c16);
-      if ((Ro::OCH % T == 0 || k < Ro::OCH) && c16 * 16 < vbytes) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(os + (p * 16 + r) * Ro::OPAD + c16 * 16);
-        st16_stream(ob0 + rowclamp(rb, r) * (uint32_t)ldo_b + (uint32_t)unit_base(p, u0, N, NP, G) * 2 + c16 * 16, v);
-      }
+      const u32x4 v = *reinterpret_cast<const u32x4*>(os + (p * 16 + r) * Ro::OPAD + c16 * 16);
+      st16_pred_stream(ob0, (uint32_t)(16 * ldo_b),
+                       rowclamp(rb, r) * (uint32_t)ldo_b + (uint32_t)unit_base(p, u0, N, NP, G) * 2 + c16 * 16, v,
+                       c16 * 16 < vbytes);
     }
   };
 
