@@ -31,7 +31,7 @@ def _codes_unpacked(c):
     return torch.cat([lo, hi], dim=1)
 
 
-@pytest.mark.parametrize("name", ["north_star", "c4"])
+@pytest.mark.parametrize("name", ["north_star", "c4", "c2"])
 def test_fullsize_roundtrip_properties(pkg, dev, name):
     cfg = pkg.inputs.CONFIGS[name]
     print(f"[full {name}] {cfg.rows}x{cfg.hidden}", flush=True)

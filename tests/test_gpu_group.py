@@ -59,7 +59,8 @@ FORMATS = [
     (64, 2048, 16, 4, 64),     # fused (4 x 8)
     (48, 5120, 16, 4, 64),     # fused (8 x 10)
     (37, 1536, 16, 4, 64),     # two-pass (no single-pass instantiation)
-    (64, 4096, 32, 4, 64),     # rank 32, fused
+    (64, 4096, 32, 4, 64),     # rank 32 (column-slab two-pass)
+    (72, 11008, 32, 4, 64),    # rank 32 at config 2's width: 6 slabs, the last one partial
     (40, 2048, 16, 4, 128),
     (33, 2048, 16, 8, 64),
     (64, 1024, 16, 8, 128),

@@ -576,6 +576,201 @@ __global__ __launch_bounds__(256) void k_quant(
   }
 }
 
+// -------------------------------------------------------------------------------------
+// Two-pass encode over column slabs (rank 16/32 rows without a single-pass kernel).
+//
+// Pass 1, k_project_slab: grid (row groups, slabs); wave w of slab s owns the 256 columns
+// c0 = 256*(8s + w) .. +255, whose V^T operands (8 K-steps of 32 columns x R/16 rank tiles)
+// stay in registers.  Per 16-row block the wave's 16 x 512 B slice goes HBM -> registers ->
+// a private LDS region (1 KB loads of two rows) and is read back in the MFMA layout; the eight
+// waves' fp32 partials are summed in LDS in a fixed order, and the slab's partial L of the
+// block is written to `part` (row r at part + r*ldp bytes, slab s at byte 4*R*s).  Columns
+// past N contribute zero (their V^T operands are zero; their loads are clamped).
+//
+// Pass 1b, k_reduce_slabs: L = bf16(sum over slabs in order).
+//
+// Pass 2, k_quant_slab: residual and quantisation with L given.  Waves are independent (no
+// barrier): global wave gw takes wave column gw % nwc (units 2*(gw % nwc) .. +1) and row
+// range gw / nwc; its slice streams through a private LDS region as in k_encode_rows, with
+// the next block's loads (and its L rows) in flight during the current block's quantisation.
+template <int R>
+__global__ __launch_bounds__(512) void k_project_slab(const uint16_t* __restrict__ X, int64_t ldx, int M, int N,
+                                                      const uint16_t* __restrict__ Vt,
+                                                      unsigned char* __restrict__ part, int64_t ldp, int RBW) {
+  constexpr int RT = R / 16, NW = 8, CW = 256, PITCH = CW * 2 + 16, NLD = 8;
+  __shared__ __attribute__((aligned(16))) unsigned char shm[NW * 16 * PITCH];
+  __shared__ f32x4 red[2][NW][RT][64];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int nrb = (M + 15) / 16;
+  const int rb0 = blockIdx.x * RBW;
+  if (rb0 >= nrb) return;  // whole workgroup
+  const int nblk = min(RBW, nrb - rb0);
+  const int s = blockIdx.y;
+  const int c0 = CW * (NW * s + w);
+  const bool live = c0 < N;  // wave-uniform
+  unsigned char* region = shm + (size_t)w * 16 * PITCH;
+  // V^T operands: vt[k][t] = Vt[16t + j][c0 + 32k + 8g .. +7] (zero past N)
+  u32x4 vt[CW / 32][RT];
+#pragma unroll
+  for (int k = 0; k < CW / 32; ++k)
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      const int c = c0 + 32 * k + 8 * g;
+      vt[k][t] = c < N ? ld16(Vt + (int64_t)(16 * t + j) * N + c) : u32x4{0u, 0u, 0u, 0u};
+    }
+  // load i: rows 2i, 2i+1 of the block, lane l -> row 2i + l/32, bytes (l%32)*16 of the slice
+  // (clamped to column N - 8 past the end: those columns meet zero operands)
+  const int lr = lane >> 5;
+  const uint32_t lcol = (uint32_t)min(c0 + (lane & 31) * 8, N - 8) * 2u;
+  auto gaddr = [&](int rb, int i) {
+    const int64_t row = min(rb * 16 + 2 * i + lr, M - 1);
+    return reinterpret_cast<const unsigned char*>(X + row * ldx) + lcol;
+  };
+  u32x4 pf[NLD];
+  auto issue = [&](int rb) {
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) pf[i] = ld16_stream(gaddr(rb, i));
+  };
+  if (live) issue(rb0);
+#pragma unroll 1
+  for (int b = 0; b < nblk; ++b) {
+    f32x4 acc[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) acc[t] = zero4();
+    if (live) {
+#pragma unroll
+      for (int i = 0; i < NLD; ++i)
+        *reinterpret_cast<u32x4*>(region + (2 * i + lr) * PITCH + (lane & 31) * 16) = pf[i];
+      u32x4 x[CW / 32];
+#pragma unroll
+      for (int k = 0; k < CW / 32; ++k) x[k] = *reinterpret_cast<const u32x4*>(region + j * PITCH + (32 * k + 8 * g) * 2);
+      if (b + 1 < nblk) issue(rb0 + b + 1);
+#pragma unroll
+      for (int k = 0; k < CW / 32; ++k)
+#pragma unroll
+        for (int t = 0; t < RT; ++t) acc[t] = mfma_16x16x32(vt[k][t], x[k], acc[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < RT; ++t) red[b & 1][w][t][lane] = acc[t];
+    lds_barrier();
+    if (w < RT) {
+      // wave t sums rank tile t over the eight waves; lane (j, g) holds L[row j][16t + 4g ..]
+      const int t = w;
+      f32x4 sum = red[b & 1][0][t][lane];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; ++w2) {
+        const f32x4 o = red[b & 1][w2][t][lane];
+        sum[0] += o[0];
+        sum[1] += o[1];
+        sum[2] += o[2];
+        sum[3] += o[3];
+      }
+      const int64_t row = min((rb0 + b) * 16 + j, M - 1);
+      *reinterpret_cast<f32x4*>(part + row * ldp + 4 * R * s + (16 * t + 4 * g) * 4) = sum;
+    }
+  }
+}
+
+template <int R>
+__global__ __launch_bounds__(256) void k_reduce_slabs(const unsigned char* __restrict__ part, int64_t ldp, int M,
+                                                      int nslab, uint16_t* __restrict__ L, int64_t ldl) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // (row, 4 ranks)
+  if (i >= (int64_t)M * (R / 4)) return;
+  const int64_t row = i / (R / 4);
+  const int q = (int)(i % (R / 4));
+  const unsigned char* p = part + row * ldp + q * 16;
+  f32x4 sum = *reinterpret_cast<const f32x4*>(p);
+  for (int sl = 1; sl < nslab; ++sl) {
+    const f32x4 o = *reinterpret_cast<const f32x4*>(p + 4 * R * sl);
+    sum[0] += o[0];
+    sum[1] += o[1];
+    sum[2] += o[2];
+    sum[3] += o[3];
+  }
+  *reinterpret_cast<u32x2*>(L + row * ldl + 4 * q) = u32x2{pack_bf16x2(sum[0], sum[1]), pack_bf16x2(sum[2], sum[3])};
+}
+
+template <int BITS, int G, int R>
+__global__ __launch_bounds__(512) void k_quant_slab(const uint16_t* __restrict__ X, int64_t ldx, int M, int N,
+                                                    const uint16_t* __restrict__ V, const uint16_t* __restrict__ Lin,
+                                                    int64_t ldl, uint8_t* __restrict__ codes, int64_t ldc,
+                                                    uint16_t* __restrict__ qparams, int64_t ldq, int nranges,
+                                                    int RBW) {
+  constexpr int NP = 8 / BITS, UPW = 2, NW = 8, CPG = G / 32, RT = R / 16, E = G / 4;
+  constexpr int PIECE = UPW * G * 2, PITCH = NP * PIECE + 16, PPL = 1024 / PIECE, LPL = 64 / PPL;
+  constexpr int RPL = PPL / NP, NLD = 16 / RPL;
+  static_assert(NP == 2 && PPL % NP == 0 && NLD * RPL == 16, "two planes, whole rows per load");
+  __shared__ __attribute__((aligned(16))) unsigned char shm[NW * 16 * PITCH];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int units = N / (G * NP), nwc = units / UPW;
+  const int gw = blockIdx.x * NW + w;
+  if (gw >= nranges * nwc) return;  // this wave only (no barriers below)
+  const int ub = UPW * (gw % nwc), rng = gw / nwc;
+  const int nrb = (M + 15) / 16;
+  const int rb0 = rng * RBW;
+  if (rb0 >= nrb) return;
+  const int nblk = min(RBW, nrb - rb0);
+  unsigned char* region = shm + (size_t)w * 16 * PITCH;
+
+  u32x2 vop[UPW][NP][G / 16][RT];
+#pragma unroll
+  for (int uu = 0; uu < UPW; ++uu)
+#pragma unroll
+    for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, ub + uu, N, NP, G), j, g, vop[uu][p]);
+
+  // load i: rows RPL*i .. of the block, lane l -> piece l/LPL (row RPL*i + (l/LPL)/NP, plane
+  // (l/LPL)%NP) at byte (l%LPL)*16; rows past the end clamp to the last row
+  const int lpc = lane / LPL, loff = (lane % LPL) * 16, lrow = lpc / NP;
+  const uint32_t xlane = (uint32_t)unit_base(lpc % NP, ub, N, NP, G) * 2u + (uint32_t)loff;
+  auto gaddr = [&](int rb, int i) {
+    const int64_t row = min((int64_t)rb * 16 + RPL * i + lrow, (int64_t)M - 1);
+    return reinterpret_cast<const unsigned char*>(X + row * ldx) + xlane;
+  };
+  u32x4 pf[NLD];
+  u32x2 lnext[RT];
+  auto issue = [&](int rb) {
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) pf[i] = ld16_stream(gaddr(rb, i));
+    const int64_t row = min(rb * 16 + j, M - 1);
+#pragma unroll
+    for (int t = 0; t < RT; ++t) lnext[t] = ld8(Lin + row * ldl + 16 * t + 4 * g);
+  };
+  issue(rb0);
+#pragma unroll 1
+  for (int b = 0; b < nblk; ++b) {
+    const int rb = rb0 + b;
+#pragma unroll
+    for (int i = 0; i < NLD; ++i)
+      *reinterpret_cast<u32x4*>(region + (RPL * i + lrow) * PITCH + (lpc % NP) * PIECE + loff) = pf[i];
+    u32x4 x[UPW][NP][CPG];
+#pragma unroll
+    for (int uu = 0; uu < UPW; ++uu)
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int k = 0; k < CPG; ++k)
+          x[uu][p][k] = *reinterpret_cast<const u32x4*>(region + j * PITCH + p * PIECE + (uu * G + E * g + 8 * k) * 2);
+    u32x2 lopn[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) lopn[t] = neg_bf16x4(lnext[t]);
+    if (b + 1 < nblk) issue(rb + 1);
+    const int row = min(rb * 16 + j, M - 1);
+    uint8_t* crow = codes + (int64_t)row * ldc;
+    uint32_t qp[UPW];
+#pragma unroll
+    for (int uu = 0; uu < UPW; ++uu) qp[uu] = quant_unit_regs<BITS, G, R>(x[uu], vop[uu], lopn, ub + uu, g, crow);
+    // the two units' (scale, zero) pairs of the row as one 16-byte store (see k_encode_rows)
+    float a = __uint_as_float(qp[0]), bq = a, c = __uint_as_float(qp[1]), d = c;
+    swap32(a, bq);
+    swap32(c, d);
+    st16_pred(qparams + (int64_t)rb * 16 * ldq, (uint32_t)(16 * ldq * 2),
+              (uint32_t)(((row - rb * 16) * ldq + ub * NP * 2) * 2),
+              u32x4{__float_as_uint(a), __float_as_uint(bq), __float_as_uint(c), __float_as_uint(d)}, g == 0);
+  }
+}
+
 // Gather the outlier channels into fp16 side columns: side[r, k] = fp16(x[r, idx[k]]).
 __global__ __launch_bounds__(256) void k_gather_side(const uint16_t* __restrict__ X, int64_t ldx, int M,
                                                      int N, const int32_t* __restrict__ oidx, int nout,
@@ -676,10 +871,58 @@ static int encode_persist_dispatch(const lrq_tensors* t, const void* x, int64_t 
   }
 }
 
+// Two-pass encode over column slabs (see k_project_slab).  The slab partials of L live in the
+// codes buffer until the quantisation pass overwrites it: row r's partials take the first
+// nslab*4*R bytes of its codes row.  Returns 0 when the shape does not fit this path.
+template <int BITS, int G, int R>
+static int encode_slabs(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s, int* status) {
+  if constexpr (BITS != 4 || R == 0) {
+    return 0;
+  } else {
+    const int M = (int)t->rows, N = (int)t->hidden;
+    constexpr int NP = 2;
+    const int units = N / (G * NP);
+    const int nslab = (N + 2047) / 2048;
+    const int64_t ldp = t->ld_codes;  // bytes
+    if (units % 2 != 0 || t->n_outlier != 0 || N % 32 != 0) return 0;
+    if ((int64_t)nslab * 4 * R > (int64_t)N / 2 || ldp % 16 != 0 || !aligned(t->codes, 16)) return 0;
+    if (t->ld_qp % 8 != 0 || !aligned(t->qparams, 16) || t->ld_L % 4 != 0 || !aligned(t->L, 8)) return 0;
+    if ((int64_t)16 * t->ld_qp * 2 >= ((int64_t)1 << 31)) return 0;
+    const int cus = cu_count();
+    const int nrb = (M + 15) / 16;
+    // pass 1: about one workgroup per CU over (row groups, slabs)
+    const int per1 = std::max(1, cus / nslab);
+    const int rbw1 = (nrb + per1 - 1) / per1;
+    hipLaunchKernelGGL((k_project_slab<R>), dim3((nrb + rbw1 - 1) / rbw1, nslab), dim3(512), 0, s,
+                       (const uint16_t*)x, ldx, M, N, (const uint16_t*)t->Vt, (unsigned char*)t->codes, ldp, rbw1);
+    int st = launch_status();
+    if (st) { *status = st; return 1; }
+    const int64_t nred = (int64_t)M * (R / 4);
+    hipLaunchKernelGGL((k_reduce_slabs<R>), dim3((unsigned)((nred + 255) / 256)), dim3(256), 0, s,
+                       (const unsigned char*)t->codes, ldp, M, nslab, (uint16_t*)t->L, t->ld_L);
+    st = launch_status();
+    if (st) { *status = st; return 1; }
+    // pass 2: 8 independent waves per workgroup, one workgroup per CU
+    const int nwc = units / 2;
+    const int nranges = std::max(1, std::min(nrb, cus * 8 / nwc));
+    const int rbw2 = (nrb + nranges - 1) / nranges;
+    const int waves = nranges * nwc;
+    hipLaunchKernelGGL((k_quant_slab<BITS, G, R>), dim3((waves + 7) / 8), dim3(512), 0, s, (const uint16_t*)x, ldx,
+                       M, N, (const uint16_t*)t->V, (const uint16_t*)t->L, t->ld_L, (uint8_t*)t->codes, t->ld_codes,
+                       (uint16_t*)t->qparams, t->ld_qp, nranges, rbw2);
+    *status = launch_status();
+    return 1;
+  }
+}
+
 template <int BITS, int G, int R>
 static int encode_twopass(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s) {
   const int M = (int)t->rows, N = (int)t->hidden;
   constexpr int NP = 8 / BITS, RB = 4;
+  {
+    int st = 0;
+    if (encode_slabs<BITS, G, R>(t, x, ldx, s, &st)) return st;
+  }
   if constexpr (R > 0) {
     hipLaunchKernelGGL((k_project<R>), dim3((M + 15) / 16), dim3(256), 0, s, (const uint16_t*)x, ldx, M, N,
                        (const uint16_t*)t->Vt, (uint16_t*)t->L, t->ld_L);
