@@ -3,6 +3,8 @@
 #include "lrq_common.h"
 #include "lrq_host.h"
 
+#include <algorithm>
+
 namespace lrq {
 
 // dst[c, r] = src[r, c]; 32x32 tiles through LDS (bank-conflict-free with the +1 pad).
@@ -24,10 +26,60 @@ __global__ __launch_bounds__(256) void k_transpose_bf16(const uint16_t* __restri
 
 // colmax[c] = max |x[r, c]| via an unsigned max on the fp32 bit pattern (valid for
 // non-negative floats).  colmax must be zeroed first (done by the host entry).
-// Grid: (ceil(cols / 512), ceil(rows / 64)); each thread owns 2 adjacent columns and
-// walks 64 rows.
+// Grid: (ceil(cols / 512), row groups of rows_per rows); 256 threads = 4 row phases x 64
+// column lanes of 8 adjacent columns (one 16-byte load per row: a wave reads 1 KB of a row),
+// 8 loads in flight per thread.  The 4 phases meet in LDS, so each workgroup issues one
+// atomic per column (few row groups keep the atomics per address low).
 __global__ __launch_bounds__(256) void k_colmax(const uint16_t* __restrict__ x, int64_t ldx, int64_t rows,
-                                                int64_t cols, unsigned int* __restrict__ colmax) {
+                                                int64_t cols, int64_t rows_per, unsigned int* __restrict__ colmax) {
+  __shared__ float red[3][64][8];
+  const int cl = threadIdx.x & 63, ph = threadIdx.x >> 6;
+  const int64_t c = ((int64_t)blockIdx.x * 64 + cl) * 8;
+  const bool live = c < cols;
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per;
+  const int64_t r1 = r0 + rows_per < rows ? r0 + rows_per : rows;
+  float m[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) m[e] = 0.f;
+  if (live) {
+    const uint16_t* p = x + c;
+    int64_t r = r0 + ph;
+    for (; r + 28 < r1; r += 32) {  // rows r, r+4, ..., r+28
+      u32x4 v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = ld16_stream(p + (r + 4 * i) * ldx);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float f[8];
+        unpack8(v[i], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m[e] = fmaxf(m[e], fabsf(f[e]));
+      }
+    }
+    for (; r < r1; r += 4) {
+      float f[8];
+      unpack8(ld16_stream(p + r * ldx), f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m[e] = fmaxf(m[e], fabsf(f[e]));
+    }
+  }
+  if (ph > 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[ph - 1][cl][e] = m[e];
+  }
+  __syncthreads();
+  if (ph == 0 && live) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float a = fmaxf(fmaxf(m[e], red[0][cl][e]), fmaxf(red[1][cl][e], red[2][cl][e]));
+      atomicMax(colmax + c + e, __float_as_uint(a));
+    }
+  }
+}
+
+// Same with 2 columns per thread (4-byte loads), for rows that are not 16-byte aligned.
+__global__ __launch_bounds__(256) void k_colmax2(const uint16_t* __restrict__ x, int64_t ldx, int64_t rows,
+                                                 int64_t cols, unsigned int* __restrict__ colmax) {
   const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 2;
   if (c >= cols) return;
   const int64_t r0 = (int64_t)blockIdx.y * 64;
@@ -47,54 +99,111 @@ __global__ void k_zero_u32(unsigned int* p, int64_t n) {
   if (i < n) p[i] = 0u;
 }
 
-// Top-k by repeated block argmax in one 1024-thread workgroup (k is small: tens of
-// channels).  Ties go to the lower column index.  Output sorted ascending.
-// LDS: hidden floats (value copy) + 1024 (value, index) reduction slots.
+// Exclusive prefix sum over the 1024 threads of the workgroup (every thread calls it); also
+// returns the total.  wsum: 16 words of LDS.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* wsum, uint32_t& total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  uint32_t incl = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = __shfl_up(incl, d);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t t = wsum[i];
+    before += i < w ? t : 0u;
+    all += t;
+  }
+  __syncthreads();  // wsum may be reused by the caller's next scan
+  total = all;
+  return before + incl - v;
+}
+
+// Top-k by radix select in one 1024-thread workgroup.  colmax values are non-negative, so
+// their fp32 bit patterns order like the values.  The k-th largest key T is fixed MSB-first,
+// 8 bits per round: a 256-bin histogram of the next byte over the keys that match the bits
+// fixed so far, then (wave 0) a scan from the top bin finds the bin holding the k-th key.
+// The result is every column with key > T and the first k - #(key > T) columns with key == T
+// (ties toward the lower index), written in ascending index order from per-thread
+// contiguous chunks and two block scans.
 __global__ __launch_bounds__(1024) void k_topk(const float* __restrict__ colmax, int hidden, int k,
                                                int32_t* __restrict__ idx) {
-  extern __shared__ float sval[];
-  float* rv = sval + hidden;
-  int* ri = reinterpret_cast<int*>(rv + 1024);
-  int* picked = ri + 1024;
-  for (int i = threadIdx.x; i < hidden; i += blockDim.x) sval[i] = colmax[i];
-  __syncthreads();
-  for (int it = 0; it < k; ++it) {
-    float bv = -1.f;
-    int bi = 0x7fffffff;
-    for (int i = threadIdx.x; i < hidden; i += blockDim.x) {
-      const float v = sval[i];
-      if (v > bv || (v == bv && i < bi)) {
-        bv = v;
-        bi = i;
-      }
-    }
-    rv[threadIdx.x] = bv;
-    ri[threadIdx.x] = bi;
+  extern __shared__ uint32_t skey[];  // hidden keys
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t wsum[16];
+  __shared__ uint32_t s_prefix, s_need;
+  const int tid = threadIdx.x, lane = tid & 63;
+  for (int i = tid; i < hidden; i += 1024) skey[i] = __float_as_uint(colmax[i]);
+  if (tid == 0) {
+    s_prefix = 0u;
+    s_need = (uint32_t)k;
+  }
+  uint32_t mask = 0u;
+#pragma unroll 1
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    if (tid < 256) hist[tid] = 0u;
     __syncthreads();
-    for (int s = 512; s > 0; s >>= 1) {
-      if ((int)threadIdx.x < s) {
-        const float ov = rv[threadIdx.x + s];
-        const int oi = ri[threadIdx.x + s];
-        if (ov > rv[threadIdx.x] || (ov == rv[threadIdx.x] && oi < ri[threadIdx.x])) {
-          rv[threadIdx.x] = ov;
-          ri[threadIdx.x] = oi;
+    const uint32_t prefix = s_prefix;
+    for (int i = tid; i < hidden; i += 1024) {
+      const uint32_t key = skey[i];
+      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid < 64) {
+      // lane l holds bins 255-4l .. 252-4l (top first)
+      uint32_t cnt[4], tot = 0;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        cnt[m] = hist[255 - (4 * lane + m)];
+        tot += cnt[m];
+      }
+      uint32_t incl = tot;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t o = __shfl_up(incl, d);
+        if (lane >= d) incl += o;
+      }
+      const uint32_t need = s_need;
+      uint32_t cum = incl - tot;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (cum < need && cum + cnt[m] >= need) {
+          s_prefix = prefix | ((uint32_t)(255 - (4 * lane + m)) << shift);
+          s_need = need - cum;
         }
+        cum += cnt[m];
       }
-      __syncthreads();
     }
-    if (threadIdx.x == 0) {
-      picked[it] = ri[0];
-      sval[ri[0]] = -2.f;  // below every |x|
-    }
+    mask |= 255u << shift;
     __syncthreads();
   }
-  // rank-sort the k picked indices ascending
-  for (int a = threadIdx.x; a < k; a += blockDim.x) {
-    const int v = picked[a];
-    int pos = 0;
-    for (int b = 0; b < k; ++b) pos += picked[b] < v;
-    idx[pos] = v;
+  const uint32_t T = s_prefix, need_eq = s_need;  // take the first need_eq keys equal to T
+  const int C = (hidden + 1023) / 1024, i0 = tid * C, i1 = min(i0 + C, hidden);
+  uint32_t n_gt = 0, n_eq = 0;
+  for (int i = i0; i < i1; ++i) {
+    const uint32_t key = skey[i];
+    n_gt += key > T;
+    n_eq += key == T;
   }
+  uint32_t tot;
+  const uint32_t eq_before = block_exclusive_scan(n_eq, wsum, tot);
+  const uint32_t take_eq = eq_before >= need_eq ? 0u : min(n_eq, need_eq - eq_before);
+  uint32_t pos = block_exclusive_scan(n_gt + take_eq, wsum, tot);
+  uint32_t eq_seen = 0;
+  for (int i = i0; i < i1; ++i) {
+    const uint32_t key = skey[i];
+    bool sel = key > T;
+    if (key == T) {
+      sel = eq_seen < take_eq;
+      ++eq_seen;
+    }
+    if (sel) idx[pos++] = i;
+  }
+  (void)lane;
 }
 
 }  // namespace lrq
@@ -122,18 +231,29 @@ extern "C" int lrq_colmax(const void* x, int64_t ldx, int64_t rows, int64_t hidd
                      (unsigned int*)colmax, hidden);
   int st = launch_status();
   if (st || rows == 0) return st;
-  dim3 grid((unsigned)((hidden / 2 + 255) / 256), (unsigned)((rows + 63) / 64));
-  hipLaunchKernelGGL(k_colmax, grid, dim3(256), 0, s, (const uint16_t*)x, ldx, rows, hidden,
-                     (unsigned int*)colmax);
+  if ((hidden % 8) == 0 && (ldx % 8) == 0 && aligned(x, 16)) {
+    // about two workgroups per CU, row groups of whole 32-row steps
+    const int64_t cgroups = (hidden + 511) / 512;
+    int64_t groups = std::max<int64_t>(1, (int64_t)cu_count() * 2 / cgroups);
+    int64_t rows_per = (rows + groups - 1) / groups;
+    rows_per = (rows_per + 31) / 32 * 32;
+    groups = (rows + rows_per - 1) / rows_per;
+    hipLaunchKernelGGL(k_colmax, dim3((unsigned)cgroups, (unsigned)groups), dim3(256), 0, s, (const uint16_t*)x, ldx,
+                       rows, hidden, rows_per, (unsigned int*)colmax);
+  } else {
+    dim3 grid((unsigned)((hidden / 2 + 255) / 256), (unsigned)((rows + 63) / 64));
+    hipLaunchKernelGGL(k_colmax2, grid, dim3(256), 0, s, (const uint16_t*)x, ldx, rows, hidden,
+                       (unsigned int*)colmax);
+  }
   return launch_status();
 }
 
 extern "C" int lrq_topk(const float* colmax, int64_t hidden, int32_t k, int32_t* idx, void* stream) {
   if (colmax == nullptr || idx == nullptr) return LRQ_ERR_NULL;
-  if (hidden <= 0 || k < 0 || k > hidden || k > 1024) return LRQ_ERR_SHAPE;
-  // LDS: hidden + 1024 floats, 1024 + k ints; keep within 160 KiB.
-  const size_t shm = (size_t)hidden * 4 + 1024 * 4 + 1024 * 4 + (size_t)k * 4;
-  if (shm > 160 * 1024) return LRQ_ERR_SHAPE;
+  if (hidden <= 0 || k < 0 || k > hidden) return LRQ_ERR_SHAPE;
+  // LDS: the hidden keys plus about 1.1 KiB of static histogram and scan words; 160 KiB total.
+  const size_t shm = (size_t)hidden * 4;
+  if (shm + 2048 > 160 * 1024) return LRQ_ERR_SHAPE;
   if (k == 0) return LRQ_OK;
   hipLaunchKernelGGL(k_topk, dim3(1), dim3(1024), shm, (hipStream_t)stream, colmax, (int)hidden, (int)k, idx);
   return launch_status();
