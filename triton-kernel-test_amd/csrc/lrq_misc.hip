@@ -44,14 +44,25 @@ __global__ __launch_bounds__(256) void k_colmax(const uint16_t* __restrict__ x, 
   if (live) {
     const uint16_t* p = x + c;
     int64_t r = r0 + ph;
-    for (; r + 28 < r1; r += 32) {  // rows r, r+4, ..., r+28
-      u32x4 v[8];
+    // batches of 8 rows (r, r+4, ..., r+28), the next batch in flight while one is reduced
+    u32x4 v[8];
+    auto issue = [&](int64_t rr) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = ld16_stream(p + (r + 4 * i) * ldx);
+      for (int i = 0; i < 8; ++i) v[i] = ld16_stream(p + (rr + 4 * i) * ldx);
+    };
+    bool more = r + 28 < r1;
+    if (more) issue(r);
+    while (more) {
+      u32x4 cur[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) cur[i] = v[i];
+      r += 32;
+      more = r + 28 < r1;
+      if (more) issue(r);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         float f[8];
-        unpack8(v[i], f);
+        unpack8(cur[i], f);
 #pragma unroll
         for (int e = 0; e < 8; ++e) m[e] = fmaxf(m[e], fabsf(f[e]));
       }
