@@ -23,6 +23,7 @@ def _xhat(c, V, bits, group):
 
 @pytest.mark.parametrize("rows,n,rank,bits,group", [
     (100, 2048, 16, 4, 64),   # config 5 row length: 16 units, one per wave
+    (9000, 2048, 16, 4, 64),  # several row blocks per workgroup (the pipelined path), last block ragged
     (64, 1024, 16, 4, 64),    # 8 units
     (48, 512, 0, 4, 64),      # 4 units, rank 0
     (40, 2048, 16, 8, 128),   # int8 / g128: 16 units

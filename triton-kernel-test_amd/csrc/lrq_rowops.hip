@@ -11,6 +11,8 @@
 #include "lrq_dequant.h"
 #include "lrq_host.h"
 
+#include <algorithm>
+
 namespace lrq {
 
 // ------------------------------------------------------------------ softmax backward
@@ -120,6 +122,173 @@ __global__ __launch_bounds__(NW * 64) void k_softmax_bwd(
   }
 }
 
+// Row-persistent softmax backward (one workgroup per CU; wave w owns unit w of every row, so
+// a workgroup holds whole rows).  dP moves as whole row segments straight from HBM into an LDS
+// tile (two tiles, block b in tile b&1), is read back in the MFMA layout, and dS is written
+// over it in the same layout; after the next barrier the workgroup stores the tile as whole
+// row segments (non-temporal, full lines).  Codes, qparams and L of the wave's unit come one
+// block ahead in registers.  Per block: barrier (block b's dP visible, block b-1's dS
+// complete) -> store block b-1's tile -> barrier (its reads returned) -> dP of block b+1 into
+// that tile -> reconstruct, row sums (one more barrier), dS.  Rows past the end repeat the
+// last row (identical stores).
+template <int BITS, int G, int NW>
+struct SmxTile {
+  static constexpr int NP = 8 / BITS;
+  static constexpr int ROWB = NW * G * NP * 2;  // bytes of a bf16 row (the workgroup's NW units)
+  static constexpr int PITCH = ROWB + 16;       // LDS row pitch (spreads the 16 rows over banks)
+  static constexpr int TILE = 16 * PITCH;
+  static constexpr int CPR = ROWB / 1024;       // 1 KB chunks per row
+  static constexpr int DPW = 16 * CPR / NW;     // dP loads per wave and block
+  static constexpr int SPT = 16 * ROWB / 16 / (NW * 64);  // 16-byte tile chunks per thread
+  static constexpr size_t LDS = 2 * (size_t)TILE + (size_t)NW * 16 * 4;
+  static_assert(ROWB % 1024 == 0 && (16 * CPR) % NW == 0 && (16 * ROWB / 16) % (NW * 64) == 0, "tile split");
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+};
+
+template <int BITS, int G, int R, int NW>
+__global__ __launch_bounds__(NW * 64) void k_softmax_rows(
+    const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
+    const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
+    const uint16_t* __restrict__ dp, int64_t lddp, uint16_t* __restrict__ ds, int64_t ldds, int RBW) {
+  using St = SmxTile<BITS, G, NW>;
+  constexpr int NP = St::NP, RT = R > 0 ? R / 16 : 1, E = G / 4;
+  extern __shared__ __attribute__((aligned(16))) unsigned char sm[];  // [2][TILE], red
+  float* red = reinterpret_cast<float*>(sm + 2 * St::TILE);          // [NW][16]
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int nrb = (M + 15) / 16;
+  const int rb0 = blockIdx.x * RBW;
+  if (rb0 >= nrb) return;  // whole workgroup
+  const int nblk = min(RBW, nrb - rb0);
+  const int u = w;
+
+  u32x2 vop[NP][G / 16][RT];
+  if constexpr (R > 0) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, u, N, NP, G), j, g, vop[p]);
+  }
+  struct Cin {
+    u32x4 cb[G / 64];
+    uint32_t qp[NP];
+    u32x2 lop[RT];
+  };
+  constexpr int kC = G / 64 + 1 + (R > 0 ? RT : 0);  // loads of one cload
+  auto cload = [&](Cin& c, int rb) {
+    const int64_t row = min(rb * 16 + j, M - 1);
+#pragma unroll
+    for (int i = 0; i < G / 64; ++i) c.cb[i] = ld16_stream(codes + row * ldc + u * G + E * g + 16 * i);
+    if constexpr (NP == 2) {
+      const u32x2 q = ld8(qparams + row * ldq + u * 4);
+      c.qp[0] = q[0];
+      c.qp[1] = q[1];
+    } else {
+      c.qp[0] = ld4(qparams + row * ldq + u * 2);
+    }
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t) c.lop[t] = ld8(Lin + row * ldl + 16 * t + 4 * g);
+    }
+  };
+  const unsigned char* dpb = reinterpret_cast<const unsigned char*>(dp);
+  unsigned char* dsb = reinterpret_cast<unsigned char*>(ds);
+  auto dma = [&](int rb, int tb) {
+    unsigned char* tile = sm + tb * St::TILE;
+#pragma unroll
+    for (int i = 0; i < St::DPW; ++i) {
+      const int q = w * St::DPW + i, r = q / St::CPR, c = q % St::CPR;
+      const int64_t row = min(rb * 16 + r, M - 1);
+      ld16_to_lds(dpb + row * lddp * 2 + c * 1024 + lane * 16, tile + r * St::PITCH + c * 1024);
+    }
+  };
+  auto store_tile = [&](int rb, int tb) {
+    const unsigned char* tile = sm + tb * St::TILE;
+#pragma unroll
+    for (int i = 0; i < St::SPT; ++i) {
+      const int k = tid + NW * 64 * i, r = k / (St::ROWB / 16), c16 = k % (St::ROWB / 16);
+      const u32x4 v = *reinterpret_cast<const u32x4*>(tile + r * St::PITCH + c16 * 16);
+      const int64_t row = min(rb * 16 + r, M - 1);
+      st16_stream(dsb + row * ldds * 2 + c16 * 16, v);
+    }
+  };
+  // the lane's bf16 columns of plane p, k-th 8-column piece, in the tile
+  auto tpos = [&](unsigned char* tile, int p, int k) {
+    return reinterpret_cast<u32x4*>(tile + j * St::PITCH + (unit_base(p, u, N, NP, G) + E * g + 8 * k) * 2);
+  };
+  auto compute = [&](const Cin& c, int tb) {
+    unsigned char* tile = sm + tb * St::TILE;
+    u32x4 pb[NP][G / 32];  // P = bf16(decode), packed (exact)
+    float part = 0.f;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      float pv[E];
+      reconstruct_plane<BITS, G, R>(c.cb, c.qp[p], p, vop[p], c.lop, pv);
+#pragma unroll
+      for (int k = 0; k < G / 32; ++k) {
+        pb[p][k] = pack8(pv + 8 * k);
+        float pr[8], dv[8];
+        unpack8(pb[p][k], pr);
+        unpack8(*tpos(tile, p, k), dv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) part = __builtin_fmaf(pr[e], dv[e], part);
+      }
+    }
+    {
+      float a = part, b = part;
+      swap32(a, b);
+      part = a + b;
+      a = part, b = part;
+      swap16(a, b);
+      part = a + b;
+    }
+    if (g == 0) red[w * 16 + j] = part;
+    lds_barrier();
+    float sum = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2) sum += red[w2 * 16 + j];
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int k = 0; k < G / 32; ++k) {
+        float pr[8], dv[8], o[8];
+        unpack8(pb[p][k], pr);
+        unpack8(*tpos(tile, p, k), dv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = pr[e] * (dv[e] - sum);
+        *tpos(tile, p, k) = pack8(o);
+      }
+  };
+  auto step = [&](Cin& cur, Cin& nxt, int b) {
+    const int tb = b & 1;
+    // block b's dP loads are done: after them this wave issued only block b's cload (kC loads);
+    // vmcnt retires in issue order on gfx9
+    __builtin_amdgcn_s_waitcnt(0x0f70 | kC);
+    lds_barrier();
+    if (b > 0) store_tile(rb0 + b - 1, tb ^ 1);
+    if (b + 1 < nblk) {
+      lds_barrier();  // every wave's reads of tile tb^1 have returned
+      __builtin_amdgcn_sched_barrier(0);
+      dma(rb0 + b + 1, tb ^ 1);
+      __builtin_amdgcn_sched_barrier(0);
+      cload(nxt, rb0 + b + 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    compute(cur, tb);
+  };
+  static_assert(kC < 16, "vmcnt immediate");
+  Cin cin[2];
+  dma(rb0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  cload(cin[0], rb0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll 1
+  for (int b = 0; b < nblk; b += 2) {
+    step(cin[0], cin[1], b);
+    if (b + 1 < nblk) step(cin[1], cin[0], b + 1);
+  }
+  lds_barrier();
+  store_tile(rb0 + nblk - 1, (nblk - 1) & 1);
+}
+
 // ------------------------------------------------------------------ dequant-GEMM
 // Grid: ceil(row blocks / RBW); NW waves; wave w takes units w, w + NW, ...; for each unit
 // it decodes the RBW row blocks and multiplies them into its partial out tiles (A's MFMA
@@ -227,10 +396,39 @@ static int softmax_launch(const lrq_tensors* t, const void* dp, int64_t lddp, vo
   return launch_status();
 }
 
-// One pass needs the whole row in one workgroup: 4, 8 or 16 units (one per wave).
+template <int BITS, int G, int R, int NW>
+static int softmax_rows_launch(const lrq_tensors* t, const void* dp, int64_t lddp, void* ds, int64_t ldds,
+                               hipStream_t s) {
+  using St = SmxTile<BITS, G, NW>;
+  const int M = (int)t->rows, N = (int)t->hidden;
+  const int nrb = (M + 15) / 16;
+  const int per_cu = std::max(1, std::min(4, (int)((160 * 1024) / St::LDS)));
+  const int wgs = std::max(1, std::min(nrb, cu_count() * per_cu));
+  const int rbw = (nrb + wgs - 1) / wgs;
+  auto kern = k_softmax_rows<BITS, G, R, NW>;
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)St::LDS);
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL(kern, dim3((nrb + rbw - 1) / rbw), dim3(NW * 64), St::LDS, s, (const uint8_t*)t->codes,
+                     t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp, (const uint16_t*)t->L, t->ld_L,
+                     (const uint16_t*)t->V, M, N, (const uint16_t*)dp, lddp, (uint16_t*)ds, ldds, rbw);
+  return launch_status();
+}
+
+// One pass needs the whole row in one workgroup: 4, 8 or 16 units (one per wave).  Rows of
+// whole 1 KB chunks take the row-persistent kernel.
 template <int BITS, int G, int R>
 static int softmax_units(const lrq_tensors* t, const void* dp, int64_t lddp, void* ds, int64_t ldds, hipStream_t s) {
   const int64_t units = t->hidden / ((int64_t)G * (8 / BITS));
+  constexpr int UB = G * (8 / BITS) * 2;  // bf16 bytes of one unit of a row
+  if ((units == 16 && (16 * UB) % 1024 == 0) || (units == 8 && (8 * UB) % 1024 == 0)) {
+    if (units == 16) {
+      if constexpr ((16 * UB) % 1024 == 0 && 2 * 16 * (16 * UB + 16) + 1024 <= 160 * 1024)
+        return softmax_rows_launch<BITS, G, R, 16>(t, dp, lddp, ds, ldds, s);
+    } else {
+      if constexpr ((8 * UB) % 1024 == 0 && 2 * 16 * (8 * UB + 16) + 512 <= 160 * 1024)
+        return softmax_rows_launch<BITS, G, R, 8>(t, dp, lddp, ds, ldds, s);
+    }
+  }
   switch (units) {
     case 4: return softmax_launch<BITS, G, R, 4, 1>(t, dp, lddp, ds, ldds, s);
     case 8: return softmax_launch<BITS, G, R, 8, 1>(t, dp, lddp, ds, ldds, s);
