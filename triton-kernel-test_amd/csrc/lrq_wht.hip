@@ -19,6 +19,8 @@
 #include "lrq_common.h"
 #include "lrq_host.h"
 
+#include <algorithm>
+
 namespace lrq {
 
 // A operand of tile parity q0 for lane (i, kg): 8 bf16 signs for e = 0..7.
@@ -84,6 +86,91 @@ __global__ __launch_bounds__(256) void k_wht128(const uint16_t* x, int64_t ldx, 
   }
 }
 
+// Row-persistent form for hidden % 512 == 0: a workgroup of 4 waves owns a 512-column slab
+// (wave w: 128-column block w of the slab) for a range of row blocks.  Each block's 16 x 1 KB
+// slice moves straight from HBM into an LDS tile (two tiles, block b in tile b&1), each wave
+// reads its block in the lane layout above, rotates it and writes the result over the same
+// positions; after the next barrier the workgroup stores the tile as whole 1 KB row segments
+// (non-temporal, full lines).  Per block: wait for block b's loads + barrier -> store block
+// b-1 -> barrier (its tile reads returned) -> load block b+1 into that tile -> rotate block b.
+// In place (x == y) is safe: a block is stored only after all of it has been read, and other
+// blocks touch other rows.  Rows past the end repeat the last row (identical stores).
+__global__ __launch_bounds__(256) void k_wht_rows(const uint16_t* x, int64_t ldx, int M, uint16_t* y, int64_t ldy,
+                                                  int RBW) {
+  constexpr int PITCH = 1024 + 16, TILE = 16 * PITCH;
+  __shared__ __attribute__((aligned(16))) unsigned char sm[2 * TILE];
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int nrb = (M + 15) / 16;
+  const int rb0 = blockIdx.x * RBW;
+  if (rb0 >= nrb) return;  // whole workgroup
+  const int nblk = min(RBW, nrb - rb0);
+  const int64_t c0 = (int64_t)blockIdx.y * 512;  // slab's first column
+  u32x4 op[2][2];  // [q0][negated]
+#pragma unroll
+  for (int q0 = 0; q0 < 2; ++q0)
+#pragma unroll
+    for (int n = 0; n < 2; ++n) op[q0][n] = wht_base_operand(j, g, q0, n != 0);
+  const float kScale = 0.08838834764831845f;  // fp32(1/sqrt(128))
+  const unsigned char* xb = reinterpret_cast<const unsigned char*>(x + c0);
+  unsigned char* yb = reinterpret_cast<unsigned char*>(y + c0);
+  auto dma = [&](int rb, int tb) {  // wave w loads rows 4w .. 4w+3
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * w + i;
+      const int64_t row = min(rb * 16 + r, M - 1);
+      ld16_to_lds(xb + row * ldx * 2 + lane * 16, sm + tb * TILE + r * PITCH);
+    }
+  };
+  auto store_tile = [&](int rb, int tb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = tid + 256 * i, r = k >> 6, c16 = k & 63;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(sm + tb * TILE + r * PITCH + c16 * 16);
+      const int64_t row = min(rb * 16 + r, M - 1);
+      st16_stream(yb + row * ldy * 2 + c16 * 16, v);
+    }
+  };
+  auto rotate = [&](int tb) {
+    unsigned char* base = sm + tb * TILE + j * PITCH + (128 * w + 32 * g) * 2;
+    u32x4 xv[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) xv[c] = *reinterpret_cast<const u32x4*>(base + 16 * c);
+    float out[32];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int flip = (((q >> 1) & c & 1) ^ ((q >> 2) & (c >> 1) & 1));
+        acc = mfma_16x16x32(op[q & 1][flip], xv[c], acc);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) out[4 * q + v] = acc[v] * kScale;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) *reinterpret_cast<u32x4*>(base + 16 * k) = pack8(out + 8 * k);
+  };
+  dma(rb0, 0);
+#pragma unroll 1
+  for (int b = 0; b < nblk; ++b) {
+    const int tb = b & 1;
+    // block b's loads are this wave's last memory operations (vmcnt retires in issue order)
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    lds_barrier();
+    if (b > 0) store_tile(rb0 + b - 1, tb ^ 1);
+    if (b + 1 < nblk) {
+      lds_barrier();  // every wave's reads of tile tb^1 have returned
+      __builtin_amdgcn_sched_barrier(0);
+      dma(rb0 + b + 1, tb ^ 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    rotate(tb);
+  }
+  lds_barrier();
+  store_tile(rb0 + nblk - 1, (nblk - 1) & 1);
+}
+
 }  // namespace lrq
 
 using namespace lrq;
@@ -103,6 +190,16 @@ extern "C" int lrq_wht128(const void* x, int64_t ldx, int64_t rows, int64_t hidd
     return LRQ_ERR_SHAPE;
   }
   if (rows == 0) return LRQ_OK;
+  if (hidden % 512 == 0) {
+    // about 4 workgroups per CU over (row ranges, 512-column slabs)
+    const int nrb = (int)((rows + 15) / 16);
+    const int slabs = (int)(hidden / 512);
+    const int ranges = std::max(1, std::min(nrb, cu_count() * 4 / slabs));
+    const int rbw = (nrb + ranges - 1) / ranges;
+    hipLaunchKernelGGL(k_wht_rows, dim3((nrb + rbw - 1) / rbw, slabs), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)x, ldx, (int)rows, (uint16_t*)y, ldy, rbw);
+    return launch_status();
+  }
   constexpr int RBW = 4;
   const int nrb = (int)((rows + 15) / 16);
   const int nblk = (int)(hidden / 128);
