@@ -141,10 +141,32 @@ def test_fused_elementwise(pkg, dev, op):
     print(f"[fused {op}] {rep}", flush=True)
 
 
-def test_outlier_channels_c3_shape(pkg, dev):
+@pytest.mark.parametrize("rows,bits,group", [
+    (96, 4, 128),    # 128-column groups: dY staged in place, 4 waves
+    (96, 8, 128),    # int8 / g128: in place, 8 waves
+    (5000, 8, 128),  # several row blocks per workgroup through the in-place pipeline
+])
+def test_fused_gelu_g128(pkg, dev, rows, bits, group):
+    hidden, rank = 4096, 16
+    print(f"[fused gelu g128] rows={rows} bits={bits}", flush=True)
+    x = pkg.inputs.activation(rows, hidden, 8, 20.0, seed=rows)
+    V = pkg.inputs.basis(hidden, rank, seed=12)
+    dy = pkg.inputs.gradient((rows, hidden), 0.02, seed=rows)
+    c = pkg.encode(x.to(dev), V.to(dev), bits=bits, group_size=group)
+    out = pkg.gelu_backward_compressed(c, dy.to(dev))
+    torch.cuda.synchronize()
+    xh = O.bf16_to_f32(O.decode(bits16(c.L), bits16(V), c.codes.cpu().numpy(), f16(c.scale), f16(c.zero),
+                                bits, group))
+    ref = O.gelu_bwd(xh, O.bf16_to_f32(bits16(dy)))
+    rep = assert_fp_close(bits16(out), ref, "fused gelu g128")
+    print(f"[fused gelu g128] {rep}", flush=True)
+
+
+@pytest.mark.parametrize("rows", [512, 4100])  # 4100: several row blocks per workgroup, ragged
+def test_outlier_channels_c3_shape(pkg, dev, rows):
     """Config 3 recipe at reduced rows: top-41 channels by abs-max, rank 0, int8/g128, GELU bwd."""
     cfg = pkg.inputs.CONFIGS["c3"]
-    inp = pkg.inputs.make(cfg, rows=512)
+    inp = pkg.inputs.make(cfg, rows=rows)
     x = inp["x"]
     print("[c3] colmax/topk", flush=True)
     xd = x.to(dev)

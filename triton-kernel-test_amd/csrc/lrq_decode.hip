@@ -396,7 +396,7 @@ struct RowsOut {
   static_assert(OCH % (NW * 64) == 0, "tile chunks split evenly over the workgroup");
 };
 
-template <int BITS, int G, int R, int NW, bool IN, bool OUTL>
+template <int BITS, int G, int R, int NW, bool IN, bool OUTL, bool INP = false>
 struct RowsLayout {
   using Tl = StagedTile<BITS, G, R, NW>;
   using Ro = RowsOut<BITS, G, NW>;
@@ -405,27 +405,29 @@ struct RowsLayout {
   static constexpr int SIDE = OUTL ? 16 * kSideMax * 2 : 0;    // side columns per block
   static constexpr int SPT = OUTL ? (16 * kSideMax + T - 1) / T : 0;
   static constexpr int ISLOT = Tl::SLOT + SIDE;                // staged inputs per block
-  static constexpr size_t FIXED = 2 * (size_t)ISLOT + (IN ? 2 : 0) * (size_t)Ro::OSLOT + 2 * (size_t)Ro::OSLOT;
+  // IN && !INP: dY has tiles of its own; INP: dY is staged into the output tiles (in place)
+  static constexpr size_t FIXED = 2 * (size_t)ISLOT + (IN && !INP ? 2 : 0) * (size_t)Ro::OSLOT + 2 * (size_t)Ro::OSLOT;
   static size_t bytes(int N) { return FIXED + (OUTL ? (size_t)(N / 32) * 4 + (size_t)N * 2 : 0); }
   // registers a block's prefetched inputs take per lane (drives the largest RBW)
   static constexpr int kRegsPerBlock = 4 * Tl::CPT + 2 + (IN ? 4 * DPT : 0) + SPT;
 };
 
-template <int BITS, int G, int R, int NW, int PD, bool OUTL, class EPI>
+template <int BITS, int G, int R, int NW, int PD, bool OUTL, bool INP, class EPI>
 __global__ __launch_bounds__(NW * 64) void k_decode_rows(
     const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
     const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
     const int32_t* __restrict__ oidx, int nout, const uint16_t* __restrict__ side, int64_t ldside, EPI epi,
     int RBW) {
   constexpr bool IN = EPI::kIn;
-  using Lay = RowsLayout<BITS, G, R, NW, IN, OUTL>;
+  static_assert(!INP || IN, "in-place staging is for consumers");
+  using Lay = RowsLayout<BITS, G, R, NW, IN, OUTL, INP>;
   using Tl = typename Lay::Tl;
   using Ro = typename Lay::Ro;
   constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, E = G / 4, T = Lay::T;
   extern __shared__ __attribute__((aligned(16))) unsigned char sm[];
   unsigned char* ism = sm;                                   // [2][ISLOT] staged codes/qparams/L/side
-  unsigned char* dsm = sm + 2 * Lay::ISLOT;                  // [2][OSLOT] input tiles (IN)
-  unsigned char* osm = dsm + (IN ? 2 : 0) * Ro::OSLOT;       // [2][OSLOT] output tiles
+  unsigned char* osm = sm + 2 * Lay::ISLOT + (IN && !INP ? 2 : 0) * Ro::OSLOT;  // [2][OSLOT] output tiles
+  unsigned char* dsm = INP ? osm : sm + 2 * Lay::ISLOT;      // [2][OSLOT] input tiles (IN)
   uint32_t* colmask = reinterpret_cast<uint32_t*>(osm + 2 * Ro::OSLOT);  // OUTL: N/32 words
   int16_t* oslot = reinterpret_cast<int16_t*>(colmask + N / 32);         // OUTL: N entries
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -597,6 +599,9 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
     stage(in[k], b);
     lds_barrier();
     if (b > 0) store_tile(rb - 1, b - 1);
+    // in place: block b + 1's dY goes into the tile just stored, so every wave's reads of it
+    // must have returned first
+    if constexpr (INP) lds_barrier();
     if (b + PD < nblk) {
       __builtin_amdgcn_sched_barrier(0);
       load(in[k], rb + PD);
@@ -656,8 +661,8 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
 // ------------------------------------------------------------------ host side
 // Waves per workgroup for k_decode_rows: NW * G = 512 columns, so each row segment is 1 KB (one
 // 16-byte vector per lane) and the tiles plus two input slots fit in LDS.
-template <int G>
-constexpr int rows_nw() { return 512 / G; }
+template <int BITS, int G>
+constexpr int rows_nw() { return G * (8 / BITS) <= 128 ? 8 : 4; }
 
 // One workgroup per CU: the workgroups of a unit group split its row blocks into runs of RBW
 // consecutive blocks, RBW being the smallest run that keeps the grid within one round.  The ring
@@ -666,8 +671,10 @@ constexpr int rows_nw() { return 512 / G; }
 // need the rest).
 template <int BITS, int G, int R, bool OUTL, class EPI>
 static int decode_rows_launch(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
-  constexpr int NW = rows_nw<G>();
-  using Lay = RowsLayout<BITS, G, R, NW, EPI::kIn, OUTL>;
+  constexpr int NW = rows_nw<BITS, G>();
+  // consumers of 128-column groups stage dY in place (separate tiles would not fit in LDS)
+  constexpr bool INP = EPI::kIn && G == 128;
+  using Lay = RowsLayout<BITS, G, R, NW, EPI::kIn, OUTL, INP>;
   constexpr int kBudget = EPI::kIn ? 100 : R == 32 ? 160 : 180;
   constexpr int kFit = kBudget / Lay::kRegsPerBlock;
   constexpr int PD = kFit >= 16 ? 16 : kFit >= 8 ? 8 : kFit >= 4 ? 4 : 2;
@@ -678,7 +685,7 @@ static int decode_rows_launch(const lrq_tensors* t, hipStream_t s, const EPI& ep
   const int rbw = (int)((nrb + per - 1) / per);
   const size_t shm = Lay::bytes(N);
   if (shm > 160 * 1024) return LRQ_ERR_UNSUPPORTED;
-  auto kern = k_decode_rows<BITS, G, R, NW, PD, OUTL, EPI>;
+  auto kern = k_decode_rows<BITS, G, R, NW, PD, OUTL, INP, EPI>;
   if (shm > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
   hipLaunchKernelGGL(kern, dim3((unsigned)((nrb + rbw - 1) / rbw), (unsigned)ug), dim3(NW * 64), shm, s,
                      (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
@@ -714,18 +721,14 @@ static int decode_launch_rbw(const lrq_tensors* t, hipStream_t s, const EPI& epi
 template <int BITS, int G, int R, class EPI>
 static int decode_launch(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
   constexpr int NP = 8 / BITS, NW = 8, BIG = EPI::kIn ? 4 : 8;
-  // Consumers of G = 128 groups keep the two-workgroups-per-CU kernels: at NW = 4 the row kernel
-  // would run four waves per CU.
   // The row kernel addresses a block's rows by 32-bit offsets: 16 rows of every operand must
   // stay below 2^31 bytes (always true for real hidden sizes; the others take the tile kernels).
   bool off32 = true;
   for (int64_t ldb : {t->ld_codes, 2 * t->ld_qp, 2 * t->ld_L, 2 * epi.in_ld(), 2 * epi.out_ld()})
     off32 = off32 && 16 * ldb < ((int64_t)1 << 31);
-  if constexpr (!(EPI::kIn && G == 128)) {
-    if (off32 && t->n_outlier == 0) return decode_rows_launch<BITS, G, R, false>(t, s, epi);
-    if constexpr (R == 0) {
-      if (off32 && t->n_outlier <= kSideMax) return decode_rows_launch<BITS, G, R, true>(t, s, epi);
-    }
+  if (off32 && t->n_outlier == 0) return decode_rows_launch<BITS, G, R, false>(t, s, epi);
+  if constexpr (R == 0) {
+    if (off32 && t->n_outlier <= kSideMax) return decode_rows_launch<BITS, G, R, true>(t, s, epi);
   }
   const int64_t units = t->hidden / (G * NP), nrb = (t->rows + 15) / 16;
   const int64_t wgs = ((nrb + BIG - 1) / BIG) * ((units + NW - 1) / NW);
