@@ -691,22 +691,52 @@ __global__ __launch_bounds__(256) void k_reduce_slabs(const unsigned char* __res
   *reinterpret_cast<u32x2*>(L + row * ldl + 4 * q) = u32x2{pack_bf16x2(sum[0], sum[1]), pack_bf16x2(sum[2], sum[3])};
 }
 
-template <int BITS, int G, int R>
+template <int BITS, int G, int R, bool OUTL>
+struct QuantSlab {
+  static constexpr int NP = 8 / BITS, UPW = 2, NW = 8;
+  static constexpr int PIECE = UPW * G * 2, PITCH = NP * PIECE + 16, PPL = 1024 / PIECE, LPL = 64 / PPL;
+  static constexpr int RPL = PPL / NP, NLD = 16 / RPL;
+  static constexpr size_t REGIONS = (size_t)NW * 16 * PITCH;
+  static size_t bytes(int N) { return REGIONS + (OUTL ? (size_t)(N / 32) * 4 + (size_t)N * 2 : 0); }
+  static_assert(PPL % NP == 0 && NLD * RPL == 16, "whole rows per load");
+};
+
+// Residual and quantisation pass of the column-slab encode (also the whole encode at rank 0).
+// OUTL: outlier columns (oidx) are zeroed before the group statistics, and their bf16 values
+// are written to the fp16 side columns from the slice in LDS (a wave-uniform loop over the
+// wave's outlier columns; one range-checked 2-byte store per row).
+template <int BITS, int G, int R, bool OUTL>
 __global__ __launch_bounds__(512) void k_quant_slab(const uint16_t* __restrict__ X, int64_t ldx, int M, int N,
                                                     const uint16_t* __restrict__ V, const uint16_t* __restrict__ Lin,
                                                     int64_t ldl, uint8_t* __restrict__ codes, int64_t ldc,
-                                                    uint16_t* __restrict__ qparams, int64_t ldq, int nranges,
+                                                    uint16_t* __restrict__ qparams, int64_t ldq,
+                                                    const int32_t* __restrict__ oidx, int nout,
+                                                    uint16_t* __restrict__ side, int64_t ldside, int nranges,
                                                     int RBW) {
-  constexpr int NP = 8 / BITS, UPW = 2, NW = 8, CPG = G / 32, RT = R / 16, E = G / 4;
-  constexpr int PIECE = UPW * G * 2, PITCH = NP * PIECE + 16, PPL = 1024 / PIECE, LPL = 64 / PPL;
-  constexpr int RPL = PPL / NP, NLD = 16 / RPL;
-  static_assert(NP == 2 && PPL % NP == 0 && NLD * RPL == 16, "two planes, whole rows per load");
-  __shared__ __attribute__((aligned(16))) unsigned char shm[NW * 16 * PITCH];
+  using Qs = QuantSlab<BITS, G, R, OUTL>;
+  constexpr int NP = Qs::NP, UPW = Qs::UPW, NW = Qs::NW, CPG = G / 32, RT = R > 0 ? R / 16 : 1, E = G / 4;
+  constexpr int PIECE = Qs::PIECE, PITCH = Qs::PITCH, LPL = Qs::LPL, RPL = Qs::RPL, NLD = Qs::NLD;
+  extern __shared__ __attribute__((aligned(16))) unsigned char shm[];
+  uint32_t* colmask = reinterpret_cast<uint32_t*>(shm + Qs::REGIONS);  // OUTL: N/32 words
+  int16_t* oslot = reinterpret_cast<int16_t*>(colmask + N / 32);      // OUTL: N entries
+  if constexpr (OUTL) {
+    for (int i = threadIdx.x; i < N / 32; i += blockDim.x) colmask[i] = 0u;
+    for (int i = threadIdx.x; i < N; i += blockDim.x) oslot[i] = -1;
+    __syncthreads();
+    for (int k = threadIdx.x; k < nout; k += blockDim.x) {
+      const int c = oidx[k];
+      if (c >= 0 && c < N) {
+        atomicOr(&colmask[c >> 5], 1u << (c & 31));
+        oslot[c] = (int16_t)k;
+      }
+    }
+    __syncthreads();  // the only barrier: waves are independent below
+  }
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
   const int units = N / (G * NP), nwc = units / UPW;
   const int gw = blockIdx.x * NW + w;
-  if (gw >= nranges * nwc) return;  // this wave only (no barriers below)
+  if (gw >= nranges * nwc) return;  // this wave only
   const int ub = UPW * (gw % nwc), rng = gw / nwc;
   const int nrb = (M + 15) / 16;
   const int rb0 = rng * RBW;
@@ -715,10 +745,12 @@ __global__ __launch_bounds__(512) void k_quant_slab(const uint16_t* __restrict__
   unsigned char* region = shm + (size_t)w * 16 * PITCH;
 
   u32x2 vop[UPW][NP][G / 16][RT];
+  if constexpr (R > 0) {
 #pragma unroll
-  for (int uu = 0; uu < UPW; ++uu)
+    for (int uu = 0; uu < UPW; ++uu)
 #pragma unroll
-    for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, ub + uu, N, NP, G), j, g, vop[uu][p]);
+      for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, ub + uu, N, NP, G), j, g, vop[uu][p]);
+  }
 
   // load i: rows RPL*i .. of the block, lane l -> piece l/LPL (row RPL*i + (l/LPL)/NP, plane
   // (l/LPL)%NP) at byte (l%LPL)*16; rows past the end clamp to the last row
@@ -733,9 +765,11 @@ __global__ __launch_bounds__(512) void k_quant_slab(const uint16_t* __restrict__
   auto issue = [&](int rb) {
 #pragma unroll
     for (int i = 0; i < NLD; ++i) pf[i] = ld16_stream(gaddr(rb, i));
-    const int64_t row = min(rb * 16 + j, M - 1);
+    if constexpr (R > 0) {
+      const int64_t row = min(rb * 16 + j, M - 1);
 #pragma unroll
-    for (int t = 0; t < RT; ++t) lnext[t] = ld8(Lin + row * ldl + 16 * t + 4 * g);
+      for (int t = 0; t < RT; ++t) lnext[t] = ld8(Lin + row * ldl + 16 * t + 4 * g);
+    }
   };
   issue(rb0);
 #pragma unroll 1
@@ -753,21 +787,53 @@ __global__ __launch_bounds__(512) void k_quant_slab(const uint16_t* __restrict__
         for (int k = 0; k < CPG; ++k)
           x[uu][p][k] = *reinterpret_cast<const u32x4*>(region + j * PITCH + p * PIECE + (uu * G + E * g + 8 * k) * 2);
     u32x2 lopn[RT];
+    if constexpr (R > 0) {
 #pragma unroll
-    for (int t = 0; t < RT; ++t) lopn[t] = neg_bf16x4(lnext[t]);
+      for (int t = 0; t < RT; ++t) lopn[t] = neg_bf16x4(lnext[t]);
+    }
     if (b + 1 < nblk) issue(rb + 1);
     const int row = min(rb * 16 + j, M - 1);
     uint8_t* crow = codes + (int64_t)row * ldc;
     uint32_t qp[UPW];
 #pragma unroll
-    for (int uu = 0; uu < UPW; ++uu) qp[uu] = quant_unit_regs<BITS, G, R>(x[uu], vop[uu], lopn, ub + uu, g, crow);
-    // the two units' (scale, zero) pairs of the row as one 16-byte store (see k_encode_rows)
-    float a = __uint_as_float(qp[0]), bq = a, c = __uint_as_float(qp[1]), d = c;
-    swap32(a, bq);
-    swap32(c, d);
-    st16_pred(qparams + (int64_t)rb * 16 * ldq, (uint32_t)(16 * ldq * 2),
-              (uint32_t)(((row - rb * 16) * ldq + ub * NP * 2) * 2),
-              u32x4{__float_as_uint(a), __float_as_uint(bq), __float_as_uint(c), __float_as_uint(d)}, g == 0);
+    for (int uu = 0; uu < UPW; ++uu)
+      qp[uu] = quant_unit_core<BITS, G, R>(x[uu], vop[uu], lopn, OUTL ? colmask : nullptr, ub + uu, N, g, crow);
+    if constexpr (NP == 2) {
+      // the two units' (scale, zero) pairs of the row as one 16-byte store (see k_encode_rows)
+      float a = __uint_as_float(qp[0]), bq = a, c = __uint_as_float(qp[1]), d = c;
+      swap32(a, bq);
+      swap32(c, d);
+      st16_pred(qparams + (int64_t)rb * 16 * ldq, (uint32_t)(16 * ldq * 2),
+                (uint32_t)(((row - rb * 16) * ldq + ub * NP * 2) * 2),
+                u32x4{__float_as_uint(a), __float_as_uint(bq), __float_as_uint(c), __float_as_uint(d)}, g == 0);
+    } else {
+      // one plane: every lane of a row holds its unit's pair
+      st8_pred(qparams + (int64_t)rb * 16 * ldq, (uint32_t)(16 * ldq * 2),
+               (uint32_t)(((row - rb * 16) * ldq + ub * 2) * 2), u32x2{qp[0], qp[1]}, g == 0);
+    }
+    if constexpr (OUTL) {
+      // side columns of the wave's units, read from the slice (lanes of quarter 0 store row j)
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc(side + (int64_t)rb * 16 * ldside, (short)0, (int)(16 * ldside * 2), 0x00020000);
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const int cb = unit_base(p, ub, N, NP, G);  // the wave's UPW*G contiguous columns of plane p
+#pragma unroll 1
+        for (int wd = 0; wd < UPW * G / 32; ++wd) {
+          uint32_t bits = __builtin_amdgcn_readfirstlane(colmask[(cb >> 5) + wd]);
+          while (bits != 0u) {
+            const int e = __builtin_ctz(bits);
+            bits &= bits - 1u;
+            const int cl = 32 * wd + e;  // column within the wave's range
+            const int k = oslot[cb + cl];
+            const uint32_t v = *reinterpret_cast<const uint16_t*>(region + j * PITCH + p * PIECE + cl * 2);
+            const uint16_t h = (uint16_t)f16_bits(__uint_as_float(v << 16));
+            __builtin_amdgcn_raw_buffer_store_b16(h, rs, g == 0 ? (uint32_t)(((row - rb * 16) * ldside + k) * 2) : 0x7ffffff0u,
+                                                  0, 0);
+          }
+        }
+      }
+    }
   }
 }
 
@@ -871,25 +937,31 @@ static int encode_persist_dispatch(const lrq_tensors* t, const void* x, int64_t 
   }
 }
 
-// Two-pass encode over column slabs (see k_project_slab).  The slab partials of L live in the
-// codes buffer until the quantisation pass overwrites it: row r's partials take the first
-// nslab*4*R bytes of its codes row.  Returns 0 when the shape does not fit this path.
+// Column-slab encode (see k_project_slab).  Rank > 0: projection partials, their reduction
+// into L, then the quantisation pass; the slab partials of L live in the codes buffer until
+// the quantisation pass overwrites it (row r's partials take the first nslab*4*R bytes of its
+// codes row).  Rank 0: the quantisation pass alone (with outlier channels, it also writes the
+// side columns).  Returns 0 when the shape does not fit this path.
 template <int BITS, int G, int R>
 static int encode_slabs(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s, int* status) {
-  if constexpr (BITS != 4 || R == 0) {
-    return 0;
-  } else {
-    const int M = (int)t->rows, N = (int)t->hidden;
-    constexpr int NP = 2;
-    const int units = N / (G * NP);
-    const int nslab = (N + 2047) / 2048;
+  constexpr int NP = 8 / BITS;
+  const int M = (int)t->rows, N = (int)t->hidden;
+  const int units = N / (G * NP);
+  const int nslab = (N + 2047) / 2048;
+  const bool outl = t->n_outlier > 0;
+  if (units % 2 != 0 || N % 32 != 0) return 0;
+  if (outl && (R > 0 || t->n_outlier > 32767 || t->side == nullptr || t->outlier_idx == nullptr)) return 0;
+  if (NP == 2 ? (t->ld_qp % 8 != 0 || !aligned(t->qparams, 16)) : (t->ld_qp % 4 != 0 || !aligned(t->qparams, 8))) return 0;
+  if ((int64_t)16 * t->ld_qp * 2 >= ((int64_t)1 << 31)) return 0;
+  if (outl && (int64_t)16 * t->ld_side * 2 >= ((int64_t)1 << 31)) return 0;
+  const size_t shm = outl ? QuantSlab<BITS, G, R, true>::bytes(N) : QuantSlab<BITS, G, R, false>::bytes(N);
+  if (shm > 160 * 1024) return 0;
+  const int cus = cu_count();
+  const int nrb = (M + 15) / 16;
+  if constexpr (R > 0) {
     const int64_t ldp = t->ld_codes;  // bytes
-    if (units % 2 != 0 || t->n_outlier != 0 || N % 32 != 0) return 0;
-    if ((int64_t)nslab * 4 * R > (int64_t)N / 2 || ldp % 16 != 0 || !aligned(t->codes, 16)) return 0;
-    if (t->ld_qp % 8 != 0 || !aligned(t->qparams, 16) || t->ld_L % 4 != 0 || !aligned(t->L, 8)) return 0;
-    if ((int64_t)16 * t->ld_qp * 2 >= ((int64_t)1 << 31)) return 0;
-    const int cus = cu_count();
-    const int nrb = (M + 15) / 16;
+    if ((int64_t)nslab * 4 * R > (int64_t)N * BITS / 8 || ldp % 16 != 0 || !aligned(t->codes, 16)) return 0;
+    if (t->ld_L % 4 != 0 || !aligned(t->L, 8)) return 0;
     // pass 1: about one workgroup per CU over (row groups, slabs)
     const int per1 = std::max(1, cus / nslab);
     const int rbw1 = (nrb + per1 - 1) / per1;
@@ -902,17 +974,26 @@ static int encode_slabs(const lrq_tensors* t, const void* x, int64_t ldx, hipStr
                        (const unsigned char*)t->codes, ldp, M, nslab, (uint16_t*)t->L, t->ld_L);
     st = launch_status();
     if (st) { *status = st; return 1; }
-    // pass 2: 8 independent waves per workgroup, one workgroup per CU
-    const int nwc = units / 2;
-    const int nranges = std::max(1, std::min(nrb, cus * 8 / nwc));
-    const int rbw2 = (nrb + nranges - 1) / nranges;
-    const int waves = nranges * nwc;
-    hipLaunchKernelGGL((k_quant_slab<BITS, G, R>), dim3((waves + 7) / 8), dim3(512), 0, s, (const uint16_t*)x, ldx,
-                       M, N, (const uint16_t*)t->V, (const uint16_t*)t->L, t->ld_L, (uint8_t*)t->codes, t->ld_codes,
-                       (uint16_t*)t->qparams, t->ld_qp, nranges, rbw2);
-    *status = launch_status();
-    return 1;
   }
+  // quantisation pass: 8 independent waves per workgroup, one workgroup per CU
+  const int nwc = units / 2;
+  const int nranges = std::max(1, std::min(nrb, cus * 8 / nwc));
+  const int rbw2 = (nrb + nranges - 1) / nranges;
+  const int waves = nranges * nwc;
+  auto launch = [&](auto kern) {
+    if (shm > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    hipLaunchKernelGGL(kern, dim3((waves + 7) / 8), dim3(512), shm, s, (const uint16_t*)x, ldx, M, N,
+                       (const uint16_t*)t->V, (const uint16_t*)t->L, t->ld_L, (uint8_t*)t->codes, t->ld_codes,
+                       (uint16_t*)t->qparams, t->ld_qp, t->outlier_idx, (int)t->n_outlier, (uint16_t*)t->side,
+                       t->ld_side, nranges, rbw2);
+  };
+  if (outl) {
+    if constexpr (R == 0) launch(k_quant_slab<BITS, G, R, true>);
+  } else {
+    launch(k_quant_slab<BITS, G, R, false>);
+  }
+  *status = launch_status();
+  return 1;
 }
 
 template <int BITS, int G, int R>
