@@ -11,6 +11,7 @@
 #include "lrq_common.h"
 #include "lrq_host.h"
 #include "lrq_dequant.h"
+#include "lrq_whtop.h"
 #include "lrq_math.h"
 
 #include <algorithm>
@@ -25,7 +26,7 @@ namespace lrq {
 // the codes: on gfx9 one in-order counter tracks loads and stores, so a load issued after
 // a row block's stores could only be consumed once those stores had completed.
 struct EpiStore {
-  static constexpr bool kIn = false;
+  static constexpr bool kIn = false, kRot = false;
   uint16_t* out;
   int64_t ld;
   __device__ __forceinline__ const uint16_t* in_row(int64_t) const { return nullptr; }
@@ -35,9 +36,15 @@ struct EpiStore {
   __device__ __forceinline__ u32x4 apply(const float* xh, u32x4) const { return pack8(xh); }
 };
 
+// EpiStore followed by the inverse of the rotated format's rotation: the row kernel rotates
+// each 128-column block of the bf16 output tile in LDS before storing it (x = WHT(bf16(Y'))).
+struct EpiStoreRot : EpiStore {
+  static constexpr bool kRot = true;
+};
+
 // silu_backward.py:6-8 on x = bf16(x_hat), fp32 (lrq_math.h).
 struct EpiSilu {
-  static constexpr bool kIn = true;
+  static constexpr bool kIn = true, kRot = false;
   const uint16_t* dy;
   int64_t lddy;
   uint16_t* dx;
@@ -57,7 +64,7 @@ struct EpiSilu {
 
 // gelu_backward.py:14-21 (tanh approximation) on x = bf16(x_hat), fp32 (lrq_math.h).
 struct EpiGelu {
-  static constexpr bool kIn = true;
+  static constexpr bool kIn = true, kRot = false;
   const uint16_t* dy;
   int64_t lddy;
   uint16_t* dx;
@@ -77,7 +84,7 @@ struct EpiGelu {
 
 // extraction_fuse_hadamard.py:5-6: x * y.
 struct EpiMul {
-  static constexpr bool kIn = true;
+  static constexpr bool kIn = true, kRot = false;
   const uint16_t* y;
   int64_t ldy;
   uint16_t* out;
@@ -583,6 +590,21 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
   // stores (a store queued behind loads waits for them), so each iteration's traffic is
   // [stores of b - 1, loads of b + PD].  With PD >= the workgroup's blocks every load is issued
   // before the first store.
+  // rotated output (EPI::kRot): wave w rotates 128-column block w of the tile (plane
+  // w / (NW*G/128), block w % (NW*G/128) of that plane's row segment) once every wave's unit
+  // is in the tile; blocks that reach past the workgroup's units are left alone (never stored)
+  constexpr int RPP = NW * G / 128;  // rotation blocks per plane of a tile row
+  static_assert(!EPI::kRot || (NP * RPP == NW && G % 64 == 0), "one rotation block per wave");
+  u32x4 wop[EPI::kRot ? 2 : 1][2];
+  if constexpr (EPI::kRot) {
+#pragma unroll
+    for (int q0 = 0; q0 < 2; ++q0)
+#pragma unroll
+      for (int n = 0; n < 2; ++n) wop[q0][n] = wht_base_operand(j, g, q0, n != 0);
+  }
+  const int rot_p = w / RPP, rot_q = w % RPP;
+  const bool rot_live = (rot_q + 1) * (128 / G) <= nu;  // the block's units are all present
+
   In in[PD];
 #pragma unroll
   for (int b = 0; b < PD; ++b)
@@ -652,6 +674,11 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
         }
       }
     }
+    if constexpr (EPI::kRot) {
+      lds_barrier();  // every wave's unit of block b is in the tile
+      if (rot_live)
+        wht128_lds(osm + (b & 1) * Ro::OSLOT + (rot_p * 16 + j) * Ro::OPAD + (128 * rot_q + 32 * g) * 2, wop);
+    }
   }
   }
   lds_barrier();
@@ -675,7 +702,7 @@ static int decode_rows_launch(const lrq_tensors* t, hipStream_t s, const EPI& ep
   // consumers of 128-column groups stage dY in place (separate tiles would not fit in LDS)
   constexpr bool INP = EPI::kIn && G == 128;
   using Lay = RowsLayout<BITS, G, R, NW, EPI::kIn, OUTL, INP>;
-  constexpr int kBudget = EPI::kIn ? 100 : R == 32 ? 160 : 180;
+  constexpr int kBudget = EPI::kIn ? 100 : EPI::kRot ? 150 : R == 32 ? 160 : 180;
   constexpr int kFit = kBudget / Lay::kRegsPerBlock;
   constexpr int PD = kFit >= 16 ? 16 : kFit >= 8 ? 8 : kFit >= 4 ? 4 : 2;
   const int M = (int)t->rows, N = (int)t->hidden;
@@ -768,12 +795,48 @@ static int check_io(const lrq_tensors* t, const void* in, int64_t ldin, const vo
 
 using namespace lrq;
 
+namespace lrq {
+// Rotated format, fused: the row kernel undoes the rotation on its LDS output tile.  Formats
+// with one 128-column rotation block per wave (int4/g64, int8/g128), no outlier channels, and
+// planes that are whole rotation blocks; returns 0 for the others.
+template <int BITS, int G, int R>
+static int decode_rot_fused(const lrq_tensors* t, hipStream_t s, uint16_t* out, int64_t ldo, int* status) {
+  if constexpr (!((BITS == 4 && G == 64) || (BITS == 8 && G == 128))) {
+    return 0;
+  } else {
+    const int64_t plane = t->hidden / (8 / BITS);
+    if (t->n_outlier != 0 || plane % 128 != 0) return 0;
+    for (int64_t ldb : {t->ld_codes, 2 * t->ld_qp, 2 * t->ld_L, 2 * ldo})
+      if (16 * ldb >= ((int64_t)1 << 31)) return 0;
+    lrq_tensors plain = *t;
+    plain.flags &= ~LRQ_FLAG_HADAMARD;
+    EpiStoreRot epi;
+    epi.out = out;
+    epi.ld = ldo;
+    *status = decode_rows_launch<BITS, G, R, false>(&plain, s, epi);
+    return 1;
+  }
+}
+
+static int decode_rot(const lrq_tensors* t, hipStream_t s, uint16_t* out, int64_t ldo, int* status) {
+  switch (format_key(t->bits, t->group, t->rank)) {
+    case format_key(4, 64, 0): return decode_rot_fused<4, 64, 0>(t, s, out, ldo, status);
+    case format_key(4, 64, 16): return decode_rot_fused<4, 64, 16>(t, s, out, ldo, status);
+    case format_key(4, 64, 32): return decode_rot_fused<4, 64, 32>(t, s, out, ldo, status);
+    case format_key(8, 128, 0): return decode_rot_fused<8, 128, 0>(t, s, out, ldo, status);
+    case format_key(8, 128, 16): return decode_rot_fused<8, 128, 16>(t, s, out, ldo, status);
+    default: return 0;
+  }
+}
+}  // namespace lrq
+
 extern "C" int lrq_decode(const lrq_tensors* t, void* out, int64_t ldo, void* stream) {
   int st = check_io(t, nullptr, 0, out, ldo, false);
   if (st) return st;
   if (t->rows == 0) return LRQ_OK;
   if (t->flags & LRQ_FLAG_HADAMARD) {
-    // rotated format: decode, then undo the rotation in place (the rotation is its own inverse)
+    if (decode_rot(t, (hipStream_t)stream, (uint16_t*)out, ldo, &st)) return st;
+    // otherwise decode, then undo the rotation in place (the rotation is its own inverse)
     lrq_tensors plain = *t;
     plain.flags &= ~LRQ_FLAG_HADAMARD;
     st = decode_dispatch(&plain, (hipStream_t)stream, EpiStore{(uint16_t*)out, ldo});

@@ -18,28 +18,11 @@
 // two register operands and their negations serve all 32 MFMAs of a block.
 #include "lrq_common.h"
 #include "lrq_host.h"
+#include "lrq_whtop.h"
 
 #include <algorithm>
 
 namespace lrq {
-
-// A operand of tile parity q0 for lane (i, kg): 8 bf16 signs for e = 0..7.
-__device__ __forceinline__ u32x4 wht_base_operand(int i, int kg, int q0, bool neg) {
-  const int v = i & 3, gp = i >> 2;
-  uint32_t w[4];
-#pragma unroll
-  for (int h = 0; h < 4; ++h) {
-    uint32_t pair = 0;
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int e = 2 * h + s;
-      const int par = (__builtin_popcount(v & e & 3) + (q0 & (e >> 2)) + __builtin_popcount(gp & kg) + (neg ? 1 : 0)) & 1;
-      pair |= (par ? 0xbf80u : 0x3f80u) << (16 * s);
-    }
-    w[h] = pair;
-  }
-  return u32x4{w[0], w[1], w[2], w[3]};
-}
 
 // Grid: (ceil(row blocks / RBW), ceil(blocks per row / 4)); 4 waves, wave w on 128-column block
 // blockIdx.y * 4 + w (idle past the end; no barrier follows).  In-place (x == y) is safe: a
@@ -111,7 +94,6 @@ __global__ __launch_bounds__(256) void k_wht_rows(const uint16_t* x, int64_t ldx
   for (int q0 = 0; q0 < 2; ++q0)
 #pragma unroll
     for (int n = 0; n < 2; ++n) op[q0][n] = wht_base_operand(j, g, q0, n != 0);
-  const float kScale = 0.08838834764831845f;  // fp32(1/sqrt(128))
   const unsigned char* xb = reinterpret_cast<const unsigned char*>(x + c0);
   unsigned char* yb = reinterpret_cast<unsigned char*>(y + c0);
   auto dma = [&](int rb, int tb) {  // wave w loads rows 4w .. 4w+3
@@ -131,26 +113,7 @@ __global__ __launch_bounds__(256) void k_wht_rows(const uint16_t* x, int64_t ldx
       st16_stream(yb + row * ldy * 2 + c16 * 16, v);
     }
   };
-  auto rotate = [&](int tb) {
-    unsigned char* base = sm + tb * TILE + j * PITCH + (128 * w + 32 * g) * 2;
-    u32x4 xv[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) xv[c] = *reinterpret_cast<const u32x4*>(base + 16 * c);
-    float out[32];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      f32x4 acc = zero4();
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int flip = (((q >> 1) & c & 1) ^ ((q >> 2) & (c >> 1) & 1));
-        acc = mfma_16x16x32(op[q & 1][flip], xv[c], acc);
-      }
-#pragma unroll
-      for (int v = 0; v < 4; ++v) out[4 * q + v] = acc[v] * kScale;
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) *reinterpret_cast<u32x4*>(base + 16 * k) = pack8(out + 8 * k);
-  };
+  auto rotate = [&](int tb) { wht128_lds(sm + tb * TILE + j * PITCH + (128 * w + 32 * g) * 2, op); };
   dma(rb0, 0);
 #pragma unroll 1
   for (int b = 0; b < nblk; ++b) {
