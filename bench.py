@@ -167,14 +167,25 @@ def build_plan(cfg, pkg, lib, dev, nbuf):
                         2 * M * N, 0))
         entries.append(("topk", lambda k: lib.lrq_topk(P(sets[k]["cm"]), N, side, c_void_p(sets[k]["c"].idx.data_ptr()),
                                                        sp), 4 * N, 0))
+    enc_flops = 4 * M * N * r
+    src = "x"
     if cfg.hadamard:
-        entries.append(("wht128", lambda k: lib.lrq_wht128(P(sets[k]["x"]), N, M, N, P(sets[k]["y"]), N, sp),
-                        4 * M * N, 2 * M * N * 128))
-        src = "y"
-    else:
-        src = "x"
+        # rotated format: the library's encode rotates x as it reads it where it can (flagged
+        # descriptor); otherwise a separate rotation pass into y, then the plain encode of y
+        flag = importlib.import_module("triton-kernel-test_amd._lib").LRQ_FLAG_HADAMARD
+        for st_ in sets:
+            st_["enc"].flags = flag
+        if lib.lrq_encode(B(sets[0]["enc"]), P(sets[0]["x"]), N, sp) == 0:
+            enc_flops += 2 * M * N * 128
+        else:
+            for st_ in sets:
+                st_["enc"].flags = 0
+            entries.append(("wht128", lambda k: lib.lrq_wht128(P(sets[k]["x"]), N, M, N, P(sets[k]["y"]), N, sp),
+                            4 * M * N, 2 * M * N * 128))
+            src = "y"
+        torch.cuda.synchronize()
     entries.append(("encode", lambda k: lib.lrq_encode(B(sets[k]["enc"]), P(sets[k][src]), N, sp), enc_b,
-                    4 * M * N * r))
+                    enc_flops))
     if cfg.consumer == "decode":
         dec_flops = 2 * M * N * r + (2 * M * N * 128 if cfg.hadamard else 0)
         dec_bytes = enc_b + (4 * M * N if cfg.hadamard else 0)

@@ -51,10 +51,13 @@ extern "C" {
 #define LRQ_ERR_ALIGN (-4)       /* pointer or leading dimension misaligned             */
 #define LRQ_ERR_WORKSPACE (-5)   /* caller workspace too small                          */
 
-/* The rotated format (config 4) is composed by the caller from lrq_wht128 and the plain
- * entry points: encode(bf16(WHT(x))), then WHT(bf16(decode)).  The flag marks a descriptor
- * as rotated; the fused entry points refuse it (LRQ_ERR_UNSUPPORTED) rather than return
- * unrotated values. */
+/* The rotated format (config 4) stores encode(bf16(WHT(x))) and decodes to
+ * WHT(bf16(decode)).  The flag marks a descriptor as rotated.  lrq_encode with the flag reads
+ * the unrotated x and rotates it as it reads (int4/g64 and int8/g128, no outlier channels,
+ * hidden/NP a multiple of 128, an even number of units per row); for other shapes it returns
+ * LRQ_ERR_UNSUPPORTED and the caller rotates x with lrq_wht128 into a buffer, then encodes
+ * that with the flag cleared.  lrq_decode undoes the rotation.  The fused consumer entry
+ * points refuse the flag (LRQ_ERR_UNSUPPORTED) rather than return unrotated values. */
 #define LRQ_FLAG_HADAMARD 1
 
 /* Descriptor of one compressed activation.  Encode writes L/codes/scale/zero/side;

@@ -79,7 +79,7 @@ def _encode(L, t, x=0x10000, ldx=4096):
     (dict(ld_codes=2056), "ALIGN"),
     (dict(codes=4097), "ALIGN"),
     (dict(rank=16), "NULL"),                   # rank 16 needs L and V
-    (dict(flags=1), "UNSUPPORTED"),            # encode takes the rotated copy, never the flag
+    (dict(flags=1, group=128), "UNSUPPORTED"),  # rotated int4/g128: rotate with lrq_wht128 first
     (dict(flags=4), "UNSUPPORTED"),
     (dict(n_outlier=3), "NULL"),               # outliers need idx and side
 ])

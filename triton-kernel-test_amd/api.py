@@ -155,8 +155,8 @@ class CompressedActivation:
         t = LrqTensors()
         t.rows, t.hidden = self.rows, self.hidden
         t.rank, t.bits, t.group = self.rank, self.bits, self.group
-        # encode takes the already-rotated activation (see ``encode``); every other entry
-        # point sees the flag
+        # encode sets the flag itself when it hands the library the unrotated activation (see
+        # ``encode``); every other entry point sees the flag
         t.flags = _lib.LRQ_FLAG_HADAMARD if (self.hadamard and not for_encode) else 0
         if self.rank:
             t.L, t.ld_L = self.L.data_ptr(), self.L.stride(0)
@@ -212,7 +212,14 @@ def encode(x: torch.Tensor, basis: Optional[LowRankBasis | torch.Tensor] = None,
     t = c.descriptor(for_encode=True)
     with torch.cuda.device(x.device):
         if hadamard:
-            # rotated format: y = bf16(WHT128(x)) into a temporary, then the plain encode of y
+            # rotated format: the library rotates x as it reads it where it can (flagged
+            # descriptor); otherwise y = bf16(WHT128(x)) into a temporary, then the plain encode
+            t.flags = _lib.LRQ_FLAG_HADAMARD
+            st = _lib.call_raw("lrq_encode", ctypes.byref(t), _p(x2), ldx, _stream(x.device))
+            if st != _lib.LRQ_ERR_UNSUPPORTED:
+                _lib.check(st, "lrq_encode")
+                return c
+            t.flags = 0
             y = torch.empty((rows, n), dtype=torch.bfloat16, device=x.device)
             call("lrq_wht128", _p(x2), ldx, rows, n, _p(y), n, _stream(x.device))
             x2, ldx = y, n

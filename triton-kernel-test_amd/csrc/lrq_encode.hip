@@ -17,6 +17,7 @@
 #include "lrq_common.h"
 #include "lrq_host.h"
 #include "lrq_quant.h"
+#include "lrq_whtop.h"
 
 #include <type_traits>
 
@@ -593,7 +594,7 @@ __global__ __launch_bounds__(256) void k_quant(
 // barrier): global wave gw takes wave column gw % nwc (units 2*(gw % nwc) .. +1) and row
 // range gw / nwc; its slice streams through a private LDS region as in k_encode_rows, with
 // the next block's loads (and its L rows) in flight during the current block's quantisation.
-template <int R>
+template <int R, bool ROT>
 __global__ __launch_bounds__(512) void k_project_slab(const uint16_t* __restrict__ X, int64_t ldx, int M, int N,
                                                       const uint16_t* __restrict__ Vt,
                                                       unsigned char* __restrict__ part, int64_t ldp, int RBW) {
@@ -610,6 +611,14 @@ __global__ __launch_bounds__(512) void k_project_slab(const uint16_t* __restrict
   const int c0 = CW * (NW * s + w);
   const bool live = c0 < N;  // wave-uniform
   unsigned char* region = shm + (size_t)w * 16 * PITCH;
+  // ROT: the slice is rotated in place (WHT-128 per 128-column block) before use
+  u32x4 wop[ROT ? 2 : 1][2];
+  if constexpr (ROT) {
+#pragma unroll
+    for (int q0 = 0; q0 < 2; ++q0)
+#pragma unroll
+      for (int n = 0; n < 2; ++n) wop[q0][n] = wht_base_operand(j, g, q0, n != 0);
+  }
   // V^T operands: vt[k][t] = Vt[16t + j][c0 + 32k + 8g .. +7] (zero past N)
   u32x4 vt[CW / 32][RT];
 #pragma unroll
@@ -642,6 +651,11 @@ __global__ __launch_bounds__(512) void k_project_slab(const uint16_t* __restrict
 #pragma unroll
       for (int i = 0; i < NLD; ++i)
         *reinterpret_cast<u32x4*>(region + (2 * i + lr) * PITCH + (lane & 31) * 16) = pf[i];
+      if constexpr (ROT) {
+#pragma unroll
+        for (int q = 0; q < CW / 128; ++q)
+          if (c0 + 128 * q < N) wht128_lds(region + j * PITCH + (128 * q + 32 * g) * 2, wop);
+      }
       u32x4 x[CW / 32];
 #pragma unroll
       for (int k = 0; k < CW / 32; ++k) x[k] = *reinterpret_cast<const u32x4*>(region + j * PITCH + (32 * k + 8 * g) * 2);
@@ -705,7 +719,7 @@ struct QuantSlab {
 // OUTL: outlier columns (oidx) are zeroed before the group statistics, and their bf16 values
 // are written to the fp16 side columns from the slice in LDS (a wave-uniform loop over the
 // wave's outlier columns; one range-checked 2-byte store per row).
-template <int BITS, int G, int R, bool OUTL>
+template <int BITS, int G, int R, bool OUTL, bool ROT>
 __global__ __launch_bounds__(512) void k_quant_slab(const uint16_t* __restrict__ X, int64_t ldx, int M, int N,
                                                     const uint16_t* __restrict__ V, const uint16_t* __restrict__ Lin,
                                                     int64_t ldl, uint8_t* __restrict__ codes, int64_t ldc,
@@ -743,6 +757,17 @@ __global__ __launch_bounds__(512) void k_quant_slab(const uint16_t* __restrict__
   if (rb0 >= nrb) return;
   const int nblk = min(RBW, nrb - rb0);
   unsigned char* region = shm + (size_t)w * 16 * PITCH;
+  // ROT: the slice is rotated in place (WHT-128 per 128-column block of each plane) before use;
+  // the host guarantees that the wave's columns of each plane start on a block boundary
+  static_assert(!(ROT && OUTL), "the rotated format has no outlier channels");
+  static_assert(!ROT || (UPW * G) % 128 == 0, "whole rotation blocks per wave and plane");
+  u32x4 wop[ROT ? 2 : 1][2];
+  if constexpr (ROT) {
+#pragma unroll
+    for (int q0 = 0; q0 < 2; ++q0)
+#pragma unroll
+      for (int n = 0; n < 2; ++n) wop[q0][n] = wht_base_operand(j, g, q0, n != 0);
+  }
 
   u32x2 vop[UPW][NP][G / 16][RT];
   if constexpr (R > 0) {
@@ -778,6 +803,12 @@ __global__ __launch_bounds__(512) void k_quant_slab(const uint16_t* __restrict__
 #pragma unroll
     for (int i = 0; i < NLD; ++i)
       *reinterpret_cast<u32x4*>(region + (RPL * i + lrow) * PITCH + (lpc % NP) * PIECE + loff) = pf[i];
+    if constexpr (ROT) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int q = 0; q < UPW * G / 128; ++q) wht128_lds(region + j * PITCH + p * PIECE + (128 * q + 32 * g) * 2, wop);
+    }
     u32x4 x[UPW][NP][CPG];
 #pragma unroll
     for (int uu = 0; uu < UPW; ++uu)
@@ -942,7 +973,7 @@ static int encode_persist_dispatch(const lrq_tensors* t, const void* x, int64_t 
 // the quantisation pass overwrites it (row r's partials take the first nslab*4*R bytes of its
 // codes row).  Rank 0: the quantisation pass alone (with outlier channels, it also writes the
 // side columns).  Returns 0 when the shape does not fit this path.
-template <int BITS, int G, int R>
+template <int BITS, int G, int R, bool ROT>
 static int encode_slabs(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s, int* status) {
   constexpr int NP = 8 / BITS;
   const int M = (int)t->rows, N = (int)t->hidden;
@@ -950,6 +981,8 @@ static int encode_slabs(const lrq_tensors* t, const void* x, int64_t ldx, hipStr
   const int nslab = (N + 2047) / 2048;
   const bool outl = t->n_outlier > 0;
   if (units % 2 != 0 || N % 32 != 0) return 0;
+  // rotated input: every wave's columns start on a 128-column block of their plane
+  if (ROT && (outl || (N / NP) % 128 != 0 || (2 * G) % 128 != 0 || (NP == 2 && G == 128))) return 0;
   if (outl && (R > 0 || t->n_outlier > 32767 || t->side == nullptr || t->outlier_idx == nullptr)) return 0;
   if (NP == 2 ? (t->ld_qp % 8 != 0 || !aligned(t->qparams, 16)) : (t->ld_qp % 4 != 0 || !aligned(t->qparams, 8))) return 0;
   if ((int64_t)16 * t->ld_qp * 2 >= ((int64_t)1 << 31)) return 0;
@@ -965,7 +998,7 @@ static int encode_slabs(const lrq_tensors* t, const void* x, int64_t ldx, hipStr
     // pass 1: about one workgroup per CU over (row groups, slabs)
     const int per1 = std::max(1, cus / nslab);
     const int rbw1 = (nrb + per1 - 1) / per1;
-    hipLaunchKernelGGL((k_project_slab<R>), dim3((nrb + rbw1 - 1) / rbw1, nslab), dim3(512), 0, s,
+    hipLaunchKernelGGL((k_project_slab<R, ROT>), dim3((nrb + rbw1 - 1) / rbw1, nslab), dim3(512), 0, s,
                        (const uint16_t*)x, ldx, M, N, (const uint16_t*)t->Vt, (unsigned char*)t->codes, ldp, rbw1);
     int st = launch_status();
     if (st) { *status = st; return 1; }
@@ -987,10 +1020,15 @@ static int encode_slabs(const lrq_tensors* t, const void* x, int64_t ldx, hipStr
                        (uint16_t*)t->qparams, t->ld_qp, t->outlier_idx, (int)t->n_outlier, (uint16_t*)t->side,
                        t->ld_side, nranges, rbw2);
   };
-  if (outl) {
-    if constexpr (R == 0) launch(k_quant_slab<BITS, G, R, true>);
+  if constexpr (ROT) {
+    if constexpr (NP == 2 && G == 128) return 0;  // not built (its registers would spill)
+    else launch(k_quant_slab<BITS, G, R, false, true>);
   } else {
-    launch(k_quant_slab<BITS, G, R, false>);
+    if (outl) {
+      if constexpr (R == 0) launch(k_quant_slab<BITS, G, R, true, false>);
+    } else {
+      launch(k_quant_slab<BITS, G, R, false, false>);
+    }
   }
   *status = launch_status();
   return 1;
@@ -1002,7 +1040,7 @@ static int encode_twopass(const lrq_tensors* t, const void* x, int64_t ldx, hipS
   constexpr int NP = 8 / BITS, RB = 4;
   {
     int st = 0;
-    if (encode_slabs<BITS, G, R>(t, x, ldx, s, &st)) return st;
+    if (encode_slabs<BITS, G, R, false>(t, x, ldx, s, &st)) return st;
   }
   if constexpr (R > 0) {
     hipLaunchKernelGGL((k_project<R>), dim3((M + 15) / 16), dim3(256), 0, s, (const uint16_t*)x, ldx, M, N,
@@ -1033,6 +1071,12 @@ static int encode_twopass(const lrq_tensors* t, const void* x, int64_t ldx, hipS
 template <int BITS, int G, int R>
 static int encode_impl(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s, int force_twopass) {
   int st = 0;
+  if (t->flags & LRQ_FLAG_HADAMARD) {
+    // rotated format: the column-slab passes rotate X in LDS as they read it
+    if (R > 0 && t->Vt == nullptr) return LRQ_ERR_NULL;
+    if (encode_slabs<BITS, G, R, true>(t, x, ldx, s, &st)) return st;
+    return LRQ_ERR_UNSUPPORTED;
+  }
   if (!force_twopass && t->n_outlier == 0 && encode_persist_dispatch<BITS, G, R>(t, x, ldx, s, &st)) return st;
   if (R > 0 && t->Vt == nullptr) return LRQ_ERR_NULL;  // the two-pass projection reads V^T
   return encode_twopass<BITS, G, R>(t, x, ldx, s);
@@ -1041,9 +1085,6 @@ static int encode_impl(const lrq_tensors* t, const void* x, int64_t ldx, hipStre
 static int encode_entry(const lrq_tensors* t, const void* x, int64_t ldx, void* stream, int force_twopass) {
   int st = validate_tensors(t);
   if (st) return st;
-  // the rotated format needs a rotated copy of x (lrq_wht128 into a caller buffer, then
-  // encode that without the flag); refusing beats silently encoding unrotated data
-  if (t->flags & LRQ_FLAG_HADAMARD) return LRQ_ERR_UNSUPPORTED;
   if (x == nullptr) return LRQ_ERR_NULL;
   if (ldx < t->hidden) return LRQ_ERR_SHAPE;
   if ((ldx % 8) != 0 || !aligned(x, 16)) return LRQ_ERR_ALIGN;
