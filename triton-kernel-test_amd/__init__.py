@@ -5,7 +5,7 @@ not a Python identifier).  The HIP library liblrq.so must be built first; nothin
 falls back to a CPU implementation.
 """
 
-from . import _lib, api, autograd, inputs  # noqa: F401
+from . import _lib, api, autograd, inputs, offload  # noqa: F401
 from .api import *  # noqa: F401,F403
 from .legacy import *  # noqa: F401,F403
 
