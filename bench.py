@@ -6,11 +6,11 @@ Default workload (BASELINE.json metric): rank-16 int4/g64 encode + decode of a b
 rotate over several HBM-resident buffer sets (> 512 MB of X) so the 256 MB MALL cannot
 serve them.  Prints ONE JSON line (driver contract).
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config north_star|c1|c2|c3|c4|c5]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config north_star|c1|c2|c3|c4|c5|lora]
                   [--no-cpu-baseline]
 
 value       = activation GB/s = 2*rows*hidden bytes / (encode + decode time per step);
-              fused-consumer configs: / (consumer time)
+              fused-consumer configs: / (consumer time); lora: / (x A + x^T g time)
 roofline    = dominant kernel's algorithmic HBM bytes per launch / its mean duration
               (K back-to-back launches between HIP events on the launch stream), against
               8 TB/s; traffic = rocprofv3 FETCH_SIZE/WRITE_SIZE bytes per launch from profiles/
@@ -97,7 +97,11 @@ def cpu_baseline(cfg, seconds: float):
                 t0 = time.perf_counter()
             xh = O.decode(e["L"], vb, e["codes"], e["scale"], e["zero"], cfg.bits, cfg.group,
                           hadamard=cfg.hadamard, side=e["side"], idx=e["idx"])
-            if cfg.consumer != "decode":
+            if cfg.consumer == "lora":
+                xf = O.bf16_to_f32(xh)
+                O.round_out(O.gemm(xf, O.bf16_to_f32(as_bits(inp["a"]))))
+                O.gemm_t(xf, O.bf16_to_f32(as_bits(inp["g"]))).astype(np.float32)
+            elif cfg.consumer != "decode":
                 f = {"silu": O.silu_bwd, "gelu": O.gelu_bwd, "softmax": O.softmax_bwd}[cfg.consumer]
                 O.round_out(f(O.bf16_to_f32(xh), O.bf16_to_f32(as_bits(inp["dy"]))))
             return time.perf_counter() - t0
@@ -112,7 +116,8 @@ def cpu_baseline(cfg, seconds: float):
                 rows = min(cfg.rows, max(rows, int(rows * seconds / max(t, 1e-3))))
                 t = run(rows)
         gbs = 2 * rows * cfg.hidden / t / 1e9
-        what = "encode+decode" if cfg.consumer == "decode" else f"decode+{cfg.consumer} backward"
+        what = {"decode": "encode+decode", "lora": "decode + x A + x^T g (LoRA factor gradients)"}.get(
+            cfg.consumer, f"decode+{cfg.consumer} backward")
         return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
                 "sample": f"numpy CPU oracle {what} of {rows} of {cfg.rows} rows x {cfg.hidden} "
                           f"(same recipe), {t:.1f} s, 1 thread"}
@@ -153,7 +158,15 @@ def build_plan(cfg, pkg, lib, dev, nbuf):
             st["y"] = torch.empty_like(x)
         if cfg.keep_channels:
             st["cm"] = torch.empty((N,), dtype=torch.float32, device=dev)
-        if cfg.consumer != "decode":
+        if cfg.consumer == "lora":
+            n = cfg.lora_rank
+            st["a"] = pkg.inputs.lora_factor(N, n, cfg.seed + i, dev)
+            st["g"] = pkg.inputs.gradient((M, n), 0.05, cfg.seed + i, dev)
+            st["xa"] = torch.empty((M, n), dtype=torch.bfloat16, device=dev)
+            st["da"] = torch.empty((N, n), dtype=torch.float32, device=dev)
+            wsb = lib.lrq_dequant_gemm_t_workspace(ctypes.byref(st["dec"]), n)
+            st["ws"] = torch.empty((max(wsb, 16) + 15) // 16 * 4, dtype=torch.float32, device=dev)
+        elif cfg.consumer != "decode":
             st["dy"] = pkg.inputs.gradient((M, N), cfg.grad_std, cfg.seed + i, dev)
         sets.append(st)
     torch.cuda.synchronize()
@@ -188,16 +201,31 @@ def build_plan(cfg, pkg, lib, dev, nbuf):
                     enc_flops))
     if cfg.consumer == "decode":
         dec_flops = 2 * M * N * r + (2 * M * N * 128 if cfg.hadamard else 0)
-        dec_bytes = enc_b + (4 * M * N if cfg.hadamard else 0)
+        # the rotation is part of the decode's algorithm, not of its minimal traffic: a decode
+        # that rotates in a separate pass moves more than these bytes and shows a lower fraction
         entries.append(("decode", lambda k: lib.lrq_decode(B(sets[k]["dec"]), P(sets[k]["out"]), N, sp),
-                        dec_bytes, dec_flops))
+                        enc_b, dec_flops))
         timed = None  # value over the whole step (round trip)
+    elif cfg.consumer == "lora":
+        # the LoRA layer's backward on the codes: x A (dequant-GEMM, bf16 out) and
+        # dA = x^T g (transposed dequant-GEMM, fp32 out); bytes = codes + qparams + L + V read
+        # once per kernel, plus each kernel's small operands and output
+        n = cfg.lora_rank
+        base = M * N * (cfg.bits / 8 + 4 / cfg.group) + 2 * M * r + 2 * N * r
+        entries.append(("xa", lambda k: lib.lrq_dequant_gemm(B(sets[k]["dec"]), P(sets[k]["a"]), n,
+                                                             P(sets[k]["xa"]), n, 0, sp),
+                        base + 2 * N * n + 2 * M * n, 2 * M * N * r + 2 * M * N * n))
+        entries.append(("da", lambda k: lib.lrq_dequant_gemm_t(B(sets[k]["dec"]), P(sets[k]["g"]), n, n,
+                                                               P(sets[k]["da"]), n, 1, P(sets[k]["ws"]),
+                                                               sets[k]["ws"].numel() * 4, sp),
+                        base + 2 * M * n + 4 * N * n, 2 * M * N * r + 2 * M * N * n))
+        timed = ["xa", "da"]  # value over both gradient kernels (the encode is the producer)
     else:
         fn = {"silu": lib.lrq_silu_bwd, "gelu": lib.lrq_gelu_bwd, "softmax": lib.lrq_softmax_bwd}[cfg.consumer]
         name = f"{cfg.consumer}_bwd"
         entries.append((name, lambda k: fn(B(sets[k]["dec"]), P(sets[k]["dy"]), N, P(sets[k]["out"]), N, sp),
                         consumer_bytes(M, N, r, cfg.bits, cfg.group, side), 2 * M * N * r))
-        timed = name  # value over the fused consumer (the encode is the producer)
+        timed = [name]  # value over the fused consumer (the encode is the producer)
     return entries, 2 * M * N, timed, sets
 
 
@@ -284,8 +312,8 @@ def main():
         value = act_bytes / (ms_step * 1e-3) / 1e9  # whole step, kernels interleaved as in use
         workload = "encode+decode" + (" with WHT-128 rotation" if cfg.hadamard else "")
     else:
-        value = act_bytes / (kernels[timed]["mean_us"] * 1e-6) / 1e9
-        workload = f"fused {timed} on the compressed activation (encode timed alongside)"
+        value = act_bytes / (sum(kernels[t]["mean_us"] for t in timed) * 1e-6) / 1e9
+        workload = f"fused {' + '.join(timed)} on the compressed activation (encode timed alongside)"
     dom_name, dom_alg, dom_us = None, 0, -1.0
     for name, _, alg, _ in entries:
         if kernels[name]["mean_us"] > dom_us:

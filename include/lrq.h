@@ -125,6 +125,23 @@ int lrq_softmax_bwd(const lrq_tensors* t, const void* dp, int64_t lddp, void* ds
 int lrq_dequant_gemm(const lrq_tensors* t, const void* a, int32_t n_out, void* out, int64_t ldo,
                      int32_t out_fp32, void* stream);
 
+/* out[hidden, n_out] = decode(t)^T @ g[rows, n_out] (g bf16 row-major, ld ldg a multiple of 4,
+ * 8-byte aligned), fp32 accumulate, decode(t) rounded to bf16 as lrq_decode returns it; out is
+ * fp32 when out_fp32 != 0, else bf16.  n_out is 16 or 32; no outlier channels, no rotated
+ * format.  This is the LoRA factor gradient dA = x^T (dy B^T) of compute_lora_gradient
+ * (low_rank_system_profile_forward.py:14-18, `x.mT @ (dy @ b.mT)`) read from the codes: a
+ * reduction over the rows.  The rows are split into groups whose fp32 partials [hidden, n_out]
+ * go to `workspace` (16-byte aligned, at least lrq_dequant_gemm_t_workspace(t, n_out) bytes),
+ * then summed in group order: results depend only on the shapes, not on timing.  rows == 0
+ * writes zeros. */
+int lrq_dequant_gemm_t(const lrq_tensors* t, const void* g, int64_t ldg, int32_t n_out, void* out,
+                       int64_t ldo, int32_t out_fp32, void* workspace, int64_t workspace_bytes,
+                       void* stream);
+
+/* Workspace bytes lrq_dequant_gemm_t needs for `t` and n_out (>= 0), or a negative LRQ_ERR_*.
+ * Host only: no HIP call. */
+int64_t lrq_dequant_gemm_t_workspace(const lrq_tensors* t, int32_t n_out);
+
 /* colmax[c] = max_r |x[r, c]| (fp32).  First half of the outlier-channel split
  * (no reference counterpart; the reference's channel split takes caller indices,
  * extraction_outlier_channel.py:11-14). */

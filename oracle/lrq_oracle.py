@@ -47,7 +47,7 @@ __all__ = [
     # outlier channels
     "colmax_abs", "topk_channels",
     # consumers
-    "silu_bwd", "gelu_bwd", "softmax_bwd", "mul", "gemm", "round_out",
+    "silu_bwd", "gelu_bwd", "softmax_bwd", "mul", "gemm", "gemm_t", "round_out",
     # legacy (reference torch forms)
     "legacy_matmul_bf16", "legacy_encode", "legacy_decode", "naive_roundtrip",
     "lowrank_add",
@@ -436,6 +436,12 @@ def mul(x: np.ndarray, y: np.ndarray) -> np.ndarray:
 def gemm(x: np.ndarray, a: np.ndarray) -> np.ndarray:
     """``x @ a`` in float64 — extraction_fuse_matmul.py:5-6."""
     return np.asarray(x, dtype=np.float64) @ np.asarray(a, dtype=np.float64)
+
+
+def gemm_t(x: np.ndarray, g: np.ndarray) -> np.ndarray:
+    """``x^T @ g`` in float64: the LoRA factor gradient ``x.mT @ (dy @ b.mT)`` with
+    g = dy @ b.mT (low_rank_system_profile_forward.py:14-18), a reduction over the rows."""
+    return np.asarray(x, dtype=np.float64).T @ np.asarray(g, dtype=np.float64)
 
 
 def round_out(v: np.ndarray) -> np.ndarray:

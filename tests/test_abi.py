@@ -105,6 +105,31 @@ def test_decode_and_consumer_argument_errors(L):
                       ctypes.c_void_p(0x20000), 24, 1, None) == L.LRQ_ERR_UNSUPPORTED
 
 
+def test_dequant_gemm_t_arguments(L):
+    """Workspace query (host only) and the argument errors of the transposed dequant-GEMM."""
+    t = _desc(L)  # 32 rows, 4096 columns, int4 / g64: 32 units -> 16 column groups of 2 units
+    ws = L.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(t), 16)
+    assert ws == 1 * 4096 * 16 * 4  # 2 row blocks < 8 waves: one row group
+    big = _desc(L, rows=16384)
+    assert L.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(big), 16) == 16 * 4096 * 16 * 4
+    # n = 32: one unit per wave (accumulator budget), 32 column groups -> 8 row groups
+    assert L.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(big), 32) == 8 * 4096 * 32 * 4
+    assert L.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(t), 24) == L.LRQ_ERR_UNSUPPORTED
+    assert L.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(_desc(L, bits=3)), 16) == L.LRQ_ERR_UNSUPPORTED
+    p, q = ctypes.c_void_p(0x10000), ctypes.c_void_p(0x20000)
+    call = lambda t_, g=p, ldg=16, n=16, o=q, ldo=16, w=ctypes.c_void_p(0x40000), wb=ws: L.call_raw(  # noqa: E731
+        "lrq_dequant_gemm_t", ctypes.byref(t_), g, ldg, n, o, ldo, 1, w, wb, None)
+    assert call(t, g=None) == L.LRQ_ERR_NULL
+    assert call(t, n=24) == L.LRQ_ERR_UNSUPPORTED
+    assert call(t, ldg=8) == L.LRQ_ERR_SHAPE
+    assert call(t, ldg=18) == L.LRQ_ERR_ALIGN
+    assert call(t, g=ctypes.c_void_p(0x10004)) == L.LRQ_ERR_ALIGN
+    assert call(t, w=None) == L.LRQ_ERR_NULL
+    assert call(t, wb=ws - 4) == L.LRQ_ERR_WORKSPACE
+    assert call(t, w=ctypes.c_void_p(0x40008)) == L.LRQ_ERR_ALIGN
+    assert call(_desc(L, flags=1)) == L.LRQ_ERR_UNSUPPORTED
+
+
 def test_legacy_argument_errors(L):
     p = ctypes.c_void_p(0x10000)
     enc = lambda K, bits, N=1024, s_rows=1: L.call_raw(  # noqa: E731

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle as O
-from parity import assert_fp_close, bits16, f16
+from parity import assert_fp_close, bits16, f16, ulp_diff_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -74,3 +74,68 @@ def test_dequant_gemm(pkg, dev, rows, hidden, rank, n_out, out_dtype):
         assert rel <= 1e-5 and np.abs(got - ref).max() <= 1e-3, (rel, np.abs(got - ref).max())
     else:
         assert_fp_close(bits16(out), ref, "dequant gemm bf16")
+
+
+@pytest.mark.parametrize("rows,hidden,rank,bits,group,n_out,out_dtype", [
+    (100, 4096, 16, 4, 64, 16, torch.float32),     # north-star width, reduced rows
+    (3000, 4096, 16, 4, 64, 16, torch.float32),    # 16 row groups, ragged last block
+    (700, 4096, 32, 4, 64, 32, torch.bfloat16),    # rank 32, n = 32, bf16 out
+    (300, 2048, 16, 8, 128, 16, torch.float32),    # int8 / g128, 2 units per wave
+    (200, 1024, 16, 4, 128, 32, torch.float32),    # int4 / g128: one unit per wave
+    (90, 384, 0, 4, 64, 16, torch.float32),        # odd unit count (3), rank 0
+    (5, 512, 0, 8, 64, 32, torch.float32),         # fewer rows than one block
+])
+def test_dequant_gemm_t(pkg, dev, rows, hidden, rank, bits, group, n_out, out_dtype):
+    """decode(c)^T @ g against the float64 product on lrq_decode's output (the x_hat the entry
+    point is defined on): fp32 out within the accumulation bound 1e-5 * (|x_hat|^T |g|) per
+    entry, bf16 out within one ulp of the once-rounded result.  Against the oracle's x_hat
+    (which lrq_decode matches to 1 ulp on <= 1e-3 of elements) within the floating-point bar."""
+    print(f"[gemm_t] rows={rows} hidden={hidden} rank={rank} b{bits} g{group} n={n_out} {out_dtype}", flush=True)
+    x = pkg.inputs.activation(rows, hidden, 8, 20.0, seed=31)
+    V = pkg.inputs.basis(hidden, rank, seed=31) if rank else None
+    gen = torch.Generator().manual_seed(32)
+    gm = (torch.randn(rows, n_out, generator=gen) * 0.05).to(torch.bfloat16)
+    c = pkg.encode(x.to(dev), V.to(dev) if V is not None else None, bits=bits, group_size=group)
+    out = pkg.dequant_gemm_t(c, gm.to(dev), out_dtype=out_dtype)
+    xd = O.bf16_to_f32(bits16(pkg.decode(c)))
+    torch.cuda.synchronize()
+    assert out.shape == (hidden, n_out)
+    gf = O.bf16_to_f32(bits16(gm))
+    ref = O.gemm_t(xd, gf)
+    bound = 1e-5 * O.gemm_t(np.abs(xd), np.abs(gf)) + 1e-9  # fp32 accumulation
+    if out_dtype == torch.float32:
+        got = out.cpu().numpy().astype(np.float64)
+        err = np.abs(got - ref)
+        assert (err <= bound).all(), (float(err.max()), float((err / bound).max()))
+        ref_o = O.gemm_t(_xhat(c, V, bits, group), gf)
+        rel = np.linalg.norm(got - ref_o) / np.linalg.norm(ref_o)
+        assert rel <= 1e-3, rel
+    else:
+        # one bf16 rounding of a sum within the accumulation bound: |got - ref| <= ulp + bound
+        got = O.bf16_to_f32(bits16(out)).astype(np.float64)
+        ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))) - 7)
+        err = np.abs(got - ref)
+        assert (err <= ulp + bound).all(), float((err / (ulp + bound)).max())
+        flips = ulp_diff_bf16(bits16(out), O.round_out(ref))
+        print(f"[gemm_t] bf16 ulp flips vs once-rounded: {int((flips > 0).sum())} of {flips.size}", flush=True)
+        rep = assert_fp_close(bits16(out), O.gemm_t(_xhat(c, V, bits, group), gf), "dequant gemm_t bf16",
+                              max_abs=np.inf)
+        print(f"[gemm_t] vs oracle x_hat {rep}", flush=True)
+
+
+def test_dequant_gemm_t_no_rows(pkg, dev):
+    """A descriptor with rows == 0 gives dA = 0 (the sum over no rows), through the C ABI."""
+    import ctypes
+    _lib = __import__("importlib").import_module("triton-kernel-test_amd._lib")
+    x = pkg.inputs.activation(16, 512, 0, 1.0, seed=3)
+    c = pkg.encode(x.to(dev), None, bits=4, group_size=64)
+    t = c.descriptor()
+    t.rows = 0
+    assert _lib.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(t), 16) == 0
+    gm = torch.ones(16, 16, dtype=torch.bfloat16, device=dev)
+    out = torch.full((512, 16), 7.0, dtype=torch.float32, device=dev)
+    s = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    st = _lib.call_raw("lrq_dequant_gemm_t", ctypes.byref(t), ctypes.c_void_p(gm.data_ptr()), 16, 16,
+                       ctypes.c_void_p(out.data_ptr()), 16, 1, None, 0, s)
+    torch.cuda.synchronize()
+    assert st == 0 and not out.any()

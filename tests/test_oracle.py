@@ -342,6 +342,22 @@ def test_consumers_match_aten_backward_functions():
     assert np.array_equal(O.mul(x.numpy(), dy.numpy()), (x * dy).numpy())
 
 
+def test_gemm_t_is_the_lora_factor_gradient():
+    """gemm_t(x, dy B^T) is dL/dA of y = x W^T + (x A) B under upstream dy, as torch autograd
+    computes it (a transposed operand or a dropped factor fails here)."""
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(37, 64, generator=g, dtype=torch.float64)
+    w = torch.randn(48, 64, generator=g, dtype=torch.float64)
+    a = torch.randn(64, 16, generator=g, dtype=torch.float64, requires_grad=True)
+    b = torch.randn(16, 48, generator=g, dtype=torch.float64)
+    dy = torch.randn(37, 48, generator=g, dtype=torch.float64)
+    y = x @ w.T + (x @ a) @ b
+    (da,) = torch.autograd.grad(y, a, dy)
+    got = O.gemm_t(x.numpy(), (dy @ b.T).numpy())
+    assert got.shape == (64, 16)
+    assert np.allclose(got, da.numpy(), rtol=1e-12, atol=1e-12)
+
+
 def test_round_out_is_single_rounding():
     v = np.array([1.0 + 2 ** -9, 1.0 + 3 * 2 ** -9, -2.5e-3], np.float64)
     assert np.array_equal(O.round_out(v), O.bf16_round(v.astype(np.float32)))

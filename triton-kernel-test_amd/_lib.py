@@ -50,6 +50,9 @@ SIGNATURES = {
     "lrq_mul": (c_int32, [_T, c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
     "lrq_softmax_bwd": (c_int32, [_T, c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
     "lrq_dequant_gemm": (c_int32, [_T, c_void_p, c_int32, c_void_p, c_int64, c_int32, c_void_p]),
+    "lrq_dequant_gemm_t": (c_int32, [_T, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p,
+                                     c_int64, c_void_p]),
+    "lrq_dequant_gemm_t_workspace": (c_int64, [_T, c_int32]),
     "lrq_colmax": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     "lrq_topk": (c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p]),
     "lrq_transpose_bf16": (c_int32, [c_void_p, c_int64, c_int64, c_void_p, c_void_p]),

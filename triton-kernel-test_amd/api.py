@@ -33,7 +33,7 @@ from ._lib import LrqTensors, call
 __all__ = [
     "LowRankBasis", "CompressedActivation", "encode", "decode", "silu_backward_compressed",
     "gelu_backward_compressed", "mul_compressed", "softmax_backward_compressed", "dequant_gemm",
-    "outlier_channels", "column_absmax", "topk_channels", "wht128",
+    "dequant_gemm_t", "outlier_channels", "column_absmax", "topk_channels", "wht128",
 ]
 
 
@@ -331,6 +331,32 @@ def dequant_gemm(c: CompressedActivation, a: torch.Tensor, out_dtype=torch.float
         call("lrq_dequant_gemm", ctypes.byref(t), _p(a), n_out, _p(o), n_out,
              1 if out_dtype == torch.float32 else 0, _stream(c.device))
     return o.reshape(tuple(c.shape[:-1]) + (n_out,))
+
+
+def dequant_gemm_t(c: CompressedActivation, g: torch.Tensor, out_dtype=torch.float32) -> torch.Tensor:
+    """decode(c)^T @ g with g[rows, n] bf16 (n = 16 or 32), reduced over the rows: the LoRA
+    factor gradient x^T (dy B^T) of compute_lora_gradient (low_rank_system_profile_forward.py:14-18)
+    read from the codes.  fp32 accumulate; output [N, n] fp32 or bf16."""
+    _require_device(g)
+    g2 = g.reshape(-1, g.shape[-1]) if g.dim() >= 2 else g
+    if g.dtype != torch.bfloat16 or g.dim() < 2 or g2.shape[0] != c.rows:
+        raise ValueError("g must be bf16 [rows, n] (leading dimensions those of the activation)")
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("out_dtype must be float32 or bfloat16")
+    if c.hadamard or c.idx is not None:
+        raise ValueError("dequant_gemm_t: rotated format and outlier channels are not supported")
+    g2 = g2.contiguous()
+    n_out = g2.shape[1]
+    t = c.descriptor()
+    ws_bytes = _lib.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(t), n_out)
+    if ws_bytes < 0:
+        _lib.check(ws_bytes, "lrq_dequant_gemm_t_workspace")
+    ws = torch.empty((max(ws_bytes, 16) + 15) // 16 * 4, dtype=torch.float32, device=c.device)
+    o = torch.empty((c.hidden, n_out), dtype=out_dtype, device=c.device)
+    with torch.cuda.device(c.device):
+        call("lrq_dequant_gemm_t", ctypes.byref(t), _p(g2), n_out, n_out, _p(o), n_out,
+             1 if out_dtype == torch.float32 else 0, _p(ws), ws.numel() * 4, _stream(c.device))
+    return o
 
 
 def column_absmax(x: torch.Tensor) -> torch.Tensor:

@@ -9,8 +9,11 @@ round trip part of autograd:
 * ``compute_lora`` / ``compute_lora_gradient`` keep the reference's formulas (the weight is a
   dense [out, in] tensor here; the reference passes a Linear module to the forward).
 * ``LoRALinearCompressed`` is an autograd Function whose forward is ``compute_lora`` and which
-  saves x in the compressed format; its backward decodes x and returns dx, dA and dB from
-  ``compute_lora_gradient`` (W is frozen, as in the reference's LoRA setting).
+  saves x in the compressed format; its backward returns dx, dA and dB of
+  ``compute_lora_gradient`` (W is frozen, as in the reference's LoRA setting).  With
+  ``fused=True`` (the default) x is never decoded: dA = x^T (dy B^T) comes from the transposed
+  dequant-GEMM and x A from the dequant-GEMM, both reading the codes (LoRA rank 16 or 32,
+  plain format); otherwise, or for other shapes, x is decoded and the formulas run on it.
 * ``compressed_saved_tensors`` is a ``torch.autograd.graph.saved_tensors_hooks`` context that
   stores every saved bf16 activation with a suitable last dimension in the compressed format
   and decodes it when backward asks for it, for any model.
@@ -26,7 +29,7 @@ from typing import Callable, Optional
 
 import torch
 
-from .api import CompressedActivation, LowRankBasis, decode, encode
+from .api import CompressedActivation, LowRankBasis, decode, dequant_gemm, dequant_gemm_t, encode
 
 __all__ = ["compute_lora", "compute_lora_gradient", "LoRALinearCompressed", "lora_linear_compressed",
            "compressed_saved_tensors", "fit_basis"]
@@ -57,26 +60,41 @@ def _flat(t: torch.Tensor) -> torch.Tensor:
 class LoRALinearCompressed(torch.autograd.Function):
     """y = compute_lora(x, W, A, B); x is saved compressed (bits, group, optional basis).
 
-    Gradients: dx, dA, dB from compute_lora_gradient on the decoded x; W gets none."""
+    Gradients: dx, dA, dB of compute_lora_gradient on the decoded x; W gets none.  ``fused``
+    reads the codes directly for dA and x A (no decoded x), see the module docstring."""
 
     @staticmethod
-    def forward(ctx, x, w, a, b, basis: Optional[LowRankBasis], bits: int, group: int):
+    def forward(ctx, x, w, a, b, basis: Optional[LowRankBasis], bits: int, group: int, fused: bool = True):
         y = compute_lora(x, w, a, b)
         ctx.c = encode(x.detach(), basis, bits=bits, group_size=group)
+        ctx.fused = fused
         ctx.save_for_backward(w, a, b)
         return y
 
     @staticmethod
     def backward(ctx, dy):
         w, a, b = ctx.saved_tensors
-        x_hat = decode(ctx.c)
-        ctx.c = None
-        dx, da, db = compute_lora_gradient(_flat(dy), _flat(x_hat), w, a, b)
-        return dx.reshape(dy.shape[:-1] + (w.shape[1],)), None, da, db, None, None, None
+        c, ctx.c = ctx.c, None
+        dy2 = _flat(dy)
+        if ctx.fused and _codes_gemm_ok(c, a, dy2):
+            dx = dy2 @ (w + b.mT @ a.mT)
+            da = dequant_gemm_t(c, dy2 @ b.mT).to(a.dtype)              # x^T (dy B^T)
+            db = dequant_gemm(c, a, out_dtype=a.dtype).reshape(-1, a.shape[1]).mT @ dy2  # (x A)^T dy
+        else:
+            dx, da, db = compute_lora_gradient(dy2, _flat(decode(c)), w, a, b)
+        return dx.reshape(dy.shape[:-1] + (w.shape[1],)), None, da, db, None, None, None, None
 
 
-def lora_linear_compressed(x, w, a, b, basis: Optional[LowRankBasis] = None, bits: int = 4, group: int = 64):
-    return LoRALinearCompressed.apply(x, w, a, b, basis, bits, group)
+def _codes_gemm_ok(c: CompressedActivation, a: torch.Tensor, dy2: torch.Tensor) -> bool:
+    """The dequant-GEMMs serve LoRA rank 16 / 32 on the plain (unrotated, no outlier
+    channels) format with bf16 operands."""
+    return (a.shape[1] in (16, 32) and not c.hadamard and c.idx is None and a.dtype == torch.bfloat16
+            and dy2.dtype == torch.bfloat16)
+
+
+def lora_linear_compressed(x, w, a, b, basis: Optional[LowRankBasis] = None, bits: int = 4, group: int = 64,
+                           fused: bool = True):
+    return LoRALinearCompressed.apply(x, w, a, b, basis, bits, group, fused)
 
 
 class compressed_saved_tensors(torch.autograd.graph.saved_tensors_hooks):

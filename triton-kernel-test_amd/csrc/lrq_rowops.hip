@@ -7,6 +7,9 @@
 //   k_dequant_gemm  out = bf16(decode(c)) @ A, A [N, n] bf16, fp32 accumulate on MFMA
 //                   (extraction_fuse_matmul.py:224-249 intends this; its kernel reads wrong
 //                   addresses, so the torch form :5-6 defines it).
+//   k_dequant_gemm_t out = bf16(decode(c))^T @ G, G [M, n] bf16: the LoRA factor gradient
+//                   x^T (dy B^T) (low_rank_system_profile_forward.py:14-18), a reduction over
+//                   rows into per-row-group partials, then k_sum_parts.
 #include "lrq_common.h"
 #include "lrq_dequant.h"
 #include "lrq_host.h"
@@ -383,6 +386,164 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm(
   }
 }
 
+// ------------------------------------------------------------------ transposed dequant-GEMM
+// part[rg][n][k] = sum over the rows m of row group rg of x_hat[m][n] * gm[m][k] (x_hat =
+// bf16(decode), k < 16 KT).  Grid: (column groups of UPW units) x (row groups of bpg 16-row
+// blocks); wave w of a workgroup takes the group's blocks w, w + NW, ... over all UPW units,
+// the next block's codes, qparams, L and gm rows loaded while the current one is computed.
+// Every MFMA operand keeps K along a lane's registers, and the reduction here runs over rows,
+// which the reconstruction holds one per lane (lane (j, g): row j, E columns).  So each 16 x 16
+// piece of x_hat is transposed by an identity MFMA (exact) into lane (column, 4 rows) -- the B
+// operand of the product -- and gm's rows by the same transpose into the A operand g^T.  The
+// product's accumulator holds, in lane (j, g), 4 consecutive k of one column n.  The NW waves'
+// accumulators are summed through LDS in wave order (deterministic) and leave as 16-byte rows.
+template <int BITS, int G, int R, int KT, int NW, int UPW>
+__global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t(
+    const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
+    const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
+    const uint16_t* __restrict__ gm, int64_t ldg, float* __restrict__ part, int bpg) {
+  constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, E = G / 4, Q = G / 16;
+  constexpr int NACC = UPW * NP * Q * KT;  // f32x4 accumulators per lane
+  constexpr int CH = NACC < 8 ? NACC : 8;  // accumulators per LDS round
+  static_assert(NACC % CH == 0, "reduction rounds");
+  __shared__ f32x4 red[NW][CH][64];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int nrb = (M + 15) / 16;
+  const int u0 = blockIdx.x * UPW;
+  const int rb_lo = blockIdx.y * bpg, rb_hi = min(rb_lo + bpg, nrb);
+  const int KO = 16 * KT;  // gm columns and part row length
+  const u32x2 ident = identity_bop(j, g);
+
+  u32x2 vop[UPW][NP][Q][RT];
+  if constexpr (R > 0) {
+#pragma unroll
+    for (int ui = 0; ui < UPW; ++ui)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, u0 + ui, N, NP, G), j, g, vop[ui][p]);
+  }
+  f32x4 acc[NACC];
+#pragma unroll
+  for (int a = 0; a < NACC; ++a) acc[a] = zero4();
+
+  struct Blk {
+    u32x4 cb[UPW][G / 64];
+    uint32_t qp[UPW][NP];
+    u32x2 lop[RT];
+    u32x2 gop[KT];
+  };
+  auto load = [&](int rb, Blk& d) {
+    const int64_t row = min(rb * 16 + j, M - 1);
+#pragma unroll
+    for (int ui = 0; ui < UPW; ++ui) {
+#pragma unroll
+      for (int i = 0; i < G / 64; ++i) d.cb[ui][i] = ld16_stream(codes + row * ldc + (u0 + ui) * G + E * g + 16 * i);
+      if constexpr (NP == 2) {
+        const u32x2 q = ld8(qparams + row * ldq + (u0 + ui) * 4);
+        d.qp[ui][0] = q[0];
+        d.qp[ui][1] = q[1];
+      } else {
+        d.qp[ui][0] = ld4(qparams + row * ldq + (u0 + ui) * 2);
+      }
+    }
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t) d.lop[t] = ld8(Lin + row * ldl + 16 * t + 4 * g);
+    }
+#pragma unroll
+    for (int t = 0; t < KT; ++t) d.gop[t] = ld8(gm + row * ldg + 16 * t + 4 * g);
+  };
+
+  int rb = rb_lo + w;
+  if (rb < rb_hi) {  // wave-uniform
+    Blk cur;
+    load(rb, cur);
+    for (; rb < rb_hi; rb += NW) {
+      Blk nxt;
+      load(min(rb + NW, rb_hi - 1), nxt);  // clamped: the last block's prefetch re-reads itself
+      // g^T operands: rows past M contribute nothing (their clamped x_hat is finite)
+      const bool live = rb * 16 + j < M;
+      u32x2 a2[KT];
+#pragma unroll
+      for (int t = 0; t < KT; ++t) {
+        const u32x2 gv = live ? cur.gop[t] : u32x2{0u, 0u};
+        const f32x4 d = mfma_16x16x16(gv, ident, zero4());  // lane (j, g): gm[4g + v][16t + j]
+        a2[t] = u32x2{pack_bf16x2_exact(d[0], d[1]), pack_bf16x2_exact(d[2], d[3])};
+      }
+#pragma unroll
+      for (int ui = 0; ui < UPW; ++ui)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          float xh[E];
+          reconstruct_plane<BITS, G, R>(cur.cb[ui], cur.qp[ui][p], p, vop[ui][p], cur.lop, xh);
+#pragma unroll
+          for (int q = 0; q < Q; ++q) {
+            // lane (j, g) holds x_hat[j][E g + 4q + e]; after the identity MFMA, lane (j, g)
+            // holds x_hat[4g + v][E (j >> 2) + 4q + (j & 3)]
+            const u32x2 xa = u32x2{pack_bf16x2(xh[4 * q], xh[4 * q + 1]), pack_bf16x2(xh[4 * q + 2], xh[4 * q + 3])};
+            const f32x4 d = mfma_16x16x16(xa, ident, zero4());
+            const u32x2 xb = u32x2{pack_bf16x2_exact(d[0], d[1]), pack_bf16x2_exact(d[2], d[3])};
+#pragma unroll
+            for (int t = 0; t < KT; ++t) {
+              f32x4& c = acc[((ui * NP + p) * Q + q) * KT + t];
+              c = mfma_16x16x16(a2[t], xb, c);
+            }
+          }
+        }
+      cur = nxt;
+    }
+  }
+
+  // acc[((ui NP + p) Q + q) KT + t] in lane (j, g), component v: column
+  // n = p N/NP + (u0 + ui) G + E (j >> 2) + 4q + (j & 3), k = 16t + 4g + v
+  float* partg = part + (int64_t)blockIdx.y * N * KO;
+#pragma unroll
+  for (int c0 = 0; c0 < NACC; c0 += CH) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) red[w][c][lane] = acc[c0 + c];
+    __syncthreads();
+    for (int e = threadIdx.x; e < CH * 64; e += NW * 64) {
+      const int c = e >> 6, ln = e & 63;
+      f32x4 s = red[0][c][ln];
+#pragma unroll
+      for (int ww = 1; ww < NW; ++ww) {
+        const f32x4 o = red[ww][c][ln];
+        s[0] += o[0];
+        s[1] += o[1];
+        s[2] += o[2];
+        s[3] += o[3];
+      }
+      const int a = c0 + c, t = a % KT, q = (a / KT) % Q, p = (a / (KT * Q)) % NP, ui = a / (KT * Q * NP);
+      const int jj = ln & 15, gg = ln >> 4;
+      const int n = p * (N / NP) + (u0 + ui) * G + E * (jj >> 2) + 4 * q + (jj & 3);
+      st16(partg + (int64_t)n * KO + 16 * t + 4 * gg,
+           u32x4{__float_as_uint(s[0]), __float_as_uint(s[1]), __float_as_uint(s[2]), __float_as_uint(s[3])});
+    }
+    __syncthreads();
+  }
+}
+
+// out[n][k] = sum over the rg row groups of part[.][n][k] in group order (fp32), for nk = N KO
+// entries; 4 consecutive k per thread.  rg == 0 (no rows) writes zeros.
+template <bool OUT_F32>
+__global__ __launch_bounds__(256) void k_sum_parts(const float* __restrict__ part, int rg, int64_t nk, int KO,
+                                                   void* __restrict__ out, int64_t ldo) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= nk) return;
+  float s[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < rg; ++r) {
+    const u32x4 v = ld16(part + (int64_t)r * nk + i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s[e] += __uint_as_float(v[e]);
+  }
+  const int64_t n = i / KO, k = i % KO;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if constexpr (OUT_F32) reinterpret_cast<float*>(out)[n * ldo + k + e] = s[e];
+    else reinterpret_cast<uint16_t*>(out)[n * ldo + k + e] = (uint16_t)pack_bf16x2(s[e], 0.f);
+  }
+}
+
 // ------------------------------------------------------------------ host side
 template <int BITS, int G, int R, int NW, int UPW>
 static int softmax_launch(const lrq_tensors* t, const void* dp, int64_t lddp, void* ds, int64_t ldds, hipStream_t s) {
@@ -459,7 +620,73 @@ static int gemm_nout(const lrq_tensors* t, const void* a, int n_out, void* out, 
   }
 }
 
-#define LRQ_FORMATS(F, ...)                                   \
+// Transposed dequant-GEMM.  Units per wave: 2 when that keeps the lane's accumulators at <= 16
+// f32x4 and the row's units pair up, else 1.  Row groups: enough workgroups for about one per
+// CU on MI355X (a fixed 256, so the summation order depends only on the shapes), at least NW
+// blocks per group.  The workspace holds one fp32 [N, n_out] partial per row group.
+static constexpr int gemm_t_upw_cap(int bits, int group, int kt) {
+  return 2 * (8 / bits) * (group / 16) * kt <= 16 ? 2 : 1;
+}
+
+struct GemmTPlan {
+  int upw, cg, rg, bpg;
+  int64_t ws_bytes;
+};
+
+static GemmTPlan gemm_t_plan(int64_t rows, int64_t hidden, int bits, int group, int n_out) {
+  constexpr int NW = 8;
+  GemmTPlan pl{};
+  const int64_t units = hidden / ((int64_t)group * (8 / bits));
+  pl.upw = (gemm_t_upw_cap(bits, group, n_out / 16) == 2 && units % 2 == 0) ? 2 : 1;
+  pl.cg = (int)(units / pl.upw);
+  const int64_t nrb = (rows + 15) / 16;
+  if (nrb == 0) return pl;  // rg = 0: the sum kernel writes zeros
+  const int64_t want = std::max<int64_t>(1, (256 + pl.cg - 1) / pl.cg);
+  const int64_t rg = std::min<int64_t>(want, std::max<int64_t>(1, nrb / NW));
+  pl.bpg = (int)((nrb + rg - 1) / rg);
+  pl.rg = (int)((nrb + pl.bpg - 1) / pl.bpg);
+  pl.ws_bytes = (int64_t)pl.rg * hidden * n_out * 4;
+  return pl;
+}
+
+template <int BITS, int G, int R, int KT, int UPW, bool F32>
+static int gemm_t_run(const lrq_tensors* t, const void* gmat, int64_t ldg, void* out, int64_t ldo, float* ws,
+                      const GemmTPlan& pl, hipStream_t s) {
+  constexpr int NW = 8;
+  const int M = (int)t->rows, N = (int)t->hidden;
+  if (pl.rg > 0)
+    hipLaunchKernelGGL((k_dequant_gemm_t<BITS, G, R, KT, NW, UPW>), dim3(pl.cg, pl.rg), dim3(NW * 64), 0, s,
+                       (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
+                       (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)gmat, ldg, ws,
+                       pl.bpg);
+  const int64_t nk = (int64_t)N * 16 * KT;
+  hipLaunchKernelGGL(k_sum_parts<F32>, dim3((unsigned)((nk / 4 + 255) / 256)), dim3(256), 0, s, ws, pl.rg, nk,
+                     16 * KT, out, ldo);
+  return launch_status();
+}
+
+template <int BITS, int G, int R, int KT, bool F32>
+static int gemm_t_upw(const lrq_tensors* t, const void* gmat, int64_t ldg, void* out, int64_t ldo, float* ws,
+                      const GemmTPlan& pl, hipStream_t s) {
+  if constexpr (gemm_t_upw_cap(BITS, G, KT) == 2) {
+    if (pl.upw == 2) return gemm_t_run<BITS, G, R, KT, 2, F32>(t, gmat, ldg, out, ldo, ws, pl, s);
+  }
+  return gemm_t_run<BITS, G, R, KT, 1, F32>(t, gmat, ldg, out, ldo, ws, pl, s);
+}
+
+template <int BITS, int G, int R>
+static int gemm_t_nout(const lrq_tensors* t, const void* gmat, int64_t ldg, int n_out, void* out, int64_t ldo,
+                       bool f32, float* ws, const GemmTPlan& pl, hipStream_t s) {
+  switch (n_out * 2 + (f32 ? 1 : 0)) {
+    case 16 * 2 + 1: return gemm_t_upw<BITS, G, R, 1, true>(t, gmat, ldg, out, ldo, ws, pl, s);
+    case 16 * 2: return gemm_t_upw<BITS, G, R, 1, false>(t, gmat, ldg, out, ldo, ws, pl, s);
+    case 32 * 2 + 1: return gemm_t_upw<BITS, G, R, 2, true>(t, gmat, ldg, out, ldo, ws, pl, s);
+    case 32 * 2: return gemm_t_upw<BITS, G, R, 2, false>(t, gmat, ldg, out, ldo, ws, pl, s);
+    default: return LRQ_ERR_UNSUPPORTED;
+  }
+}
+
+#define LRQ_FORMATS(F, ...)                                 \
   switch (format_key(t->bits, t->group, t->rank)) {           \
     case format_key(4, 64, 0): return F<4, 64, 0>(__VA_ARGS__);    \
     case format_key(4, 64, 16): return F<4, 64, 16>(__VA_ARGS__);  \
@@ -504,4 +731,33 @@ extern "C" int lrq_dequant_gemm(const lrq_tensors* t, const void* a, int32_t n_o
   hipStream_t s = (hipStream_t)stream;
   const bool f32 = out_fp32 != 0;
   LRQ_FORMATS(gemm_nout, t, a, n_out, out, ldo, f32, s)
+}
+
+extern "C" int64_t lrq_dequant_gemm_t_workspace(const lrq_tensors* t, int32_t n_out) {
+  int st = validate_tensors(t);
+  if (st) return st;
+  if (n_out != 16 && n_out != 32) return LRQ_ERR_UNSUPPORTED;
+  return gemm_t_plan(t->rows, t->hidden, t->bits, t->group, n_out).ws_bytes;
+}
+
+extern "C" int lrq_dequant_gemm_t(const lrq_tensors* t, const void* g, int64_t ldg, int32_t n_out, void* out,
+                                  int64_t ldo, int32_t out_fp32, void* workspace, int64_t workspace_bytes,
+                                  void* stream) {
+  int st = validate_tensors(t);
+  if (st) return st;
+  if (g == nullptr || out == nullptr) return LRQ_ERR_NULL;
+  if (n_out != 16 && n_out != 32) return LRQ_ERR_UNSUPPORTED;
+  if (ldg < n_out || ldo < n_out) return LRQ_ERR_SHAPE;
+  if (!aligned(g, 8) || (ldg % 4) != 0 || !aligned(out, out_fp32 ? 4 : 2)) return LRQ_ERR_ALIGN;
+  if ((t->flags & LRQ_FLAG_HADAMARD) || t->n_outlier > 0) return LRQ_ERR_UNSUPPORTED;
+  const GemmTPlan pl = gemm_t_plan(t->rows, t->hidden, t->bits, t->group, n_out);
+  if (pl.ws_bytes > 0) {
+    if (workspace == nullptr) return LRQ_ERR_NULL;
+    if (workspace_bytes < pl.ws_bytes) return LRQ_ERR_WORKSPACE;
+    if (!aligned(workspace, 16)) return LRQ_ERR_ALIGN;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  const bool f32 = out_fp32 != 0;
+  float* ws = reinterpret_cast<float*>(workspace);
+  LRQ_FORMATS(gemm_t_nout, t, g, ldg, n_out, out, ldo, f32, ws, pl, s)
 }

@@ -23,7 +23,7 @@ from dataclasses import dataclass, field
 
 import torch
 
-__all__ = ["Config", "CONFIGS", "activation", "basis", "gradient", "softmax_probs", "make"]
+__all__ = ["Config", "CONFIGS", "activation", "basis", "gradient", "softmax_probs", "lora_factor", "make"]
 
 
 @dataclass(frozen=True)
@@ -38,7 +38,8 @@ class Config:
     outlier_scale: float = 1.0
     keep_channels: int = 0      # channels kept dense as fp16 side columns (top-k by abs-max)
     hadamard: bool = False
-    consumer: str = "decode"    # decode | silu | gelu | softmax
+    consumer: str = "decode"    # decode | silu | gelu | softmax | lora
+    lora_rank: int = 16         # consumer "lora": n of the LoRA factor A [hidden, n] and of g [rows, n]
     grad_std: float = 0.02
     seed: int = 0
     softmax_shape: tuple = field(default=())
@@ -53,6 +54,8 @@ CONFIGS = {
     "c4": Config("c4", 16384, 5120, 16, 4, 64, n_outlier=16, outlier_scale=30.0, hadamard=True, seed=4),
     "c5": Config("c5", 2 * 32 * 2048, 2048, 16, 4, 64, consumer="softmax", seed=5,
                  softmax_shape=(2, 32, 2048, 2048)),
+    # the LoRA layer's backward from the north-star format: x A and dA = x^T (dy B^T)
+    "lora": Config("lora", 16384, 4096, 16, 4, 64, n_outlier=8, outlier_scale=20.0, consumer="lora", seed=6),
 }
 
 
@@ -101,6 +104,16 @@ def make(cfg: Config, rows: int | None = None, device="cpu") -> dict:
     else:
         out["x"] = activation(rows, cfg.hidden, cfg.n_outlier, cfg.outlier_scale, cfg.seed, device)
     out["V"] = basis(cfg.hidden, cfg.rank, cfg.seed) if cfg.rank else None
-    if cfg.consumer != "decode":
+    if cfg.consumer == "lora":
+        out["a"] = lora_factor(cfg.hidden, cfg.lora_rank, cfg.seed, device)
+        out["g"] = gradient((rows, cfg.lora_rank), 0.05, cfg.seed, device)
+    elif cfg.consumer != "decode":
         out["dy"] = gradient((rows, cfg.hidden), cfg.grad_std, cfg.seed, device)
     return out
+
+
+def lora_factor(hidden: int, n: int, seed: int = 0, device="cpu") -> torch.Tensor:
+    """A LoRA factor A[hidden, n] ~ N(0, 1/hidden); bf16."""
+    g = _gen(seed + 3_000_017, device)
+    return (torch.randn((hidden, n), generator=g, device=device, dtype=torch.float32) / math.sqrt(hidden)
+            ).to(torch.bfloat16)
