@@ -6,11 +6,12 @@ Default workload (BASELINE.json metric): rank-16 int4/g64 encode + decode of a b
 rotate over several HBM-resident buffer sets (> 512 MB of X) so the 256 MB MALL cannot
 serve them.  Prints ONE JSON line (driver contract).
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config north_star|c1|c2|c3|c4|c5|lora]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config north_star|c1|c2|c3|c4|c5|lora|legacy]
                   [--no-cpu-baseline]
 
 value       = activation GB/s = 2*rows*hidden bytes / (encode + decode time per step);
-              fused-consumer configs: / (consumer time); lora: / (x A + x^T g time)
+              fused-consumer configs: / (consumer time); lora: / (x A + x^T g time);
+              legacy: / (encode + outlier compaction + decode time)
 roofline    = dominant kernel's algorithmic HBM bytes per launch / its mean duration
               (K back-to-back launches between HIP events on the launch stream), against
               8 TB/s; traffic = rocprofv3 FETCH_SIZE/WRITE_SIZE bytes per launch from profiles/
@@ -85,7 +86,22 @@ def cpu_baseline(cfg, seconds: float):
         V = pkg.inputs.basis(cfg.hidden, cfg.rank, cfg.seed) if cfg.rank else None
         vb = as_bits(V) if V is not None else None
 
+        def run_legacy(r):
+            ops = pkg.inputs.legacy_operands(cfg)
+            lb, rb, sb = as_bits(ops["l"][:r]), as_bits(ops["r"]), as_bits(ops["s"])
+            xb = as_bits(pkg.inputs.activation(r, cfg.hidden, cfg.n_outlier, cfg.outlier_scale, cfg.seed))[None]
+            tau = O.kth_smallest_abs(O.legacy_residual(lb, rb, xb[0]), int(xb[0].size * 0.99))
+            t0 = time.perf_counter()
+            o, q = O.legacy_encode(lb, rb, xb, sb, cfg.bits, tau)
+            idx, vals = O.to_coo(o)
+            dense = np.zeros_like(o)
+            dense[tuple(idx)] = vals
+            O.legacy_decode(lb, rb, q, dense, sb, cfg.bits)
+            return time.perf_counter() - t0
+
         def run(r):
+            if cfg.consumer == "legacy":
+                return run_legacy(r)
             inp = pkg.inputs.make(cfg, rows=r)
             xb = as_bits(inp["x"])
             idx = None
@@ -116,7 +132,8 @@ def cpu_baseline(cfg, seconds: float):
                 rows = min(cfg.rows, max(rows, int(rows * seconds / max(t, 1e-3))))
                 t = run(rows)
         gbs = 2 * rows * cfg.hidden / t / 1e9
-        what = {"decode": "encode+decode", "lora": "decode + x A + x^T g (LoRA factor gradients)"}.get(
+        what = {"decode": "encode+decode", "lora": "decode + x A + x^T g (LoRA factor gradients)",
+                "legacy": "legacy encode + outliers to COO + decode"}.get(
             cfg.consumer, f"decode+{cfg.consumer} backward")
         return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
                 "sample": f"numpy CPU oracle {what} of {rows} of {cfg.rows} rows x {cfg.hidden} "
@@ -132,10 +149,73 @@ def consumer_bytes(rows, hidden, rank, bits, group, n_side=0):
     return b + 2 * rows * n_side
 
 
+def build_plan_legacy(cfg, pkg, lib, dev, nbuf):
+    """The reference's own format: encode (codes + dense outliers), the GPU compaction of the
+    outliers to COO, and the decode reading the COO pieces; l / r rows sized for x[1, M, N]."""
+    import torch
+    c_void_p = ctypes.c_void_p
+    sp = c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    M, N, K, bits = cfg.rows, cfg.hidden, cfg.rank, cfg.bits
+    ops = pkg.inputs.legacy_operands(cfg, dev)
+    l, r, s = ops["l"], ops["r"], ops["s"]
+    rt = r.t().contiguous()
+    npc = (N + 63) // 64
+    cap = M * N // 32
+    wsb = lib.lrq_coo_workspace(1, M, N)
+    sets = []
+    for i in range(nbuf):
+        x = pkg.inputs.activation(M, N, cfg.n_outlier, cfg.outlier_scale, cfg.seed + i, dev).view(1, M, N)
+        sets.append(dict(x=x, o=torch.empty_like(x), q=torch.empty((1, M, N * bits // 8), dtype=torch.uint8, device=dev),
+                         idx=torch.empty((3, cap), dtype=torch.int64, device=dev),
+                         vals=torch.empty((cap,), dtype=torch.bfloat16, device=dev),
+                         nnz=torch.empty((1,), dtype=torch.int64, device=dev),
+                         ptr=torch.empty((M * npc + 1,), dtype=torch.int64, device=dev),
+                         ws=torch.empty(((wsb + 7) // 8,), dtype=torch.int64, device=dev),
+                         out=torch.empty_like(x)))
+    tau = float(pkg.outlier_threshold(l, r, sets[0]["x"]).item())  # 1 % outliers, as the reference calibrates
+    P = lambda t: c_void_p(t.data_ptr())  # noqa: E731
+    enc = lambda k: lib.lrq_legacy_encode(P(l), P(rt), K, P(sets[k]["x"]), 1, M, N, M * N, N, P(s), 1, bits,  # noqa: E731
+                                          tau, P(sets[k]["o"]), P(sets[k]["q"]), sp)
+    cmp_ = lambda k: lib.lrq_coo_compact(P(sets[k]["o"]), 1, M, N, P(sets[k]["idx"]), cap, P(sets[k]["vals"]),  # noqa: E731
+                                         cap, P(sets[k]["nnz"]), P(sets[k]["ptr"]), P(sets[k]["ws"]), wsb, sp)
+    dec = lambda k: lib.lrq_legacy_decode_coo(P(l), P(rt), K, P(sets[k]["q"]), P(sets[k]["ptr"]),  # noqa: E731
+                                              c_void_p(sets[k]["idx"].data_ptr() + 2 * cap * 8), P(sets[k]["vals"]),
+                                              cap, P(s), 1, 1, M, N, bits, P(sets[k]["out"]), sp)
+    for k in range(nbuf):
+        if enc(k) or cmp_(k):
+            raise RuntimeError("legacy encode / compaction failed")
+    torch.cuda.synchronize()
+    nnz = max(int(st["nnz"].item()) for st in sets)
+    if nnz > cap:
+        raise RuntimeError(f"{nnz} outliers exceed the bench capacity {cap}")
+    small = 2 * (M * K + N * K) + 2 * N
+    entries = [
+        ("encode", enc, M * N * (2 + bits / 8 + 2) + small, 2 * M * N * K),
+        # algorithmic: the dense outliers read once, the COO written, the piece pointers written
+        ("compact", cmp_, M * N * 2 + nnz * 26 + M * npc * 8, 0),
+        ("decode", dec, M * N * (bits / 8 + 2) + nnz * 10 + M * npc * 8 + small, 2 * M * N * K),
+    ]
+    # the reference's sparse conversion of the same dense outliers, for comparison (it
+    # synchronises the host to size its output): mean over 20 calls
+    o0 = sets[0]["o"]
+    o0.to_sparse()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(20):
+        o0.to_sparse()
+    torch.cuda.synchronize()
+    sets[0]["torch_to_sparse_us"] = (time.perf_counter() - t0) / 20 * 1e6
+    sets[0]["nnz_count"] = nnz
+    sets[0]["tau"] = tau
+    return entries, 2 * M * N, ["encode", "compact", "decode"], sets
+
+
 def build_plan(cfg, pkg, lib, dev, nbuf):
     """Per-config step: a list of (name, launch(k) -> status, algorithmic bytes, mfma flops) run
     in order on buffer set k, plus the step's activation bytes and how `value` is formed."""
     import torch
+    if cfg.consumer == "legacy":
+        return build_plan_legacy(cfg, pkg, lib, dev, nbuf)
     c_void_p = ctypes.c_void_p
     sp = c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     M, N, r = cfg.rows, cfg.hidden, cfg.rank
@@ -314,6 +394,8 @@ def main():
     else:
         value = act_bytes / (sum(kernels[t]["mean_us"] for t in timed) * 1e-6) / 1e9
         workload = f"fused {' + '.join(timed)} on the compressed activation (encode timed alongside)"
+        if cfg.consumer == "legacy":
+            workload = "reference format: encode + outliers to COO on the GPU + decode from the COO pieces"
     dom_name, dom_alg, dom_us = None, 0, -1.0
     for name, _, alg, _ in entries:
         if kernels[name]["mean_us"] > dom_us:
@@ -343,6 +425,9 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": (traffic or {}).get("bytes_per_launch")},
     }
+    if cfg.consumer == "legacy":
+        line["legacy"] = {"outliers": _sets[0]["nnz_count"], "threshold": _sets[0]["tau"],
+                          "torch_to_sparse_us": round(_sets[0]["torch_to_sparse_us"], 1)}
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -181,6 +181,43 @@ int lrq_legacy_decode(const void* l, const void* rt, int32_t K, const void* q, c
                       const void* s, int64_t s_rows, int64_t B, int64_t M, int64_t N, int32_t bits,
                       void* out, void* stream);
 
+/* Dense -> COO compaction of the legacy outliers o[B, M, N] (bf16, contiguous): the coalesced COO
+ * tensor o.to_sparse() builds (low_rank_extraction_fuse_compression_quantization.py:149), on the
+ * device and without a host synchronisation.  Entries (bf16 bits not +-0) in row-major order:
+ * indices int64 [3, ld_idx] (rows b, m, n; entry e in column e), values bf16 [cap]; entries at
+ * positions >= cap are not written, and *nnz (int64, device) is the full count, so nnz > cap
+ * tells the caller to grow the buffers and call again.  piece_ptr int64 [B*M*ceil(N/64) + 1]
+ * receives the first entry of every 64-column piece of a row (the last element is nnz): the
+ * lookup lrq_legacy_decode_coo reads.  workspace: lrq_coo_workspace(B, M, N) bytes, 8-aligned. */
+int lrq_coo_compact(const void* o, int64_t B, int64_t M, int64_t N, int64_t* indices, int64_t ld_idx,
+                    void* values, int64_t cap, int64_t* nnz, int64_t* piece_ptr, void* workspace,
+                    int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes of lrq_coo_compact (>= 0), or a negative LRQ_ERR_*.  Host only. */
+int64_t lrq_coo_workspace(int64_t B, int64_t M, int64_t N);
+
+/* lrq_legacy_decode with the outliers as COO pieces instead of a dense tensor: piece_ptr as
+ * lrq_coo_compact writes it, cols = the entries' column indices (int64, row 2 of its indices),
+ * vals = their bf16 values, n_entries = how many entries cols / vals hold (reads are clamped to
+ * it: entries a too-small compaction dropped are missing from the result, so check nnz first).  Each element adds the outlier of its own column, if any, at the same
+ * point of the torch form as the dense decode: the two give the same bits.  Replaces the
+ * o.to_dense() of low_rank_addition_fuse_decompression_dequantization
+ * (low_rank_extraction_fuse_decompression_dequantization.py:136). */
+int lrq_legacy_decode_coo(const void* l, const void* rt, int32_t K, const void* q, const int64_t* piece_ptr,
+                          const int64_t* cols, const void* vals, int64_t n_entries, const void* s,
+                          int64_t s_rows, int64_t B, int64_t M, int64_t N, int32_t bits, void* out,
+                          void* stream);
+
+/* *out = the k-th smallest (1-based) of |bf16(x - bf16(l @ r))| over one [M, N] slice of x (rows
+ * ldx_m apart), as fp32 on the device: the outlier threshold
+ * torch.kthvalue((x[0] - L_x @ R_x).flatten().abs().to(torch.float32), k) of
+ * low_rank_system_profile_forward.py:45 (k = numel * 0.99 there), with the residual computed as
+ * lrq_legacy_encode computes it.  Two histogram passes over the 15-bit magnitudes; M * N < 2^32,
+ * 1 <= k <= M * N.  workspace >= 2048 bytes, 16-aligned. */
+int lrq_legacy_kth_residual(const void* l, const void* rt, int32_t K, const void* x, int64_t M, int64_t N,
+                            int64_t ldx_m, int64_t k, float* out, void* workspace, int64_t workspace_bytes,
+                            void* stream);
+
 /* Fused legacy consumers (no outliers): op = 0 store x_hat, 1 SiLU backward with y as dy
  * (extraction_fuse_silu_backward.py:192-216), 2 elementwise product with y
  * (extraction_fuse_hadamard.py:185-209).  y, out: [B, M, N] bf16 contiguous. */

@@ -49,7 +49,8 @@ __all__ = [
     # consumers
     "silu_bwd", "gelu_bwd", "softmax_bwd", "mul", "gemm", "gemm_t", "round_out",
     # legacy (reference torch forms)
-    "legacy_matmul_bf16", "legacy_encode", "legacy_decode", "naive_roundtrip",
+    "legacy_matmul_bf16", "legacy_encode", "legacy_decode", "naive_roundtrip", "legacy_residual",
+    "kth_smallest_abs", "to_coo",
     "lowrank_add",
 ]
 
@@ -489,6 +490,33 @@ def legacy_encode(l_bits, r_bits, x_bits, s_bits, bits: int = 8, outlier: float 
     half = 1 << (bits - 1)
     c = (np.clip(np.rint(d), -half, half - 1) + half).astype(np.uint8)
     return bf16_round(o), pack_rowplanar(c, bits)
+
+
+def legacy_residual(l_bits, r_bits, x_bits) -> np.ndarray:
+    """``x - l @ r`` on bf16 tensors (bf16(l @ r), then the bf16 subtraction), as the encode's
+    first line (low_rank_extraction_fuse_compression_quantization.py:154) and the threshold
+    calibration (low_rank_system_profile_forward.py:45) compute it.  Returns bf16 bits."""
+    lr = bf16_to_f32(legacy_matmul_bf16(l_bits, r_bits))
+    return _bf16_op(bf16_to_f32(np.asarray(x_bits, dtype=np.uint16)), lr, np.subtract)
+
+
+def kth_smallest_abs(x_bits, k: int) -> np.float32:
+    """``torch.kthvalue(x.flatten().abs().to(torch.float32), k).values`` for bf16 x: the k-th
+    smallest magnitude, 1-based (low_rank_system_profile_forward.py:45).
+    Pinned by: torch.kthvalue on the same magnitudes (tests/test_oracle.py)."""
+    a = np.abs(bf16_to_f32(np.asarray(x_bits, dtype=np.uint16)).ravel())
+    return np.float32(np.partition(a, k - 1)[k - 1])
+
+
+def to_coo(o_bits):
+    """``o.to_sparse()`` of a bf16 tensor (low_rank_extraction_fuse_compression_quantization.py:149,
+    :170): the entries whose value is not zero (bits other than +0 / -0), in row-major order;
+    returns (indices int64 [ndim, nnz], value bits uint16 [nnz]).
+    Pinned by: torch's to_sparse on the same tensor (tests/test_oracle.py)."""
+    o_bits = np.asarray(o_bits, dtype=np.uint16)
+    nz = (o_bits & 0x7FFF) != 0
+    idx = np.stack(np.nonzero(nz)).astype(np.int64) if o_bits.ndim else np.zeros((0, 0), np.int64)
+    return idx, o_bits[nz]
 
 
 def legacy_decode(l_bits, r_bits, q, o_bits, s_bits, bits: int = 8):

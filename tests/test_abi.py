@@ -130,6 +130,36 @@ def test_dequant_gemm_t_arguments(L):
     assert call(_desc(L, flags=1)) == L.LRQ_ERR_UNSUPPORTED
 
 
+def test_coo_and_threshold_arguments(L):
+    """Workspace sizes (host only) and argument errors of the outlier compaction, the COO decode
+    and the threshold selection."""
+    assert L.call_raw("lrq_coo_workspace", 2, 100, 1024) == ((2 * 100 * 16 + 4095) // 4096) * 16
+    assert L.call_raw("lrq_coo_workspace", 1, 0, 64) == 0
+    assert L.call_raw("lrq_coo_workspace", 1, 4, 0) == L.LRQ_ERR_SHAPE
+    p, w = ctypes.c_void_p(0x10000), ctypes.c_void_p(0x40000)
+    compact = lambda o=p, cap=64, ld=64, ws=w, wb=16, nnz=p, ptr=p: L.call_raw(  # noqa: E731
+        "lrq_coo_compact", o, 1, 16, 512, p, ld, p, cap, nnz, ptr, ws, wb, None)
+    assert compact(o=None) == L.LRQ_ERR_NULL
+    assert compact(ptr=None) == L.LRQ_ERR_NULL
+    assert compact(ld=32) == L.LRQ_ERR_SHAPE             # ld_idx < cap
+    assert compact(ws=None) == L.LRQ_ERR_NULL
+    assert compact(wb=8) == L.LRQ_ERR_WORKSPACE
+    assert compact(nnz=ctypes.c_void_p(0x10004)) == L.LRQ_ERR_ALIGN
+    dec = lambda K=16, ptr=p, n=10, cols=p: L.call_raw(  # noqa: E731
+        "lrq_legacy_decode_coo", p, p, K, p, ptr, cols, p, n, p, 1, 1, 64, 1024, 4, p, None)
+    assert dec(K=8) == L.LRQ_ERR_UNSUPPORTED
+    assert dec(ptr=None) == L.LRQ_ERR_NULL
+    assert dec(n=-1) == L.LRQ_ERR_SHAPE
+    assert dec(cols=None) == L.LRQ_ERR_NULL
+    kth = lambda k=5, ws=w, wb=2048, M=64: L.call_raw(  # noqa: E731
+        "lrq_legacy_kth_residual", p, p, 16, p, M, 1024, 1024, k, p, ws, wb, None)
+    assert kth(k=0) == L.LRQ_ERR_SHAPE
+    assert kth(k=64 * 1024 + 1) == L.LRQ_ERR_SHAPE
+    assert kth(ws=None) == L.LRQ_ERR_NULL
+    assert kth(wb=1024) == L.LRQ_ERR_WORKSPACE
+    assert kth(M=1 << 23) == L.LRQ_ERR_SHAPE             # M * N >= 2^32: 32-bit bin counts
+
+
 def test_legacy_argument_errors(L):
     p = ctypes.c_void_p(0x10000)
     enc = lambda K, bits, N=1024, s_rows=1: L.call_raw(  # noqa: E731

@@ -185,3 +185,92 @@ def test_outlier_extraction_forms(pkg, dev):
     ref = xb.copy()
     ref[:, idx, :] = 0
     assert np.array_equal(bits16(x2), ref)
+
+
+# ------------------------------------------------------------------ outliers as COO on the GPU
+COO_SHAPES = [(2, 100, 1024), (1, 33, 70), (64, 4096), (5000,), (3, 7, 96), (2, 3, 4, 64)]
+
+
+def _sparse_dense(shape, seed, keep=0.03):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(shape, generator=g) * 8
+    x = torch.where(torch.rand(shape, generator=g) < 1 - keep, torch.zeros(shape), x)
+    x.view(-1)[::11] = -0.0  # negative zeros are not entries
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("shape", COO_SHAPES)
+def test_coo_compaction_is_to_sparse(pkg, dev, shape):
+    """The GPU compaction gives o.to_sparse() exactly (indices, value bits, coalesced), and piece
+    pointers = the first entry of every 64-column piece of a row."""
+    print(f"[coo] shape={shape}", flush=True)
+    x = _sparse_dense(shape, sum(shape))
+    idx_ref, val_ref = O.to_coo(bits16(x))
+    sp = pkg.legacy._to_sparse(x.to(dev))
+    torch.cuda.synchronize()
+    assert sp.is_sparse and sp.is_coalesced() and tuple(sp.shape) == shape
+    assert np.array_equal(sp.indices().cpu().numpy(), idx_ref)
+    assert np.array_equal(bits16(sp.values()), val_ref)
+    if len(shape) <= 3:
+        c = pkg.compact_outliers(x.to(dev))
+        B, M, N = (1,) * (3 - len(shape)) + shape
+        full = np.zeros((3, idx_ref.shape[1]), np.int64)
+        full[3 - len(shape):] = idx_ref
+        npc = (N + 63) // 64
+        pid = (full[0] * M + full[1]) * npc + full[2] // 64
+        ptr_ref = np.searchsorted(pid, np.arange(B * M * npc + 1))
+        assert np.array_equal(c.piece_ptr.cpu().numpy(), ptr_ref)
+        assert int(c.nnz.item()) == idx_ref.shape[1]
+
+
+def test_coo_capacity_overflow(pkg, dev):
+    """Fewer slots than entries: the first `cap` entries are written, nnz is the full count and
+    to_sparse refuses."""
+    x = _sparse_dense((40, 1024), 9, keep=0.1)
+    idx_ref, val_ref = O.to_coo(bits16(x))
+    n = idx_ref.shape[1]
+    c = pkg.compact_outliers(x.to(dev), capacity=n // 3)
+    torch.cuda.synchronize()
+    assert int(c.nnz.item()) == n
+    k = n // 3
+    assert np.array_equal(c.indices[1:, :k].cpu().numpy(), idx_ref[:, :k])
+    assert np.array_equal(bits16(c.values[:k]), val_ref[:k])
+    with pytest.raises(RuntimeError):
+        c.to_sparse()
+
+
+@pytest.mark.parametrize("B,M,N,K,bits,s_rows,tau", [CASES[0], CASES[1], CASES[2], CASES[5]])
+def test_legacy_decode_coo_is_dense_decode(pkg, dev, B, M, N, K, bits, s_rows, tau):
+    """The decode that reads COO pieces gives the dense decode's bits, for the encode's own
+    LegacyOutliers (no host synchronisation) and for a torch sparse tensor."""
+    print(f"[coo decode] B={B} M={M} N={N} K={K} bits={bits}", flush=True)
+    l, r, x, s = _inputs(2000 + N + bits, B, M, N, K, s_rows)
+    ld, rd, xd, sd = l.to(dev), r.to(dev), x.to(dev), s.to(dev)
+    oc, q = pkg.legacy_encode_coo(ld, rd, xd, sd, quantize_bit=bits, outlier=tau)
+    o_sp, q2 = pkg.low_rank_addition_fuse_compression_quantization(ld, rd, xd, sd, quantize_bit=bits, outlier=tau)
+    assert torch.equal(q, q2)
+    dense = o_sp.to_dense()
+    a = pkg.low_rank_addition_fuse_decompression_dequantization(ld, rd, q, oc, sd, quantize_bit=bits)
+    b = pkg.low_rank_addition_fuse_decompression_dequantization(ld, rd, q, o_sp, sd, quantize_bit=bits)
+    c = pkg.low_rank_addition_fuse_decompression_dequantization(ld, rd, q, dense, sd, quantize_bit=bits)
+    torch.cuda.synchronize()
+    assert int(oc.nnz.item()) == o_sp._nnz() > 0
+    assert torch.equal(a, c) and torch.equal(b, c)
+    o_ref, _ = O.legacy_encode(bits16(l), bits16(r), bits16(x), bits16(s), bits, tau)
+    xh_ref = O.legacy_decode(bits16(l), bits16(r), q.cpu().numpy(), bits16(dense), bits16(s), bits)
+    assert _frac_mismatch(bits16(a), xh_ref) <= TIE_BUDGET
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 1024, 16), (50, 100, 20), (128, 2048, 32)])
+def test_outlier_threshold_is_kthvalue(pkg, dev, M, N, K):
+    """outlier_threshold = torch.kthvalue(|x[0] - l @ r|, int(numel * 0.99)) of
+    low_rank_system_profile_forward.py:45, on the oracle's residual; and the extreme ranks."""
+    print(f"[kth] M={M} N={N} K={K}", flush=True)
+    l, r, x, _ = _inputs(3000 + N, 2, M, N, K, 1)
+    xr = O.legacy_residual(bits16(l), bits16(r), bits16(x)[0])
+    ld, rd, xd = l.to(dev), r.to(dev), x.to(dev)
+    got = pkg.outlier_threshold(ld, rd, xd)
+    want = O.kth_smallest_abs(xr, int(M * N * 0.99))
+    assert got.item() == want, (got.item(), want)
+    for k in (1, M * N // 3, M * N):
+        assert pkg.residual_kthvalue(ld, rd, xd[0], k).item() == O.kth_smallest_abs(xr, k), k

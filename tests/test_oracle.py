@@ -3,8 +3,8 @@
 Each oracle function is checked against something independent of its own formula:
   * known answers built by construction (tests/golden/known_answers.json, written by
     tests/golden/make_known_answers.py from integer arithmetic alone);
-  * library routines: torch's bf16 / fp16 conversions, torch.matmul, torch.topk and the
-    aten backward functions (silu_backward, gelu_backward(approximate='tanh'),
+  * library routines: torch's bf16 / fp16 conversions, torch.matmul, torch.topk,
+    torch.kthvalue, Tensor.to_sparse, autograd, and the aten backward functions (silu_backward, gelu_backward(approximate='tanh'),
     _softmax_backward_data), evaluated in float64 on the CPU;
   * an independent torch-eager restatement of the reference's torch forms
     (low_rank_extraction_fuse_compression_quantization.py:153-171,
@@ -361,3 +361,46 @@ def test_gemm_t_is_the_lora_factor_gradient():
 def test_round_out_is_single_rounding():
     v = np.array([1.0 + 2 ** -9, 1.0 + 3 * 2 ** -9, -2.5e-3], np.float64)
     assert np.array_equal(O.round_out(v), O.bf16_round(v.astype(np.float32)))
+
+
+def test_legacy_residual_matches_torch_restatement():
+    """legacy_residual = the reference's `x - l @ r` on CPU bf16 tensors (rare GEMM-order flips)."""
+    g = torch.Generator().manual_seed(44)
+    l = (torch.randn(24, 16, generator=g) * 0.5).to(torch.bfloat16)
+    r = (torch.randn(16, 64, generator=g) * 0.5).to(torch.bfloat16)
+    x = (torch.randn(24, 64, generator=g) * 2).to(torch.bfloat16)
+    b16 = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+    got = O.legacy_residual(b16(l), b16(r), b16(x))
+    assert (got != b16(x - l @ r)).mean() <= 2e-3
+    # the encode's residual: with threshold 0 every nonzero residual is an outlier, o == xr
+    o, _ = O.legacy_encode(b16(l), b16(r), b16(x)[None], np.full((1, 64), 0x3F80, np.uint16), 8, 0.0)
+    nz = (got & 0x7FFF) != 0
+    assert np.array_equal(o[0][nz], got[nz])
+
+
+def test_kth_smallest_abs_matches_torch_kthvalue():
+    g = torch.Generator().manual_seed(45)
+    x = (torch.randn(37, 53, generator=g) * 3).to(torch.bfloat16)
+    x[0, :5] = 0.0
+    x[1, :3] = -0.0
+    x[2, :9] = 1.5  # ties
+    xb = x.contiguous().view(torch.int16).numpy().view(np.uint16)
+    n = x.numel()
+    for k in (1, 7, n // 2, int(n * 0.99), n):
+        ref = torch.kthvalue(x.flatten().abs().to(torch.float32), k).values.item()
+        assert O.kth_smallest_abs(xb, k) == np.float32(ref), k
+
+
+@pytest.mark.parametrize("shape", [(2, 5, 70), (40, 33), (300,)])
+def test_to_coo_matches_torch_to_sparse(shape):
+    g = torch.Generator().manual_seed(46)
+    x = torch.randn(shape, generator=g)
+    x = torch.where(torch.rand(shape, generator=g) < 0.9, torch.zeros(shape), x)
+    x.view(-1)[::7] = -0.0  # negative zeros are not entries
+    x = x.to(torch.bfloat16)
+    xb = x.contiguous().view(torch.int16).numpy().view(np.uint16)
+    idx, vals = O.to_coo(xb)
+    sp = x.to_sparse()
+    assert sp.is_coalesced()
+    assert np.array_equal(idx, sp.indices().numpy())
+    assert np.array_equal(vals, sp.values().contiguous().view(torch.int16).numpy().view(np.uint16))

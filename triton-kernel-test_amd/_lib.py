@@ -64,6 +64,14 @@ SIGNATURES = {
                                     c_int64, c_int64, c_int64, c_int32, c_void_p, c_void_p]),
     "lrq_legacy_fused": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int64, c_int64,
                                    c_int64, c_int64, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
+    "lrq_coo_compact": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                                  c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
+    "lrq_coo_workspace": (c_int64, [c_int64, c_int64, c_int64]),
+    "lrq_legacy_decode_coo": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p,
+                                        c_int64, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int32, c_void_p,
+                                        c_void_p]),
+    "lrq_legacy_kth_residual": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_int64, c_int64,
+                                          c_int64, c_void_p, c_void_p, c_int64, c_void_p]),
     "lrq_lowrank_add": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_int64, c_int64,
                                   c_void_p, c_void_p]),
     "lrq_dense_elementwise": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),

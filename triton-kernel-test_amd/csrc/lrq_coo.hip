@@ -1,0 +1,329 @@
+// Dense -> COO compaction of the legacy format's outliers.
+//
+// The reference returns the encode's outliers as `o.to_sparse()`
+// (low_rank_extraction_fuse_compression_quantization.py:149): a coalesced COO tensor whose
+// entry count the host must learn before it can allocate, a device -> host synchronisation in
+// the middle of the encode.  Here the compaction runs on the GPU in three stream-ordered
+// kernels and the count stays on the device:
+//
+//   k_coo_count   a workgroup per chunk of kChunk pieces (a piece = 64 columns of one row,
+//                 8 lanes x 8 columns): nonzeros per piece into LDS, an exclusive scan over
+//                 the chunk, the piece offsets within the chunk into piece_ptr and the chunk
+//                 total into the workspace.
+//   k_coo_scan    one workgroup: exclusive scan of the chunk totals (64-bit), nnz.
+//   k_coo_scatter the count kernel's mapping again: each lane's nonzeros go to
+//                 chunk offset + piece offset + its rank among the piece's 8 lanes, in column
+//                 order, so the entries come out in row-major order (coalesced); piece_ptr
+//                 becomes global.  Entries at positions >= cap are not written.
+//
+// piece_ptr[row * npc + c / 64] is the first entry of the piece holding column c of a row
+// (npc = ceil(N / 64) pieces per row; piece_ptr[rows * npc] = nnz): the legacy decode reads
+// the outliers of a 64-column piece from it without a dense tensor.  A value is an entry when
+// its bf16 bits are not +0 or -0 (what to_sparse keeps of a bf16 tensor).
+#include "lrq_common.h"
+#include "lrq_host.h"
+
+namespace lrq {
+
+constexpr int kPiece = 64;
+constexpr int kChunk = 4096;  // pieces per chunk
+constexpr int kCooThreads = 1024;
+constexpr int kStage = 8 * kPiece;  // entries one wave's 8 pieces can hold
+
+// Exclusive prefix sum over the 1024 threads of the workgroup; returns the total in `total`.
+__device__ __forceinline__ uint32_t coo_block_scan(uint32_t v, uint32_t* wsum, uint32_t& total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  uint32_t incl = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = __shfl_up(incl, d);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+#pragma unroll
+  for (int i = 0; i < kCooThreads / 64; ++i) {
+    const uint32_t t = wsum[i];
+    before += i < w ? t : 0u;
+    all += t;
+  }
+  __syncthreads();
+  total = all;
+  return before + incl - v;
+}
+
+// The nonzero mask of the 8 columns col0 .. col0+7 of one row (bit i: column col0 + i), and
+// their bf16 bits.  VEC: the row is 16-byte aligned and N % 8 == 0, so one 16-byte load.  The
+// loads are unconditional (clamped addresses, values past the row dropped afterwards): a load
+// under a per-lane branch would make the compiler wait for every load in flight at the join.
+template <bool VEC>
+__device__ __forceinline__ uint32_t coo_lane_mask(const uint16_t* __restrict__ row, int64_t col0, int64_t N,
+                                                  uint32_t (&v)[4]) {
+  if (VEC) {
+    const bool in = col0 < N;
+    const u32x4 w = ld16(row + (in ? col0 : N - 8));
+    v[0] = in ? w[0] : 0u, v[1] = in ? w[1] : 0u, v[2] = in ? w[2] : 0u, v[3] = in ? w[3] : 0u;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t c = col0 + 2 * i;
+      const uint32_t lo = row[min(c, N - 1)], hi = row[min(c + 1, N - 1)];
+      v[i] = (c < N ? lo : 0u) | (c + 1 < N ? hi << 16 : 0u);
+    }
+  }
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m |= ((v[i] & 0x7fffu) != 0u ? 1u : 0u) << (2 * i);
+    m |= ((v[i] & 0x7fff0000u) != 0u ? 1u : 0u) << (2 * i + 1);
+  }
+  return m;
+}
+
+// Row offset and piece-in-row of chunk-local piece `local`: 32-bit arithmetic (rem0 < npc <=
+// 2^25, local < kChunk), the chunk's first row and remainder computed once.
+__device__ __forceinline__ void piece_rc(uint32_t rem0, uint32_t npc, uint32_t local, uint32_t& dr, uint32_t& pcol) {
+  const uint32_t t1 = rem0 + local;
+  dr = t1 / npc;
+  pcol = t1 - dr * npc;
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kCooThreads) void k_coo_count(const uint16_t* __restrict__ o, int64_t N, int64_t npc,
+                                                           int64_t npieces, int64_t* __restrict__ piece_ptr,
+                                                           uint32_t* __restrict__ chunk_total) {
+  __shared__ uint32_t cnt[kChunk];
+  __shared__ uint32_t wsum[kCooThreads / 64];
+  const int t = threadIdx.x, q = t & 7;
+  const int64_t pc0 = (int64_t)blockIdx.x * kChunk;
+  const int64_t row0 = pc0 / npc;
+  const uint32_t rem0 = (uint32_t)(pc0 - row0 * npc), npc32 = (uint32_t)npc;
+  // UN iterations' loads are issued before any of them is counted
+  constexpr int UN = 8, IT = kChunk / (kCooThreads / 8);
+  static_assert(IT % UN == 0, "unroll");
+  for (int it0 = 0; it0 < IT; it0 += UN) {
+    uint32_t m[UN];
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const uint32_t local = (it0 + u) * (kCooThreads / 8) + (t >> 3);
+      const uint32_t lc = (uint32_t)min((int64_t)local, npieces - 1 - pc0);  // clamped: loaded, not counted
+      uint32_t dr, pcol;
+      piece_rc(rem0, npc32, lc, dr, pcol);
+      uint32_t v[4];
+      m[u] = coo_lane_mask<VEC>(o + (row0 + dr) * N, (int64_t)pcol * kPiece + 8 * q, N, v);
+      m[u] = pc0 + local < npieces ? m[u] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      uint32_t n = __builtin_popcount(m[u]);
+      n += __shfl_xor(n, 1);
+      n += __shfl_xor(n, 2);
+      n += __shfl_xor(n, 4);
+      if (q == 0) cnt[(it0 + u) * (kCooThreads / 8) + (t >> 3)] = n;
+    }
+  }
+  __syncthreads();
+  constexpr int PPT = kChunk / kCooThreads;  // pieces per thread in the scan
+  uint32_t c[PPT], s = 0;
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    c[i] = cnt[t * PPT + i];
+    s += c[i];
+  }
+  uint32_t total;
+  uint32_t off = coo_block_scan(s, wsum, total);
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const int64_t pc = pc0 + t * PPT + i;
+    if (pc < npieces) piece_ptr[pc] = off;
+    off += c[i];
+  }
+  if (t == 0) chunk_total[blockIdx.x] = total;
+}
+
+// One workgroup: chunk_off[c] = sum of the totals of chunks < c; nnz and piece_ptr[npieces].
+__global__ __launch_bounds__(kCooThreads) void k_coo_scan(const uint32_t* __restrict__ chunk_total, int64_t nchunks,
+                                                          uint64_t* __restrict__ chunk_off, int64_t npieces,
+                                                          int64_t* __restrict__ piece_ptr, int64_t* __restrict__ nnz) {
+  __shared__ uint32_t wsum[kCooThreads / 64];
+  uint64_t base = 0;
+  for (int64_t c0 = 0; c0 < nchunks; c0 += kCooThreads) {
+    const int64_t c = c0 + threadIdx.x;
+    const uint32_t v = c < nchunks ? chunk_total[c] : 0u;
+    uint32_t total;
+    const uint32_t off = coo_block_scan(v, wsum, total);  // < 2^32: 1024 chunks of <= 2^18 entries
+    if (c < nchunks) chunk_off[c] = base + off;
+    base += total;
+  }
+  if (threadIdx.x == 0) {
+    piece_ptr[npieces] = (int64_t)base;
+    nnz[0] = (int64_t)base;
+  }
+}
+
+// Branch-free predicated stores into a wave-uniform region of `len` bytes (an offset past it is
+// dropped by the hardware): the entries are written without per-lane branches, so the loads of
+// the next pieces stay in flight.
+__device__ __forceinline__ void st8_region(void* base, uint32_t len, uint32_t off, uint64_t v, bool keep) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)len, 0x00020000);
+  __builtin_amdgcn_raw_buffer_store_b64(u32x2{(uint32_t)v, (uint32_t)(v >> 32)}, r, keep ? off : 0x7ffffff0u, 0, 0);
+}
+__device__ __forceinline__ void st2_region(void* base, uint32_t len, uint32_t off, uint16_t v, bool keep) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)len, 0x00020000);
+  __builtin_amdgcn_raw_buffer_store_b16(v, r, keep ? off : 0x7ffffff0u, 0, 0);
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kCooThreads) void k_coo_scatter(const uint16_t* __restrict__ o, int64_t M, int64_t N,
+                                                             int64_t npc, int64_t npieces,
+                                                             int64_t* __restrict__ piece_ptr,
+                                                             const uint64_t* __restrict__ chunk_off,
+                                                             const uint32_t* __restrict__ chunk_total,
+                                                             int64_t* __restrict__ idx, int64_t ld_idx,
+                                                             uint16_t* __restrict__ val, int64_t cap) {
+  // per wave: up to 8 pieces x 64 entries, then one dump slot per lane; entry = (row offset,
+  // column, value bits)
+  __shared__ u32x4 stage[kCooThreads / 64][kStage + 64];
+  const int t = threadIdx.x, q = t & 7, lane = t & 63, w = t >> 6;
+  const int64_t pc0 = (int64_t)blockIdx.x * kChunk;
+  const int64_t coff = (int64_t)chunk_off[blockIdx.x];
+  const int64_t row0 = pc0 / npc;
+  const uint32_t rem0 = (uint32_t)(pc0 - row0 * npc), npc32 = (uint32_t)npc;
+  const int64_t b0 = row0 / M;
+  const uint32_t m0 = (uint32_t)(row0 - b0 * M), M32 = (uint32_t)M;
+  // the chunk's entries are positions coff .. coff + total - 1; the part below cap is written
+  const int64_t nw = max((int64_t)0, min((int64_t)chunk_total[blockIdx.x], cap - coff));
+  const uint32_t len8 = (uint32_t)(nw * 8), len2 = (uint32_t)(nw * 2);
+  int64_t* ib = idx + min(coff, cap);
+  int64_t* im = ib + ld_idx;
+  int64_t* in = im + ld_idx;
+  uint16_t* vb = val + min(coff, cap);
+  const uint32_t plen8 = (uint32_t)(min((int64_t)kChunk, npieces - pc0) * 8);
+  constexpr int UN = 4, IT = kChunk / (kCooThreads / 8);
+  static_assert(IT % UN == 0, "unroll");
+  for (int it0 = 0; it0 < IT; it0 += UN) {
+    // loads of UN pieces first (masks, values, piece offsets), then their entries
+    uint32_t mu[UN], vu[UN][4], dru[UN], pcu[UN];
+    int64_t lo[UN];
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const uint32_t local = (uint32_t)min((int64_t)(it0 + u) * (kCooThreads / 8) + (t >> 3), npieces - 1 - pc0);
+      piece_rc(rem0, npc32, local, dru[u], pcu[u]);
+      mu[u] = coo_lane_mask<VEC>(o + (row0 + dru[u]) * N, (int64_t)pcu[u] * kPiece + 8 * q, N, vu[u]);
+      lo[u] = piece_ptr[pc0 + local];
+    }
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const int64_t pc = pc0 + (it0 + u) * (kCooThreads / 8) + (t >> 3);
+      const bool live = pc < npieces;  // past the last piece: a clamped duplicate, written nowhere
+      const uint32_t m = live ? mu[u] : 0u;
+      // rank of this lane's first entry among the piece's 8 lanes (lanes 8k .. 8k+7 of the wave)
+      const uint32_t n = __builtin_popcount(m);
+      uint32_t incl = n;
+#pragma unroll
+      for (int d = 1; d < 8; d <<= 1) {
+        const uint32_t up = __shfl_up(incl, d, 8);
+        if (q >= d) incl += up;
+      }
+      // the wave's 8 pieces are consecutive, so its entries are positions wbase .. wbase + wcnt - 1;
+      // wcnt is the sum of the lanes' counts (lanes past the last piece count nothing; their
+      // clamped offsets must not be used for it)
+      const uint32_t lo32 = (uint32_t)lo[u];
+      const uint32_t wbase = __shfl(lo32, 0);
+      uint32_t wcnt = n;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) wcnt += __shfl_xor(wcnt, d);
+      // stage the lane's entries in the wave's LDS area at their rank (slot kStage + lane takes
+      // the writes of entries a lane does not have: no branch around the stores)
+      uint32_t rel = lo32 + (incl - n) - wbase;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const bool has = (m >> i) & 1u;
+        const uint32_t slot = has ? rel : kStage + lane;
+        stage[w][slot] = u32x4{dru[u], pcu[u] * kPiece + 8 * q + i, (vu[u][i >> 1] >> (16 * (i & 1))) & 0xffffu, 0u};
+        rel += has ? 1u : 0u;
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes are done
+      __builtin_amdgcn_wave_barrier();
+      // write them out coalesced: lane e of each round takes entry e
+      const uint32_t nround = __builtin_amdgcn_readfirstlane((wcnt + 63) / 64);
+      for (uint32_t r = 0; r < nround; ++r) {
+        const uint32_t e = r * 64 + lane;
+        const u32x4 en = stage[w][min(e, (uint32_t)kStage - 1)];
+        const uint32_t mr = m0 + en[0], qb = mr / M32;
+        const bool keep = e < wcnt;
+        const uint32_t off = wbase + e;
+        st8_region(ib, len8, off * 8, (uint64_t)(b0 + qb), keep);
+        st8_region(im, len8, off * 8, (uint64_t)(mr - qb * M32), keep);
+        st8_region(in, len8, off * 8, (uint64_t)en[1], keep);
+        st2_region(vb, len2, off * 2, (uint16_t)en[2], keep);
+      }
+      __builtin_amdgcn_wave_barrier();  // the area is reused by the next piece
+      // the piece's global first entry (the store's value depends on the lanes' reads of it)
+      st8_region(piece_ptr + pc0, plen8, (uint32_t)(pc - pc0) * 8, (uint64_t)(coff + lo[u]), q == 0 && live);
+    }
+  }
+}
+
+struct CooPlan {
+  int64_t npc, npieces, nchunks, ws_bytes;
+};
+
+static CooPlan coo_plan(int64_t B, int64_t M, int64_t N) {
+  CooPlan p{};
+  p.npc = (N + kPiece - 1) / kPiece;
+  p.npieces = B * M * p.npc;
+  p.nchunks = (p.npieces + kChunk - 1) / kChunk;
+  p.ws_bytes = p.nchunks * 16;  // uint32 totals (padded to 8 bytes) + uint64 offsets
+  return p;
+}
+
+}  // namespace lrq
+
+using namespace lrq;
+
+extern "C" int64_t lrq_coo_workspace(int64_t B, int64_t M, int64_t N) {
+  if (B < 0 || M < 0 || N <= 0) return LRQ_ERR_SHAPE;
+  return coo_plan(B, M, N).ws_bytes;
+}
+
+extern "C" int lrq_coo_compact(const void* o, int64_t B, int64_t M, int64_t N, int64_t* indices, int64_t ld_idx,
+                               void* values, int64_t cap, int64_t* nnz, int64_t* piece_ptr, void* workspace,
+                               int64_t workspace_bytes, void* stream) {
+  if (o == nullptr || nnz == nullptr || piece_ptr == nullptr) return LRQ_ERR_NULL;
+  if (B < 0 || M < 0 || N <= 0 || cap < 0 || ld_idx < cap) return LRQ_ERR_SHAPE;
+  if (M > INT32_MAX || N > INT32_MAX) return LRQ_ERR_SHAPE;  // 32-bit row / piece arithmetic
+  if (cap > 0 && (indices == nullptr || values == nullptr)) return LRQ_ERR_NULL;
+  if (!aligned(o, 2) || !aligned(indices, 8) || !aligned(values, 2) || !aligned(nnz, 8) || !aligned(piece_ptr, 8))
+    return LRQ_ERR_ALIGN;
+  const CooPlan p = coo_plan(B, M, N);
+  if (p.nchunks > ((int64_t)1 << 31) - 1) return LRQ_ERR_SHAPE;
+  if (p.nchunks > 0) {
+    if (workspace == nullptr) return LRQ_ERR_NULL;
+    if (workspace_bytes < p.ws_bytes) return LRQ_ERR_WORKSPACE;
+    if (!aligned(workspace, 8)) return LRQ_ERR_ALIGN;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  uint64_t* chunk_off = reinterpret_cast<uint64_t*>(workspace);
+  uint32_t* chunk_total = reinterpret_cast<uint32_t*>(chunk_off + p.nchunks);
+  const bool vec = N % 8 == 0 && aligned(o, 16);
+  const uint16_t* ob = (const uint16_t*)o;
+  if (p.nchunks > 0) {
+    if (vec) hipLaunchKernelGGL(k_coo_count<true>, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, ob, N, p.npc,
+                                p.npieces, piece_ptr, chunk_total);
+    else hipLaunchKernelGGL(k_coo_count<false>, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, ob, N, p.npc,
+                            p.npieces, piece_ptr, chunk_total);
+  }
+  hipLaunchKernelGGL(k_coo_scan, dim3(1), dim3(kCooThreads), 0, s, chunk_total, p.nchunks, chunk_off, p.npieces,
+                     piece_ptr, nnz);
+  if (p.nchunks > 0) {
+    if (vec) hipLaunchKernelGGL(k_coo_scatter<true>, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, ob, M, N,
+                                p.npc, p.npieces, piece_ptr, chunk_off, chunk_total, indices, ld_idx,
+                                (uint16_t*)values, cap);
+    else hipLaunchKernelGGL(k_coo_scatter<false>, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, ob, M, N,
+                            p.npc, p.npieces, piece_ptr, chunk_off, chunk_total, indices, ld_idx, (uint16_t*)values,
+                            cap);
+  }
+  return launch_status();
+}

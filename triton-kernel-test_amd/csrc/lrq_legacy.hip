@@ -12,6 +12,10 @@
 //   fused   decode without outliers, then store / SiLU backward / product with y
 //           (extraction_fuse_silu_backward.py:192-216, extraction_fuse_hadamard.py:185-209)
 //   add     torch_low_rank_addition (low_rank_extraction_speed.py:106-107): bf16(x + bf16(l @ r))
+//   hist    histogram of the 15-bit magnitudes |bf16(x - bf16(l @ r))| (the encode's residual), for
+//           the outlier threshold torch.kthvalue(|x[0] - l @ r|, k) of
+//           low_rank_system_profile_forward.py:45: a 256-bin pass over the top 8 bits, then a
+//           128-bin pass over the low 7 bits of the keys in the selected bin.
 //
 // l is [M, K] and rt = r^T is [N, K] (K = 16 or 32, zero-padded by the caller as the reference
 // pads K < 16); s is [1 or B, N].  bf16(l @ r) is the fp32 rounding of the exact sum, then bf16
@@ -30,7 +34,7 @@
 
 namespace lrq {
 
-enum LegacyMode : int { kEncode = 0, kDecode = 1, kFusedStore = 2, kFusedSilu = 3, kFusedMul = 4, kAdd = 5 };
+enum LegacyMode : int { kEncode = 0, kDecode = 1, kFusedStore = 2, kFusedSilu = 3, kFusedMul = 4, kAdd = 5, kHist = 6 };
 
 struct LegacyArgs {
   const uint16_t* l;    // [M, K]
@@ -41,6 +45,13 @@ struct LegacyArgs {
   int64_t s_rows;
   const uint8_t* qin;   // decode / fused codes [B, M, N/NP]
   const uint16_t* oin;  // decode outliers, dense [B, M, N], or null
+  const int64_t* optr;  // decode outliers as COO: first entry of each 64-column piece of a row,
+  const int64_t* ocol;  //   [B * M * npc + 1]; the entries' column indices and bf16 values, in
+  const uint16_t* oval; //   row-major order (lrq_coo_compact's output)
+  int64_t npc;          // 64-column pieces per row, ceil(N / 64)
+  int64_t ncap;         // entries the COO arrays hold: reads are clamped to [0, ncap)
+  uint32_t* hist;       // hist: 256 global bins
+  const int64_t* sel;   // hist: sel[0] = the selected top-8-bit bin, or -1 in the first pass
   const uint16_t* y;    // fused SiLU dy / product operand [B, M, N]
   uint16_t* out;        // decode / fused / add output [B, M, N]
   uint16_t* oout;       // encode outliers, dense [B, M, N]
@@ -62,12 +73,21 @@ __device__ __forceinline__ uint32_t legacy_code(float x, float lr, float sc, flo
 }
 
 // Decode of one element: bf16(bf16(bf16((code - 2^(b-1)) * s) + o) + lr); with !HAS_O the add
-// of o (exact zero) is skipped.
+// of o (exact zero) is skipped.  The outliers come as a dense tensor (OSRC 1) or as COO pieces
+// (OSRC 2); both feed the same per-element add, so the two give the same bits.
 template <int BITS, bool HAS_O>
 __device__ __forceinline__ float legacy_value(uint32_t code, float sc, float o, float lr) {
   float a = bf16r((float)((int)code - (1 << (BITS - 1))) * sc);
   if constexpr (HAS_O) a = bf16r(a + o);
   return bf16r(a + lr);
+}
+
+// Histogram bin of a residual xr (bf16 value) for the pass that sel selects, or -1 if the key
+// is not counted in this pass.
+__device__ __forceinline__ int hist_bin(float xr, int64_t sel) {
+  const uint32_t key = (__float_as_uint(xr) >> 16) & 0x7fffu;
+  if (sel < 0) return (int)(key >> 7);
+  return (int64_t)(key >> 7) == sel ? (int)(key & 127u) : -1;
 }
 
 template <int MODE>
@@ -77,12 +97,36 @@ __device__ __forceinline__ float legacy_consume(float xh, float yv) {
   else return xh;
 }
 
+// The outlier values of columns c0 .. c0 + E - 1 of row `bm` (b * M + m) from the COO pieces:
+// the entries of the piece holding c0 (the E columns never straddle a piece boundary).
+template <int E>
+__device__ __forceinline__ void coo_piece_values(const LegacyArgs& a, int64_t bm, int64_t c0, float* oo) {
+#pragma unroll
+  for (int e = 0; e < E; ++e) oo[e] = 0.f;
+  const int64_t pc = bm * a.npc + c0 / 64;
+  const int64_t e1 = min(a.optr[pc + 1], a.ncap);
+  for (int64_t k = max(a.optr[pc], (int64_t)0); k < e1; ++k) {
+    const int64_t d = a.ocol[k] - c0;
+    const float v = __uint_as_float((uint32_t)a.oval[k] << 16);
+#pragma unroll
+    for (int e = 0; e < E; ++e) oo[e] = d == e ? v : oo[e];
+  }
+}
+
 // ------------------------------------------------------------------ MFMA path
 // Grid: (ceil(M / (64 * RB)), N / (64 * NP), B); 4 waves; wave w walks row blocks
-// (blockIdx.x * RB + i) * 64 + w * 16, i < RB, of unit blockIdx.y.
-template <int MODE, int BITS, int K, int RB, bool HAS_O>
+// (blockIdx.x * RB + i) * 64 + w * 16, i < RB, of unit blockIdx.y.  OSRC: outliers absent (0),
+// dense (1) or COO pieces (2), decode only.
+template <int MODE, int BITS, int K, int RB, int OSRC>
 __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
-  constexpr int NP = (MODE == kAdd) ? 1 : 8 / BITS, G = 64, E = 16, RT = K / 16;
+  constexpr int NP = (MODE == kAdd || MODE == kHist) ? 1 : 8 / BITS, G = 64, E = 16, RT = K / 16;
+  __shared__ uint32_t lh[MODE == kHist ? 256 : 1];
+  int64_t sel = -1;
+  if constexpr (MODE == kHist) {
+    lh[threadIdx.x] = 0u;
+    sel = a.sel[0];
+    __syncthreads();
+  }
   constexpr uint32_t kMask = BITS == 8 ? 0xffu : (1u << BITS) - 1u;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
@@ -119,11 +163,23 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
 #pragma unroll
       for (int e = 0; e < E; ++e) lr[e] = bf16r(lr[e]);
       float sc[E];
-      if constexpr (MODE != kAdd) {
+      if constexpr (MODE != kAdd && MODE != kHist) {
         unpack8(ld16(srow + c0), sc);
         unpack8(ld16(srow + c0 + 8), sc + 8);
       }
-      if constexpr (MODE == kEncode || MODE == kAdd) {
+      if constexpr (MODE == kHist) {
+        float xv[E];
+        const uint16_t* xp = a.x + rr * a.ldx_m + c0;
+        unpack8(ld16(xp), xv);
+        unpack8(ld16(xp + 8), xv + 8);
+        if (row < M) {
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            const int bin = hist_bin(bf16r(xv[e] - lr[e]), sel);
+            if (bin >= 0) atomicAdd(&lh[bin], 1u);
+          }
+        }
+      } else if constexpr (MODE == kEncode || MODE == kAdd) {
         float xv[E];
         const uint16_t* xp = a.x + (int64_t)b * a.ldx_b + rr * a.ldx_m + c0;
         unpack8(ld16(xp), xv);
@@ -143,10 +199,11 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
         }
       } else {
         float ov[E], oo[E], yv[E];
-        if constexpr (MODE == kDecode && HAS_O) {
+        if constexpr (MODE == kDecode && OSRC == 1) {
           unpack8(ld16(a.oin + erow + c0), oo);
           unpack8(ld16(a.oin + erow + c0 + 8), oo + 8);
         }
+        if constexpr (MODE == kDecode && OSRC == 2) coo_piece_values<E>(a, (int64_t)b * M + rr, c0, oo);
         if constexpr (MODE == kFusedSilu || MODE == kFusedMul) {
           unpack8(ld16(a.y + erow + c0), yv);
           unpack8(ld16(a.y + erow + c0 + 8), yv + 8);
@@ -154,7 +211,7 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
 #pragma unroll
         for (int e = 0; e < E; ++e) {
           const uint32_t code = (qb[e >> 2] >> (8 * (e & 3) + BITS * p)) & kMask;
-          const float xh = legacy_value<BITS, MODE == kDecode && HAS_O>(code, sc[e], oo[e], lr[e]);
+          const float xh = legacy_value<BITS, MODE == kDecode && OSRC != 0>(code, sc[e], oo[e], lr[e]);
           ov[e] = legacy_consume<MODE>(xh, yv[e]);
         }
         st16(a.out + erow + c0, pack8(ov));
@@ -168,11 +225,15 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
       st16(a.qout + ((int64_t)b * M + rr) * NB + u * G + E * g, u32x4{word[0], word[1], word[2], word[3]});
     }
   }
+  if constexpr (MODE == kHist) {
+    __syncthreads();
+    if (lh[threadIdx.x] != 0u) atomicAdd(&a.hist[threadIdx.x], lh[threadIdx.x]);
+  }
 }
 
 // ------------------------------------------------------------------ scalar path
 // One thread per packed byte position c of one row; grid.x enumerates (b, m, 256-byte chunk).
-template <int MODE, int BITS, bool HAS_O>
+template <int MODE, int BITS, int OSRC>
 __global__ __launch_bounds__(256) void k_legacy_scalar(LegacyArgs a, int K, int64_t chunks) {
   constexpr int NP = (MODE == kAdd) ? 1 : 8 / BITS;
   constexpr uint32_t kMask = BITS == 8 ? 0xffu : (1u << BITS) - 1u;
@@ -210,41 +271,109 @@ __global__ __launch_bounds__(256) void k_legacy_scalar(LegacyArgs a, int K, int6
       const float sc = __uint_as_float((uint32_t)srow[col] << 16);
       const uint32_t code = (byte >> (BITS * p)) & kMask;
       float o = 0.f, yv = 0.f;
-      if constexpr (MODE == kDecode && HAS_O) o = __uint_as_float((uint32_t)a.oin[erow + col] << 16);
+      if constexpr (MODE == kDecode && OSRC == 1) o = __uint_as_float((uint32_t)a.oin[erow + col] << 16);
+      if constexpr (MODE == kDecode && OSRC == 2) {
+        const int64_t pc = bm * a.npc + col / 64, e1 = min(a.optr[pc + 1], a.ncap);
+        for (int64_t k = max(a.optr[pc], (int64_t)0); k < e1; ++k)
+          if (a.ocol[k] == col) o = __uint_as_float((uint32_t)a.oval[k] << 16);
+      }
       if constexpr (MODE == kFusedSilu || MODE == kFusedMul) yv = __uint_as_float((uint32_t)a.y[erow + col] << 16);
-      const float xh = legacy_value<BITS, MODE == kDecode && HAS_O>(code, sc, o, lr);
+      const float xh = legacy_value<BITS, MODE == kDecode && OSRC != 0>(code, sc, o, lr);
       a.out[erow + col] = (uint16_t)pack_bf16x2(legacy_consume<MODE>(xh, yv), 0.f);
     }
   }
   if constexpr (MODE == kEncode) a.qout[bm * NB + c] = (uint8_t)qout;
 }
 
+// Scalar form of the hist pass: one thread per column of one row (any shape).
+__global__ __launch_bounds__(256) void k_hist_scalar(LegacyArgs a, int K, int64_t chunks) {
+  __shared__ uint32_t lh[256];
+  lh[threadIdx.x] = 0u;
+  const int64_t sel = a.sel[0];
+  __syncthreads();
+  const int64_t m = blockIdx.x / chunks;
+  const int64_t c = (blockIdx.x - m * chunks) * 256 + threadIdx.x;
+  if (c < a.N) {
+    const uint16_t* lrow = a.l + m * K;
+    const uint16_t* rrow = a.rt + c * K;
+    double acc = 0.0;
+    for (int k = 0; k < K; ++k)
+      acc = __builtin_fma((double)__uint_as_float((uint32_t)lrow[k] << 16),
+                          (double)__uint_as_float((uint32_t)rrow[k] << 16), acc);
+    const float xv = __uint_as_float((uint32_t)a.x[m * a.ldx_m + c] << 16);
+    const int bin = hist_bin(bf16r(xv - bf16r((float)acc)), sel);
+    if (bin >= 0) atomicAdd(&lh[bin], 1u);
+  }
+  __syncthreads();
+  if (lh[threadIdx.x] != 0u) atomicAdd(&a.hist[threadIdx.x], lh[threadIdx.x]);
+}
+
+// hist[0..255] = 0, sel = {-1, k}.
+__global__ __launch_bounds__(256) void k_kth_init(uint32_t* __restrict__ hist, int64_t* __restrict__ sel, int64_t k) {
+  hist[threadIdx.x] = 0u;
+  if (threadIdx.x == 0) {
+    sel[0] = -1;
+    sel[1] = k;
+  }
+}
+
+// The bin holding the sel[1]-th smallest key (1-based) of the histogram.  First pass: sel =
+// {bin, rank within it}, histogram cleared for the second pass.  Second pass (fine): the key
+// (sel[0] << 7 | bin) as an fp32 value in out.  256 threads, one bin each.
+__global__ __launch_bounds__(256) void k_kth_select(uint32_t* __restrict__ hist, int64_t* __restrict__ sel, int fine,
+                                                    float* __restrict__ out) {
+  __shared__ uint64_t wsum[4];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const uint64_t h = (fine && t >= 128) ? 0u : hist[t];
+  const uint64_t k = (uint64_t)sel[1];
+  uint64_t incl = h;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint64_t o = __shfl_up(incl, d);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  for (int i = 0; i < w; ++i) incl += wsum[i];
+  const int64_t prev = sel[0];
+  __syncthreads();  // every thread has read sel before it is rewritten
+  if (incl >= k && incl - h < k) {  // exactly one bin: the cumulative count first reaches k
+    if (!fine) {
+      sel[0] = t;
+      sel[1] = (int64_t)(k - (incl - h));
+    } else {
+      out[0] = __uint_as_float((uint32_t)((prev << 7) | t) << 16);
+    }
+  }
+  hist[t] = 0u;
+}
+
 // ------------------------------------------------------------------ host side
-template <int MODE, int BITS, bool HAS_O>
+template <int MODE, int BITS, int OSRC>
 static int legacy_launch(const LegacyArgs& a, int K, int64_t B, bool mfma_ok, hipStream_t st) {
   constexpr int NP = (MODE == kAdd) ? 1 : 8 / BITS;
   const int64_t NB = a.N / NP;
   if (mfma_ok && NB % 64 == 0 && NB / 64 <= 65535 && B <= 65535) {
     constexpr int RB = 4;
     dim3 grid((unsigned)((a.M + 64 * RB - 1) / (64 * RB)), (unsigned)(NB / 64), (unsigned)B);
-    if (K == 16) hipLaunchKernelGGL((k_legacy_mfma<MODE, BITS, 16, RB, HAS_O>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((k_legacy_mfma<MODE, BITS, 32, RB, HAS_O>), grid, dim3(256), 0, st, a);
+    if (K == 16) hipLaunchKernelGGL((k_legacy_mfma<MODE, BITS, 16, RB, OSRC>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((k_legacy_mfma<MODE, BITS, 32, RB, OSRC>), grid, dim3(256), 0, st, a);
   } else {
     const int64_t chunks = (NB + 255) / 256;
     if (B * a.M * chunks > INT32_MAX) return LRQ_ERR_SHAPE;
-    hipLaunchKernelGGL((k_legacy_scalar<MODE, BITS, HAS_O>), dim3((unsigned)(B * a.M * chunks)), dim3(256), 0, st, a,
+    hipLaunchKernelGGL((k_legacy_scalar<MODE, BITS, OSRC>), dim3((unsigned)(B * a.M * chunks)), dim3(256), 0, st, a,
                        K, chunks);
   }
   return launch_status();
 }
 
-template <int MODE, bool HAS_O>
+template <int MODE, int OSRC>
 static int legacy_bits(const LegacyArgs& a, int K, int64_t B, int bits, bool mfma_ok, hipStream_t st) {
   switch (bits) {
-    case 1: return legacy_launch<MODE, 1, HAS_O>(a, K, B, mfma_ok, st);
-    case 2: return legacy_launch<MODE, 2, HAS_O>(a, K, B, mfma_ok, st);
-    case 4: return legacy_launch<MODE, 4, HAS_O>(a, K, B, mfma_ok, st);
-    case 8: return legacy_launch<MODE, 8, HAS_O>(a, K, B, mfma_ok, st);
+    case 1: return legacy_launch<MODE, 1, OSRC>(a, K, B, mfma_ok, st);
+    case 2: return legacy_launch<MODE, 2, OSRC>(a, K, B, mfma_ok, st);
+    case 4: return legacy_launch<MODE, 4, OSRC>(a, K, B, mfma_ok, st);
+    case 8: return legacy_launch<MODE, 8, OSRC>(a, K, B, mfma_ok, st);
     default: return LRQ_ERR_UNSUPPORTED;
   }
 }
@@ -288,7 +417,7 @@ extern "C" int lrq_legacy_encode(const void* l, const void* rt, int32_t K, const
   a.s = (const uint16_t*)s, a.s_rows = s_rows, a.oout = (uint16_t*)o, a.qout = (uint8_t*)q, a.M = M, a.N = N;
   a.tau = bf16_value_host(bf16_bits_host(outlier));
   const bool mfma_ok = vec_ok({l, rt, x, s, o, q}) && ldx_b % 8 == 0 && ldx_m % 8 == 0 && N % 8 == 0;
-  return legacy_bits<kEncode, false>(a, K, B, bits, mfma_ok, (hipStream_t)stream);
+  return legacy_bits<kEncode, 0>(a, K, B, bits, mfma_ok, (hipStream_t)stream);
 }
 
 extern "C" int lrq_legacy_decode(const void* l, const void* rt, int32_t K, const void* q, const void* o,
@@ -303,8 +432,8 @@ extern "C" int lrq_legacy_decode(const void* l, const void* rt, int32_t K, const
   a.l = (const uint16_t*)l, a.rt = (const uint16_t*)rt, a.s = (const uint16_t*)s, a.s_rows = s_rows;
   a.qin = (const uint8_t*)q, a.oin = (const uint16_t*)o, a.out = (uint16_t*)out, a.M = M, a.N = N;
   const bool mfma_ok = vec_ok({l, rt, q, o, s, out}) && N % 8 == 0;
-  if (o != nullptr) return legacy_bits<kDecode, true>(a, K, B, bits, mfma_ok, (hipStream_t)stream);
-  return legacy_bits<kDecode, false>(a, K, B, bits, mfma_ok, (hipStream_t)stream);
+  if (o != nullptr) return legacy_bits<kDecode, 1>(a, K, B, bits, mfma_ok, (hipStream_t)stream);
+  return legacy_bits<kDecode, 0>(a, K, B, bits, mfma_ok, (hipStream_t)stream);
 }
 
 extern "C" int lrq_legacy_fused(const void* l, const void* rt, int32_t K, const void* q, const void* s,
@@ -322,9 +451,9 @@ extern "C" int lrq_legacy_fused(const void* l, const void* rt, int32_t K, const 
   const bool mfma_ok = vec_ok({l, rt, q, s, y, out}) && N % 8 == 0;
   hipStream_t hs = (hipStream_t)stream;
   switch (op) {
-    case 0: return legacy_bits<kFusedStore, false>(a, K, B, bits, mfma_ok, hs);
-    case 1: return legacy_bits<kFusedSilu, false>(a, K, B, bits, mfma_ok, hs);
-    default: return legacy_bits<kFusedMul, false>(a, K, B, bits, mfma_ok, hs);
+    case 0: return legacy_bits<kFusedStore, 0>(a, K, B, bits, mfma_ok, hs);
+    case 1: return legacy_bits<kFusedSilu, 0>(a, K, B, bits, mfma_ok, hs);
+    default: return legacy_bits<kFusedMul, 0>(a, K, B, bits, mfma_ok, hs);
   }
 }
 
@@ -339,5 +468,58 @@ extern "C" int lrq_lowrank_add(const void* l, const void* rt, int32_t K, const v
   a.l = (const uint16_t*)l, a.rt = (const uint16_t*)rt, a.x = (const uint16_t*)x, a.ldx_b = M * N, a.ldx_m = N;
   a.out = (uint16_t*)out, a.M = M, a.N = N;
   const bool mfma_ok = vec_ok({l, rt, x, out}) && N % 8 == 0;
-  return legacy_launch<kAdd, 8, false>(a, K, B, mfma_ok, (hipStream_t)stream);
+  return legacy_launch<kAdd, 8, 0>(a, K, B, mfma_ok, (hipStream_t)stream);
+}
+
+extern "C" int lrq_legacy_decode_coo(const void* l, const void* rt, int32_t K, const void* q, const int64_t* piece_ptr,
+                                     const int64_t* cols, const void* vals, int64_t n_entries, const void* s,
+                                     int64_t s_rows, int64_t B, int64_t M, int64_t N, int32_t bits, void* out,
+                                     void* stream) {
+  int st = legacy_check(l, rt, K, B, M, N, bits, s, s_rows, true);
+  if (st) return st;
+  if (q == nullptr || out == nullptr || piece_ptr == nullptr) return LRQ_ERR_NULL;
+  if (n_entries < 0) return LRQ_ERR_SHAPE;
+  if (n_entries > 0 && (cols == nullptr || vals == nullptr)) return LRQ_ERR_NULL;
+  if (!aligned(out, 2) || !aligned(piece_ptr, 8) || !aligned(cols, 8) || !aligned(vals, 2)) return LRQ_ERR_ALIGN;
+  if (B == 0 || M == 0) return LRQ_OK;
+  LegacyArgs a{};
+  a.l = (const uint16_t*)l, a.rt = (const uint16_t*)rt, a.s = (const uint16_t*)s, a.s_rows = s_rows;
+  a.qin = (const uint8_t*)q, a.out = (uint16_t*)out, a.M = M, a.N = N;
+  a.optr = piece_ptr, a.ocol = cols, a.oval = (const uint16_t*)vals, a.npc = (N + 63) / 64, a.ncap = n_entries;
+  const bool mfma_ok = vec_ok({l, rt, q, s, out}) && N % 8 == 0;
+  return legacy_bits<kDecode, 2>(a, K, B, bits, mfma_ok, (hipStream_t)stream);
+}
+
+extern "C" int lrq_legacy_kth_residual(const void* l, const void* rt, int32_t K, const void* x, int64_t M, int64_t N,
+                                       int64_t ldx_m, int64_t k, float* out, void* workspace, int64_t workspace_bytes,
+                                       void* stream) {
+  int st = legacy_check(l, rt, K, 1, M, N, 8, nullptr, 1, false);
+  if (st) return st;
+  if (x == nullptr || out == nullptr || workspace == nullptr) return LRQ_ERR_NULL;
+  if (ldx_m < N) return LRQ_ERR_SHAPE;
+  if (M * N >= ((int64_t)1 << 32) || k < 1 || k > M * N) return LRQ_ERR_SHAPE;
+  if (workspace_bytes < 2048) return LRQ_ERR_WORKSPACE;
+  if (!aligned(x, 2) || !aligned(out, 4) || !aligned(workspace, 16)) return LRQ_ERR_ALIGN;
+  hipStream_t hs = (hipStream_t)stream;
+  uint32_t* hist = reinterpret_cast<uint32_t*>(workspace);
+  int64_t* sel = reinterpret_cast<int64_t*>(hist + 256);
+  LegacyArgs a{};
+  a.l = (const uint16_t*)l, a.rt = (const uint16_t*)rt, a.x = (const uint16_t*)x, a.ldx_b = 0, a.ldx_m = ldx_m;
+  a.M = M, a.N = N, a.hist = hist, a.sel = sel;
+  const bool mfma_ok = vec_ok({l, rt, x}) && ldx_m % 8 == 0 && N % 64 == 0 && N / 64 <= 65535;
+  hipLaunchKernelGGL(k_kth_init, dim3(1), dim3(256), 0, hs, hist, sel, k);
+  for (int fine = 0; fine < 2; ++fine) {
+    if (mfma_ok) {
+      constexpr int RB = 4;
+      dim3 grid((unsigned)((M + 64 * RB - 1) / (64 * RB)), (unsigned)(N / 64), 1u);
+      if (K == 16) hipLaunchKernelGGL((k_legacy_mfma<kHist, 8, 16, RB, 0>), grid, dim3(256), 0, hs, a);
+      else hipLaunchKernelGGL((k_legacy_mfma<kHist, 8, 32, RB, 0>), grid, dim3(256), 0, hs, a);
+    } else {
+      const int64_t chunks = (N + 255) / 256;
+      if (M * chunks > INT32_MAX) return LRQ_ERR_SHAPE;
+      hipLaunchKernelGGL(k_hist_scalar, dim3((unsigned)(M * chunks)), dim3(256), 0, hs, a, (int)K, chunks);
+    }
+    hipLaunchKernelGGL(k_kth_select, dim3(1), dim3(256), 0, hs, hist, sel, fine, out);
+  }
+  return launch_status();
 }

@@ -23,7 +23,8 @@ from dataclasses import dataclass, field
 
 import torch
 
-__all__ = ["Config", "CONFIGS", "activation", "basis", "gradient", "softmax_probs", "lora_factor", "make"]
+__all__ = ["Config", "CONFIGS", "activation", "basis", "gradient", "softmax_probs", "lora_factor", "legacy_operands",
+           "make"]
 
 
 @dataclass(frozen=True)
@@ -38,7 +39,7 @@ class Config:
     outlier_scale: float = 1.0
     keep_channels: int = 0      # channels kept dense as fp16 side columns (top-k by abs-max)
     hadamard: bool = False
-    consumer: str = "decode"    # decode | silu | gelu | softmax | lora
+    consumer: str = "decode"    # decode | silu | gelu | softmax | lora | legacy
     lora_rank: int = 16         # consumer "lora": n of the LoRA factor A [hidden, n] and of g [rows, n]
     grad_std: float = 0.02
     seed: int = 0
@@ -56,6 +57,9 @@ CONFIGS = {
                  softmax_shape=(2, 32, 2048, 2048)),
     # the LoRA layer's backward from the north-star format: x A and dA = x^T (dy B^T)
     "lora": Config("lora", 16384, 4096, 16, 4, 64, n_outlier=8, outlier_scale=20.0, consumer="lora", seed=6),
+    # the reference's own format (legacy): rank-16 factors, 2-bit symmetric codes (the system
+    # profile's quantize_bit=2), outliers above the 99th percentile kept as COO
+    "legacy": Config("legacy", 16384, 4096, 16, 2, 0, n_outlier=8, outlier_scale=20.0, consumer="legacy", seed=7),
 }
 
 
@@ -110,6 +114,16 @@ def make(cfg: Config, rows: int | None = None, device="cpu") -> dict:
     elif cfg.consumer != "decode":
         out["dy"] = gradient((rows, cfg.hidden), cfg.grad_std, cfg.seed, device)
     return out
+
+
+def legacy_operands(cfg: Config, device="cpu") -> dict:
+    """Factors l [rows, K], r [K, hidden] (N(0, 0.25)) and per-column scale s [1, hidden]
+    (U(0.05, 0.35)) of the legacy format, bf16, drawn on the CPU."""
+    g = _gen(cfg.seed + 4_000_037, "cpu")
+    l = (torch.randn((cfg.rows, cfg.rank), generator=g) * 0.5).to(torch.bfloat16)
+    r = (torch.randn((cfg.rank, cfg.hidden), generator=g) * 0.5).to(torch.bfloat16)
+    s = (0.05 + 0.3 * torch.rand((1, cfg.hidden), generator=g)).to(torch.bfloat16)
+    return {"l": l.to(device), "r": r.to(device), "s": s.to(device)}
 
 
 def lora_factor(hidden: int, n: int, seed: int = 0, device="cpu") -> torch.Tensor:

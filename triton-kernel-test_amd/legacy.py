@@ -19,12 +19,23 @@ defects (s[0] only, tile-planar packing, unmasked scratch stores) are not reprod
   triton_hadamard                                      extraction_fuse_hadamard.py:62
   torch_extract_unstructured                           extraction_outlier_channel.py:5
   torch_extract_channel                                extraction_outlier_channel.py:11
+
+The outliers these functions return sparse (``o.to_sparse()`` in the reference) are compacted on
+the GPU by ``lrq_coo_compact``; ``compact_outliers`` / ``legacy_encode_coo`` keep them as a
+``LegacyOutliers`` (COO buffers with the entry count on the device, no host synchronisation),
+which the decode reads directly.  ``outlier_threshold`` is the reference's calibration
+``torch.kthvalue(|x[0] - L_x @ R_x|, k)`` (low_rank_system_profile_forward.py:45) on the GPU.
 """
 
 from __future__ import annotations
 
+import ctypes
+from dataclasses import dataclass
+from typing import Optional
+
 import torch
 
+from . import _lib
 from ._lib import call
 from .api import _p, _require_device, _stream
 
@@ -43,6 +54,11 @@ __all__ = [
     "triton_hadamard",
     "torch_extract_unstructured",
     "torch_extract_channel",
+    "LegacyOutliers",
+    "compact_outliers",
+    "legacy_encode_coo",
+    "outlier_threshold",
+    "residual_kthvalue",
 ]
 
 _OP_STORE, _OP_SILU, _OP_MUL = 0, 1, 2
@@ -84,6 +100,103 @@ def _bits(quantize_bit: int) -> int:
     return int(quantize_bit)
 
 
+@dataclass
+class LegacyOutliers:
+    """Legacy-format outliers as COO on the device: ``indices`` int64 [3, cap] (b, m, n; entry e
+    in column e), ``values`` bf16 [cap], ``nnz`` int64 [1] (device; may exceed cap, then the
+    entries past cap were not written), ``piece_ptr`` int64 [B*M*ceil(N/64) + 1] (first entry of
+    each 64-column piece of a row), ``shape`` the dense shape (1 to 3 dims)."""
+    indices: torch.Tensor
+    values: torch.Tensor
+    nnz: torch.Tensor
+    piece_ptr: torch.Tensor
+    shape: tuple
+
+    @property
+    def capacity(self) -> int:
+        return self.values.numel()
+
+    def check(self) -> "LegacyOutliers":
+        """Raise if the compaction dropped entries (nnz > capacity); one host synchronisation."""
+        n = int(self.nnz.item())
+        if n > self.capacity:
+            raise RuntimeError(f"{n} outliers exceed the capacity {self.capacity}; compact again with a larger one")
+        return self
+
+    def to_sparse(self) -> torch.Tensor:
+        """The coalesced sparse COO tensor (one host synchronisation, for the entry count)."""
+        n = int(self.check().nnz.item())
+        nd = len(self.shape)
+        return torch.sparse_coo_tensor(self.indices[3 - nd:, :n], self.values[:n], self.shape, is_coalesced=True,
+                                       check_invariants=True)
+
+
+def _bmn(shape) -> tuple:
+    if len(shape) == 3:
+        return tuple(shape)
+    if len(shape) == 2:
+        return (1, shape[0], shape[1])
+    if len(shape) == 1:
+        return (1, 1, shape[0])
+    raise ValueError("outlier tensors have 1 to 3 dimensions")
+
+
+def compact_outliers(o: torch.Tensor, capacity: Optional[int] = None) -> LegacyOutliers:
+    """Dense bf16 outliers -> LegacyOutliers on the GPU (lrq_coo_compact), no synchronisation.
+    capacity defaults to max(1024, numel / 32)."""
+    _require_device(o)
+    o = o.to(torch.bfloat16).contiguous()
+    B, M, N = _bmn(tuple(o.shape))
+    cap = max(1024, o.numel() // 32) if capacity is None else int(capacity)
+    dev = o.device
+    npc = (N + 63) // 64
+    idx = torch.empty((3, cap), dtype=torch.int64, device=dev)
+    vals = torch.empty((cap,), dtype=torch.bfloat16, device=dev)
+    nnz = torch.empty((1,), dtype=torch.int64, device=dev)
+    ptr = torch.empty((B * M * npc + 1,), dtype=torch.int64, device=dev)
+    wsb = _lib.call_raw("lrq_coo_workspace", B, M, N)
+    _lib.check(min(wsb, 0), "lrq_coo_workspace")
+    ws = torch.empty((max(wsb, 8) + 7) // 8, dtype=torch.int64, device=dev)
+    with torch.cuda.device(dev):
+        call("lrq_coo_compact", _p(o), B, M, N, _p(idx), cap, _p(vals), cap, _p(nnz), _p(ptr), _p(ws),
+             ws.numel() * 8, _stream(dev))
+    return LegacyOutliers(idx, vals, nnz, ptr, tuple(o.shape))
+
+
+def _to_sparse(o: torch.Tensor) -> torch.Tensor:
+    """``o.to_sparse()`` through the GPU compaction (one synchronisation, as to_sparse has).
+    Tensors of more than 3 dimensions are compacted as [prod(leading), M, N] and their leading
+    index unravelled afterwards (row-major order is the same)."""
+    shape = tuple(o.shape)
+    o3 = o.reshape((-1,) + shape[-2:]) if len(shape) > 3 else o
+    c = compact_outliers(o3)
+    n = int(c.nnz.item())
+    if n > c.capacity:
+        c = compact_outliers(o3, capacity=n)
+    sp = c.to_sparse()
+    if len(shape) <= 3:
+        return sp
+    lead, rest = sp.indices()[0], []
+    for d in reversed(shape[:-2]):
+        rest.append(lead % d)
+        lead = torch.div(lead, d, rounding_mode="floor")
+    ind = torch.cat([torch.stack(rest[::-1]), sp.indices()[1:]])
+    return torch.sparse_coo_tensor(ind, sp.values(), shape, is_coalesced=True)
+
+
+def _coo_pieces(o, B: int, M: int, N: int):
+    """(piece_ptr, cols, vals, entries) of the decode for LegacyOutliers or a sparse COO tensor."""
+    if isinstance(o, LegacyOutliers):
+        return o.piece_ptr, o.indices[2], o.values, o.capacity
+    o = o.coalesce()
+    ind = o.indices()
+    b, m, n = ([torch.zeros_like(ind[0])] * (3 - ind.shape[0])) + list(ind)
+    npc = (N + 63) // 64
+    pid = (b * M + m) * npc + torch.div(n, 64, rounding_mode="floor")
+    ptr = torch.searchsorted(pid, torch.arange(B * M * npc + 1, device=pid.device, dtype=torch.int64))
+    return ptr, n.contiguous(), o.values().to(torch.bfloat16).contiguous(), int(n.numel())
+
+
 def low_rank_addition_fuse_compression_quantization(l, r, x, s, quantize_bit=8, outlier=5.):
     """Encode x[B, M, N] - l@r: threshold outliers (returned sparse COO, like the reference) and
     symmetric per-column quantisation with row-planar packing.  Returns (o, q)."""
@@ -106,11 +219,37 @@ def low_rank_addition_fuse_compression_quantization(l, r, x, s, quantize_bit=8, 
         q = torch.empty((B, M, N // (8 // bits)), device=x.device, dtype=torch.uint8)
         call("lrq_legacy_encode", _p(l2), _p(rt), K, _p(x), B, M, N, x.stride(0), x.stride(1), _p(s2),
              s2.shape[0], bits, float(outlier), _p(o), _p(q), _stream(x.device))
-    return o.to_sparse(), q
+        o = _to_sparse(o)
+    return o, q
+
+
+def legacy_encode_coo(l, r, x, s, quantize_bit=8, outlier=5., capacity: Optional[int] = None):
+    """low_rank_addition_fuse_compression_quantization with the outliers kept as LegacyOutliers
+    (compacted on the GPU, entry count left on the device): no host synchronisation.  A decode
+    of it reads at most `capacity` entries; ``LegacyOutliers.check()`` tells whether any were
+    dropped."""
+    bits = _bits(quantize_bit)
+    _require_device(x)
+    M, _ = l.shape
+    _, N = r.shape
+    B = x.shape[0]
+    if tuple(x.shape) != (B, M, N):
+        raise ValueError(f"x must be [B, {M}, {N}]")
+    if x.stride(2) != 1:
+        x = x.contiguous()
+    with torch.cuda.device(x.device):
+        l2, rt, K = _factors(l, r)
+        s2 = _scale(s, B, N)
+        o = torch.empty((B, M, N), device=x.device, dtype=torch.bfloat16)
+        q = torch.empty((B, M, N // (8 // bits)), device=x.device, dtype=torch.uint8)
+        call("lrq_legacy_encode", _p(l2), _p(rt), K, _p(x), B, M, N, x.stride(0), x.stride(1), _p(s2),
+             s2.shape[0], bits, float(outlier), _p(o), _p(q), _stream(x.device))
+        return compact_outliers(o, capacity), q
 
 
 def low_rank_addition_fuse_decompression_dequantization(l, r, q, o, s, quantize_bit=8, outlier=5.):
-    """Decode: bf16(bf16(bf16(c*s) + o) + bf16(l@r)).  ``o`` may be sparse COO, dense or None."""
+    """Decode: bf16(bf16(bf16(c*s) + o) + bf16(l@r)).  ``o`` may be sparse COO, LegacyOutliers,
+    dense or None; COO outliers are read by the decode kernel itself (no dense tensor)."""
     assert l.shape[1] == r.shape[0], "Incompatible dimensions"
     assert l.is_contiguous(), "Matrix A must be contiguous"
     assert r.is_contiguous(), "Matrix B must be contiguous"
@@ -120,16 +259,52 @@ def low_rank_addition_fuse_decompression_dequantization(l, r, q, o, s, quantize_
     _, N = r.shape
     B = q.shape[0]
     q = q.contiguous()
-    if o is not None:
+    coo = isinstance(o, LegacyOutliers) or (o is not None and o.is_sparse)
+    if o is not None and not isinstance(o, LegacyOutliers):
         _require_device(o)
-        o = (o.to_dense() if o.is_sparse else o).to(torch.bfloat16).contiguous()
+        if not coo:
+            o = o.to(torch.bfloat16).contiguous()
     with torch.cuda.device(q.device):
         l2, rt, K = _factors(l, r)
         s2 = _scale(s, B, N)
         x = torch.empty((B, M, N), device=q.device, dtype=torch.bfloat16)
-        call("lrq_legacy_decode", _p(l2), _p(rt), K, _p(q), _p(o), _p(s2), s2.shape[0], B, M, N, bits,
-             _p(x), _stream(q.device))
+        if coo:
+            ptr, cols, vals, n = _coo_pieces(o, B, M, N)
+            call("lrq_legacy_decode_coo", _p(l2), _p(rt), K, _p(q), _p(ptr), _p(cols), _p(vals), n, _p(s2),
+                 s2.shape[0], B, M, N, bits, _p(x), _stream(q.device))
+        else:
+            call("lrq_legacy_decode", _p(l2), _p(rt), K, _p(q), _p(o), _p(s2), s2.shape[0], B, M, N, bits,
+                 _p(x), _stream(q.device))
     return x
+
+
+def residual_kthvalue(l, r, x, k: int) -> torch.Tensor:
+    """torch.kthvalue(|x - l @ r|.flatten().to(torch.float32), k).values for x[M, N] (bf16
+    arithmetic of the reference: the residual rounded to bf16), on the GPU: a 0-dim fp32 device
+    tensor (lrq_legacy_kth_residual)."""
+    _require_device(x)
+    M, _ = l.shape
+    _, N = r.shape
+    if x.dim() != 2 or tuple(x.shape) != (M, N):
+        raise ValueError(f"x must be [{M}, {N}]")
+    x = x.to(torch.bfloat16)
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    out = torch.empty((), dtype=torch.float32, device=x.device)
+    ws = torch.empty((256,), dtype=torch.int64, device=x.device)
+    with torch.cuda.device(x.device):
+        l2, rt, K = _factors(l, r)
+        call("lrq_legacy_kth_residual", _p(l2), _p(rt), K, _p(x), M, N, x.stride(0), int(k), _p(out), _p(ws),
+             ws.numel() * 8, _stream(x.device))
+    return out
+
+
+def outlier_threshold(l, r, x, fraction: float = 0.01) -> torch.Tensor:
+    """The reference's threshold calibration (low_rank_system_profile_forward.py:45):
+    kthvalue of |x[0] - l @ r| at k = int(x[0].numel() * (1 - fraction)), on the GPU (a 0-dim
+    fp32 device tensor; the reference takes ``.item()`` of it)."""
+    x0 = x[0] if x.dim() == 3 else x
+    return residual_kthvalue(l, r, x0, int(x0.numel() * (1 - fraction)))
 
 
 def low_rank_addition(l, r, x):
@@ -253,7 +428,7 @@ def torch_extract_unstructured(x, threshold):
     tau = float(threshold.item() if isinstance(threshold, torch.Tensor) else threshold)
     with torch.cuda.device(x2.device):
         call("lrq_threshold_split", _p(x2), x2.numel(), tau, _p(o), _p(rest), _stream(x2.device))
-    return o.to_sparse(), rest
+    return _to_sparse(o), rest
 
 
 def torch_extract_channel(x, channel_index):
