@@ -295,9 +295,10 @@ __global__ __launch_bounds__(NW * 64) void k_softmax_rows(
 // ------------------------------------------------------------------ dequant-GEMM
 // Grid: ceil(row blocks / RBW); NW waves; wave w takes units w, w + NW, ...; for each unit
 // it decodes the RBW row blocks and multiplies them into its partial out tiles (A's MFMA
-// operand is regenerated per unit with the identity-MFMA transpose of lrq_common.h).  The NW
+// operand is regenerated per unit with the identity-MFMA transpose of lrq_common.h).  A unit's
+// inputs sit in one of SL register slots, loaded while the previous unit is computed.  The NW
 // partial tiles of a row block are then summed through LDS, each wave summing 1/NW of it.
-template <int BITS, int G, int R, int NOUT, int NW, int RBW, bool OUT_F32>
+template <int BITS, int G, int R, int NOUT, int NW, int RBW, int SL, bool OUT_F32>
 __global__ __launch_bounds__(NW * 64) void k_dequant_gemm(
     const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
     const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
@@ -317,45 +318,68 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm(
 #pragma unroll
     for (int t = 0; t < TO; ++t) acc[b][t] = zero4();
 
-  for (int u = w; u < units; u += NW) {
+  // L of the RBW row blocks (the same for every unit)
+  u32x2 lop[RBW][RT];
+#pragma unroll
+  for (int b = 0; b < RBW; ++b) {
+    const int64_t row = min(min(rb0 + b, nrb - 1) * 16 + j, M - 1);
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t) lop[b][t] = ld8(Lin + row * ldl + 16 * t + 4 * g);
+    }
+  }
+  // per unit: V and A operands, codes and qparams of the RBW blocks; the wave's units
+  // w, w + NW, ... go through SL register slots, the next unit's loads in flight while one
+  // is computed (clamped unit index for the slots past the wave's last unit)
+  struct UIn {
     u32x2 vop[NP][G / 16][RT];
     u32x2 va[NP][G / 16][TO];
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      if constexpr (R > 0) load_vops<G, R>(V, unit_base(p, u, N, NP, G), j, g, vop[p]);
-      load_vops<G, NOUT>(A, unit_base(p, u, N, NP, G), j, g, va[p]);
-    }
     u32x4 cb[RBW][G / 64];
     uint32_t qp[RBW][NP];
-    u32x2 lop[RBW][RT];
+  };
+  auto load_unit = [&](int u, UIn& d) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      if constexpr (R > 0) load_vops<G, R>(V, unit_base(p, u, N, NP, G), j, g, d.vop[p]);
+      load_vops<G, NOUT>(A, unit_base(p, u, N, NP, G), j, g, d.va[p]);
+    }
 #pragma unroll
     for (int b = 0; b < RBW; ++b) {
       const int64_t row = min(min(rb0 + b, nrb - 1) * 16 + j, M - 1);
 #pragma unroll
-      for (int i = 0; i < G / 64; ++i) cb[b][i] = ld16_stream(codes + row * ldc + u * G + E * g + 16 * i);
+      for (int i = 0; i < G / 64; ++i) d.cb[b][i] = ld16_stream(codes + row * ldc + u * G + E * g + 16 * i);
       if constexpr (NP == 2) {
         const u32x2 q = ld8(qparams + row * ldq + u * 4);
-        qp[b][0] = q[0];
-        qp[b][1] = q[1];
+        d.qp[b][0] = q[0];
+        d.qp[b][1] = q[1];
       } else {
-        qp[b][0] = ld4(qparams + row * ldq + u * 2);
-      }
-      if constexpr (R > 0) {
-#pragma unroll
-        for (int t = 0; t < RT; ++t) lop[b][t] = ld8(Lin + row * ldl + 16 * t + 4 * g);
+        d.qp[b][0] = ld4(qparams + row * ldq + u * 2);
       }
     }
+  };
+  auto compute_unit = [&](const UIn& d) {
 #pragma unroll
     for (int b = 0; b < RBW; ++b)
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
         float xh[E];
-        reconstruct_plane<BITS, G, R>(cb[b], qp[b][p], p, vop[p], lop[b], xh);
+        reconstruct_plane<BITS, G, R>(d.cb[b], d.qp[b][p], p, d.vop[p], lop[b], xh);
         u32x4 xb[G / 32];
 #pragma unroll
         for (int k = 0; k < G / 32; ++k) xb[k] = pack8(xh + 8 * k);  // x_hat = bf16(reconstruction)
-        project_unit<G, NOUT>(va[p], xb, ident, acc[b]);
+        project_unit<G, NOUT>(d.va[p], xb, ident, acc[b]);
       }
+  };
+  const int nu = w < units ? (units - w + NW - 1) / NW : 0;
+  UIn ring[SL];
+#pragma unroll
+  for (int sl = 0; sl < SL; ++sl) load_unit(min(w + sl * NW, units - 1), ring[sl]);
+  for (int i0 = 0; i0 < nu; i0 += SL) {
+#pragma unroll
+    for (int sl = 0; sl < SL; ++sl) {
+      if (i0 + sl < nu) compute_unit(ring[sl]);  // wave-uniform; no memory operation inside
+      load_unit(min(w + (i0 + sl + SL) * NW, units - 1), ring[sl]);
+    }
   }
 
   // acc[b][t] in lane (j, g), component v: out[row j][16t + 4g + v] (partial over this wave's units)
@@ -397,7 +421,7 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm(
 // operand of the product -- and gm's rows by the same transpose into the A operand g^T.  The
 // product's accumulator holds, in lane (j, g), 4 consecutive k of one column n.  The NW waves'
 // accumulators are summed through LDS in wave order (deterministic) and leave as 16-byte rows.
-template <int BITS, int G, int R, int KT, int NW, int UPW>
+template <int BITS, int G, int R, int KT, int NW, int UPW, int PD>
 __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t(
     const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
     const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
@@ -454,43 +478,55 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t(
     for (int t = 0; t < KT; ++t) d.gop[t] = ld8(gm + row * ldg + 16 * t + 4 * g);
   };
 
-  int rb = rb_lo + w;
-  if (rb < rb_hi) {  // wave-uniform
-    Blk cur;
-    load(rb, cur);
-    for (; rb < rb_hi; rb += NW) {
-      Blk nxt;
-      load(min(rb + NW, rb_hi - 1), nxt);  // clamped: the last block's prefetch re-reads itself
-      // g^T operands: rows past M contribute nothing (their clamped x_hat is finite)
-      const bool live = rb * 16 + j < M;
-      u32x2 a2[KT];
+  // one block's contribution; blocks past the wave's last (the ring's tail) add nothing
+  auto process = [&](const Blk& cur, int rb, bool blive) {
+    // g^T operands: rows past M contribute nothing (their clamped x_hat is finite)
+    const bool live = blive && rb * 16 + j < M;
+    u32x2 a2[KT];
 #pragma unroll
-      for (int t = 0; t < KT; ++t) {
-        const u32x2 gv = live ? cur.gop[t] : u32x2{0u, 0u};
-        const f32x4 d = mfma_16x16x16(gv, ident, zero4());  // lane (j, g): gm[4g + v][16t + j]
-        a2[t] = u32x2{pack_bf16x2_exact(d[0], d[1]), pack_bf16x2_exact(d[2], d[3])};
-      }
+    for (int t = 0; t < KT; ++t) {
+      const u32x2 gv = live ? cur.gop[t] : u32x2{0u, 0u};
+      const f32x4 d = mfma_16x16x16(gv, ident, zero4());  // lane (j, g): gm[4g + v][16t + j]
+      a2[t] = u32x2{pack_bf16x2_exact(d[0], d[1]), pack_bf16x2_exact(d[2], d[3])};
+    }
 #pragma unroll
-      for (int ui = 0; ui < UPW; ++ui)
+    for (int ui = 0; ui < UPW; ++ui)
 #pragma unroll
-        for (int p = 0; p < NP; ++p) {
-          float xh[E];
-          reconstruct_plane<BITS, G, R>(cur.cb[ui], cur.qp[ui][p], p, vop[ui][p], cur.lop, xh);
+      for (int p = 0; p < NP; ++p) {
+        float xh[E];
+        reconstruct_plane<BITS, G, R>(cur.cb[ui], cur.qp[ui][p], p, vop[ui][p], cur.lop, xh);
 #pragma unroll
-          for (int q = 0; q < Q; ++q) {
-            // lane (j, g) holds x_hat[j][E g + 4q + e]; after the identity MFMA, lane (j, g)
-            // holds x_hat[4g + v][E (j >> 2) + 4q + (j & 3)]
-            const u32x2 xa = u32x2{pack_bf16x2(xh[4 * q], xh[4 * q + 1]), pack_bf16x2(xh[4 * q + 2], xh[4 * q + 3])};
-            const f32x4 d = mfma_16x16x16(xa, ident, zero4());
-            const u32x2 xb = u32x2{pack_bf16x2_exact(d[0], d[1]), pack_bf16x2_exact(d[2], d[3])};
+        for (int q = 0; q < Q; ++q) {
+          // lane (j, g) holds x_hat[j][E g + 4q + e]; after the identity MFMA, lane (j, g)
+          // holds x_hat[4g + v][E (j >> 2) + 4q + (j & 3)]
+          const u32x2 xa = u32x2{pack_bf16x2(xh[4 * q], xh[4 * q + 1]), pack_bf16x2(xh[4 * q + 2], xh[4 * q + 3])};
+          const f32x4 d = mfma_16x16x16(xa, ident, zero4());
+          const u32x2 xb = u32x2{pack_bf16x2_exact(d[0], d[1]), pack_bf16x2_exact(d[2], d[3])};
 #pragma unroll
-            for (int t = 0; t < KT; ++t) {
-              f32x4& c = acc[((ui * NP + p) * Q + q) * KT + t];
-              c = mfma_16x16x16(a2[t], xb, c);
-            }
+          for (int t = 0; t < KT; ++t) {
+            f32x4& c = acc[((ui * NP + p) * Q + q) * KT + t];
+            c = mfma_16x16x16(a2[t], xb, c);
           }
         }
-      cur = nxt;
+      }
+  };
+
+  // the wave's blocks rb_lo + w + i NW, i < nb, through a ring of PD register slots: slot s
+  // holds block i0 + s and is refilled with block i0 + s + PD right after it is used (clamped
+  // loads; every load is issued by every lane)
+  const int nb = rb_lo + w < rb_hi ? (rb_hi - rb_lo - w + NW - 1) / NW : 0;
+  if (nb > 0) {  // wave-uniform
+    const int last = rb_hi - 1;
+    Blk ring[PD];
+#pragma unroll
+    for (int sl = 0; sl < PD; ++sl) load(min(rb_lo + w + sl * NW, last), ring[sl]);
+    for (int i0 = 0; i0 < nb; i0 += PD) {
+#pragma unroll
+      for (int sl = 0; sl < PD; ++sl) {
+        const int rb = rb_lo + w + (i0 + sl) * NW;
+        process(ring[sl], rb, i0 + sl < nb);
+        load(min(rb + PD * NW, last), ring[sl]);
+      }
     }
   }
 
@@ -600,10 +636,13 @@ static int softmax_units(const lrq_tensors* t, const void* dp, int64_t lddp, voi
 
 template <int BITS, int G, int R, int NOUT, bool F32>
 static int gemm_launch(const lrq_tensors* t, const void* a, void* out, int64_t ldo, hipStream_t s) {
-  constexpr int NW = 8, RBW = 4;
+  // row blocks per workgroup: 4, or 2 where a unit's register slot is large (two slots in flight)
+  constexpr int UC = G * (8 / BITS);  // columns of one unit
+  constexpr int NW = 8, RBW = (UC >= 256 && NOUT == 32) ? 1 : (UC >= 256 || NOUT == 32 || R == 32) ? 2 : 4;
+  constexpr int SL = (UC >= 256 && NOUT == 32 && R > 0) ? 1 : 2;  // unit slots in flight
   const int M = (int)t->rows, N = (int)t->hidden;
   const int nrb = (M + 15) / 16;
-  hipLaunchKernelGGL((k_dequant_gemm<BITS, G, R, NOUT, NW, RBW, F32>), dim3((nrb + RBW - 1) / RBW), dim3(NW * 64), 0,
+  hipLaunchKernelGGL((k_dequant_gemm<BITS, G, R, NOUT, NW, RBW, SL, F32>), dim3((nrb + RBW - 1) / RBW), dim3(NW * 64), 0,
                      s, (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
                      (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)a, out, ldo);
   return launch_status();
@@ -653,9 +692,10 @@ template <int BITS, int G, int R, int KT, int UPW, bool F32>
 static int gemm_t_run(const lrq_tensors* t, const void* gmat, int64_t ldg, void* out, int64_t ldo, float* ws,
                       const GemmTPlan& pl, hipStream_t s) {
   constexpr int NW = 8;
+  constexpr int PD = G * (8 / BITS) * KT >= 512 ? 2 : 4;  // ring depth within the register budget
   const int M = (int)t->rows, N = (int)t->hidden;
   if (pl.rg > 0)
-    hipLaunchKernelGGL((k_dequant_gemm_t<BITS, G, R, KT, NW, UPW>), dim3(pl.cg, pl.rg), dim3(NW * 64), 0, s,
+    hipLaunchKernelGGL((k_dequant_gemm_t<BITS, G, R, KT, NW, UPW, PD>), dim3(pl.cg, pl.rg), dim3(NW * 64), 0, s,
                        (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
                        (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)gmat, ldg, ws,
                        pl.bpg);
