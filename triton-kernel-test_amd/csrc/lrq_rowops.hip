@@ -413,8 +413,9 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm(
 // ------------------------------------------------------------------ transposed dequant-GEMM
 // part[rg][n][k] = sum over the rows m of row group rg of x_hat[m][n] * gm[m][k] (x_hat =
 // bf16(decode), k < 16 KT).  Grid: (column groups of UPW units) x (row groups of bpg 16-row
-// blocks); wave w of a workgroup takes the group's blocks w, w + NW, ... over all UPW units,
-// the next block's codes, qparams, L and gm rows loaded while the current one is computed.
+// blocks) in one XCD-aware dimension; wave w of a workgroup takes the group's blocks w, w + NW,
+// ... over all UPW units, through a ring of PD register slots (loads of later blocks in flight
+// while one is computed).
 // Every MFMA operand keeps K along a lane's registers, and the reduction here runs over rows,
 // which the reconstruction holds one per lane (lane (j, g): row j, E columns).  So each 16 x 16
 // piece of x_hat is transposed by an identity MFMA (exact) into lane (column, 4 rows) -- the B
@@ -425,7 +426,7 @@ template <int BITS, int G, int R, int KT, int NW, int UPW, int PD>
 __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t(
     const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
     const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
-    const uint16_t* __restrict__ gm, int64_t ldg, float* __restrict__ part, int bpg) {
+    const uint16_t* __restrict__ gm, int64_t ldg, float* __restrict__ part, int bpg, int ncg, bool xcd_map) {
   constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, E = G / 4, Q = G / 16;
   constexpr int NACC = UPW * NP * Q * KT;  // f32x4 accumulators per lane
   constexpr int CH = NACC < 8 ? NACC : 8;  // accumulators per LDS round
@@ -434,8 +435,15 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t(
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
   const int nrb = (M + 15) / 16;
-  const int u0 = blockIdx.x * UPW;
-  const int rb_lo = blockIdx.y * bpg, rb_hi = min(rb_lo + bpg, nrb);
+  // workgroup -> (column group, row group).  Workgroups go to the 8 XCDs round-robin by id, and
+  // every column group of a row group reads the same qparams, L and g lines: with xcd_map the
+  // ids of one XCD (id % 8) take whole row groups, so each line is fetched into one XCD's L2
+  // only (without it, 8 L2s fetch it: 2.2x the algorithmic HBM bytes at the north-star shape)
+  const int id = blockIdx.x;
+  const int cgi = xcd_map ? (id >> 3) % ncg : id % ncg;
+  const int rgi = xcd_map ? (id & 7) + 8 * ((id >> 3) / ncg) : id / ncg;
+  const int u0 = cgi * UPW;
+  const int rb_lo = rgi * bpg, rb_hi = min(rb_lo + bpg, nrb);
   const int KO = 16 * KT;  // gm columns and part row length
   const u32x2 ident = identity_bop(j, g);
 
@@ -532,7 +540,7 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t(
 
   // acc[((ui NP + p) Q + q) KT + t] in lane (j, g), component v: column
   // n = p N/NP + (u0 + ui) G + E (j >> 2) + 4q + (j & 3), k = 16t + 4g + v
-  float* partg = part + (int64_t)blockIdx.y * N * KO;
+  float* partg = part + (int64_t)rgi * N * KO;
 #pragma unroll
   for (int c0 = 0; c0 < NACC; c0 += CH) {
 #pragma unroll
@@ -695,10 +703,10 @@ static int gemm_t_run(const lrq_tensors* t, const void* gmat, int64_t ldg, void*
   constexpr int PD = G * (8 / BITS) * KT >= 512 ? 2 : 4;  // ring depth within the register budget
   const int M = (int)t->rows, N = (int)t->hidden;
   if (pl.rg > 0)
-    hipLaunchKernelGGL((k_dequant_gemm_t<BITS, G, R, KT, NW, UPW, PD>), dim3(pl.cg, pl.rg), dim3(NW * 64), 0, s,
+    hipLaunchKernelGGL((k_dequant_gemm_t<BITS, G, R, KT, NW, UPW, PD>), dim3(pl.cg * pl.rg), dim3(NW * 64), 0, s,
                        (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
                        (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)gmat, ldg, ws,
-                       pl.bpg);
+                       pl.bpg, pl.cg, pl.rg % 8 == 0);
   const int64_t nk = (int64_t)N * 16 * KT;
   hipLaunchKernelGGL(k_sum_parts<F32>, dim3((unsigned)((nk / 4 + 255) / 256)), dim3(256), 0, s, ws, pl.rg, nk,
                      16 * KT, out, ldo);
