@@ -11,18 +11,21 @@ namespace lrq {
 // dy * s * (1 + x * (1 - s)), s = sigmoid(x).
 __device__ __forceinline__ float silu_bwd_f32(float x, float dy) {
   const float s = __builtin_amdgcn_rcpf(1.f + __expf(-x));
-  return dy * (s * (1.f + x * (1.f - s)));
+  return dy * (s * __builtin_fmaf(x, 1.f - s, 1.f));
 }
 
 // gelu_backward.py:14-21 (tanh approximation): 0.5 * ((1 + t) + x * (1 - t^2) * g' ) * dy,
 // t = tanh(gamma * (x + kappa * x^3)), g' = gamma * (1 + 3 * kappa * x^2).
+// With s = sigmoid(2u) (u the tanh argument): 1 + t = 2s and 1 - t^2 = 4s(1 - s), so the
+// derivative is s * (1 + 2x g' (1 - s)): one exp, one reciprocal and 11 other operations.
 __device__ __forceinline__ float gelu_bwd_f32(float x, float dy) {
   constexpr float kGamma = 0.7978845608028654f, kKappa = 0.044715f;
+  constexpr float kLog2e = 1.4426950408889634f;
   const float x2 = x * x;
-  const float u = kGamma * (x + kKappa * x2 * x);
-  // tanh(u) = 1 - 2 / (exp(2u) + 1); saturates correctly at +-1.
-  const float th = 1.f - 2.f * __builtin_amdgcn_rcpf(__expf(2.f * u) + 1.f);
-  return 0.5f * ((1.f + th) + x * ((1.f - th * th) * kGamma * (1.f + 3.f * kKappa * x2))) * dy;
+  const float u2 = x * __builtin_fmaf(2.f * kGamma * kKappa, x2, 2.f * kGamma);  // 2u
+  const float s = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-kLog2e * u2));
+  const float g2 = x * __builtin_fmaf(6.f * kGamma * kKappa, x2, 2.f * kGamma);  // 2x g'
+  return (s * __builtin_fmaf(g2, 1.f - s, 1.f)) * dy;
 }
 
 // fp32 -> nearest bf16 value, as fp32 (the rounding every bf16 torch op applies).
