@@ -656,13 +656,17 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
         float xh[E];
         reconstruct_plane<BITS, G, R>(cb, qp[p], p, vop[p], lop, xh);
         if constexpr (OUTL) {
+          // the lane's outlier columns one by one (usually none or one): a select over the E
+          // values per outlier, instead of a test, a table read and a select per value
           const int c0 = unit_base(p, u, N, NP, G) + E * g;  // E consecutive columns in one mask word
-          const uint32_t mbits = colmask[c0 >> 5] >> (c0 & 31);
-          if (mbits != 0u) {
-            const uint16_t* ss = reinterpret_cast<const uint16_t*>(slot + Tl::SLOT) + j * kSideMax;
+          uint32_t mbits = (colmask[c0 >> 5] >> (c0 & 31)) & (E >= 32 ? ~0u : (1u << E) - 1u);
+          const uint16_t* ss = reinterpret_cast<const uint16_t*>(slot + Tl::SLOT) + j * kSideMax;
+          while (mbits != 0u) {
+            const int e0 = __builtin_ctz(mbits);
+            mbits &= mbits - 1u;
+            const float v = f16_val(ss[oslot[c0 + e0]]);
 #pragma unroll
-            for (int e = 0; e < E; ++e)
-              if ((mbits >> e) & 1u) xh[e] = f16_val(ss[oslot[c0 + e]]);
+            for (int e = 0; e < E; ++e) xh[e] = e == e0 ? v : xh[e];
           }
         }
 #pragma unroll
