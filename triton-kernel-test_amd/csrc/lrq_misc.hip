@@ -28,12 +28,15 @@ __global__ __launch_bounds__(256) void k_transpose_bf16(const uint16_t* __restri
 // non-negative floats).  colmax must be zeroed first (done by the host entry).
 // Grid: (ceil(cols / 512), row groups of rows_per rows); 256 threads = 4 row phases x 64
 // column lanes of 8 adjacent columns (one 16-byte load per row: a wave reads 1 KB of a row),
-// 8 loads in flight per thread.  The 4 phases meet in LDS, so each workgroup issues one
+// 16 loads in flight per thread.  The 4 phases meet in LDS, so each workgroup issues one
 // atomic per column (few row groups keep the atomics per address low).
 __global__ __launch_bounds__(256) void k_colmax(const uint16_t* __restrict__ x, int64_t ldx, int64_t rows,
                                                 int64_t cols, int64_t rows_per, unsigned int* __restrict__ colmax) {
   __shared__ float red[3][64][8];
-  const int cl = threadIdx.x & 63, ph = threadIdx.x >> 6;
+  // the row phase is wave-uniform (readfirstlane), so the batch loop's branches are scalar: a
+  // load under a per-lane branch would make the compiler wait for it at the join, and nothing
+  // would overlap.  Lanes past the last column read the last 8 columns and store nothing.
+  const int cl = threadIdx.x & 63, ph = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t c = ((int64_t)blockIdx.x * 64 + cl) * 8;
   const bool live = c < cols;
   const int64_t r0 = (int64_t)blockIdx.y * rows_per;
@@ -41,31 +44,42 @@ __global__ __launch_bounds__(256) void k_colmax(const uint16_t* __restrict__ x, 
   float m[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) m[e] = 0.f;
-  if (live) {
-    const uint16_t* p = x + c;
+  {
+    const uint16_t* p = x + (live ? c : cols - 8);
     int64_t r = r0 + ph;
-    // batches of 8 rows (r, r+4, ..., r+28), the next batch in flight while one is reduced
-    u32x4 v[8];
+    // batches of kB rows (r, r+4, ..., r+4(kB-1)), the next batch in flight while one is reduced
+    constexpr int kB = 16;
+    u32x4 v[kB];
     auto issue = [&](int64_t rr) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = ld16_stream(p + (rr + 4 * i) * ldx);
+      for (int i = 0; i < kB; ++i) v[i] = ld16_stream(p + (rr + 4 * i) * ldx);
     };
-    bool more = r + 28 < r1;
-    if (more) issue(r);
-    while (more) {
-      u32x4 cur[8];
+    auto reduce = [&](const u32x4 (&b)[kB]) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) cur[i] = v[i];
-      r += 32;
-      more = r + 28 < r1;
-      if (more) issue(r);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < kB; ++i) {
         float f[8];
-        unpack8(cur[i], f);
+        unpack8(b[i], f);
 #pragma unroll
         for (int e = 0; e < 8; ++e) m[e] = fmaxf(m[e], fabsf(f[e]));
       }
+    };
+    // full batches (r + 4(kB-1) < r1); the loop issues the next batch unconditionally, so the
+    // wait for a batch leaves the next one in flight (a conditional issue would make the
+    // compiler wait for both at the join)
+    constexpr int kSpan = 4 * kB;
+    const int nbat = __builtin_amdgcn_readfirstlane(r + kSpan - 4 < r1 ? (int)((r1 - r - kSpan + 3) / kSpan) + 1 : 0);
+    if (nbat > 0) {
+      issue(r);
+      for (int bi = 0; bi + 1 < nbat; ++bi) {
+        u32x4 cur[kB];
+#pragma unroll
+        for (int i = 0; i < kB; ++i) cur[i] = v[i];
+        r += kSpan;
+        issue(r);
+        reduce(cur);
+      }
+      reduce(v);
+      r += kSpan;
     }
     for (; r < r1; r += 4) {
       float f[8];
@@ -243,11 +257,11 @@ extern "C" int lrq_colmax(const void* x, int64_t ldx, int64_t rows, int64_t hidd
   int st = launch_status();
   if (st || rows == 0) return st;
   if ((hidden % 8) == 0 && (ldx % 8) == 0 && aligned(x, 16)) {
-    // about two workgroups per CU, row groups of whole 32-row steps
+    // about two workgroups per CU, row groups of whole 64-row steps (4 phases x 16-row batches)
     const int64_t cgroups = (hidden + 511) / 512;
     int64_t groups = std::max<int64_t>(1, (int64_t)cu_count() * 2 / cgroups);
     int64_t rows_per = (rows + groups - 1) / groups;
-    rows_per = (rows_per + 31) / 32 * 32;
+    rows_per = (rows_per + 63) / 64 * 64;
     groups = (rows + rows_per - 1) / rows_per;
     hipLaunchKernelGGL(k_colmax, dim3((unsigned)cgroups, (unsigned)groups), dim3(256), 0, s, (const uint16_t*)x, ldx,
                        rows, hidden, rows_per, (unsigned int*)colmax);
