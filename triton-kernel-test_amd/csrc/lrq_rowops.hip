@@ -575,7 +575,18 @@ __global__ __launch_bounds__(256) void k_sum_parts(const float* __restrict__ par
   const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (i >= nk) return;
   float s[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int r = 0; r < rg; ++r) {
+  // 8 groups' loads in flight at a time, summed in group order
+  int r = 0;
+  for (; r + 8 <= rg; r += 8) {
+    u32x4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = ld16(part + (int64_t)(r + k) * nk + i);
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[e] += __uint_as_float(v[k][e]);
+  }
+  for (; r < rg; ++r) {
     const u32x4 v = ld16(part + (int64_t)r * nk + i);
 #pragma unroll
     for (int e = 0; e < 4; ++e) s[e] += __uint_as_float(v[e]);
