@@ -194,3 +194,33 @@ def test_empty_inputs_are_no_ops(L):
     p = ctypes.c_void_p(0x10000)
     assert L.call_raw("lrq_dense_elementwise", 0, p, p, p, 0, None) == L.LRQ_OK
     assert L.call_raw("lrq_wht128", p, 1024, 0, 1024, p, 1024, None) == L.LRQ_OK
+
+
+def test_header_compiles_as_c_and_a_c_host_links(tmp_path):
+    """A plain C host: include/lrq.h compiles as C99 with warnings as errors, links against
+    liblrq.so and calls the host-only entry points (no GPU needed)."""
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    lib = ROOT / "triton-kernel-test_amd" / "liblrq.so"
+    src = tmp_path / "host.c"
+    src.write_text(
+        '#include <stdio.h>\n#include "lrq.h"\n'
+        "int main(void) {\n"
+        "  lrq_tensors t = {0};\n"
+        "  t.rows = 32; t.hidden = 4096; t.bits = 4; t.group = 64;\n"
+        "  t.codes = (void*)0x1000; t.ld_codes = 2048; t.qparams = (void*)0x2000; t.ld_qp = 128;\n"
+        "  long long ws = (long long)lrq_dequant_gemm_t_workspace(&t, 16);\n"
+        "  long long cw = (long long)lrq_coo_workspace(1, 16, 512);\n"
+        '  printf("%d %lld %lld %s\\n", lrq_abi_version(), ws, cw, lrq_status_string(LRQ_ERR_SHAPE));\n'
+        "  return lrq_encode(&t, 0, 4096, 0) == LRQ_ERR_NULL ? 0 : 1;\n"
+        "}\n")
+    exe = tmp_path / "host"
+    subprocess.run([cc, "-std=c99", "-Wall", "-Wextra", "-Werror", "-pedantic", f"-I{ROOT / 'include'}", str(src),
+                    str(lib), f"-Wl,-rpath,{lib.parent}", "-o", str(exe)], check=True, capture_output=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    ver, ws, cw, msg = r.stdout.split(maxsplit=3)
+    assert ver == "1" and int(ws) == 4096 * 16 * 4 and int(cw) == 16 and msg.strip()
