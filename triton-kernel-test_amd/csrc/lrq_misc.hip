@@ -173,9 +173,22 @@ __global__ __launch_bounds__(1024) void k_topk(const float* __restrict__ colmax,
     if (tid < 256) hist[tid] = 0u;
     __syncthreads();
     const uint32_t prefix = s_prefix;
-    for (int i = tid; i < hidden; i += 1024) {
-      const uint32_t key = skey[i];
-      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    // the keys crowd into few bins (colmax values span few exponents), so a wave adds each
+    // distinct bin of its 64 keys once (ballot + popcount) instead of 64 colliding LDS atomics
+    for (int it = 0; it < (hidden + 1023) / 1024; ++it) {
+      const int i = it * 1024 + tid;
+      const uint32_t key = i < hidden ? skey[i] : 0u;
+      const uint32_t bin = (key >> shift) & 255u;
+      bool pend = i < hidden && (key & mask) == prefix;
+      uint64_t active = __ballot(pend);
+      while (active != 0u) {
+        const int leader = __ffsll((unsigned long long)active) - 1;
+        const uint32_t b = __shfl(bin, leader);
+        const uint64_t same = __ballot(pend && bin == b);
+        if (lane == leader) atomicAdd(&hist[b], (uint32_t)__popcll(same));
+        pend = pend && bin != b;
+        active &= ~same;
+      }
     }
     __syncthreads();
     if (tid < 64) {
