@@ -182,9 +182,8 @@ __global__ __launch_bounds__(kCooThreads) void k_coo_scatter(const uint16_t* __r
                                                              const uint32_t* __restrict__ chunk_total,
                                                              int64_t* __restrict__ idx, int64_t ld_idx,
                                                              uint16_t* __restrict__ val, int64_t cap) {
-  // per wave: up to 8 pieces x 64 entries, then one dump slot per lane; entry = (row offset,
-  // column, value bits)
-  __shared__ u32x4 stage[kCooThreads / 64][kStage + 64];
+  // per wave: up to 8 pieces x 64 entries; entry = (row offset, column, value bits)
+  __shared__ u32x4 stage[kCooThreads / 64][kStage];
   const int t = threadIdx.x, q = t & 7, lane = t & 63, w = t >> 6;
   const int64_t pc0 = (int64_t)blockIdx.x * kChunk;
   const int64_t coff = (int64_t)chunk_off[blockIdx.x];
@@ -234,15 +233,15 @@ __global__ __launch_bounds__(kCooThreads) void k_coo_scatter(const uint16_t* __r
       uint32_t wcnt = n;
 #pragma unroll
       for (int d = 1; d < 64; d <<= 1) wcnt += __shfl_xor(wcnt, d);
-      // stage the lane's entries in the wave's LDS area at their rank (slot kStage + lane takes
-      // the writes of entries a lane does not have: no branch around the stores)
+      // stage the lane's entries (usually none) in the wave's LDS area at their rank, one set
+      // bit at a time: only LDS stores sit under this per-lane loop, so no memory load waits
       uint32_t rel = lo32 + (incl - n) - wbase;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const bool has = (m >> i) & 1u;
-        const uint32_t slot = has ? rel : kStage + lane;
-        stage[w][slot] = u32x4{dru[u], pcu[u] * kPiece + 8 * q + i, (vu[u][i >> 1] >> (16 * (i & 1))) & 0xffffu, 0u};
-        rel += has ? 1u : 0u;
+      uint32_t mm = m;
+      while (mm != 0u) {
+        const int i = __builtin_ctz(mm);
+        mm &= mm - 1u;
+        const uint32_t word = i < 2 ? vu[u][0] : i < 4 ? vu[u][1] : i < 6 ? vu[u][2] : vu[u][3];
+        stage[w][rel++] = u32x4{dru[u], pcu[u] * kPiece + 8 * q + i, (word >> (16 * (i & 1))) & 0xffffu, 0u};
       }
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes are done
       __builtin_amdgcn_wave_barrier();
