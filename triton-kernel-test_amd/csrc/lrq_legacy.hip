@@ -128,7 +128,7 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
     __syncthreads();
   }
   constexpr uint32_t kMask = BITS == 8 ? 0xffu : (1u << BITS) - 1u;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int j = lane & 15, g = lane >> 4;
   const int u = blockIdx.y, b = blockIdx.z;
   const int M = (int)a.M, N = (int)a.N;
@@ -141,8 +141,9 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
   const float zero[E] = {};
 
   for (int i = 0; i < RB; ++i) {
-    const int row = (blockIdx.x * RB + i) * 64 + w * 16 + j;
-    if (row - j >= M) break;  // whole 16-row block past the end (uniform per wave)
+    const int row0 = (blockIdx.x * RB + i) * 64 + w * 16;  // wave-uniform: a scalar exit
+    if (row0 >= M) break;  // whole 16-row block past the end
+    const int row = row0 + j;
     const int64_t rr = min(row, M - 1);
     const int64_t erow = ((int64_t)b * M + rr) * N;  // element offset of the row in [B, M, N] outputs
     u32x2 lop[RT];
