@@ -92,3 +92,78 @@ def test_fullsize_fused_equals_decode_then_op(pkg, dev):
     unfused = pkg.triton_silu_backward(pkg.decode(c), dy)
     torch.cuda.synchronize()
     assert torch.equal(fused, unfused)
+
+
+
+def test_fullsize_lora_gradients_on_codes(pkg, dev):
+    """lora config (the north-star format at its full size): x_hat^T g from the codes is within
+    the fp32 accumulation bound 1e-5 * |x_hat|^T |g| of the float64 product on lrq_decode's
+    x_hat (the one dequant_gemm_t is defined on); x_hat A within relative L2 1e-5 and max-abs
+    1e-3 of the float64 product (dequant_gemm's x_hat matches lrq_decode's to 1 ulp)."""
+    cfg = pkg.inputs.CONFIGS["lora"]
+    print(f"[full lora] {cfg.rows}x{cfg.hidden} n={cfg.lora_rank}", flush=True)
+    inp = pkg.inputs.make(cfg, device=dev)
+    c = pkg.encode(inp["x"], inp["V"].to(dev), bits=cfg.bits, group_size=cfg.group)
+    xa = pkg.dequant_gemm(c, inp["a"])
+    da = pkg.dequant_gemm_t(c, inp["g"])
+    xd = pkg.decode(c).double()
+    a, g = inp["a"].double(), inp["g"].double()
+    torch.cuda.synchronize()
+    ref_da = xd.T @ g
+    bound = 1e-5 * (xd.abs().T @ g.abs()) + 1e-12
+    worst = float(((da.double() - ref_da).abs() / bound).max())
+    print(f"[full lora] dA worst error / bound {worst:.3f}", flush=True)
+    assert worst <= 1.0
+    ref_xa = xd @ a
+    rel = float((xa.double() - ref_xa).norm() / ref_xa.norm())
+    mx = float((xa.double() - ref_xa).abs().max())
+    print(f"[full lora] xA rel-L2 {rel:.2e} max-abs {mx:.2e}", flush=True)
+    assert rel <= 1e-5 and mx <= 1e-3
+
+
+def _prev_bf16(v: float) -> float:
+    """The largest bf16 value below the positive bf16 value v."""
+    b = torch.tensor(v, dtype=torch.bfloat16).view(torch.int16)
+    return (b - 1).view(torch.bfloat16).item()
+
+
+def test_fullsize_legacy_outliers(pkg, dev):
+    """legacy config (the reference's format at [16384, 4096], 2-bit, threshold at 1 %):
+
+      * the GPU threshold tau is the k-th smallest |residual| of the encode's own residual:
+        at most numel - k entries exceed tau, more than numel - k reach it (the encode's
+        outlier count at tau and at the bf16 value below tau);
+      * tau agrees with torch.kthvalue of torch's own bf16 residual to within one bf16 step;
+      * the GPU COO compaction equals torch's to_sparse of the same dense outliers, entry for
+        entry, and the decode from COO pieces equals the dense decode bit for bit."""
+    cfg = pkg.inputs.CONFIGS["legacy"]
+    print(f"[full legacy] {cfg.rows}x{cfg.hidden} bits={cfg.bits}", flush=True)
+    ops = pkg.inputs.legacy_operands(cfg, dev)
+    l, r, s = ops["l"], ops["r"], ops["s"]
+    x = pkg.inputs.activation(cfg.rows, cfg.hidden, cfg.n_outlier, cfg.outlier_scale, cfg.seed, dev)[None]
+    numel = cfg.rows * cfg.hidden
+    k = int(numel * 0.99)
+    tau = pkg.outlier_threshold(l, r, x).item()
+    assert tau > 0
+    oc, q = pkg.legacy_encode_coo(l, r, x, s, quantize_bit=cfg.bits, outlier=tau)
+    below, _ = pkg.legacy_encode_coo(l, r, x, s, quantize_bit=cfg.bits, outlier=_prev_bf16(tau))
+    n_above, n_reach = int(oc.nnz.item()), int(below.nnz.item())
+    print(f"[full legacy] tau {tau} above {n_above} reach {n_reach} numel-k {numel - k}", flush=True)
+    assert n_above <= numel - k < n_reach
+    oc.check()
+    below.check()
+    resid = (x[0] - l @ r).abs().flatten().float()
+    ref_tau = torch.kthvalue(resid, k).values.item()
+    del resid
+    assert abs(tau - ref_tau) <= 2.0 ** -7 * ref_tau, (tau, ref_tau)
+    o_sp, q2 = pkg.low_rank_addition_fuse_compression_quantization(l, r, x, s, quantize_bit=cfg.bits, outlier=tau)
+    assert torch.equal(q, q2)
+    dense = o_sp.to_dense()
+    ref_sp = dense.to_sparse()
+    assert o_sp._nnz() == ref_sp._nnz() == n_above
+    assert torch.equal(o_sp.indices(), ref_sp.indices())
+    assert torch.equal(o_sp.values().view(torch.int16), ref_sp.values().view(torch.int16))
+    xa = pkg.low_rank_addition_fuse_decompression_dequantization(l, r, q, oc, s, quantize_bit=cfg.bits)
+    xb = pkg.low_rank_addition_fuse_decompression_dequantization(l, r, q, dense, s, quantize_bit=cfg.bits)
+    torch.cuda.synchronize()
+    assert torch.equal(xa, xb)
