@@ -55,7 +55,10 @@ def test_softmax_bwd_unsupported_width(pkg, dev):
 @pytest.mark.parametrize("rows,hidden,rank,n_out,out_dtype", [
     (100, 4096, 16, 32, torch.float32),   # R12 build shape (reduced rows), fp32 out
     (64, 4096, 16, 32, torch.bfloat16),   # bf16 out
-    (50, 2048, 0, 16, torch.float32),     # rank 0, n = 16
+    (50, 2048, 0, 16, torch.float32),     # rank 0, n = 16 (wave-resident kernel, 2 units per wave)
+    (100, 4096, 16, 16, torch.float32),   # lora shape (reduced rows): wave-resident, 4 units per wave
+    (37, 4096, 16, 16, torch.bfloat16),   # ragged last row block, bf16 out
+    (60, 3072, 16, 16, torch.float32),    # 24 units: not a multiple of the waves (unit-walking kernel)
 ])
 def test_dequant_gemm(pkg, dev, rows, hidden, rank, n_out, out_dtype):
     print(f"[gemm] rows={rows} hidden={hidden} rank={rank} n={n_out} {out_dtype}", flush=True)

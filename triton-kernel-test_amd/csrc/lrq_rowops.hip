@@ -410,6 +410,119 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm(
   }
 }
 
+// Dequant-GEMM for n = 16 when the row's units split evenly over the waves (NU per wave):
+// wave w owns units NU*w .. NU*w + NU-1 and keeps their reconstruction operands and the
+// transposed A operands in registers for the whole kernel (loaded and transposed once, not per
+// unit visit as in k_dequant_gemm).  It walks the workgroup's RBW row blocks with the codes,
+// qparams and L of the next SL blocks in flight; the block loop is unrolled, so every slot and
+// accumulator index is static and blocks past the last one issue no loads.  Rows past the end
+// repeat the last row (their sums are not stored).  The 8 partial tiles of a block are summed
+// through LDS in wave order as in k_dequant_gemm.
+template <int BITS, int G, int R, int NW, int NU, int RBW, int SL, bool OUT_F32>
+__global__ __launch_bounds__(NW * 64) void k_dequant_gemm_w(
+    const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
+    const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
+    const uint16_t* __restrict__ A, void* __restrict__ out, int64_t ldo) {
+  constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, E = G / 4;
+  static_assert(R == 0 || R == 16, "rank 0 or 16");
+  __shared__ f32x4 part[NW][64];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int nrb = (M + 15) / 16;
+  const int rb0 = blockIdx.x * RBW;
+  const int ub = w * NU;
+  const u32x2 ident = identity_bop(j, g);
+
+  u32x2 vop[NU][NP][G / 16][RT];
+  u32x4 vt[NU][NP][G / 32][1];
+#pragma unroll
+  for (int uu = 0; uu < NU; ++uu)
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int base = unit_base(p, ub + uu, N, NP, G);
+      if constexpr (R > 0) load_vops<G, R>(V, base, j, g, vop[uu][p]);
+      u32x2 va[G / 16][1];
+      load_vops<G, 16>(A, base, j, g, va);
+      transpose_vops<G, 16>(va, ident, vt[uu][p]);
+    }
+
+  struct BIn {
+    u32x4 cb[NU][G / 64];
+    uint32_t qp[NU][NP];
+    u32x2 lop[RT];
+  };
+  auto load_blk = [&](int rb, BIn& d) {
+    const int64_t row = min(min(rb, nrb - 1) * 16 + j, M - 1);
+#pragma unroll
+    for (int uu = 0; uu < NU; ++uu) {
+#pragma unroll
+      for (int i = 0; i < G / 64; ++i) d.cb[uu][i] = ld16_stream(codes + row * ldc + (ub + uu) * G + E * g + 16 * i);
+      if constexpr (NP == 2) {
+        const u32x2 q = ld8(qparams + row * ldq + (ub + uu) * 4);
+        d.qp[uu][0] = q[0];
+        d.qp[uu][1] = q[1];
+      } else {
+        d.qp[uu][0] = ld4(qparams + row * ldq + (ub + uu) * 2);
+      }
+    }
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t) d.lop[t] = ld8(Lin + row * ldl + 16 * t + 4 * g);
+    }
+  };
+  auto compute_blk = [&](const BIn& d, f32x4& acc) {
+#pragma unroll
+    for (int uu = 0; uu < NU; ++uu)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        float xh[E];
+        reconstruct_plane<BITS, G, R>(d.cb[uu], d.qp[uu][p], p, vop[uu][p], d.lop, xh);
+        u32x4 xb[G / 32];
+#pragma unroll
+        for (int k = 0; k < G / 32; ++k) xb[k] = pack8(xh + 8 * k);  // x_hat = bf16(reconstruction)
+        project_unit_vt<G, 16>(vt[uu][p], xb, &acc);
+      }
+  };
+
+  f32x4 acc[RBW];
+  BIn ring[SL];
+#pragma unroll
+  for (int b = 0; b < RBW; ++b) acc[b] = zero4();
+#pragma unroll
+  for (int sl = 0; sl < SL && sl < RBW; ++sl) load_blk(rb0 + sl, ring[sl]);
+#pragma unroll
+  for (int b = 0; b < RBW; ++b) {
+    compute_blk(ring[b % SL], acc[b]);
+    if (b + SL < RBW) load_blk(rb0 + b + SL, ring[b % SL]);
+  }
+
+  // acc[b] in lane (j, g), component v: out[row j][4g + v] (partial over this wave's units)
+  constexpr int F = 256 / NW, S = 64 / F, PPL = NW / S;
+  static_assert(F >= 1 && F <= 64 && 64 % F == 0 && NW % S == 0, "out reduction split");
+  const float* partf = reinterpret_cast<const float*>(&part[0][0]);
+#pragma unroll
+  for (int b = 0; b < RBW; ++b) {
+    if (rb0 + b >= nrb) break;  // uniform
+    part[w][lane] = acc[b];
+    __syncthreads();
+    const int f = lane % F, pg = lane / F;
+    const int fi = w * F + f;
+    const int src = (fi >> 2) & 63, v = fi & 3;
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) s += partf[((pg * PPL + i) * 64 + src) * 4 + v];
+#pragma unroll
+    for (int m = F; m < 64; m <<= 1) s += __shfl_xor(s, m);
+    const int row = (rb0 + b) * 16 + (src & 15);
+    const int col = 4 * (src >> 4) + v;
+    if (pg == 0 && row < M) {
+      if constexpr (OUT_F32) reinterpret_cast<float*>(out)[(int64_t)row * ldo + col] = s;
+      else reinterpret_cast<uint16_t*>(out)[(int64_t)row * ldo + col] = (uint16_t)pack_bf16x2(s, 0.f);
+    }
+    __syncthreads();
+  }
+}
+
 // ------------------------------------------------------------------ transposed dequant-GEMM
 // part[rg][n][k] = sum over the rows m of row group rg of x_hat[m][n] * gm[m][k] (x_hat =
 // bf16(decode), k < 16 KT).  Grid: (column groups of UPW units) x (row groups of bpg 16-row
@@ -661,6 +774,21 @@ static int gemm_launch(const lrq_tensors* t, const void* a, void* out, int64_t l
   constexpr int SL = (UC >= 256 && NOUT == 32 && R > 0) ? 1 : 2;  // unit slots in flight
   const int M = (int)t->rows, N = (int)t->hidden;
   const int nrb = (M + 15) / 16;
+  if constexpr (NOUT == 16 && R <= 16) {
+    // units split evenly over the waves: the wave-resident kernel (NU units per wave)
+    const int units = N / (UC);
+    auto wlaunch = [&](auto nu) {
+      constexpr int NU = decltype(nu)::value, WRBW = 4, WSL = 2;
+      hipLaunchKernelGGL((k_dequant_gemm_w<BITS, G, R, NW, NU, WRBW, WSL, F32>), dim3((nrb + WRBW - 1) / WRBW),
+                         dim3(NW * 64), 0, s, (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams,
+                         t->ld_qp, (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)a,
+                         out, ldo);
+      return launch_status();
+    };
+    if (units == NW * 4) return wlaunch(std::integral_constant<int, 4>{});
+    if (units == NW * 2) return wlaunch(std::integral_constant<int, 2>{});
+    if (units == NW) return wlaunch(std::integral_constant<int, 1>{});
+  }
   hipLaunchKernelGGL((k_dequant_gemm<BITS, G, R, NOUT, NW, RBW, SL, F32>), dim3((nrb + RBW - 1) / RBW), dim3(NW * 64), 0,
                      s, (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
                      (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)a, out, ldo);
