@@ -12,10 +12,17 @@ serve them.  Prints ONE JSON line (driver contract).
 value       = activation GB/s = 2*rows*hidden bytes / (encode + decode time per step);
               fused-consumer configs: / (consumer time); lora: / (x A + x^T g time);
               legacy: / (encode + outlier compaction + decode time)
+timing      = exactly --warmup untimed steps, then exactly --steps timed steps between two HIP
+              events on the launch stream (synchronised before and after); `settled` repeats
+              the timed steps after --settle-seconds of sustained work, as a separate field
 roofline    = dominant kernel's algorithmic HBM bytes per launch / its mean duration
-              (K back-to-back launches between HIP events on the launch stream), against
-              8 TB/s; traffic = rocprofv3 FETCH_SIZE/WRITE_SIZE bytes per launch from profiles/
-cpu_baseline= the CPU oracle (numpy, 1 thread) on a bounded row sample of the same workload
+              (K back-to-back launches between HIP events on the launch stream, the queue
+              pre-filled so host launch cost is not timed), against 8 TB/s; traffic =
+              rocprofv3 FETCH_SIZE/WRITE_SIZE bytes per launch from profiles/
+mfma        = MFMA utilisation of the projection / GEMM kernels from rocprofv3 counters
+              (SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE) in profiles/, where measured
+cpu_baseline= PyTorch-eager fp32 restatement (oracle/lrq_torch.py) on all host cores,
+              1 warm-up + median of 3, on a bounded row sample of the same workload
 """
 
 from __future__ import annotations
@@ -43,13 +50,13 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=20)
-    # untimed warm-up continues until this much wall time has passed (the GPU's clocks settle
-    # over about a second of sustained work; a short warm-up measures the ramp, not the rate)
-    ap.add_argument("--warmup-seconds", type=float, default=2.0)
+    # after the headline measurement: this much sustained work, then the K steps again,
+    # reported as `settled` (the GPU's clocks settle over about a second of sustained work)
+    ap.add_argument("--settle-seconds", type=float, default=2.0)
     ap.add_argument("--config", default="north_star")
     ap.add_argument("--nbuf", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=3.0, help="target seconds per CPU baseline run")
     return ap.parse_args()
 
 
@@ -71,79 +78,94 @@ def traffic_from_profiles(name: str):
         return None
 
 
+def mfma_from_profiles(config: str):
+    """MFMA utilisation per kernel from the committed rocprofv3 counter summary, if present."""
+    p = ROOT / "profiles" / f"mfma_{config}.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text())
+    except Exception:
+        return None
+
+
 def cpu_baseline(cfg, seconds: float):
-    """Time the numpy CPU oracle on a row sample of the same workload, sized to ~`seconds`:
-    encode + decode for the round-trip configs, decode + consumer for the fused ones (the
-    encode is the producer there and is not timed).  One thread."""
-    import numpy as np
+    """Time the PyTorch-eager fp32 restatement (oracle/lrq_torch.py) on the host's cores, on
+    a row sample of the same workload sized to about `seconds` per run: encode + decode for
+    the round-trip configs, decode + consumer for the fused ones (the encode is their
+    producer and is not timed), decode + x A + x^T g for lora, the reference's torch
+    encode + to_sparse + decode for legacy.  1 warm-up run, then the median of 3."""
+    import platform
+
     import torch
-    try:
-        from threadpoolctl import threadpool_limits
-    except Exception:  # pragma: no cover
-        threadpool_limits = None
-    import oracle as O
+    from oracle import lrq_torch as T
     pkg = importlib.import_module("triton-kernel-test_amd")
-    ctx = threadpool_limits(1) if threadpool_limits else None
-    as_bits = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    cpu = platform.processor() or "unknown"
     try:
-        V = pkg.inputs.basis(cfg.hidden, cfg.rank, cfg.seed) if cfg.rank else None
-        vb = as_bits(V) if V is not None else None
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    V = pkg.inputs.basis(cfg.hidden, cfg.rank, cfg.seed) if cfg.rank else None
 
-        def run_legacy(r):
+    def prepare(r):
+        if cfg.consumer == "legacy":
             ops = pkg.inputs.legacy_operands(cfg)
-            lb, rb, sb = as_bits(ops["l"][:r]), as_bits(ops["r"]), as_bits(ops["s"])
-            xb = as_bits(pkg.inputs.activation(r, cfg.hidden, cfg.n_outlier, cfg.outlier_scale, cfg.seed))[None]
-            tau = O.kth_smallest_abs(O.legacy_residual(lb, rb, xb[0]), int(xb[0].size * 0.99))
-            t0 = time.perf_counter()
-            o, q = O.legacy_encode(lb, rb, xb, sb, cfg.bits, tau)
-            idx, vals = O.to_coo(o)
-            dense = np.zeros_like(o)
-            dense[tuple(idx)] = vals
-            O.legacy_decode(lb, rb, q, dense, sb, cfg.bits)
-            return time.perf_counter() - t0
+            x = pkg.inputs.activation(r, cfg.hidden, cfg.n_outlier, cfg.outlier_scale, cfg.seed)[None]
+            l = ops["l"][:r]
+            tau = float(torch.kthvalue((x[0] - l @ ops["r"]).flatten().abs().float(), int(x[0].numel() * 0.99)).values)
+            return dict(x=x, l=l, r=ops["r"], s=ops["s"], tau=tau)
+        inp = pkg.inputs.make(cfg, rows=r)
+        if cfg.keep_channels:
+            inp["idx"] = torch.sort(torch.topk(inp["x"].float().abs().amax(0), cfg.keep_channels).indices).values
+        if cfg.consumer != "decode":
+            inp["enc"] = T.encode(inp["x"], V, cfg.bits, cfg.group, cfg.hadamard, inp.get("idx"))
+        return inp
 
-        def run(r):
-            if cfg.consumer == "legacy":
-                return run_legacy(r)
-            inp = pkg.inputs.make(cfg, rows=r)
-            xb = as_bits(inp["x"])
-            idx = None
-            if cfg.keep_channels:
-                idx = O.topk_channels(O.colmax_abs(xb), cfg.keep_channels)
-            t0 = time.perf_counter()
-            e = O.encode(xb, vb, cfg.bits, cfg.group, hadamard=cfg.hadamard, outlier_idx=idx)
-            if cfg.consumer != "decode":
-                t0 = time.perf_counter()
-            xh = O.decode(e["L"], vb, e["codes"], e["scale"], e["zero"], cfg.bits, cfg.group,
-                          hadamard=cfg.hadamard, side=e["side"], idx=e["idx"])
+    def run(inp):
+        t0 = time.perf_counter()
+        if cfg.consumer == "legacy":
+            o, q = T.legacy_encode(inp["l"], inp["r"], inp["x"], inp["s"], cfg.bits, inp["tau"])
+            o = T.to_coo(o)
+            T.legacy_decode(inp["l"], inp["r"], q, o.to_dense(), inp["s"], cfg.bits)
+        elif cfg.consumer == "decode":
+            e = T.encode(inp["x"], V, cfg.bits, cfg.group, cfg.hadamard, inp.get("idx"))
+            T.decode(e, V, cfg.bits, cfg.group, cfg.hadamard)
+        else:
+            xh = T.decode(inp["enc"], V, cfg.bits, cfg.group, cfg.hadamard)
             if cfg.consumer == "lora":
-                xf = O.bf16_to_f32(xh)
-                O.round_out(O.gemm(xf, O.bf16_to_f32(as_bits(inp["a"]))))
-                O.gemm_t(xf, O.bf16_to_f32(as_bits(inp["g"]))).astype(np.float32)
-            elif cfg.consumer != "decode":
-                f = {"silu": O.silu_bwd, "gelu": O.gelu_bwd, "softmax": O.softmax_bwd}[cfg.consumer]
-                O.round_out(f(O.bf16_to_f32(xh), O.bf16_to_f32(as_bits(inp["dy"]))))
-            return time.perf_counter() - t0
+                xf = xh.float()
+                (xf @ inp["a"].float()).bfloat16()
+                xf.T @ inp["g"].float()
+            else:
+                {"silu": T.silu_bwd, "gelu": T.gelu_bwd, "softmax": T.softmax_bwd}[cfg.consumer](xh, inp["dy"])
+        return time.perf_counter() - t0
 
-        rows = 32
-        t = run(rows)
-        while t < seconds / 8 and rows < cfg.rows:
-            rows = min(cfg.rows, rows * 2)
-            t = run(rows)
-        for _ in range(2):  # two refinements: the first runs carry one-time setup costs
-            if t < 0.8 * seconds and rows < cfg.rows:
-                rows = min(cfg.rows, max(rows, int(rows * seconds / max(t, 1e-3))))
-                t = run(rows)
-        gbs = 2 * rows * cfg.hidden / t / 1e9
-        what = {"decode": "encode+decode", "lora": "decode + x A + x^T g (LoRA factor gradients)",
-                "legacy": "legacy encode + outliers to COO + decode"}.get(
-            cfg.consumer, f"decode+{cfg.consumer} backward")
-        return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-                "sample": f"numpy CPU oracle {what} of {rows} of {cfg.rows} rows x {cfg.hidden} "
-                          f"(same recipe), {t:.1f} s, 1 thread"}
-    finally:
-        if ctx is not None:
-            ctx.__exit__(None, None, None)
+    rows = min(cfg.rows, 256)
+    inp = prepare(rows)
+    t = run(inp)
+    while t < seconds / 4 and rows < cfg.rows:
+        rows = min(cfg.rows, rows * 4)
+        inp = prepare(rows)
+        t = run(inp)
+    if t < 0.7 * seconds and rows < cfg.rows:
+        rows = min(cfg.rows, max(rows, int(rows * seconds / max(t, 1e-3))))
+        inp = prepare(rows)
+        run(inp)  # warm-up at the final size
+    times = [run(inp) for _ in range(3)]
+    t = statistics.median(times)
+    gbs = 2 * rows * cfg.hidden / t / 1e9
+    what = {"decode": "encode+decode", "lora": "decode + x A + x^T g (LoRA factor gradients)",
+            "legacy": "reference torch encode + to_sparse + decode"}.get(cfg.consumer, f"decode+{cfg.consumer} backward")
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"PyTorch-eager fp32 {what} (oracle/lrq_torch.py) of {rows} of {cfg.rows} rows x {cfg.hidden} "
+                      f"(same recipe), median of 3 runs {', '.join(f'{x:.2f}' for x in times)} s after 1 warm-up, "
+                      f"{cores} threads",
+            "cpu": cpu, "torch": torch.__version__}
 
 
 def consumer_bytes(rows, hidden, rank, bits, group, n_side=0):
@@ -343,32 +365,60 @@ def main():
         if st:
             raise RuntimeError(f"launch failed: {lib_mod.status_string(st)}")
 
+    # ---- exactly W untimed warm-up steps
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    warm = args.warmup
-    t_warm = time.perf_counter()
-    while time.perf_counter() - t_warm < args.warmup_seconds:
-        for _ in range(50):
-            step(warm)
-            warm += 1
-        torch.cuda.synchronize()
 
-    # ---- timed region: exactly K steps, nothing else on the stream
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
+    def timed_steps():
+        """Exactly K steps between two events on the launch stream, synchronised before and
+        after; returns (ms per step, host ms spent enqueueing them)."""
+        t_start = torch.cuda.Event(enable_timing=True)
+        t_end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        h0 = time.perf_counter()
+        t_start.record(stream)
+        for i in range(args.steps):
+            step(i)
+        t_end.record(stream)
+        h1 = time.perf_counter()
+        torch.cuda.synchronize()
+        return t_start.elapsed_time(t_end) / args.steps, (h1 - h0) * 1e3
+
+    # ---- timed region (the headline): exactly K steps, nothing else on the stream
+    ms_step, host_ms = timed_steps()
+
+    # ---- the same K steps again after a stretch of sustained work (clock-settled figure)
+    settled = None
+    if args.settle_seconds > 0:
+        n_settle, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.settle_seconds:
+            for _ in range(50):
+                step(n_settle)
+                n_settle += 1
+            torch.cuda.synchronize()
+        ms_settled, _ = timed_steps()
+        settled = {"ms_per_step": round(ms_settled, 5), "after_steps": n_settle,
+                   "after_seconds": args.settle_seconds}
+
+    # The per-kernel measurements below pre-fill the stream with a spin kernel so that the host
+    # can enqueue every launch before the first one starts: what is timed is the GPU, not the
+    # host's launch cost (ctypes + several launches per entry can take longer than a kernel).
+    probe_a, probe_b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    probe_a.record(stream)
+    torch.cuda._sleep(1 << 20)
+    probe_b.record(stream)
     torch.cuda.synchronize()
-    t_start.record(stream)
-    for i in range(args.steps):
-        step(i)
-    t_end.record(stream)
-    torch.cuda.synchronize()
-    total_ms = t_start.elapsed_time(t_end)
-    ms_step = total_ms / args.steps
+    cycles_per_us = (1 << 20) / max(probe_a.elapsed_time(probe_b) * 1e3, 1.0)
+
+    def prefill(host_us):
+        torch.cuda._sleep(int(max(host_us * 1.5 + 200.0, 200.0) * cycles_per_us))
 
     # ---- in-step breakdown (a separate pass): HIP events between the kernels of each step
     ne = len(entries)
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(ne + 1)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    prefill(host_ms * 1e3 * 1.5)
     for i in range(args.steps):
         step(i, evs[i])
     torch.cuda.synchronize()
@@ -379,6 +429,12 @@ def main():
     for e, (name, fn, _, _) in enumerate(entries):
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
+        h0 = time.perf_counter()
+        for i in range(2):
+            fn(i % args.nbuf)
+        torch.cuda.synchronize()
+        per_call_us = (time.perf_counter() - h0) * 1e6 / 2
+        prefill(per_call_us * args.steps)
         a.record(stream)
         for i in range(args.steps):
             fn(i % args.nbuf)
@@ -397,7 +453,7 @@ def main():
                          "hbm_frac": round(alg / (mean * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         if flops:
             tf = flops / (mean * 1e-3) / 1e12
-            kernels[name].update(mfma_tflops=round(tf, 2), mfma_util=round(tf / BF16_DENSE_TFLOPS, 5))
+            kernels[name].update(mfma_tflops=round(tf, 2), mfma_util_derived=round(tf / BF16_DENSE_TFLOPS, 5))
     if timed is None:
         value = act_bytes / (ms_step * 1e-3) / 1e9  # whole step, kernels interleaved as in use
         workload = "encode+decode" + (" with WHT-128 rotation" if cfg.hadamard else "")
@@ -420,7 +476,7 @@ def main():
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": warm,
+        "warmup": args.warmup,
         "ms_per_step": round(ms_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -430,11 +486,22 @@ def main():
         "config": {"workload": f"{args.config}: {workload}", "rows": cfg.rows, "hidden": cfg.hidden,
                    "rank": cfg.rank, "bits": cfg.bits, "group": cfg.group, "buffers": args.nbuf},
         "hbm_frac_step": round(step_alg / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "host_enqueue_ms": round(host_ms, 3),
         "kernels": kernels,
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": (traffic or {}).get("bytes_per_launch")},
     }
+    if settled is not None:
+        ms_s = settled["ms_per_step"]
+        settled["value"] = round(act_bytes / (ms_s * 1e-3) / 1e9, 2) if timed is None else None
+        settled["hbm_frac_step"] = round(step_alg / (ms_s * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        line["settled"] = settled
+    mf = mfma_from_profiles(args.config)
+    if mf is not None:
+        line["mfma"] = {k: {"util": v.get("mfma_util"), "busy_cycles_per_launch": v.get("busy_cycles_per_launch")}
+                        for k, v in mf.get("kernels", {}).items()}
+        line["mfma"]["source"] = f"profiles/mfma_{args.config}.json (rocprofv3 counters)"
     if cfg.consumer == "legacy":
         line["legacy"] = {"outliers": _sets[0]["nnz_count"], "threshold": _sets[0]["tau"],
                           "torch_to_sparse_us": round(_sets[0]["torch_to_sparse_us"], 1)}

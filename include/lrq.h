@@ -92,10 +92,6 @@ typedef struct lrq_tensors {
  * over X when hidden has a single-pass kernel, otherwise two passes. */
 int lrq_encode(const lrq_tensors* t, const void* x, int64_t ldx, void* stream);
 
-/* Same result as lrq_encode, always through the two-pass kernels (projection pass, then
- * residual/quantisation pass).  Diagnostic and test hook; no reference counterpart. */
-int lrq_encode_twopass(const lrq_tensors* t, const void* x, int64_t ldx, void* stream);
-
 /* Decode `t` into out[rows, hidden] bf16.
  * Replaces low_rank_addition_fuse_decompression_dequantization
  * (low_rank_extraction_fuse_decompression_dequantization.py:116-152, kernel :13-113). */

@@ -31,24 +31,36 @@ def test_algorithmic_bytes():
     assert bench.consumer_bytes(M, N, r, 4, 64) == M * N * (0.5 + 4 / 64 + 4) + 2 * M * r + 2 * N * r
 
 
-def test_cpu_baseline_fields():
+@pytest.mark.parametrize("config", ["north_star", "c3", "lora", "legacy"])
+def test_cpu_baseline_fields(config):
+    """The CPU baseline is the torch-eager restatement on every core the process may use, with
+    the host recorded (a tiny time budget here)."""
     import importlib
+    import os
+
+    import torch
     pkg = importlib.import_module("triton-kernel-test_amd")
-    cb = bench.cpu_baseline(pkg.inputs.CONFIGS["north_star"], 0.2)
-    assert cb["kind"] == "port" and cb["cores"] == 1 and cb["unit"] == "GB/s" and cb["value"] > 0
-    assert "rows" in cb["sample"]
+    threads = torch.get_num_threads()
+    try:
+        cb = bench.cpu_baseline(pkg.inputs.CONFIGS[config], 0.05)
+    finally:
+        torch.set_num_threads(threads)
+    assert cb["kind"] == "port" and cb["unit"] == "GB/s" and cb["value"] > 0
+    assert cb["cores"] == len(os.sched_getaffinity(0))
+    assert "rows" in cb["sample"] and "median of 3" in cb["sample"]
+    assert cb["cpu"] and cb["torch"] == torch.__version__
 
 
 @pytest.mark.gpu
 def test_bench_line_on_gpu():
     r = subprocess.run([sys.executable, "-u", str(ROOT / "bench.py"), "--steps", "5", "--warmup", "1",
-                        "--warmup-seconds", "0", "--no-cpu-baseline"], capture_output=True, text=True, timeout=300)
+                        "--settle-seconds", "0", "--no-cpu-baseline"], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stderr[-2000:]
     line = json.loads([x for x in r.stdout.splitlines() if x.startswith("{")][-1])
     for k in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better", "scaling",
               "vs_baseline", "dtype", "data", "config", "roofline"):
         assert k in line, k
-    assert line["n_gpus"] == 1 and line["steps"] == 5 and line["value"] > 0
+    assert line["n_gpus"] == 1 and line["steps"] == 5 and line["warmup"] == 1 and line["value"] > 0
     rf = line["roofline"]
     assert rf["bound"] == "hbm" and rf["unit"] == "GB/s" and 0 < rf["frac"] < 1.2
     assert "workload" in line["config"]

@@ -141,6 +141,26 @@ def test_fused_elementwise(pkg, dev, op):
     print(f"[fused {op}] {rep}", flush=True)
 
 
+def test_fused_silu_c2_format(pkg, dev):
+    """Config 2's format (rank 32, hidden 11008, int4/g64, 172 groups per row) on a row sample:
+    the fused SiLU backward against the oracle's decompress-then-op on the device's codes."""
+    cfg = pkg.inputs.CONFIGS["c2"]
+    rows = 80
+    inp = pkg.inputs.make(cfg, rows=rows)
+    print(f"[c2 silu] rows={rows} hidden={cfg.hidden} rank={cfg.rank}", flush=True)
+    c = pkg.encode(inp["x"].to(dev), inp["V"].to(dev), bits=cfg.bits, group_size=cfg.group)
+    out = pkg.silu_backward_compressed(c, inp["dy"].to(dev))
+    torch.cuda.synchronize()
+    vb = bits16(inp["V"])
+    ref_enc = O.encode(bits16(inp["x"]), vb, cfg.bits, cfg.group, l_override=bits16(c.L))
+    assert_codes(c.codes.cpu().numpy(), ref_enc, cfg.bits, what="c2 codes")
+    xh = O.bf16_to_f32(O.decode(bits16(c.L), vb, c.codes.cpu().numpy(), f16(c.scale), f16(c.zero), cfg.bits,
+                                cfg.group))
+    ref = O.silu_bwd(xh, O.bf16_to_f32(bits16(inp["dy"])))
+    rep = assert_fp_close(bits16(out), ref, "c2 fused silu")
+    print(f"[c2 silu] {rep}", flush=True)
+
+
 @pytest.mark.parametrize("rows,bits,group", [
     (96, 4, 128),    # 128-column groups: dY staged in place, 4 waves
     (96, 8, 128),    # int8 / g128: in place, 8 waves

@@ -52,24 +52,30 @@ def test_softmax_bwd_unsupported_width(pkg, dev):
         pkg.softmax_backward_compressed(c, x.to(dev))
 
 
-@pytest.mark.parametrize("rows,hidden,rank,n_out,out_dtype", [
-    (100, 4096, 16, 32, torch.float32),   # R12 build shape (reduced rows), fp32 out
-    (64, 4096, 16, 32, torch.bfloat16),   # bf16 out
-    (50, 2048, 0, 16, torch.float32),     # rank 0, n = 16 (wave-resident kernel, 2 units per wave)
-    (100, 4096, 16, 16, torch.float32),   # lora shape (reduced rows): wave-resident, 4 units per wave
-    (37, 4096, 16, 16, torch.bfloat16),   # ragged last row block, bf16 out
-    (60, 3072, 16, 16, torch.float32),    # 24 units: not a multiple of the waves (unit-walking kernel)
+@pytest.mark.parametrize("rows,hidden,rank,n_out,out_dtype,bits,group", [
+    (100, 4096, 16, 32, torch.float32, 4, 64),   # R12 build shape (reduced rows), fp32 out
+    (64, 4096, 16, 32, torch.bfloat16, 4, 64),   # bf16 out
+    (50, 2048, 0, 16, torch.float32, 4, 64),     # rank 0, n = 16 (wave-resident kernel, 2 units per wave)
+    (100, 4096, 16, 16, torch.float32, 4, 64),   # lora shape (reduced rows): wave-resident, 4 units per wave
+    (37, 4096, 16, 16, torch.bfloat16, 4, 64),   # ragged last row block, bf16 out
+    (60, 3072, 16, 16, torch.float32, 4, 64),    # 24 units: not a multiple of the waves (unit-walking kernel)
+    (64, 1024, 16, 16, torch.float32, 4, 64),    # 8 units: wave-resident, 1 unit per wave
+    (100, 2048, 16, 16, torch.float32, 8, 128),  # int8 / g128, 16 units: 2 per wave (one plane per unit)
+    (100, 2048, 0, 16, torch.bfloat16, 8, 64),   # int8 / g64, 32 units: 4 per wave, rank 0
+    (100, 2048, 16, 16, torch.float32, 4, 128),  # int4 / g128, 8 units: 1 per wave, two code loads per lane
+    (80, 2048, 16, 32, torch.float32, 8, 64),    # int8, n = 32: the unit-walking kernel
+    (70, 2048, 16, 32, torch.bfloat16, 4, 128),  # int4 / g128, n = 32: the unit-walking kernel
 ])
-def test_dequant_gemm(pkg, dev, rows, hidden, rank, n_out, out_dtype):
-    print(f"[gemm] rows={rows} hidden={hidden} rank={rank} n={n_out} {out_dtype}", flush=True)
+def test_dequant_gemm(pkg, dev, rows, hidden, rank, n_out, out_dtype, bits, group):
+    print(f"[gemm] rows={rows} hidden={hidden} rank={rank} n={n_out} {out_dtype} int{bits}/g{group}", flush=True)
     x = pkg.inputs.activation(rows, hidden, 8, 20.0, seed=21)
     V = pkg.inputs.basis(hidden, rank, seed=21) if rank else None
     g = torch.Generator().manual_seed(22)
     a = (torch.randn(hidden, n_out, generator=g) / np.sqrt(hidden)).to(torch.bfloat16)
-    c = pkg.encode(x.to(dev), V.to(dev) if V is not None else None, bits=4, group_size=64)
+    c = pkg.encode(x.to(dev), V.to(dev) if V is not None else None, bits=bits, group_size=group)
     out = pkg.dequant_gemm(c, a.to(dev), out_dtype=out_dtype)
     torch.cuda.synchronize()
-    xh = _xhat(c, V, 4, 64)
+    xh = _xhat(c, V, bits, group)
     ref = O.gemm(xh, O.bf16_to_f32(bits16(a)))
     if out_dtype == torch.float32:
         got = out.cpu().numpy().astype(np.float64)

@@ -404,3 +404,68 @@ def test_to_coo_matches_torch_to_sparse(shape):
     assert sp.is_coalesced()
     assert np.array_equal(idx, sp.indices().numpy())
     assert np.array_equal(vals, sp.values().contiguous().view(torch.int16).numpy().view(np.uint16))
+
+
+# ------------------------------------------------------------------ the torch-eager CPU baseline
+@pytest.mark.parametrize("rows,hidden,rank,bits,group,hadamard,k", [
+    (64, 1024, 16, 4, 64, False, 0),
+    (64, 1024, 32, 8, 128, True, 0),
+    (64, 1024, 0, 8, 128, False, 9),
+    (128, 2048, 16, 4, 64, False, 5),
+])
+def test_torch_restatement_matches_oracle(pkg, rows, hidden, rank, bits, group, hadamard, k):
+    """oracle/lrq_torch.py (the CPU baseline bench.py times) computes what lrq_oracle computes:
+    L within one bf16 ulp on <= 1% of entries (fp32 vs exact sums), codes equal given that L
+    except for <= 1e-4 rounding flips, qparams equal, and the decode within the floating-point
+    bar (bf16-exact where no rotation reorders the sums)."""
+    from oracle import lrq_torch as T
+    from parity import assert_fp_close, bits16, ulp_diff_bf16
+    x = pkg.inputs.activation(rows, hidden, 8, 20.0, seed=3)
+    V = pkg.inputs.basis(hidden, rank, seed=3) if rank else None
+    idx = (torch.tensor(sorted(np.random.default_rng(0).choice(hidden, k, replace=False)), dtype=torch.int32)
+           if k else None)
+    e = T.encode(x, V, bits, group, hadamard, idx)
+    vb = bits16(V) if rank else None
+    ib = idx.numpy() if k else None
+    if rank:
+        d = ulp_diff_bf16(bits16(e["L"]), O.encode(bits16(x), vb, bits, group, hadamard=hadamard, outlier_idx=ib)["L"])
+        assert d.max() <= (64 if hadamard else 1) and (d > 0).mean() <= 1e-2
+    ref = O.encode(bits16(x), vb, bits, group, hadamard=hadamard, outlier_idx=ib,
+                   l_override=bits16(e["L"]) if rank else None)
+    cu = O.unpack_rowplanar(e["codes"].numpy(), bits).astype(np.int32)
+    cr = ref["codes_unpacked"].astype(np.int32)
+    assert np.abs(cu - cr).max() <= 1 and (cu != cr).mean() <= 1e-4
+    assert np.array_equal(e["scale"].numpy(), ref["scale"]) and np.array_equal(e["zero"].numpy(), ref["zero"])
+    if k:
+        assert np.array_equal(e["side"].numpy(), ref["side"])
+    xh = T.decode(e, V, bits, group, hadamard)
+    ro = O.reconstruct_f32(bits16(e["L"]) if rank else None, vb, e["codes"].numpy(), e["scale"].numpy(),
+                           e["zero"].numpy(), bits, group, hadamard=hadamard, side=ref["side"], idx=ib)
+    assert_fp_close(bits16(xh), ro.astype(np.float64), "torch decode")
+    if not hadamard:
+        assert (ulp_diff_bf16(bits16(xh), O.round_out(ro)) > 0).mean() <= 1e-5
+
+
+def test_torch_restatement_consumers_and_legacy(pkg):
+    """The torch-eager consumers and the reference's torch legacy forms against lrq_oracle."""
+    from oracle import lrq_torch as T
+    from parity import assert_fp_close, bits16, ulp_diff_bf16
+    x = pkg.inputs.activation(64, 1024, 0, 1.0, seed=4)
+    dy = pkg.inputs.gradient((64, 1024), 0.02, seed=4)
+    xf, dyf = O.bf16_to_f32(bits16(x)), O.bf16_to_f32(bits16(dy))
+    assert_fp_close(bits16(T.silu_bwd(x, dy)), O.silu_bwd(xf, dyf), "torch silu")
+    assert_fp_close(bits16(T.gelu_bwd(x, dy)), O.gelu_bwd(xf, dyf), "torch gelu")
+    p = pkg.inputs.softmax_probs((64, 1024), seed=4)
+    assert_fp_close(bits16(T.softmax_bwd(p, dy)), O.softmax_bwd(O.bf16_to_f32(bits16(p)), dyf), "torch softmax")
+    cfg = pkg.inputs.CONFIGS["legacy"]
+    ops = pkg.inputs.legacy_operands(cfg)
+    l, r, s = ops["l"][:256], ops["r"][:, :1024], ops["s"][:, :1024]
+    xl = pkg.inputs.activation(256, 1024, 8, 20.0, seed=1)[None]
+    for bits in (2, 4, 8):
+        o, q = T.legacy_encode(l, r, xl, s, bits, 2.0)
+        ro, rq = O.legacy_encode(bits16(l), bits16(r), bits16(xl), bits16(s), bits, 2.0)
+        assert np.array_equal(q.numpy(), rq)
+        assert np.array_equal(O.bf16_to_f32(bits16(o)), O.bf16_to_f32(ro))  # equal values (+-0 alike)
+        xh = T.legacy_decode(l, r, q, o, s, bits)
+        d = ulp_diff_bf16(bits16(xh), O.legacy_decode(bits16(l), bits16(r), rq, ro, bits16(s), bits))
+        assert d.max() <= 1 and (d > 0).mean() <= 1e-4

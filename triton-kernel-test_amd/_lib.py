@@ -40,7 +40,8 @@ class LrqTensors(ctypes.Structure):
 
 _T = POINTER(LrqTensors)
 
-# name -> (restype, argtypes); must cover every function declared in include/lrq.h
+# name -> (restype, argtypes); must cover every function declared in include/*.h (the drop-in
+# ABI in lrq.h and the test hooks in lrq_test_hooks.h)
 SIGNATURES = {
     "lrq_encode": (c_int32, [_T, c_void_p, c_int64, c_void_p]),
     "lrq_encode_twopass": (c_int32, [_T, c_void_p, c_int64, c_void_p]),

@@ -205,6 +205,9 @@ def encode(x: torch.Tensor, basis: Optional[LowRankBasis | torch.Tensor] = None,
         _require_device(outlier_idx)
         outlier_idx = outlier_idx.to(torch.int32).contiguous()
     k = 0 if outlier_idx is None else outlier_idx.numel()
+    if hadamard and k:
+        # the side columns would hold rotated values that no decode-side entry point accepts
+        raise ValueError("encode: outlier channels do not combine with the rotated (hadamard) format")
     bufs = _alloc(rows, n, bits, group_size, rank, k, x.device)
     c = CompressedActivation(codes=bufs["codes"], qparams=bufs["qparams"], L=bufs["L"],
                              basis=basis, side=bufs["side"], idx=outlier_idx if k else None,

@@ -309,20 +309,20 @@ extern "C" int lrq_coo_compact(const void* o, int64_t B, int64_t M, int64_t N, i
   const bool vec = N % 8 == 0 && aligned(o, 16);
   const uint16_t* ob = (const uint16_t*)o;
   if (p.nchunks > 0) {
-    if (vec) hipLaunchKernelGGL(k_coo_count<true>, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, ob, N, p.npc,
-                                p.npieces, piece_ptr, chunk_total);
-    else hipLaunchKernelGGL(k_coo_count<false>, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, ob, N, p.npc,
-                            p.npieces, piece_ptr, chunk_total);
+    if (vec) LRQ_TRY(launch(k_coo_count<true>, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, ob, N, p.npc,
+                                p.npieces, piece_ptr, chunk_total));
+    else LRQ_TRY(launch(k_coo_count<false>, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, ob, N, p.npc,
+                            p.npieces, piece_ptr, chunk_total));
   }
-  hipLaunchKernelGGL(k_coo_scan, dim3(1), dim3(kCooThreads), 0, s, chunk_total, p.nchunks, chunk_off, p.npieces,
-                     piece_ptr, nnz);
+  LRQ_TRY(launch(k_coo_scan, dim3(1), dim3(kCooThreads), 0, s, chunk_total, p.nchunks, chunk_off, p.npieces,
+                     piece_ptr, nnz));
   if (p.nchunks > 0) {
-    if (vec) hipLaunchKernelGGL(k_coo_scatter<true>, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, ob, M, N,
+    if (vec) LRQ_TRY(launch(k_coo_scatter<true>, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, ob, M, N,
                                 p.npc, p.npieces, piece_ptr, chunk_off, chunk_total, indices, ld_idx,
-                                (uint16_t*)values, cap);
-    else hipLaunchKernelGGL(k_coo_scatter<false>, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, ob, M, N,
+                                (uint16_t*)values, cap));
+    else LRQ_TRY(launch(k_coo_scatter<false>, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, ob, M, N,
                             p.npc, p.npieces, piece_ptr, chunk_off, chunk_total, indices, ld_idx, (uint16_t*)values,
-                            cap);
+                            cap));
   }
-  return launch_status();
+  return LRQ_OK;
 }

@@ -718,11 +718,11 @@ static int decode_rows_launch(const lrq_tensors* t, hipStream_t s, const EPI& ep
   if (shm > 160 * 1024) return LRQ_ERR_UNSUPPORTED;
   auto kern = k_decode_rows<BITS, G, R, NW, PD, OUTL, INP, EPI>;
   if (shm > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-  hipLaunchKernelGGL(kern, dim3((unsigned)((nrb + rbw - 1) / rbw), (unsigned)ug), dim3(NW * 64), shm, s,
+  LRQ_TRY(launch(kern, dim3((unsigned)((nrb + rbw - 1) / rbw), (unsigned)ug), dim3(NW * 64), shm, s,
                      (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
                      (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, t->outlier_idx, (int)t->n_outlier,
-                     (const uint16_t*)t->side, t->ld_side, epi, rbw);
-  return launch_status();
+                     (const uint16_t*)t->side, t->ld_side, epi, rbw));
+  return LRQ_OK;
 }
 
 template <int BITS, int G, int R, int RBW, class EPI>
@@ -734,17 +734,17 @@ static int decode_launch_rbw(const lrq_tensors* t, hipStream_t s, const EPI& epi
   dim3 grid((nrb + RBW - 1) / RBW, (units + NW - 1) / NW);
   if (t->n_outlier > 0) {
     const size_t shm = (size_t)(N / 32) * 4 + (size_t)N * 2;
-    hipLaunchKernelGGL((k_decode<BITS, G, R, true, NW, RBW, PD, EPI>), grid, dim3(NW * 64), shm, s,
+    LRQ_TRY(launch((k_decode<BITS, G, R, true, NW, RBW, PD, EPI>), grid, dim3(NW * 64), shm, s,
                        (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
                        (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, t->outlier_idx, t->n_outlier,
-                       (const uint16_t*)t->side, t->ld_side, epi);
+                       (const uint16_t*)t->side, t->ld_side, epi));
   } else {
     const size_t shm = 2 * (size_t)StagedTile<BITS, G, R, NW>::SLOT;
-    hipLaunchKernelGGL((k_decode_staged<BITS, G, R, NW, RBW, EPI>), grid, dim3(NW * 64), shm, s,
+    LRQ_TRY(launch((k_decode_staged<BITS, G, R, NW, RBW, EPI>), grid, dim3(NW * 64), shm, s,
                        (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
-                       (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, epi);
+                       (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, epi));
   }
-  return launch_status();
+  return LRQ_OK;
 }
 
 // 8 row blocks per wave (4 when the consumer also streams a second tensor in) when that

@@ -150,12 +150,12 @@ static int grid_for(int64_t work) {
 template <int OP>
 static int dense_launch(const void* x, const void* y, void* out, int64_t n, hipStream_t s) {
   if (aligned(x, 16) && aligned(y, 16) && aligned(out, 16))
-    hipLaunchKernelGGL((k_dense_elementwise<OP>), dim3(grid_for(n / 8)), dim3(256), 0, s, (const uint16_t*)x,
-                       (const uint16_t*)y, (uint16_t*)out, n);
+    LRQ_TRY(launch((k_dense_elementwise<OP>), dim3(grid_for(n / 8)), dim3(256), 0, s, (const uint16_t*)x,
+                       (const uint16_t*)y, (uint16_t*)out, n));
   else
-    hipLaunchKernelGGL((k_dense_elementwise_scalar<OP>), dim3(grid_for(n)), dim3(256), 0, s, (const uint16_t*)x,
-                       (const uint16_t*)y, (uint16_t*)out, n);
-  return launch_status();
+    LRQ_TRY(launch((k_dense_elementwise_scalar<OP>), dim3(grid_for(n)), dim3(256), 0, s, (const uint16_t*)x,
+                       (const uint16_t*)y, (uint16_t*)out, n));
+  return LRQ_OK;
 }
 
 }  // namespace lrq
@@ -185,12 +185,12 @@ extern "C" int lrq_dense_softmax_bwd(const void* y, const void* g, void* out, in
   hipStream_t s = (hipStream_t)stream;
   const bool vec = n_cols % 8 == 0 && n_cols <= 256 * 8 * 4 && aligned(y, 16) && aligned(g, 16) && aligned(out, 16);
   if (vec)
-    hipLaunchKernelGGL((k_dense_softmax_bwd<true>), dim3((unsigned)rows), dim3(256), 0, s, (const uint16_t*)y,
-                       (const uint16_t*)g, (uint16_t*)out, n_cols);
+    LRQ_TRY(launch((k_dense_softmax_bwd<true>), dim3((unsigned)rows), dim3(256), 0, s, (const uint16_t*)y,
+                       (const uint16_t*)g, (uint16_t*)out, n_cols));
   else
-    hipLaunchKernelGGL((k_dense_softmax_bwd<false>), dim3((unsigned)rows), dim3(256), 0, s, (const uint16_t*)y,
-                       (const uint16_t*)g, (uint16_t*)out, n_cols);
-  return launch_status();
+    LRQ_TRY(launch((k_dense_softmax_bwd<false>), dim3((unsigned)rows), dim3(256), 0, s, (const uint16_t*)y,
+                       (const uint16_t*)g, (uint16_t*)out, n_cols));
+  return LRQ_OK;
 }
 
 extern "C" int lrq_threshold_split(const void* x, int64_t n, float threshold, void* outlier, void* rest,
@@ -200,9 +200,9 @@ extern "C" int lrq_threshold_split(const void* x, int64_t n, float threshold, vo
   if (!aligned(x, 2) || !aligned(outlier, 2) || !aligned(rest, 2)) return LRQ_ERR_ALIGN;
   if (n == 0) return LRQ_OK;
   const float tau = bf16_value_host(bf16_bits_host(threshold));
-  hipLaunchKernelGGL(k_threshold_split, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)x, n, tau,
-                     (uint16_t*)outlier, (uint16_t*)rest);
-  return launch_status();
+  LRQ_TRY(launch(k_threshold_split, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)x, n, tau,
+                     (uint16_t*)outlier, (uint16_t*)rest));
+  return LRQ_OK;
 }
 
 extern "C" int lrq_gather_rows_zero(void* x, int64_t B, int64_t M, int64_t N, const int32_t* idx, int32_t k,
@@ -211,7 +211,7 @@ extern "C" int lrq_gather_rows_zero(void* x, int64_t B, int64_t M, int64_t N, co
   if (B < 0 || M < 0 || N < 0 || k < 0 || B * (int64_t)k > INT32_MAX) return LRQ_ERR_SHAPE;
   if (!aligned(x, 2) || (out != nullptr && !aligned(out, 2)) || (idx != nullptr && !aligned(idx, 4))) return LRQ_ERR_ALIGN;
   if (B == 0 || k == 0 || N == 0) return LRQ_OK;
-  hipLaunchKernelGGL(k_gather_rows_zero, dim3((unsigned)(B * k)), dim3(256), 0, (hipStream_t)stream, (uint16_t*)x, M, N,
-                     idx, (int)k, (uint16_t*)out);
-  return launch_status();
+  LRQ_TRY(launch(k_gather_rows_zero, dim3((unsigned)(B * k)), dim3(256), 0, (hipStream_t)stream, (uint16_t*)x, M, N,
+                     idx, (int)k, (uint16_t*)out));
+  return LRQ_OK;
 }

@@ -893,10 +893,10 @@ static int launch_persist_rbw(const lrq_tensors* t, const void* x, int64_t ldx, 
   auto kern = k_encode_persist<BITS, G, R, NW, UPW, DB, VLDS, RBW>;
   if (shm > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
   const int nrb = (int)((t->rows + 15) / 16);
-  hipLaunchKernelGGL(kern, dim3((nrb + RBW - 1) / RBW), dim3(NW * 64), shm, s, (const uint16_t*)x, ldx,
+  LRQ_TRY(launch(kern, dim3((nrb + RBW - 1) / RBW), dim3(NW * 64), shm, s, (const uint16_t*)x, ldx,
                      (int)t->rows, (int)t->hidden, (const uint16_t*)t->V, (uint16_t*)t->L, t->ld_L,
-                     (uint8_t*)t->codes, t->ld_codes, (uint16_t*)t->qparams, t->ld_qp);
-  return launch_status();
+                     (uint8_t*)t->codes, t->ld_codes, (uint16_t*)t->qparams, t->ld_qp));
+  return LRQ_OK;
 }
 
 // Row blocks per workgroup: 4 when that still gives every CU a workgroup, else 1 (one
@@ -918,10 +918,10 @@ static int launch_rows(const lrq_tensors* t, const void* x, int64_t ldx, hipStre
   const int64_t nrb = (t->rows + 15) / 16, cus = cu_count();
   const int rbw = (int)((nrb + cus - 1) / cus);
   const int64_t wgs = (nrb + rbw - 1) / rbw;
-  hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(NW * 64), Re::LDS, s, (const uint16_t*)x, ldx, (int)t->rows,
+  LRQ_TRY(launch(kern, dim3((unsigned)wgs), dim3(NW * 64), Re::LDS, s, (const uint16_t*)x, ldx, (int)t->rows,
                      (int)t->hidden, (const uint16_t*)t->V, (uint16_t*)t->L, t->ld_L, (uint8_t*)t->codes,
-                     t->ld_codes, (uint16_t*)t->qparams, t->ld_qp, rbw);
-  return launch_status();
+                     t->ld_codes, (uint16_t*)t->qparams, t->ld_qp, rbw));
+  return LRQ_OK;
 }
 
 // Returns 1 and launches when a single-pass kernel exists for this shape, else 0.
@@ -998,14 +998,12 @@ static int encode_slabs(const lrq_tensors* t, const void* x, int64_t ldx, hipStr
     // pass 1: about one workgroup per CU over (row groups, slabs)
     const int per1 = std::max(1, cus / nslab);
     const int rbw1 = (nrb + per1 - 1) / per1;
-    hipLaunchKernelGGL((k_project_slab<R, ROT>), dim3((nrb + rbw1 - 1) / rbw1, nslab), dim3(512), 0, s,
-                       (const uint16_t*)x, ldx, M, N, (const uint16_t*)t->Vt, (unsigned char*)t->codes, ldp, rbw1);
-    int st = launch_status();
+    int st = launch((k_project_slab<R, ROT>), dim3((nrb + rbw1 - 1) / rbw1, nslab), dim3(512), 0, s,
+                    (const uint16_t*)x, ldx, M, N, (const uint16_t*)t->Vt, (unsigned char*)t->codes, ldp, rbw1);
     if (st) { *status = st; return 1; }
     const int64_t nred = (int64_t)M * (R / 4);
-    hipLaunchKernelGGL((k_reduce_slabs<R>), dim3((unsigned)((nred + 255) / 256)), dim3(256), 0, s,
-                       (const unsigned char*)t->codes, ldp, M, nslab, (uint16_t*)t->L, t->ld_L);
-    st = launch_status();
+    st = launch((k_reduce_slabs<R>), dim3((unsigned)((nred + 255) / 256)), dim3(256), 0, s,
+                (const unsigned char*)t->codes, ldp, M, nslab, (uint16_t*)t->L, t->ld_L);
     if (st) { *status = st; return 1; }
   }
   // quantisation pass: 8 independent waves per workgroup, one workgroup per CU
@@ -1013,24 +1011,23 @@ static int encode_slabs(const lrq_tensors* t, const void* x, int64_t ldx, hipStr
   const int nranges = std::max(1, std::min(nrb, cus * 8 / nwc));
   const int rbw2 = (nrb + nranges - 1) / nranges;
   const int waves = nranges * nwc;
-  auto launch = [&](auto kern) {
+  auto quant = [&](auto kern) {
     if (shm > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-    hipLaunchKernelGGL(kern, dim3((waves + 7) / 8), dim3(512), shm, s, (const uint16_t*)x, ldx, M, N,
-                       (const uint16_t*)t->V, (const uint16_t*)t->L, t->ld_L, (uint8_t*)t->codes, t->ld_codes,
-                       (uint16_t*)t->qparams, t->ld_qp, t->outlier_idx, (int)t->n_outlier, (uint16_t*)t->side,
-                       t->ld_side, nranges, rbw2);
+    *status = launch(kern, dim3((waves + 7) / 8), dim3(512), shm, s, (const uint16_t*)x, ldx, M, N,
+                     (const uint16_t*)t->V, (const uint16_t*)t->L, t->ld_L, (uint8_t*)t->codes, t->ld_codes,
+                     (uint16_t*)t->qparams, t->ld_qp, t->outlier_idx, (int)t->n_outlier, (uint16_t*)t->side,
+                     t->ld_side, nranges, rbw2);
   };
   if constexpr (ROT) {
     if constexpr (NP == 2 && G == 128) return 0;  // not built (its registers would spill)
-    else launch(k_quant_slab<BITS, G, R, false, true>);
+    else quant(k_quant_slab<BITS, G, R, false, true>);
   } else {
     if (outl) {
-      if constexpr (R == 0) launch(k_quant_slab<BITS, G, R, true, false>);
+      if constexpr (R == 0) quant(k_quant_slab<BITS, G, R, true, false>);
     } else {
-      launch(k_quant_slab<BITS, G, R, false, false>);
+      quant(k_quant_slab<BITS, G, R, false, false>);
     }
   }
-  *status = launch_status();
   return 1;
 }
 
@@ -1043,29 +1040,25 @@ static int encode_twopass(const lrq_tensors* t, const void* x, int64_t ldx, hipS
     if (encode_slabs<BITS, G, R, false>(t, x, ldx, s, &st)) return st;
   }
   if constexpr (R > 0) {
-    hipLaunchKernelGGL((k_project<R>), dim3((M + 15) / 16), dim3(256), 0, s, (const uint16_t*)x, ldx, M, N,
-                       (const uint16_t*)t->Vt, (uint16_t*)t->L, t->ld_L);
-    int st = launch_status();
-    if (st) return st;
+    LRQ_TRY(launch((k_project<R>), dim3((M + 15) / 16), dim3(256), 0, s, (const uint16_t*)x, ldx, M, N,
+                       (const uint16_t*)t->Vt, (uint16_t*)t->L, t->ld_L));
   }
   const int units = N / (G * NP);
   dim3 grid((M + 64 * RB - 1) / (64 * RB), units);
   if (t->n_outlier > 0) {
-    hipLaunchKernelGGL((k_quant<BITS, G, R, RB, true>), grid, dim3(256), (size_t)(N / 32) * 4, s,
+    LRQ_TRY(launch((k_quant<BITS, G, R, RB, true>), grid, dim3(256), (size_t)(N / 32) * 4, s,
                        (const uint16_t*)x, ldx, M, N, (const uint16_t*)t->V, (const uint16_t*)t->L, t->ld_L,
                        (uint8_t*)t->codes, t->ld_codes, (uint16_t*)t->qparams, t->ld_qp, t->outlier_idx,
-                       t->n_outlier);
-    int st = launch_status();
-    if (st) return st;
+                       t->n_outlier));
     const int64_t n = (int64_t)M * t->n_outlier;
-    hipLaunchKernelGGL(k_gather_side, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const uint16_t*)x,
-                       ldx, M, N, t->outlier_idx, t->n_outlier, (uint16_t*)t->side, t->ld_side);
+    LRQ_TRY(launch(k_gather_side, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const uint16_t*)x,
+                       ldx, M, N, t->outlier_idx, t->n_outlier, (uint16_t*)t->side, t->ld_side));
   } else {
-    hipLaunchKernelGGL((k_quant<BITS, G, R, RB, false>), grid, dim3(256), 0, s, (const uint16_t*)x, ldx, M, N,
+    LRQ_TRY(launch((k_quant<BITS, G, R, RB, false>), grid, dim3(256), 0, s, (const uint16_t*)x, ldx, M, N,
                        (const uint16_t*)t->V, (const uint16_t*)t->L, t->ld_L, (uint8_t*)t->codes, t->ld_codes,
-                       (uint16_t*)t->qparams, t->ld_qp, nullptr, 0);
+                       (uint16_t*)t->qparams, t->ld_qp, nullptr, 0));
   }
-  return launch_status();
+  return LRQ_OK;
 }
 
 template <int BITS, int G, int R>

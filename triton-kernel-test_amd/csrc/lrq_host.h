@@ -6,8 +6,12 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <cstring>
 #include <initializer_list>
+#include <tuple>
+#include <type_traits>
+#include <utility>
 
 #include "../../include/lrq.h"
 
@@ -32,18 +36,45 @@ static inline float bf16_value_host(uint16_t h) {
 
 static constexpr int format_key(int bits, int group, int rank) { return bits * 100000 + group * 100 + rank; }
 
-// Compute units of the current device (256 on MI355X); launch shapes are sized from it.
+// Compute units of the current device (256 on MI355X); launch shapes are sized from it.  The
+// attribute is read once per device and kept (a constant of the hardware, so the cache is
+// the same for every caller and thread; a racing first read stores the same value).
 static inline int cu_count() {
+  constexpr int kMaxDev = 64;
+  static std::atomic<int> cached[kMaxDev];
   int dev = 0, n = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev >= 0 && dev < kMaxDev) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+  if (dev >= 0 && dev < kMaxDev) cached[dev].store(n, std::memory_order_relaxed);
   return n;
 }
 
-static inline int launch_status() {
-  hipError_t e = hipGetLastError();
+// Launches kernel k and returns the status of this launch only: hipLaunchKernel's own
+// result, so an error that an earlier call left on the thread is neither reported here nor
+// cleared.  The arguments are converted to the kernel's parameter types first.
+template <typename... P, typename... A>
+static inline int launch(void (*k)(P...), dim3 grid, dim3 block, size_t shm, hipStream_t s, A&&... args) {
+  static_assert(sizeof...(P) == sizeof...(A), "kernel argument count");
+  std::tuple<std::decay_t<P>...> params(std::forward<A>(args)...);
+  void* argv[sizeof...(P) > 0 ? sizeof...(P) : 1];
+  std::apply([&](auto&... p) {
+    int i = 0;
+    ((argv[i++] = (void*)&p), ...);
+  }, params);
+  const hipError_t e = hipLaunchKernel((const void*)k, grid, block, argv, shm, s);
   return e == hipSuccess ? LRQ_OK : (int)e;
 }
+
+// Returns from the enclosing function with a non-zero status.
+#define LRQ_TRY(expr)                            \
+  do {                                           \
+    const int lrq_try_status_ = (expr);          \
+    if (lrq_try_status_ != LRQ_OK) return lrq_try_status_; \
+  } while (0)
 
 // Validates a group-mode descriptor (Vt is checked by the two-pass encode, its only reader).
 static inline int validate_tensors(const lrq_tensors* t) {

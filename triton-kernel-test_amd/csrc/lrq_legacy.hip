@@ -357,15 +357,15 @@ static int legacy_launch(const LegacyArgs& a, int K, int64_t B, bool mfma_ok, hi
   if (mfma_ok && NB % 64 == 0 && NB / 64 <= 65535 && B <= 65535) {
     constexpr int RB = 4;
     dim3 grid((unsigned)((a.M + 64 * RB - 1) / (64 * RB)), (unsigned)(NB / 64), (unsigned)B);
-    if (K == 16) hipLaunchKernelGGL((k_legacy_mfma<MODE, BITS, 16, RB, OSRC>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((k_legacy_mfma<MODE, BITS, 32, RB, OSRC>), grid, dim3(256), 0, st, a);
+    if (K == 16) LRQ_TRY(launch((k_legacy_mfma<MODE, BITS, 16, RB, OSRC>), grid, dim3(256), 0, st, a));
+    else LRQ_TRY(launch((k_legacy_mfma<MODE, BITS, 32, RB, OSRC>), grid, dim3(256), 0, st, a));
   } else {
     const int64_t chunks = (NB + 255) / 256;
     if (B * a.M * chunks > INT32_MAX) return LRQ_ERR_SHAPE;
-    hipLaunchKernelGGL((k_legacy_scalar<MODE, BITS, OSRC>), dim3((unsigned)(B * a.M * chunks)), dim3(256), 0, st, a,
-                       K, chunks);
+    LRQ_TRY(launch((k_legacy_scalar<MODE, BITS, OSRC>), dim3((unsigned)(B * a.M * chunks)), dim3(256), 0, st, a,
+                       K, chunks));
   }
-  return launch_status();
+  return LRQ_OK;
 }
 
 template <int MODE, int OSRC>
@@ -508,19 +508,19 @@ extern "C" int lrq_legacy_kth_residual(const void* l, const void* rt, int32_t K,
   a.l = (const uint16_t*)l, a.rt = (const uint16_t*)rt, a.x = (const uint16_t*)x, a.ldx_b = 0, a.ldx_m = ldx_m;
   a.M = M, a.N = N, a.hist = hist, a.sel = sel;
   const bool mfma_ok = vec_ok({l, rt, x}) && ldx_m % 8 == 0 && N % 64 == 0 && N / 64 <= 65535;
-  hipLaunchKernelGGL(k_kth_init, dim3(1), dim3(256), 0, hs, hist, sel, k);
+  LRQ_TRY(launch(k_kth_init, dim3(1), dim3(256), 0, hs, hist, sel, k));
   for (int fine = 0; fine < 2; ++fine) {
     if (mfma_ok) {
       constexpr int RB = 4;
       dim3 grid((unsigned)((M + 64 * RB - 1) / (64 * RB)), (unsigned)(N / 64), 1u);
-      if (K == 16) hipLaunchKernelGGL((k_legacy_mfma<kHist, 8, 16, RB, 0>), grid, dim3(256), 0, hs, a);
-      else hipLaunchKernelGGL((k_legacy_mfma<kHist, 8, 32, RB, 0>), grid, dim3(256), 0, hs, a);
+      if (K == 16) LRQ_TRY(launch((k_legacy_mfma<kHist, 8, 16, RB, 0>), grid, dim3(256), 0, hs, a));
+      else LRQ_TRY(launch((k_legacy_mfma<kHist, 8, 32, RB, 0>), grid, dim3(256), 0, hs, a));
     } else {
       const int64_t chunks = (N + 255) / 256;
       if (M * chunks > INT32_MAX) return LRQ_ERR_SHAPE;
-      hipLaunchKernelGGL(k_hist_scalar, dim3((unsigned)(M * chunks)), dim3(256), 0, hs, a, (int)K, chunks);
+      LRQ_TRY(launch(k_hist_scalar, dim3((unsigned)(M * chunks)), dim3(256), 0, hs, a, (int)K, chunks));
     }
-    hipLaunchKernelGGL(k_kth_select, dim3(1), dim3(256), 0, hs, hist, sel, fine, out);
+    LRQ_TRY(launch(k_kth_select, dim3(1), dim3(256), 0, hs, hist, sel, fine, out));
   }
-  return launch_status();
+  return LRQ_OK;
 }

@@ -254,9 +254,9 @@ extern "C" int lrq_transpose_bf16(const void* src, int64_t rows, int64_t cols, v
   if (!aligned(src, 2) || !aligned(dst, 2)) return LRQ_ERR_ALIGN;
   if (rows == 0 || cols == 0) return LRQ_OK;
   dim3 grid((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32));
-  hipLaunchKernelGGL(k_transpose_bf16, grid, dim3(256), 0, (hipStream_t)stream, (const uint16_t*)src, rows,
-                     cols, (uint16_t*)dst);
-  return launch_status();
+  LRQ_TRY(launch(k_transpose_bf16, grid, dim3(256), 0, (hipStream_t)stream, (const uint16_t*)src, rows,
+                     cols, (uint16_t*)dst));
+  return LRQ_OK;
 }
 
 extern "C" int lrq_colmax(const void* x, int64_t ldx, int64_t rows, int64_t hidden, float* colmax,
@@ -265,10 +265,9 @@ extern "C" int lrq_colmax(const void* x, int64_t ldx, int64_t rows, int64_t hidd
   if (rows < 0 || hidden <= 0 || ldx < hidden || (hidden % 2) != 0) return LRQ_ERR_SHAPE;
   if ((ldx % 2) != 0 || !aligned(x, 4) || !aligned(colmax, 4)) return LRQ_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(k_zero_u32, dim3((unsigned)((hidden + 255) / 256)), dim3(256), 0, s,
-                     (unsigned int*)colmax, hidden);
-  int st = launch_status();
-  if (st || rows == 0) return st;
+  LRQ_TRY(launch(k_zero_u32, dim3((unsigned)((hidden + 255) / 256)), dim3(256), 0, s,
+                     (unsigned int*)colmax, hidden));
+  if (rows == 0) return LRQ_OK;
   if ((hidden % 8) == 0 && (ldx % 8) == 0 && aligned(x, 16)) {
     // about four workgroups per CU (two measured slower, eight slower still: one atomic per
     // column per workgroup), row groups of whole 64-row steps (4 phases x 16-row batches)
@@ -277,14 +276,14 @@ extern "C" int lrq_colmax(const void* x, int64_t ldx, int64_t rows, int64_t hidd
     int64_t rows_per = (rows + groups - 1) / groups;
     rows_per = (rows_per + 63) / 64 * 64;
     groups = (rows + rows_per - 1) / rows_per;
-    hipLaunchKernelGGL(k_colmax, dim3((unsigned)cgroups, (unsigned)groups), dim3(256), 0, s, (const uint16_t*)x, ldx,
-                       rows, hidden, rows_per, (unsigned int*)colmax);
+    LRQ_TRY(launch(k_colmax, dim3((unsigned)cgroups, (unsigned)groups), dim3(256), 0, s, (const uint16_t*)x, ldx,
+                       rows, hidden, rows_per, (unsigned int*)colmax));
   } else {
     dim3 grid((unsigned)((hidden / 2 + 255) / 256), (unsigned)((rows + 63) / 64));
-    hipLaunchKernelGGL(k_colmax2, grid, dim3(256), 0, s, (const uint16_t*)x, ldx, rows, hidden,
-                       (unsigned int*)colmax);
+    LRQ_TRY(launch(k_colmax2, grid, dim3(256), 0, s, (const uint16_t*)x, ldx, rows, hidden,
+                       (unsigned int*)colmax));
   }
-  return launch_status();
+  return LRQ_OK;
 }
 
 extern "C" int lrq_topk(const float* colmax, int64_t hidden, int32_t k, int32_t* idx, void* stream) {
@@ -294,8 +293,8 @@ extern "C" int lrq_topk(const float* colmax, int64_t hidden, int32_t k, int32_t*
   const size_t shm = (size_t)hidden * 4;
   if (shm + 2048 > 160 * 1024) return LRQ_ERR_SHAPE;
   if (k == 0) return LRQ_OK;
-  hipLaunchKernelGGL(k_topk, dim3(1), dim3(1024), shm, (hipStream_t)stream, colmax, (int)hidden, (int)k, idx);
-  return launch_status();
+  LRQ_TRY(launch(k_topk, dim3(1), dim3(1024), shm, (hipStream_t)stream, colmax, (int)hidden, (int)k, idx));
+  return LRQ_OK;
 }
 
 extern "C" const char* lrq_status_string(int status) {

@@ -718,11 +718,11 @@ static int softmax_launch(const lrq_tensors* t, const void* dp, int64_t lddp, vo
   constexpr int RBW = 2;
   const int M = (int)t->rows, N = (int)t->hidden;
   const int nrb = (M + 15) / 16;
-  hipLaunchKernelGGL((k_softmax_bwd<BITS, G, R, NW, UPW, RBW>), dim3((nrb + RBW - 1) / RBW), dim3(NW * 64), 0, s,
+  LRQ_TRY(launch((k_softmax_bwd<BITS, G, R, NW, UPW, RBW>), dim3((nrb + RBW - 1) / RBW), dim3(NW * 64), 0, s,
                      (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
                      (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)dp, lddp,
-                     (uint16_t*)ds, ldds);
-  return launch_status();
+                     (uint16_t*)ds, ldds));
+  return LRQ_OK;
 }
 
 template <int BITS, int G, int R, int NW>
@@ -737,10 +737,10 @@ static int softmax_rows_launch(const lrq_tensors* t, const void* dp, int64_t ldd
   auto kern = k_softmax_rows<BITS, G, R, NW>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)St::LDS);
   if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL(kern, dim3((nrb + rbw - 1) / rbw), dim3(NW * 64), St::LDS, s, (const uint8_t*)t->codes,
+  LRQ_TRY(launch(kern, dim3((nrb + rbw - 1) / rbw), dim3(NW * 64), St::LDS, s, (const uint8_t*)t->codes,
                      t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp, (const uint16_t*)t->L, t->ld_L,
-                     (const uint16_t*)t->V, M, N, (const uint16_t*)dp, lddp, (uint16_t*)ds, ldds, rbw);
-  return launch_status();
+                     (const uint16_t*)t->V, M, N, (const uint16_t*)dp, lddp, (uint16_t*)ds, ldds, rbw));
+  return LRQ_OK;
 }
 
 // One pass needs the whole row in one workgroup: 4, 8 or 16 units (one per wave).  Rows of
@@ -779,20 +779,20 @@ static int gemm_launch(const lrq_tensors* t, const void* a, void* out, int64_t l
     const int units = N / (UC);
     auto wlaunch = [&](auto nu) {
       constexpr int NU = decltype(nu)::value, WRBW = 4, WSL = 2;
-      hipLaunchKernelGGL((k_dequant_gemm_w<BITS, G, R, NW, NU, WRBW, WSL, F32>), dim3((nrb + WRBW - 1) / WRBW),
+      LRQ_TRY(launch((k_dequant_gemm_w<BITS, G, R, NW, NU, WRBW, WSL, F32>), dim3((nrb + WRBW - 1) / WRBW),
                          dim3(NW * 64), 0, s, (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams,
                          t->ld_qp, (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)a,
-                         out, ldo);
-      return launch_status();
+                         out, ldo));
+      return LRQ_OK;
     };
     if (units == NW * 4) return wlaunch(std::integral_constant<int, 4>{});
     if (units == NW * 2) return wlaunch(std::integral_constant<int, 2>{});
     if (units == NW) return wlaunch(std::integral_constant<int, 1>{});
   }
-  hipLaunchKernelGGL((k_dequant_gemm<BITS, G, R, NOUT, NW, RBW, SL, F32>), dim3((nrb + RBW - 1) / RBW), dim3(NW * 64), 0,
+  LRQ_TRY(launch((k_dequant_gemm<BITS, G, R, NOUT, NW, RBW, SL, F32>), dim3((nrb + RBW - 1) / RBW), dim3(NW * 64), 0,
                      s, (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
-                     (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)a, out, ldo);
-  return launch_status();
+                     (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)a, out, ldo));
+  return LRQ_OK;
 }
 
 template <int BITS, int G, int R>
@@ -842,14 +842,14 @@ static int gemm_t_run(const lrq_tensors* t, const void* gmat, int64_t ldg, void*
   constexpr int PD = G * (8 / BITS) * KT >= 512 ? 2 : 4;  // ring depth within the register budget
   const int M = (int)t->rows, N = (int)t->hidden;
   if (pl.rg > 0)
-    hipLaunchKernelGGL((k_dequant_gemm_t<BITS, G, R, KT, NW, UPW, PD>), dim3(pl.cg * pl.rg), dim3(NW * 64), 0, s,
+    LRQ_TRY(launch((k_dequant_gemm_t<BITS, G, R, KT, NW, UPW, PD>), dim3(pl.cg * pl.rg), dim3(NW * 64), 0, s,
                        (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
                        (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)gmat, ldg, ws,
-                       pl.bpg, pl.cg, pl.rg % 8 == 0);
+                       pl.bpg, pl.cg, pl.rg % 8 == 0));
   const int64_t nk = (int64_t)N * 16 * KT;
-  hipLaunchKernelGGL(k_sum_parts<F32>, dim3((unsigned)((nk / 4 + 255) / 256)), dim3(256), 0, s, ws, pl.rg, nk,
-                     16 * KT, out, ldo);
-  return launch_status();
+  LRQ_TRY(launch(k_sum_parts<F32>, dim3((unsigned)((nk / 4 + 255) / 256)), dim3(256), 0, s, ws, pl.rg, nk,
+                     16 * KT, out, ldo));
+  return LRQ_OK;
 }
 
 template <int BITS, int G, int R, int KT, bool F32>

@@ -159,15 +159,15 @@ extern "C" int lrq_wht128(const void* x, int64_t ldx, int64_t rows, int64_t hidd
     const int slabs = (int)(hidden / 512);
     const int ranges = std::max(1, std::min(nrb, cu_count() * 4 / slabs));
     const int rbw = (nrb + ranges - 1) / ranges;
-    hipLaunchKernelGGL(k_wht_rows, dim3((nrb + rbw - 1) / rbw, slabs), dim3(256), 0, (hipStream_t)stream,
-                       (const uint16_t*)x, ldx, (int)rows, (uint16_t*)y, ldy, rbw);
-    return launch_status();
+    LRQ_TRY(launch(k_wht_rows, dim3((nrb + rbw - 1) / rbw, slabs), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)x, ldx, (int)rows, (uint16_t*)y, ldy, rbw));
+    return LRQ_OK;
   }
   constexpr int RBW = 4;
   const int nrb = (int)((rows + 15) / 16);
   const int nblk = (int)(hidden / 128);
   dim3 grid((nrb + RBW - 1) / RBW, (nblk + 3) / 4);
-  hipLaunchKernelGGL((k_wht128<RBW>), grid, dim3(256), 0, (hipStream_t)stream, (const uint16_t*)x, ldx, (int)rows,
-                     (int)hidden, (uint16_t*)y, ldy);
-  return launch_status();
+  LRQ_TRY(launch((k_wht128<RBW>), grid, dim3(256), 0, (hipStream_t)stream, (const uint16_t*)x, ldx, (int)rows,
+                     (int)hidden, (uint16_t*)y, ldy));
+  return LRQ_OK;
 }

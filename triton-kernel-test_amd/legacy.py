@@ -371,11 +371,12 @@ def triton_matmul_decompress(q, l, r, s, y, quantize_bit=2):
     """(decode(q) ) @ y per batch: x_hat[B, M, N] @ y[B, N, n] -> bf16 [B, M, n].
 
     The legacy per-column format is decoded by the HIP decode kernel and multiplied by the
-    library GEMM; the fused dequant-GEMM kernel serves the group-mode format
-    (``api.dequant_gemm``)."""
+    library GEMM in fp32 (bf16 operands are exact in fp32), so the product is rounded to bf16
+    once, as the fused kernels round theirs; the fused dequant-GEMM kernel serves the
+    group-mode format (``api.dequant_gemm``)."""
     a = _legacy_fused(_OP_STORE, l, r, q, s, None, quantize_bit)
     _require_device(y)
-    return torch.matmul(a, y.to(torch.bfloat16).contiguous())
+    return torch.matmul(a.float(), y.to(torch.bfloat16).float()).to(torch.bfloat16)
 
 
 def _dense(op, x, y):
