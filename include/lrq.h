@@ -138,6 +138,22 @@ int lrq_dequant_gemm_t(const lrq_tensors* t, const void* g, int64_t ldg, int32_t
  * Host only: no HIP call. */
 int64_t lrq_dequant_gemm_t_workspace(const lrq_tensors* t, int32_t n_out);
 
+/* Largest workspace lrq_dequant_gemm_t_noalloc can serve from its own scratch (bytes). */
+#define LRQ_GEMM_T_SCRATCH_BYTES (16 * 1024 * 1024)
+
+/* Allocation-free form of lrq_dequant_gemm_t.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments, kernels and results as
+ * lrq_dequant_gemm_t, without the workspace: the row-group partials go to a scratch array of
+ * LRQ_GEMM_T_SCRATCH_BYTES that the library keeps in device memory, one per GPU it runs on,
+ * held until the process ends.  The call allocates nothing.  Shapes whose
+ * lrq_dequant_gemm_t_workspace(t, n_out) exceeds the scratch return LRQ_ERR_WORKSPACE (checked
+ * on the host before any HIP call).  Every call on one GPU shares that GPU's scratch, and the
+ * scratch keeps the last call's partials: calls that overlap on one GPU (different streams or
+ * threads without ordering between them) race; calls ordered on one stream do not. */
+int lrq_dequant_gemm_t_noalloc(const lrq_tensors* t, const void* g, int64_t ldg, int32_t n_out, void* out,
+                               int64_t ldo, int32_t out_fp32, void* stream);
+
 /* colmax[c] = max_r |x[r, c]| (fp32).  First half of the outlier-channel split
  * (no reference counterpart; the reference's channel split takes caller indices,
  * extraction_outlier_channel.py:11-14). */

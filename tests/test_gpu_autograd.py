@@ -12,7 +12,8 @@ pytestmark = pytest.mark.gpu
 
 
 def _rel(a, b):
-    return float((a.double().cpu() - b.double().cpu()).norm() / b.double().cpu().norm())
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return float((a - b).norm() / b.norm())
 
 
 def _f64_lora(x, w, a, b, dy):

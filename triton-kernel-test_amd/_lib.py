@@ -21,6 +21,7 @@ LRQ_ERR_UNSUPPORTED = -3
 LRQ_ERR_ALIGN = -4
 LRQ_ERR_WORKSPACE = -5
 LRQ_FLAG_HADAMARD = 1
+LRQ_GEMM_T_SCRATCH_BYTES = 16 * 1024 * 1024  # include/lrq.h
 
 
 class LrqTensors(ctypes.Structure):
@@ -54,6 +55,7 @@ SIGNATURES = {
     "lrq_dequant_gemm_t": (c_int32, [_T, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p,
                                      c_int64, c_void_p]),
     "lrq_dequant_gemm_t_workspace": (c_int64, [_T, c_int32]),
+    "lrq_dequant_gemm_t_noalloc": (c_int32, [_T, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p]),
     "lrq_colmax": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     "lrq_topk": (c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p]),
     "lrq_transpose_bf16": (c_int32, [c_void_p, c_int64, c_int64, c_void_p, c_void_p]),

@@ -33,7 +33,7 @@ from ._lib import LrqTensors, call
 __all__ = [
     "LowRankBasis", "CompressedActivation", "encode", "decode", "silu_backward_compressed",
     "gelu_backward_compressed", "mul_compressed", "softmax_backward_compressed", "dequant_gemm",
-    "dequant_gemm_t", "outlier_channels", "column_absmax", "topk_channels", "wht128",
+    "dequant_gemm_t", "dequant_gemm_t_noalloc", "outlier_channels", "column_absmax", "topk_channels", "wht128",
 ]
 
 
@@ -360,6 +360,27 @@ def dequant_gemm_t(c: CompressedActivation, g: torch.Tensor, out_dtype=torch.flo
         call("lrq_dequant_gemm_t", ctypes.byref(t), _p(g2), n_out, n_out, _p(o), n_out,
              1 if out_dtype == torch.float32 else 0, _p(ws), ws.numel() * 4, _stream(c.device))
     return o
+
+
+def dequant_gemm_t_noalloc(c: CompressedActivation, g: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """``dequant_gemm_t`` into a caller-provided ``out`` [N, n] (fp32 or bf16, contiguous), with
+    the library's own device scratch in place of a workspace: neither this function nor the
+    library allocates device memory, so it can run under HIP graph capture.  ``g`` must be a
+    contiguous bf16 [rows, n].  Calls that overlap on one GPU share the scratch and race."""
+    _require_device(g, out)
+    if g.dtype != torch.bfloat16 or g.dim() != 2 or g.shape[0] != c.rows or not g.is_contiguous():
+        raise ValueError("g must be a contiguous bf16 [rows, n]")
+    n_out = g.shape[1]
+    if out.dtype not in (torch.float32, torch.bfloat16) or tuple(out.shape) != (c.hidden, n_out) \
+            or not out.is_contiguous():
+        raise ValueError("out must be a contiguous fp32 or bf16 [N, n]")
+    if c.hadamard or c.idx is not None:
+        raise ValueError("dequant_gemm_t_noalloc: rotated format and outlier channels are not supported")
+    t = c.descriptor()
+    with torch.cuda.device(c.device):
+        call("lrq_dequant_gemm_t_noalloc", ctypes.byref(t), _p(g), n_out, n_out, _p(out), n_out,
+             1 if out.dtype == torch.float32 else 0, _stream(c.device))
+    return out
 
 
 def column_absmax(x: torch.Tensor) -> torch.Tensor:

@@ -15,6 +15,7 @@
 #include "lrq_host.h"
 
 #include <algorithm>
+#include <mutex>
 
 namespace lrq {
 
@@ -873,6 +874,38 @@ static int gemm_t_nout(const lrq_tensors* t, const void* gmat, int64_t ldg, int 
   }
 }
 
+// ---------------------------------------------------------------- allocation-free scratch
+// lrq_dequant_gemm_t_noalloc keeps its row-group partials here instead of in a caller
+// workspace.  Each GPU holds its own copy of the array at its own address; host code may not
+// pass the array's name to a kernel (on the host it is only a stand-in), so the device address
+// is looked up once per device with hipGetSymbolAddress and kept.  No partial is read before
+// it is written (k_dequant_gemm_t writes every partial of its row group, k_sum_parts reads
+// them), so nothing needs clearing between calls.
+static __device__ __align__(256) float scratch[LRQ_GEMM_T_SCRATCH_BYTES / sizeof(float)];
+
+static constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static float* g_scratch_ptr[kMaxDevices];
+
+// The current device's scratch address (looked up on the device's first call), or a positive
+// hipError_t.
+static int scratch_on_current_device(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return (int)hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (ptr == nullptr) return (int)hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return LRQ_OK;
+}
+
 #define LRQ_FORMATS(F, ...)                                 \
   switch (format_key(t->bits, t->group, t->rank)) {           \
     case format_key(4, 64, 0): return F<4, 64, 0>(__VA_ARGS__);    \
@@ -946,5 +979,24 @@ extern "C" int lrq_dequant_gemm_t(const lrq_tensors* t, const void* g, int64_t l
   hipStream_t s = (hipStream_t)stream;
   const bool f32 = out_fp32 != 0;
   float* ws = reinterpret_cast<float*>(workspace);
+  LRQ_FORMATS(gemm_t_nout, t, g, ldg, n_out, out, ldo, f32, ws, pl, s)
+}
+
+extern "C" int lrq_dequant_gemm_t_noalloc(const lrq_tensors* t, const void* g, int64_t ldg, int32_t n_out, void* out,
+                                          int64_t ldo, int32_t out_fp32, void* stream) {
+  int st = validate_tensors(t);
+  if (st) return st;
+  if (g == nullptr || out == nullptr) return LRQ_ERR_NULL;
+  if (n_out != 16 && n_out != 32) return LRQ_ERR_UNSUPPORTED;
+  if (ldg < n_out || ldo < n_out) return LRQ_ERR_SHAPE;
+  if (!aligned(g, 8) || (ldg % 4) != 0 || !aligned(out, out_fp32 ? 4 : 2)) return LRQ_ERR_ALIGN;
+  if ((t->flags & LRQ_FLAG_HADAMARD) || t->n_outlier > 0) return LRQ_ERR_UNSUPPORTED;
+  const GemmTPlan pl = gemm_t_plan(t->rows, t->hidden, t->bits, t->group, n_out);
+  if (pl.ws_bytes > (int64_t)LRQ_GEMM_T_SCRATCH_BYTES) return LRQ_ERR_WORKSPACE;
+  float* ws = nullptr;
+  st = scratch_on_current_device(&ws);
+  if (st) return st;
+  hipStream_t s = (hipStream_t)stream;
+  const bool f32 = out_fp32 != 0;
   LRQ_FORMATS(gemm_t_nout, t, g, ldg, n_out, out, ldo, f32, ws, pl, s)
 }
