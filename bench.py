@@ -15,6 +15,8 @@ value       = activation GB/s = 2*rows*hidden bytes / (encode + decode time per 
 timing      = exactly --warmup untimed steps, then exactly --steps timed steps between two HIP
               events on the launch stream (synchronised before and after); `settled` repeats
               the timed steps after --settle-seconds of sustained work, as a separate field
+cold_*      = the step's last kernel (decode / consumer) timed alone with its inputs HBM-cold:
+              a 1 GiB fill before each launch evicts the L2s and the 256 MB MALL
 roofline    = dominant kernel's algorithmic HBM bytes per launch / its mean duration
               (K back-to-back launches between HIP events on the launch stream, the queue
               pre-filled so host launch cost is not timed), against 8 TB/s; traffic =
@@ -55,6 +57,7 @@ def parse():
     ap.add_argument("--settle-seconds", type=float, default=2.0)
     ap.add_argument("--config", default="north_star")
     ap.add_argument("--nbuf", type=int, default=4)
+    ap.add_argument("--cold-steps", type=int, default=20, help="timed launches of the last kernel with HBM-cold inputs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=3.0, help="target seconds per CPU baseline run")
     return ap.parse_args()
@@ -442,6 +445,25 @@ def main():
         torch.cuda.synchronize()
         solo.append(a.elapsed_time(b) / args.steps)
 
+    # ---- the step's last kernel (decode / fused consumer) with its inputs HBM-cold: before each
+    # timed launch a 1 GiB fill evicts the L2s and the 256 MB MALL, so the codes the encode
+    # wrote are read from HBM (in the step they may still sit in the MALL)
+    cold = None
+    if args.cold_steps > 0:
+        last_name, last_fn = entries[-1][0], entries[-1][1]
+        scrub = torch.empty((1 << 29,), dtype=torch.bfloat16, device=dev)
+        cms = []
+        for i in range(args.cold_steps):
+            scrub.fill_(float(i % 7))
+            ca, cb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ca.record(stream)
+            last_fn(i % args.nbuf)
+            cb.record(stream)
+            torch.cuda.synchronize()
+            cms.append(ca.elapsed_time(cb))
+        del scrub
+        cold = (last_name, statistics.median(cms))
+
     kernels = {}
     for e, (name, _, alg, flops) in enumerate(entries):
         ms = [ev[e].elapsed_time(ev[e + 1]) for ev in evs]
@@ -451,6 +473,9 @@ def main():
                          "in_step_median_us": round(med * 1e3, 2),
                          "alg_GBs": round(alg / (mean * 1e-3) / 1e9, 1),
                          "hbm_frac": round(alg / (mean * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        if cold is not None and cold[0] == name:
+            kernels[name].update(cold_median_us=round(cold[1] * 1e3, 2),
+                                 cold_hbm_frac=round(alg / (cold[1] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
         if flops:
             tf = flops / (mean * 1e-3) / 1e12
             kernels[name].update(mfma_tflops=round(tf, 2), mfma_util_derived=round(tf / BF16_DENSE_TFLOPS, 5))

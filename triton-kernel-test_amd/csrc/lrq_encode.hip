@@ -283,16 +283,17 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
   // of UPW*G rows), passes through the region, and is read back in the operand layout before
   // the region receives block rb0.
   if constexpr (DMA) {
-    // V operands straight from global memory (L2-resident after the first workgroups) in the
-    // residual layout, transposed once for the projection; then the whole of block rb0.
+    // The whole of block rb0 first (HBM), then the V operands (L2-resident after the first
+    // workgroups) in the residual layout, transposed once for the projection: the memory
+    // pipeline serves a wave's requests in order, so X's requests leave before V's.
     const int rb = min(rb0, nrb - 1);
+#pragma unroll
+    for (int rd = 0; rd < Re::NR; ++rd) issue(0, rb, rd);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int uu = 0; uu < UPW; ++uu)
 #pragma unroll
       for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, ub + uu, N, NP, G), j, g, vop[uu][p]);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int rd = 0; rd < Re::NR; ++rd) issue(0, rb, rd);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int uu = 0; uu < UPW; ++uu)
