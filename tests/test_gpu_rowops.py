@@ -44,12 +44,35 @@ def test_softmax_bwd_compressed(pkg, dev, rows, n, rank, bits, group):
     print(f"[softmax] {rep}", flush=True)
 
 
-def test_softmax_bwd_unsupported_width(pkg, dev):
-    """A row that does not fit one workgroup (32 units) is refused, not computed wrongly."""
-    x = torch.rand(16, 4096, dtype=torch.float32).to(torch.bfloat16)
-    c = pkg.encode(x.to(dev), None, bits=4, group_size=64)
-    with pytest.raises(ValueError):
-        pkg.softmax_backward_compressed(c, x.to(dev))
+@pytest.mark.parametrize("rows,n,rank,bits,group", [
+    (100, 4096, 16, 4, 64),   # 32 units: four held per wave (reference bench width, softmax_backward.py:80)
+    (37, 8192, 16, 4, 64),    # 64 units, streamed unit by unit, ragged last row block
+    (64, 3072, 16, 4, 64),    # 24 units: not a multiple of the waves
+    (48, 1536, 0, 4, 64),     # 12 units, rank 0
+    (40, 4096, 32, 4, 64),    # rank 32
+    (70, 4096, 16, 8, 128),   # int8 / g128: 32 units
+    (30, 4096, 16, 4, 128),   # int4 / g128 (256-column units, loaded one at a time)
+    (16, 640, 16, 8, 64),     # 10 units: two waves hold two units, six hold one
+    (20, 384, 16, 4, 64),     # 3 units: fewer units than waves
+    (24, 3072, 16, 4, 128),   # int4 / g128, 12 units: two held per wave at most
+    (50, 2048, 16, 8, 64),    # int8 / g64, 32 units held, V operands parked in LDS
+])
+def test_softmax_bwd_compressed_wide(pkg, dev, rows, n, rank, bits, group):
+    """Rows of any width: the fused softmax backward against the oracle's decompress-then-op
+    on the device's codes."""
+    print(f"[softmax wide] rows={rows} n={n} rank={rank} bits={bits} g={group}", flush=True)
+    g = torch.Generator().manual_seed(50 + n + rank)
+    logits = torch.randn(rows, n, generator=g) / np.sqrt(128.0)
+    p = torch.softmax(logits, dim=-1).to(torch.bfloat16)
+    dp = (torch.randn(rows, n, generator=g) * 0.02).to(torch.bfloat16)
+    V = pkg.inputs.basis(n, rank, seed=9) if rank else None
+    c = pkg.encode(p.to(dev), V.to(dev) if V is not None else None, bits=bits, group_size=group)
+    ds = pkg.softmax_backward_compressed(c, dp.to(dev))
+    torch.cuda.synchronize()
+    ph = _xhat(c, V, bits, group)
+    ref = O.softmax_bwd(ph, O.bf16_to_f32(bits16(dp)))
+    rep = assert_fp_close(bits16(ds), ref, "fused softmax bwd (wide)", max_abs=1e-3)
+    print(f"[softmax wide] {rep}", flush=True)
 
 
 @pytest.mark.parametrize("rows,hidden,rank,n_out,out_dtype,bits,group", [

@@ -126,6 +126,210 @@ __global__ __launch_bounds__(NW * 64) void k_softmax_bwd(
   }
 }
 
+// Two-sweep softmax backward for rows of any number of units (rows too wide for one pass in
+// a workgroup).  Grid: ceil(row blocks / RBW) workgroups of NW waves; wave w takes units
+// w, w + NW, ... of the row.  Sweep 1 reconstructs P = bf16(decode) unit by unit and sums
+// P * dP per row (quad swaps, then LDS across the waves); sweep 2 reconstructs P again and
+// writes dS = P (dP - sum).  The row sum is taken in a fixed order (lane pairs, wave order),
+// so dS does not depend on timing.  Rows past the end repeat the last row (identical stores).
+//   HOLD > 0 (rows of NW .. NW*HOLD units, rank 0 or 16): every wave requests all of its units'
+//            codes, qparams and dP of the row block at once and keeps them in registers for
+//            both sweeps, so they are read once; the units' V operands are parked in the
+//            wave's LDS slots at the start (operand order: one conflict-free 512-byte read
+//            per operand) and read from there at each use.
+//   HOLD = 0 (any width): each unit's inputs, V operands included, are requested one unit
+//            ahead (a clamped repeat of the last unit at the end, so no load sits under a
+//            branch) and read again in sweep 2.
+template <int BITS, int G, int R, int NW, int HOLD>
+struct Smx2s {
+  static constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1;
+  static constexpr int VSLOT = NP * (G / 16) * RT * 64 * 8;  // one unit's V operands in LDS
+  static constexpr size_t LDS = (HOLD > 0 && R > 0) ? (size_t)NW * HOLD * VSLOT : 0;
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+};
+
+template <int BITS, int G, int R, int NW, int HOLD>
+__global__ __launch_bounds__(NW * 64) void k_softmax_2s(
+    const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
+    const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
+    const uint16_t* __restrict__ dp, int64_t lddp, uint16_t* __restrict__ ds, int64_t ldds, int RBW) {
+  using Sm = Smx2s<BITS, G, R, NW, HOLD>;
+  constexpr int NP = Sm::NP, RT = Sm::RT, E = G / 4;
+  static_assert(HOLD == 0 || R <= 16, "held units keep one rank tile of V operands");
+  __shared__ float red[NW][16];
+  extern __shared__ __attribute__((aligned(16))) unsigned char vsm[];  // HOLD, R > 0: [NW][HOLD][VSLOT]
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int nrb = (M + 15) / 16;
+  const int units = N / (G * NP);
+  const int nmine = (units - w + NW - 1) / NW;  // units of this wave (0 when units < NW and w >= units)
+  struct In {
+    u32x4 cb[G / 64];
+    uint32_t qp[NP];
+    u32x4 d[NP][G / 32];
+  };
+  using Vop = u32x2[NP][G / 16][RT];
+  auto load = [&](In& in, int64_t row, int u) {
+#pragma unroll
+    for (int i = 0; i < G / 64; ++i) in.cb[i] = ld16_stream(codes + row * ldc + u * G + E * g + 16 * i);
+    if constexpr (NP == 2) {
+      const u32x2 q = ld8(qparams + row * ldq + u * 4);
+      in.qp[0] = q[0];
+      in.qp[1] = q[1];
+    } else {
+      in.qp[0] = ld4(qparams + row * ldq + u * 2);
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int k = 0; k < G / 32; ++k) {
+        const uint16_t* a = dp + row * lddp + unit_base(p, u, N, NP, G) + E * g + 8 * k;
+        in.d[p][k] = HOLD > 0 ? ld16_stream(a) : ld16(a);
+      }
+  };
+  auto load_v = [&](Vop& v, int u) {
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, u, N, NP, G), j, g, v[p]);
+    }
+  };
+  // the LDS slot of held unit h of this wave; operand (p, q, t) is 64 lanes x 8 bytes
+  auto vslot = [&](int h) { return reinterpret_cast<u32x2*>(vsm + ((size_t)w * HOLD + h) * Sm::VSLOT); };
+  auto read_v = [&](Vop& v, int h) {
+    if constexpr (R > 0) {
+      const u32x2* sl = vslot(h);
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int q = 0; q < G / 16; ++q)
+#pragma unroll
+          for (int t = 0; t < RT; ++t) v[p][q][t] = sl[((p * (G / 16) + q) * RT + t) * 64 + lane];
+    }
+  };
+  // sweep 0: part += P * dP over the unit's lane columns; sweep 1: dS = P (dP - sum)
+  auto work = [&](const In& cur, const Vop& v, int u, int sweep, const u32x2* lop, int64_t row, float& part,
+                  float sum) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      float pv[E], dv[E];
+      reconstruct_plane<BITS, G, R>(cur.cb, cur.qp[p], p, v[p], lop, pv);
+#pragma unroll
+      for (int k = 0; k < G / 32; ++k) unpack8(cur.d[p][k], dv + 8 * k);
+      if (sweep == 0) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) part = __builtin_fmaf(bf16_roundtrip(pv[e]), dv[e], part);
+      } else {
+        float o[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) o[e] = bf16_roundtrip(pv[e]) * (dv[e] - sum);
+        const int c0 = unit_base(p, u, N, NP, G) + E * g;
+#pragma unroll
+        for (int k = 0; k < G / 32; ++k) st16(ds + row * ldds + c0 + 8 * k, pack8(o + 8 * k));
+      }
+    }
+  };
+  // the row's four lanes, then the NW waves in order (through LDS)
+  auto row_sum = [&](float part) {
+    float a = part, c = part;
+    swap32(a, c);
+    part = a + c;
+    a = part, c = part;
+    swap16(a, c);
+    part = a + c;
+    if (g == 0) red[w][j] = part;
+    lds_barrier();
+    float sum = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2) sum += red[w2][j];
+    lds_barrier();  // every wave has read red before the next row block rewrites it
+    return sum;
+  };
+  if constexpr (HOLD > 0 && R > 0) {
+    // park this wave's V operands (the host launches this form only when 1 <= nmine <= HOLD);
+    // a wave reads back only the slots it wrote, in order, so no barrier is needed
+#pragma unroll
+    for (int h = 0; h < HOLD; ++h) {
+      if (h < nmine) {
+        Vop v;
+        load_v(v, w + h * NW);
+        u32x2* sl = vslot(h);
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+          for (int q = 0; q < G / 16; ++q)
+#pragma unroll
+            for (int t = 0; t < RT; ++t) sl[((p * (G / 16) + q) * RT + t) * 64 + lane] = v[p][q][t];
+      }
+    }
+  }
+  const int rb_end = min(nrb, (blockIdx.x + 1) * RBW);
+#pragma unroll 1
+  for (int rb = blockIdx.x * RBW; rb < rb_end; ++rb) {
+    const int64_t row = min(rb * 16 + j, M - 1);
+    u32x2 lop[RT];
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t) lop[t] = ld8(Lin + row * ldl + 16 * t + 4 * g);
+    }
+    if constexpr (HOLD > 0) {
+      In in[HOLD];
+#pragma unroll
+      for (int h = 0; h < HOLD; ++h) load(in[h], row, w + min(h, nmine - 1) * NW);
+      float part = 0.f;
+#pragma unroll
+      for (int h = 0; h < HOLD; ++h) {
+        if (h < nmine) {
+          Vop v;
+          read_v(v, h);
+          work(in[h], v, w + h * NW, 0, lop, row, part, 0.f);
+        }
+      }
+      const float sum = row_sum(part);
+#pragma unroll
+      for (int h = 0; h < HOLD; ++h) {
+        if (h < nmine) {
+          Vop v;
+          read_v(v, h);
+          work(in[h], v, w + h * NW, 1, lop, row, part, sum);
+        }
+      }
+    } else {
+      float part = 0.f, sum = 0.f;
+#pragma unroll 1
+      for (int sweep = 0; sweep < 2; ++sweep) {
+        if (nmine > 0) {
+          // units of 256 columns are loaded right before use (two in flight would spill)
+          constexpr bool DB = G * NP <= 128;
+          In in[DB ? 2 : 1];
+          Vop v[DB ? 2 : 1];
+          if constexpr (DB) {
+            load(in[0], row, w);
+            load_v(v[0], w);
+          }
+#pragma unroll 1
+          for (int i = 0; i < nmine; i += 2) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              if (i + h >= nmine) break;  // wave-uniform
+              const int u = w + (i + h) * NW;
+              if constexpr (DB) {
+                const int un = w + min(i + h + 1, nmine - 1) * NW;
+                load(in[h ^ 1], row, un);
+                load_v(v[h ^ 1], un);
+              } else {
+                load(in[0], row, u);
+                load_v(v[0], u);
+              }
+              work(in[DB ? h : 0], v[DB ? h : 0], u, sweep, lop, row, part, sum);
+            }
+          }
+        }
+        if (sweep == 0) sum = row_sum(part);
+      }
+    }
+  }
+}
+
 // Row-persistent softmax backward (one workgroup per CU; wave w owns unit w of every row, so
 // a workgroup holds whole rows).  dP moves as whole row segments straight from HBM into an LDS
 // tile (two tiles, block b in tile b&1), is read back in the MFMA layout, and dS is written
@@ -744,8 +948,36 @@ static int softmax_rows_launch(const lrq_tensors* t, const void* dp, int64_t ldd
   return LRQ_OK;
 }
 
+// Any other row width: the two-sweep kernel, about four workgroups per CU.
+template <int BITS, int G, int R>
+static int softmax_2s_launch(const lrq_tensors* t, const void* dp, int64_t lddp, void* ds, int64_t ldds,
+                             hipStream_t s) {
+  constexpr int NW = 8;
+  // units held in registers per wave: four units of 128 columns, two of 256 (rank 32: none)
+  constexpr int HOLD = R > 16 ? 0 : G * (8 / BITS) <= 128 ? 4 : 2;
+  using Sm = Smx2s<BITS, G, R, NW, HOLD>;
+  const int M = (int)t->rows, N = (int)t->hidden;
+  const int64_t units = t->hidden / ((int64_t)G * (8 / BITS));
+  const int nrb = (M + 15) / 16;
+  const int wgs = std::max(1, std::min(nrb, cu_count() * 4));
+  const int rbw = (nrb + wgs - 1) / wgs;
+  auto go = [&](auto kern, size_t shm) {
+    if (shm > 64 * 1024) {
+      const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+      if (e != hipSuccess) return (int)e;
+    }
+    return launch(kern, dim3((nrb + rbw - 1) / rbw), dim3(NW * 64), shm, s, (const uint8_t*)t->codes, t->ld_codes,
+                  (const uint16_t*)t->qparams, t->ld_qp, (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N,
+                  (const uint16_t*)dp, lddp, (uint16_t*)ds, ldds, rbw);
+  };
+  if constexpr (HOLD > 0) {
+    if (units >= NW && units <= (int64_t)NW * HOLD) return go(k_softmax_2s<BITS, G, R, NW, HOLD>, Sm::LDS);
+  }
+  return go(k_softmax_2s<BITS, G, R, NW, 0>, 0);
+}
+
 // One pass needs the whole row in one workgroup: 4, 8 or 16 units (one per wave).  Rows of
-// whole 1 KB chunks take the row-persistent kernel.
+// whole 1 KB chunks take the row-persistent kernel; every other width the two-sweep kernel.
 template <int BITS, int G, int R>
 static int softmax_units(const lrq_tensors* t, const void* dp, int64_t lddp, void* ds, int64_t ldds, hipStream_t s) {
   const int64_t units = t->hidden / ((int64_t)G * (8 / BITS));
@@ -763,7 +995,7 @@ static int softmax_units(const lrq_tensors* t, const void* dp, int64_t lddp, voi
     case 4: return softmax_launch<BITS, G, R, 4, 1>(t, dp, lddp, ds, ldds, s);
     case 8: return softmax_launch<BITS, G, R, 8, 1>(t, dp, lddp, ds, ldds, s);
     case 16: return softmax_launch<BITS, G, R, 16, 1>(t, dp, lddp, ds, ldds, s);
-    default: return LRQ_ERR_UNSUPPORTED;
+    default: return softmax_2s_launch<BITS, G, R>(t, dp, lddp, ds, ldds, s);
   }
 }
 

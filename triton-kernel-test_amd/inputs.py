@@ -55,6 +55,9 @@ CONFIGS = {
     "c4": Config("c4", 16384, 5120, 16, 4, 64, n_outlier=16, outlier_scale=30.0, hadamard=True, seed=4),
     "c5": Config("c5", 2 * 32 * 2048, 2048, 16, 4, 64, consumer="softmax", seed=5,
                  softmax_shape=(2, 32, 2048, 2048)),
+    # config 5's recipe at the reference softmax bench's widest rows (softmax_backward.py:80, N = 4096):
+    # 4 of the 64 (batch, head) pairs of [2, 32, 4096, 4096], i.e. 16384 rows of 4096 (two-sweep kernel)
+    "c5w": Config("c5w", 4 * 4096, 4096, 16, 4, 64, consumer="softmax", seed=8, softmax_shape=(2, 32, 4096, 4096)),
     # the LoRA layer's backward from the north-star format: x A and dA = x^T (dy B^T)
     "lora": Config("lora", 16384, 4096, 16, 4, 64, n_outlier=8, outlier_scale=20.0, consumer="lora", seed=6),
     # the reference's own format (legacy): rank-16 factors, 2-bit symmetric codes (the system
