@@ -41,6 +41,22 @@ def ulp_diff_bf16(a_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
     return np.abs(ordered(a_bits) - ordered(b_bits))
 
 
+def assert_decode_close(dev_bits: np.ndarray, ref_bits: np.ndarray, what: str, frac=1e-3, abs_tol=2.0 ** -20) -> dict:
+    """Decoded bf16 vs the oracle's: at most one bf16 ulp apart, on at most ``frac`` of the
+    elements, except where the reconstruction cancels to a tiny value.  The MFMA forms
+    code*scale + zero + L V^T (terms of order one) in fp32 accumulation, which can sit a few
+    2^-24-sized steps from the exact sum; at a result near zero that is several bf16 ulps, so
+    there the bar is an absolute one (abs_tol, far below any quantisation step)."""
+    d = ulp_diff_bf16(dev_bits, ref_bits)
+    a = O.bf16_to_f32(dev_bits).astype(np.float64)
+    b = O.bf16_to_f32(ref_bits).astype(np.float64)
+    far = (d > 1) & (np.abs(a - b) > abs_tol)
+    rep = dict(max_ulp=int(d.max()) if d.size else 0, frac_ulp=float((d > 0).mean()) if d.size else 0.0,
+               n_cancel=int(((d > 1) & ~far).sum()), n_far=int(far.sum()))
+    assert rep["n_far"] == 0 and rep["frac_ulp"] <= frac, f"{what}: {rep}"
+    return rep
+
+
 def code_mismatch_report(gpu_packed: np.ndarray, ref: dict, bits: int) -> dict:
     """Compare packed codes with the oracle's; classify mismatches.
 

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import oracle as O
-from parity import (assert_codes, assert_fp_close, bits16, code_mismatch_report, f16, from_bits,
+from parity import (assert_codes, assert_decode_close, assert_fp_close, bits16, code_mismatch_report, f16, from_bits,
                     ulp_diff_bf16)
 
 pytestmark = pytest.mark.gpu
@@ -32,12 +32,12 @@ def _check_encode(pkg, dev, x, V, bits, group, twopass=False, outlier_idx=None):
     rep = {}
     if V is not None:
         lg = bits16(c.L)
-        ref_full = O.encode(xb, vb, bits, group)
+        ref_full = O.encode(xb, vb, bits, group, outlier_idx=outlier_idx)
         d = ulp_diff_bf16(lg, ref_full["L"])
         rep["L_flips"] = int((d > 0).sum())
         assert d.max() <= 1, f"L differs by {d.max()} ulps"
         assert rep["L_flips"] <= max(2, 1e-3 * d.size), rep
-        ref = O.encode(xb, vb, bits, group, l_override=lg)
+        ref = O.encode(xb, vb, bits, group, outlier_idx=outlier_idx, l_override=lg)
     else:
         ref_full = ref = O.encode(xb, None, bits, group, outlier_idx=outlier_idx)
     codes = c.codes.cpu().numpy()
@@ -82,6 +82,37 @@ def test_encode_decode_formats(pkg, dev, rows, hidden, rank, bits, group):
                       f16(c.scale), f16(c.zero), bits, group)
     d = ulp_diff_bf16(bits16(xh), ref_xh)
     assert d.max() <= 1 and (d > 0).mean() <= 1e-3, (d.max(), (d > 0).mean())
+
+
+@pytest.mark.parametrize("rows,hidden,rank,bits,group,k", [
+    (100, 4096, 16, 4, 64, 41),   # row-staged single pass (4 units per wave), config 3's channel count
+    (5000, 4096, 16, 4, 64, 8),   # several row blocks per workgroup, ragged
+    (64, 2048, 16, 4, 64, 9),     # row-staged, 2 units per wave (slice staged through registers)
+    (64, 4096, 32, 4, 64, 41),    # rank 32: the column-slab passes
+    (72, 11008, 32, 4, 64, 20),   # config 2's format
+    (40, 4096, 16, 8, 128, 41),   # int8 / g128 with rank 16: the slab passes
+    (33, 1536, 16, 4, 64, 5),     # the slab passes (no single-pass kernel for 12 units)
+])
+def test_outlier_channels_with_low_rank(pkg, dev, rows, hidden, rank, bits, group, k):
+    """Outlier channels combined with the rank-r extraction: the channels are zeroed before the
+    projection and kept as fp16 side columns (low_rank_extraction_fuse_compression_quantization.py:66-82
+    subtracts l@r and splits outliers in one kernel).  Encode, decode and a fused consumer
+    against the oracle."""
+    print(f"[outliers+rank] rows={rows} hidden={hidden} rank={rank} int{bits}/g{group} k={k}", flush=True)
+    x = pkg.inputs.activation(rows, hidden, n_outlier=k, outlier_scale=50.0, seed=rows + k)
+    V = pkg.inputs.basis(hidden, rank, seed=k)
+    idx = O.topk_channels(O.colmax_abs(bits16(x)), k)
+    c, ref, rep = _check_encode(pkg, dev, x, V, bits, group, outlier_idx=idx)
+    print(f"[outliers+rank] {rep}", flush=True)
+    xh = pkg.decode(c)
+    dy = pkg.inputs.gradient((rows, hidden), 0.02, seed=k)
+    dx = pkg.silu_backward_compressed(c, dy.to(dev))
+    torch.cuda.synchronize()
+    ref_xh = O.decode(bits16(c.L), bits16(V), c.codes.cpu().numpy(), f16(c.scale), f16(c.zero), bits, group,
+                      side=f16(c.side), idx=idx)
+    print(f"[outliers+rank] decode {assert_decode_close(bits16(xh), ref_xh, 'decode, outliers+rank')}", flush=True)
+    assert np.array_equal(bits16(xh)[:, idx], ref_xh[:, idx])  # the side columns come back exactly
+    assert_fp_close(bits16(dx), O.silu_bwd(O.bf16_to_f32(ref_xh), O.bf16_to_f32(bits16(dy))), "silu, outliers+rank")
 
 
 @pytest.mark.parametrize("rows,hidden,rank,bits,group", [(100, 4096, 16, 4, 64), (64, 5120, 16, 4, 64)])

@@ -758,8 +758,11 @@ static int decode_launch(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
   for (int64_t ldb : {t->ld_codes, 2 * t->ld_qp, 2 * t->ld_L, 2 * epi.in_ld(), 2 * epi.out_ld()})
     off32 = off32 && 16 * ldb < ((int64_t)1 << 31);
   if (off32 && t->n_outlier == 0) return decode_rows_launch<BITS, G, R, false>(t, s, epi);
-  if constexpr (R == 0) {
-    if (off32 && t->n_outlier <= kSideMax) return decode_rows_launch<BITS, G, R, true>(t, s, epi);
+  if (off32 && t->n_outlier <= kSideMax) {
+    // the row kernel's tiles, side slots and outlier tables may not fit in LDS (a consumer at
+    // rank > 0): then the tile kernel below
+    const int st = decode_rows_launch<BITS, G, R, true>(t, s, epi);
+    if (st != LRQ_ERR_UNSUPPORTED) return st;
   }
   const int64_t units = t->hidden / (G * NP), nrb = (t->rows + 15) / 16;
   const int64_t wgs = ((nrb + BIG - 1) / BIG) * ((units + NW - 1) / NW);

@@ -213,11 +213,16 @@ struct RowsEnc {
   static_assert(LDS <= 160 * 1024, "LDS budget");
 };
 
-template <int BITS, int G, int R, int NW, int UPW>
+// OUTL: outlier channels.  The V operand rows of outlier columns are zeroed once, so the
+// projection is that of Y with those columns zeroed (the same products and sums) and their
+// residuals are zeroed before the group statistics; their bf16 values go to the fp16 side
+// columns from the slice in LDS.  LDS: Re::LDS + N/32 mask words + N slot entries.
+template <int BITS, int G, int R, int NW, int UPW, bool OUTL>
 __global__ __launch_bounds__(NW * 64) void k_encode_rows(
     const uint16_t* __restrict__ X, int64_t ldx, int M, int N, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ Lout, int64_t ldl, uint8_t* __restrict__ codes, int64_t ldc,
-    uint16_t* __restrict__ qparams, int64_t ldq, int RBW) {
+    uint16_t* __restrict__ qparams, int64_t ldq, int RBW, const int32_t* __restrict__ oidx, int nout,
+    uint16_t* __restrict__ side, int64_t ldside) {
   using Re = RowsEnc<BITS, G, R, NW, UPW>;
   constexpr int NP = Re::NP, CPG = G / 32, RT = Re::RT, E = G / 4;
   static_assert(NP == 2 && (UPW == 2 || UPW == 4), "the qparams gather below is written for 2 planes x 2 or 4 units");
@@ -231,6 +236,64 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
   if (rb0 >= nrb) return;  // whole workgroup (no barrier reached)
   const int nblk = min(RBW, nrb - rb0);
   const int ub = w * UPW;  // first unit of this wave
+  uint32_t* colmask = reinterpret_cast<uint32_t*>(shm + Re::LDS);  // OUTL: N/32 words
+  int16_t* oslot = reinterpret_cast<int16_t*>(colmask + N / 32);   // OUTL: N entries
+  if constexpr (OUTL) {
+    for (int i = threadIdx.x; i < N / 32; i += NW * 64) colmask[i] = 0u;
+    for (int i = threadIdx.x; i < N; i += NW * 64) oslot[i] = -1;
+    __syncthreads();
+    for (int k = threadIdx.x; k < nout; k += NW * 64) {
+      const int c = oidx[k];
+      if (c >= 0 && c < N) {
+        atomicOr(&colmask[c >> 5], 1u << (c & 31));
+        oslot[c] = (int16_t)k;
+      }
+    }
+    __syncthreads();
+  }
+  // zero the V operand rows of outlier columns (lane (j, g) of operand q holds V row
+  // vrow_res(base, j, q))
+  auto mask_vops = [&](u32x2 (&vo)[UPW][NP][G / 16][RT]) {
+    if constexpr (OUTL) {
+#pragma unroll
+      for (int uu = 0; uu < UPW; ++uu)
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+          for (int q = 0; q < G / 16; ++q) {
+            const int c = vrow_res<G>(unit_base(p, ub + uu, N, NP, G), j, q);
+            const bool z = (colmask[c >> 5] >> (c & 31)) & 1u;
+#pragma unroll
+            for (int t = 0; t < RT; ++t) vo[uu][p][q][t] = z ? u32x2{0u, 0u} : vo[uu][p][q][t];
+          }
+    }
+  };
+  // side columns of the wave's units, read from the slice in the region (lanes of quarter 0
+  // store row j; rows past the end repeat the last row)
+  auto side_store = [&](int rb, int row) {
+    if constexpr (OUTL) {
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc(side + (int64_t)rb * 16 * ldside, (short)0, (int)(16 * ldside * 2), 0x00020000);
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const int cb = unit_base(p, ub, N, NP, G);  // the wave's UPW*G contiguous columns of plane p
+#pragma unroll 1
+        for (int wd = 0; wd < UPW * G / 32; ++wd) {
+          uint32_t bits = __builtin_amdgcn_readfirstlane(colmask[(cb >> 5) + wd]);
+          while (bits != 0u) {
+            const int e = __builtin_ctz(bits);
+            bits &= bits - 1u;
+            const int cl = 32 * wd + e;  // column within the wave's range
+            const int k = oslot[cb + cl];
+            const uint32_t v = *reinterpret_cast<const uint16_t*>(region + j * Re::PITCH + p * Re::PIECE + cl * 2);
+            const uint16_t h = (uint16_t)f16_bits(__uint_as_float(v << 16));
+            __builtin_amdgcn_raw_buffer_store_b16(h, rs, g == 0 ? (uint32_t)(((row - rb * 16) * ldside + k) * 2) : 0x7ffffff0u,
+                                                  0, 0);
+          }
+        }
+      }
+    }
+  };
 
   // With one row per load instruction (RPL == 1) a load's 1 KB lands contiguously in the
   // region, so it goes straight from HBM to LDS (no staging registers); the registers saved
@@ -295,6 +358,7 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
 #pragma unroll
       for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, ub + uu, N, NP, G), j, g, vop[uu][p]);
     __builtin_amdgcn_sched_barrier(0);
+    mask_vops(vop);
 #pragma unroll
     for (int uu = 0; uu < UPW; ++uu)
 #pragma unroll
@@ -327,6 +391,7 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
             const int vr = uu * G + vrow_res<G>(0, j, q);  // V row within the plane's range
             vop[uu][p][q][t] = *reinterpret_cast<const u32x2*>(region + p * VB + vr * R * 2 + 32 * t + 8 * g);
           }
+    mask_vops(vop);
     // the region is rewritten below: every read above must have returned
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_sched_barrier(0);
@@ -366,6 +431,7 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
 #pragma unroll
         for (int k = 0; k < CPG; ++k)
           x[uu][p][k] = *reinterpret_cast<const u32x4*>(region + j * Re::PITCH + p * Re::PIECE + (uu * G + E * g + 8 * k) * 2);
+    side_store(rb, row);
     if constexpr (DMA) {
       // the region may be overwritten once every read of the slice has returned
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
@@ -426,7 +492,10 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
     uint32_t qp[UPW];
 #pragma unroll
     for (int uu = 0; uu < UPW; ++uu) {
-      qp[uu] = quant_unit_regs<BITS, G, R>(x[uu], vop[uu], lopn, ub + uu, g, crow);
+      if constexpr (OUTL)
+        qp[uu] = quant_unit_core<BITS, G, R>(x[uu], vop[uu], lopn, colmask, ub + uu, N, g, crow);
+      else
+        qp[uu] = quant_unit_regs<BITS, G, R>(x[uu], vop[uu], lopn, ub + uu, g, crow);
       if (uu == 1 && next) {
         __builtin_amdgcn_sched_barrier(0);
         land(1, 1);
@@ -595,13 +664,15 @@ __global__ __launch_bounds__(256) void k_quant(
 // barrier): global wave gw takes wave column gw % nwc (units 2*(gw % nwc) .. +1) and row
 // range gw / nwc; its slice streams through a private LDS region as in k_encode_rows, with
 // the next block's loads (and its L rows) in flight during the current block's quantisation.
-template <int R, bool ROT>
+template <int R, bool ROT, bool OUTL>
 __global__ __launch_bounds__(512) void k_project_slab(const uint16_t* __restrict__ X, int64_t ldx, int M, int N,
                                                       const uint16_t* __restrict__ Vt,
-                                                      unsigned char* __restrict__ part, int64_t ldp, int RBW) {
+                                                      unsigned char* __restrict__ part, int64_t ldp, int RBW,
+                                                      const int32_t* __restrict__ oidx, int nout) {
   constexpr int RT = R / 16, NW = 8, CW = 256, PITCH = CW * 2 + 16, NLD = 8;
   __shared__ __attribute__((aligned(16))) unsigned char shm[NW * 16 * PITCH];
   __shared__ f32x4 red[2][NW][RT][64];
+  extern __shared__ uint32_t pmask[];  // OUTL: N/32 words, outlier columns
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
   const int nrb = (M + 15) / 16;
@@ -629,6 +700,28 @@ __global__ __launch_bounds__(512) void k_project_slab(const uint16_t* __restrict
       const int c = c0 + 32 * k + 8 * g;
       vt[k][t] = c < N ? ld16(Vt + (int64_t)(16 * t + j) * N + c) : u32x4{0u, 0u, 0u, 0u};
     }
+  if constexpr (OUTL) {
+    // outlier columns meet zero V^T operands: the projection of Y with those columns zeroed
+    for (int i = threadIdx.x; i < N / 32; i += 512) pmask[i] = 0u;
+    __syncthreads();
+    for (int k = threadIdx.x; k < nout; k += 512) {
+      const int c = oidx[k];
+      if (c >= 0 && c < N) atomicOr(&pmask[c >> 5], 1u << (c & 31));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < CW / 32; ++k) {
+      const int c = c0 + 32 * k + 8 * g;  // 8 columns inside one mask word
+      const uint32_t b8 = c < N ? (pmask[c >> 5] >> (c & 31)) & 0xffu : 0u;
+#pragma unroll
+      for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint32_t keep = (((b8 >> (2 * d)) & 1u) ? 0u : 0x0000ffffu) | (((b8 >> (2 * d + 1)) & 1u) ? 0u : 0xffff0000u);
+          vt[k][t][d] &= keep;
+        }
+    }
+  }
   // load i: rows 2i, 2i+1 of the block, lane l -> row 2i + l/32, bytes (l%32)*16 of the slice
   // (clamped to column N - 8 past the end: those columns meet zero operands)
   const int lr = lane >> 5;
@@ -910,19 +1003,37 @@ static int launch_persist(const lrq_tensors* t, const void* x, int64_t ldx, hipS
 }
 
 // k_encode_rows: one workgroup per CU, each walking ceil(row blocks / CUs) consecutive blocks.
-template <int BITS, int G, int R, int UPW>
+template <int BITS, int G, int R, int UPW, bool OUTL>
 static int launch_rows(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s) {
   constexpr int NW = 8;
   using Re = RowsEnc<BITS, G, R, NW, UPW>;
-  auto kern = k_encode_rows<BITS, G, R, NW, UPW>;
-  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)Re::LDS);
+  auto kern = k_encode_rows<BITS, G, R, NW, UPW, OUTL>;
+  const size_t shm = Re::LDS + (OUTL ? (size_t)(t->hidden / 32) * 4 + (size_t)t->hidden * 2 : 0);
+  const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+  if (e != hipSuccess) return (int)e;
   const int64_t nrb = (t->rows + 15) / 16, cus = cu_count();
   const int rbw = (int)((nrb + cus - 1) / cus);
   const int64_t wgs = (nrb + rbw - 1) / rbw;
-  LRQ_TRY(launch(kern, dim3((unsigned)wgs), dim3(NW * 64), Re::LDS, s, (const uint16_t*)x, ldx, (int)t->rows,
-                     (int)t->hidden, (const uint16_t*)t->V, (uint16_t*)t->L, t->ld_L, (uint8_t*)t->codes,
-                     t->ld_codes, (uint16_t*)t->qparams, t->ld_qp, rbw));
+  LRQ_TRY(launch(kern, dim3((unsigned)wgs), dim3(NW * 64), shm, s, (const uint16_t*)x, ldx, (int)t->rows,
+                 (int)t->hidden, (const uint16_t*)t->V, (uint16_t*)t->L, t->ld_L, (uint8_t*)t->codes, t->ld_codes,
+                 (uint16_t*)t->qparams, t->ld_qp, rbw, t->outlier_idx, (int)t->n_outlier, (uint16_t*)t->side,
+                 t->ld_side));
   return LRQ_OK;
+}
+
+// The row-staged kernel with or without outlier channels (the side columns' 16-row stride must
+// fit a buffer range and the mask and slot tables the LDS).
+template <int BITS, int G, int R, int UPW>
+static int launch_rows_any(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s, int* status) {
+  if (t->n_outlier == 0) {
+    *status = launch_rows<BITS, G, R, UPW, false>(t, x, ldx, s);
+    return 1;
+  }
+  using Re = RowsEnc<BITS, G, R, 8, UPW>;
+  if (t->n_outlier > 32767 || (int64_t)16 * t->ld_side * 2 >= ((int64_t)1 << 31)) return 0;
+  if (Re::LDS + (size_t)(t->hidden / 32) * 4 + (size_t)t->hidden * 2 > 160 * 1024) return 0;
+  *status = launch_rows<BITS, G, R, UPW, true>(t, x, ldx, s);
+  return 1;
 }
 
 // Returns 1 and launches when a single-pass kernel exists for this shape, else 0.
@@ -937,29 +1048,29 @@ static int encode_persist_dispatch(const lrq_tensors* t, const void* x, int64_t 
     constexpr bool wide_ok = G * NP <= 128;
     const int64_t units = t->hidden / ((int64_t)G * NP);
     switch (units) {
-      case 8: *status = launch_persist<BITS, G, R, 4, 2, true>(t, x, ldx, s); return 1;
+      case 8:
+        if (t->n_outlier > 0) return 0;
+        *status = launch_persist<BITS, G, R, 4, 2, true>(t, x, ldx, s);
+        return 1;
       case 16:
         // row-staged kernel (8 waves x 2 units; 16-byte qparams stores per row)
         if constexpr (BITS == 4 && G == 64) {
-          if (t->ld_qp % 8 == 0 && aligned(t->qparams, 16)) {
-            *status = launch_rows<BITS, G, R, 2>(t, x, ldx, s);
-            return 1;
-          }
+          if (t->ld_qp % 8 == 0 && aligned(t->qparams, 16)) return launch_rows_any<BITS, G, R, 2>(t, x, ldx, s, status);
         }
+        if (t->n_outlier > 0) return 0;
         *status = launch_persist<BITS, G, R, 8, 2, true>(t, x, ldx, s);
         return 1;
       case 32:
         // row-staged kernel (8 waves x 4 units)
         if constexpr (BITS == 4 && G == 64) {
-          if (t->ld_qp % 8 == 0 && aligned(t->qparams, 16)) {
-            *status = launch_rows<BITS, G, R, 4>(t, x, ldx, s);
-            return 1;
-          }
+          if (t->ld_qp % 8 == 0 && aligned(t->qparams, 16)) return launch_rows_any<BITS, G, R, 4>(t, x, ldx, s, status);
         }
+        if (t->n_outlier > 0) return 0;
         *status = launch_persist<BITS, G, R, 16, 2, true>(t, x, ldx, s);
         return 1;
       case 40:
         if constexpr (wide_ok) {
+          if (t->n_outlier > 0) return 0;
           *status = launch_persist<BITS, G, R, 8, 5, false>(t, x, ldx, s);
           return 1;
         }
@@ -984,7 +1095,7 @@ static int encode_slabs(const lrq_tensors* t, const void* x, int64_t ldx, hipStr
   if (units % 2 != 0 || N % 32 != 0) return 0;
   // rotated input: every wave's columns start on a 128-column block of their plane
   if (ROT && (outl || (N / NP) % 128 != 0 || (2 * G) % 128 != 0 || (NP == 2 && G == 128))) return 0;
-  if (outl && (R > 0 || t->n_outlier > 32767 || t->side == nullptr || t->outlier_idx == nullptr)) return 0;
+  if (outl && (t->n_outlier > 32767 || t->side == nullptr || t->outlier_idx == nullptr)) return 0;
   if (NP == 2 ? (t->ld_qp % 8 != 0 || !aligned(t->qparams, 16)) : (t->ld_qp % 4 != 0 || !aligned(t->qparams, 8))) return 0;
   if ((int64_t)16 * t->ld_qp * 2 >= ((int64_t)1 << 31)) return 0;
   if (outl && (int64_t)16 * t->ld_side * 2 >= ((int64_t)1 << 31)) return 0;
@@ -999,8 +1110,12 @@ static int encode_slabs(const lrq_tensors* t, const void* x, int64_t ldx, hipStr
     // pass 1: about one workgroup per CU over (row groups, slabs)
     const int per1 = std::max(1, cus / nslab);
     const int rbw1 = (nrb + per1 - 1) / per1;
-    int st = launch((k_project_slab<R, ROT>), dim3((nrb + rbw1 - 1) / rbw1, nslab), dim3(512), 0, s,
-                    (const uint16_t*)x, ldx, M, N, (const uint16_t*)t->Vt, (unsigned char*)t->codes, ldp, rbw1);
+    int st = outl ? launch((k_project_slab<R, ROT, true>), dim3((nrb + rbw1 - 1) / rbw1, nslab), dim3(512),
+                           (size_t)(N / 32) * 4, s, (const uint16_t*)x, ldx, M, N, (const uint16_t*)t->Vt,
+                           (unsigned char*)t->codes, ldp, rbw1, t->outlier_idx, (int)t->n_outlier)
+                  : launch((k_project_slab<R, ROT, false>), dim3((nrb + rbw1 - 1) / rbw1, nslab), dim3(512), 0, s,
+                           (const uint16_t*)x, ldx, M, N, (const uint16_t*)t->Vt, (unsigned char*)t->codes, ldp,
+                           rbw1, nullptr, 0);
     if (st) { *status = st; return 1; }
     const int64_t nred = (int64_t)M * (R / 4);
     st = launch((k_reduce_slabs<R>), dim3((unsigned)((nred + 255) / 256)), dim3(256), 0, s,
@@ -1024,7 +1139,7 @@ static int encode_slabs(const lrq_tensors* t, const void* x, int64_t ldx, hipStr
     else quant(k_quant_slab<BITS, G, R, false, true>);
   } else {
     if (outl) {
-      if constexpr (R == 0) quant(k_quant_slab<BITS, G, R, true, false>);
+      quant(k_quant_slab<BITS, G, R, true, false>);
     } else {
       quant(k_quant_slab<BITS, G, R, false, false>);
     }
@@ -1040,6 +1155,8 @@ static int encode_twopass(const lrq_tensors* t, const void* x, int64_t ldx, hipS
     int st = 0;
     if (encode_slabs<BITS, G, R, false>(t, x, ldx, s, &st)) return st;
   }
+  // the fallback projection reads V^T straight from memory: no outlier mask there
+  if (R > 0 && t->n_outlier > 0) return LRQ_ERR_UNSUPPORTED;
   if constexpr (R > 0) {
     LRQ_TRY(launch((k_project<R>), dim3((M + 15) / 16), dim3(256), 0, s, (const uint16_t*)x, ldx, M, N,
                        (const uint16_t*)t->Vt, (uint16_t*)t->L, t->ld_L));
@@ -1071,7 +1188,7 @@ static int encode_impl(const lrq_tensors* t, const void* x, int64_t ldx, hipStre
     if (encode_slabs<BITS, G, R, true>(t, x, ldx, s, &st)) return st;
     return LRQ_ERR_UNSUPPORTED;
   }
-  if (!force_twopass && t->n_outlier == 0 && encode_persist_dispatch<BITS, G, R>(t, x, ldx, s, &st)) return st;
+  if (!force_twopass && encode_persist_dispatch<BITS, G, R>(t, x, ldx, s, &st)) return st;
   if (R > 0 && t->Vt == nullptr) return LRQ_ERR_NULL;  // the two-pass projection reads V^T
   return encode_twopass<BITS, G, R>(t, x, ldx, s);
 }

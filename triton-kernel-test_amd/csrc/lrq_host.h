@@ -102,7 +102,6 @@ static inline int validate_tensors(const lrq_tensors* t) {
   if ((t->ld_qp % 4) != 0 || !aligned(t->qparams, 8)) return LRQ_ERR_ALIGN;
   if (t->n_outlier < 0 || t->n_outlier > t->hidden) return LRQ_ERR_SHAPE;
   if (t->n_outlier > 0) {
-    if (t->rank != 0) return LRQ_ERR_UNSUPPORTED;
     if (t->outlier_idx == nullptr || t->side == nullptr) return LRQ_ERR_NULL;
     if (t->ld_side < t->n_outlier) return LRQ_ERR_SHAPE;
     if (!aligned(t->side, 2) || !aligned(t->outlier_idx, 4)) return LRQ_ERR_ALIGN;
