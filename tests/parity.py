@@ -57,6 +57,27 @@ def assert_decode_close(dev_bits: np.ndarray, ref_bits: np.ndarray, what: str, f
     return rep
 
 
+def assert_rotated_close(dev_bits: np.ndarray, ref_bits: np.ndarray, what: str, frac=1e-2, k=4) -> dict:
+    """Rotated-format decode (x_hat = bf16(WHT128(y))) vs the oracle's.  A one-ulp difference in
+    one reconstructed value y (the MFMA's fp32 sum at rank 32, see assert_decode_close) moves
+    all 128 outputs of its block by ulp(y)/sqrt(128), which flips some of them by an ulp and,
+    where an output cancels to a small value, by several.  Bar: every element within one ulp of
+    its own plus k such moves at the block's largest magnitude, flips on at most ``frac``."""
+    a = O.bf16_to_f32(dev_bits).astype(np.float64)
+    b = O.bf16_to_f32(ref_bits).astype(np.float64)
+    rows, n = b.shape
+    blk = np.abs(b).reshape(rows, n // 128, 128).max(axis=2)
+    move = k * np.exp2(np.floor(np.log2(np.maximum(blk, 1e-30))) - 7) / np.sqrt(128.0)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(b), 1e-30))) - 7)
+    tol = ulp + np.repeat(move, 128, axis=1)
+    err = np.abs(a - b)
+    d = ulp_diff_bf16(dev_bits, ref_bits)
+    rep = dict(max_ulp=int(d.max()) if d.size else 0, frac_ulp=float((d > 0).mean()) if d.size else 0.0,
+               worst=float((err / tol).max()) if d.size else 0.0)
+    assert rep["worst"] <= 1.0 and rep["frac_ulp"] <= frac, f"{what}: {rep}"
+    return rep
+
+
 def code_mismatch_report(gpu_packed: np.ndarray, ref: dict, bits: int) -> dict:
     """Compare packed codes with the oracle's; classify mismatches.
 

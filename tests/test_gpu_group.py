@@ -115,6 +115,30 @@ def test_outlier_channels_with_low_rank(pkg, dev, rows, hidden, rank, bits, grou
     assert_fp_close(bits16(dx), O.silu_bwd(O.bf16_to_f32(ref_xh), O.bf16_to_f32(bits16(dy))), "silu, outliers+rank")
 
 
+@pytest.mark.parametrize("rows,hidden,rank,bits,group,k", [
+    (100, 4096, 0, 4, 64, 100),    # more side columns than the row decode stages: the tile decode
+    (70, 4096, 16, 4, 64, 200),    # rank 16
+    (40, 2048, 0, 8, 128, 65),     # int8 / g128, one past the row decode's limit
+])
+def test_many_outlier_channels(pkg, dev, rows, hidden, rank, bits, group, k):
+    """More than 64 outlier channels: encode and decode (k_decode, the tile kernel) against the
+    oracle, and a fused consumer on the same path."""
+    print(f"[outliers>64] rows={rows} hidden={hidden} rank={rank} int{bits}/g{group} k={k}", flush=True)
+    x = pkg.inputs.activation(rows, hidden, n_outlier=k, outlier_scale=50.0, seed=k)
+    V = pkg.inputs.basis(hidden, rank, seed=k) if rank else None
+    idx = O.topk_channels(O.colmax_abs(bits16(x)), k)
+    c, ref, rep = _check_encode(pkg, dev, x, V, bits, group, outlier_idx=idx)
+    xh = pkg.decode(c)
+    dy = pkg.inputs.gradient((rows, hidden), 0.02, seed=k)
+    dx = pkg.gelu_backward_compressed(c, dy.to(dev))
+    torch.cuda.synchronize()
+    ref_xh = O.decode(bits16(c.L) if rank else None, bits16(V) if rank else None, c.codes.cpu().numpy(),
+                      f16(c.scale), f16(c.zero), bits, group, side=f16(c.side), idx=idx)
+    print(f"[outliers>64] decode {assert_decode_close(bits16(xh), ref_xh, 'decode, >64 outliers')}", flush=True)
+    assert np.array_equal(bits16(xh)[:, idx], ref_xh[:, idx])
+    assert_fp_close(bits16(dx), O.gelu_bwd(O.bf16_to_f32(ref_xh), O.bf16_to_f32(bits16(dy))), "gelu, >64 outliers")
+
+
 @pytest.mark.parametrize("rows,hidden,rank,bits,group", [(100, 4096, 16, 4, 64), (64, 5120, 16, 4, 64)])
 def test_twopass_matches_fused(pkg, dev, rows, hidden, rank, bits, group):
     print(f"[twopass] rows={rows} hidden={hidden}", flush=True)

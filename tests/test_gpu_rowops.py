@@ -108,6 +108,52 @@ def test_dequant_gemm(pkg, dev, rows, hidden, rank, n_out, out_dtype, bits, grou
         assert_fp_close(bits16(out), ref, "dequant gemm bf16")
 
 
+@pytest.mark.parametrize("rows,hidden,rank,n_out,out_dtype,bits,group,k", [
+    (100, 4096, 16, 16, torch.float32, 4, 64, 8),     # wave-resident kernel (4 units per wave)
+    (37, 2048, 0, 16, torch.bfloat16, 4, 64, 33),     # wave-resident, rank 0, two side chunks, ragged rows
+    (90, 3072, 16, 32, torch.float32, 4, 64, 40),     # unit-walking kernel, n = 32
+    (64, 2048, 32, 16, torch.float32, 4, 64, 64),     # rank 32, the largest side count (64)
+    (50, 2048, 0, 16, torch.float32, 8, 128, 5),      # int8 / g128, rank 0
+    (70, 2048, 16, 16, torch.float32, 4, 128, 12),    # int4 / g128 (256-column units)
+    (60, 3072, 16, 16, torch.bfloat16, 4, 128, 20),   # int4 / g128, unit-walking kernel, one unit slot
+])
+def test_dequant_gemm_outliers(pkg, dev, rows, hidden, rank, n_out, out_dtype, bits, group, k):
+    """x_hat @ A with outlier channels (x_hat[:, idx] = bf16(side)): against the float64 product
+    on the oracle's x_hat with the side columns substituted, to the bars of test_dequant_gemm."""
+    print(f"[gemm outl] rows={rows} hidden={hidden} rank={rank} n={n_out} {out_dtype} int{bits}/g{group} k={k}",
+          flush=True)
+    x = pkg.inputs.activation(rows, hidden, n_outlier=k, outlier_scale=50.0, seed=rows + k)
+    V = pkg.inputs.basis(hidden, rank, seed=k) if rank else None
+    idx = O.topk_channels(O.colmax_abs(bits16(x)), k)
+    gen = torch.Generator().manual_seed(k)
+    a = (torch.randn(hidden, n_out, generator=gen) / np.sqrt(hidden)).to(torch.bfloat16)
+    c = pkg.encode(x.to(dev), V.to(dev) if V is not None else None, bits=bits, group_size=group,
+                   outlier_idx=torch.as_tensor(idx, dtype=torch.int32, device=dev))
+    out = pkg.dequant_gemm(c, a.to(dev), out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    xh = O.bf16_to_f32(O.decode(bits16(c.L) if rank else None, bits16(V) if rank else None, c.codes.cpu().numpy(),
+                                f16(c.scale), f16(c.zero), bits, group, side=f16(c.side), idx=idx))
+    ref = O.gemm(xh, O.bf16_to_f32(bits16(a)))
+    if out_dtype == torch.float32:
+        got = out.cpu().numpy().astype(np.float64)
+        rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+        assert rel <= 1e-5 and np.abs(got - ref).max() <= 1e-3 * max(1.0, np.abs(ref).max()), \
+            (rel, np.abs(got - ref).max())
+    else:
+        assert_fp_close(bits16(out), ref, "dequant gemm bf16, outliers")
+
+
+def test_dequant_gemm_outlier_limit(pkg, dev):
+    """More than 64 outlier channels: the fused GEMM refuses (LRQ_ERR_UNSUPPORTED), no result."""
+    x = pkg.inputs.activation(32, 2048, n_outlier=65, outlier_scale=50.0, seed=4)
+    idx = O.topk_channels(O.colmax_abs(bits16(x)), 65)
+    c = pkg.encode(x.to(dev), None, bits=4, group_size=64,
+                   outlier_idx=torch.as_tensor(idx, dtype=torch.int32, device=dev))
+    a = torch.zeros(2048, 16, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError, match="lrq_dequant_gemm"):
+        pkg.dequant_gemm(c, a)
+
+
 @pytest.mark.parametrize("rows,hidden,rank,bits,group,n_out,out_dtype", [
     (100, 4096, 16, 4, 64, 16, torch.float32),     # north-star width, reduced rows
     (3000, 4096, 16, 4, 64, 16, torch.float32),    # 16 row groups, ragged last block

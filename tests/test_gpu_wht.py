@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle as O
-from parity import TIE_BUDGET, assert_codes, assert_fp_close, bits16, f16, ulp_diff_bf16
+from parity import TIE_BUDGET, assert_codes, assert_fp_close, assert_rotated_close, bits16, f16, ulp_diff_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -79,3 +79,97 @@ def test_rotated_format_c4_recipe(pkg, dev, rows, n):
     out = pkg.silu_backward_compressed(c, dy.to(dev))
     xhf = O.bf16_to_f32(ref_xh)
     assert_fp_close(bits16(out), O.silu_bwd(xhf, O.bf16_to_f32(bits16(dy))), "rotated SiLU bwd")
+
+
+@pytest.mark.parametrize("rows,n,rank,bits,group,op", [
+    (37, 5120, 16, 4, 64, "silu"),    # config 4's format: fused in the row decode (EpiRot), ragged rows
+    (64, 2560, 0, 4, 64, "gelu"),     # rank 0; 20 units (a workgroup with 4 of its 8 units)
+    (40, 2048, 32, 4, 64, "mul"),     # rank 32 (two blocks in flight)
+    (30, 2048, 16, 8, 128, "silu"),   # int8 / g128: decode into the output, then the dense op in place
+    (24, 2048, 16, 4, 64, "softmax"), # softmax: decode into the output, then the dense backward in place
+])
+def test_rotated_consumers(pkg, dev, rows, n, rank, bits, group, op):
+    """Consumers on the rotated format: bit-identical to the dense op on the device's own decode
+    (the same rotation code and the same elementwise formula), and within the floating-point bar
+    of the oracle's rotated decode followed by the op in float64."""
+    print(f"[rot consumer] rows={rows} n={n} rank={rank} int{bits}/g{group} {op}", flush=True)
+    x = pkg.inputs.activation(rows, n, 8, 20.0, seed=n + rank)
+    if op == "softmax":
+        x = torch.softmax(x.float() / 8.0, dim=-1).to(torch.bfloat16)
+    V = pkg.inputs.basis(n, rank, seed=3) if rank else None
+    c = pkg.encode(x.to(dev), V.to(dev) if V is not None else None, bits=bits, group_size=group, hadamard=True)
+    y = pkg.inputs.gradient((rows, n), 0.02, seed=rows)
+    fn = {"silu": pkg.silu_backward_compressed, "gelu": pkg.gelu_backward_compressed,
+          "mul": pkg.mul_compressed, "softmax": pkg.softmax_backward_compressed}[op]
+    out = fn(c, y.to(dev))
+    xh = pkg.decode(c)
+    torch.cuda.synchronize()
+    xd = O.bf16_to_f32(bits16(xh))
+    yf = O.bf16_to_f32(bits16(y))
+    ref_dev = {"silu": O.silu_bwd, "gelu": O.gelu_bwd, "mul": O.mul, "softmax": O.softmax_bwd}[op](xd, yf)
+    assert_fp_close(bits16(out), ref_dev, f"rotated {op} vs the device decode")
+    # the very same fp32 formula on the same x_hat: the library's dense kernels on the decode
+    dense = {"silu": pkg.triton_silu_backward, "gelu": pkg.triton_gelu_backward, "mul": pkg.triton_hadamard,
+             "softmax": pkg.triton_softmax_backward}[op](xh, y.to(dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(bits16(out), bits16(dense))
+    ref_xh = O.decode(bits16(c.L) if rank else None, bits16(V) if rank else None, c.codes.cpu().numpy(),
+                      f16(c.scale), f16(c.zero), bits, group, hadamard=True)
+    # rank 32 reconstructs with MFMA fp32 sums that can sit a step from the oracle's, and the
+    # rotation spreads such a difference over 128 outputs
+    print(f"[rot consumer] decode {assert_rotated_close(bits16(xh), ref_xh, 'rotated decode')}", flush=True)
+    ref = {"silu": O.silu_bwd, "gelu": O.gelu_bwd, "mul": O.mul, "softmax": O.softmax_bwd}[op](
+        O.bf16_to_f32(ref_xh), yf)
+    rep = assert_fp_close(bits16(out), ref, f"rotated {op} vs the oracle")
+    print(f"[rot consumer] {rep}", flush=True)
+
+
+@pytest.mark.parametrize("rows,n,rank,n_out,out_dtype,bits,group", [
+    (64, 5120, 16, 16, torch.float32, 4, 64),     # config 4's format
+    (37, 2560, 0, 32, torch.bfloat16, 4, 64),     # 20 units: the last step holds 4 of 8; ragged rows
+    (40, 2048, 16, 16, torch.float32, 8, 128),    # int8 / g128: one rotation block per unit
+    (30, 2048, 16, 32, torch.float32, 4, 128),    # int4 / g128, n = 32: two blocks per unit, no prefetch
+    (50, 1024, 0, 16, torch.float32, 8, 64),      # int8 / g64: half a block per unit, four row blocks per workgroup
+])
+def test_rotated_dequant_gemm(pkg, dev, rows, n, rank, n_out, out_dtype, bits, group):
+    """x_hat @ A on the rotated format, fused: against the float64 product on the device's rotated
+    decode (the kernel rotates with the decode's routine, so the x_hat is the same) within the
+    fp32 accumulation bound, and against the oracle's rotated decode within the floating-point bar."""
+    print(f"[rot gemm] rows={rows} n={n} rank={rank} n_out={n_out} {out_dtype} int{bits}/g{group}", flush=True)
+    x = pkg.inputs.activation(rows, n, 8, 20.0, seed=n + n_out)
+    V = pkg.inputs.basis(n, rank, seed=5) if rank else None
+    gen = torch.Generator().manual_seed(n_out)
+    a = (torch.randn(n, n_out, generator=gen) / np.sqrt(n)).to(torch.bfloat16)
+    c = pkg.encode(x.to(dev), V.to(dev) if V is not None else None, bits=bits, group_size=group, hadamard=True)
+    out = pkg.dequant_gemm(c, a.to(dev), out_dtype=out_dtype)
+    xh = pkg.decode(c)
+    torch.cuda.synchronize()
+    xd = O.bf16_to_f32(bits16(xh)).astype(np.float64)
+    af = O.bf16_to_f32(bits16(a)).astype(np.float64)
+    ref = xd @ af
+    bound = 1e-5 * (np.abs(xd) @ np.abs(af)) + 1e-9
+    if out_dtype == torch.float32:
+        got = out.cpu().numpy().astype(np.float64)
+        err = np.abs(got - ref)
+        assert (err <= bound).all(), (float(err.max()), float((err / bound).max()))
+    else:
+        got = O.bf16_to_f32(bits16(out)).astype(np.float64)
+        ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))) - 7)
+        assert (np.abs(got - ref) <= ulp + bound).all()
+    ref_xh = O.decode(bits16(c.L) if rank else None, bits16(V) if rank else None, c.codes.cpu().numpy(),
+                      f16(c.scale), f16(c.zero), bits, group, hadamard=True)
+    ref_o = O.gemm(O.bf16_to_f32(ref_xh), af)
+    if out_dtype == torch.float32:
+        rel = np.linalg.norm(got - ref_o) / np.linalg.norm(ref_o)
+        assert rel <= 1e-3, rel
+    else:
+        assert_fp_close(bits16(out), ref_o, "rotated dequant gemm bf16 vs the oracle")
+
+
+def test_rotated_dequant_gemm_straddling_planes(pkg, dev):
+    """int4/g64 at 384 columns: planes of 192 columns, so rotation blocks straddle the planes and
+    the fused GEMM refuses (the decode still works through its separate rotation pass)."""
+    x = pkg.inputs.activation(16, 384, 0, 1.0, seed=1)
+    c = pkg.encode(x.to(dev), None, bits=4, group_size=64, hadamard=True)
+    with pytest.raises(ValueError, match="lrq_dequant_gemm"):
+        pkg.dequant_gemm(c, torch.zeros(384, 16, dtype=torch.bfloat16, device=dev))

@@ -271,24 +271,12 @@ def decode(c: CompressedActivation, out: Optional[torch.Tensor] = None) -> torch
     return o
 
 
-_DENSE_OP = {"lrq_silu_bwd": 0, "lrq_gelu_bwd": 1, "lrq_mul": 2}
-
-
 def _fused(name: str, c: CompressedActivation, y: torch.Tensor, argname: str) -> torch.Tensor:
+    if c.hadamard or (c.idx is not None and name == "lrq_softmax_bwd"):
+        # the library's two-kernel forms of these (decode into the output, then the dense op in
+        # place) take rows of exactly `hidden` elements
+        y = y.contiguous()
     y2, ldy = _operand(c, y, argname)
-    if c.hadamard:
-        # rotated format: the inverse rotation needs whole 128-column blocks, so decode (which
-        # rotates back) and apply the consumer on the result
-        xh = decode(c)
-        o = torch.empty_like(xh)
-        y3 = y.contiguous()
-        with torch.cuda.device(c.device):
-            if name == "lrq_softmax_bwd":
-                call("lrq_dense_softmax_bwd", _p(xh), _p(y3), _p(o), c.rows, c.hidden, _stream(c.device))
-            else:
-                call("lrq_dense_elementwise", _DENSE_OP[name], _p(xh), _p(y3), _p(o), xh.numel(),
-                     _stream(c.device))
-        return o
     o = _out_like(c, None)
     t = c.descriptor()
     with torch.cuda.device(c.device):
@@ -325,9 +313,6 @@ def dequant_gemm(c: CompressedActivation, a: torch.Tensor, out_dtype=torch.float
     n_out = a.shape[1]
     if out_dtype not in (torch.float32, torch.bfloat16):
         raise ValueError("out_dtype must be float32 or bfloat16")
-    if c.hadamard:
-        xh = decode(c).reshape(c.rows, c.hidden)
-        return torch.matmul(xh.float(), a.float()).to(out_dtype).reshape(tuple(c.shape[:-1]) + (n_out,))
     o = torch.empty((c.rows, n_out), dtype=out_dtype, device=c.device)
     t = c.descriptor()
     with torch.cuda.device(c.device):

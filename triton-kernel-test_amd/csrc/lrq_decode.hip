@@ -42,6 +42,16 @@ struct EpiStoreRot : EpiStore {
   static constexpr bool kRot = true;
 };
 
+// A consumer on the rotated format: the compute pass stores bf16(Y') like EpiStore, the
+// rotation pass applies the consumer to the rotated values (x_hat = bf16(WHT(bf16(Y'))), the
+// decode's result) with the matching second-tensor values, and stores that.
+template <class Inner>
+struct EpiRot : Inner {
+  static constexpr bool kRot = true;
+  __device__ __forceinline__ u32x4 apply(const float* xh, u32x4) const { return pack8(xh); }
+  __device__ __forceinline__ u32x4 rot_apply(const float* y, u32x4 in) const { return Inner::apply(y, in); }
+};
+
 // silu_backward.py:6-8 on x = bf16(x_hat), fp32 (lrq_math.h).
 struct EpiSilu {
   static constexpr bool kIn = true, kRot = false;
@@ -427,6 +437,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
     int RBW) {
   constexpr bool IN = EPI::kIn;
   static_assert(!INP || IN, "in-place staging is for consumers");
+  static_assert(!(INP && EPI::kRot), "a rotated consumer keeps its second tensor in tiles of its own");
   using Lay = RowsLayout<BITS, G, R, NW, IN, OUTL, INP>;
   using Tl = typename Lay::Tl;
   using Ro = typename Lay::Ro;
@@ -680,8 +691,18 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
     }
     if constexpr (EPI::kRot) {
       lds_barrier();  // every wave's unit of block b is in the tile
-      if (rot_live)
-        wht128_lds(osm + (b & 1) * Ro::OSLOT + (rot_p * 16 + j) * Ro::OPAD + (128 * rot_q + 32 * g) * 2, wop);
+      if (rot_live) {
+        const int roff = (rot_p * 16 + j) * Ro::OPAD + (128 * rot_q + 32 * g) * 2;
+        if constexpr (IN) {
+          // the consumer's second tensor sits at the same place in the input tile
+          const unsigned char* rd = dsm + (b & 1) * Ro::OSLOT + roff;
+          wht128_lds_map(osm + (b & 1) * Ro::OSLOT + roff, wop, [&](int k, const float* y) {
+            return epi.rot_apply(y, *reinterpret_cast<const u32x4*>(rd + 16 * k));
+          });
+        } else {
+          wht128_lds(osm + (b & 1) * Ro::OSLOT + roff, wop);
+        }
+      }
     }
   }
   }
@@ -703,12 +724,14 @@ constexpr int rows_nw() { return G * (8 / BITS) <= 128 ? 8 : 4; }
 template <int BITS, int G, int R, bool OUTL, class EPI>
 static int decode_rows_launch(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
   constexpr int NW = rows_nw<BITS, G>();
-  // consumers of 128-column groups stage dY in place (separate tiles would not fit in LDS)
-  constexpr bool INP = EPI::kIn && G == 128;
+  // consumers of 128-column groups stage dY in place (separate tiles would not fit in LDS; a
+  // rotated consumer cannot, and is refused by the LDS check below)
+  constexpr bool INP = EPI::kIn && G == 128 && !EPI::kRot;
   using Lay = RowsLayout<BITS, G, R, NW, EPI::kIn, OUTL, INP>;
   constexpr int kBudget = EPI::kIn ? 100 : EPI::kRot ? 150 : R == 32 ? 160 : 180;
   constexpr int kFit = kBudget / Lay::kRegsPerBlock;
-  constexpr int PD = kFit >= 16 ? 16 : kFit >= 8 ? 8 : kFit >= 4 ? 4 : 2;
+  // (a rotated consumer at rank 32 also holds the rotation operands: two blocks in flight)
+  constexpr int PD = (EPI::kIn && EPI::kRot && R == 32) ? 2 : kFit >= 16 ? 16 : kFit >= 8 ? 8 : kFit >= 4 ? 4 : 2;
   const int M = (int)t->rows, N = (int)t->hidden;
   const int units = N / (G * (8 / BITS));
   const int64_t ug = (units + NW - 1) / NW, nrb = (M + 15) / 16, cus = cu_count();
@@ -825,6 +848,39 @@ static int decode_rot_fused(const lrq_tensors* t, hipStream_t s, uint16_t* out, 
   }
 }
 
+// Rotated format with a consumer, fused into the row kernel (EpiRot): int4/g64 (int8/g128's
+// row kernel has no LDS left for the consumer's own tiles), no outlier channels, planes of whole
+// rotation blocks; returns 0 for the others.
+template <int BITS, int G, int R, class EPI>
+static int consumer_rot_fused(const lrq_tensors* t, hipStream_t s, const EPI& inner, int* status) {
+  if constexpr (!(BITS == 4 && G == 64)) {
+    return 0;
+  } else {
+    const int64_t plane = t->hidden / (8 / BITS);
+    if (t->n_outlier != 0 || plane % 128 != 0) return 0;
+    for (int64_t ldb : {t->ld_codes, 2 * t->ld_qp, 2 * t->ld_L, 2 * inner.in_ld(), 2 * inner.out_ld()})
+      if (16 * ldb >= ((int64_t)1 << 31)) return 0;
+    lrq_tensors plain = *t;
+    plain.flags &= ~LRQ_FLAG_HADAMARD;
+    EpiRot<EPI> epi;
+    static_cast<EPI&>(epi) = inner;
+    const int st = decode_rows_launch<BITS, G, R, false>(&plain, s, epi);
+    if (st == LRQ_ERR_UNSUPPORTED) return 0;
+    *status = st;
+    return 1;
+  }
+}
+
+template <class EPI>
+static int consumer_rot(const lrq_tensors* t, hipStream_t s, const EPI& inner, int* status) {
+  switch (format_key(t->bits, t->group, t->rank)) {
+    case format_key(4, 64, 0): return consumer_rot_fused<4, 64, 0>(t, s, inner, status);
+    case format_key(4, 64, 16): return consumer_rot_fused<4, 64, 16>(t, s, inner, status);
+    case format_key(4, 64, 32): return consumer_rot_fused<4, 64, 32>(t, s, inner, status);
+    default: return 0;
+  }
+}
+
 static int decode_rot(const lrq_tensors* t, hipStream_t s, uint16_t* out, int64_t ldo, int* status) {
   switch (format_key(t->bits, t->group, t->rank)) {
     case format_key(4, 64, 0): return decode_rot_fused<4, 64, 0>(t, s, out, ldo, status);
@@ -853,25 +909,36 @@ extern "C" int lrq_decode(const lrq_tensors* t, void* out, int64_t ldo, void* st
   return decode_dispatch(t, (hipStream_t)stream, EpiStore{(uint16_t*)out, ldo});
 }
 
-extern "C" int lrq_silu_bwd(const lrq_tensors* t, const void* dy, int64_t lddy, void* dx, int64_t lddx,
-                            void* stream) {
-  int st = check_io(t, dy, lddy, dx, lddx, true);
+namespace lrq {
+// The elementwise consumers (op as lrq_dense_elementwise numbers them).  The rotated format goes
+// to the fused row kernel where it can, else decode into `out` (rotation undone) and the dense
+// op in place over it: two kernels, no scratch.  The second form needs rows of exactly `hidden`
+// elements in both tensors (the dense kernel is flat).
+template <class EPI>
+static int consumer(const lrq_tensors* t, const void* in, int64_t ldin, void* out, int64_t ldo, int op,
+                    void* stream) {
+  int st = check_io(t, in, ldin, out, ldo, true);
   if (st) return st;
   if (t->rows == 0) return LRQ_OK;
-  return decode_dispatch(t, (hipStream_t)stream, EpiSilu{(const uint16_t*)dy, lddy, (uint16_t*)dx, lddx});
+  const EPI epi{(const uint16_t*)in, ldin, (uint16_t*)out, ldo};
+  if (!(t->flags & LRQ_FLAG_HADAMARD)) return decode_dispatch(t, (hipStream_t)stream, epi);
+  if (consumer_rot(t, (hipStream_t)stream, epi, &st)) return st;
+  if (ldin != t->hidden || ldo != t->hidden) return LRQ_ERR_UNSUPPORTED;
+  LRQ_TRY(lrq_decode(t, out, ldo, stream));
+  return lrq_dense_elementwise(op, out, in, out, t->rows * t->hidden, stream);
+}
+}  // namespace lrq
+
+extern "C" int lrq_silu_bwd(const lrq_tensors* t, const void* dy, int64_t lddy, void* dx, int64_t lddx,
+                            void* stream) {
+  return consumer<EpiSilu>(t, dy, lddy, dx, lddx, 0, stream);
 }
 
 extern "C" int lrq_gelu_bwd(const lrq_tensors* t, const void* dy, int64_t lddy, void* dx, int64_t lddx,
                             void* stream) {
-  int st = check_io(t, dy, lddy, dx, lddx, true);
-  if (st) return st;
-  if (t->rows == 0) return LRQ_OK;
-  return decode_dispatch(t, (hipStream_t)stream, EpiGelu{(const uint16_t*)dy, lddy, (uint16_t*)dx, lddx});
+  return consumer<EpiGelu>(t, dy, lddy, dx, lddx, 1, stream);
 }
 
 extern "C" int lrq_mul(const lrq_tensors* t, const void* y, int64_t ldy, void* out, int64_t ldo, void* stream) {
-  int st = check_io(t, y, ldy, out, ldo, true);
-  if (st) return st;
-  if (t->rows == 0) return LRQ_OK;
-  return decode_dispatch(t, (hipStream_t)stream, EpiMul{(const uint16_t*)y, ldy, (uint16_t*)out, ldo});
+  return consumer<EpiMul>(t, y, ldy, out, ldo, 2, stream);
 }

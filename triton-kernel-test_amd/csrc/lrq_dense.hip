@@ -23,8 +23,9 @@ __device__ __forceinline__ float dense_op(float x, float y) {
 
 // 8 elements (16 bytes) per thread per step, grid-stride; the scalar tail covers n % 8.
 template <int OP>
-__global__ __launch_bounds__(256) void k_dense_elementwise(const uint16_t* __restrict__ x, const uint16_t* __restrict__ y,
-                                                           uint16_t* __restrict__ out, int64_t n) {
+// out may be x (in place: each element is read and written by the same thread, reads first).
+__global__ __launch_bounds__(256) void k_dense_elementwise(const uint16_t* x, const uint16_t* __restrict__ y,
+                                                           uint16_t* out, int64_t n) {
   const int64_t nv = n / 8;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nv; i += stride) {
@@ -44,9 +45,8 @@ __global__ __launch_bounds__(256) void k_dense_elementwise(const uint16_t* __res
 
 // Same, for operands that are not 16-byte aligned: one element per thread.
 template <int OP>
-__global__ __launch_bounds__(256) void k_dense_elementwise_scalar(const uint16_t* __restrict__ x,
-                                                                  const uint16_t* __restrict__ y,
-                                                                  uint16_t* __restrict__ out, int64_t n) {
+__global__ __launch_bounds__(256) void k_dense_elementwise_scalar(const uint16_t* x, const uint16_t* __restrict__ y,
+                                                                  uint16_t* out, int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; k < n; k += stride) {
     const float a = __uint_as_float((uint32_t)x[k] << 16), b = __uint_as_float((uint32_t)y[k] << 16);
@@ -69,8 +69,10 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 // 4 per thread, so y and g stay in registers between the reduction and the output;
 // otherwise one element per thread per step, with the row re-read (from L2) for the output.
 template <bool VEC>
-__global__ __launch_bounds__(256) void k_dense_softmax_bwd(const uint16_t* __restrict__ y, const uint16_t* __restrict__ g,
-                                                           uint16_t* __restrict__ out, int64_t n) {
+// out may be y (in place: a row's outputs are written only after every read of the row that
+// precedes them in the thread, and each element by the thread that read it).
+__global__ __launch_bounds__(256) void k_dense_softmax_bwd(const uint16_t* y, const uint16_t* __restrict__ g,
+                                                           uint16_t* out, int64_t n) {
   __shared__ float red[4];
   const int64_t base = (int64_t)blockIdx.x * n;
   if constexpr (VEC) {

@@ -13,6 +13,7 @@
 #include "lrq_common.h"
 #include "lrq_dequant.h"
 #include "lrq_host.h"
+#include "lrq_whtop.h"
 
 #include <algorithm>
 #include <mutex>
@@ -503,19 +504,116 @@ __global__ __launch_bounds__(NW * 64) void k_softmax_rows(
 // operand is regenerated per unit with the identity-MFMA transpose of lrq_common.h).  A unit's
 // inputs sit in one of SL register slots, loaded while the previous unit is computed.  The NW
 // partial tiles of a row block are then summed through LDS, each wave summing 1/NW of it.
-template <int BITS, int G, int R, int NOUT, int NW, int RBW, int SL, bool OUT_F32>
+// Outlier channels in the dequant-GEMMs: x_hat[:, idx] = bf16(side), so
+//   out = sum over the other columns of x_hat A  +  bf16(side) @ A[idx, :].
+// The first sum is the ordinary kernel with A's operand rows of outlier columns zeroed (once);
+// the second enters the same fp32 accumulators as extra K entries (one 16x16x32 step per 32
+// side columns, added by wave 0 per row block): the products and the accumulation are those
+// of the decoded activation's GEMM.  Up to kSideGemmMax side columns.
+constexpr int kSideGemmMax = 64;
+
+template <int TO>
+struct SideGemm {
+  static constexpr int KC = kSideGemmMax / 32;
+  // lane (i, g), chunk m, tile t: A[idx[32m + 8g + e]][16t + i], e < 8 (0 past nout and for an
+  // index outside [0, N), which the decode ignores too)
+  u32x4 a[KC][TO];
+  __device__ __forceinline__ void load_a(const uint16_t* __restrict__ A, int n_out, int N,
+                                         const int32_t* __restrict__ oidx, int nout, int i, int g) {
+#pragma unroll
+    for (int m = 0; m < KC; ++m)
+#pragma unroll
+      for (int t = 0; t < TO; ++t) {
+        uint32_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int sc = 32 * m + 8 * g + e;
+          const int c = oidx[min(sc, nout - 1)];
+          const bool ok = sc < nout && c >= 0 && c < N;
+          const uint16_t v = A[(int64_t)(ok ? c : 0) * n_out + 16 * t + i];
+          h[e] = ok ? v : 0u;
+        }
+        a[m][t] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+      }
+  }
+  // the lane's side values of row `row` for every chunk (columns past nout clamp to a valid one)
+  __device__ static __forceinline__ void load_b(uint32_t (&sd)[KC][8], const uint16_t* __restrict__ side,
+                                                int64_t ldside, int64_t row, int nout, int g) {
+#pragma unroll
+    for (int m = 0; m < KC; ++m)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sd[m][e] = side[row * ldside + min(32 * m + 8 * g + e, nout - 1)];
+  }
+  __device__ __forceinline__ void apply(const uint32_t (&sd)[KC][8], f32x4* acc, int nout) const {
+#pragma unroll
+    for (int m = 0; m < KC; ++m) {
+      if (32 * m >= nout) break;  // uniform
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = f16_val(sd[m][e]);
+      const u32x4 b = pack8(f);  // bf16(side), as the decode returns it
+#pragma unroll
+      for (int t = 0; t < TO; ++t) acc[t] = mfma_16x16x32(a[m][t], b, acc[t]);
+    }
+  }
+};
+
+// acc[b * TO + t] += side term of row block rb0 + b, tile t (after the main loop, so the side
+// operands hold no registers while the units are walked).
+template <int TO, int RBW>
+__device__ __forceinline__ void add_side_term(const uint16_t* __restrict__ A, int n_out, int N,
+                                              const int32_t* __restrict__ oidx, int nout,
+                                              const uint16_t* __restrict__ side, int64_t ldside, int rb0, int nrb,
+                                              int M, int j, int g, f32x4* acc) {
+  SideGemm<TO> sg;
+  sg.load_a(A, n_out, N, oidx, nout, j, g);
+#pragma unroll
+  for (int b = 0; b < RBW; ++b) {
+    uint32_t sd[SideGemm<TO>::KC][8];
+    SideGemm<TO>::load_b(sd, side, ldside, min(min(rb0 + b, nrb - 1) * 16 + j, M - 1), nout, g);
+    sg.apply(sd, acc + b * TO, nout);
+  }
+}
+
+// Column mask of the outlier channels in LDS (N/32 words), built by the whole workgroup.
+__device__ __forceinline__ void build_colmask(uint32_t* mask, int N, const int32_t* __restrict__ oidx, int nout) {
+  for (int i = threadIdx.x; i < N / 32; i += blockDim.x) mask[i] = 0u;
+  __syncthreads();
+  for (int k = threadIdx.x; k < nout; k += blockDim.x) {
+    const int c = oidx[k];
+    if (c >= 0 && c < N) atomicOr(&mask[c >> 5], 1u << (c & 31));
+  }
+  __syncthreads();
+}
+
+// Zero the operand rows (lane (j, g) of operand q holds row vrow_res(base, j, q)) of outlier columns.
+template <int G, int T>
+__device__ __forceinline__ void mask_rows(u32x2 (&op)[G / 16][T], const uint32_t* mask, int base, int j) {
+#pragma unroll
+  for (int q = 0; q < G / 16; ++q) {
+    const int c = vrow_res<G>(base, j, q);
+    const bool z = (mask[c >> 5] >> (c & 31)) & 1u;
+#pragma unroll
+    for (int t = 0; t < T; ++t) op[q][t] = z ? u32x2{0u, 0u} : op[q][t];
+  }
+}
+
+template <int BITS, int G, int R, int NOUT, int NW, int RBW, int SL, bool OUT_F32, bool OUTL>
 __global__ __launch_bounds__(NW * 64) void k_dequant_gemm(
     const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
     const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
-    const uint16_t* __restrict__ A, void* __restrict__ out, int64_t ldo) {
+    const uint16_t* __restrict__ A, void* __restrict__ out, int64_t ldo, const int32_t* __restrict__ oidx, int nout,
+    const uint16_t* __restrict__ side, int64_t ldside) {
   constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, TO = NOUT / 16, E = G / 4;
   __shared__ f32x4 part[NW][TO][64];
+  extern __shared__ uint32_t gmask[];  // OUTL: N/32 words
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int nrb = (M + 15) / 16;
   const int rb0 = blockIdx.x * RBW;
   const int units = N / (G * NP);
   const u32x2 ident = identity_bop(j, g);
+  if constexpr (OUTL) build_colmask(gmask, N, oidx, nout);
 
   f32x4 acc[RBW][TO];
 #pragma unroll
@@ -547,6 +645,7 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm(
     for (int p = 0; p < NP; ++p) {
       if constexpr (R > 0) load_vops<G, R>(V, unit_base(p, u, N, NP, G), j, g, d.vop[p]);
       load_vops<G, NOUT>(A, unit_base(p, u, N, NP, G), j, g, d.va[p]);
+      if constexpr (OUTL) mask_rows<G, TO>(d.va[p], gmask, unit_base(p, u, N, NP, G), j);
     }
 #pragma unroll
     for (int b = 0; b < RBW; ++b) {
@@ -586,6 +685,9 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm(
       load_unit(min(w + (i0 + sl + SL) * NW, units - 1), ring[sl]);
     }
   }
+  if constexpr (OUTL) {
+    if (w == 0) add_side_term<TO, RBW>(A, NOUT, N, oidx, nout, side, ldside, rb0, nrb, M, j, g, &acc[0][0]);
+  }
 
   // acc[b][t] in lane (j, g), component v: out[row j][16t + 4g + v] (partial over this wave's units)
   constexpr int F = TO * 256 / NW, S = 64 / F, PPL = NW / S;
@@ -615,6 +717,159 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm(
   }
 }
 
+// Dequant-GEMM on the rotated format: x_hat = bf16(WHT128(bf16(Y'))) blockwise, the rotated
+// decode's result, times A.  Wave w takes unit s*NW + w at step s; per step and row block the
+// waves write bf16(Y') of their units into an LDS tile laid out as the rotated decode's output
+// tile (16 rows x NP planes x NW*G columns), rotate its 128-column blocks in place with the
+// decode's own routine (wht128_lds: the same bf16 x_hat, bit for bit), read their units back in
+// the B-operand layout and project as k_dequant_gemm does.  Planes must be whole rotation blocks
+// (plane % 128 == 0), so every block of a step is complete.
+template <int BITS, int G, int R, int NOUT, int NW, int RBW, bool OUT_F32>
+__global__ __launch_bounds__(NW * 64) void k_dequant_gemm_rot(
+    const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
+    const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
+    const uint16_t* __restrict__ A, void* __restrict__ out, int64_t ldo) {
+  constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, TO = NOUT / 16, E = G / 4;
+  constexpr int SEG = NW * G;           // columns of one plane per step
+  constexpr int OPAD = SEG * 2 + 16;    // LDS row pitch in bytes (spreads the 16 rows over banks)
+  constexpr int TILE = 16 * NP * OPAD;  // one row block's tile
+  constexpr int RB = SEG / 128;         // rotation blocks per plane and step
+  static_assert(SEG % 128 == 0 && OPAD % 16 == 0, "whole rotation blocks, 16-byte rows");
+  __shared__ f32x4 part[NW][TO][64];
+  extern __shared__ __attribute__((aligned(16))) unsigned char tile[];  // [RBW][TILE]
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int nrb = (M + 15) / 16;
+  const int rb0 = blockIdx.x * RBW;
+  const int units = N / (G * NP);
+  const int steps = (units + NW - 1) / NW;
+  const u32x2 ident = identity_bop(j, g);
+  u32x4 wop[2][2];
+#pragma unroll
+  for (int q0 = 0; q0 < 2; ++q0)
+#pragma unroll
+    for (int n = 0; n < 2; ++n) wop[q0][n] = wht_base_operand(j, g, q0, n != 0);
+
+  f32x4 acc[RBW][TO];
+#pragma unroll
+  for (int b = 0; b < RBW; ++b)
+#pragma unroll
+    for (int t = 0; t < TO; ++t) acc[b][t] = zero4();
+  u32x2 lop[RBW][RT];
+#pragma unroll
+  for (int b = 0; b < RBW; ++b) {
+    const int64_t row = min(min(rb0 + b, nrb - 1) * 16 + j, M - 1);
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t) lop[b][t] = ld8(Lin + row * ldl + 16 * t + 4 * g);
+    }
+  }
+  struct UIn {
+    u32x2 vop[NP][G / 16][RT];
+    u32x2 va[NP][G / 16][TO];
+    u32x4 cb[RBW][G / 64];
+    uint32_t qp[RBW][NP];
+  };
+  auto load_unit = [&](int u, UIn& d) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      if constexpr (R > 0) load_vops<G, R>(V, unit_base(p, u, N, NP, G), j, g, d.vop[p]);
+      load_vops<G, NOUT>(A, unit_base(p, u, N, NP, G), j, g, d.va[p]);
+    }
+#pragma unroll
+    for (int b = 0; b < RBW; ++b) {
+      const int64_t row = min(min(rb0 + b, nrb - 1) * 16 + j, M - 1);
+#pragma unroll
+      for (int i = 0; i < G / 64; ++i) d.cb[b][i] = ld16_stream(codes + row * ldc + u * G + E * g + 16 * i);
+      if constexpr (NP == 2) {
+        const u32x2 q = ld8(qparams + row * ldq + u * 4);
+        d.qp[b][0] = q[0];
+        d.qp[b][1] = q[1];
+      } else {
+        d.qp[b][0] = ld4(qparams + row * ldq + u * 2);
+      }
+    }
+  };
+  // the next step's inputs are loaded while this one is computed, except where a unit's
+  // registers are large (256-column units with n = 32 and rank > 0): then after its last read
+  constexpr bool PF = !(G * NP >= 256 && NOUT == 32 && R > 0);
+  UIn cur, nxt;
+  load_unit(min(w, units - 1), cur);
+  for (int s = 0; s < steps; ++s) {
+    const int u = s * NW + w;
+    const bool live = u < units;            // wave-uniform
+    const int ncols = min(NW, units - s * NW) * G;  // columns of each plane present in this step
+    if (PF && s + 1 < steps) load_unit(min(u + NW, units - 1), nxt);
+    if (live) {
+#pragma unroll
+      for (int b = 0; b < RBW; ++b)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          float xh[E];
+          reconstruct_plane<BITS, G, R>(cur.cb[b], cur.qp[b][p], p, cur.vop[p], lop[b], xh);
+#pragma unroll
+          for (int k = 0; k < E / 8; ++k)
+            *reinterpret_cast<u32x4*>(tile + b * TILE + (p * 16 + j) * OPAD + (w * G + E * g + 8 * k) * 2) =
+                pack8(xh + 8 * k);
+        }
+    }
+    __syncthreads();
+    for (int k = w; k < NP * RB; k += NW) {  // wave-uniform
+      const int p = k / RB, q = k % RB;
+      if ((q + 1) * 128 <= ncols) {
+#pragma unroll
+        for (int b = 0; b < RBW; ++b) wht128_lds(tile + b * TILE + (p * 16 + j) * OPAD + (128 * q + 32 * g) * 2, wop);
+      }
+    }
+    __syncthreads();
+    if (live) {
+#pragma unroll
+      for (int b = 0; b < RBW; ++b)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          u32x4 xb[G / 32];
+#pragma unroll
+          for (int k = 0; k < G / 32; ++k)
+            xb[k] = *reinterpret_cast<const u32x4*>(tile + b * TILE + (p * 16 + j) * OPAD + (w * G + E * g + 8 * k) * 2);
+          project_unit<G, NOUT>(cur.va[p], xb, ident, acc[b]);
+        }
+    }
+    __syncthreads();  // the tiles are rewritten by the next step
+    if constexpr (PF) {
+      cur = nxt;
+    } else {
+      if (s + 1 < steps) load_unit(min(u + NW, units - 1), cur);
+    }
+  }
+
+  // acc[b][t] in lane (j, g), component v: out[row j][16t + 4g + v] (as in k_dequant_gemm)
+  constexpr int F = TO * 256 / NW, S = 64 / F, PPL = NW / S;
+  static_assert(F >= 1 && F <= 64 && 64 % F == 0 && NW % S == 0, "out reduction split");
+  const float* partf = reinterpret_cast<const float*>(&part[0][0][0]);
+#pragma unroll
+  for (int b = 0; b < RBW; ++b) {
+    if (rb0 + b >= nrb) break;  // uniform
+#pragma unroll
+    for (int t = 0; t < TO; ++t) part[w][t][lane] = acc[b][t];
+    __syncthreads();
+    const int f = lane % F, pg = lane / F;
+    const int fi = w * F + f;
+    const int t = fi >> 8, src = (fi >> 2) & 63, v = fi & 3;
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) sum += partf[(((pg * PPL + i) * TO + t) * 64 + src) * 4 + v];
+#pragma unroll
+    for (int m = F; m < 64; m <<= 1) sum += __shfl_xor(sum, m);
+    const int row = (rb0 + b) * 16 + (src & 15);
+    const int col = 16 * t + 4 * (src >> 4) + v;
+    if (pg == 0 && row < M) {
+      if constexpr (OUT_F32) reinterpret_cast<float*>(out)[(int64_t)row * ldo + col] = sum;
+      else reinterpret_cast<uint16_t*>(out)[(int64_t)row * ldo + col] = (uint16_t)pack_bf16x2(sum, 0.f);
+    }
+    __syncthreads();
+  }
+}
+
 // Dequant-GEMM for n = 16 when the row's units split evenly over the waves (NU per wave):
 // wave w owns units NU*w .. NU*w + NU-1 and keeps their reconstruction operands and the
 // transposed A operands in registers for the whole kernel (loaded and transposed once, not per
@@ -623,20 +878,23 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm(
 // accumulator index is static and blocks past the last one issue no loads.  Rows past the end
 // repeat the last row (their sums are not stored).  The 8 partial tiles of a block are summed
 // through LDS in wave order as in k_dequant_gemm.
-template <int BITS, int G, int R, int NW, int NU, int RBW, int SL, bool OUT_F32>
+template <int BITS, int G, int R, int NW, int NU, int RBW, int SL, bool OUT_F32, bool OUTL>
 __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_w(
     const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
     const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
-    const uint16_t* __restrict__ A, void* __restrict__ out, int64_t ldo) {
+    const uint16_t* __restrict__ A, void* __restrict__ out, int64_t ldo, const int32_t* __restrict__ oidx, int nout,
+    const uint16_t* __restrict__ side, int64_t ldside) {
   constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, E = G / 4;
   static_assert(R == 0 || R == 16, "rank 0 or 16");
   __shared__ f32x4 part[NW][64];
+  extern __shared__ uint32_t gmask[];  // OUTL: N/32 words
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
   const int nrb = (M + 15) / 16;
   const int rb0 = blockIdx.x * RBW;
   const int ub = w * NU;
   const u32x2 ident = identity_bop(j, g);
+  if constexpr (OUTL) build_colmask(gmask, N, oidx, nout);
 
   u32x2 vop[NU][NP][G / 16][RT];
   u32x4 vt[NU][NP][G / 32][1];
@@ -648,6 +906,7 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_w(
       if constexpr (R > 0) load_vops<G, R>(V, base, j, g, vop[uu][p]);
       u32x2 va[G / 16][1];
       load_vops<G, 16>(A, base, j, g, va);
+      if constexpr (OUTL) mask_rows<G, 1>(va, gmask, base, j);
       transpose_vops<G, 16>(va, ident, vt[uu][p]);
     }
 
@@ -699,6 +958,9 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_w(
   for (int b = 0; b < RBW; ++b) {
     compute_blk(ring[b % SL], acc[b]);
     if (b + SL < RBW) load_blk(rb0 + b + SL, ring[b % SL]);
+  }
+  if constexpr (OUTL) {
+    if (w == 0) add_side_term<1, RBW>(A, 16, N, oidx, nout, side, ldside, rb0, nrb, M, j, g, acc);
   }
 
   // acc[b] in lane (j, g), component v: out[row j][4g + v] (partial over this wave's units)
@@ -999,42 +1261,78 @@ static int softmax_units(const lrq_tensors* t, const void* dp, int64_t lddp, voi
   }
 }
 
-template <int BITS, int G, int R, int NOUT, bool F32>
+template <int BITS, int G, int R, int NOUT, bool F32, bool OUTL>
 static int gemm_launch(const lrq_tensors* t, const void* a, void* out, int64_t ldo, hipStream_t s) {
   // row blocks per workgroup: 4, or 2 where a unit's register slot is large (two slots in flight)
   constexpr int UC = G * (8 / BITS);  // columns of one unit
   constexpr int NW = 8, RBW = (UC >= 256 && NOUT == 32) ? 1 : (UC >= 256 || NOUT == 32 || R == 32) ? 2 : 4;
-  constexpr int SL = (UC >= 256 && NOUT == 32 && R > 0) ? 1 : 2;  // unit slots in flight
+  // unit slots in flight (one where a slot is large; the outlier mask adds registers to a slot)
+  constexpr int SL = (UC >= 256 && R > 0 && (NOUT == 32 || OUTL)) ? 1 : 2;
   const int M = (int)t->rows, N = (int)t->hidden;
   const int nrb = (M + 15) / 16;
+  const size_t shm = OUTL ? (size_t)(N / 32) * 4 : 0;
   if constexpr (NOUT == 16 && R <= 16) {
     // units split evenly over the waves: the wave-resident kernel (NU units per wave)
     const int units = N / (UC);
     auto wlaunch = [&](auto nu) {
       constexpr int NU = decltype(nu)::value, WRBW = 4, WSL = 2;
-      LRQ_TRY(launch((k_dequant_gemm_w<BITS, G, R, NW, NU, WRBW, WSL, F32>), dim3((nrb + WRBW - 1) / WRBW),
-                         dim3(NW * 64), 0, s, (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams,
-                         t->ld_qp, (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)a,
-                         out, ldo));
+      LRQ_TRY(launch((k_dequant_gemm_w<BITS, G, R, NW, NU, WRBW, WSL, F32, OUTL>), dim3((nrb + WRBW - 1) / WRBW),
+                     dim3(NW * 64), shm, s, (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams,
+                     t->ld_qp, (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)a, out,
+                     ldo, t->outlier_idx, (int)t->n_outlier, (const uint16_t*)t->side, t->ld_side));
       return LRQ_OK;
     };
     if (units == NW * 4) return wlaunch(std::integral_constant<int, 4>{});
     if (units == NW * 2) return wlaunch(std::integral_constant<int, 2>{});
     if (units == NW) return wlaunch(std::integral_constant<int, 1>{});
   }
-  LRQ_TRY(launch((k_dequant_gemm<BITS, G, R, NOUT, NW, RBW, SL, F32>), dim3((nrb + RBW - 1) / RBW), dim3(NW * 64), 0,
-                     s, (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
-                     (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)a, out, ldo));
+  LRQ_TRY(launch((k_dequant_gemm<BITS, G, R, NOUT, NW, RBW, SL, F32, OUTL>), dim3((nrb + RBW - 1) / RBW),
+                 dim3(NW * 64), shm, s, (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
+                 (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)a, out, ldo,
+                 t->outlier_idx, (int)t->n_outlier, (const uint16_t*)t->side, t->ld_side));
+  return LRQ_OK;
+}
+
+// Rotated format (no outlier channels; planes of whole rotation blocks).  Row blocks per
+// workgroup: as many as fit in about 64 KB of tiles (one to four).
+template <int BITS, int G, int R, int NOUT, bool F32>
+static int gemm_rot_launch(const lrq_tensors* t, const void* a, void* out, int64_t ldo, hipStream_t s) {
+  constexpr int NP = 8 / BITS, NW = 8;
+  constexpr int TILE = 16 * NP * (NW * G * 2 + 16);
+  constexpr int RBW = 4 * TILE <= 68 * 1024 ? 4 : 2 * TILE <= 68 * 1024 ? 2 : 1;
+  if (t->n_outlier != 0 || (t->hidden / NP) % 128 != 0) return LRQ_ERR_UNSUPPORTED;
+  const int M = (int)t->rows, N = (int)t->hidden;
+  const int nrb = (M + 15) / 16;
+  const size_t shm = (size_t)RBW * TILE;
+  auto kern = k_dequant_gemm_rot<BITS, G, R, NOUT, NW, RBW, F32>;
+  if (shm > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+  LRQ_TRY(launch(kern, dim3((nrb + RBW - 1) / RBW), dim3(NW * 64), shm, s, (const uint8_t*)t->codes, t->ld_codes,
+                 (const uint16_t*)t->qparams, t->ld_qp, (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N,
+                 (const uint16_t*)a, out, ldo));
   return LRQ_OK;
 }
 
 template <int BITS, int G, int R>
 static int gemm_nout(const lrq_tensors* t, const void* a, int n_out, void* out, int64_t ldo, bool f32, hipStream_t s) {
-  switch (n_out * 2 + (f32 ? 1 : 0)) {
-    case 16 * 2 + 1: return gemm_launch<BITS, G, R, 16, true>(t, a, out, ldo, s);
-    case 16 * 2: return gemm_launch<BITS, G, R, 16, false>(t, a, out, ldo, s);
-    case 32 * 2 + 1: return gemm_launch<BITS, G, R, 32, true>(t, a, out, ldo, s);
-    case 32 * 2: return gemm_launch<BITS, G, R, 32, false>(t, a, out, ldo, s);
+  if (t->flags & LRQ_FLAG_HADAMARD) {
+    switch (n_out * 2 + (f32 ? 1 : 0)) {
+      case 16 * 2 + 1: return gemm_rot_launch<BITS, G, R, 16, true>(t, a, out, ldo, s);
+      case 16 * 2: return gemm_rot_launch<BITS, G, R, 16, false>(t, a, out, ldo, s);
+      case 32 * 2 + 1: return gemm_rot_launch<BITS, G, R, 32, true>(t, a, out, ldo, s);
+      case 32 * 2: return gemm_rot_launch<BITS, G, R, 32, false>(t, a, out, ldo, s);
+      default: return LRQ_ERR_UNSUPPORTED;
+    }
+  }
+  const bool o = t->n_outlier > 0;
+  switch (n_out * 4 + (f32 ? 2 : 0) + (o ? 1 : 0)) {
+    case 16 * 4 + 2: return gemm_launch<BITS, G, R, 16, true, false>(t, a, out, ldo, s);
+    case 16 * 4 + 3: return gemm_launch<BITS, G, R, 16, true, true>(t, a, out, ldo, s);
+    case 16 * 4: return gemm_launch<BITS, G, R, 16, false, false>(t, a, out, ldo, s);
+    case 16 * 4 + 1: return gemm_launch<BITS, G, R, 16, false, true>(t, a, out, ldo, s);
+    case 32 * 4 + 2: return gemm_launch<BITS, G, R, 32, true, false>(t, a, out, ldo, s);
+    case 32 * 4 + 3: return gemm_launch<BITS, G, R, 32, true, true>(t, a, out, ldo, s);
+    case 32 * 4: return gemm_launch<BITS, G, R, 32, false, false>(t, a, out, ldo, s);
+    case 32 * 4 + 1: return gemm_launch<BITS, G, R, 32, false, true>(t, a, out, ldo, s);
     default: return LRQ_ERR_UNSUPPORTED;
   }
 }
@@ -1164,8 +1462,14 @@ extern "C" int lrq_softmax_bwd(const lrq_tensors* t, const void* dp, int64_t ldd
   if (st) return st;
   st = validate_rows16(ds, ldds, t->hidden);
   if (st) return st;
-  if ((t->flags & LRQ_FLAG_HADAMARD) || t->n_outlier > 0) return LRQ_ERR_UNSUPPORTED;
   if (t->rows == 0) return LRQ_OK;
+  if ((t->flags & LRQ_FLAG_HADAMARD) || t->n_outlier > 0) {
+    // the rotated format and outlier channels: decode into ds (rotation undone, side columns
+    // substituted), then the dense backward in place over it; rows of exactly `hidden` elements
+    if (lddp != t->hidden || ldds != t->hidden) return LRQ_ERR_UNSUPPORTED;
+    LRQ_TRY(lrq_decode(t, ds, ldds, stream));
+    return lrq_dense_softmax_bwd(ds, dp, ds, t->rows, t->hidden, stream);
+  }
   hipStream_t s = (hipStream_t)stream;
   LRQ_FORMATS(softmax_units, t, dp, lddp, ds, ldds, s)
 }
@@ -1178,7 +1482,7 @@ extern "C" int lrq_dequant_gemm(const lrq_tensors* t, const void* a, int32_t n_o
   if (n_out != 16 && n_out != 32) return LRQ_ERR_UNSUPPORTED;
   if (ldo < n_out) return LRQ_ERR_SHAPE;
   if (!aligned(a, 8) || !aligned(out, out_fp32 ? 4 : 2)) return LRQ_ERR_ALIGN;
-  if ((t->flags & LRQ_FLAG_HADAMARD) || t->n_outlier > 0) return LRQ_ERR_UNSUPPORTED;
+  if (t->n_outlier > kSideGemmMax) return LRQ_ERR_UNSUPPORTED;
   if (t->rows == 0) return LRQ_OK;
   hipStream_t s = (hipStream_t)stream;
   const bool f32 = out_fp32 != 0;

@@ -27,7 +27,10 @@ __device__ __forceinline__ u32x4 wht_base_operand(int i, int kg, int q0, bool ne
 // Rotate in place the 16 x 128 bf16 block whose lane (j, g) part (row j, columns 32g .. 32g+31)
 // starts at `base` in LDS: y = bf16(fp32(sum_k H[o, k] x[k]) * fp32(1/sqrt(128))).
 // op = the four wht_base_operand forms [q0][negated].
-__device__ __forceinline__ void wht128_lds(unsigned char* base, const u32x4 (&op)[2][2]) {
+// f(k, y + 8k) gives the 8 bf16 stored for the lane's columns 32g + 8k .. +7 from their fp32
+// rotated values (wht128_lds stores bf16(y); a fused consumer stores its result instead).
+template <class F>
+__device__ __forceinline__ void wht128_lds_map(unsigned char* base, const u32x4 (&op)[2][2], F f) {
   const float kScale = 0.08838834764831845f;  // fp32(1/sqrt(128))
   u32x4 xv[4];
 #pragma unroll
@@ -45,7 +48,11 @@ __device__ __forceinline__ void wht128_lds(unsigned char* base, const u32x4 (&op
     for (int v = 0; v < 4; ++v) out[4 * q + v] = acc[v] * kScale;
   }
 #pragma unroll
-  for (int k = 0; k < 4; ++k) *reinterpret_cast<u32x4*>(base + 16 * k) = pack8(out + 8 * k);
+  for (int k = 0; k < 4; ++k) *reinterpret_cast<u32x4*>(base + 16 * k) = f(k, out + 8 * k);
+}
+
+__device__ __forceinline__ void wht128_lds(unsigned char* base, const u32x4 (&op)[2][2]) {
+  wht128_lds_map(base, op, [](int, const float* y) { return pack8(y); });
 }
 
 }  // namespace lrq
