@@ -301,13 +301,15 @@ def encode(x_bits: np.ndarray, v_bits, bits: int = 4, group: int = 64, hadamard:
     """Group-mode encode of a bf16 activation x [M, N] (no reference function; north-star format).
 
     Steps (all on the CPU, float32 unless stated):
-      Y  = bf16(wht128_rows(x)) if hadamard else fp32(x)   (the rotated activation is bf16)
-      side[:, k] = fp16(x[:, idx[k]]); Y[:, idx] = 0            (outlier channels, if any)
+      side[:, k] = fp16(x[:, idx[k]])                            (outlier channels, if any)
+      Y  = bf16(wht128_rows(x with the idx columns zeroed)) if hadamard, else fp32(x) with
+           Y[:, idx] = 0   (the rotated activation is bf16; the channels leave before the
+                            rotation, which would otherwise spread them over their blocks)
       L  = bf16(fp32(exact(Y @ V)))                              (if rank > 0)
       R  = fp32(exact(Y - L @ V^T))   (one rounding: the kernels form it as an MFMA whose
                                        accumulator input is Y, the same form the decode
                                        uses for Y'; else R = Y)
-      R[:, idx] = 0
+      R[:, idx] = 0   (not rotated: the rotated columns are all quantised)
       codes, scale, zero = quant_groups(R)
       packed = pack_rowplanar(codes)
     Returns a dict with the format (L, codes, scale, zero, side, idx) and the
@@ -318,14 +320,20 @@ def encode(x_bits: np.ndarray, v_bits, bits: int = 4, group: int = 64, hadamard:
     x_bits = np.asarray(x_bits, dtype=np.uint16)
     m, n = x_bits.shape
     x = bf16_to_f32(x_bits)
-    y = bf16_to_f32(wht128_bf16(x_bits)) if hadamard else x.copy()
     idx = None
     side = None
     if outlier_idx is not None and len(outlier_idx) > 0:
         idx = np.asarray(outlier_idx, dtype=np.int32)
-        assert not hadamard, "outlier channels combine with the rotation only in rank-0 form here"
         side = x[:, idx].astype(np.float16)
-        y[:, idx] = 0.0
+    if hadamard:
+        xm = x_bits.copy()
+        if idx is not None:
+            xm[:, idx] = 0
+        y = bf16_to_f32(wht128_bf16(xm))
+    else:
+        y = x.copy()
+        if idx is not None:
+            y[:, idx] = 0.0
     rank = 0 if v_bits is None else int(np.asarray(v_bits).shape[1])
     if rank > 0:
         if l_override is None:
@@ -337,7 +345,7 @@ def encode(x_bits: np.ndarray, v_bits, bits: int = 4, group: int = 64, hadamard:
     else:
         l_bits, l32, p = None, None, None
         r = y
-    if idx is not None:
+    if idx is not None and not hadamard:
         r[:, idx] = 0.0
     codes, scale, zero, t = quant_groups(r, bits, group)
     return dict(L=l_bits, codes=pack_rowplanar(codes, bits), scale=scale, zero=zero, side=side,
@@ -354,10 +362,12 @@ def reconstruct_f32(l_bits, v_bits, packed, scale, zero, bits: int, group: int, 
     y = dequant_groups(codes, scale, zero, group)
     if l_bits is not None and v_bits is not None and np.asarray(v_bits).shape[1] > 0:
         y = (y.astype(np.float64) + lowrank_product(l_bits, v_bits)).astype(np.float32)  # one rounding
-    if idx is not None and len(idx) > 0:
-        y[:, np.asarray(idx)] = np.asarray(side, dtype=np.float16).astype(np.float32)
+    has_side = idx is not None and len(idx) > 0
     if hadamard:
+        # rotate back, then the side columns (they were taken out before the rotation)
         y = wht128_rows(bf16_to_f32(bf16_round(y)))
+    if has_side:
+        y[:, np.asarray(idx)] = np.asarray(side, dtype=np.float16).astype(np.float32)
     return y
 
 
@@ -367,8 +377,9 @@ def decode(l_bits, v_bits, packed, scale, zero, bits: int, group: int, hadamard=
 
       d  = fp32(code) * scale + zero
       Y' = fp32(exact(d + L @ V^T))   (one rounding; rank > 0)
-      Y'[:, idx] = side     (outlier channels)
-      X' = wht128_rows(bf16(Y'))  (rotation is its own inverse; it takes bf16 input)
+      Y'[:, idx] = side     (outlier channels; the plain format)
+      X' = wht128_rows(bf16(Y')), then X'[:, idx] = side   (the rotated format: the rotation is
+           its own inverse, takes bf16 input, and the side columns enter after it)
     Returns bf16 bits [M, N].
     """
     return bf16_round(reconstruct_f32(l_bits, v_bits, packed, scale, zero, bits, group, hadamard,

@@ -73,12 +73,12 @@ def encode(x: torch.Tensor, V: torch.Tensor | None, bits: int = 4, group: int = 
     """Group-mode encode of a bf16 x [M, N] on the CPU (``lrq_oracle.encode``, fp32 sums)."""
     m, n = x.shape
     y = x.float()
-    if hadamard:
-        y = wht128(y).bfloat16().float()
     side = None
     if outlier_idx is not None and outlier_idx.numel() > 0:
         side = x[:, outlier_idx.long()].half()
-        y[:, outlier_idx.long()] = 0.0
+        y[:, outlier_idx.long()] = 0.0  # before the rotation
+    if hadamard:
+        y = wht128(y).bfloat16().float()
     L = None
     if V is not None:
         v = V.float()
@@ -86,7 +86,7 @@ def encode(x: torch.Tensor, V: torch.Tensor | None, bits: int = 4, group: int = 
         r = y - L.float() @ v.T
     else:
         r = y
-    if side is not None:
+    if side is not None and not hadamard:
         r[:, outlier_idx.long()] = 0.0
     qmax = (1 << bits) - 1
     rg = r.reshape(m, n // group, group)
@@ -103,19 +103,21 @@ def encode(x: torch.Tensor, V: torch.Tensor | None, bits: int = 4, group: int = 
 
 def decode(e: dict, V: torch.Tensor | None, bits: int, group: int, hadamard: bool = False) -> torch.Tensor:
     """Group-mode decode (``lrq_oracle.decode``): bf16(codes*scale + zero + L V^T), side
-    columns substituted, the rotation undone on the bf16 result."""
+    columns substituted (the rotated format: the rotation undone on the bf16 result first)."""
     codes = unpack_rowplanar(e["codes"], bits)
     m, n = codes.shape
     y = (codes.float().reshape(m, n // group, group) * e["scale"].float()[..., None]
          + e["zero"].float()[..., None]).reshape(m, n)
     if V is not None and e["L"] is not None:
         y = torch.addmm(y, e["L"].float(), V.float().T)
-    if e.get("side") is not None:
-        y[:, e["idx"].long()] = e["side"].float()
-    out = y.bfloat16()
+    side = e.get("side")
+    if side is not None and not hadamard:
+        y[:, e["idx"].long()] = side.float()
     if hadamard:
-        out = wht128(out.float()).bfloat16()
-    return out
+        y = wht128(y.bfloat16().float())
+        if side is not None:
+            y[:, e["idx"].long()] = side.float()  # after the rotation
+    return y.bfloat16()
 
 
 def silu_bwd(x: torch.Tensor, dy: torch.Tensor) -> torch.Tensor:

@@ -173,3 +173,57 @@ def test_rotated_dequant_gemm_straddling_planes(pkg, dev):
     c = pkg.encode(x.to(dev), None, bits=4, group_size=64, hadamard=True)
     with pytest.raises(ValueError, match="lrq_dequant_gemm"):
         pkg.dequant_gemm(c, torch.zeros(384, 16, dtype=torch.bfloat16, device=dev))
+
+
+@pytest.mark.parametrize("rows,n,rank,bits,group,k", [
+    (64, 5120, 16, 4, 64, 16),    # config 4 with its 16 outlier channels kept as side columns
+    (40, 2048, 0, 4, 64, 9),      # rank 0
+    (30, 2048, 32, 4, 64, 5),     # rank 32
+    (36, 2048, 16, 8, 128, 12),   # int8 / g128
+    (20, 2048, 16, 4, 64, 100),   # more side columns than the row decode stages
+])
+def test_outliers_with_rotation(pkg, dev, rows, n, rank, bits, group, k):
+    """Outlier channels on the rotated format: they leave X before the rotation (fp16 side
+    columns of the original values) and return after the inverse rotation.  Encode against
+    the oracle (L within an ulp, codes given the device L), decode within the rotated bar with the
+    side columns exact, a fused consumer bit-identical to the dense op on the device decode, and
+    the dequant-GEMM (up to 64 channels) within the fp32 accumulation bound."""
+    print(f"[outliers+rot] rows={rows} n={n} rank={rank} int{bits}/g{group} k={k}", flush=True)
+    x = pkg.inputs.activation(rows, n, k, 40.0, seed=k + rank)
+    V = pkg.inputs.basis(n, rank, seed=k) if rank else None
+    xb = bits16(x)
+    vb = bits16(V) if rank else None
+    idx = O.topk_channels(O.colmax_abs(xb), k)
+    c = pkg.encode(x.to(dev), V.to(dev) if V is not None else None, bits=bits, group_size=group, hadamard=True,
+                   outlier_idx=torch.as_tensor(idx, dtype=torch.int32, device=dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(f16(c.side).view(np.uint16), O.bf16_to_f32(xb[:, idx]).astype(np.float16).view(np.uint16))
+    ref_full = O.encode(xb, vb, bits, group, hadamard=True, outlier_idx=idx)
+    if rank:
+        lg = bits16(c.L)
+        d = ulp_diff_bf16(lg, ref_full["L"])
+        assert d.max() <= 1 and (d > 0).sum() <= max(2, 1e-3 * d.size)
+    ref = O.encode(xb, vb, bits, group, hadamard=True, outlier_idx=idx, l_override=bits16(c.L) if rank else None)
+    codes = c.codes.cpu().numpy()
+    rep = assert_codes(codes, ref, bits, what="rotated codes with side columns | device L")
+    print(f"[outliers+rot] codes {rep}", flush=True)
+    xh = pkg.decode(c)
+    dy = pkg.inputs.gradient((rows, n), 0.02, seed=k)
+    dx = pkg.silu_backward_compressed(c, dy.to(dev))
+    dense = pkg.triton_silu_backward(xh, dy.to(dev))
+    torch.cuda.synchronize()
+    ref_xh = O.decode(bits16(c.L) if rank else None, vb, codes, f16(c.scale), f16(c.zero), bits, group,
+                      hadamard=True, side=f16(c.side), idx=idx)
+    assert np.array_equal(bits16(xh)[:, idx], ref_xh[:, idx])
+    print(f"[outliers+rot] decode {assert_rotated_close(bits16(xh), ref_xh, 'rotated decode with side columns')}",
+          flush=True)
+    assert np.array_equal(bits16(dx), bits16(dense))
+    if k <= 64:
+        a = (torch.randn(n, 16, generator=torch.Generator().manual_seed(k)) / np.sqrt(n)).to(torch.bfloat16)
+        out = pkg.dequant_gemm(c, a.to(dev))
+        torch.cuda.synchronize()
+        xd = O.bf16_to_f32(bits16(xh)).astype(np.float64)
+        af = O.bf16_to_f32(bits16(a)).astype(np.float64)
+        err = np.abs(out.cpu().numpy().astype(np.float64) - xd @ af)
+        bound = 1e-5 * (np.abs(xd) @ np.abs(af)) + 1e-9
+        assert (err <= bound).all(), float((err / bound).max())

@@ -412,6 +412,7 @@ def test_to_coo_matches_torch_to_sparse(shape):
     (64, 1024, 32, 8, 128, True, 0),
     (64, 1024, 0, 8, 128, False, 9),
     (128, 2048, 16, 4, 64, False, 5),
+    (64, 1024, 16, 4, 64, True, 7),
 ])
 def test_torch_restatement_matches_oracle(pkg, rows, hidden, rank, bits, group, hadamard, k):
     """oracle/lrq_torch.py (the CPU baseline bench.py times) computes what lrq_oracle computes:
@@ -469,3 +470,35 @@ def test_torch_restatement_consumers_and_legacy(pkg):
         xh = T.legacy_decode(l, r, q, o, s, bits)
         d = ulp_diff_bf16(bits16(xh), O.legacy_decode(bits16(l), bits16(r), rq, ro, bits16(s), bits))
         assert d.max() <= 1 and (d > 0).mean() <= 1e-4
+
+
+@pytest.mark.parametrize("rank", [0, 16])
+def test_outliers_with_rotation_compose(pkg, rank):
+    """Outlier channels on the rotated format: the channels leave before the rotation.  Pinned
+    by composition: the encode equals the rotated encode of x with those columns zeroed (plus
+    the fp16 side columns of the original x), and the decode equals the rotated decode of that
+    encode with the side columns written over its idx columns afterwards.  Dropping the zeroing,
+    or substituting before the rotation, fails one of these."""
+    x = pkg.inputs.activation(48, 1024, 6, 40.0, seed=11)
+    xb = O.bf16_round(x.float().numpy())
+    vb = O.bf16_round(pkg.inputs.basis(1024, rank, seed=11).float().numpy()) if rank else None
+    idx = O.topk_channels(O.colmax_abs(xb), 6)
+    e = O.encode(xb, vb, 4, 64, hadamard=True, outlier_idx=idx)
+    xm = xb.copy()
+    xm[:, idx] = 0
+    e0 = O.encode(xm, vb, 4, 64, hadamard=True)
+    assert np.array_equal(e["codes"], e0["codes"])
+    assert np.array_equal(e["scale"].view(np.uint16), e0["scale"].view(np.uint16))
+    if rank:
+        assert np.array_equal(e["L"], e0["L"])
+    assert np.array_equal(e["side"], O.bf16_to_f32(xb[:, idx]).astype(np.float16))
+    d = O.decode(e["L"], vb, e["codes"], e["scale"], e["zero"], 4, 64, hadamard=True, side=e["side"], idx=idx)
+    d0 = O.decode(e0["L"], vb, e0["codes"], e0["scale"], e0["zero"], 4, 64, hadamard=True)
+    rest = np.setdiff1d(np.arange(1024), idx)
+    assert np.array_equal(d[:, rest], d0[:, rest])
+    assert np.array_equal(d[:, idx], O.bf16_round(e["side"].astype(np.float32)))
+    # the outlier channels come back exactly where fp16 holds them; the rest at the quantiser's scale
+    xf = O.bf16_to_f32(xb).astype(np.float64)
+    err = O.bf16_to_f32(d).astype(np.float64) - xf
+    assert np.abs(err[:, idx]).max() <= 2.0 ** -11 * np.abs(xf[:, idx]).max()
+    assert np.linalg.norm(err) / np.linalg.norm(xf) < 0.1

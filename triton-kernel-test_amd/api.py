@@ -205,9 +205,6 @@ def encode(x: torch.Tensor, basis: Optional[LowRankBasis | torch.Tensor] = None,
         _require_device(outlier_idx)
         outlier_idx = outlier_idx.to(torch.int32).contiguous()
     k = 0 if outlier_idx is None else outlier_idx.numel()
-    if hadamard and k:
-        # the side columns would hold rotated values that no decode-side entry point accepts
-        raise ValueError("encode: outlier channels do not combine with the rotated (hadamard) format")
     bufs = _alloc(rows, n, bits, group_size, rank, k, x.device)
     c = CompressedActivation(codes=bufs["codes"], qparams=bufs["qparams"], L=bufs["L"],
                              basis=basis, side=bufs["side"], idx=outlier_idx if k else None,
@@ -219,7 +216,8 @@ def encode(x: torch.Tensor, basis: Optional[LowRankBasis | torch.Tensor] = None,
             # descriptor); otherwise y = bf16(WHT128(x)) into a temporary, then the plain encode
             t.flags = _lib.LRQ_FLAG_HADAMARD
             st = _lib.call_raw("lrq_encode", ctypes.byref(t), _p(x2), ldx, _stream(x.device))
-            if st != _lib.LRQ_ERR_UNSUPPORTED:
+            if st != _lib.LRQ_ERR_UNSUPPORTED or k:
+                # (outlier channels leave X before the rotation: no rotated copy can stand in)
                 _lib.check(st, "lrq_encode")
                 return c
             t.flags = 0

@@ -666,7 +666,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
       for (int p = 0; p < NP; ++p) {
         float xh[E];
         reconstruct_plane<BITS, G, R>(cb, qp[p], p, vop[p], lop, xh);
-        if constexpr (OUTL) {
+        if constexpr (OUTL && !EPI::kRot) {  // (the rotated format: after the rotation, below)
           // the lane's outlier columns one by one (usually none or one): a select over the E
           // values per outlier, instead of a test, a table read and a select per value
           const int c0 = unit_base(p, u, N, NP, G) + E * g;  // E consecutive columns in one mask word
@@ -693,11 +693,38 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
       lds_barrier();  // every wave's unit of block b is in the tile
       if (rot_live) {
         const int roff = (rot_p * 16 + j) * Ro::OPAD + (128 * rot_q + 32 * g) * 2;
+        // OUTL: the side columns enter after the rotation; the lane's 32 columns c0 .. c0+31 of
+        // the block share one mask word
+        const int c0 = unit_base(rot_p, u0, N, NP, G) + 128 * rot_q + 32 * g;
+        const uint32_t mword = OUTL ? colmask[c0 >> 5] : 0u;
+        const uint16_t* ss = reinterpret_cast<const uint16_t*>(ism + (b & 1) * Lay::ISLOT + Tl::SLOT) + j * kSideMax;
+        auto subst = [&](int k, const float* y, float* o) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = y[e];
+          if constexpr (OUTL) {
+            uint32_t m8 = (mword >> (8 * k)) & 0xffu;
+            while (m8 != 0u) {
+              const int e0 = __builtin_ctz(m8);
+              m8 &= m8 - 1u;
+              const float v = f16_val(ss[oslot[c0 + 8 * k + e0]]);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) o[e] = e == e0 ? v : o[e];
+            }
+          }
+        };
         if constexpr (IN) {
           // the consumer's second tensor sits at the same place in the input tile
           const unsigned char* rd = dsm + (b & 1) * Ro::OSLOT + roff;
           wht128_lds_map(osm + (b & 1) * Ro::OSLOT + roff, wop, [&](int k, const float* y) {
-            return epi.rot_apply(y, *reinterpret_cast<const u32x4*>(rd + 16 * k));
+            float o[8];
+            subst(k, y, o);
+            return epi.rot_apply(o, *reinterpret_cast<const u32x4*>(rd + 16 * k));
+          });
+        } else if constexpr (OUTL) {
+          wht128_lds_map(osm + (b & 1) * Ro::OSLOT + roff, wop, [&](int k, const float* y) {
+            float o[8];
+            subst(k, y, o);
+            return pack8(o);
           });
         } else {
           wht128_lds(osm + (b & 1) * Ro::OSLOT + roff, wop);
@@ -730,8 +757,14 @@ static int decode_rows_launch(const lrq_tensors* t, hipStream_t s, const EPI& ep
   using Lay = RowsLayout<BITS, G, R, NW, EPI::kIn, OUTL, INP>;
   constexpr int kBudget = EPI::kIn ? 100 : EPI::kRot ? 150 : R == 32 ? 160 : 180;
   constexpr int kFit = kBudget / Lay::kRegsPerBlock;
-  // (a rotated consumer at rank 32 also holds the rotation operands: two blocks in flight)
-  constexpr int PD = (EPI::kIn && EPI::kRot && R == 32) ? 2 : kFit >= 16 ? 16 : kFit >= 8 ? 8 : kFit >= 4 ? 4 : 2;
+  // (a rotated consumer at rank 32, or with side columns, also holds the rotation operands and
+  // the substitution's state: two blocks in flight; the rotated decode with side columns: four)
+  constexpr int PD = (EPI::kIn && EPI::kRot && (R == 32 || OUTL)) ? 2
+                     : (EPI::kRot && OUTL)                           ? 4
+                     : kFit >= 16                                    ? 16
+                     : kFit >= 8                                     ? 8
+                     : kFit >= 4                                     ? 4
+                                                                     : 2;
   const int M = (int)t->rows, N = (int)t->hidden;
   const int units = N / (G * (8 / BITS));
   const int64_t ug = (units + NW - 1) / NW, nrb = (M + 15) / 16, cus = cu_count();
@@ -826,45 +859,64 @@ static int check_io(const lrq_tensors* t, const void* in, int64_t ldin, const vo
 using namespace lrq;
 
 namespace lrq {
-// Rotated format, fused: the row kernel undoes the rotation on its LDS output tile.  Formats
-// with one 128-column rotation block per wave (int4/g64, int8/g128), no outlier channels, and
-// planes that are whole rotation blocks; returns 0 for the others.
+// Rotated format, fused: the row kernel undoes the rotation on its LDS output tile, then writes
+// the side columns over it.  Formats with one 128-column rotation block per wave (int4/g64,
+// int8/g128), up to kSideMax outlier channels, and planes that are whole rotation blocks;
+// returns 0 for the others.
 template <int BITS, int G, int R>
 static int decode_rot_fused(const lrq_tensors* t, hipStream_t s, uint16_t* out, int64_t ldo, int* status) {
   if constexpr (!((BITS == 4 && G == 64) || (BITS == 8 && G == 128))) {
     return 0;
   } else {
     const int64_t plane = t->hidden / (8 / BITS);
-    if (t->n_outlier != 0 || plane % 128 != 0) return 0;
-    for (int64_t ldb : {t->ld_codes, 2 * t->ld_qp, 2 * t->ld_L, 2 * ldo})
+    if (t->n_outlier > kSideMax || plane % 128 != 0) return 0;
+    for (int64_t ldb : {t->ld_codes, 2 * t->ld_qp, 2 * t->ld_L, 2 * ldo, 2 * t->ld_side})
       if (16 * ldb >= ((int64_t)1 << 31)) return 0;
     lrq_tensors plain = *t;
     plain.flags &= ~LRQ_FLAG_HADAMARD;
     EpiStoreRot epi;
     epi.out = out;
     epi.ld = ldo;
-    *status = decode_rows_launch<BITS, G, R, false>(&plain, s, epi);
+    const int st = t->n_outlier > 0 ? decode_rows_launch<BITS, G, R, true>(&plain, s, epi)
+                                    : decode_rows_launch<BITS, G, R, false>(&plain, s, epi);
+    if (st == LRQ_ERR_UNSUPPORTED) return 0;  // its tiles do not fit in LDS
+    *status = st;
     return 1;
   }
 }
 
+// out[r, idx[k]] = bf16(side[r, k]) (indices outside [0, N) skipped): the side columns of the
+// rotated format, written after the separate rotation pass.
+__global__ __launch_bounds__(256) void k_scatter_side(const uint16_t* __restrict__ side, int64_t ldside, int M, int N,
+                                                      const int32_t* __restrict__ oidx, int nout,
+                                                      uint16_t* __restrict__ out, int64_t ldo) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)M * nout) return;
+  const int64_t r = i / nout;
+  const int k = (int)(i - r * nout);
+  const int c = oidx[k];
+  if (c < 0 || c >= N) return;
+  out[r * ldo + c] = (uint16_t)pack_bf16x2(f16_val(side[r * ldside + k]), 0.f);
+}
+
 // Rotated format with a consumer, fused into the row kernel (EpiRot): int4/g64 (int8/g128's
-// row kernel has no LDS left for the consumer's own tiles), no outlier channels, planes of whole
-// rotation blocks; returns 0 for the others.
+// row kernel has no LDS left for the consumer's own tiles), up to kSideMax outlier channels,
+// planes of whole rotation blocks; returns 0 for the others.
 template <int BITS, int G, int R, class EPI>
 static int consumer_rot_fused(const lrq_tensors* t, hipStream_t s, const EPI& inner, int* status) {
   if constexpr (!(BITS == 4 && G == 64)) {
     return 0;
   } else {
     const int64_t plane = t->hidden / (8 / BITS);
-    if (t->n_outlier != 0 || plane % 128 != 0) return 0;
-    for (int64_t ldb : {t->ld_codes, 2 * t->ld_qp, 2 * t->ld_L, 2 * inner.in_ld(), 2 * inner.out_ld()})
+    if (t->n_outlier > kSideMax || plane % 128 != 0) return 0;
+    for (int64_t ldb : {t->ld_codes, 2 * t->ld_qp, 2 * t->ld_L, 2 * inner.in_ld(), 2 * inner.out_ld(), 2 * t->ld_side})
       if (16 * ldb >= ((int64_t)1 << 31)) return 0;
     lrq_tensors plain = *t;
     plain.flags &= ~LRQ_FLAG_HADAMARD;
     EpiRot<EPI> epi;
     static_cast<EPI&>(epi) = inner;
-    const int st = decode_rows_launch<BITS, G, R, false>(&plain, s, epi);
+    const int st = t->n_outlier > 0 ? decode_rows_launch<BITS, G, R, true>(&plain, s, epi)
+                                    : decode_rows_launch<BITS, G, R, false>(&plain, s, epi);
     if (st == LRQ_ERR_UNSUPPORTED) return 0;
     *status = st;
     return 1;
@@ -899,12 +951,19 @@ extern "C" int lrq_decode(const lrq_tensors* t, void* out, int64_t ldo, void* st
   if (t->rows == 0) return LRQ_OK;
   if (t->flags & LRQ_FLAG_HADAMARD) {
     if (decode_rot(t, (hipStream_t)stream, (uint16_t*)out, ldo, &st)) return st;
-    // otherwise decode, then undo the rotation in place (the rotation is its own inverse)
+    // otherwise decode, undo the rotation in place (the rotation is its own inverse), then
+    // write the side columns
     lrq_tensors plain = *t;
     plain.flags &= ~LRQ_FLAG_HADAMARD;
-    st = decode_dispatch(&plain, (hipStream_t)stream, EpiStore{(uint16_t*)out, ldo});
-    if (st) return st;
-    return lrq_wht128(out, ldo, t->rows, t->hidden, out, ldo, stream);
+    plain.n_outlier = 0;
+    LRQ_TRY(decode_dispatch(&plain, (hipStream_t)stream, EpiStore{(uint16_t*)out, ldo}));
+    LRQ_TRY(lrq_wht128(out, ldo, t->rows, t->hidden, out, ldo, stream));
+    if (t->n_outlier == 0) return LRQ_OK;
+    const int64_t n = t->rows * t->n_outlier;
+    LRQ_TRY(launch(k_scatter_side, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                   (const uint16_t*)t->side, t->ld_side, (int)t->rows, (int)t->hidden, t->outlier_idx,
+                   (int)t->n_outlier, (uint16_t*)out, ldo));
+    return LRQ_OK;
   }
   return decode_dispatch(t, (hipStream_t)stream, EpiStore{(uint16_t*)out, ldo});
 }

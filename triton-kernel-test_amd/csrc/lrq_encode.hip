@@ -700,8 +700,11 @@ __global__ __launch_bounds__(512) void k_project_slab(const uint16_t* __restrict
       const int c = c0 + 32 * k + 8 * g;
       vt[k][t] = c < N ? ld16(Vt + (int64_t)(16 * t + j) * N + c) : u32x4{0u, 0u, 0u, 0u};
     }
+  // the lane's 8 columns of X as kept (ROT && OUTL: outlier columns zeroed before the rotation)
+  uint32_t xkeep[4] = {~0u, ~0u, ~0u, ~0u};
+  const int lr = lane >> 5;
+  const uint32_t lcol = (uint32_t)min(c0 + (lane & 31) * 8, N - 8) * 2u;
   if constexpr (OUTL) {
-    // outlier columns meet zero V^T operands: the projection of Y with those columns zeroed
     for (int i = threadIdx.x; i < N / 32; i += 512) pmask[i] = 0u;
     __syncthreads();
     for (int k = threadIdx.x; k < nout; k += 512) {
@@ -709,6 +712,17 @@ __global__ __launch_bounds__(512) void k_project_slab(const uint16_t* __restrict
       if (c >= 0 && c < N) atomicOr(&pmask[c >> 5], 1u << (c & 31));
     }
     __syncthreads();
+  }
+  if constexpr (OUTL && ROT) {
+    // the rotated format: the channels leave X before the rotation (the rotated columns are all
+    // projected)
+    const int c = (int)(lcol / 2u);  // 8 columns inside one mask word
+    const uint32_t b8 = (pmask[c >> 5] >> (c & 31)) & 0xffu;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      xkeep[d] = (((b8 >> (2 * d)) & 1u) ? 0u : 0x0000ffffu) | (((b8 >> (2 * d + 1)) & 1u) ? 0u : 0xffff0000u);
+  } else if constexpr (OUTL) {
+    // outlier columns meet zero V^T operands: the projection of Y with those columns zeroed
 #pragma unroll
     for (int k = 0; k < CW / 32; ++k) {
       const int c = c0 + 32 * k + 8 * g;  // 8 columns inside one mask word
@@ -724,8 +738,6 @@ __global__ __launch_bounds__(512) void k_project_slab(const uint16_t* __restrict
   }
   // load i: rows 2i, 2i+1 of the block, lane l -> row 2i + l/32, bytes (l%32)*16 of the slice
   // (clamped to column N - 8 past the end: those columns meet zero operands)
-  const int lr = lane >> 5;
-  const uint32_t lcol = (uint32_t)min(c0 + (lane & 31) * 8, N - 8) * 2u;
   auto gaddr = [&](int rb, int i) {
     const int64_t row = min(rb * 16 + 2 * i + lr, M - 1);
     return reinterpret_cast<const unsigned char*>(X + row * ldx) + lcol;
@@ -743,8 +755,11 @@ __global__ __launch_bounds__(512) void k_project_slab(const uint16_t* __restrict
     for (int t = 0; t < RT; ++t) acc[t] = zero4();
     if (live) {
 #pragma unroll
-      for (int i = 0; i < NLD; ++i)
-        *reinterpret_cast<u32x4*>(region + (2 * i + lr) * PITCH + (lane & 31) * 16) = pf[i];
+      for (int i = 0; i < NLD; ++i) {
+        u32x4 v = pf[i];
+        if constexpr (OUTL && ROT) v = u32x4{v[0] & xkeep[0], v[1] & xkeep[1], v[2] & xkeep[2], v[3] & xkeep[3]};
+        *reinterpret_cast<u32x4*>(region + (2 * i + lr) * PITCH + (lane & 31) * 16) = v;
+      }
       if constexpr (ROT) {
 #pragma unroll
         for (int q = 0; q < CW / 128; ++q)
@@ -852,8 +867,8 @@ __global__ __launch_bounds__(512) void k_quant_slab(const uint16_t* __restrict__
   const int nblk = min(RBW, nrb - rb0);
   unsigned char* region = shm + (size_t)w * 16 * PITCH;
   // ROT: the slice is rotated in place (WHT-128 per 128-column block of each plane) before use;
-  // the host guarantees that the wave's columns of each plane start on a block boundary
-  static_assert(!(ROT && OUTL), "the rotated format has no outlier channels");
+  // the host guarantees that the wave's columns of each plane start on a block boundary.  With
+  // OUTL the side columns are taken from the slice and zeroed in it before the rotation.
   static_assert(!ROT || (UPW * G) % 128 == 0, "whole rotation blocks per wave and plane");
   u32x4 wop[ROT ? 2 : 1][2];
   if constexpr (ROT) {
@@ -890,13 +905,42 @@ __global__ __launch_bounds__(512) void k_quant_slab(const uint16_t* __restrict__
       for (int t = 0; t < RT; ++t) lnext[t] = ld8(Lin + row * ldl + 16 * t + 4 * g);
     }
   };
+  // side columns of the wave's units, read from the slice (lanes of quarter 0 store row j); a
+  // wave-uniform loop over the wave's outlier columns, one range-checked 2-byte store per row.
+  // zero: the columns are then zeroed in the slice (every lane of row j writes the same 0).
+  auto side_pass = [&](int rb, int row, bool zero) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(side + (int64_t)rb * 16 * ldside, (short)0, (int)(16 * ldside * 2), 0x00020000);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int cb = unit_base(p, ub, N, NP, G);  // the wave's UPW*G contiguous columns of plane p
+#pragma unroll 1
+      for (int wd = 0; wd < UPW * G / 32; ++wd) {
+        uint32_t bits = __builtin_amdgcn_readfirstlane(colmask[(cb >> 5) + wd]);
+        while (bits != 0u) {
+          const int e = __builtin_ctz(bits);
+          bits &= bits - 1u;
+          const int cl = 32 * wd + e;  // column within the wave's range
+          const int k = oslot[cb + cl];
+          uint16_t* px = reinterpret_cast<uint16_t*>(region + j * PITCH + p * PIECE + cl * 2);
+          const uint32_t v = *px;
+          const uint16_t h = (uint16_t)f16_bits(__uint_as_float(v << 16));
+          __builtin_amdgcn_raw_buffer_store_b16(h, rs, g == 0 ? (uint32_t)(((row - rb * 16) * ldside + k) * 2) : 0x7ffffff0u,
+                                                0, 0);
+          if (zero) *px = 0;
+        }
+      }
+    }
+  };
   issue(rb0);
 #pragma unroll 1
   for (int b = 0; b < nblk; ++b) {
     const int rb = rb0 + b;
+    const int row = min(rb * 16 + j, M - 1);
 #pragma unroll
     for (int i = 0; i < NLD; ++i)
       *reinterpret_cast<u32x4*>(region + (RPL * i + lrow) * PITCH + (lpc % NP) * PIECE + loff) = pf[i];
+    if constexpr (OUTL && ROT) side_pass(rb, row, true);
     if constexpr (ROT) {
 #pragma unroll
       for (int p = 0; p < NP; ++p)
@@ -917,12 +961,12 @@ __global__ __launch_bounds__(512) void k_quant_slab(const uint16_t* __restrict__
       for (int t = 0; t < RT; ++t) lopn[t] = neg_bf16x4(lnext[t]);
     }
     if (b + 1 < nblk) issue(rb + 1);
-    const int row = min(rb * 16 + j, M - 1);
     uint8_t* crow = codes + (int64_t)row * ldc;
     uint32_t qp[UPW];
 #pragma unroll
     for (int uu = 0; uu < UPW; ++uu)
-      qp[uu] = quant_unit_core<BITS, G, R>(x[uu], vop[uu], lopn, OUTL ? colmask : nullptr, ub + uu, N, g, crow);
+      qp[uu] = quant_unit_core<BITS, G, R>(x[uu], vop[uu], lopn, (OUTL && !ROT) ? colmask : nullptr, ub + uu, N, g,
+                                           crow);
     if constexpr (NP == 2) {
       // the two units' (scale, zero) pairs of the row as one 16-byte store (see k_encode_rows)
       float a = __uint_as_float(qp[0]), bq = a, c = __uint_as_float(qp[1]), d = c;
@@ -936,29 +980,7 @@ __global__ __launch_bounds__(512) void k_quant_slab(const uint16_t* __restrict__
       st8_pred(qparams + (int64_t)rb * 16 * ldq, (uint32_t)(16 * ldq * 2),
                (uint32_t)(((row - rb * 16) * ldq + ub * 2) * 2), u32x2{qp[0], qp[1]}, g == 0);
     }
-    if constexpr (OUTL) {
-      // side columns of the wave's units, read from the slice (lanes of quarter 0 store row j)
-      const __amdgpu_buffer_rsrc_t rs =
-          __builtin_amdgcn_make_buffer_rsrc(side + (int64_t)rb * 16 * ldside, (short)0, (int)(16 * ldside * 2), 0x00020000);
-#pragma unroll
-      for (int p = 0; p < NP; ++p) {
-        const int cb = unit_base(p, ub, N, NP, G);  // the wave's UPW*G contiguous columns of plane p
-#pragma unroll 1
-        for (int wd = 0; wd < UPW * G / 32; ++wd) {
-          uint32_t bits = __builtin_amdgcn_readfirstlane(colmask[(cb >> 5) + wd]);
-          while (bits != 0u) {
-            const int e = __builtin_ctz(bits);
-            bits &= bits - 1u;
-            const int cl = 32 * wd + e;  // column within the wave's range
-            const int k = oslot[cb + cl];
-            const uint32_t v = *reinterpret_cast<const uint16_t*>(region + j * PITCH + p * PIECE + cl * 2);
-            const uint16_t h = (uint16_t)f16_bits(__uint_as_float(v << 16));
-            __builtin_amdgcn_raw_buffer_store_b16(h, rs, g == 0 ? (uint32_t)(((row - rb * 16) * ldside + k) * 2) : 0x7ffffff0u,
-                                                  0, 0);
-          }
-        }
-      }
-    }
+    if constexpr (OUTL && !ROT) side_pass(rb, row, false);
   }
 }
 
@@ -1094,7 +1116,7 @@ static int encode_slabs(const lrq_tensors* t, const void* x, int64_t ldx, hipStr
   const bool outl = t->n_outlier > 0;
   if (units % 2 != 0 || N % 32 != 0) return 0;
   // rotated input: every wave's columns start on a 128-column block of their plane
-  if (ROT && (outl || (N / NP) % 128 != 0 || (2 * G) % 128 != 0 || (NP == 2 && G == 128))) return 0;
+  if (ROT && ((N / NP) % 128 != 0 || (2 * G) % 128 != 0 || (NP == 2 && G == 128))) return 0;
   if (outl && (t->n_outlier > 32767 || t->side == nullptr || t->outlier_idx == nullptr)) return 0;
   if (NP == 2 ? (t->ld_qp % 8 != 0 || !aligned(t->qparams, 16)) : (t->ld_qp % 4 != 0 || !aligned(t->qparams, 8))) return 0;
   if ((int64_t)16 * t->ld_qp * 2 >= ((int64_t)1 << 31)) return 0;
@@ -1136,6 +1158,7 @@ static int encode_slabs(const lrq_tensors* t, const void* x, int64_t ldx, hipStr
   };
   if constexpr (ROT) {
     if constexpr (NP == 2 && G == 128) return 0;  // not built (its registers would spill)
+    else if (outl) quant(k_quant_slab<BITS, G, R, true, true>);
     else quant(k_quant_slab<BITS, G, R, false, true>);
   } else {
     if (outl) {

@@ -86,10 +86,7 @@ static inline int validate_tensors(const lrq_tensors* t) {
   if ((t->flags & ~LRQ_FLAG_HADAMARD) != 0) return LRQ_ERR_UNSUPPORTED;
   const int64_t np = 8 / t->bits;
   if (t->hidden % (t->group * np) != 0) return LRQ_ERR_SHAPE;
-  if (t->flags & LRQ_FLAG_HADAMARD) {
-    if (t->hidden % 128 != 0) return LRQ_ERR_SHAPE;
-    if (t->n_outlier != 0) return LRQ_ERR_UNSUPPORTED;
-  }
+  if ((t->flags & LRQ_FLAG_HADAMARD) && t->hidden % 128 != 0) return LRQ_ERR_SHAPE;
   if (t->rank > 0) {
     if (t->L == nullptr || t->V == nullptr) return LRQ_ERR_NULL;
     if (t->ld_L < t->rank) return LRQ_ERR_SHAPE;

@@ -723,12 +723,15 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm(
 // tile (16 rows x NP planes x NW*G columns), rotate its 128-column blocks in place with the
 // decode's own routine (wht128_lds: the same bf16 x_hat, bit for bit), read their units back in
 // the B-operand layout and project as k_dequant_gemm does.  Planes must be whole rotation blocks
-// (plane % 128 == 0), so every block of a step is complete.
-template <int BITS, int G, int R, int NOUT, int NW, int RBW, bool OUT_F32>
+// (plane % 128 == 0), so every block of a step is complete.  OUTL: the side columns replace
+// x_hat's outlier columns after the rotation, so, as in k_dequant_gemm, A's rows of those
+// columns are zeroed and the side term is added at the end.
+template <int BITS, int G, int R, int NOUT, int NW, int RBW, bool OUT_F32, bool OUTL>
 __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_rot(
     const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
     const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
-    const uint16_t* __restrict__ A, void* __restrict__ out, int64_t ldo) {
+    const uint16_t* __restrict__ A, void* __restrict__ out, int64_t ldo, const int32_t* __restrict__ oidx, int nout,
+    const uint16_t* __restrict__ side, int64_t ldside) {
   constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, TO = NOUT / 16, E = G / 4;
   constexpr int SEG = NW * G;           // columns of one plane per step
   constexpr int OPAD = SEG * 2 + 16;    // LDS row pitch in bytes (spreads the 16 rows over banks)
@@ -736,7 +739,8 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_rot(
   constexpr int RB = SEG / 128;         // rotation blocks per plane and step
   static_assert(SEG % 128 == 0 && OPAD % 16 == 0, "whole rotation blocks, 16-byte rows");
   __shared__ f32x4 part[NW][TO][64];
-  extern __shared__ __attribute__((aligned(16))) unsigned char tile[];  // [RBW][TILE]
+  extern __shared__ __attribute__((aligned(16))) unsigned char tile[];  // [RBW][TILE], OUTL: + N/32 words
+  uint32_t* gmask = reinterpret_cast<uint32_t*>(tile + RBW * TILE);
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
   const int nrb = (M + 15) / 16;
@@ -744,6 +748,7 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_rot(
   const int units = N / (G * NP);
   const int steps = (units + NW - 1) / NW;
   const u32x2 ident = identity_bop(j, g);
+  if constexpr (OUTL) build_colmask(gmask, N, oidx, nout);
   u32x4 wop[2][2];
 #pragma unroll
   for (int q0 = 0; q0 < 2; ++q0)
@@ -775,6 +780,7 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_rot(
     for (int p = 0; p < NP; ++p) {
       if constexpr (R > 0) load_vops<G, R>(V, unit_base(p, u, N, NP, G), j, g, d.vop[p]);
       load_vops<G, NOUT>(A, unit_base(p, u, N, NP, G), j, g, d.va[p]);
+      if constexpr (OUTL) mask_rows<G, TO>(d.va[p], gmask, unit_base(p, u, N, NP, G), j);
     }
 #pragma unroll
     for (int b = 0; b < RBW; ++b) {
@@ -840,6 +846,9 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_rot(
     } else {
       if (s + 1 < steps) load_unit(min(u + NW, units - 1), cur);
     }
+  }
+  if constexpr (OUTL) {
+    if (w == 0) add_side_term<TO, RBW>(A, NOUT, N, oidx, nout, side, ldside, rb0, nrb, M, j, g, &acc[0][0]);
   }
 
   // acc[b][t] in lane (j, g), component v: out[row j][16t + 4g + v] (as in k_dequant_gemm)
@@ -1295,35 +1304,41 @@ static int gemm_launch(const lrq_tensors* t, const void* a, void* out, int64_t l
 
 // Rotated format (no outlier channels; planes of whole rotation blocks).  Row blocks per
 // workgroup: as many as fit in about 64 KB of tiles (one to four).
-template <int BITS, int G, int R, int NOUT, bool F32>
+template <int BITS, int G, int R, int NOUT, bool F32, bool OUTL>
 static int gemm_rot_launch(const lrq_tensors* t, const void* a, void* out, int64_t ldo, hipStream_t s) {
   constexpr int NP = 8 / BITS, NW = 8;
   constexpr int TILE = 16 * NP * (NW * G * 2 + 16);
   constexpr int RBW = 4 * TILE <= 68 * 1024 ? 4 : 2 * TILE <= 68 * 1024 ? 2 : 1;
-  if (t->n_outlier != 0 || (t->hidden / NP) % 128 != 0) return LRQ_ERR_UNSUPPORTED;
+  if ((t->hidden / NP) % 128 != 0) return LRQ_ERR_UNSUPPORTED;
   const int M = (int)t->rows, N = (int)t->hidden;
   const int nrb = (M + 15) / 16;
-  const size_t shm = (size_t)RBW * TILE;
-  auto kern = k_dequant_gemm_rot<BITS, G, R, NOUT, NW, RBW, F32>;
+  const size_t shm = (size_t)RBW * TILE + (OUTL ? (size_t)(N / 32) * 4 : 0);
+  auto kern = k_dequant_gemm_rot<BITS, G, R, NOUT, NW, RBW, F32, OUTL>;
+  if (shm > 160 * 1024) return LRQ_ERR_UNSUPPORTED;
   if (shm > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
   LRQ_TRY(launch(kern, dim3((nrb + RBW - 1) / RBW), dim3(NW * 64), shm, s, (const uint8_t*)t->codes, t->ld_codes,
                  (const uint16_t*)t->qparams, t->ld_qp, (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N,
-                 (const uint16_t*)a, out, ldo));
+                 (const uint16_t*)a, out, ldo, t->outlier_idx, (int)t->n_outlier, (const uint16_t*)t->side,
+                 t->ld_side));
   return LRQ_OK;
 }
 
 template <int BITS, int G, int R>
 static int gemm_nout(const lrq_tensors* t, const void* a, int n_out, void* out, int64_t ldo, bool f32, hipStream_t s) {
+  const bool o = t->n_outlier > 0;
   if (t->flags & LRQ_FLAG_HADAMARD) {
-    switch (n_out * 2 + (f32 ? 1 : 0)) {
-      case 16 * 2 + 1: return gemm_rot_launch<BITS, G, R, 16, true>(t, a, out, ldo, s);
-      case 16 * 2: return gemm_rot_launch<BITS, G, R, 16, false>(t, a, out, ldo, s);
-      case 32 * 2 + 1: return gemm_rot_launch<BITS, G, R, 32, true>(t, a, out, ldo, s);
-      case 32 * 2: return gemm_rot_launch<BITS, G, R, 32, false>(t, a, out, ldo, s);
+    switch (n_out * 4 + (f32 ? 2 : 0) + (o ? 1 : 0)) {
+      case 16 * 4 + 2: return gemm_rot_launch<BITS, G, R, 16, true, false>(t, a, out, ldo, s);
+      case 16 * 4 + 3: return gemm_rot_launch<BITS, G, R, 16, true, true>(t, a, out, ldo, s);
+      case 16 * 4: return gemm_rot_launch<BITS, G, R, 16, false, false>(t, a, out, ldo, s);
+      case 16 * 4 + 1: return gemm_rot_launch<BITS, G, R, 16, false, true>(t, a, out, ldo, s);
+      case 32 * 4 + 2: return gemm_rot_launch<BITS, G, R, 32, true, false>(t, a, out, ldo, s);
+      case 32 * 4 + 3: return gemm_rot_launch<BITS, G, R, 32, true, true>(t, a, out, ldo, s);
+      case 32 * 4: return gemm_rot_launch<BITS, G, R, 32, false, false>(t, a, out, ldo, s);
+      case 32 * 4 + 1: return gemm_rot_launch<BITS, G, R, 32, false, true>(t, a, out, ldo, s);
       default: return LRQ_ERR_UNSUPPORTED;
     }
   }
-  const bool o = t->n_outlier > 0;
   switch (n_out * 4 + (f32 ? 2 : 0) + (o ? 1 : 0)) {
     case 16 * 4 + 2: return gemm_launch<BITS, G, R, 16, true, false>(t, a, out, ldo, s);
     case 16 * 4 + 3: return gemm_launch<BITS, G, R, 16, true, true>(t, a, out, ldo, s);
