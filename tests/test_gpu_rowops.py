@@ -201,6 +201,39 @@ def test_dequant_gemm_t(pkg, dev, rows, hidden, rank, bits, group, n_out, out_dt
         print(f"[gemm_t] vs oracle x_hat {rep}", flush=True)
 
 
+@pytest.mark.parametrize("rows,hidden,rank,bits,group,n_out,k,out_dtype", [
+    (300, 4096, 16, 4, 64, 16, 8, torch.float32),     # lora format with its 8 channels kept
+    (1000, 2048, 0, 8, 128, 32, 41, torch.bfloat16),  # config 3's channel count, bf16 out
+    (70, 1024, 32, 4, 64, 16, 100, torch.float32),    # more channels than the fused GEMM takes
+])
+def test_dequant_gemm_t_outliers(pkg, dev, rows, hidden, rank, bits, group, n_out, k, out_dtype):
+    """decode(c)^T @ g with outlier channels (output rows idx from the side columns), against the
+    float64 product on lrq_decode's output within the fp32 accumulation bound (one bf16 rounding
+    more for bf16 out); the allocation-free entry point gives the same bits."""
+    print(f"[gemm_t outl] rows={rows} hidden={hidden} rank={rank} int{bits}/g{group} n={n_out} k={k}", flush=True)
+    x = pkg.inputs.activation(rows, hidden, n_outlier=k, outlier_scale=50.0, seed=k)
+    V = pkg.inputs.basis(hidden, rank, seed=k) if rank else None
+    idx = O.topk_channels(O.colmax_abs(bits16(x)), k)
+    gm = (torch.randn(rows, n_out, generator=torch.Generator().manual_seed(k)) * 0.05).to(torch.bfloat16)
+    c = pkg.encode(x.to(dev), V.to(dev) if V is not None else None, bits=bits, group_size=group,
+                   outlier_idx=torch.as_tensor(idx, dtype=torch.int32, device=dev))
+    out = pkg.dequant_gemm_t(c, gm.to(dev), out_dtype=out_dtype)
+    out2 = torch.empty_like(out)
+    pkg.dequant_gemm_t_noalloc(c, gm.to(dev), out2)
+    xd = O.bf16_to_f32(bits16(pkg.decode(c))).astype(np.float64)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits16(out) if out_dtype == torch.bfloat16 else out.cpu().numpy(),
+                          bits16(out2) if out_dtype == torch.bfloat16 else out2.cpu().numpy())
+    gf = O.bf16_to_f32(bits16(gm)).astype(np.float64)
+    ref = xd.T @ gf
+    bound = 1e-5 * (np.abs(xd).T @ np.abs(gf)) + 1e-9
+    got = out.cpu().numpy().astype(np.float64) if out_dtype == torch.float32 else \
+        O.bf16_to_f32(bits16(out)).astype(np.float64)
+    ulp = 0 if out_dtype == torch.float32 else np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))) - 7)
+    err = np.abs(got - ref)
+    assert (err <= ulp + bound).all(), float((err / (ulp + bound)).max())
+
+
 def test_dequant_gemm_t_no_rows(pkg, dev):
     """A descriptor with rows == 0 gives dA = 0 (the sum over no rows), through the C ABI."""
     import ctypes

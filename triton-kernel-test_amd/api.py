@@ -329,8 +329,8 @@ def dequant_gemm_t(c: CompressedActivation, g: torch.Tensor, out_dtype=torch.flo
         raise ValueError("g must be bf16 [rows, n] (leading dimensions those of the activation)")
     if out_dtype not in (torch.float32, torch.bfloat16):
         raise ValueError("out_dtype must be float32 or bfloat16")
-    if c.hadamard or c.idx is not None:
-        raise ValueError("dequant_gemm_t: rotated format and outlier channels are not supported")
+    if c.hadamard:
+        raise ValueError("dequant_gemm_t: the rotated format is not supported")
     g2 = g2.contiguous()
     n_out = g2.shape[1]
     t = c.descriptor()
@@ -357,8 +357,8 @@ def dequant_gemm_t_noalloc(c: CompressedActivation, g: torch.Tensor, out: torch.
     if out.dtype not in (torch.float32, torch.bfloat16) or tuple(out.shape) != (c.hidden, n_out) \
             or not out.is_contiguous():
         raise ValueError("out must be a contiguous fp32 or bf16 [N, n]")
-    if c.hadamard or c.idx is not None:
-        raise ValueError("dequant_gemm_t_noalloc: rotated format and outlier channels are not supported")
+    if c.hadamard:
+        raise ValueError("dequant_gemm_t_noalloc: the rotated format is not supported")
     t = c.descriptor()
     with torch.cuda.device(c.device):
         call("lrq_dequant_gemm_t_noalloc", ctypes.byref(t), _p(g), n_out, n_out, _p(out), n_out,

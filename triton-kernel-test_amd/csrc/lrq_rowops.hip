@@ -1156,6 +1156,57 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t(
   }
 }
 
+// Outlier channels in dequant_gemm_t: x_hat[:, idx[k]] = bf16(side[:, k]), so output row idx[k]
+// is sum over the rows of bf16(side[m, k]) * G[m, :].  One workgroup per channel overwrites that
+// row after the main kernels (fp32 sums, a block reduction in a fixed order).
+template <int KO, bool OUT_F32>
+__global__ __launch_bounds__(256) void k_side_gemm_t(const uint16_t* __restrict__ side, int64_t ldside, int M, int N,
+                                                     const int32_t* __restrict__ oidx, const uint16_t* __restrict__ G,
+                                                     int64_t ldg, void* __restrict__ out, int64_t ldo) {
+  __shared__ float red[KO][256];
+  const int k = blockIdx.x, c = oidx[k];
+  if (c < 0 || c >= N) return;  // whole workgroup
+  float acc[KO];
+#pragma unroll
+  for (int q = 0; q < KO; ++q) acc[q] = 0.f;
+  for (int m = threadIdx.x; m < M; m += 256) {
+    const float sv = __uint_as_float(pack_bf16x2(f16_val(side[(int64_t)m * ldside + k]), 0.f) << 16);  // bf16(side)
+#pragma unroll
+    for (int q = 0; q < KO; q += 4) {
+      const u32x2 gv = ld8(G + (int64_t)m * ldg + q);
+      acc[q + 0] = __builtin_fmaf(sv, __uint_as_float(gv[0] << 16), acc[q + 0]);
+      acc[q + 1] = __builtin_fmaf(sv, __uint_as_float(gv[0] & 0xffff0000u), acc[q + 1]);
+      acc[q + 2] = __builtin_fmaf(sv, __uint_as_float(gv[1] << 16), acc[q + 2]);
+      acc[q + 3] = __builtin_fmaf(sv, __uint_as_float(gv[1] & 0xffff0000u), acc[q + 3]);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < KO; ++q) red[q][threadIdx.x] = acc[q];
+  __syncthreads();
+  if (threadIdx.x < KO) {
+    float sum = 0.f;
+    for (int i = 0; i < 256; ++i) sum += red[threadIdx.x][i];
+    if constexpr (OUT_F32) reinterpret_cast<float*>(out)[(int64_t)c * ldo + threadIdx.x] = sum;
+    else reinterpret_cast<uint16_t*>(out)[(int64_t)c * ldo + threadIdx.x] = (uint16_t)pack_bf16x2(sum, 0.f);
+  }
+}
+
+static int side_gemm_t(const lrq_tensors* t, const void* g, int64_t ldg, int n_out, void* out, int64_t ldo, bool f32,
+                       hipStream_t s) {
+  if (t->n_outlier == 0) return LRQ_OK;
+  const dim3 grid((unsigned)t->n_outlier), block(256);
+  const int M = (int)t->rows, N = (int)t->hidden;
+  const auto* sd = (const uint16_t*)t->side;
+  const auto* gg = (const uint16_t*)g;
+  switch (n_out * 2 + (f32 ? 1 : 0)) {
+    case 16 * 2 + 1: return launch((k_side_gemm_t<16, true>), grid, block, 0, s, sd, t->ld_side, M, N, t->outlier_idx, gg, ldg, out, ldo);
+    case 16 * 2: return launch((k_side_gemm_t<16, false>), grid, block, 0, s, sd, t->ld_side, M, N, t->outlier_idx, gg, ldg, out, ldo);
+    case 32 * 2 + 1: return launch((k_side_gemm_t<32, true>), grid, block, 0, s, sd, t->ld_side, M, N, t->outlier_idx, gg, ldg, out, ldo);
+    case 32 * 2: return launch((k_side_gemm_t<32, false>), grid, block, 0, s, sd, t->ld_side, M, N, t->outlier_idx, gg, ldg, out, ldo);
+    default: return LRQ_ERR_UNSUPPORTED;
+  }
+}
+
 // out[n][k] = sum over the rg row groups of part[.][n][k] in group order (fp32), for nk = N KO
 // entries; 4 consecutive k per thread.  rg == 0 (no rows) writes zeros.
 template <bool OUT_F32>
@@ -1520,7 +1571,7 @@ extern "C" int lrq_dequant_gemm_t(const lrq_tensors* t, const void* g, int64_t l
   if (n_out != 16 && n_out != 32) return LRQ_ERR_UNSUPPORTED;
   if (ldg < n_out || ldo < n_out) return LRQ_ERR_SHAPE;
   if (!aligned(g, 8) || (ldg % 4) != 0 || !aligned(out, out_fp32 ? 4 : 2)) return LRQ_ERR_ALIGN;
-  if ((t->flags & LRQ_FLAG_HADAMARD) || t->n_outlier > 0) return LRQ_ERR_UNSUPPORTED;
+  if (t->flags & LRQ_FLAG_HADAMARD) return LRQ_ERR_UNSUPPORTED;
   const GemmTPlan pl = gemm_t_plan(t->rows, t->hidden, t->bits, t->group, n_out);
   if (pl.ws_bytes > 0) {
     if (workspace == nullptr) return LRQ_ERR_NULL;
@@ -1530,7 +1581,8 @@ extern "C" int lrq_dequant_gemm_t(const lrq_tensors* t, const void* g, int64_t l
   hipStream_t s = (hipStream_t)stream;
   const bool f32 = out_fp32 != 0;
   float* ws = reinterpret_cast<float*>(workspace);
-  LRQ_FORMATS(gemm_t_nout, t, g, ldg, n_out, out, ldo, f32, ws, pl, s)
+  LRQ_TRY([&]() -> int { LRQ_FORMATS(gemm_t_nout, t, g, ldg, n_out, out, ldo, f32, ws, pl, s) }());
+  return side_gemm_t(t, g, ldg, n_out, out, ldo, f32, s);
 }
 
 extern "C" int lrq_dequant_gemm_t_noalloc(const lrq_tensors* t, const void* g, int64_t ldg, int32_t n_out, void* out,
@@ -1541,7 +1593,7 @@ extern "C" int lrq_dequant_gemm_t_noalloc(const lrq_tensors* t, const void* g, i
   if (n_out != 16 && n_out != 32) return LRQ_ERR_UNSUPPORTED;
   if (ldg < n_out || ldo < n_out) return LRQ_ERR_SHAPE;
   if (!aligned(g, 8) || (ldg % 4) != 0 || !aligned(out, out_fp32 ? 4 : 2)) return LRQ_ERR_ALIGN;
-  if ((t->flags & LRQ_FLAG_HADAMARD) || t->n_outlier > 0) return LRQ_ERR_UNSUPPORTED;
+  if (t->flags & LRQ_FLAG_HADAMARD) return LRQ_ERR_UNSUPPORTED;
   const GemmTPlan pl = gemm_t_plan(t->rows, t->hidden, t->bits, t->group, n_out);
   if (pl.ws_bytes > (int64_t)LRQ_GEMM_T_SCRATCH_BYTES) return LRQ_ERR_WORKSPACE;
   float* ws = nullptr;
@@ -1549,5 +1601,6 @@ extern "C" int lrq_dequant_gemm_t_noalloc(const lrq_tensors* t, const void* g, i
   if (st) return st;
   hipStream_t s = (hipStream_t)stream;
   const bool f32 = out_fp32 != 0;
-  LRQ_FORMATS(gemm_t_nout, t, g, ldg, n_out, out, ldo, f32, ws, pl, s)
+  LRQ_TRY([&]() -> int { LRQ_FORMATS(gemm_t_nout, t, g, ldg, n_out, out, ldo, f32, ws, pl, s) }());
+  return side_gemm_t(t, g, ldg, n_out, out, ldo, f32, s);
 }
