@@ -57,6 +57,28 @@ def assert_decode_close(dev_bits: np.ndarray, ref_bits: np.ndarray, what: str, f
     return rep
 
 
+def assert_projection_close(l_bits: np.ndarray, y: np.ndarray, v_bits: np.ndarray, what: str, frac=1e-3) -> dict:
+    """Device L (bf16 of fp32 sums of y V) vs the exact projection y V (float64).  The device
+    rounds each 32-term MFMA step, the two accumulator chains and the partials of each wave or
+    slab: at most 16 fp32 roundings on the way of any term, each below 2^-24 times the running
+    sum of magnitudes S = |y| |V|.  Bar: every element within one bf16 ulp of the exact value
+    plus 2^-19 S (twice that bound), and one-ulp flips against the oracle's L (the exact sum
+    rounded once) on at most ``frac`` of the elements.  Where L cancels to a value much below S
+    the fp32 steps are several bf16 ulps of it; a wrong partial or row is off by far more."""
+    yv = np.asarray(y, dtype=np.float64)
+    v = O.bf16_to_f32(v_bits).astype(np.float64)
+    exact = yv @ v
+    big = np.abs(yv) @ np.abs(v)
+    dev = O.bf16_to_f32(l_bits).astype(np.float64)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(exact), 1e-30))) - 7)
+    tol = ulp + 2.0 ** -19 * big
+    d = ulp_diff_bf16(l_bits, O.bf16_round(exact.astype(np.float32)))
+    rep = dict(max_ulp=int(d.max()) if d.size else 0, frac_ulp=float((d > 0).mean()) if d.size else 0.0,
+               worst=float((np.abs(dev - exact) / tol).max()) if d.size else 0.0)
+    assert rep["worst"] <= 1.0 and rep["frac_ulp"] <= frac, f"{what}: {rep}"
+    return rep
+
+
 def assert_rotated_close(dev_bits: np.ndarray, ref_bits: np.ndarray, what: str, frac=1e-2, k=4) -> dict:
     """Rotated-format decode (x_hat = bf16(WHT128(y))) vs the oracle's.  A one-ulp difference in
     one reconstructed value y (the MFMA's fp32 sum at rank 32, see assert_decode_close) moves

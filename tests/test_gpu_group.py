@@ -11,8 +11,8 @@ import pytest
 import torch
 
 import oracle as O
-from parity import (assert_codes, assert_decode_close, assert_fp_close, bits16, code_mismatch_report, f16, from_bits,
-                    ulp_diff_bf16)
+from parity import (assert_codes, assert_decode_close, assert_fp_close, assert_projection_close, bits16,
+                    code_mismatch_report, f16, from_bits, ulp_diff_bf16)
 
 pytestmark = pytest.mark.gpu
 
@@ -139,17 +139,30 @@ def test_many_outlier_channels(pkg, dev, rows, hidden, rank, bits, group, k):
     assert_fp_close(bits16(dx), O.gelu_bwd(O.bf16_to_f32(ref_xh), O.bf16_to_f32(bits16(dy))), "gelu, >64 outliers")
 
 
-@pytest.mark.parametrize("rows,hidden,rank,bits,group", [(100, 4096, 16, 4, 64), (64, 5120, 16, 4, 64)])
-def test_twopass_matches_fused(pkg, dev, rows, hidden, rank, bits, group):
-    print(f"[twopass] rows={rows} hidden={hidden}", flush=True)
+# 4100 rows: 257 row blocks, so on 256 CUs the single-pass kernels walk two blocks per
+# workgroup (the next block's loads in flight) and the last block is ragged; 5120 columns take
+# the tile-staged kernel, plain and rotated
+@pytest.mark.parametrize("rows,hidden,rank,bits,group,hadamard", [
+    (100, 4096, 16, 4, 64, False), (64, 5120, 16, 4, 64, False), (4100, 4096, 16, 4, 64, False),
+    (4100, 5120, 16, 4, 64, False), (4100, 5120, 16, 4, 64, True), (37, 5120, 16, 4, 64, True)])
+def test_twopass_matches_fused(pkg, dev, rows, hidden, rank, bits, group, hadamard):
+    print(f"[twopass] rows={rows} hidden={hidden} hadamard={hadamard}", flush=True)
     x = pkg.inputs.activation(rows, hidden, 8, 20.0, seed=3).to(dev)
     V = pkg.inputs.basis(hidden, rank, seed=3).to(dev)
-    a = pkg.encode(x, V, bits=bits, group_size=group)
-    b = pkg.encode(x, V, bits=bits, group_size=group, _twopass=True)
+    a = pkg.encode(x, V, bits=bits, group_size=group, hadamard=hadamard)
+    b = pkg.encode(x, V, bits=bits, group_size=group, hadamard=hadamard, _twopass=True)
     torch.cuda.synchronize()
+    # both against the exact projection of the (rotated) activation, within their fp32
+    # accumulation bound
+    y = O.bf16_to_f32(bits16(pkg.wht128(x) if hadamard else x))
+    vb = bits16(V)
+    ra = assert_projection_close(bits16(a.L), y, vb, "fused L")
+    rb = assert_projection_close(bits16(b.L), y, vb, "two-pass L")
+    print(f"[twopass] L fused {ra}, two-pass {rb}", flush=True)
     dl = ulp_diff_bf16(bits16(a.L), bits16(b.L))
-    assert dl.max() <= 1
     same_l = (dl == 0).all(axis=1)
+    print(f"[twopass] rows with the same L: {same_l.mean():.3f}", flush=True)
+    assert same_l.mean() > 0.05
     # rows whose L agrees must agree bit-for-bit in codes/scales/zeros
     ca, cb = a.codes.cpu().numpy(), b.codes.cpu().numpy()
     assert np.array_equal(ca[same_l], cb[same_l])

@@ -1,8 +1,8 @@
 """CPU replay of the direct global-to-LDS loads (ld16_to_lds, csrc/lrq_common.h).
 
-Three kernels move 16 bytes per lane from global memory straight into LDS with
-__builtin_amdgcn_global_load_lds: k_encode_rows (csrc/lrq_encode.hip), k_softmax_rows
-(csrc/lrq_rowops.hip) and k_wht_rows (csrc/lrq_wht.hip).  This file restates, in numpy, the
+Four kernels move 16 bytes per lane from global memory straight into LDS with
+__builtin_amdgcn_global_load_lds: k_encode_rows and k_encode_tiles (csrc/lrq_encode.hip),
+k_softmax_rows (csrc/lrq_rowops.hip) and k_wht_rows (csrc/lrq_wht.hip).  This file restates, in numpy, the
 host launch arithmetic (grid, row blocks per workgroup) and each kernel's source and
 destination address arithmetic, and checks for every instance and launch shape that the
 library's callers use (bench.py's configurations and the GPU tests' shapes) that
@@ -12,7 +12,11 @@ library's callers use (bench.py's configurations and the GPU tests' shapes) that
     region (encode) or the block's tile (softmax, rotation),
   * no two lanes of one workgroup write the same LDS bytes for one row block.
 
-No GPU is needed; a change to any of the three kernels' addressing must be mirrored here.
+For k_encode_tiles, whose tiles are swizzled (chunk c of tile row r at position c ^ r), the
+replay also checks that the read-back (projection / quantisation layout and the rotation's
+layout) finds every column where the loads put it.
+
+No GPU is needed; a change to any of these kernels' addressing must be mirrored here.
 """
 
 from __future__ import annotations
@@ -105,6 +109,69 @@ def test_encode_rows_direct_loads_stay_in_bounds(cus):
     assert n > 0
     # the 2-unit-per-wave instance (hidden 2048) stages through registers: nothing to check
     assert encode_rows_replay(64, 2048, 2048, 256, upw=2) == 0
+
+
+# ----------------------------------------------------------------------------- k_encode_tiles
+def encode_tiles_replay(M, N, ldx, cus, upw=5, nw=8):
+    """k_encode_tiles<upw, rot> as encode_tiles_dispatch() launches it (int4/g64: units of 128
+    columns, tiles of 16 rows x 128 columns, 4 KB)."""
+    NT, TILE = nw * upw, 16 * 256
+    LDS = NT * TILE
+    assert N == NT * 128 and LDS <= LDS_BYTES
+    nrb = (M + 15) // 16
+    rbw = (nrb + cus - 1) // cus
+    grid = (nrb + rbw - 1) // rbw
+    lane = np.arange(64)
+    lr, lq = lane >> 4, lane & 15
+    checked = 0
+    for rbs in _blocks(grid, rbw, nrb):
+        for rb in (rbs[0], rbs[-1]):
+            dst_all, col_at = [], np.full(LDS // 16, -1, dtype=np.int64)  # LDS chunk -> (row, global chunk)
+            for w in range(nw):
+                for i in range(upw):
+                    t = w + nw * i
+                    for k in range(4):
+                        r = 4 * k + lr
+                        row = np.minimum(rb * 16 + r, M - 1)
+                        gsrc = row * ldx * 2 + 256 * t + 16 * (lq ^ r)        # issue_one()
+                        ldst = t * TILE + 1024 * k + 16 * lane
+                        _check(gsrc, ldst, gbytes=((M - 1) * ldx + N) * 2, lds_alloc=LDS, lo=t * TILE,
+                               hi=(t + 1) * TILE, what=f"k_encode_tiles M={M} N={N} ldx={ldx} cus={cus} w={w}")
+                        assert ((gsrc % (ldx * 2)) // 256 == t).all(), "a tile holds columns of another tile"
+                        dst_all.append(ldst)
+                        col_at[ldst // 16] = r * 1000 + (gsrc % (ldx * 2)) // 16
+                        checked += gsrc.size
+            d = np.concatenate(dst_all)
+            assert np.unique(d).size == d.size == LDS // 16, "every LDS chunk written exactly once per block"
+            # read-back: lane (j, g) of wave w reads unit u = w*upw + uu, plane p, chunk
+            # 8(u%2) + 2g + k of tile p*NT/2 + u/2, row j, at position chunk ^ j
+            j, g = lane & 15, lane >> 4
+            for w in range(nw):
+                for uu in range(upw):
+                    u = w * upw + uu
+                    for p in range(2):
+                        tp = p * (NT // 2) + u // 2
+                        for k in range(2):
+                            c = 8 * (u % 2) + 2 * g + k
+                            pos = (tp * TILE + 256 * j + 16 * (c ^ j)) // 16
+                            want_col = (p * (N // 2) + 64 * u + 16 * g + 8 * k)   # unit_base(p, u) + 16g + 8k
+                            assert (col_at[pos] == j * 1000 + want_col // 8).all(), "read-back finds other columns"
+                # the rotation's layout: lane (j, g) chunks 4g + c of its tiles' row j
+                for i in range(upw):
+                    t = w + nw * i
+                    for c in range(4):
+                        pos = (t * TILE + 256 * j + 16 * ((4 * g + c) ^ j)) // 16
+                        assert (col_at[pos] == j * 1000 + (128 * t) // 8 + 4 * g + c).all()
+    return checked
+
+
+@pytest.mark.parametrize("cus", CU_COUNTS)
+def test_encode_tiles_direct_loads_stay_in_bounds(cus):
+    n = 0
+    for rows, extra in [(16384, 0), (1, 0), (5, 0), (16, 0), (37, 0), (48, 0), (64, 0), (100, 0), (4100, 0),
+                        (5000, 0), (64, 64), (33, 8)]:
+        n += encode_tiles_replay(rows, 5120, 5120 + extra, cus)
+    assert n > 0
 
 
 # ----------------------------------------------------------------------------- k_softmax_rows

@@ -215,7 +215,8 @@ def encode(x: torch.Tensor, basis: Optional[LowRankBasis | torch.Tensor] = None,
             # rotated format: the library rotates x as it reads it where it can (flagged
             # descriptor); otherwise y = bf16(WHT128(x)) into a temporary, then the plain encode
             t.flags = _lib.LRQ_FLAG_HADAMARD
-            st = _lib.call_raw("lrq_encode", ctypes.byref(t), _p(x2), ldx, _stream(x.device))
+            st = _lib.call_raw("lrq_encode_twopass" if _twopass else "lrq_encode", ctypes.byref(t), _p(x2), ldx,
+                               _stream(x.device))
             if st != _lib.LRQ_ERR_UNSUPPORTED or k:
                 # (outlier channels leave X before the rotation: no rotated copy can stand in)
                 _lib.check(st, "lrq_encode")

@@ -541,6 +541,218 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
 }
 
 // -------------------------------------------------------------------------------------
+// Tile-staged single-pass encode for rows too wide for per-wave regions (int4/g64, NW*UPW
+// units of 128 columns; 40 units = 5120 columns fill the 160 KB of LDS with one 16-row block).
+//
+// The block lives in LDS as N/128 tiles of 16 rows x 128 columns (4 KB): tile t holds
+// columns 128t .. 128t+127, its row r at byte 256r, and the row's 16-byte chunk c (columns
+// 8c .. 8c+7) at position c ^ r, so that the 16 lanes of a column quarter (rows 0..15) read
+// 16 different bank groups.  A direct load (1 KB) fills 4 rows of one tile: lane l writes
+// position l % 16 of row 4i + l / 16 and reads that row's chunk (l % 16) ^ row from HBM, so the
+// permutation costs nothing.  Wave w loads (and, with ROT, rotates in place: WHT-128 per tile
+// row, the oracle's summation order) its tiles T_i = w + NW*i, i < UPW.
+//
+// A CU keeps about 32 KB of loads in flight and a wave that issues more waits at the issue,
+// so the next block's tiles are requested one per wave at a time (4 KB, 32 KB per CU)
+// between the current block's phases, and each is rotated as soon as it has landed, between
+// the current block's units:
+//   [top: T_4 of this block landed, rotated] barrier; read the units' columns (MFMA layout);
+//   barrier; T_0 | projection | T_1 | partials into the first KB of T_4 (this wave's slot),
+//   barrier, L summed in a fixed order, barrier | T_2 | unit 0 | T_3 | unit 1 | unit 2 |
+//   rotate T_0 | T_4 | unit 3 | rotate T_1 | unit 4, L store | rotate T_2, T_3.
+// (A rotation needs about 50 registers; by unit 2 the first units' columns are dead.)
+// Waits are counted vmcnt (memory operations retire in issue order): the number of this
+// wave's memory operations issued after the tile's last load.
+// Unit u of plane p is half u % 2 of tile p*NT/2 + u/2.  V operands stay in registers; the
+// projection's V^T operands are regenerated each block with identity MFMAs.  Rows past the
+// end repeat the last row (no predicated stores).
+template <int UPW, bool ROT>
+struct TilesEnc {
+  static constexpr int NW = 8, NT = NW * UPW, TILE = 16 * 256;
+  static constexpr size_t LDS = (size_t)NT * TILE;
+  static_assert(NT % 2 == 0 && LDS <= 160 * 1024, "tiles of both planes; LDS budget");
+};
+
+// s_waitcnt immediate for vmcnt(n), n < 64 (gfx9: low bits [3:0], high bits [15:14]); expcnt
+// and lgkmcnt are not waited for.
+constexpr int vmcnt_imm(int n) { return 0x0f70 | (n & 15) | ((n >> 4) << 14); }
+
+template <int UPW, bool ROT>
+__global__ __launch_bounds__(512) void k_encode_tiles(const uint16_t* __restrict__ X, int64_t ldx, int M, int N,
+                                                      const uint16_t* __restrict__ V, uint16_t* __restrict__ Lout,
+                                                      int64_t ldl, uint8_t* __restrict__ codes, int64_t ldc,
+                                                      uint16_t* __restrict__ qparams, int64_t ldq, int RBW) {
+  using Te = TilesEnc<UPW, ROT>;
+  constexpr int BITS = 4, G = 64, R = 16, NP = 2, CPG = 2, NW = Te::NW, NT = Te::NT, TILE = Te::TILE;
+  static_assert(UPW == 5, "the load / rotation schedule below is written for five tiles per wave");
+  extern __shared__ __attribute__((aligned(16))) unsigned char shm[];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int nrb = (M + 15) / 16;
+  const int rb0 = blockIdx.x * RBW;
+  if (rb0 >= nrb) return;  // whole workgroup (no barrier reached)
+  const int nblk = min(RBW, nrb - rb0);
+  const int ub = w * UPW;
+
+  // tile i of this wave: rows 4k .. 4k+3 per load; lane l covers row 4k + l/16, chunk
+  // (l % 16) ^ row, landing at position l % 16 (rows past the end clamp to the last row).  The
+  // address is the block's first row (wave-uniform) plus a 32-bit lane offset.
+  const int lr = lane >> 4, lq = lane & 15;
+  const uint32_t ldx2 = (uint32_t)ldx * 2u;
+  auto tile_ptr = [&](int i) { return shm + (size_t)(w + NW * i) * TILE; };
+  auto issue_tile = [&](int rb, int i) {
+    const int t = w + NW * i;
+    const int lim = M - 1 - rb * 16;  // last row of the block that exists (>= 0)
+    const unsigned char* base = reinterpret_cast<const unsigned char*>(X + (int64_t)rb * 16 * ldx) + 256 * t;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = 4 * k + lr;
+      ld16_to_lds(base + ((uint32_t)min(r, lim) * ldx2 + 16u * (uint32_t)(lq ^ r)), tile_ptr(i) + 1024 * k);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // wait until tile i's loads have landed (n memory operations of this wave issued after them),
+  // then rotate it in place (without ROT only the wait for the block's last tile, at the top)
+  auto rotate_tile = [&](int i, auto n_tag, bool top = false) {
+    if (ROT || top) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(decltype(n_tag)::value));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (ROT) {
+      // the sign operands, formed per use from this lane's two dwords: the empty asm hides that
+      // they are loop-invariant, so they do not stay live across the quantisation (whose peak
+      // is within a few registers of the budget)
+      int jj = j;
+      asm volatile("" : "+v"(jj));
+      u32x4 op[2][2];
+      wht_operands_from_pair(wht_sign_dword(jj, g, 0, false, 0), wht_sign_dword(jj, g, 0, false, 1), op);
+      wht128_lds_swz(tile_ptr(i) + 256 * j, g, j, op);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // memory operations of this wave after each tile's loads, up to its rotation (see above)
+  using C5 = std::integral_constant<int, 5>;
+  using C13 = std::integral_constant<int, 13>;
+  using C18 = std::integral_constant<int, 18>;
+  using C19 = std::integral_constant<int, 19>;
+  using C20 = std::integral_constant<int, 20>;
+
+  // Prologue: block rb0 (HBM) first, then the V operands (L2-resident after the first
+  // workgroups).
+#pragma unroll
+  for (int i = 0; i < UPW; ++i) issue_tile(rb0, i);
+  u32x2 vop[UPW][NP][G / 16][1];
+#pragma unroll
+  for (int uu = 0; uu < UPW; ++uu)
+#pragma unroll
+    for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, ub + uu, N, NP, G), j, g, vop[uu][p]);
+  f32x4* slot_own = reinterpret_cast<f32x4*>(tile_ptr(UPW - 1));  // first KB of T_4
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (ROT) {
+#pragma unroll
+    for (int i = 0; i < UPW - 1; ++i) rotate_tile(i, std::integral_constant<int, 0>{});
+  }
+
+  auto block = [&](auto next_tag, int b) {
+    constexpr bool next = decltype(next_tag)::value;
+    const int rb = __builtin_amdgcn_readfirstlane(rb0 + b);
+    const int row = min(rb * 16 + j, M - 1);
+    // T_4 of this block: 5 operations after it (units 3, 4 and the L store of the previous
+    // block; none after the prologue)
+    if (b == 0)
+      rotate_tile(UPW - 1, std::integral_constant<int, 0>{}, true);
+    else
+      rotate_tile(UPW - 1, C5{}, true);
+    lds_barrier();  // every tile landed and rotated
+    u32x4 x[UPW][NP][CPG];
+#pragma unroll
+    for (int uu = 0; uu < UPW; ++uu)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const int u = ub + uu;
+        const unsigned char* tr = shm + (size_t)(p * (NT / 2) + u / 2) * TILE + 256 * j;
+#pragma unroll
+        for (int k = 0; k < CPG; ++k) x[uu][p][k] = *reinterpret_cast<const u32x4*>(tr + 16 * ((8 * (u & 1) + 2 * g + k) ^ j));
+      }
+    lds_barrier();  // every wave's reads of the block returned: the tiles may be refilled
+    if (next) issue_tile(rb + 1, 0);
+
+    f32x4 acc[2][1];
+    acc[0][0] = acc[1][0] = zero4();
+    {
+      int jj = j;  // (as for the rotation's operands)
+      asm volatile("" : "+v"(jj));
+      const u32x2 ident = identity_bop(jj, g);
+#pragma unroll
+      for (int uu = 0; uu < UPW; ++uu)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) project_unit<G, R>(vop[uu][p], x[uu][p], ident, acc[(uu * NP + p) & 1]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (next) issue_tile(rb + 1, 1);
+    {
+      f32x4 a = acc[0][0];
+      a[0] += acc[1][0][0];
+      a[1] += acc[1][0][1];
+      a[2] += acc[1][0][2];
+      a[3] += acc[1][0][3];
+      slot_own[lane] = a;
+    }
+    lds_barrier();
+    u32x2 lop[1], lopn[1];
+    {
+      // the eight waves' partials of this lane position, in wave order
+      f32x4 sacc = zero4();
+#pragma unroll
+      for (int w2 = 0; w2 < NW; ++w2) {
+        const f32x4 o = reinterpret_cast<const f32x4*>(shm + (size_t)(w2 + NW * (UPW - 1)) * TILE)[lane];
+        if (w2 == 0) {
+          sacc = o;
+        } else {
+          sacc[0] += o[0];
+          sacc[1] += o[1];
+          sacc[2] += o[2];
+          sacc[3] += o[3];
+        }
+      }
+      // lane (j, g) holds L[row j][4g + v]
+      lop[0] = u32x2{pack_bf16x2(sacc[0], sacc[1]), pack_bf16x2(sacc[2], sacc[3])};
+      lopn[0] = neg_bf16x4(lop[0]);
+    }
+    lds_barrier();  // every wave's partial sums read: the slot KB may be refilled
+    if (next) issue_tile(rb + 1, 2);
+    uint8_t* crow = codes + (int64_t)row * ldc;
+    uint16_t* qrow = qparams + (int64_t)row * ldq;
+    auto unit = [&](int uu) {
+      quant_unit<BITS, G, R>(x[uu], vop[uu], lopn, nullptr, ub + uu, N, g, crow, qrow);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    unit(0);
+    if (next) issue_tile(rb + 1, 3);
+    unit(1);
+    unit(2);
+    if (next) {
+      rotate_tile(0, C18{});
+      issue_tile(rb + 1, 4);
+    }
+    unit(3);
+    if (next) rotate_tile(1, C20{});
+    unit(4);
+    st8_pred(Lout + (int64_t)rb * 16 * ldl, (uint32_t)(16 * ldl * 2), (uint32_t)(((row - rb * 16) * ldl + 4 * g) * 2),
+             lop[0], w == 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (next) {
+      rotate_tile(2, C19{});
+      rotate_tile(3, C13{});
+    }
+  };
+#pragma unroll 1
+  for (int b = 0; b < nblk - 1; ++b) block(std::true_type{}, b);
+  block(std::false_type{}, nblk - 1);
+}
+
+// -------------------------------------------------------------------------------------
 // Projection only (first pass of the two-pass encode).  Grid: ceil(rows / 16) workgroups
 // of 4 waves; wave w sums 32-column chunks w, w + 4, ... of the row.  Uses V^T [R, N].
 template <int R>
@@ -1043,6 +1255,31 @@ static int launch_rows(const lrq_tensors* t, const void* x, int64_t ldx, hipStre
   return LRQ_OK;
 }
 
+// k_encode_tiles (int4/g64, rank 16, NW*UPW units, no outlier channels): one workgroup per CU,
+// each walking ceil(row blocks / CUs) consecutive blocks.  Returns 0 (nothing launched) when
+// the shape does not fit or the device refuses the workgroup's 160 KB of LDS.
+template <int BITS, int G, int R, bool ROT>
+static int encode_tiles_dispatch(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s, int* status) {
+  if constexpr (BITS != 4 || G != 64 || R != 16) {
+    return 0;
+  } else {
+    constexpr int UPW = 5;
+    using Te = TilesEnc<UPW, ROT>;
+    if (t->hidden != (int64_t)Te::NT * 128 || t->n_outlier > 0) return 0;
+    if ((int64_t)16 * t->ld_L * 2 >= ((int64_t)1 << 31)) return 0;
+    auto kern = k_encode_tiles<UPW, ROT>;
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)Te::LDS) != hipSuccess)
+      return 0;
+    const int64_t nrb = (t->rows + 15) / 16, cus = cu_count();
+    const int rbw = (int)((nrb + cus - 1) / cus);
+    const int64_t wgs = (nrb + rbw - 1) / rbw;
+    *status = launch(kern, dim3((unsigned)wgs), dim3(Te::NW * 64), Te::LDS, s, (const uint16_t*)x, ldx, (int)t->rows,
+                     (int)t->hidden, (const uint16_t*)t->V, (uint16_t*)t->L, t->ld_L, (uint8_t*)t->codes,
+                     t->ld_codes, (uint16_t*)t->qparams, t->ld_qp, rbw);
+    return 1;
+  }
+}
+
 // The row-staged kernel with or without outlier channels (the side columns' 16-row stride must
 // fit a buffer range and the mask and slot tables the LDS).
 template <int BITS, int G, int R, int UPW>
@@ -1091,6 +1328,7 @@ static int encode_persist_dispatch(const lrq_tensors* t, const void* x, int64_t 
         *status = launch_persist<BITS, G, R, 16, 2, true>(t, x, ldx, s);
         return 1;
       case 40:
+        if (encode_tiles_dispatch<BITS, G, R, false>(t, x, ldx, s, status)) return 1;
         if constexpr (wide_ok) {
           if (t->n_outlier > 0) return 0;
           *status = launch_persist<BITS, G, R, 8, 5, false>(t, x, ldx, s);
@@ -1206,7 +1444,9 @@ template <int BITS, int G, int R>
 static int encode_impl(const lrq_tensors* t, const void* x, int64_t ldx, hipStream_t s, int force_twopass) {
   int st = 0;
   if (t->flags & LRQ_FLAG_HADAMARD) {
-    // rotated format: the column-slab passes rotate X in LDS as they read it
+    // rotated format: the single-pass tile kernel, or the column-slab passes, rotate X in LDS
+    // as they read it
+    if (!force_twopass && encode_tiles_dispatch<BITS, G, R, true>(t, x, ldx, s, &st)) return st;
     if (R > 0 && t->Vt == nullptr) return LRQ_ERR_NULL;
     if (encode_slabs<BITS, G, R, true>(t, x, ldx, s, &st)) return st;
     return LRQ_ERR_UNSUPPORTED;

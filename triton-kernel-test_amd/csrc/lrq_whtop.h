@@ -6,6 +6,46 @@
 
 namespace lrq {
 
+// Dword h (bf16 signs of e = 2h, 2h+1) of the A operand of tile parity q0 for lane (i, kg):
+// the sign of element e is (-1)^(popcount(i & e & 3) + (q0 & (e >> 2)) + popcount((i >> 2) & kg) + neg).
+__host__ __device__ constexpr uint32_t wht_sign_dword(int i, int kg, int q0, bool neg, int h) {
+  uint32_t pair = 0;
+  for (int s = 0; s < 2; ++s) {
+    const int e = 2 * h + s;
+    const int par = (__builtin_popcount((unsigned)(i & 3 & e & 3)) + (q0 & (e >> 2)) +
+                     __builtin_popcount((unsigned)((i >> 2) & kg)) + (neg ? 1 : 0)) & 1;
+    pair |= (par ? 0xbf80u : 0x3f80u) << (16 * s);
+  }
+  return pair;
+}
+
+// Every operand of a lane is built from its two dwords A = dword 0 and B = dword 1 of the
+// (q0 = 0, neg = false) form: (A, B, A, B) for q0 = 0 and (A, B, A^F, B^F) for q0 = 1, all xor F
+// when negated (F = 0x80008000 flips both bf16 signs).  Checked for every lane and form:
+constexpr bool wht_sign_pair_form_holds() {
+  constexpr uint32_t F = 0x80008000u;
+  for (int i = 0; i < 16; ++i)
+    for (int kg = 0; kg < 4; ++kg)
+      for (int q0 = 0; q0 < 2; ++q0)
+        for (int n = 0; n < 2; ++n) {
+          const uint32_t a = wht_sign_dword(i, kg, 0, false, 0), b = wht_sign_dword(i, kg, 0, false, 1);
+          const uint32_t want[4] = {a, b, q0 ? a ^ F : a, q0 ? b ^ F : b};
+          for (int h = 0; h < 4; ++h)
+            if (wht_sign_dword(i, kg, q0, n != 0, h) != (n ? want[h] ^ F : want[h])) return false;
+        }
+  return true;
+}
+static_assert(wht_sign_pair_form_holds(), "WHT sign operands from two dwords per lane");
+
+// The four operand forms [q0][negated] of a lane from its two dwords (see above).
+__device__ __forceinline__ void wht_operands_from_pair(uint32_t a, uint32_t b, u32x4 (&op)[2][2]) {
+  constexpr uint32_t F = 0x80008000u;
+  op[0][0] = u32x4{a, b, a, b};
+  op[0][1] = u32x4{a ^ F, b ^ F, a ^ F, b ^ F};
+  op[1][0] = u32x4{a, b, a ^ F, b ^ F};
+  op[1][1] = u32x4{a ^ F, b ^ F, a, b};
+}
+
 // A operand of tile parity q0 for lane (i, kg): 8 bf16 signs for e = 0..7.
 __device__ __forceinline__ u32x4 wht_base_operand(int i, int kg, int q0, bool neg) {
   const int v = i & 3, gp = i >> 2;
@@ -29,30 +69,49 @@ __device__ __forceinline__ u32x4 wht_base_operand(int i, int kg, int q0, bool ne
 // op = the four wht_base_operand forms [q0][negated].
 // f(k, y + 8k) gives the 8 bf16 stored for the lane's columns 32g + 8k .. +7 from their fp32
 // rotated values (wht128_lds stores bf16(y); a fused consumer stores its result instead).
-template <class F>
-__device__ __forceinline__ void wht128_lds_map(unsigned char* base, const u32x4 (&op)[2][2], F f) {
+// at(c) is the LDS address of the lane's 16-byte chunk c (columns 32g + 8c .. +7).
+template <class A, class F>
+__device__ __forceinline__ void wht128_lds_at(A at, const u32x4 (&op)[2][2], F f) {
   const float kScale = 0.08838834764831845f;  // fp32(1/sqrt(128))
   u32x4 xv[4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) xv[c] = *reinterpret_cast<const u32x4*>(base + 16 * c);
-  float out[32];
+  for (int c = 0; c < 4; ++c) xv[c] = *reinterpret_cast<const u32x4*>(at(c));
+  // two halves of the outputs (chunks 0-1, then 2-3): every input is in registers already,
+  // and half the output registers are live at a time
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    f32x4 acc = zero4();
+  for (int h = 0; h < 2; ++h) {
+    float out[16];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int flip = (((q >> 1) & c & 1) ^ ((q >> 2) & (c >> 1) & 1));
-      acc = mfma_16x16x32(op[q & 1][flip], xv[c], acc);
+    for (int qq = 0; qq < 4; ++qq) {
+      const int q = 4 * h + qq;
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int flip = (((q >> 1) & c & 1) ^ ((q >> 2) & (c >> 1) & 1));
+        acc = mfma_16x16x32(op[q & 1][flip], xv[c], acc);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) out[4 * qq + v] = acc[v] * kScale;
     }
 #pragma unroll
-    for (int v = 0; v < 4; ++v) out[4 * q + v] = acc[v] * kScale;
+    for (int kk = 0; kk < 2; ++kk) *reinterpret_cast<u32x4*>(at(2 * h + kk)) = f(2 * h + kk, out + 8 * kk);
   }
-#pragma unroll
-  for (int k = 0; k < 4; ++k) *reinterpret_cast<u32x4*>(base + 16 * k) = f(k, out + 8 * k);
+}
+
+template <class F>
+__device__ __forceinline__ void wht128_lds_map(unsigned char* base, const u32x4 (&op)[2][2], F f) {
+  wht128_lds_at([base](int c) { return base + 16 * c; }, op, f);
 }
 
 __device__ __forceinline__ void wht128_lds(unsigned char* base, const u32x4 (&op)[2][2]) {
   wht128_lds_map(base, op, [](int, const float* y) { return pack8(y); });
+}
+
+// wht128_lds on a row of a swizzled tile: the row's 16-byte chunk c (columns 8c .. 8c+7 of the
+// 128) sits at row + 16 * (c ^ sw), sw < 16; the lane's chunks are 4g .. 4g+3.
+__device__ __forceinline__ void wht128_lds_swz(unsigned char* row, int g, int sw, const u32x4 (&op)[2][2]) {
+  wht128_lds_at([=](int c) { return row + 16 * ((4 * g + c) ^ sw); }, op,
+                [](int, const float* y) { return pack8(y); });
 }
 
 }  // namespace lrq
