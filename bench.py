@@ -6,12 +6,15 @@ Default workload (BASELINE.json metric): rank-16 int4/g64 encode + decode of a b
 rotate over several HBM-resident buffer sets (> 512 MB of X) so the 256 MB MALL cannot
 serve them.  Prints ONE JSON line (driver contract).
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config north_star|c1|c2|c3|c4|c5|lora|legacy]
+  python bench.py [--gpus 1] [--steps K] [--warmup W]
+                  [--config north_star|c1|c2|c3|c4|c5|c5w|lora|legacy|ref_enc|ref_dec] [--m M]
                   [--no-cpu-baseline]
 
 value       = activation GB/s = 2*rows*hidden bytes / (encode + decode time per step);
               fused-consumer configs: / (consumer time); lora: / (x A + x^T g time);
-              legacy: / (encode + outlier compaction + decode time)
+              legacy: / (encode + outlier compaction + decode time); ref_enc / ref_dec (the
+              reference's own speed tests, x [4, M, M]): / (1-bit encode + compaction) and
+              / (2-bit decode from COO)
 timing      = exactly --warmup untimed steps, then exactly --steps timed steps between two HIP
               events on the launch stream (synchronised before and after); `settled` repeats
               the timed steps after --settle-seconds of sustained work, as a separate field
@@ -56,6 +59,7 @@ def parse():
     # reported as `settled` (the GPU's clocks settle over about a second of sustained work)
     ap.add_argument("--settle-seconds", type=float, default=2.0)
     ap.add_argument("--config", default="north_star")
+    ap.add_argument("--m", type=int, default=0, help="ref_enc / ref_dec: M of x [4, M, M] (the reference's sweep)")
     ap.add_argument("--nbuf", type=int, default=4)
     ap.add_argument("--cold-steps", type=int, default=20, help="timed launches of the last kernel with HBM-cold inputs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -116,6 +120,17 @@ def cpu_baseline(cfg, seconds: float):
     V = pkg.inputs.basis(cfg.hidden, cfg.rank, cfg.seed) if cfg.rank else None
 
     def prepare(r):
+        if cfg.consumer in ("ref_enc", "ref_dec"):
+            ops = pkg.inputs.ref_operands(cfg)
+            g = torch.Generator().manual_seed(cfg.seed)
+            d = dict(l=ops["l"][:r], r=ops["r"], s=ops["s"][:1])
+            if cfg.consumer == "ref_enc":
+                d["x"] = torch.randn((1, r, cfg.hidden), generator=g).to(torch.bfloat16)
+            else:
+                d["q"] = torch.randint(0, 256, (1, r, cfg.hidden * cfg.bits // 8), generator=g, dtype=torch.uint8)
+                o = torch.randn((1, r, cfg.hidden), generator=g).to(torch.bfloat16)
+                d["o"] = (o * (o > 1)).to_sparse()
+            return d
         if cfg.consumer == "legacy":
             ops = pkg.inputs.legacy_operands(cfg)
             x = pkg.inputs.activation(r, cfg.hidden, cfg.n_outlier, cfg.outlier_scale, cfg.seed)[None]
@@ -131,7 +146,12 @@ def cpu_baseline(cfg, seconds: float):
 
     def run(inp):
         t0 = time.perf_counter()
-        if cfg.consumer == "legacy":
+        if cfg.consumer == "ref_enc":
+            o, q = T.legacy_encode(inp["l"], inp["r"], inp["x"], inp["s"], cfg.bits, cfg.tau)
+            T.to_coo(o)
+        elif cfg.consumer == "ref_dec":
+            T.legacy_decode(inp["l"], inp["r"], inp["q"], inp["o"].to_dense(), inp["s"], cfg.bits)
+        elif cfg.consumer == "legacy":
             o, q = T.legacy_encode(inp["l"], inp["r"], inp["x"], inp["s"], cfg.bits, inp["tau"])
             o = T.to_coo(o)
             T.legacy_decode(inp["l"], inp["r"], q, o.to_dense(), inp["s"], cfg.bits)
@@ -148,22 +168,26 @@ def cpu_baseline(cfg, seconds: float):
                 {"silu": T.silu_bwd, "gelu": T.gelu_bwd, "softmax": T.softmax_bwd}[cfg.consumer](xh, inp["dy"])
         return time.perf_counter() - t0
 
-    rows = min(cfg.rows, 256)
+    limit = cfg.hidden if cfg.consumer in ("ref_enc", "ref_dec") else cfg.rows  # (one batch of x [B, M, M])
+    rows = min(limit, 256)
     inp = prepare(rows)
     t = run(inp)
-    while t < seconds / 4 and rows < cfg.rows:
-        rows = min(cfg.rows, rows * 4)
+    while t < seconds / 4 and rows < limit:
+        rows = min(limit, rows * 4)
         inp = prepare(rows)
         t = run(inp)
-    if t < 0.7 * seconds and rows < cfg.rows:
-        rows = min(cfg.rows, max(rows, int(rows * seconds / max(t, 1e-3))))
+    if t < 0.7 * seconds and rows < limit:
+        rows = min(limit, max(rows, int(rows * seconds / max(t, 1e-3))))
         inp = prepare(rows)
         run(inp)  # warm-up at the final size
     times = [run(inp) for _ in range(3)]
     t = statistics.median(times)
     gbs = 2 * rows * cfg.hidden / t / 1e9
     what = {"decode": "encode+decode", "lora": "decode + x A + x^T g (LoRA factor gradients)",
-            "legacy": "reference torch encode + to_sparse + decode"}.get(cfg.consumer, f"decode+{cfg.consumer} backward")
+            "legacy": "reference torch encode + to_sparse + decode",
+            "ref_enc": "reference torch encode + to_sparse (one batch's rows of x [B, M, M])",
+            "ref_dec": "reference to_dense + torch decode (one batch's rows of x [B, M, M])"}.get(
+                cfg.consumer, f"decode+{cfg.consumer} backward")
     return {"value": round(gbs, 4), "unit": "GB/s", "cores": cores, "kind": "port",
             "sample": f"PyTorch-eager fp32 {what} (oracle/lrq_torch.py) of {rows} of {cfg.rows} rows x {cfg.hidden} "
                       f"(same recipe), median of 3 runs {', '.join(f'{x:.2f}' for x in times)} s after 1 warm-up, "
@@ -238,12 +262,83 @@ def build_plan_legacy(cfg, pkg, lib, dev, nbuf):
     return entries, 2 * M * N, ["encode", "compact", "decode"], sets
 
 
+def build_plan_ref(cfg, pkg, lib, dev, nbuf):
+    """The reference's own speed tests of its format, x [B, M, M] (see inputs.CONFIGS): ref_enc =
+    the 1-bit encode (codes + dense outliers) and the GPU compaction of the outliers to COO (the
+    reference's o.to_sparse(), without its host synchronisation); ref_dec = the 2-bit decode
+    reading COO outliers o = N(0,1) * (o > 1) (built once by the same compaction, not timed)."""
+    import torch
+    c_void_p = ctypes.c_void_p
+    sp = c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    B, M, N, K, bits = cfg.batch, cfg.hidden, cfg.hidden, cfg.rank, cfg.bits
+    ops = pkg.inputs.ref_operands(cfg, dev)
+    l, r, s = ops["l"], ops["r"], ops["s"]
+    rt = r.t().contiguous()
+    npc = (N + 63) // 64
+    P = lambda t: c_void_p(t.data_ptr())  # noqa: E731
+    wsb = lib.lrq_coo_workspace(B, M, N)
+    cap = B * M * N // 64 if cfg.consumer == "ref_enc" else int(0.2 * B * M * N) + 1024
+    sets = []
+    for i in range(nbuf):
+        g = torch.Generator(device=dev)
+        g.manual_seed(cfg.seed + 101 * i)
+        st = dict(idx=torch.empty((3, cap), dtype=torch.int64, device=dev),
+                  vals=torch.empty((cap,), dtype=torch.bfloat16, device=dev),
+                  nnz=torch.empty((1,), dtype=torch.int64, device=dev),
+                  ptr=torch.empty((B * M * npc + 1,), dtype=torch.int64, device=dev),
+                  ws=torch.empty(((wsb + 7) // 8,), dtype=torch.int64, device=dev))
+        if cfg.consumer == "ref_enc":
+            st["x"] = torch.randn((B, M, N), generator=g, device=dev).to(torch.bfloat16)
+            st["o"] = torch.empty_like(st["x"])
+            st["q"] = torch.empty((B, M, N * bits // 8), dtype=torch.uint8, device=dev)
+        else:
+            st["q"] = torch.randint(0, 256, (B, M, N * bits // 8), generator=g, device=dev, dtype=torch.uint8)
+            st["out"] = torch.empty((B, M, N), dtype=torch.bfloat16, device=dev)
+            o = torch.randn((B, M, N), generator=g, device=dev).to(torch.bfloat16)
+            o = o * (o > 1)
+            if lib.lrq_coo_compact(P(o), B, M, N, P(st["idx"]), cap, P(st["vals"]), cap, P(st["nnz"]), P(st["ptr"]),
+                                   P(st["ws"]), wsb, sp):
+                raise RuntimeError("compaction failed")
+            torch.cuda.synchronize()
+            del o
+        sets.append(st)
+    enc = lambda k: lib.lrq_legacy_encode(P(l), P(rt), K, P(sets[k]["x"]), B, M, N, M * N, N, P(s), B, bits,  # noqa: E731
+                                          cfg.tau, P(sets[k]["o"]), P(sets[k]["q"]), sp)
+    cmp_ = lambda k: lib.lrq_coo_compact(P(sets[k]["o"]), B, M, N, P(sets[k]["idx"]), cap, P(sets[k]["vals"]),  # noqa: E731
+                                         cap, P(sets[k]["nnz"]), P(sets[k]["ptr"]), P(sets[k]["ws"]), wsb, sp)
+    dec = lambda k: lib.lrq_legacy_decode_coo(P(l), P(rt), K, P(sets[k]["q"]), P(sets[k]["ptr"]),  # noqa: E731
+                                              c_void_p(sets[k]["idx"].data_ptr() + 2 * cap * 8), P(sets[k]["vals"]),
+                                              cap, P(s), B, B, M, N, bits, P(sets[k]["out"]), sp)
+    if cfg.consumer == "ref_enc":
+        for k in range(nbuf):
+            if enc(k) or cmp_(k):
+                raise RuntimeError("encode / compaction failed")
+    torch.cuda.synchronize()
+    nnz = max(int(st["nnz"].item()) for st in sets)
+    if nnz > cap:
+        raise RuntimeError(f"{nnz} outliers exceed the bench capacity {cap}")
+    small = 2 * (M * K + N * K) + 2 * B * N
+    E = B * M * N
+    if cfg.consumer == "ref_enc":
+        entries = [("encode", enc, E * (2 + bits / 8 + 2) + small, 2 * E * K),
+                   ("compact", cmp_, E * 2 + nnz * 26 + B * M * npc * 8, 0)]
+        timed = ["encode", "compact"]
+    else:
+        entries = [("decode", dec, E * (bits / 8 + 2) + nnz * 10 + B * M * npc * 8 + small, 2 * E * K)]
+        timed = ["decode"]
+    sets[0]["nnz_count"] = nnz
+    sets[0]["tau"] = cfg.tau
+    return entries, 2 * E, timed, sets
+
+
 def build_plan(cfg, pkg, lib, dev, nbuf):
     """Per-config step: a list of (name, launch(k) -> status, algorithmic bytes, mfma flops) run
     in order on buffer set k, plus the step's activation bytes and how `value` is formed."""
     import torch
     if cfg.consumer == "legacy":
         return build_plan_legacy(cfg, pkg, lib, dev, nbuf)
+    if cfg.consumer in ("ref_enc", "ref_dec"):
+        return build_plan_ref(cfg, pkg, lib, dev, nbuf)
     c_void_p = ctypes.c_void_p
     sp = c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     M, N, r = cfg.rows, cfg.hidden, cfg.rank
@@ -350,6 +445,9 @@ def main():
     lib_mod = import_module("triton-kernel-test_amd._lib")
     lib = lib_mod.load()
     cfg = pkg.inputs.CONFIGS[args.config]
+    if args.m and cfg.consumer in ("ref_enc", "ref_dec"):
+        import dataclasses
+        cfg = dataclasses.replace(cfg, rows=cfg.batch * args.m, hidden=args.m)
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream(dev)
@@ -487,6 +585,12 @@ def main():
         workload = f"fused {' + '.join(timed)} on the compressed activation (encode timed alongside)"
         if cfg.consumer == "legacy":
             workload = "reference format: encode + outliers to COO on the GPU + decode from the COO pieces"
+        elif cfg.consumer == "ref_enc":
+            workload = (f"reference speed test, x [{cfg.batch}, {cfg.hidden}, {cfg.hidden}]: {cfg.bits}-bit encode, "
+                        f"threshold {cfg.tau:g}, outliers compacted to COO on the GPU")
+        elif cfg.consumer == "ref_dec":
+            workload = (f"reference speed test, x [{cfg.batch}, {cfg.hidden}, {cfg.hidden}]: {cfg.bits}-bit decode "
+                        f"from COO outliers N(0,1) * (o > 1)")
     dom_name, dom_alg, dom_us = None, 0, -1.0
     for name, _, alg, _ in entries:
         if kernels[name]["mean_us"] > dom_us:
@@ -530,6 +634,9 @@ def main():
     if cfg.consumer == "legacy":
         line["legacy"] = {"outliers": _sets[0]["nnz_count"], "threshold": _sets[0]["tau"],
                           "torch_to_sparse_us": round(_sets[0]["torch_to_sparse_us"], 1)}
+    if cfg.consumer in ("ref_enc", "ref_dec"):
+        line["legacy"] = {"outliers": _sets[0]["nnz_count"], "threshold": _sets[0]["tau"], "batch": cfg.batch,
+                          "M": cfg.hidden}
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
     print(json.dumps(line), flush=True)

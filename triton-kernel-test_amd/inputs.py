@@ -23,8 +23,8 @@ from dataclasses import dataclass, field
 
 import torch
 
-__all__ = ["Config", "CONFIGS", "activation", "basis", "gradient", "softmax_probs", "lora_factor", "legacy_operands",
-           "make"]
+__all__ = ["Config", "CONFIGS", "REF_M", "activation", "basis", "gradient", "softmax_probs", "lora_factor",
+           "legacy_operands", "ref_operands", "make"]
 
 
 @dataclass(frozen=True)
@@ -39,11 +39,13 @@ class Config:
     outlier_scale: float = 1.0
     keep_channels: int = 0      # channels kept dense as fp16 side columns (top-k by abs-max)
     hadamard: bool = False
-    consumer: str = "decode"    # decode | silu | gelu | softmax | lora | legacy
+    consumer: str = "decode"    # decode | silu | gelu | softmax | lora | legacy | ref_enc | ref_dec
     lora_rank: int = 16         # consumer "lora": n of the LoRA factor A [hidden, n] and of g [rows, n]
     grad_std: float = 0.02
     seed: int = 0
     softmax_shape: tuple = field(default=())
+    batch: int = 1              # ref_enc / ref_dec: x is [batch, rows / batch, hidden]
+    tau: float = 0.0            # ref_enc: the outlier threshold
 
 
 CONFIGS = {
@@ -63,7 +65,16 @@ CONFIGS = {
     # the reference's own format (legacy): rank-16 factors, 2-bit symmetric codes (the system
     # profile's quantize_bit=2), outliers above the 99th percentile kept as COO
     "legacy": Config("legacy", 16384, 4096, 16, 2, 0, n_outlier=8, outlier_scale=20.0, consumer="legacy", seed=7),
+    # the reference's own speed tests of its format (low_rank_kernel_encode_speed_test.py:28-48,
+    # low_rank_kernel_decode_speed_test.py:28-53): x [4, M, M] ~ N(0,1), l [M, 16] and r [16, M]
+    # ~ N(0,1), s = N(0,1) + 2 per batch row; 1-bit encode with threshold 12 (outliers compacted to
+    # COO on the GPU), 2-bit decode from COO outliers o = N(0,1) * (o > 1).  M is 256 * {2, 12, ..,
+    # 72} there; bench.py --m picks it (default 8192).
+    "ref_enc": Config("ref_enc", 4 * 8192, 8192, 16, 1, 0, consumer="ref_enc", seed=9, batch=4, tau=12.0),
+    "ref_dec": Config("ref_dec", 4 * 8192, 8192, 16, 2, 0, consumer="ref_dec", seed=10, batch=4),
 }
+
+REF_M = [256 * i for i in range(2, 80, 10)]  # the reference speed tests' sweep: 512 .. 18432
 
 
 def _gen(seed: int, device) -> torch.Generator:
@@ -127,6 +138,17 @@ def legacy_operands(cfg: Config, device="cpu") -> dict:
     r = (torch.randn((cfg.rank, cfg.hidden), generator=g) * 0.5).to(torch.bfloat16)
     s = (0.05 + 0.3 * torch.rand((1, cfg.hidden), generator=g)).to(torch.bfloat16)
     return {"l": l.to(device), "r": r.to(device), "s": s.to(device)}
+
+
+def ref_operands(cfg: Config, device="cpu") -> dict:
+    """The reference speed tests' operands for x [B, M, M]: l [M, 16], r [16, M] ~ N(0,1),
+    s [B, M] = N(0,1) + 2 (bf16)."""
+    B, M = cfg.batch, cfg.hidden
+    g = _gen(cfg.seed + 5_000_011, device)
+    l = torch.randn((M, cfg.rank), generator=g, device=device).to(torch.bfloat16)
+    r = torch.randn((cfg.rank, M), generator=g, device=device).to(torch.bfloat16)
+    s = (torch.randn((B, M), generator=g, device=device) + 2).to(torch.bfloat16)
+    return {"l": l, "r": r, "s": s}
 
 
 def lora_factor(hidden: int, n: int, seed: int = 0, device="cpu") -> torch.Tensor:
