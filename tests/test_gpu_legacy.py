@@ -261,6 +261,33 @@ def test_legacy_decode_coo_is_dense_decode(pkg, dev, B, M, N, K, bits, s_rows, t
     assert _frac_mismatch(bits16(a), xh_ref) <= TIE_BUDGET
 
 
+# the reference decode test's outliers (low_rank_kernel_decode_speed_test.py:38-40): o = N(0,1) *
+# (o > 1), about 16 % of the elements, above the density at which the decode gathers each wave's
+# COO pieces into an LDS tile; random codes, per-batch scales; every bit width, ragged rows
+@pytest.mark.parametrize("B,M,N,bits", [(2, 100, 1024, 2), (1, 70, 2048, 1), (2, 33, 512, 4), (1, 50, 512, 8),
+                                        (4, 64, 1024, 2)])
+def test_legacy_decode_dense_coo(pkg, dev, B, M, N, bits):
+    print(f"[dense coo decode] B={B} M={M} N={N} bits={bits}", flush=True)
+    g = torch.Generator().manual_seed(3000 + N + bits)
+    l = torch.randn(M, 16, generator=g).to(torch.bfloat16)
+    r = torch.randn(16, N, generator=g).to(torch.bfloat16)
+    s = (torch.randn(B, N, generator=g) + 2).to(torch.bfloat16)
+    q = torch.randint(0, 256, (B, M, N * bits // 8), generator=g, dtype=torch.uint8)
+    o = torch.randn(B, M, N, generator=g).to(torch.bfloat16)
+    o = o * (o > 1)
+    ld, rd, sd, qd, od = l.to(dev), r.to(dev), s.to(dev), q.to(dev), o.to(dev)
+    oc = pkg.compact_outliers(od, capacity=o.numel())
+    a = pkg.low_rank_addition_fuse_decompression_dequantization(ld, rd, qd, oc, sd, quantize_bit=bits)
+    b = pkg.low_rank_addition_fuse_decompression_dequantization(ld, rd, qd, od.to_sparse(), sd, quantize_bit=bits)
+    c = pkg.low_rank_addition_fuse_decompression_dequantization(ld, rd, qd, od, sd, quantize_bit=bits)
+    torch.cuda.synchronize()
+    nnz = int(oc.nnz.item())
+    assert nnz * 16 > o.numel(), "the case must take the dense-COO path"
+    assert torch.equal(a, c) and torch.equal(b, c)
+    xh_ref = O.legacy_decode(bits16(l), bits16(r), q.numpy(), bits16(o), bits16(s), bits)
+    assert _frac_mismatch(bits16(a), xh_ref) <= TIE_BUDGET
+
+
 @pytest.mark.parametrize("M,N,K", [(256, 1024, 16), (50, 100, 20), (128, 2048, 32)])
 def test_outlier_threshold_is_kthvalue(pkg, dev, M, N, K):
     """outlier_threshold = torch.kthvalue(|x[0] - l @ r|, int(numel * 0.99)) of

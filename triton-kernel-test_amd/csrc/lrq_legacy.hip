@@ -97,8 +97,9 @@ __device__ __forceinline__ float legacy_consume(float xh, float yv) {
   else return xh;
 }
 
-// The outlier values of columns c0 .. c0 + E - 1 of row `bm` (b * M + m) from the COO pieces:
-// the entries of the piece holding c0 (the E columns never straddle a piece boundary).
+// The outlier values of columns c0 .. c0 + E - 1 of row `bm` (b * M + m) from the COO pieces
+// (sparse outliers, OSRC 2): the entries of the piece holding c0 (the E columns never straddle a
+// piece boundary), one at a time.
 template <int E>
 __device__ __forceinline__ void coo_piece_values(const LegacyArgs& a, int64_t bm, int64_t c0, float* oo) {
 #pragma unroll
@@ -113,14 +114,73 @@ __device__ __forceinline__ void coo_piece_values(const LegacyArgs& a, int64_t bm
   }
 }
 
+// Denser outliers (OSRC 3): the COO pieces of a wave's 16 rows x one unit (NP pieces of 64
+// columns per row) go into the wave's
+// LDS tile ot[row][plane][64] (bf16 bits).  The four lanes of a row share its pieces: every
+// plane's piece bounds are requested at once, then in each pass lane (j, g) requests entries
+// g, g + 4, .. (KL per piece) of each of its row's pieces, all of them before any is used
+// (clamped indices; no load sits under a branch), and writes those that fall in the piece into
+// the tile after the lane has zeroed its own 16 columns of every plane.  Another pass runs only
+// while some piece of the wave has more entries.  Entries of a coalesced COO are unique per
+// position (so no two lanes write the same one), and entries outside the piece are ignored.
+template <int NP, int KL>
+__device__ __forceinline__ void coo_tile(const LegacyArgs& a, int64_t bm, int u, int N, int j, int g,
+                                         uint16_t* __restrict__ ot) {
+  int64_t s0[NP], s1[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int64_t pc = bm * a.npc + (int64_t)(p * (N / NP) + u * 64) / 64;
+    s0[p] = a.optr[pc];
+    s1[p] = a.optr[pc + 1];
+  }
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    uint16_t* r = ot + (j * NP + p) * 64 + 16 * g;
+    st16(r, u32x4{0u, 0u, 0u, 0u});
+    st16(r + 8, u32x4{0u, 0u, 0u, 0u});
+    s0[p] = max(s0[p], (int64_t)0);
+    s1[p] = min(s1[p], a.ncap);
+  }
+  if (a.ncap <= 0) return;  // uniform: no entries at all
+  const uint32_t* col32 = reinterpret_cast<const uint32_t*>(a.ocol);  // low dword of each int64 column
+  for (int pass = 0;; ++pass) {
+    uint32_t cv[NP][KL];
+    uint16_t vv[NP][KL];
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int i = 0; i < KL; ++i) {
+        const int64_t k = min(s0[p] + (int64_t)(4 * KL * pass + g + 4 * i), a.ncap - 1);
+        cv[p][i] = col32[2 * k];
+        vv[p][i] = a.oval[k];
+      }
+    bool more = false;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int64_t base = p * (N / NP) + u * 64;
+#pragma unroll
+      for (int i = 0; i < KL; ++i) {
+        const int64_t k = s0[p] + (int64_t)(4 * KL * pass + g + 4 * i);
+        const int64_t d = (int64_t)cv[p][i] - base;
+        if (k < s1[p] && d >= 0 && d < 64) ot[(j * NP + p) * 64 + (int)d] = vv[p][i];
+      }
+      more |= s1[p] - s0[p] > (int64_t)4 * KL * (pass + 1);
+    }
+    if (!__builtin_amdgcn_ballot_w64(more)) break;  // uniform
+  }
+}
+
 // ------------------------------------------------------------------ MFMA path
 // Grid: (ceil(M / (64 * RB)), N / (64 * NP), B); 4 waves; wave w walks row blocks
 // (blockIdx.x * RB + i) * 64 + w * 16, i < RB, of unit blockIdx.y.  OSRC: outliers absent (0),
-// dense (1) or COO pieces (2), decode only.
+// dense (1) or COO pieces (2: looked up per lane, for sparse outliers; 3: gathered per wave into
+// an LDS tile, for denser ones), decode only.
 template <int MODE, int BITS, int K, int RB, int OSRC>
 __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
   constexpr int NP = (MODE == kAdd || MODE == kHist) ? 1 : 8 / BITS, G = 64, E = 16, RT = K / 16;
   __shared__ uint32_t lh[MODE == kHist ? 256 : 1];
+  // decode from denser COO outliers: each wave's outlier tile (16 rows x NP planes x 64 columns, bf16)
+  __shared__ __attribute__((aligned(16))) uint16_t otile[(MODE == kDecode && OSRC == 3) ? 4 * 16 * NP * 64 : 8];
   int64_t sel = -1;
   if constexpr (MODE == kHist) {
     lh[threadIdx.x] = 0u;
@@ -155,6 +215,8 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
     uint32_t byte[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) byte[e] = 0u;
+    uint16_t* ot = otile + (size_t)w * 16 * NP * 64;
+    if constexpr (MODE == kDecode && OSRC == 3) coo_tile<NP, 4>(a, (int64_t)b * M + rr, u, N, j, g, ot);
 
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
@@ -205,6 +267,11 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
           unpack8(ld16(a.oin + erow + c0 + 8), oo + 8);
         }
         if constexpr (MODE == kDecode && OSRC == 2) coo_piece_values<E>(a, (int64_t)b * M + rr, c0, oo);
+        if constexpr (MODE == kDecode && OSRC == 3) {
+          const uint16_t* r = ot + (j * NP + p) * 64 + 16 * g;
+          unpack8(*reinterpret_cast<const u32x4*>(r), oo);
+          unpack8(*reinterpret_cast<const u32x4*>(r + 8), oo + 8);
+        }
         if constexpr (MODE == kFusedSilu || MODE == kFusedMul) {
           unpack8(ld16(a.y + erow + c0), yv);
           unpack8(ld16(a.y + erow + c0 + 8), yv + 8);
@@ -273,7 +340,7 @@ __global__ __launch_bounds__(256) void k_legacy_scalar(LegacyArgs a, int K, int6
       const uint32_t code = (byte >> (BITS * p)) & kMask;
       float o = 0.f, yv = 0.f;
       if constexpr (MODE == kDecode && OSRC == 1) o = __uint_as_float((uint32_t)a.oin[erow + col] << 16);
-      if constexpr (MODE == kDecode && OSRC == 2) {
+      if constexpr (MODE == kDecode && OSRC >= 2) {  // COO pieces (both lookups give the same values)
         const int64_t pc = bm * a.npc + col / 64, e1 = min(a.optr[pc + 1], a.ncap);
         for (int64_t k = max(a.optr[pc], (int64_t)0); k < e1; ++k)
           if (a.ocol[k] == col) o = __uint_as_float((uint32_t)a.oval[k] << 16);
@@ -488,6 +555,9 @@ extern "C" int lrq_legacy_decode_coo(const void* l, const void* rt, int32_t K, c
   a.qin = (const uint8_t*)q, a.out = (uint16_t*)out, a.M = M, a.N = N;
   a.optr = piece_ptr, a.ocol = cols, a.oval = (const uint16_t*)vals, a.npc = (N + 63) / 64, a.ncap = n_entries;
   const bool mfma_ok = vec_ok({l, rt, q, s, out}) && N % 8 == 0;
+  // more than about 4 entries per 64-column piece (1/16 of the elements): the wave gathers its
+  // pieces' entries cooperatively (an LDS tile); sparser: each lane reads its piece's few entries
+  if (mfma_ok && n_entries * 16 > B * M * N) return legacy_bits<kDecode, 3>(a, K, B, bits, mfma_ok, (hipStream_t)stream);
   return legacy_bits<kDecode, 2>(a, K, B, bits, mfma_ok, (hipStream_t)stream);
 }
 
