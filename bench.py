@@ -12,8 +12,8 @@ serve them.  Prints ONE JSON line (driver contract).
 
 value       = activation GB/s = 2*rows*hidden bytes / (encode + decode time per step);
               fused-consumer configs: / (consumer time); lora: / (x A + x^T g time);
-              legacy: / (encode + outlier compaction + decode time); ref_enc / ref_dec (the
-              reference's own speed tests, x [4, M, M]): / (1-bit encode + compaction) and
+              legacy: / (encode with its outlier compaction + decode time); ref_enc / ref_dec
+              (the reference's own speed tests, x [4, M, M]): / (1-bit encode + compaction) and
               / (2-bit decode from COO)
 timing      = exactly --warmup untimed steps, then exactly --steps timed steps between two HIP
               events on the launch stream (synchronised before and after); `settled` repeats
@@ -226,27 +226,31 @@ def build_plan_legacy(cfg, pkg, lib, dev, nbuf):
                          out=torch.empty_like(x)))
     tau = float(pkg.outlier_threshold(l, r, sets[0]["x"]).item())  # 1 % outliers, as the reference calibrates
     P = lambda t: c_void_p(t.data_ptr())  # noqa: E731
-    enc = lambda k: lib.lrq_legacy_encode(P(l), P(rt), K, P(sets[k]["x"]), 1, M, N, M * N, N, P(s), 1, bits,  # noqa: E731
-                                          tau, P(sets[k]["o"]), P(sets[k]["q"]), sp)
-    cmp_ = lambda k: lib.lrq_coo_compact(P(sets[k]["o"]), 1, M, N, P(sets[k]["idx"]), cap, P(sets[k]["vals"]),  # noqa: E731
-                                         cap, P(sets[k]["nnz"]), P(sets[k]["ptr"]), P(sets[k]["ws"]), wsb, sp)
+    # the encode and the outlier compaction in one call (the encode counts each piece's outliers,
+    # so the compaction reads the dense outliers once)
+    enc = lambda k: lib.lrq_legacy_encode_coo(P(l), P(rt), K, P(sets[k]["x"]), 1, M, N, M * N, N, P(s), 1,  # noqa: E731
+                                              bits, tau, P(sets[k]["o"]), P(sets[k]["q"]), P(sets[k]["idx"]), cap,
+                                              P(sets[k]["vals"]), cap, P(sets[k]["nnz"]), P(sets[k]["ptr"]),
+                                              P(sets[k]["ws"]), wsb, sp)
     dec = lambda k: lib.lrq_legacy_decode_coo(P(l), P(rt), K, P(sets[k]["q"]), P(sets[k]["ptr"]),  # noqa: E731
                                               c_void_p(sets[k]["idx"].data_ptr() + 2 * cap * 8), P(sets[k]["vals"]),
                                               cap, P(s), 1, 1, M, N, bits, P(sets[k]["out"]), sp)
     for k in range(nbuf):
-        if enc(k) or cmp_(k):
+        if enc(k):
             raise RuntimeError("legacy encode / compaction failed")
     torch.cuda.synchronize()
     nnz = max(int(st["nnz"].item()) for st in sets)
     if nnz > cap:
         raise RuntimeError(f"{nnz} outliers exceed the bench capacity {cap}")
     small = 2 * (M * K + N * K) + 2 * N
+    # algorithmic: encode = x read, codes and the dense outliers written; compaction = the dense
+    # outliers read once, the COO and the piece pointers written
+    enc_b, cmp_b = M * N * (2 + bits / 8 + 2) + small, M * N * 2 + nnz * 26 + M * npc * 8
     entries = [
-        ("encode", enc, M * N * (2 + bits / 8 + 2) + small, 2 * M * N * K),
-        # algorithmic: the dense outliers read once, the COO written, the piece pointers written
-        ("compact", cmp_, M * N * 2 + nnz * 26 + M * npc * 8, 0),
+        ("encode_coo", enc, enc_b + cmp_b, 2 * M * N * K),
         ("decode", dec, M * N * (bits / 8 + 2) + nnz * 10 + M * npc * 8 + small, 2 * M * N * K),
     ]
+    sets[0]["alg_split"] = {"encode": enc_b, "compact": cmp_b}
     # the reference's sparse conversion of the same dense outliers, for comparison (it
     # synchronises the host to size its output): mean over 20 calls
     o0 = sets[0]["o"]
@@ -259,7 +263,7 @@ def build_plan_legacy(cfg, pkg, lib, dev, nbuf):
     sets[0]["torch_to_sparse_us"] = (time.perf_counter() - t0) / 20 * 1e6
     sets[0]["nnz_count"] = nnz
     sets[0]["tau"] = tau
-    return entries, 2 * M * N, ["encode", "compact", "decode"], sets
+    return entries, 2 * M * N, ["encode_coo", "decode"], sets
 
 
 def build_plan_ref(cfg, pkg, lib, dev, nbuf):
@@ -302,16 +306,16 @@ def build_plan_ref(cfg, pkg, lib, dev, nbuf):
             torch.cuda.synchronize()
             del o
         sets.append(st)
-    enc = lambda k: lib.lrq_legacy_encode(P(l), P(rt), K, P(sets[k]["x"]), B, M, N, M * N, N, P(s), B, bits,  # noqa: E731
-                                          cfg.tau, P(sets[k]["o"]), P(sets[k]["q"]), sp)
-    cmp_ = lambda k: lib.lrq_coo_compact(P(sets[k]["o"]), B, M, N, P(sets[k]["idx"]), cap, P(sets[k]["vals"]),  # noqa: E731
-                                         cap, P(sets[k]["nnz"]), P(sets[k]["ptr"]), P(sets[k]["ws"]), wsb, sp)
+    enc = lambda k: lib.lrq_legacy_encode_coo(P(l), P(rt), K, P(sets[k]["x"]), B, M, N, M * N, N, P(s), B,  # noqa: E731
+                                              bits, cfg.tau, P(sets[k]["o"]), P(sets[k]["q"]), P(sets[k]["idx"]),
+                                              cap, P(sets[k]["vals"]), cap, P(sets[k]["nnz"]), P(sets[k]["ptr"]),
+                                              P(sets[k]["ws"]), wsb, sp)
     dec = lambda k: lib.lrq_legacy_decode_coo(P(l), P(rt), K, P(sets[k]["q"]), P(sets[k]["ptr"]),  # noqa: E731
                                               c_void_p(sets[k]["idx"].data_ptr() + 2 * cap * 8), P(sets[k]["vals"]),
                                               cap, P(s), B, B, M, N, bits, P(sets[k]["out"]), sp)
     if cfg.consumer == "ref_enc":
         for k in range(nbuf):
-            if enc(k) or cmp_(k):
+            if enc(k):
                 raise RuntimeError("encode / compaction failed")
     torch.cuda.synchronize()
     nnz = max(int(st["nnz"].item()) for st in sets)
@@ -320,9 +324,10 @@ def build_plan_ref(cfg, pkg, lib, dev, nbuf):
     small = 2 * (M * K + N * K) + 2 * B * N
     E = B * M * N
     if cfg.consumer == "ref_enc":
-        entries = [("encode", enc, E * (2 + bits / 8 + 2) + small, 2 * E * K),
-                   ("compact", cmp_, E * 2 + nnz * 26 + B * M * npc * 8, 0)]
-        timed = ["encode", "compact"]
+        enc_b, cmp_b = E * (2 + bits / 8 + 2) + small, E * 2 + nnz * 26 + B * M * npc * 8
+        entries = [("encode_coo", enc, enc_b + cmp_b, 2 * E * K)]
+        timed = ["encode_coo"]
+        sets[0]["alg_split"] = {"encode": enc_b, "compact": cmp_b}
     else:
         entries = [("decode", dec, E * (bits / 8 + 2) + nnz * 10 + B * M * npc * 8 + small, 2 * E * K)]
         timed = ["decode"]
@@ -637,6 +642,8 @@ def main():
     if cfg.consumer in ("ref_enc", "ref_dec"):
         line["legacy"] = {"outliers": _sets[0]["nnz_count"], "threshold": _sets[0]["tau"], "batch": cfg.batch,
                           "M": cfg.hidden}
+    if "alg_split" in _sets[0]:
+        line["legacy"]["alg_bytes"] = _sets[0]["alg_split"]
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
     print(json.dumps(line), flush=True)

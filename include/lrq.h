@@ -208,6 +208,18 @@ int lrq_coo_compact(const void* o, int64_t B, int64_t M, int64_t N, int64_t* ind
 /* Workspace bytes of lrq_coo_compact (>= 0), or a negative LRQ_ERR_*.  Host only. */
 int64_t lrq_coo_workspace(int64_t B, int64_t M, int64_t N);
 
+/* lrq_legacy_encode followed by lrq_coo_compact of its outliers, with the compaction's count pass
+ * done inside the encode (each 64-column piece's entries counted as they are quantised), so the
+ * dense outliers o are read once, by the scatter: the reference's encode plus o.to_sparse()
+ * (low_rank_extraction_fuse_compression_quantization.py:118-150), without its host
+ * synchronisation.  Arguments as the two calls take them (o is still written: the scatter reads
+ * it); shapes the encode's vectorised path does not take run the two calls. */
+int lrq_legacy_encode_coo(const void* l, const void* rt, int32_t K, const void* x, int64_t B, int64_t M,
+                          int64_t N, int64_t ldx_b, int64_t ldx_m, const void* s, int64_t s_rows,
+                          int32_t bits, float outlier, void* o, void* q, int64_t* indices, int64_t ld_idx,
+                          void* values, int64_t cap, int64_t* nnz, int64_t* piece_ptr, void* workspace,
+                          int64_t workspace_bytes, void* stream);
+
 /* lrq_legacy_decode with the outliers as COO pieces instead of a dense tensor: piece_ptr as
  * lrq_coo_compact writes it, cols = the entries' column indices (int64, row 2 of its indices),
  * vals = their bf16 values, n_entries = how many entries cols / vals hold (reads are clamped to

@@ -31,7 +31,7 @@ def test_algorithmic_bytes():
     assert bench.consumer_bytes(M, N, r, 4, 64) == M * N * (0.5 + 4 / 64 + 4) + 2 * M * r + 2 * N * r
 
 
-@pytest.mark.parametrize("config", ["north_star", "c3", "lora", "legacy"])
+@pytest.mark.parametrize("config", ["north_star", "c3", "lora", "legacy", "ref_enc", "ref_dec"])
 def test_cpu_baseline_fields(config):
     """The CPU baseline is the torch-eager restatement on every core the process may use, with
     the host recorded (a tiny time budget here)."""

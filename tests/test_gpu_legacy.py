@@ -11,6 +11,9 @@ widths, unaligned row strides), K below 16 and between 16 and 32 (zero-padded, R
 batch-shared and per-batch scales, 1/2/4/8-bit codes.
 """
 
+import ctypes
+import importlib
+
 import numpy as np
 import pytest
 import torch
@@ -259,6 +262,41 @@ def test_legacy_decode_coo_is_dense_decode(pkg, dev, B, M, N, K, bits, s_rows, t
     o_ref, _ = O.legacy_encode(bits16(l), bits16(r), bits16(x), bits16(s), bits, tau)
     xh_ref = O.legacy_decode(bits16(l), bits16(r), q.cpu().numpy(), bits16(dense), bits16(s), bits)
     assert _frac_mismatch(bits16(a), xh_ref) <= TIE_BUDGET
+
+
+@pytest.mark.parametrize("B,M,N,K,bits,s_rows,tau", [CASES[0], CASES[1], CASES[2], CASES[5],
+                                                    (2, 37, 512, 16, 1, 2, 1.5), (1, 80, 1024, 16, 2, 1, 0.5)])
+def test_legacy_encode_coo_is_encode_then_compact(pkg, dev, B, M, N, K, bits, s_rows, tau):
+    """lrq_legacy_encode_coo (the encode counting each piece's outliers, then offsets, chunk scan and
+    scatter) gives exactly what lrq_legacy_encode followed by lrq_coo_compact gives: codes, dense
+    outliers, COO indices and values, entry count and piece pointers (dense-ish outliers with a low
+    threshold included)."""
+    print(f"[encode_coo] B={B} M={M} N={N} K={K} bits={bits} tau={tau}", flush=True)
+    lib = importlib.import_module("triton-kernel-test_amd._lib").load()
+    L = importlib.import_module("triton-kernel-test_amd.legacy")
+    l, r, x, s = _inputs(4000 + N + bits, B, M, N, K, s_rows)
+    ld, rd, xd, sd = l.to(dev), r.to(dev), x.to(dev), s.to(dev)
+    cap = B * M * N
+    oc, q, o = L._encode_coo(ld, rd, xd, sd, bits, tau, cap)
+    # the two-call path on the same inputs
+    o2 = torch.empty_like(o)
+    q2 = torch.empty_like(q)
+    l2, rt, KK = L._factors(ld, rd)
+    s2 = L._scale(sd, B, N)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.lrq_legacy_encode(P(l2), P(rt), KK, P(xd), B, M, N, xd.stride(0), xd.stride(1), P(s2), s2.shape[0],
+                                 bits, float(tau), P(o2), P(q2), sp) == 0
+    c2 = pkg.compact_outliers(o2, capacity=cap)
+    torch.cuda.synchronize()
+    n = int(oc.nnz.item())
+    assert n == int(c2.nnz.item()) > 0
+    assert torch.equal(q, q2) and torch.equal(o, o2)
+    assert torch.equal(oc.piece_ptr, c2.piece_ptr)
+    assert torch.equal(oc.indices[:, :n], c2.indices[:, :n]) and torch.equal(oc.values[:n], c2.values[:n])
+    # and the reference-named wrapper returns that sparse tensor
+    o_sp, q3 = pkg.low_rank_addition_fuse_compression_quantization(ld, rd, xd, sd, quantize_bit=bits, outlier=tau)
+    assert torch.equal(q3, q) and torch.equal(o_sp.to_dense(), o.view(o_sp.shape))
 
 
 # the reference decode test's outliers (low_rank_kernel_decode_speed_test.py:38-40): o = N(0,1) *

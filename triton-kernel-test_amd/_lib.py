@@ -70,6 +70,10 @@ SIGNATURES = {
     "lrq_coo_compact": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                   c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
     "lrq_coo_workspace": (c_int64, [c_int64, c_int64, c_int64]),
+    "lrq_legacy_encode_coo": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_int64, c_int64,
+                                        c_int64, c_int64, c_void_p, c_int64, c_int32, c_float, c_void_p,
+                                        c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p,
+                                        c_void_p, c_int64, c_void_p]),
     "lrq_legacy_decode_coo": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p,
                                         c_int64, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int32, c_void_p,
                                         c_void_p]),

@@ -21,6 +21,7 @@
 // the outliers of a 64-column piece from it without a dense tensor.  A value is an entry when
 // its bf16 bits are not +0 or -0 (what to_sparse keeps of a bf16 tensor).
 #include "lrq_common.h"
+#include "lrq_coo.h"
 #include "lrq_host.h"
 
 namespace lrq {
@@ -129,6 +130,34 @@ __global__ __launch_bounds__(kCooThreads) void k_coo_count(const uint16_t* __res
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
     c[i] = cnt[t * PPT + i];
+    s += c[i];
+  }
+  uint32_t total;
+  uint32_t off = coo_block_scan(s, wsum, total);
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const int64_t pc = pc0 + t * PPT + i;
+    if (pc < npieces) piece_ptr[pc] = off;
+    off += c[i];
+  }
+  if (t == 0) chunk_total[blockIdx.x] = total;
+}
+
+// The count pass when the counts are already in piece_ptr (written by the legacy encode): per
+// chunk, the exclusive scan of its pieces' counts replaces them by chunk-local offsets, and the
+// chunk total goes to the workspace (the tail of k_coo_count, reading 8 bytes per piece instead
+// of the piece's 128 bytes of outliers).
+__global__ __launch_bounds__(kCooThreads) void k_coo_offsets(int64_t npieces, int64_t* __restrict__ piece_ptr,
+                                                             uint32_t* __restrict__ chunk_total) {
+  __shared__ uint32_t wsum[kCooThreads / 64];
+  const int t = threadIdx.x;
+  const int64_t pc0 = (int64_t)blockIdx.x * kChunk;
+  constexpr int PPT = kChunk / kCooThreads;
+  uint32_t c[PPT], s = 0;
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const int64_t pc = min(pc0 + t * PPT + i, npieces - 1);  // clamped: loaded, not counted
+    c[i] = pc0 + t * PPT + i < npieces ? (uint32_t)piece_ptr[pc] : 0u;
     s += c[i];
   }
   uint32_t total;
@@ -287,9 +316,9 @@ extern "C" int64_t lrq_coo_workspace(int64_t B, int64_t M, int64_t N) {
   return coo_plan(B, M, N).ws_bytes;
 }
 
-extern "C" int lrq_coo_compact(const void* o, int64_t B, int64_t M, int64_t N, int64_t* indices, int64_t ld_idx,
-                               void* values, int64_t cap, int64_t* nnz, int64_t* piece_ptr, void* workspace,
-                               int64_t workspace_bytes, void* stream) {
+int lrq::coo_compact_check(const void* o, int64_t B, int64_t M, int64_t N, int64_t* indices, int64_t ld_idx,
+                           void* values, int64_t cap, int64_t* nnz, int64_t* piece_ptr, void* workspace,
+                           int64_t workspace_bytes) {
   if (o == nullptr || nnz == nullptr || piece_ptr == nullptr) return LRQ_ERR_NULL;
   if (B < 0 || M < 0 || N <= 0 || cap < 0 || ld_idx < cap) return LRQ_ERR_SHAPE;
   if (M > INT32_MAX || N > INT32_MAX) return LRQ_ERR_SHAPE;  // 32-bit row / piece arithmetic
@@ -303,17 +332,13 @@ extern "C" int lrq_coo_compact(const void* o, int64_t B, int64_t M, int64_t N, i
     if (workspace_bytes < p.ws_bytes) return LRQ_ERR_WORKSPACE;
     if (!aligned(workspace, 8)) return LRQ_ERR_ALIGN;
   }
-  hipStream_t s = (hipStream_t)stream;
-  uint64_t* chunk_off = reinterpret_cast<uint64_t*>(workspace);
-  uint32_t* chunk_total = reinterpret_cast<uint32_t*>(chunk_off + p.nchunks);
-  const bool vec = N % 8 == 0 && aligned(o, 16);
-  const uint16_t* ob = (const uint16_t*)o;
-  if (p.nchunks > 0) {
-    if (vec) LRQ_TRY(launch(k_coo_count<true>, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, ob, N, p.npc,
-                                p.npieces, piece_ptr, chunk_total));
-    else LRQ_TRY(launch(k_coo_count<false>, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, ob, N, p.npc,
-                            p.npieces, piece_ptr, chunk_total));
-  }
+  return LRQ_OK;
+}
+
+// The chunk scan and the scatter (after the count pass, or the encode's counts and their offsets).
+static int coo_scan_scatter(const uint16_t* ob, int64_t M, int64_t N, const CooPlan& p, int64_t* indices,
+                            int64_t ld_idx, void* values, int64_t cap, int64_t* nnz, int64_t* piece_ptr,
+                            uint64_t* chunk_off, uint32_t* chunk_total, bool vec, hipStream_t s) {
   LRQ_TRY(launch(k_coo_scan, dim3(1), dim3(kCooThreads), 0, s, chunk_total, p.nchunks, chunk_off, p.npieces,
                      piece_ptr, nnz));
   if (p.nchunks > 0) {
@@ -325,4 +350,38 @@ extern "C" int lrq_coo_compact(const void* o, int64_t B, int64_t M, int64_t N, i
                             cap));
   }
   return LRQ_OK;
+}
+
+int lrq::coo_compact_counted(const void* o, int64_t B, int64_t M, int64_t N, int64_t* indices, int64_t ld_idx,
+                             void* values, int64_t cap, int64_t* nnz, int64_t* piece_ptr, void* workspace,
+                             hipStream_t s) {
+  const CooPlan p = coo_plan(B, M, N);
+  uint64_t* chunk_off = reinterpret_cast<uint64_t*>(workspace);
+  uint32_t* chunk_total = reinterpret_cast<uint32_t*>(chunk_off + p.nchunks);
+  if (p.nchunks > 0)
+    LRQ_TRY(launch(k_coo_offsets, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, p.npieces, piece_ptr,
+                   chunk_total));
+  return coo_scan_scatter((const uint16_t*)o, M, N, p, indices, ld_idx, values, cap, nnz, piece_ptr, chunk_off,
+                          chunk_total, N % 8 == 0 && aligned(o, 16), s);
+}
+
+extern "C" int lrq_coo_compact(const void* o, int64_t B, int64_t M, int64_t N, int64_t* indices, int64_t ld_idx,
+                               void* values, int64_t cap, int64_t* nnz, int64_t* piece_ptr, void* workspace,
+                               int64_t workspace_bytes, void* stream) {
+  const int st = coo_compact_check(o, B, M, N, indices, ld_idx, values, cap, nnz, piece_ptr, workspace,
+                                   workspace_bytes);
+  if (st) return st;
+  const CooPlan p = coo_plan(B, M, N);
+  hipStream_t s = (hipStream_t)stream;
+  uint64_t* chunk_off = reinterpret_cast<uint64_t*>(workspace);
+  uint32_t* chunk_total = reinterpret_cast<uint32_t*>(chunk_off + p.nchunks);
+  const bool vec = N % 8 == 0 && aligned(o, 16);
+  const uint16_t* ob = (const uint16_t*)o;
+  if (p.nchunks > 0) {
+    if (vec) LRQ_TRY(launch(k_coo_count<true>, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, ob, N, p.npc,
+                                p.npieces, piece_ptr, chunk_total));
+    else LRQ_TRY(launch(k_coo_count<false>, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, ob, N, p.npc,
+                            p.npieces, piece_ptr, chunk_total));
+  }
+  return coo_scan_scatter(ob, M, N, p, indices, ld_idx, values, cap, nnz, piece_ptr, chunk_off, chunk_total, vec, s);
 }

@@ -29,6 +29,7 @@
 //   * k_legacy_scalar — any shape: one thread per packed byte, l @ r summed in fp64 (the
 //     products of bf16 values are exact and so is their fp64 sum for K <= 32).
 #include "lrq_common.h"
+#include "lrq_coo.h"
 #include "lrq_host.h"
 #include "lrq_math.h"
 
@@ -49,6 +50,7 @@ struct LegacyArgs {
   const int64_t* ocol;  //   [B * M * npc + 1]; the entries' column indices and bf16 values, in
   const uint16_t* oval; //   row-major order (lrq_coo_compact's output)
   int64_t npc;          // 64-column pieces per row, ceil(N / 64)
+  int64_t* pcnt;        // encode with counts: outliers per 64-column piece, [B * M * npc]
   int64_t ncap;         // entries the COO arrays hold: reads are clamped to [0, ncap)
   uint32_t* hist;       // hist: 256 global bins
   const int64_t* sel;   // hist: sel[0] = the selected top-8-bit bin, or -1 in the first pass
@@ -62,11 +64,14 @@ struct LegacyArgs {
 
 // Encode of one element given its bf16 input x, bf16(l @ r) lr and scale sc: returns the code
 // (0 .. 2^b - 1) and writes the outlier value (0 unless an outlier).
+// big: |xr| > tau, i.e. o = xr; with tau >= 0 that is exactly an outlier entry the compaction
+// keeps (o's bf16 bits not +-0).
 template <int BITS>
-__device__ __forceinline__ uint32_t legacy_code(float x, float lr, float sc, float tau, float& o) {
+__device__ __forceinline__ uint32_t legacy_code(float x, float lr, float sc, float tau, float& o, bool& big) {
   constexpr float half = (float)(1 << (BITS - 1));
   const float xr = bf16r(x - lr);
-  o = fabsf(xr) > tau ? xr : 0.f;
+  big = fabsf(xr) > tau;
+  o = big ? xr : 0.f;
   const float d = bf16r((xr - o) / sc);  // IEEE division, then the bf16 rounding of the torch op
   const float c = __builtin_amdgcn_fmed3f(rintf(d), -half, half - 1.f);
   return (uint32_t)(int)(c + half);
@@ -172,9 +177,10 @@ __device__ __forceinline__ void coo_tile(const LegacyArgs& a, int64_t bm, int u,
 
 // ------------------------------------------------------------------ MFMA path
 // Grid: (ceil(M / (64 * RB)), N / (64 * NP), B); 4 waves; wave w walks row blocks
-// (blockIdx.x * RB + i) * 64 + w * 16, i < RB, of unit blockIdx.y.  OSRC: outliers absent (0),
-// dense (1) or COO pieces (2: looked up per lane, for sparse outliers; 3: gathered per wave into
-// an LDS tile, for denser ones), decode only.
+// (blockIdx.x * RB + i) * 64 + w * 16, i < RB, of unit blockIdx.y.  OSRC, decode: outliers
+// absent (0), dense (1) or COO pieces (2: looked up per lane, for sparse outliers; 3: gathered
+// per wave into an LDS tile, for denser ones); encode: 1 also writes each 64-column piece's
+// outlier count (a.pcnt), the compaction's first pass.
 template <int MODE, int BITS, int K, int RB, int OSRC>
 __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
   constexpr int NP = (MODE == kAdd || MODE == kHist) ? 1 : 8 / BITS, G = 64, E = 16, RT = K / 16;
@@ -249,10 +255,30 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
         unpack8(ld16(xp + 8), xv + 8);
         if constexpr (MODE == kEncode) {
           float ov[E];
+          uint32_t n = 0;
 #pragma unroll
-          for (int e = 0; e < E; ++e) byte[e] |= legacy_code<BITS>(xv[e], lr[e], sc[e], a.tau, ov[e]) << (BITS * p);
+          for (int e = 0; e < E; ++e) {
+            bool hit;
+            byte[e] |= legacy_code<BITS>(xv[e], lr[e], sc[e], a.tau, ov[e], hit) << (BITS * p);
+            n += hit ? 1u : 0u;
+          }
           st16(a.oout + erow + c0, pack8(ov));
           st16(a.oout + erow + c0 + 8, pack8(ov + 8));
+          if constexpr (OSRC == 1) {
+            // the piece's entries (counted above as the codes were formed) over the row's four
+            // lanes (two lane swaps); lane g = 0 of each row stores the count through a
+            // range-checked store (the other lanes' offsets fall outside the range: no branch)
+            float nf = __uint_as_float(n), t0 = nf, t1 = nf;
+            swap32(t0, t1);
+            nf = __uint_as_float(__float_as_uint(t0) + __float_as_uint(t1));
+            t0 = t1 = nf;
+            swap16(t0, t1);
+            n = __float_as_uint(t0) + __float_as_uint(t1);
+            int64_t* prow = a.pcnt + ((int64_t)b * M + row0) * a.npc;  // the block's first row
+            st8_pred(prow, (uint32_t)(16 * a.npc * 8),
+                     (uint32_t)(((rr - row0) * a.npc + unit_base(p, u, N, NP, G) / 64) * 8), u32x2{n, 0u},
+                     g == 0 && row < M);
+          }
         } else {
           float ov[E];
 #pragma unroll
@@ -330,7 +356,8 @@ __global__ __launch_bounds__(256) void k_legacy_scalar(LegacyArgs a, int K, int6
       const float xv = __uint_as_float((uint32_t)a.x[b * a.ldx_b + m * a.ldx_m + col] << 16);
       const float sc = __uint_as_float((uint32_t)srow[col] << 16);
       float o;
-      qout |= legacy_code<BITS>(xv, lr, sc, a.tau, o) << (BITS * p);
+      bool hit;
+      qout |= legacy_code<BITS>(xv, lr, sc, a.tau, o, hit) << (BITS * p);
       a.oout[erow + col] = (uint16_t)pack_bf16x2(o, 0.f);
     } else if constexpr (MODE == kAdd) {
       const float xv = __uint_as_float((uint32_t)a.x[b * a.ldx_b + m * a.ldx_m + col] << 16);
@@ -486,6 +513,42 @@ extern "C" int lrq_legacy_encode(const void* l, const void* rt, int32_t K, const
   a.tau = bf16_value_host(bf16_bits_host(outlier));
   const bool mfma_ok = vec_ok({l, rt, x, s, o, q}) && ldx_b % 8 == 0 && ldx_m % 8 == 0 && N % 8 == 0;
   return legacy_bits<kEncode, 0>(a, K, B, bits, mfma_ok, (hipStream_t)stream);
+}
+
+// lrq_legacy_encode whose outlier compaction starts from the piece counts the encode writes (the
+// MFMA path), so the dense outliers are read once (by the scatter); other shapes take the encode
+// and the full compaction.
+extern "C" int lrq_legacy_encode_coo(const void* l, const void* rt, int32_t K, const void* x, int64_t B, int64_t M,
+                                     int64_t N, int64_t ldx_b, int64_t ldx_m, const void* s, int64_t s_rows,
+                                     int32_t bits, float outlier, void* o, void* q, int64_t* indices, int64_t ld_idx,
+                                     void* values, int64_t cap, int64_t* nnz, int64_t* piece_ptr, void* workspace,
+                                     int64_t workspace_bytes, void* stream) {
+  int st = legacy_check(l, rt, K, B, M, N, bits, s, s_rows, true);
+  if (st) return st;
+  if (x == nullptr || o == nullptr || q == nullptr) return LRQ_ERR_NULL;
+  if (ldx_m < N || (M > 1 && B > 1 && ldx_b < ldx_m * (M - 1) + N)) return LRQ_ERR_SHAPE;
+  if (!aligned(x, 2) || !aligned(o, 2)) return LRQ_ERR_ALIGN;
+  st = coo_compact_check(o, B, M, N, indices, ld_idx, values, cap, nnz, piece_ptr, workspace, workspace_bytes);
+  if (st) return st;
+  const int NP = 8 / bits;
+  const bool mfma_ok = vec_ok({l, rt, x, s, o, q}) && ldx_b % 8 == 0 && ldx_m % 8 == 0 && N % 8 == 0;
+  const int64_t NB = N / NP;
+  const float tau = bf16_value_host(bf16_bits_host(outlier));
+  // (with tau >= 0 an element's |xr| > tau is exactly "an entry"; a negative threshold keeps every
+  // element but the +-0 ones, counted by the compaction's own pass)
+  const bool counted = mfma_ok && NB % 64 == 0 && NB / 64 <= 65535 && B <= 65535 && aligned(o, 16) && tau >= 0.f;
+  if (!counted || B == 0 || M == 0) {
+    LRQ_TRY(lrq_legacy_encode(l, rt, K, x, B, M, N, ldx_b, ldx_m, s, s_rows, bits, outlier, o, q, stream));
+    return lrq_coo_compact(o, B, M, N, indices, ld_idx, values, cap, nnz, piece_ptr, workspace, workspace_bytes,
+                           stream);
+  }
+  LegacyArgs a{};
+  a.l = (const uint16_t*)l, a.rt = (const uint16_t*)rt, a.x = (const uint16_t*)x, a.ldx_b = ldx_b, a.ldx_m = ldx_m;
+  a.s = (const uint16_t*)s, a.s_rows = s_rows, a.oout = (uint16_t*)o, a.qout = (uint8_t*)q, a.M = M, a.N = N;
+  a.tau = tau;
+  a.npc = (N + 63) / 64, a.pcnt = piece_ptr;
+  LRQ_TRY((legacy_bits<kEncode, 1>(a, K, B, bits, true, (hipStream_t)stream)));
+  return coo_compact_counted(o, B, M, N, indices, ld_idx, values, cap, nnz, piece_ptr, workspace, (hipStream_t)stream);
 }
 
 extern "C" int lrq_legacy_decode(const void* l, const void* rt, int32_t K, const void* q, const void* o,

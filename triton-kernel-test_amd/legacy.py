@@ -141,6 +141,17 @@ def _bmn(shape) -> tuple:
     raise ValueError("outlier tensors have 1 to 3 dimensions")
 
 
+def _coo_buffers(B: int, M: int, N: int, cap: int, dev):
+    npc = (N + 63) // 64
+    wsb = _lib.call_raw("lrq_coo_workspace", B, M, N)
+    _lib.check(min(wsb, 0), "lrq_coo_workspace")
+    return dict(idx=torch.empty((3, cap), dtype=torch.int64, device=dev),
+                vals=torch.empty((cap,), dtype=torch.bfloat16, device=dev),
+                nnz=torch.empty((1,), dtype=torch.int64, device=dev),
+                ptr=torch.empty((B * M * npc + 1,), dtype=torch.int64, device=dev),
+                ws=torch.empty((max(wsb, 8) + 7) // 8, dtype=torch.int64, device=dev))
+
+
 def compact_outliers(o: torch.Tensor, capacity: Optional[int] = None) -> LegacyOutliers:
     """Dense bf16 outliers -> LegacyOutliers on the GPU (lrq_coo_compact), no synchronisation.
     capacity defaults to max(1024, numel / 32)."""
@@ -149,18 +160,11 @@ def compact_outliers(o: torch.Tensor, capacity: Optional[int] = None) -> LegacyO
     B, M, N = _bmn(tuple(o.shape))
     cap = max(1024, o.numel() // 32) if capacity is None else int(capacity)
     dev = o.device
-    npc = (N + 63) // 64
-    idx = torch.empty((3, cap), dtype=torch.int64, device=dev)
-    vals = torch.empty((cap,), dtype=torch.bfloat16, device=dev)
-    nnz = torch.empty((1,), dtype=torch.int64, device=dev)
-    ptr = torch.empty((B * M * npc + 1,), dtype=torch.int64, device=dev)
-    wsb = _lib.call_raw("lrq_coo_workspace", B, M, N)
-    _lib.check(min(wsb, 0), "lrq_coo_workspace")
-    ws = torch.empty((max(wsb, 8) + 7) // 8, dtype=torch.int64, device=dev)
+    bf = _coo_buffers(B, M, N, cap, dev)
     with torch.cuda.device(dev):
-        call("lrq_coo_compact", _p(o), B, M, N, _p(idx), cap, _p(vals), cap, _p(nnz), _p(ptr), _p(ws),
-             ws.numel() * 8, _stream(dev))
-    return LegacyOutliers(idx, vals, nnz, ptr, tuple(o.shape))
+        call("lrq_coo_compact", _p(o), B, M, N, _p(bf["idx"]), cap, _p(bf["vals"]), cap, _p(bf["nnz"]),
+             _p(bf["ptr"]), _p(bf["ws"]), bf["ws"].numel() * 8, _stream(dev))
+    return LegacyOutliers(bf["idx"], bf["vals"], bf["nnz"], bf["ptr"], tuple(o.shape))
 
 
 def _to_sparse(o: torch.Tensor) -> torch.Tensor:
@@ -197,6 +201,30 @@ def _coo_pieces(o, B: int, M: int, N: int):
     return ptr, n.contiguous(), o.values().to(torch.bfloat16).contiguous(), int(n.numel())
 
 
+def _encode_coo(l, r, x, s, bits: int, outlier: float, capacity: Optional[int]):
+    """lrq_legacy_encode_coo: (LegacyOutliers, q, the dense outliers it compacted)."""
+    _require_device(x)
+    M, _ = l.shape
+    _, N = r.shape
+    B = x.shape[0]
+    if tuple(x.shape) != (B, M, N):
+        raise ValueError(f"x must be [B, {M}, {N}]")
+    if x.stride(2) != 1:
+        x = x.contiguous()
+    with torch.cuda.device(x.device):
+        l2, rt, K = _factors(l, r)
+        s2 = _scale(s, B, N)
+        o = torch.empty((B, M, N), device=x.device, dtype=torch.bfloat16)
+        q = torch.empty((B, M, N // (8 // bits)), device=x.device, dtype=torch.uint8)
+        cap = max(1024, o.numel() // 32) if capacity is None else int(capacity)
+        bf = _coo_buffers(B, M, N, cap, x.device)
+        # the encode counts each piece's outliers as it writes them (the compaction's first pass)
+        call("lrq_legacy_encode_coo", _p(l2), _p(rt), K, _p(x), B, M, N, x.stride(0), x.stride(1), _p(s2),
+             s2.shape[0], bits, float(outlier), _p(o), _p(q), _p(bf["idx"]), cap, _p(bf["vals"]), cap,
+             _p(bf["nnz"]), _p(bf["ptr"]), _p(bf["ws"]), bf["ws"].numel() * 8, _stream(x.device))
+    return LegacyOutliers(bf["idx"], bf["vals"], bf["nnz"], bf["ptr"], tuple(o.shape)), q, o
+
+
 def low_rank_addition_fuse_compression_quantization(l, r, x, s, quantize_bit=8, outlier=5.):
     """Encode x[B, M, N] - l@r: threshold outliers (returned sparse COO, like the reference) and
     symmetric per-column quantisation with row-planar packing.  Returns (o, q)."""
@@ -204,47 +232,20 @@ def low_rank_addition_fuse_compression_quantization(l, r, x, s, quantize_bit=8, 
     assert l.is_contiguous(), "Matrix A must be contiguous"
     assert r.is_contiguous(), "Matrix B must be contiguous"
     bits = _bits(quantize_bit)
-    _require_device(x)
-    M, _ = l.shape
-    _, N = r.shape
-    B = x.shape[0]
-    if tuple(x.shape) != (B, M, N):
-        raise ValueError(f"x must be [B, {M}, {N}]")
-    if x.stride(2) != 1:
-        x = x.contiguous()
-    with torch.cuda.device(x.device):
-        l2, rt, K = _factors(l, r)
-        s2 = _scale(s, B, N)
-        o = torch.empty((B, M, N), device=x.device, dtype=torch.bfloat16)
-        q = torch.empty((B, M, N // (8 // bits)), device=x.device, dtype=torch.uint8)
-        call("lrq_legacy_encode", _p(l2), _p(rt), K, _p(x), B, M, N, x.stride(0), x.stride(1), _p(s2),
-             s2.shape[0], bits, float(outlier), _p(o), _p(q), _stream(x.device))
-        o = _to_sparse(o)
-    return o, q
+    oc, q, o = _encode_coo(l, r, x, s, bits, outlier, None)
+    n = int(oc.nnz.item())  # the host synchronisation to_sparse has too
+    if n > oc.capacity:
+        oc = compact_outliers(o, capacity=n)
+    return oc.to_sparse(), q
 
 
 def legacy_encode_coo(l, r, x, s, quantize_bit=8, outlier=5., capacity: Optional[int] = None):
     """low_rank_addition_fuse_compression_quantization with the outliers kept as LegacyOutliers
-    (compacted on the GPU, entry count left on the device): no host synchronisation.  A decode
-    of it reads at most `capacity` entries; ``LegacyOutliers.check()`` tells whether any were
-    dropped."""
-    bits = _bits(quantize_bit)
-    _require_device(x)
-    M, _ = l.shape
-    _, N = r.shape
-    B = x.shape[0]
-    if tuple(x.shape) != (B, M, N):
-        raise ValueError(f"x must be [B, {M}, {N}]")
-    if x.stride(2) != 1:
-        x = x.contiguous()
-    with torch.cuda.device(x.device):
-        l2, rt, K = _factors(l, r)
-        s2 = _scale(s, B, N)
-        o = torch.empty((B, M, N), device=x.device, dtype=torch.bfloat16)
-        q = torch.empty((B, M, N // (8 // bits)), device=x.device, dtype=torch.uint8)
-        call("lrq_legacy_encode", _p(l2), _p(rt), K, _p(x), B, M, N, x.stride(0), x.stride(1), _p(s2),
-             s2.shape[0], bits, float(outlier), _p(o), _p(q), _stream(x.device))
-        return compact_outliers(o, capacity), q
+    (compacted on the GPU, the encode doing the compaction's count pass, entry count left on the
+    device): no host synchronisation.  A decode of it reads at most `capacity` entries;
+    ``LegacyOutliers.check()`` tells whether any were dropped."""
+    oc, q, _ = _encode_coo(l, r, x, s, _bits(quantize_bit), outlier, capacity)
+    return oc, q
 
 
 def low_rank_addition_fuse_decompression_dequantization(l, r, q, o, s, quantize_bit=8, outlier=5.):
