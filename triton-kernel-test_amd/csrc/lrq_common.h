@@ -31,6 +31,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace lrq {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -102,6 +104,24 @@ __device__ __forceinline__ u32x4 ld16_stream(const void* p) {
 __device__ __forceinline__ u32x2 ld8_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
 }
+// s_waitcnt immediate for vmcnt(n), n < 64 (gfx9: low bits [3:0], high bits [15:14]); expcnt
+// and lgkmcnt are not waited for.
+constexpr int vmcnt_imm(int n) { return 0x0f70 | (n & 15) | ((n >> 4) << 14); }
+
+// f(std::integral_constant<int, i>) for i = I .. N-1, unrolled at compile time (each call sees
+// its index as a constant expression, e.g. for a counted wait).
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+// Make a register value opaque to the compiler: it can no longer be recomputed or reloaded
+// from memory at a later use, so operands loaded once for a whole loop stay in registers.
+__device__ __forceinline__ void pin(u32x2& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(u32x4& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ __forceinline__ void st8(void* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }
 __device__ __forceinline__ void st4(void* p, uint32_t v) { *reinterpret_cast<uint32_t*>(p) = v; }

@@ -573,10 +573,6 @@ struct TilesEnc {
   static_assert(NT % 2 == 0 && LDS <= 160 * 1024, "tiles of both planes; LDS budget");
 };
 
-// s_waitcnt immediate for vmcnt(n), n < 64 (gfx9: low bits [3:0], high bits [15:14]); expcnt
-// and lgkmcnt are not waited for.
-constexpr int vmcnt_imm(int n) { return 0x0f70 | (n & 15) | ((n >> 4) << 14); }
-
 template <int UPW, bool ROT>
 __global__ __launch_bounds__(512) void k_encode_tiles(const uint16_t* __restrict__ X, int64_t ldx, int M, int N,
                                                       const uint16_t* __restrict__ V, uint16_t* __restrict__ Lout,

@@ -907,17 +907,6 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_w(
 
   u32x2 vop[NU][NP][G / 16][RT];
   u32x4 vt[NU][NP][G / 32][1];
-#pragma unroll
-  for (int uu = 0; uu < NU; ++uu)
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      const int base = unit_base(p, ub + uu, N, NP, G);
-      if constexpr (R > 0) load_vops<G, R>(V, base, j, g, vop[uu][p]);
-      u32x2 va[G / 16][1];
-      load_vops<G, 16>(A, base, j, g, va);
-      if constexpr (OUTL) mask_rows<G, 1>(va, gmask, base, j);
-      transpose_vops<G, 16>(va, ident, vt[uu][p]);
-    }
 
   struct BIn {
     u32x4 cb[NU][G / 64];
@@ -957,16 +946,74 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_w(
       }
   };
 
+  // The first SL blocks' loads go out before the operand set-up, so their latency overlaps it.
+  // Where the resident operands and the slots fit the register budget together, the operand
+  // loads all go out before the first transpose (one round trip) and the resident operands are
+  // pinned: otherwise the compiler may reload them per block, and the wait for such a reload
+  // would also drain every block load issued before it.  Else each unit-plane is loaded and
+  // transposed in turn, and the compiler's reloads are the cheaper choice.
+  constexpr int kResident = NU * NP * ((R > 0 ? G / 16 * RT * 2 : 0) + G / 32 * 4);
+  constexpr int kSlots = SL * (NU * (G / 64) * 4 + NU * NP + 2 * RT);
+  constexpr bool kPin = kResident + kSlots <= 190;
   f32x4 acc[RBW];
   BIn ring[SL];
 #pragma unroll
-  for (int b = 0; b < RBW; ++b) acc[b] = zero4();
-#pragma unroll
   for (int sl = 0; sl < SL && sl < RBW; ++sl) load_blk(rb0 + sl, ring[sl]);
+  if constexpr (kPin) __builtin_amdgcn_sched_barrier(0);
+  if constexpr (kPin) {
+    {
+      u32x2 va[NU][NP][G / 16][1];
+#pragma unroll
+      for (int uu = 0; uu < NU; ++uu)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          const int base = unit_base(p, ub + uu, N, NP, G);
+          if constexpr (R > 0) load_vops<G, R>(V, base, j, g, vop[uu][p]);
+          load_vops<G, 16>(A, base, j, g, va[uu][p]);
+        }
+#pragma unroll
+      for (int uu = 0; uu < NU; ++uu)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          if constexpr (OUTL) mask_rows<G, 1>(va[uu][p], gmask, unit_base(p, ub + uu, N, NP, G), j);
+          transpose_vops<G, 16>(va[uu][p], ident, vt[uu][p]);
+        }
+    }
+#pragma unroll
+    for (int uu = 0; uu < NU; ++uu)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+#pragma unroll
+        for (int k = 0; k < G / 32; ++k) pin(vt[uu][p][k][0]);
+        if constexpr (R > 0) {
+#pragma unroll
+          for (int q = 0; q < G / 16; ++q)
+#pragma unroll
+            for (int t = 0; t < RT; ++t) pin(vop[uu][p][q][t]);
+        }
+      }
+  } else {
+#pragma unroll
+    for (int uu = 0; uu < NU; ++uu)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const int base = unit_base(p, ub + uu, N, NP, G);
+        if constexpr (R > 0) load_vops<G, R>(V, base, j, g, vop[uu][p]);
+        u32x2 va[G / 16][1];
+        load_vops<G, 16>(A, base, j, g, va);
+        if constexpr (OUTL) mask_rows<G, 1>(va, gmask, base, j);
+        transpose_vops<G, 16>(va, ident, vt[uu][p]);
+      }
+  }
+#pragma unroll
+  for (int b = 0; b < RBW; ++b) acc[b] = zero4();
+  if constexpr (kPin) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int b = 0; b < RBW; ++b) {
     compute_blk(ring[b % SL], acc[b]);
+    if constexpr (kPin) __builtin_amdgcn_sched_barrier(0);
     if (b + SL < RBW) load_blk(rb0 + b + SL, ring[b % SL]);
+    if constexpr (kPin) __builtin_amdgcn_sched_barrier(0);
   }
   if constexpr (OUTL) {
     if (w == 0) add_side_term<1, RBW>(A, 16, N, oidx, nout, side, ldside, rb0, nrb, M, j, g, acc);
@@ -1005,21 +1052,30 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_w(
 // blocks) in one XCD-aware dimension; wave w of a workgroup takes the group's blocks w, w + NW,
 // ... over all UPW units, through a ring of PD register slots (loads of later blocks in flight
 // while one is computed).
-// Every MFMA operand keeps K along a lane's registers, and the reduction here runs over rows,
-// which the reconstruction holds one per lane (lane (j, g): row j, E columns).  So each 16 x 16
-// piece of x_hat is transposed by an identity MFMA (exact) into lane (column, 4 rows) -- the B
-// operand of the product -- and gm's rows by the same transpose into the A operand g^T.  The
-// product's accumulator holds, in lane (j, g), 4 consecutive k of one column n.  The NW waves'
+// Every MFMA operand keeps K along a lane's registers, and the reduction here runs over rows.
+// So the reconstruction is made directly in that layout: with L as the A operand and V as the
+// B operand, the low-rank MFMA's output holds, in lane (j, g), rows 4g .. 4g+3 of one column
+// (the C operand, code * scale + zero, is built in the same layout from four rows' codes and
+// qparams).  Packed to bf16 it is the B operand of the product with gm^T (gm's rows transposed
+// once per block by an identity MFMA), whose accumulator holds, in lane (j, g), 4 consecutive k
+// of that column.  The columns of the workgroup's span (UPW G per plane) are dealt to lanes in
+// byte order: lane j reads the BPL = UPW G / 16 consecutive code bytes BPL j .. of each of its
+// rows, and byte t of them is its column in tile t (TT = BPL tiles per plane).  The NW waves'
 // accumulators are summed through LDS in wave order (deterministic) and leave as 16-byte rows.
-template <int BITS, int G, int R, int KT, int NW, int UPW, int PD>
+template <int BITS, int G, int R, int KT, int NW, int UPW, int PD, int NBM>
 __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t(
     const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
     const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
     const uint16_t* __restrict__ gm, int64_t ldg, float* __restrict__ part, int bpg, int ncg, bool xcd_map) {
-  constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, E = G / 4, Q = G / 16;
-  constexpr int NACC = UPW * NP * Q * KT;  // f32x4 accumulators per lane
-  constexpr int CH = NACC < 8 ? NACC : 8;  // accumulators per LDS round
+  constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1;
+  constexpr int SPAN = UPW * G;             // columns of one plane in the workgroup's span
+  constexpr int BPL = SPAN / 16, TT = BPL;  // code bytes per lane and row; tiles per plane
+  constexpr int DW = BPL / 4;               // code dwords per lane and row
+  constexpr int NACC = NP * TT * KT;        // f32x4 accumulators per lane
+  constexpr int CH = NACC < 8 ? NACC : 8;   // accumulators per LDS round
   static_assert(NACC % CH == 0, "reduction rounds");
+  static_assert(BPL % 4 == 0 && BPL <= 16 && G % BPL == 0, "a lane's bytes are whole dwords of one unit");
+  static_assert(NP <= 2, "4- or 8-bit codes");
   __shared__ f32x4 red[NW][CH][64];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
@@ -1029,53 +1085,92 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t(
   // ids of one XCD (id % 8) take whole row groups, so each line is fetched into one XCD's L2
   // only (without it, 8 L2s fetch it: 2.2x the algorithmic HBM bytes at the north-star shape)
   const int id = blockIdx.x;
-  const int cgi = xcd_map ? (id >> 3) % ncg : id % ncg;
-  const int rgi = xcd_map ? (id & 7) + 8 * ((id >> 3) / ncg) : id / ncg;
+  // (the divisions run on the vector unit: readfirstlane brings the uniform results back to
+  // scalar registers, so that all block addressing below stays scalar)
+  const int cgi = __builtin_amdgcn_readfirstlane(xcd_map ? (id >> 3) % ncg : id % ncg);
+  const int rgi = __builtin_amdgcn_readfirstlane(xcd_map ? (id & 7) + 8 * ((id >> 3) / ncg) : id / ncg);
   const int u0 = cgi * UPW;
+  const int ul = u0 + (BPL * j) / G;        // the unit of lane j's columns
   const int rb_lo = rgi * bpg, rb_hi = min(rb_lo + bpg, nrb);
   const int KO = 16 * KT;  // gm columns and part row length
   const u32x2 ident = identity_bop(j, g);
 
-  u32x2 vop[UPW][NP][Q][RT];
+  // B operands of the low-rank term: lane (j, g) holds V[column of tile t][ranks 4g ..] (and
+  // 16 + 4g .. at rank 32, the K order of residual_unit)
+  u32x2 vop[NP][TT][RT];
   if constexpr (R > 0) {
 #pragma unroll
-    for (int ui = 0; ui < UPW; ++ui)
+    for (int p = 0; p < NP; ++p)
 #pragma unroll
-      for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, u0 + ui, N, NP, G), j, g, vop[ui][p]);
+      for (int t = 0; t < TT; ++t)
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+          vop[p][t][r] = ld8(V + (int64_t)(p * (N / NP) + u0 * G + BPL * j + t) * R + 16 * r + 4 * g);
   }
   f32x4 acc[NACC];
 #pragma unroll
   for (int a = 0; a < NACC; ++a) acc[a] = zero4();
 
   struct Blk {
-    u32x4 cb[UPW][G / 64];
-    uint32_t qp[UPW][NP];
-    u32x2 lop[RT];
-    u32x2 gop[KT];
+    uint32_t cw[4][DW];  // rows 4g + v: code dwords (bytes BPL j .. of the span)
+    uint32_t qp[4][NP];  // rows 4g + v: (scale, zero) of each plane of the lane's unit
+    u32x2 lop[RT];       // row j: L ranks 4g .. (A operand)
+    u32x2 gop[KT];       // row j: gm columns 16t + 4g ..
   };
+  // A block's loads: 32-bit lane offsets from the block's wave-uniform bases.  Row clamping
+  // (rows past M repeat the last row) is a min on the offsets, min(r, lim) * ld = min(r * ld,
+  // lim * ld), with the lane's r * ld computed once (row strides below 2^24 bytes, checked by the
+  // launch, keep every offset in 32 bits).
+  const uint32_t ldc1 = (uint32_t)ldc, ldq2 = (uint32_t)ldq * 2, ldl2 = (uint32_t)ldl * 2, ldg2 = (uint32_t)ldg * 2;
+  uint32_t coff[4], qoff[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    coff[v] = (uint32_t)(4 * g + v) * ldc1;
+    qoff[v] = (uint32_t)(4 * g + v) * ldq2;
+  }
+  const uint32_t loff = (uint32_t)j * ldl2, goff = (uint32_t)j * ldg2;
+  const uint32_t cl = (uint32_t)(BPL * j), ql = (uint32_t)(ul * NP * 4), rl = (uint32_t)(8 * g);
   auto load = [&](int rb, Blk& d) {
-    const int64_t row = min(rb * 16 + j, M - 1);
+    const int r0 = rb * 16;                  // wave-uniform
+    const uint32_t lim = (uint32_t)(M - 1 - r0);
+    const uint8_t* cbase = codes + (int64_t)r0 * ldc + u0 * G;
+    const uint8_t* qbase = reinterpret_cast<const uint8_t*>(qparams + (int64_t)r0 * ldq);
 #pragma unroll
-    for (int ui = 0; ui < UPW; ++ui) {
+    for (int v = 0; v < 4; ++v) {
+      const uint8_t* cp = cbase + (min(coff[v], lim * ldc1) + cl);
+      if constexpr (DW == 4) {
+        const u32x4 c = ld16_stream(cp);
 #pragma unroll
-      for (int i = 0; i < G / 64; ++i) d.cb[ui][i] = ld16_stream(codes + row * ldc + (u0 + ui) * G + E * g + 16 * i);
-      if constexpr (NP == 2) {
-        const u32x2 q = ld8(qparams + row * ldq + (u0 + ui) * 4);
-        d.qp[ui][0] = q[0];
-        d.qp[ui][1] = q[1];
+        for (int e = 0; e < 4; ++e) d.cw[v][e] = c[e];
+      } else if constexpr (DW == 2) {
+        const u32x2 c = ld8_stream(cp);
+        d.cw[v][0] = c[0];
+        d.cw[v][1] = c[1];
       } else {
-        d.qp[ui][0] = ld4(qparams + row * ldq + (u0 + ui) * 2);
+        d.cw[v][0] = ld4(cp);
+      }
+      const uint8_t* qq = qbase + (min(qoff[v], lim * ldq2) + ql);
+      if constexpr (NP == 2) {
+        const u32x2 q = ld8(qq);
+        d.qp[v][0] = q[0];
+        d.qp[v][1] = q[1];
+      } else {
+        d.qp[v][0] = ld4(qq);
       }
     }
     if constexpr (R > 0) {
+      const uint8_t* lbase = reinterpret_cast<const uint8_t*>(Lin + (int64_t)r0 * ldl);
+      const uint32_t lo = min(loff, lim * ldl2) + rl;
 #pragma unroll
-      for (int t = 0; t < RT; ++t) d.lop[t] = ld8(Lin + row * ldl + 16 * t + 4 * g);
+      for (int t = 0; t < RT; ++t) d.lop[t] = ld8(lbase + (lo + 32 * t));
     }
+    const uint8_t* gbase = reinterpret_cast<const uint8_t*>(gm + (int64_t)r0 * ldg);
+    const uint32_t go = min(goff, lim * ldg2) + rl;
 #pragma unroll
-    for (int t = 0; t < KT; ++t) d.gop[t] = ld8(gm + row * ldg + 16 * t + 4 * g);
+    for (int t = 0; t < KT; ++t) d.gop[t] = ld8(gbase + (go + 32 * t));
   };
 
-  // one block's contribution; blocks past the wave's last (the ring's tail) add nothing
+  // one block's contribution (none for a block past the wave's last: blive false)
   auto process = [&](const Blk& cur, int rb, bool blive) {
     // g^T operands: rows past M contribute nothing (their clamped x_hat is finite)
     const bool live = blive && rb * 16 + j < M;
@@ -1087,48 +1182,77 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t(
       a2[t] = u32x2{pack_bf16x2_exact(d[0], d[1]), pack_bf16x2_exact(d[2], d[3])};
     }
 #pragma unroll
-    for (int ui = 0; ui < UPW; ++ui)
+    for (int p = 0; p < NP; ++p) {
+      float sf[4], zf[4];
 #pragma unroll
-      for (int p = 0; p < NP; ++p) {
-        float xh[E];
-        reconstruct_plane<BITS, G, R>(cur.cb[ui], cur.qp[ui][p], p, vop[ui][p], cur.lop, xh);
+      for (int v = 0; v < 4; ++v) {
+        sf[v] = f16_val(cur.qp[v][p] & 0xffffu);
+        zf[v] = f16_val(cur.qp[v][p] >> 16);
+      }
 #pragma unroll
-        for (int q = 0; q < Q; ++q) {
-          // lane (j, g) holds x_hat[j][E g + 4q + e]; after the identity MFMA, lane (j, g)
-          // holds x_hat[4g + v][E (j >> 2) + 4q + (j & 3)]
-          const u32x2 xa = u32x2{pack_bf16x2(xh[4 * q], xh[4 * q + 1]), pack_bf16x2(xh[4 * q + 2], xh[4 * q + 3])};
-          const f32x4 d = mfma_16x16x16(xa, ident, zero4());
-          const u32x2 xb = u32x2{pack_bf16x2_exact(d[0], d[1]), pack_bf16x2_exact(d[2], d[3])};
+      for (int dw = 0; dw < DW; ++dw) {
+        uint32_t wq[4];  // row 4g + v: plane p's codes of tiles 4 dw .. 4 dw + 3, one per byte
 #pragma unroll
-          for (int t = 0; t < KT; ++t) {
-            f32x4& c = acc[((ui * NP + p) * Q + q) * KT + t];
-            c = mfma_16x16x16(a2[t], xb, c);
+        for (int v = 0; v < 4; ++v) {
+          const uint32_t wd = cur.cw[v][dw];
+          wq[v] = NP == 1 ? wd : ((wd >> (BITS * p)) & (0x01010101u * ((1u << BITS) - 1u)));
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int t = 4 * dw + e;
+          f32x4 x;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float q = e == 0 ? ubyte_f32<0>(wq[v]) : e == 1 ? ubyte_f32<1>(wq[v]) : e == 2 ? ubyte_f32<2>(wq[v])
+                                                                                             : ubyte_f32<3>(wq[v]);
+            x[v] = __builtin_fmaf(q, sf[v], zf[v]);
+          }
+          // + (L V^T)[4g + v][column], rounded once with the C operand above
+          if constexpr (R == 16) {
+            x = mfma_16x16x16(cur.lop[0], vop[p][t][0], x);
+          } else if constexpr (R == 32) {
+            x = mfma_16x16x32(u32x4{cur.lop[0][0], cur.lop[0][1], cur.lop[1][0], cur.lop[1][1]},
+                              u32x4{vop[p][t][0][0], vop[p][t][0][1], vop[p][t][1][0], vop[p][t][1][1]}, x);
+          }
+          const u32x2 xb = u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};  // x_hat rows 4g + v
+#pragma unroll
+          for (int kt = 0; kt < KT; ++kt) {
+            f32x4& c = acc[(p * TT + t) * KT + kt];
+            c = mfma_16x16x16(a2[kt], xb, c);
           }
         }
       }
+    }
   };
 
-  // the wave's blocks rb_lo + w + i NW, i < nb, through a ring of PD register slots: slot s
-  // holds block i0 + s and is refilled with block i0 + s + PD right after it is used (clamped
-  // loads; every load is issued by every lane)
+  // The wave's blocks rb_lo + w + i NW, i < nb, in chunks of NBM blocks.  A chunk is straight-
+  // line code without branches: its first PD blocks' loads go out together, and each block's
+  // slot is refilled with the block PD later right after it is used, so every wait counts
+  // exactly the loads issued after the slot's own.  (A loop over the ring makes the compiler
+  // merge the slot states of the loop entry and back edge, and a branch around a block lets it
+  // sink that block's loads to their use; either way a block would wait for nearly every load
+  // in flight.)  Loads are clamped to the group's last block; blocks past the wave's last are
+  // computed with a zero gm operand and add nothing.  The launch picks NBM to cover the waves'
+  // block counts where it can.
   const int nb = rb_lo + w < rb_hi ? (rb_hi - rb_lo - w + NW - 1) / NW : 0;
-  if (nb > 0) {  // wave-uniform
-    const int last = rb_hi - 1;
+  const int last = rb_hi - 1;
+  for (int c0 = 0; c0 < nb; c0 += NBM) {  // wave-uniform
     Blk ring[PD];
 #pragma unroll
-    for (int sl = 0; sl < PD; ++sl) load(min(rb_lo + w + sl * NW, last), ring[sl]);
-    for (int i0 = 0; i0 < nb; i0 += PD) {
-#pragma unroll
-      for (int sl = 0; sl < PD; ++sl) {
-        const int rb = rb_lo + w + (i0 + sl) * NW;
-        process(ring[sl], rb, i0 + sl < nb);
-        load(min(rb + PD * NW, last), ring[sl]);
-      }
-    }
+    for (int sl = 0; sl < PD; ++sl) load(min(rb_lo + w + (c0 + sl) * NW, last), ring[sl]);
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, NBM>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      const int rb = rb_lo + w + (c0 + i) * NW;
+      process(ring[i % PD], rb, c0 + i < nb);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (i + PD < NBM) load(min(rb + PD * NW, last), ring[i % PD]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
   }
 
-  // acc[((ui NP + p) Q + q) KT + t] in lane (j, g), component v: column
-  // n = p N/NP + (u0 + ui) G + E (j >> 2) + 4q + (j & 3), k = 16t + 4g + v
+  // acc[(p TT + t) KT + kt] in lane (j, g), component v: column
+  // n = p N/NP + u0 G + BPL j + t, k = 16 kt + 4g + v
   float* partg = part + (int64_t)rgi * N * KO;
 #pragma unroll
   for (int c0 = 0; c0 < NACC; c0 += CH) {
@@ -1146,10 +1270,10 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t(
         s[2] += o[2];
         s[3] += o[3];
       }
-      const int a = c0 + c, t = a % KT, q = (a / KT) % Q, p = (a / (KT * Q)) % NP, ui = a / (KT * Q * NP);
+      const int a = c0 + c, kt = a % KT, t = (a / KT) % TT, p = a / (KT * TT);
       const int jj = ln & 15, gg = ln >> 4;
-      const int n = p * (N / NP) + (u0 + ui) * G + E * (jj >> 2) + 4 * q + (jj & 3);
-      st16(partg + (int64_t)n * KO + 16 * t + 4 * gg,
+      const int n = p * (N / NP) + u0 * G + BPL * jj + t;
+      st16(partg + (int64_t)n * KO + 16 * kt + 4 * gg,
            u32x4{__float_as_uint(s[0]), __float_as_uint(s[1]), __float_as_uint(s[2]), __float_as_uint(s[3])});
     }
     __syncthreads();
@@ -1321,6 +1445,13 @@ static int softmax_units(const lrq_tensors* t, const void* dp, int64_t lddp, voi
   }
 }
 
+// k_dequant_gemm_t addresses a block's rows by 32-bit offsets (row in block x row stride):
+// strides below 2^24 bytes keep them in range.
+static bool strides_fit24(const lrq_tensors* t, int64_t ldg_elems) {
+  constexpr int64_t kLim = int64_t(1) << 24;
+  return t->ld_codes < kLim && t->ld_qp * 2 < kLim && t->ld_L * 2 < kLim && ldg_elems * 2 < kLim;
+}
+
 template <int BITS, int G, int R, int NOUT, bool F32, bool OUTL>
 static int gemm_launch(const lrq_tensors* t, const void* a, void* out, int64_t ldo, hipStream_t s) {
   // row blocks per workgroup: 4, or 2 where a unit's register slot is large (two slots in flight)
@@ -1333,9 +1464,10 @@ static int gemm_launch(const lrq_tensors* t, const void* a, void* out, int64_t l
   const size_t shm = OUTL ? (size_t)(N / 32) * 4 : 0;
   if constexpr (NOUT == 16 && R <= 16) {
     // units split evenly over the waves: the wave-resident kernel (NU units per wave)
-    const int units = N / (UC);
+    const int units = N / UC;
     auto wlaunch = [&](auto nu) {
-      constexpr int NU = decltype(nu)::value, WRBW = 4, WSL = 2;
+      // one block in flight with the outlier mask (its registers would not fit beside a second)
+      constexpr int NU = decltype(nu)::value, WRBW = 4, WSL = OUTL ? 1 : 2;
       LRQ_TRY(launch((k_dequant_gemm_w<BITS, G, R, NW, NU, WRBW, WSL, F32, OUTL>), dim3((nrb + WRBW - 1) / WRBW),
                      dim3(NW * 64), shm, s, (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams,
                      t->ld_qp, (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)a, out,
@@ -1436,13 +1568,21 @@ template <int BITS, int G, int R, int KT, int UPW, bool F32>
 static int gemm_t_run(const lrq_tensors* t, const void* gmat, int64_t ldg, void* out, int64_t ldo, float* ws,
                       const GemmTPlan& pl, hipStream_t s) {
   constexpr int NW = 8;
-  constexpr int PD = G * (8 / BITS) * KT >= 512 ? 2 : 4;  // ring depth within the register budget
+  // ring depth within the register budget
+  constexpr int PD = (G * (8 / BITS) * KT >= 512 || (R == 32 && UPW == 2)) ? 2 : 4;
   const int M = (int)t->rows, N = (int)t->hidden;
-  if (pl.rg > 0)
-    LRQ_TRY(launch((k_dequant_gemm_t<BITS, G, R, KT, NW, UPW, PD>), dim3(pl.cg * pl.rg), dim3(NW * 64), 0, s,
-                       (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,
-                       (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)gmat, ldg, ws,
-                       pl.bpg, pl.cg, pl.rg % 8 == 0));
+  if (!strides_fit24(t, ldg)) return LRQ_ERR_UNSUPPORTED;
+  if (pl.rg > 0) {
+    // blocks per chunk: the waves' block count ceil(bpg / NW) where it is at most 4, else 8;
+    // just the ring's PD blocks where the accumulators alone take 128 registers
+    constexpr bool kBig = (8 / BITS) * (UPW * G / 16) * KT > 16;
+    auto kern = kBig ? k_dequant_gemm_t<BITS, G, R, KT, NW, UPW, PD, PD>
+                : (pl.bpg + NW - 1) / NW <= 4 ? k_dequant_gemm_t<BITS, G, R, KT, NW, UPW, PD, kBig ? PD : 4>
+                                              : k_dequant_gemm_t<BITS, G, R, KT, NW, UPW, PD, kBig ? PD : 8>;
+    LRQ_TRY(launch(kern, dim3(pl.cg * pl.rg), dim3(NW * 64), 0, s, (const uint8_t*)t->codes, t->ld_codes,
+                   (const uint16_t*)t->qparams, t->ld_qp, (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M,
+                   N, (const uint16_t*)gmat, ldg, ws, pl.bpg, pl.cg, pl.rg % 8 == 0));
+  }
   const int64_t nk = (int64_t)N * 16 * KT;
   LRQ_TRY(launch(k_sum_parts<F32>, dim3((unsigned)((nk / 4 + 255) / 256)), dim3(256), 0, s, ws, pl.rg, nk,
                      16 * KT, out, ldo));
