@@ -1535,13 +1535,12 @@ static int gemm_nout(const lrq_tensors* t, const void* a, int n_out, void* out, 
   }
 }
 
-// Transposed dequant-GEMM.  Units per wave: 2 when that keeps the lane's accumulators at <= 16
-// f32x4 and the row's units pair up, else 1.  Row groups: enough workgroups for about one per
-// CU on MI355X (a fixed 256, so the summation order depends only on the shapes), at least NW
-// blocks per group.  The workspace holds one fp32 [N, n_out] partial per row group.
-static constexpr int gemm_t_upw_cap(int bits, int group, int kt) {
-  return 2 * (8 / bits) * (group / 16) * kt <= 16 ? 2 : 1;
-}
+// Transposed dequant-GEMM.  One unit per workgroup (measured on MI355X at the LoRA shape,
+// 16384 x 4096 int4/g64: 17.7 us against 20.7 us with two units per workgroup; a ring of two
+// blocks in flight beat three or four, 17.7 against 18.6 / 20.7 us).  Row groups: enough
+// workgroups for about one per CU on MI355X (a fixed 256, so the summation order depends only on
+// the shapes), at least NW blocks per group.  The workspace holds one fp32 [N, n_out] partial
+// per row group.
 
 struct GemmTPlan {
   int upw, cg, rg, bpg;
@@ -1552,7 +1551,7 @@ static GemmTPlan gemm_t_plan(int64_t rows, int64_t hidden, int bits, int group, 
   constexpr int NW = 8;
   GemmTPlan pl{};
   const int64_t units = hidden / ((int64_t)group * (8 / bits));
-  pl.upw = (gemm_t_upw_cap(bits, group, n_out / 16) == 2 && units % 2 == 0) ? 2 : 1;
+  pl.upw = 1;
   pl.cg = (int)(units / pl.upw);
   const int64_t nrb = (rows + 15) / 16;
   if (nrb == 0) return pl;  // rg = 0: the sum kernel writes zeros
@@ -1564,12 +1563,11 @@ static GemmTPlan gemm_t_plan(int64_t rows, int64_t hidden, int bits, int group, 
   return pl;
 }
 
-template <int BITS, int G, int R, int KT, int UPW, bool F32>
+template <int BITS, int G, int R, int KT, bool F32>
 static int gemm_t_run(const lrq_tensors* t, const void* gmat, int64_t ldg, void* out, int64_t ldo, float* ws,
                       const GemmTPlan& pl, hipStream_t s) {
   constexpr int NW = 8;
-  // ring depth within the register budget
-  constexpr int PD = (G * (8 / BITS) * KT >= 512 || (R == 32 && UPW == 2)) ? 2 : 4;
+  constexpr int UPW = 1, PD = 2;  // units per workgroup, blocks in flight per wave
   const int M = (int)t->rows, N = (int)t->hidden;
   if (!strides_fit24(t, ldg)) return LRQ_ERR_UNSUPPORTED;
   if (pl.rg > 0) {
@@ -1589,23 +1587,14 @@ static int gemm_t_run(const lrq_tensors* t, const void* gmat, int64_t ldg, void*
   return LRQ_OK;
 }
 
-template <int BITS, int G, int R, int KT, bool F32>
-static int gemm_t_upw(const lrq_tensors* t, const void* gmat, int64_t ldg, void* out, int64_t ldo, float* ws,
-                      const GemmTPlan& pl, hipStream_t s) {
-  if constexpr (gemm_t_upw_cap(BITS, G, KT) == 2) {
-    if (pl.upw == 2) return gemm_t_run<BITS, G, R, KT, 2, F32>(t, gmat, ldg, out, ldo, ws, pl, s);
-  }
-  return gemm_t_run<BITS, G, R, KT, 1, F32>(t, gmat, ldg, out, ldo, ws, pl, s);
-}
-
 template <int BITS, int G, int R>
 static int gemm_t_nout(const lrq_tensors* t, const void* gmat, int64_t ldg, int n_out, void* out, int64_t ldo,
                        bool f32, float* ws, const GemmTPlan& pl, hipStream_t s) {
   switch (n_out * 2 + (f32 ? 1 : 0)) {
-    case 16 * 2 + 1: return gemm_t_upw<BITS, G, R, 1, true>(t, gmat, ldg, out, ldo, ws, pl, s);
-    case 16 * 2: return gemm_t_upw<BITS, G, R, 1, false>(t, gmat, ldg, out, ldo, ws, pl, s);
-    case 32 * 2 + 1: return gemm_t_upw<BITS, G, R, 2, true>(t, gmat, ldg, out, ldo, ws, pl, s);
-    case 32 * 2: return gemm_t_upw<BITS, G, R, 2, false>(t, gmat, ldg, out, ldo, ws, pl, s);
+    case 16 * 2 + 1: return gemm_t_run<BITS, G, R, 1, true>(t, gmat, ldg, out, ldo, ws, pl, s);
+    case 16 * 2: return gemm_t_run<BITS, G, R, 1, false>(t, gmat, ldg, out, ldo, ws, pl, s);
+    case 32 * 2 + 1: return gemm_t_run<BITS, G, R, 2, true>(t, gmat, ldg, out, ldo, ws, pl, s);
+    case 32 * 2: return gemm_t_run<BITS, G, R, 2, false>(t, gmat, ldg, out, ldo, ws, pl, s);
     default: return LRQ_ERR_UNSUPPORTED;
   }
 }
