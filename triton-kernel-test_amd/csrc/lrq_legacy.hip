@@ -60,6 +60,7 @@ struct LegacyArgs {
   uint8_t* qout;        // encode codes [B, M, N/NP]
   int64_t M, N;
   float tau;            // outlier threshold, already rounded to bf16
+  int rb;               // MFMA path: 64-row blocks per workgroup
 };
 
 // Encode of one element given its bf16 input x, bf16(l @ r) lr and scale sc: returns the code
@@ -176,12 +177,12 @@ __device__ __forceinline__ void coo_tile(const LegacyArgs& a, int64_t bm, int u,
 }
 
 // ------------------------------------------------------------------ MFMA path
-// Grid: (ceil(M / (64 * RB)), N / (64 * NP), B); 4 waves; wave w walks row blocks
-// (blockIdx.x * RB + i) * 64 + w * 16, i < RB, of unit blockIdx.y.  OSRC, decode: outliers
+// Grid: (ceil(M / (64 * rb)), N / (64 * NP), B); 4 waves; wave w walks row blocks
+// (blockIdx.x * rb + i) * 64 + w * 16, i < rb, of unit blockIdx.y.  OSRC, decode: outliers
 // absent (0), dense (1) or COO pieces (2: looked up per lane, for sparse outliers; 3: gathered
 // per wave into an LDS tile, for denser ones); encode: 1 also writes each 64-column piece's
 // outlier count (a.pcnt), the compaction's first pass.
-template <int MODE, int BITS, int K, int RB, int OSRC>
+template <int MODE, int BITS, int K, int OSRC>
 __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
   constexpr int NP = (MODE == kAdd || MODE == kHist) ? 1 : 8 / BITS, G = 64, E = 16, RT = K / 16;
   __shared__ uint32_t lh[MODE == kHist ? 256 : 1];
@@ -206,8 +207,8 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
   for (int p = 0; p < NP; ++p) load_vops<G, K>(a.rt, unit_base(p, u, N, NP, G), j, g, vop[p]);
   const float zero[E] = {};
 
-  for (int i = 0; i < RB; ++i) {
-    const int row0 = (blockIdx.x * RB + i) * 64 + w * 16;  // wave-uniform: a scalar exit
+  for (int i = 0; i < a.rb; ++i) {
+    const int row0 = (blockIdx.x * a.rb + i) * 64 + w * 16;  // wave-uniform: a scalar exit
     if (row0 >= M) break;  // whole 16-row block past the end
     const int row = row0 + j;
     const int64_t rr = min(row, M - 1);
@@ -444,15 +445,26 @@ __global__ __launch_bounds__(256) void k_kth_select(uint32_t* __restrict__ hist,
 }
 
 // ------------------------------------------------------------------ host side
+// 64-row blocks per workgroup of the MFMA path: 4, or 2 / 1 where 4 would give fewer than two
+// workgroups per CU (small M or few units: the reference speed tests' M = 512 gives 8).
+static int legacy_rows_per_wg(int64_t M, int64_t wg_cols) {
+  const int64_t want = 2 * (int64_t)cu_count();
+  for (int rb = 4; rb > 1; rb /= 2)
+    if ((M + 64 * rb - 1) / (64 * rb) * wg_cols >= want) return rb;
+  return 1;
+}
+
 template <int MODE, int BITS, int OSRC>
 static int legacy_launch(const LegacyArgs& a, int K, int64_t B, bool mfma_ok, hipStream_t st) {
   constexpr int NP = (MODE == kAdd) ? 1 : 8 / BITS;
   const int64_t NB = a.N / NP;
   if (mfma_ok && NB % 64 == 0 && NB / 64 <= 65535 && B <= 65535) {
-    constexpr int RB = 4;
-    dim3 grid((unsigned)((a.M + 64 * RB - 1) / (64 * RB)), (unsigned)(NB / 64), (unsigned)B);
-    if (K == 16) LRQ_TRY(launch((k_legacy_mfma<MODE, BITS, 16, RB, OSRC>), grid, dim3(256), 0, st, a));
-    else LRQ_TRY(launch((k_legacy_mfma<MODE, BITS, 32, RB, OSRC>), grid, dim3(256), 0, st, a));
+    // 4 row blocks per workgroup, fewer where that would leave under two workgroups per CU
+    LegacyArgs la = a;
+    la.rb = legacy_rows_per_wg(a.M, NB / 64 * B);
+    dim3 grid((unsigned)((a.M + 64 * la.rb - 1) / (64 * la.rb)), (unsigned)(NB / 64), (unsigned)B);
+    if (K == 16) LRQ_TRY(launch((k_legacy_mfma<MODE, BITS, 16, OSRC>), grid, dim3(256), 0, st, la));
+    else LRQ_TRY(launch((k_legacy_mfma<MODE, BITS, 32, OSRC>), grid, dim3(256), 0, st, la));
   } else {
     const int64_t chunks = (NB + 255) / 256;
     if (B * a.M * chunks > INT32_MAX) return LRQ_ERR_SHAPE;
@@ -644,10 +656,10 @@ extern "C" int lrq_legacy_kth_residual(const void* l, const void* rt, int32_t K,
   LRQ_TRY(launch(k_kth_init, dim3(1), dim3(256), 0, hs, hist, sel, k));
   for (int fine = 0; fine < 2; ++fine) {
     if (mfma_ok) {
-      constexpr int RB = 4;
-      dim3 grid((unsigned)((M + 64 * RB - 1) / (64 * RB)), (unsigned)(N / 64), 1u);
-      if (K == 16) LRQ_TRY(launch((k_legacy_mfma<kHist, 8, 16, RB, 0>), grid, dim3(256), 0, hs, a));
-      else LRQ_TRY(launch((k_legacy_mfma<kHist, 8, 32, RB, 0>), grid, dim3(256), 0, hs, a));
+      a.rb = legacy_rows_per_wg(M, N / 64);
+      dim3 grid((unsigned)((M + 64 * a.rb - 1) / (64 * a.rb)), (unsigned)(N / 64), 1u);
+      if (K == 16) LRQ_TRY(launch((k_legacy_mfma<kHist, 8, 16, 0>), grid, dim3(256), 0, hs, a));
+      else LRQ_TRY(launch((k_legacy_mfma<kHist, 8, 32, 0>), grid, dim3(256), 0, hs, a));
     } else {
       const int64_t chunks = (N + 255) / 256;
       if (M * chunks > INT32_MAX) return LRQ_ERR_SHAPE;
