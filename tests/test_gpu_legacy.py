@@ -51,6 +51,30 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+def test_legacy_encode_extreme_scales(pkg, dev, bits):
+    """Scales outside [2^-100, 2^100] (here 2^-110 and 2^105, in a few columns of some units)
+    send their workgroups to the IEEE division; the other units take the reciprocal form.
+    Codes and outliers equal the oracle's on both."""
+    B, M, N, K, tau = 1, 64, 2048, 16, 5.0
+    l, r, x, s = _inputs(4242 + bits, B, M, N, K, 1)
+    s = s.float()
+    s[0, 3] = 2.0 ** -110
+    s[0, 700] = 2.0 ** 105
+    s[0, N - 1] = -(2.0 ** -110)
+    s = s.to(torch.bfloat16)
+    lb, rb, xb, sb = bits16(l), bits16(r), bits16(x), bits16(s)
+    o_sp, q = pkg.low_rank_addition_fuse_compression_quantization(l.to(dev), r.to(dev), x.to(dev), s.to(dev),
+                                                                  quantize_bit=bits, outlier=tau)
+    torch.cuda.synchronize()
+    o_ref, q_ref = O.legacy_encode(lb, rb, xb, sb, bits, tau)
+    qg = q.cpu().numpy()
+    assert _frac_mismatch(qg, q_ref) <= TIE_BUDGET
+    og = bits16(o_sp.to_dense())
+    nz = (O.bf16_to_f32(o_ref) != 0) | (O.bf16_to_f32(og) != 0)
+    assert _frac_mismatch(og[nz], o_ref[nz]) <= TIE_BUDGET
+
+
 @pytest.mark.parametrize("B,M,N,K,bits,s_rows,tau", CASES)
 def test_legacy_encode_decode(pkg, dev, B, M, N, K, bits, s_rows, tau):
     l, r, x, s = _inputs(1000 + N + bits, B, M, N, K, s_rows)

@@ -78,6 +78,34 @@ __device__ __forceinline__ uint32_t legacy_code(float x, float lr, float sc, flo
   return (uint32_t)(int)(c + half);
 }
 
+// legacy_code with the division by the scale taken as q0 = a * rc clamped to +-2^20, then
+// q0 + rc * (a - sc * q0) (both steps fmas), rc = 1/sc rounded once: Markstein's correction of a
+// quotient within an ulp by a correctly rounded reciprocal (for a quotient of bf16 values no
+// fp32 rounding tie exists).  The clamp only touches quotients whose code saturates either way.
+// For scales with 2^-100 <= |sc| <= 2^100 the codes equal legacy_code's for every finite bf16
+// numerator and every bit width: checked exhaustively on the host (3.3e9 pairs) by the
+// repository's legacy division test.  Other scales take legacy_code.
+template <int BITS>
+__device__ __forceinline__ uint32_t legacy_code_rc(float x, float lr, float sc, float rc, float tau, float& o,
+                                                   bool& big) {
+  constexpr float half = (float)(1 << (BITS - 1));
+  const float xr = bf16r(x - lr);
+  big = fabsf(xr) > tau;
+  o = big ? xr : 0.f;
+  const float a = xr - o;
+  const float q0 = __builtin_amdgcn_fmed3f(a * rc, -0x1p20f, 0x1p20f);
+  const float q = __builtin_fmaf(__builtin_fmaf(-sc, q0, a), rc, q0);
+  const float d = bf16r(q);
+  const float c = __builtin_amdgcn_fmed3f(rintf(d), -half, half - 1.f);
+  return (uint32_t)(int)(c + half);
+}
+
+// Scales that legacy_code_rc serves exactly (NaN fails the test).
+__device__ __forceinline__ bool rc_scale_ok(float sc) {
+  const float m = fabsf(sc);
+  return m >= 0x1p-100f && m <= 0x1p100f;
+}
+
 // Decode of one element: bf16(bf16(bf16((code - 2^(b-1)) * s) + o) + lr); with !HAS_O the add
 // of o (exact zero) is skipped.  The outliers come as a dense tensor (OSRC 1) or as COO pieces
 // (OSRC 2); both feed the same per-element add, so the two give the same bits.
@@ -207,6 +235,22 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
   for (int p = 0; p < NP; ++p) load_vops<G, K>(a.rt, unit_base(p, u, N, NP, G), j, g, vop[p]);
   const float zero[E] = {};
 
+  // encode: the unit's scales and their reciprocals (one IEEE division per column) in LDS, for
+  // every row of the workgroup; rc_ok: every scale is one legacy_code_rc serves exactly
+  __shared__ __attribute__((aligned(16))) float stab[MODE == kEncode ? 2 * NP * G : 4];
+  bool rc_ok = false;
+  if constexpr (MODE == kEncode) {
+    int ok = 1;
+    for (int i = threadIdx.x; i < NP * G; i += 256) {
+      const int p = i / G, c = i % G;
+      const float sv = bf_lo(srow[unit_base(p, u, N, NP, G) + c]);
+      stab[i] = sv;
+      stab[NP * G + i] = 1.0f / sv;
+      ok &= rc_scale_ok(sv) ? 1 : 0;
+    }
+    rc_ok = __syncthreads_and(ok) != 0;
+  }
+
   for (int i = 0; i < a.rb; ++i) {
     const int row0 = (blockIdx.x * a.rb + i) * 64 + w * 16;  // wave-uniform: a scalar exit
     if (row0 >= M) break;  // whole 16-row block past the end
@@ -232,8 +276,20 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
       residual_unit<G, K>(vop[p], lop, zero, lr);
 #pragma unroll
       for (int e = 0; e < E; ++e) lr[e] = bf16r(lr[e]);
-      float sc[E];
-      if constexpr (MODE != kAdd && MODE != kHist) {
+      float sc[E], rc[E];
+      if constexpr (MODE == kEncode) {
+        const float* sp = stab + p * G + E * g;
+#pragma unroll
+        for (int k = 0; k < E; k += 4) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(sp + k);
+          const f32x4 w = *reinterpret_cast<const f32x4*>(sp + NP * G + k);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            sc[k + e] = v[e];
+            rc[k + e] = w[e];
+          }
+        }
+      } else if constexpr (MODE != kAdd && MODE != kHist) {
         unpack8(ld16(srow + c0), sc);
         unpack8(ld16(srow + c0 + 8), sc + 8);
       }
@@ -257,11 +313,20 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
         if constexpr (MODE == kEncode) {
           float ov[E];
           uint32_t n = 0;
+          if (rc_ok) {  // workgroup-uniform
 #pragma unroll
-          for (int e = 0; e < E; ++e) {
-            bool hit;
-            byte[e] |= legacy_code<BITS>(xv[e], lr[e], sc[e], a.tau, ov[e], hit) << (BITS * p);
-            n += hit ? 1u : 0u;
+            for (int e = 0; e < E; ++e) {
+              bool hit;
+              byte[e] |= legacy_code_rc<BITS>(xv[e], lr[e], sc[e], rc[e], a.tau, ov[e], hit) << (BITS * p);
+              n += hit ? 1u : 0u;
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+              bool hit;
+              byte[e] |= legacy_code<BITS>(xv[e], lr[e], sc[e], a.tau, ov[e], hit) << (BITS * p);
+              n += hit ? 1u : 0u;
+            }
           }
           st16(a.oout + erow + c0, pack8(ov));
           st16(a.oout + erow + c0 + 8, pack8(ov + 8));
