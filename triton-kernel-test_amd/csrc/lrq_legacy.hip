@@ -150,23 +150,28 @@ __device__ __forceinline__ void coo_piece_values(const LegacyArgs& a, int64_t bm
 
 // Denser outliers (OSRC 3): the COO pieces of a wave's 16 rows x one unit (NP pieces of 64
 // columns per row) go into the wave's
-// LDS tile ot[row][plane][64] (bf16 bits).  The four lanes of a row share its pieces: every
-// plane's piece bounds are requested at once, then in each pass lane (j, g) requests entries
+// LDS tile ot[row][plane][64] (bf16 bits).  The four lanes of a row share its pieces: the piece
+// bounds come from coo_bounds (requested a block ahead), then in each pass lane (j, g) requests entries
 // g, g + 4, .. (KL per piece) of each of its row's pieces, all of them before any is used
 // (clamped indices; no load sits under a branch), and writes those that fall in the piece into
 // the tile after the lane has zeroed its own 16 columns of every plane.  Another pass runs only
 // while some piece of the wave has more entries.  Entries of a coalesced COO are unique per
 // position (so no two lanes write the same one), and entries outside the piece are ignored.
-template <int NP, int KL>
-__device__ __forceinline__ void coo_tile(const LegacyArgs& a, int64_t bm, int u, int N, int j, int g,
-                                         uint16_t* __restrict__ ot) {
-  int64_t s0[NP], s1[NP];
+// The piece bounds of row bm's NP pieces of unit u (requested together; coo_tile uses them).
+template <int NP>
+__device__ __forceinline__ void coo_bounds(const LegacyArgs& a, int64_t bm, int u, int N, int64_t (&s0)[NP],
+                                           int64_t (&s1)[NP]) {
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int64_t pc = bm * a.npc + (int64_t)(p * (N / NP) + u * 64) / 64;
     s0[p] = a.optr[pc];
     s1[p] = a.optr[pc + 1];
   }
+}
+
+template <int NP, int KL>
+__device__ __forceinline__ void coo_tile(const LegacyArgs& a, int64_t (&s0)[NP], int64_t (&s1)[NP], int u, int N,
+                                         int j, int g, uint16_t* __restrict__ ot) {
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     uint16_t* r = ot + (j * NP + p) * 64 + 16 * g;
@@ -251,6 +256,22 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
     rc_ok = __syncthreads_and(ok) != 0;
   }
 
+  // decode and fused consumers: the next row block's L operand, codes and COO piece bounds are
+  // requested before the current block is computed (nl / nq / ns0 / ns1 carry them over)
+  constexpr bool kCodes = MODE == kDecode || MODE == kFusedStore || MODE == kFusedSilu || MODE == kFusedMul;
+  constexpr int NPB = (MODE == kDecode && OSRC == 3) ? NP : 1;  // COO piece bounds per lane
+  u32x2 nl[RT];
+  u32x4 nq = u32x4{0u, 0u, 0u, 0u};
+  int64_t ns0[NPB], ns1[NPB];
+  auto fetch_next = [&](int i) {  // block i of the workgroup (rows clamped to the last)
+    const int64_t rn = min((blockIdx.x * a.rb + i) * 64 + w * 16 + j, M - 1);
+#pragma unroll
+    for (int t = 0; t < RT; ++t) nl[t] = ld8(a.l + rn * K + 16 * t + 4 * g);
+    nq = ld16(a.qin + ((int64_t)b * M + rn) * NB + u * G + E * g);
+    if constexpr (MODE == kDecode && OSRC == 3) coo_bounds<NP>(a, (int64_t)b * M + rn, u, N, ns0, ns1);
+  };
+  if constexpr (kCodes) fetch_next(0);
+
   for (int i = 0; i < a.rb; ++i) {
     const int row0 = (blockIdx.x * a.rb + i) * 64 + w * 16;  // wave-uniform: a scalar exit
     if (row0 >= M) break;  // whole 16-row block past the end
@@ -258,16 +279,27 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
     const int64_t rr = min(row, M - 1);
     const int64_t erow = ((int64_t)b * M + rr) * N;  // element offset of the row in [B, M, N] outputs
     u32x2 lop[RT];
-#pragma unroll
-    for (int t = 0; t < RT; ++t) lop[t] = ld8(a.l + rr * K + 16 * t + 4 * g);
     u32x4 qb = u32x4{0u, 0u, 0u, 0u};
-    if constexpr (MODE == kDecode || MODE == kFusedStore || MODE == kFusedSilu || MODE == kFusedMul)
-      qb = ld16(a.qin + ((int64_t)b * M + rr) * NB + u * G + E * g);
+    int64_t s0[NPB], s1[NPB];
+    if constexpr (kCodes) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t) lop[t] = nl[t];
+      qb = nq;
+#pragma unroll
+      for (int q = 0; q < NPB; ++q) {
+        s0[q] = ns0[q];
+        s1[q] = ns1[q];
+      }
+      fetch_next(min(i + 1, a.rb - 1));  // (the last block fetches itself again: unused)
+    } else {
+#pragma unroll
+      for (int t = 0; t < RT; ++t) lop[t] = ld8(a.l + rr * K + 16 * t + 4 * g);
+    }
     uint32_t byte[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) byte[e] = 0u;
     uint16_t* ot = otile + (size_t)w * 16 * NP * 64;
-    if constexpr (MODE == kDecode && OSRC == 3) coo_tile<NP, 4>(a, (int64_t)b * M + rr, u, N, j, g, ot);
+    if constexpr (MODE == kDecode && OSRC == 3) coo_tile<NP, 2>(a, s0, s1, u, N, j, g, ot);
 
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
