@@ -256,9 +256,11 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
     rc_ok = __syncthreads_and(ok) != 0;
   }
 
-  // decode and fused consumers: the next row block's L operand, codes and COO piece bounds are
-  // requested before the current block is computed (nl / nq / ns0 / ns1 carry them over)
+  // decode from the COO tile: the next row block's L operand, codes and COO piece bounds are
+  // requested before the current block is computed (nl / nq / ns0 / ns1 carry them over; the
+  // other modes measured slower with the carried registers)
   constexpr bool kCodes = MODE == kDecode || MODE == kFusedStore || MODE == kFusedSilu || MODE == kFusedMul;
+  constexpr bool kPre = MODE == kDecode && OSRC == 3;
   constexpr int NPB = (MODE == kDecode && OSRC == 3) ? NP : 1;  // COO piece bounds per lane
   u32x2 nl[RT];
   u32x4 nq = u32x4{0u, 0u, 0u, 0u};
@@ -270,7 +272,7 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
     nq = ld16(a.qin + ((int64_t)b * M + rn) * NB + u * G + E * g);
     if constexpr (MODE == kDecode && OSRC == 3) coo_bounds<NP>(a, (int64_t)b * M + rn, u, N, ns0, ns1);
   };
-  if constexpr (kCodes) fetch_next(0);
+  if constexpr (kPre) fetch_next(0);
 
   for (int i = 0; i < a.rb; ++i) {
     const int row0 = (blockIdx.x * a.rb + i) * 64 + w * 16;  // wave-uniform: a scalar exit
@@ -281,7 +283,7 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
     u32x2 lop[RT];
     u32x4 qb = u32x4{0u, 0u, 0u, 0u};
     int64_t s0[NPB], s1[NPB];
-    if constexpr (kCodes) {
+    if constexpr (kPre) {
 #pragma unroll
       for (int t = 0; t < RT; ++t) lop[t] = nl[t];
       qb = nq;
@@ -294,6 +296,7 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
     } else {
 #pragma unroll
       for (int t = 0; t < RT; ++t) lop[t] = ld8(a.l + rr * K + 16 * t + 4 * g);
+      if constexpr (kCodes) qb = ld16(a.qin + ((int64_t)b * M + rr) * NB + u * G + E * g);
     }
     uint32_t byte[E];
 #pragma unroll
