@@ -273,6 +273,23 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
     if constexpr (MODE == kDecode && OSRC == 3) coo_bounds<NP>(a, (int64_t)b * M + rn, u, N, ns0, ns1);
   };
   if constexpr (kPre) fetch_next(0);
+  // encode at 2 bits and more: the next row block's x (and L operand) is requested before the
+  // current block is computed (nx carries it over; at 1 bit its 64 registers would halve the
+  // waves per SIMD)
+  constexpr bool kPreX = MODE == kEncode && NP <= 4;
+  u32x4 nx[kPreX ? NP : 1][2];
+  auto fetch_x = [&](int i) {
+    const int64_t rn = min((blockIdx.x * a.rb + i) * 64 + w * 16 + j, M - 1);
+#pragma unroll
+    for (int t = 0; t < RT; ++t) nl[t] = ld8(a.l + rn * K + 16 * t + 4 * g);
+#pragma unroll
+    for (int p = 0; p < (kPreX ? NP : 1); ++p) {
+      const uint16_t* xp = a.x + (int64_t)b * a.ldx_b + rn * a.ldx_m + unit_base(p, u, N, NP, G) + E * g;
+      nx[p][0] = ld16(xp);
+      nx[p][1] = ld16(xp + 8);
+    }
+  };
+  if constexpr (kPreX) fetch_x(0);
 
   for (int i = 0; i < a.rb; ++i) {
     const int row0 = (blockIdx.x * a.rb + i) * 64 + w * 16;  // wave-uniform: a scalar exit
@@ -293,10 +310,22 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
         s1[q] = ns1[q];
       }
       fetch_next(min(i + 1, a.rb - 1));  // (the last block fetches itself again: unused)
+    } else if constexpr (kPreX) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t) lop[t] = nl[t];
     } else {
 #pragma unroll
       for (int t = 0; t < RT; ++t) lop[t] = ld8(a.l + rr * K + 16 * t + 4 * g);
       if constexpr (kCodes) qb = ld16(a.qin + ((int64_t)b * M + rr) * NB + u * G + E * g);
+    }
+    u32x4 cx[kPreX ? NP : 1][2];
+    if constexpr (kPreX) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        cx[p][0] = nx[p][0];
+        cx[p][1] = nx[p][1];
+      }
+      fetch_x(min(i + 1, a.rb - 1));  // (the last block fetches itself again: unused)
     }
     uint32_t byte[E];
 #pragma unroll
@@ -342,9 +371,14 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
         }
       } else if constexpr (MODE == kEncode || MODE == kAdd) {
         float xv[E];
-        const uint16_t* xp = a.x + (int64_t)b * a.ldx_b + rr * a.ldx_m + c0;
-        unpack8(ld16(xp), xv);
-        unpack8(ld16(xp + 8), xv + 8);
+        if constexpr (kPreX) {
+          unpack8(cx[p][0], xv);
+          unpack8(cx[p][1], xv + 8);
+        } else {
+          const uint16_t* xp = a.x + (int64_t)b * a.ldx_b + rr * a.ldx_m + c0;
+          unpack8(ld16(xp), xv);
+          unpack8(ld16(xp + 8), xv + 8);
+        }
         if constexpr (MODE == kEncode) {
           float ov[E];
           uint32_t n = 0;
