@@ -117,12 +117,12 @@ def test_decode_and_consumer_argument_errors(L):
 
 def test_dequant_gemm_t_arguments(L):
     """Workspace query (host only) and the argument errors of the transposed dequant-GEMM."""
-    t = _desc(L)  # 32 rows, 4096 columns, int4 / g64: 32 units -> 16 column groups of 2 units
+    t = _desc(L)  # 32 rows, 4096 columns, int4 / g64: 32 units -> 32 column groups of 1 unit
     ws = L.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(t), 16)
     assert ws == 1 * 4096 * 16 * 4  # 2 row blocks < 8 waves: one row group
     big = _desc(L, rows=16384)
-    assert L.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(big), 16) == 16 * 4096 * 16 * 4
-    # n = 32: one unit per wave (accumulator budget), 32 column groups -> 8 row groups
+    # 32 column groups -> ceil(256 / 32) = 8 row groups, for n = 16 and n = 32 alike
+    assert L.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(big), 16) == 8 * 4096 * 16 * 4
     assert L.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(big), 32) == 8 * 4096 * 32 * 4
     assert L.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(t), 24) == L.LRQ_ERR_UNSUPPORTED
     assert L.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(_desc(L, bits=3)), 16) == L.LRQ_ERR_UNSUPPORTED
