@@ -213,6 +213,41 @@ struct RowsEnc {
   static_assert(LDS <= 160 * 1024, "LDS budget");
 };
 
+// Direct-to-LDS slices (RowsEnc::PPL == NP): the next block's 16 row loads are issued in
+// pieces at points 0 (after the current slice is read), 1 (after the partial sums) and 2 + u
+// (after unit u is quantised); n[pt] loads at point pt.
+#ifndef LRQ_ENC_SCHED_U4
+#define LRQ_ENC_SCHED_U4 4, 8, 0, 4, 0, 0
+#endif
+#ifndef LRQ_ENC_SCHED_U2
+#define LRQ_ENC_SCHED_U2 4, 8, 0, 4
+#endif
+template <int UPW>
+struct DmaSched;
+template <>
+struct DmaSched<4> {
+  static constexpr int n[6] = {LRQ_ENC_SCHED_U4};
+};
+template <>
+struct DmaSched<2> {
+  static constexpr int n[4] = {LRQ_ENC_SCHED_U2};
+};
+// loads issued before point pt
+template <int UPW>
+constexpr int dma_begin(int pt) {
+  int s = 0;
+  for (int i = 0; i < pt; ++i) s += DmaSched<UPW>::n[i];
+  return s;
+}
+// units quantised after the last point that issues loads
+template <int UPW>
+constexpr int dma_units_after() {
+  int last = 0;
+  for (int i = 0; i < UPW + 2; ++i)
+    if (DmaSched<UPW>::n[i] > 0) last = i;
+  return last < 2 ? UPW : UPW - 1 - (last - 2);
+}
+
 // OUTL: outlier channels.  The V operand rows of outlier columns are zeroed once, so the
 // projection is that of Y with those columns zeroed (the same products and sums) and their
 // residuals are zeroed before the group statistics; their bf16 values go to the fp16 side
@@ -333,6 +368,13 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
         pf[buf][i] = ld16_stream(gaddr(rb, round * Re::RL + i));
     }
   };
+  // DMA: the loads of schedule point pt (rows dma_begin(pt) .. dma_begin(pt + 1) - 1)
+  auto issue_pt = [&](auto pt_tag, int rb) {
+    constexpr int pt = decltype(pt_tag)::value;
+    if constexpr (DMA)
+      static_for<dma_begin<UPW>(pt), dma_begin<UPW>(pt + 1)>(
+          [&](auto i) { ld16_to_lds(gaddr(rb, i), region + (int)i * Re::PITCH); });
+  };
   auto land = [&](int buf, int round) {
     if constexpr (!DMA) {
 #pragma unroll
@@ -411,10 +453,12 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
     const int rbn = __builtin_amdgcn_readfirstlane(min(rb0 + b + 1, nrb - 1));
     if constexpr (DMA) {
       // Wait until the slice's loads have written the region.  vmcnt retires in issue order
-      // on gfx9 (loads and stores alike); after the last round of a block's loads this wave
-      // issues exactly kAfter stores (the codes of units 2.., the qparams and L rows), which
-      // need not complete here.  Block 0's loads are the prologue's last memory operations.
-      constexpr int kAfter = (UPW - 2) * (E / 16) + 1 + RT;
+      // on gfx9 (loads and stores alike); after the last of a block's loads this wave issues
+      // exactly kAfter stores (the codes of the units quantised after it, the qparams and L
+      // rows), which need not complete here.  Block 0's loads are the prologue's last memory
+      // operations.
+      static_assert(dma_begin<UPW>(UPW + 2) == Re::NLD, "the schedule issues every load of a block once");
+      constexpr int kAfter = dma_units_after<UPW>() * (E / 16) + 1 + RT;
       static_assert(kAfter < 16, "vmcnt immediate");
       if (b == 0)
         __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
@@ -437,7 +481,12 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (next) issue(0, rbn, 0);
+    if (next) {
+      if constexpr (DMA)
+        issue_pt(std::integral_constant<int, 0>{}, rbn);
+      else
+        issue(0, rbn, 0);
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     f32x4 acc[2][RT];
@@ -483,9 +532,13 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
     // (at most two rounds in flight: round 0 overlaps the projection, 1 and 2 the first two
     // units, 3 the last two)
     if (next) {
-      land(0, 0);
-      issue(1, rbn, 1);
-      issue(0, rbn, 2);
+      if constexpr (DMA) {
+        issue_pt(std::integral_constant<int, 1>{}, rbn);
+      } else {
+        land(0, 0);
+        issue(1, rbn, 1);
+        issue(0, rbn, 2);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
     uint8_t* crow = codes + (int64_t)rb * 16 * ldc + (uint32_t)(row - rb * 16) * (uint32_t)ldc;
@@ -496,7 +549,16 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
         qp[uu] = quant_unit_core<BITS, G, R>(x[uu], vop[uu], lopn, colmask, ub + uu, N, g, crow);
       else
         qp[uu] = quant_unit_regs<BITS, G, R>(x[uu], vop[uu], lopn, ub + uu, g, crow);
-      if (uu == 1 && next) {
+      if constexpr (DMA) {
+        if (next)
+          static_for<0, UPW>([&](auto u) {
+            if (uu == u && DmaSched<UPW>::n[2 + u] > 0) {
+              __builtin_amdgcn_sched_barrier(0);
+              issue_pt(std::integral_constant<int, 2 + u>{}, rbn);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+          });
+      } else if (uu == 1 && next) {
         __builtin_amdgcn_sched_barrier(0);
         land(1, 1);
         issue(1, rbn, 3);

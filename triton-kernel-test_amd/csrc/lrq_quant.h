@@ -8,13 +8,36 @@ namespace lrq {
 
 // r = fp32(x - L V^T) over the lane's G/4 columns of one unit-plane, rounded once (an MFMA
 // whose accumulator input is x; lopn holds -L), or r = x at rank 0.
+//
+// Rank 16: x reaches fp32 through the MFMA pipe instead of VALU unpacking: an identity step
+// I * x (exact: one product of 1 per output, the rest zero) puts x[row][16g + 4q + v] in the
+// accumulator layout, and the reconstruction step adds -L V^T to it with one rounding, as above.
+#ifndef LRQ_RES_IDMFMA
+#define LRQ_RES_IDMFMA 1
+#endif
 template <int G, int R>
 __device__ __forceinline__ void residual_plane(const u32x4 (&x)[G / 32],
                                                const u32x2 (&vop)[G / 16][R > 0 ? R / 16 : 1],
                                                const u32x2* lopn, float* r) {
+  if constexpr (R == 16 && LRQ_RES_IDMFMA) {
+    const int l = __lane_id();
+    const u32x2 ida = identity_bop(l & 15, l >> 4);  // A operand: I[i][4g + e], e < 4, for lane (i, g)
 #pragma unroll
-  for (int k = 0; k < G / 32; ++k) unpack8(x[k], r + 8 * k);
-  if constexpr (R > 0) residual_unit<G, R>(vop, lopn, r, r);
+    for (int q = 0; q < G / 16; ++q) {
+      // B operand: lane (row, g) holds x[row][16g + 4q + e], e < 4 (dwords 2(q%2), +1 of x[q/2])
+      const u32x2 xb = u32x2{x[q >> 1][2 * (q & 1)], x[q >> 1][2 * (q & 1) + 1]};
+      f32x4 acc = mfma_16x16x16(ida, xb, zero4());
+      acc = mfma_16x16x16(vop[q][0], lopn[0], acc);
+      r[4 * q + 0] = acc[0];
+      r[4 * q + 1] = acc[1];
+      r[4 * q + 2] = acc[2];
+      r[4 * q + 3] = acc[3];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < G / 32; ++k) unpack8(x[k], r + 8 * k);
+    if constexpr (R > 0) residual_unit<G, R>(vop, lopn, r, r);
+  }
 }
 
 // Lane-local min / max of n values: min(min(acc, a), b) chains, one v_min3 / v_max3 per
