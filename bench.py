@@ -63,6 +63,8 @@ def parse():
     ap.add_argument("--nbuf", type=int, default=4)
     ap.add_argument("--cold-steps", type=int, default=20, help="timed launches of the last kernel with HBM-cold inputs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--lora-split", action="store_true",
+                    help="lora: time x A and x^T g as the two separate kernels instead of the one-pass entry")
     ap.add_argument("--cpu-seconds", type=float, default=3.0, help="target seconds per CPU baseline run")
     return ap.parse_args()
 
@@ -336,7 +338,7 @@ def build_plan_ref(cfg, pkg, lib, dev, nbuf):
     return entries, 2 * E, timed, sets
 
 
-def build_plan(cfg, pkg, lib, dev, nbuf):
+def build_plan(cfg, pkg, lib, dev, nbuf, lora_split=False):
     """Per-config step: a list of (name, launch(k) -> status, algorithmic bytes, mfma flops) run
     in order on buffer set k, plus the step's activation bytes and how `value` is formed."""
     import torch
@@ -420,6 +422,16 @@ def build_plan(cfg, pkg, lib, dev, nbuf):
         # once per kernel, plus each kernel's small operands and output
         n = cfg.lora_rank
         base = M * N * (cfg.bits / 8 + 4 / cfg.group) + 2 * M * r + 2 * N * r
+        lws = lib.lrq_lora_grads_workspace(B(sets[0]["dec"]), n)
+        if lws > 0 and not lora_split:
+            # both products from one pass over the codes (lrq_lora_grads): codes + qparams + L + V
+            # once, A and g, x A out (bf16) and dA out (fp32)
+            lw = torch.empty((lws + 15) // 16 * 4, dtype=torch.float32, device=dev)
+            entries.append(("lora_grads", lambda k: lib.lrq_lora_grads(B(sets[k]["dec"]), P(sets[k]["a"]), n, P(sets[k]["g"]),
+                                                                  n, n, P(sets[k]["xa"]), n, 0, P(sets[k]["da"]), n, 1,
+                                                                  P(lw), lw.numel() * 4, sp),
+                            base + 2 * N * n + 4 * M * n + 4 * N * n, 2 * M * N * r + 4 * M * N * n))
+            return entries, 2 * M * N, ["lora_grads"], sets
         entries.append(("xa", lambda k: lib.lrq_dequant_gemm(B(sets[k]["dec"]), P(sets[k]["a"]), n,
                                                              P(sets[k]["xa"]), n, 0, sp),
                         base + 2 * N * n + 2 * M * n, 2 * M * N * r + 2 * M * N * n))
@@ -457,7 +469,7 @@ def main():
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream(dev)
 
-    entries, act_bytes, timed, _sets = build_plan(cfg, pkg, lib, dev, args.nbuf)
+    entries, act_bytes, timed, _sets = build_plan(cfg, pkg, lib, dev, args.nbuf, lora_split=args.lora_split)
 
     def step(i, ev=None):
         k = i % args.nbuf

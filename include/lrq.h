@@ -138,6 +138,27 @@ int lrq_dequant_gemm_t(const lrq_tensors* t, const void* g, int64_t ldg, int32_t
  * Host only: no HIP call. */
 int64_t lrq_dequant_gemm_t_workspace(const lrq_tensors* t, int32_t n_out);
 
+/* Both LoRA factor-gradient products that read the saved activation, in one pass over its
+ * codes: xa[rows, n_out] = decode(t) a (a bf16 [hidden, n_out], row stride lda) — the x A whose
+ * transpose times dy is dB — and da[hidden, n_out] = decode(t)^T g (g bf16 [rows, n_out], row
+ * stride ldg, 8-byte aligned) — dA = x^T (dy B^T); compute_lora_gradient
+ * (low_rank_system_profile_forward.py:14-18, `(x @ a).mT @ dy` and `x.mT @ (dy @ b.mT)`).  Same
+ * results as lrq_dequant_gemm (xa) and lrq_dequant_gemm_t (da) up to the order of the fp32
+ * additions: decode(t) rounded to bf16 as lrq_decode returns it, fp32 accumulate; each output
+ * fp32 when its *_fp32 flag is non-zero (16-byte aligned rows of a multiple of 4 elements), else
+ * bf16 (8-byte aligned).  int4 / group 64 / rank 16, n_out 16, a multiple of 4 units (512
+ * columns) per row, no outlier channels, no rotated format (else LRQ_ERR_UNSUPPORTED: use the two
+ * entry points).  The fp32 partials of column and row groups go to `workspace` (16-byte
+ * aligned, lrq_lora_grads_workspace(t, n_out) bytes) and are summed in group order, so results
+ * depend only on the shapes.  rows == 0 writes zeros to da. */
+int lrq_lora_grads(const lrq_tensors* t, const void* a, int64_t lda, const void* g, int64_t ldg, int32_t n_out,
+                   void* xa, int64_t ldxa, int32_t xa_fp32, void* da, int64_t ldda, int32_t da_fp32,
+                   void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes lrq_lora_grads needs for `t` and n_out (>= 0), or a negative LRQ_ERR_*.
+ * Host only: no HIP call. */
+int64_t lrq_lora_grads_workspace(const lrq_tensors* t, int32_t n_out);
+
 /* Largest workspace lrq_dequant_gemm_t_noalloc can serve from its own scratch (bytes). */
 #define LRQ_GEMM_T_SCRATCH_BYTES (16 * 1024 * 1024)
 

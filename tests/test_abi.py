@@ -140,6 +140,33 @@ def test_dequant_gemm_t_arguments(L):
     assert call(_desc(L, flags=1)) == L.LRQ_ERR_UNSUPPORTED
 
 
+def test_lora_grads_arguments(L):
+    """Workspace query (host only) and the argument errors of the one-pass LoRA products."""
+    def r16(**kw):
+        t_ = _desc(L, rank=16, ld_L=16, V=0x40000, **kw)
+        t_.L = 0x30000  # (the descriptor's L field; _desc's own first argument is the library)
+        return t_
+    big = r16(rows=16384)
+    # 32 units -> 8 column groups of 4; 1024 row blocks -> 32 row groups of 32 blocks
+    ws = L.call_raw("lrq_lora_grads_workspace", ctypes.byref(big), 16)
+    assert ws == 8 * 16384 * 16 * 4 + 32 * 4096 * 16 * 4
+    # 32 rows: 2 row groups of one block
+    assert L.call_raw("lrq_lora_grads_workspace", ctypes.byref(r16()), 16) == 8 * 32 * 64 + 2 * 4096 * 64
+    for t_, n in ((r16(), 32), (_desc(L), 16), (r16(hidden=1792, ld_codes=896, ld_qp=56), 16), (r16(flags=1), 16)):
+        assert L.call_raw("lrq_lora_grads_workspace", ctypes.byref(t_), n) == L.LRQ_ERR_UNSUPPORTED
+    p = lambda v: ctypes.c_void_p(v)  # noqa: E731
+    call = lambda a=p(0x10000), g=p(0x20000), ldg=16, xa=p(0x50000), ldxa=16, da=p(0x60000), w=p(0x70000), wb=ws: (  # noqa: E731
+        L.call_raw("lrq_lora_grads", ctypes.byref(big), a, 16, g, ldg, 16, xa, ldxa, 0, da, 16, 1, w, wb, None))
+    assert call(a=None) == L.LRQ_ERR_NULL
+    assert call(ldg=8) == L.LRQ_ERR_SHAPE
+    assert call(g=p(0x20004)) == L.LRQ_ERR_ALIGN
+    assert call(ldxa=18) == L.LRQ_ERR_ALIGN
+    assert call(da=p(0x60008)) == L.LRQ_ERR_ALIGN  # fp32 da: 16-byte rows
+    assert call(w=None) == L.LRQ_ERR_NULL
+    assert call(wb=ws - 16) == L.LRQ_ERR_WORKSPACE
+    assert call(w=p(0x70008)) == L.LRQ_ERR_ALIGN
+
+
 def test_coo_and_threshold_arguments(L):
     """Workspace sizes (host only) and argument errors of the outlier compaction, the COO decode
     and the threshold selection."""

@@ -5,6 +5,8 @@ representation: x_hat = bf16(oracle decode of the device codes), then the formul
 float64, rounded once (tests/parity.py bars).
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -250,3 +252,42 @@ def test_dequant_gemm_t_no_rows(pkg, dev):
                        ctypes.c_void_p(out.data_ptr()), 16, 1, None, 0, s)
     torch.cuda.synchronize()
     assert st == 0 and not out.any()
+
+
+@pytest.mark.parametrize("rows,hidden,out_dtype", [
+    (1000, 4096, torch.float32), (17, 4096, torch.float32), (300, 2048, torch.bfloat16),
+    (4100, 4096, torch.float32), (600, 8192, torch.bfloat16), (64, 1536, torch.float32)])
+def test_lora_grads_one_pass(pkg, dev, rows, hidden, out_dtype):
+    """lora_grads: x_hat A and x_hat^T g from one pass over the codes, against the float64
+    products on lrq_decode's output (fp32 out: within the fp32 accumulation bound 1e-5 * |x_hat||.|
+    per entry; bf16 out: within one ulp plus that bound), and against the two separate entry
+    points (dequant_gemm, dequant_gemm_t) within twice the bound.  4100 rows: 257 row blocks, row
+    groups of 9 blocks; 17 rows: groups of one block, waves with none; 1536 columns: 3 column groups."""
+    print(f"[lora_grads] rows={rows} hidden={hidden} {out_dtype}", flush=True)
+    x = pkg.inputs.activation(rows, hidden, 8, 20.0, seed=41)
+    V = pkg.inputs.basis(hidden, 16, seed=41)
+    gen = torch.Generator().manual_seed(42)
+    a = (torch.randn(hidden, 16, generator=gen) * 0.05).to(torch.bfloat16)
+    gm = (torch.randn(rows, 16, generator=gen) * 0.05).to(torch.bfloat16)
+    c = pkg.encode(x.to(dev), V.to(dev), bits=4, group_size=64)
+    t = c.descriptor()
+    assert pkg._lib.call_raw("lrq_lora_grads_workspace", ctypes.byref(t), 16) > 0  # the one-pass kernel
+    xa, da = pkg.lora_grads(c, a.to(dev), gm.to(dev), xa_dtype=out_dtype, da_dtype=out_dtype)
+    xa_s = pkg.dequant_gemm(c, a.to(dev), out_dtype=out_dtype).reshape(rows, 16)
+    da_s = pkg.dequant_gemm_t(c, gm.to(dev), out_dtype=out_dtype)
+    xd = O.bf16_to_f32(bits16(pkg.decode(c))).astype(np.float64)
+    torch.cuda.synchronize()
+    af, gf = O.bf16_to_f32(bits16(a)), O.bf16_to_f32(bits16(gm))
+    checks = (("xa", xa, xa_s, O.gemm(xd, af), 1e-5 * O.gemm(np.abs(xd), np.abs(af)) + 1e-9),
+              ("da", da, da_s, O.gemm_t(xd, gf), 1e-5 * O.gemm_t(np.abs(xd), np.abs(gf)) + 1e-9))
+    for name, got_t, sep_t, ref, bound in checks:
+        if out_dtype == torch.float32:
+            got, sep = got_t.cpu().numpy().astype(np.float64), sep_t.cpu().numpy().astype(np.float64)
+            ulp = 0.0
+        else:
+            got, sep = (O.bf16_to_f32(bits16(v)).astype(np.float64) for v in (got_t, sep_t))
+            ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))) - 7)
+        err = np.abs(got - ref)
+        assert (err <= ulp + bound).all(), (name, float((err / (ulp + bound)).max()))
+        assert (np.abs(got - sep) <= 2 * (ulp + bound)).all(), name
+        print(f"[lora_grads] {name}: worst error / bound {float((err / (ulp + bound)).max()):.3f}", flush=True)

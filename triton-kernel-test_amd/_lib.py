@@ -55,6 +55,9 @@ SIGNATURES = {
     "lrq_dequant_gemm_t": (c_int32, [_T, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p,
                                      c_int64, c_void_p]),
     "lrq_dequant_gemm_t_workspace": (c_int64, [_T, c_int32]),
+    "lrq_lora_grads": (c_int32, [_T, c_void_p, c_int64, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32,
+                                 c_void_p, c_int64, c_int32, c_void_p, c_int64, c_void_p]),
+    "lrq_lora_grads_workspace": (c_int64, [_T, c_int32]),
     "lrq_dequant_gemm_t_noalloc": (c_int32, [_T, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p]),
     "lrq_colmax": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     "lrq_topk": (c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p]),

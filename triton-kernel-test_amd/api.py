@@ -33,7 +33,8 @@ from ._lib import LrqTensors, call
 __all__ = [
     "LowRankBasis", "CompressedActivation", "encode", "decode", "silu_backward_compressed",
     "gelu_backward_compressed", "mul_compressed", "softmax_backward_compressed", "dequant_gemm",
-    "dequant_gemm_t", "dequant_gemm_t_noalloc", "outlier_channels", "column_absmax", "topk_channels", "wht128",
+    "dequant_gemm_t", "dequant_gemm_t_noalloc", "lora_grads", "outlier_channels", "column_absmax", "topk_channels",
+    "wht128",
 ]
 
 
@@ -344,6 +345,40 @@ def dequant_gemm_t(c: CompressedActivation, g: torch.Tensor, out_dtype=torch.flo
         call("lrq_dequant_gemm_t", ctypes.byref(t), _p(g2), n_out, n_out, _p(o), n_out,
              1 if out_dtype == torch.float32 else 0, _p(ws), ws.numel() * 4, _stream(c.device))
     return o
+
+
+def lora_grads(c: CompressedActivation, a: torch.Tensor, g: torch.Tensor, xa_dtype=torch.bfloat16,
+               da_dtype=torch.float32) -> tuple[torch.Tensor, torch.Tensor]:
+    """(decode(c) @ a, decode(c)^T @ g) — the two products of compute_lora_gradient
+    (low_rank_system_profile_forward.py:14-18) that read the saved x, from one pass over the codes
+    where the format allows it (int4 / g64 / rank 16, n = 16, rows of a multiple of 512 columns);
+    otherwise ``dequant_gemm`` and ``dequant_gemm_t``.  a: bf16 [N, n]; g: bf16 [rows, n]."""
+    _require_device(a, g)
+    g2 = g.reshape(-1, g.shape[-1]) if g.dim() >= 2 else g
+    if a.dtype != torch.bfloat16 or a.dim() != 2 or a.shape[0] != c.hidden:
+        raise ValueError("a must be bf16 [N, n]")
+    if g.dtype != torch.bfloat16 or g.dim() < 2 or g2.shape[0] != c.rows or g2.shape[1] != a.shape[1]:
+        raise ValueError("g must be bf16 [rows, n] (leading dimensions those of the activation)")
+    for d in (xa_dtype, da_dtype):
+        if d not in (torch.float32, torch.bfloat16):
+            raise ValueError("output dtypes must be float32 or bfloat16")
+    n_out = a.shape[1]
+    t = c.descriptor()
+    ws_bytes = _lib.call_raw("lrq_lora_grads_workspace", ctypes.byref(t), n_out)
+    if ws_bytes == _lib.LRQ_ERR_UNSUPPORTED or c.hadamard:
+        xa = dequant_gemm(c, a, out_dtype=xa_dtype).reshape(-1, n_out)
+        return xa, dequant_gemm_t(c, g2, out_dtype=da_dtype)
+    if ws_bytes < 0:
+        _lib.check(ws_bytes, "lrq_lora_grads_workspace")
+    a2, g2 = a.contiguous(), g2.contiguous()
+    ws = torch.empty((max(ws_bytes, 16) + 15) // 16 * 4, dtype=torch.float32, device=c.device)
+    xa = torch.empty((c.rows, n_out), dtype=xa_dtype, device=c.device)
+    da = torch.empty((c.hidden, n_out), dtype=da_dtype, device=c.device)
+    with torch.cuda.device(c.device):
+        call("lrq_lora_grads", ctypes.byref(t), _p(a2), n_out, _p(g2), n_out, n_out, _p(xa), n_out,
+             1 if xa_dtype == torch.float32 else 0, _p(da), n_out, 1 if da_dtype == torch.float32 else 0,
+             _p(ws), ws.numel() * 4, _stream(c.device))
+    return xa, da
 
 
 def dequant_gemm_t_noalloc(c: CompressedActivation, g: torch.Tensor, out: torch.Tensor) -> torch.Tensor:

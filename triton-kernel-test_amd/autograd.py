@@ -11,9 +11,10 @@ round trip part of autograd:
 * ``LoRALinearCompressed`` is an autograd Function whose forward is ``compute_lora`` and which
   saves x in the compressed format; its backward returns dx, dA and dB of
   ``compute_lora_gradient`` (W is frozen, as in the reference's LoRA setting).  With
-  ``fused=True`` (the default) x is never decoded: dA = x^T (dy B^T) comes from the transposed
-  dequant-GEMM and x A from the dequant-GEMM, both reading the codes (LoRA rank 16 or 32,
-  plain format); otherwise, or for other shapes, x is decoded and the formulas run on it.
+  ``fused=True`` (the default) x is never decoded: dA = x^T (dy B^T) and x A come from the codes,
+  in one pass for both (``lora_grads``: int4 / g64 / rank 16, LoRA rank 16) or from the
+  transposed dequant-GEMM and the dequant-GEMM (LoRA rank 16 or 32, plain format); otherwise,
+  or for other shapes, x is decoded and the formulas run on it.
 * ``compressed_saved_tensors`` is a ``torch.autograd.graph.saved_tensors_hooks`` context that
   stores every saved bf16 activation with a suitable last dimension in the compressed format
   and decodes it when backward asks for it, for any model.
@@ -29,7 +30,7 @@ from typing import Callable, Optional
 
 import torch
 
-from .api import CompressedActivation, LowRankBasis, decode, dequant_gemm, dequant_gemm_t, encode
+from .api import CompressedActivation, LowRankBasis, decode, encode, lora_grads
 
 __all__ = ["compute_lora", "compute_lora_gradient", "LoRALinearCompressed", "lora_linear_compressed",
            "compressed_saved_tensors", "fit_basis"]
@@ -78,8 +79,10 @@ class LoRALinearCompressed(torch.autograd.Function):
         dy2 = _flat(dy)
         if ctx.fused and _codes_gemm_ok(c, a, dy2):
             dx = dy2 @ (w + b.mT @ a.mT)
-            da = dequant_gemm_t(c, dy2 @ b.mT).to(a.dtype)              # x^T (dy B^T)
-            db = dequant_gemm(c, a, out_dtype=a.dtype).reshape(-1, a.shape[1]).mT @ dy2  # (x A)^T dy
+            # x A and x^T (dy B^T) from one pass over the codes where the format allows it
+            xa, da = lora_grads(c, a, dy2 @ b.mT, xa_dtype=a.dtype, da_dtype=torch.float32)
+            da = da.to(a.dtype)
+            db = xa.mT @ dy2  # (x A)^T dy
         else:
             dx, da, db = compute_lora_gradient(dy2, _flat(decode(c)), w, a, b)
         return dx.reshape(dy.shape[:-1] + (w.shape[1],)), None, da, db, None, None, None, None
