@@ -119,6 +119,14 @@ def test_fullsize_lora_gradients_on_codes(pkg, dev):
     mx = float((xa.double() - ref_xa).abs().max())
     print(f"[full lora] xA rel-L2 {rel:.2e} max-abs {mx:.2e}", flush=True)
     assert rel <= 1e-5 and mx <= 1e-3
+    # both products from one pass over the codes (lora_grads), fp32 out: each within the fp32
+    # accumulation bound of its float64 product
+    xa1, da1 = pkg.lora_grads(c, inp["a"], inp["g"], xa_dtype=torch.float32, da_dtype=torch.float32)
+    torch.cuda.synchronize()
+    w_da = float(((da1.double() - ref_da).abs() / bound).max())
+    w_xa = float(((xa1.double() - ref_xa).abs() / (1e-5 * (xd.abs() @ a.abs()) + 1e-12)).max())
+    print(f"[full lora] one pass: dA worst error / bound {w_da:.3f}, xA {w_xa:.3f}", flush=True)
+    assert w_da <= 1.0 and w_xa <= 1.0
 
 
 def _prev_bf16(v: float) -> float:
