@@ -129,24 +129,42 @@ __device__ __forceinline__ void st16_stream(void* p, u32x4 v) {
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
 
+// A pointer the caller knows to be wave-uniform, in scalar registers: a buffer resource built from
+// a base the compiler cannot prove uniform is wrapped in a waterfall loop (one pass per distinct
+// value, with compares and exec-mask updates around every buffer access).
+template <class T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
+
+// Raw buffer resource over the `len`-byte region at `base`, both wave-uniform by the caller's
+// contract; they are moved to scalar registers so the compiler emits no waterfall loop.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(void* base, uint32_t len) {
+  return __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(base), (short)0,
+                                           (int)__builtin_amdgcn_readfirstlane(len), 0x00020000);
+}
+
 // Predicated 8-byte store without a branch: a raw buffer store over the `len`-byte region at
 // the wave-uniform `base`; lanes with !keep use an offset past the region, which the
 // hardware drops.  (A branch around a store would make the compiler drain every
 // outstanding memory operation at the next use of a load — gfx9 counts loads and stores
 // in one in-order counter.)
 __device__ __forceinline__ void st8_pred(void* base, uint32_t len, uint32_t off, u32x2 v, bool keep) {
-  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)len, 0x00020000);
+  const __amdgpu_buffer_rsrc_t r = uniform_rsrc(base, len);
   __builtin_amdgcn_raw_buffer_store_b64(v, r, keep ? off : 0x7ffffff0u, 0, 0);
 }
 
 // 16-byte form of st8_pred (offset 16-byte aligned within the region).
 __device__ __forceinline__ void st16_pred(void* base, uint32_t len, uint32_t off, u32x4 v, bool keep) {
-  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)len, 0x00020000);
+  const __amdgpu_buffer_rsrc_t r = uniform_rsrc(base, len);
   __builtin_amdgcn_raw_buffer_store_b128(v, r, keep ? off : 0x7ffffff0u, 0, 0);
 }
 // st16_pred as a non-temporal (streaming) store.
 __device__ __forceinline__ void st16_pred_stream(void* base, uint32_t len, uint32_t off, u32x4 v, bool keep) {
-  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)len, 0x00020000);
+  const __amdgpu_buffer_rsrc_t r = uniform_rsrc(base, len);
   __builtin_amdgcn_raw_buffer_store_b128(v, r, keep ? off : 0x7ffffff0u, 0, 2);
 }
 

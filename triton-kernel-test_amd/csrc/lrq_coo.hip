@@ -195,11 +195,11 @@ __global__ __launch_bounds__(kCooThreads) void k_coo_scan(const uint32_t* __rest
 // dropped by the hardware): the entries are written without per-lane branches, so the loads of
 // the next pieces stay in flight.
 __device__ __forceinline__ void st8_region(void* base, uint32_t len, uint32_t off, uint64_t v, bool keep) {
-  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)len, 0x00020000);
+  const __amdgpu_buffer_rsrc_t r = uniform_rsrc(base, len);
   __builtin_amdgcn_raw_buffer_store_b64(u32x2{(uint32_t)v, (uint32_t)(v >> 32)}, r, keep ? off : 0x7ffffff0u, 0, 0);
 }
 __device__ __forceinline__ void st2_region(void* base, uint32_t len, uint32_t off, uint16_t v, bool keep) {
-  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)len, 0x00020000);
+  const __amdgpu_buffer_rsrc_t r = uniform_rsrc(base, len);
   __builtin_amdgcn_raw_buffer_store_b16(v, r, keep ? off : 0x7ffffff0u, 0, 0);
 }
 

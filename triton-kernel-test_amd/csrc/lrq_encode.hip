@@ -308,7 +308,7 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
   auto side_store = [&](int rb, int row) {
     if constexpr (OUTL) {
       const __amdgpu_buffer_rsrc_t rs =
-          __builtin_amdgcn_make_buffer_rsrc(side + (int64_t)rb * 16 * ldside, (short)0, (int)(16 * ldside * 2), 0x00020000);
+          uniform_rsrc(side + (int64_t)rb * 16 * ldside, (uint32_t)(16 * ldside * 2));
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
         const int cb = unit_base(p, ub, N, NP, G);  // the wave's UPW*G contiguous columns of plane p
@@ -1180,7 +1180,7 @@ __global__ __launch_bounds__(512) void k_quant_slab(const uint16_t* __restrict__
   // zero: the columns are then zeroed in the slice (every lane of row j writes the same 0).
   auto side_pass = [&](int rb, int row, bool zero) {
     const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(side + (int64_t)rb * 16 * ldside, (short)0, (int)(16 * ldside * 2), 0x00020000);
+        uniform_rsrc(side + (int64_t)rb * 16 * ldside, (uint32_t)(16 * ldside * 2));
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       const int cb = unit_base(p, ub, N, NP, G);  // the wave's UPW*G contiguous columns of plane p
