@@ -169,12 +169,23 @@ __device__ __forceinline__ void coo_bounds(const LegacyArgs& a, int64_t bm, int 
   }
 }
 
+// Entries each lane requests per piece and pass (4 lanes per row: 4 * KL entries of a piece per pass).
+#ifndef LRQ_COO_KL
+#define LRQ_COO_KL 2
+#endif
+// bf16 of padding after each row of the COO tile: rows 16 bytes apart in the LDS banks, so the
+// 16-byte accesses of 8 consecutive lanes (8 rows) fall in distinct banks.
+#ifndef LRQ_COO_PAD
+#define LRQ_COO_PAD 8
+#endif
+template <int NP>
+constexpr int coo_row_stride() { return NP * 64 + LRQ_COO_PAD; }
 template <int NP, int KL>
 __device__ __forceinline__ void coo_tile(const LegacyArgs& a, int64_t (&s0)[NP], int64_t (&s1)[NP], int u, int N,
                                          int j, int g, uint16_t* __restrict__ ot) {
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
-    uint16_t* r = ot + (j * NP + p) * 64 + 16 * g;
+    uint16_t* r = ot + j * coo_row_stride<NP>() + p * 64 + 16 * g;
     st16(r, u32x4{0u, 0u, 0u, 0u});
     st16(r + 8, u32x4{0u, 0u, 0u, 0u});
     s0[p] = max(s0[p], (int64_t)0);
@@ -201,7 +212,7 @@ __device__ __forceinline__ void coo_tile(const LegacyArgs& a, int64_t (&s0)[NP],
       for (int i = 0; i < KL; ++i) {
         const int64_t k = s0[p] + (int64_t)(4 * KL * pass + g + 4 * i);
         const int64_t d = (int64_t)cv[p][i] - base;
-        if (k < s1[p] && d >= 0 && d < 64) ot[(j * NP + p) * 64 + (int)d] = vv[p][i];
+        if (k < s1[p] && d >= 0 && d < 64) ot[j * coo_row_stride<NP>() + p * 64 + (int)d] = vv[p][i];
       }
       more |= s1[p] - s0[p] > (int64_t)4 * KL * (pass + 1);
     }
@@ -210,8 +221,23 @@ __device__ __forceinline__ void coo_tile(const LegacyArgs& a, int64_t (&s0)[NP],
 }
 
 // ------------------------------------------------------------------ MFMA path
-// Grid: (ceil(M / (64 * rb)), N / (64 * NP), B); 4 waves; wave w walks row blocks
-// (blockIdx.x * rb + i) * 64 + w * 16, i < rb, of unit blockIdx.y.  OSRC, decode: outliers
+// Workgroup i of a launch runs on XCD i % 8 (round-robin dispatch); the tiles are renumbered so
+// that each XCD walks one contiguous range of tiles, in tile order.  With units fastest, the
+// workgroups of one XCD that run together cover neighbouring units of the same rows, which share
+// L2 lines of the COO entries (a piece's entries do not start on a line boundary), of the code
+// rows and of the output rows.
+#ifndef LRQ_LEG_XCD
+#define LRQ_LEG_XCD 1
+#endif
+__device__ __forceinline__ int legacy_tile(int i, int n) {
+  if (!LRQ_LEG_XCD) return i;
+  const int per = n / 8, rem = n % 8, x = i % 8, k = i / 8;
+  return x < rem ? x * (per + 1) + k : rem * (per + 1) + (x - rem) * per + k;
+}
+
+// Grid: ceil(M / (64 * rb)) * (N / (64 * NP)) * B workgroups (one dimension); 4 waves; the
+// workgroup's tile (b, bx, u) comes from legacy_tile; wave w walks row blocks
+// (bx * rb + i) * 64 + w * 16, i < rb, of unit u.  OSRC, decode: outliers
 // absent (0), dense (1) or COO pieces (2: looked up per lane, for sparse outliers; 3: gathered
 // per wave into an LDS tile, for denser ones); encode: 1 also writes each 64-column piece's
 // outlier count (a.pcnt), the compaction's first pass.
@@ -220,7 +246,7 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
   constexpr int NP = (MODE == kAdd || MODE == kHist) ? 1 : 8 / BITS, G = 64, E = 16, RT = K / 16;
   __shared__ uint32_t lh[MODE == kHist ? 256 : 1];
   // decode from denser COO outliers: each wave's outlier tile (16 rows x NP planes x 64 columns, bf16)
-  __shared__ __attribute__((aligned(16))) uint16_t otile[(MODE == kDecode && OSRC == 3) ? 4 * 16 * NP * 64 : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t otile[(MODE == kDecode && OSRC == 3) ? 4 * 16 * coo_row_stride<NP>() : 8];
   int64_t sel = -1;
   if constexpr (MODE == kHist) {
     lh[threadIdx.x] = 0u;
@@ -230,8 +256,13 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
   constexpr uint32_t kMask = BITS == 8 ? 0xffu : (1u << BITS) - 1u;
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int j = lane & 15, g = lane >> 4;
-  const int u = blockIdx.y, b = blockIdx.z;
   const int M = (int)a.M, N = (int)a.N;
+  // tile t = (batch, 64-row chunk, unit), units fastest; see legacy_tile
+  const int nu = N / NP / G, gx = (M + 64 * a.rb - 1) / (64 * a.rb);
+  const int t = __builtin_amdgcn_readfirstlane(legacy_tile(blockIdx.x, gridDim.x));
+  const int u = __builtin_amdgcn_readfirstlane(t % nu);
+  const int bx = __builtin_amdgcn_readfirstlane((t / nu) % gx);
+  const int b = __builtin_amdgcn_readfirstlane(t / (nu * gx));
   const int64_t NB = N / NP;  // bytes per code row
   const uint16_t* srow = a.s + (a.s_rows == 1 ? 0 : (int64_t)b * N);
 
@@ -240,20 +271,25 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
   for (int p = 0; p < NP; ++p) load_vops<G, K>(a.rt, unit_base(p, u, N, NP, G), j, g, vop[p]);
   const float zero[E] = {};
 
-  // encode: the unit's scales and their reciprocals (one IEEE division per column) in LDS, for
-  // every row of the workgroup; rc_ok: every scale is one legacy_code_rc serves exactly
-  __shared__ __attribute__((aligned(16))) float stab[MODE == kEncode ? 2 * NP * G : 4];
+  // the unit's scales in LDS for every row block of the workgroup (the same columns throughout),
+  // and for the encode their reciprocals (one IEEE division per column); rc_ok: every scale is
+  // one legacy_code_rc serves exactly
+  constexpr bool kScales = MODE != kAdd && MODE != kHist;
+  __shared__ __attribute__((aligned(16))) float stab[MODE == kEncode ? 2 * NP * G : (kScales ? NP * G : 4)];
   bool rc_ok = false;
-  if constexpr (MODE == kEncode) {
+  if constexpr (kScales) {
     int ok = 1;
     for (int i = threadIdx.x; i < NP * G; i += 256) {
       const int p = i / G, c = i % G;
       const float sv = bf_lo(srow[unit_base(p, u, N, NP, G) + c]);
       stab[i] = sv;
-      stab[NP * G + i] = 1.0f / sv;
-      ok &= rc_scale_ok(sv) ? 1 : 0;
+      if constexpr (MODE == kEncode) {
+        stab[NP * G + i] = 1.0f / sv;
+        ok &= rc_scale_ok(sv) ? 1 : 0;
+      }
     }
-    rc_ok = __syncthreads_and(ok) != 0;
+    if constexpr (MODE == kEncode) rc_ok = __syncthreads_and(ok) != 0;
+    else __syncthreads();
   }
 
   // decode from the COO tile: the next row block's L operand, codes and COO piece bounds are
@@ -266,7 +302,7 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
   u32x4 nq = u32x4{0u, 0u, 0u, 0u};
   int64_t ns0[NPB], ns1[NPB];
   auto fetch_next = [&](int i) {  // block i of the workgroup (rows clamped to the last)
-    const int64_t rn = min((blockIdx.x * a.rb + i) * 64 + w * 16 + j, M - 1);
+    const int64_t rn = min((bx * a.rb + i) * 64 + w * 16 + j, M - 1);
 #pragma unroll
     for (int t = 0; t < RT; ++t) nl[t] = ld8(a.l + rn * K + 16 * t + 4 * g);
     nq = ld16(a.qin + ((int64_t)b * M + rn) * NB + u * G + E * g);
@@ -279,7 +315,7 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
   constexpr bool kPreX = MODE == kEncode && NP <= 4;
   u32x4 nx[kPreX ? NP : 1][2];
   auto fetch_x = [&](int i) {
-    const int64_t rn = min((blockIdx.x * a.rb + i) * 64 + w * 16 + j, M - 1);
+    const int64_t rn = min((bx * a.rb + i) * 64 + w * 16 + j, M - 1);
 #pragma unroll
     for (int t = 0; t < RT; ++t) nl[t] = ld8(a.l + rn * K + 16 * t + 4 * g);
 #pragma unroll
@@ -292,7 +328,7 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
   if constexpr (kPreX) fetch_x(0);
 
   for (int i = 0; i < a.rb; ++i) {
-    const int row0 = (blockIdx.x * a.rb + i) * 64 + w * 16;  // wave-uniform: a scalar exit
+    const int row0 = (bx * a.rb + i) * 64 + w * 16;  // wave-uniform: a scalar exit
     if (row0 >= M) break;  // whole 16-row block past the end
     const int row = row0 + j;
     const int64_t rr = min(row, M - 1);
@@ -330,8 +366,8 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
     uint32_t byte[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) byte[e] = 0u;
-    uint16_t* ot = otile + (size_t)w * 16 * NP * 64;
-    if constexpr (MODE == kDecode && OSRC == 3) coo_tile<NP, 2>(a, s0, s1, u, N, j, g, ot);
+    uint16_t* ot = otile + (size_t)w * 16 * coo_row_stride<NP>();
+    if constexpr (MODE == kDecode && OSRC == 3) coo_tile<NP, LRQ_COO_KL>(a, s0, s1, u, N, j, g, ot);
 
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
@@ -353,9 +389,14 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
             rc[k + e] = w[e];
           }
         }
-      } else if constexpr (MODE != kAdd && MODE != kHist) {
-        unpack8(ld16(srow + c0), sc);
-        unpack8(ld16(srow + c0 + 8), sc + 8);
+      } else if constexpr (kScales) {
+        const float* sp = stab + p * G + E * g;
+#pragma unroll
+        for (int k = 0; k < E; k += 4) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(sp + k);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sc[k + e] = v[e];
+        }
       }
       if constexpr (MODE == kHist) {
         float xv[E];
@@ -429,7 +470,7 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
         }
         if constexpr (MODE == kDecode && OSRC == 2) coo_piece_values<E>(a, (int64_t)b * M + rr, c0, oo);
         if constexpr (MODE == kDecode && OSRC == 3) {
-          const uint16_t* r = ot + (j * NP + p) * 64 + 16 * g;
+          const uint16_t* r = ot + j * coo_row_stride<NP>() + p * 64 + 16 * g;
           unpack8(*reinterpret_cast<const u32x4*>(r), oo);
           unpack8(*reinterpret_cast<const u32x4*>(r + 8), oo + 8);
         }
@@ -592,11 +633,13 @@ template <int MODE, int BITS, int OSRC>
 static int legacy_launch(const LegacyArgs& a, int K, int64_t B, bool mfma_ok, hipStream_t st) {
   constexpr int NP = (MODE == kAdd) ? 1 : 8 / BITS;
   const int64_t NB = a.N / NP;
-  if (mfma_ok && NB % 64 == 0 && NB / 64 <= 65535 && B <= 65535) {
+  const int rb = legacy_rows_per_wg(a.M, NB / 64 * B);
+  const int64_t nwg = (a.M + 64 * rb - 1) / (64 * rb) * (NB / 64) * B;
+  if (mfma_ok && NB % 64 == 0 && nwg <= INT32_MAX) {
     // 4 row blocks per workgroup, fewer where that would leave under two workgroups per CU
     LegacyArgs la = a;
-    la.rb = legacy_rows_per_wg(a.M, NB / 64 * B);
-    dim3 grid((unsigned)((a.M + 64 * la.rb - 1) / (64 * la.rb)), (unsigned)(NB / 64), (unsigned)B);
+    la.rb = rb;
+    const dim3 grid((unsigned)nwg);
     if (K == 16) LRQ_TRY(launch((k_legacy_mfma<MODE, BITS, 16, OSRC>), grid, dim3(256), 0, st, la));
     else LRQ_TRY(launch((k_legacy_mfma<MODE, BITS, 32, OSRC>), grid, dim3(256), 0, st, la));
   } else {
@@ -786,12 +829,12 @@ extern "C" int lrq_legacy_kth_residual(const void* l, const void* rt, int32_t K,
   LegacyArgs a{};
   a.l = (const uint16_t*)l, a.rt = (const uint16_t*)rt, a.x = (const uint16_t*)x, a.ldx_b = 0, a.ldx_m = ldx_m;
   a.M = M, a.N = N, a.hist = hist, a.sel = sel;
-  const bool mfma_ok = vec_ok({l, rt, x}) && ldx_m % 8 == 0 && N % 64 == 0 && N / 64 <= 65535;
+  const bool mfma_ok = vec_ok({l, rt, x}) && ldx_m % 8 == 0 && N % 64 == 0;
   LRQ_TRY(launch(k_kth_init, dim3(1), dim3(256), 0, hs, hist, sel, k));
   for (int fine = 0; fine < 2; ++fine) {
     if (mfma_ok) {
       a.rb = legacy_rows_per_wg(M, N / 64);
-      dim3 grid((unsigned)((M + 64 * a.rb - 1) / (64 * a.rb)), (unsigned)(N / 64), 1u);
+      const dim3 grid((unsigned)((M + 64 * a.rb - 1) / (64 * a.rb) * (N / 64)));  // < 2^26 (M * N < 2^32)
       if (K == 16) LRQ_TRY(launch((k_legacy_mfma<kHist, 8, 16, 0>), grid, dim3(256), 0, hs, a));
       else LRQ_TRY(launch((k_legacy_mfma<kHist, 8, 32, 0>), grid, dim3(256), 0, hs, a));
     } else {
