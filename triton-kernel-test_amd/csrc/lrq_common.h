@@ -140,6 +140,15 @@ __device__ __forceinline__ T* uniform_ptr(T* p) {
   return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
 }
 
+// XCD-aware tile order: workgroup i of an n-workgroup launch runs on XCD i % 8 (round-robin
+// dispatch).  The returned tile index gives each XCD one contiguous range of tiles, walked in
+// order, so workgroups that run together on one XCD (one L2) take neighbouring tiles.  A bijection
+// of [0, n).
+__device__ __forceinline__ int xcd_tile(int i, int n) {
+  const int per = n / 8, rem = n % 8, x = i % 8, k = i / 8;
+  return x < rem ? x * (per + 1) + k : rem * (per + 1) + (x - rem) * per + k;
+}
+
 // Raw buffer resource over the `len`-byte region at `base`, both wave-uniform by the caller's
 // contract; they are moved to scalar registers so the compiler emits no waterfall loop.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(void* base, uint32_t len) {

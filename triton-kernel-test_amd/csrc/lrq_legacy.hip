@@ -221,23 +221,11 @@ __device__ __forceinline__ void coo_tile(const LegacyArgs& a, int64_t (&s0)[NP],
 }
 
 // ------------------------------------------------------------------ MFMA path
-// Workgroup i of a launch runs on XCD i % 8 (round-robin dispatch); the tiles are renumbered so
-// that each XCD walks one contiguous range of tiles, in tile order.  With units fastest, the
-// workgroups of one XCD that run together cover neighbouring units of the same rows, which share
-// L2 lines of the COO entries (a piece's entries do not start on a line boundary), of the code
-// rows and of the output rows.
-#ifndef LRQ_LEG_XCD
-#define LRQ_LEG_XCD 1
-#endif
-__device__ __forceinline__ int legacy_tile(int i, int n) {
-  if (!LRQ_LEG_XCD) return i;
-  const int per = n / 8, rem = n % 8, x = i % 8, k = i / 8;
-  return x < rem ? x * (per + 1) + k : rem * (per + 1) + (x - rem) * per + k;
-}
-
 // Grid: ceil(M / (64 * rb)) * (N / (64 * NP)) * B workgroups (one dimension); 4 waves; the
-// workgroup's tile (b, bx, u) comes from legacy_tile; wave w walks row blocks
-// (bx * rb + i) * 64 + w * 16, i < rb, of unit u.  OSRC, decode: outliers
+// workgroup's tile t = (b, bx, u), units fastest, is xcd_tile of its index: the workgroups of one
+// XCD that run together cover neighbouring units of the same rows, which share L2 lines of the COO
+// entries (a piece's entries do not start on a line boundary), of the code rows and of the output
+// rows.  Wave w walks row blocks (bx * rb + i) * 64 + w * 16, i < rb, of unit u.  OSRC, decode: outliers
 // absent (0), dense (1) or COO pieces (2: looked up per lane, for sparse outliers; 3: gathered
 // per wave into an LDS tile, for denser ones); encode: 1 also writes each 64-column piece's
 // outlier count (a.pcnt), the compaction's first pass.
@@ -257,9 +245,9 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int j = lane & 15, g = lane >> 4;
   const int M = (int)a.M, N = (int)a.N;
-  // tile t = (batch, 64-row chunk, unit), units fastest; see legacy_tile
+  // tile t = (batch, 64-row chunk, unit), units fastest
   const int nu = N / NP / G, gx = (M + 64 * a.rb - 1) / (64 * a.rb);
-  const int t = __builtin_amdgcn_readfirstlane(legacy_tile(blockIdx.x, gridDim.x));
+  const int t = __builtin_amdgcn_readfirstlane(xcd_tile(blockIdx.x, gridDim.x));
   const int u = __builtin_amdgcn_readfirstlane(t % nu);
   const int bx = __builtin_amdgcn_readfirstlane((t / nu) % gx);
   const int b = __builtin_amdgcn_readfirstlane(t / (nu * gx));

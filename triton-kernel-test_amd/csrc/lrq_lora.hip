@@ -43,8 +43,10 @@ __global__ __launch_bounds__(512) void k_lora_grads(
   const int wc = w & 3, wr = w >> 2;
   // (the divisions run on the vector unit: readfirstlane brings the uniform results back to
   // scalar registers, so that all block addressing below stays scalar)
-  const int cgi = __builtin_amdgcn_readfirstlane((int)blockIdx.x % ncg);
-  const int rgi = __builtin_amdgcn_readfirstlane((int)blockIdx.x / ncg);
+  // the column groups of one row group on one XCD: they read the same L and g rows
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int cgi = __builtin_amdgcn_readfirstlane(tile % ncg);
+  const int rgi = __builtin_amdgcn_readfirstlane(tile / ncg);
   const int nrb = (M + 15) / 16;
   const int rb_lo = rgi * bpg, rb_hi = min(rb_lo + bpg, nrb);  // the host gives every row group a block
   const int u = __builtin_amdgcn_readfirstlane(cgi * Ge::UPW + wc);
