@@ -26,13 +26,14 @@ __global__ __launch_bounds__(256) void k_transpose_bf16(const uint16_t* __restri
 
 // colmax[c] = max |x[r, c]| via an unsigned max on the fp32 bit pattern (valid for
 // non-negative floats).  colmax must be zeroed first (done by the host entry).
-// Grid: (ceil(cols / 512), row groups of rows_per rows); 256 threads = 4 row phases x 64
-// column lanes of 8 adjacent columns (one 16-byte load per row: a wave reads 1 KB of a row),
-// 16 loads in flight per thread.  The 4 phases meet in LDS, so each workgroup issues one
-// atomic per column (few row groups keep the atomics per address low).
-__global__ __launch_bounds__(256) void k_colmax(const uint16_t* __restrict__ x, int64_t ldx, int64_t rows,
-                                                int64_t cols, int64_t rows_per, unsigned int* __restrict__ colmax) {
-  __shared__ float red[3][64][8];
+// Grid: (ceil(cols / 512), row groups of rows_per rows); PH waves = PH row phases x 64 column
+// lanes of 8 adjacent columns (one 16-byte load per row: a wave reads 1 KB of a row), 16 loads
+// in flight per thread.  The PH phases meet in LDS, so each workgroup issues one atomic per
+// column (few row groups keep the atomics per address low).
+template <int PH>
+__global__ __launch_bounds__(PH * 64) void k_colmax(const uint16_t* __restrict__ x, int64_t ldx, int64_t rows,
+                                                     int64_t cols, int64_t rows_per, unsigned int* __restrict__ colmax) {
+  __shared__ float red[PH - 1][64][8];
   // the row phase is wave-uniform (readfirstlane), so the batch loop's branches are scalar: a
   // load under a per-lane branch would make the compiler wait for it at the join, and nothing
   // would overlap.  Lanes past the last column read the last 8 columns and store nothing.
@@ -47,12 +48,12 @@ __global__ __launch_bounds__(256) void k_colmax(const uint16_t* __restrict__ x, 
   {
     const uint16_t* p = x + (live ? c : cols - 8);
     int64_t r = r0 + ph;
-    // batches of kB rows (r, r+4, ..., r+4(kB-1)), the next batch in flight while one is reduced
+    // batches of kB rows (r, r+PH, ..., r+PH(kB-1)), the next batch in flight while one is reduced
     constexpr int kB = 16;
     u32x4 v[kB];
     auto issue = [&](int64_t rr) {
 #pragma unroll
-      for (int i = 0; i < kB; ++i) v[i] = ld16_stream(p + (rr + 4 * i) * ldx);
+      for (int i = 0; i < kB; ++i) v[i] = ld16_stream(p + (rr + PH * i) * ldx);
     };
     auto reduce = [&](const u32x4 (&b)[kB]) {
 #pragma unroll
@@ -63,11 +64,12 @@ __global__ __launch_bounds__(256) void k_colmax(const uint16_t* __restrict__ x, 
         for (int e = 0; e < 8; ++e) m[e] = fmaxf(m[e], fabsf(f[e]));
       }
     };
-    // full batches (r + 4(kB-1) < r1); the loop issues the next batch unconditionally, so the
+    // full batches (r + PH(kB-1) < r1); the loop issues the next batch unconditionally, so the
     // wait for a batch leaves the next one in flight (a conditional issue would make the
     // compiler wait for both at the join)
-    constexpr int kSpan = 4 * kB;
-    const int nbat = __builtin_amdgcn_readfirstlane(r + kSpan - 4 < r1 ? (int)((r1 - r - kSpan + 3) / kSpan) + 1 : 0);
+    constexpr int kSpan = PH * kB;
+    const int nbat =
+        __builtin_amdgcn_readfirstlane(r + kSpan - PH < r1 ? (int)((r1 - r - kSpan + PH - 1) / kSpan) + 1 : 0);
     if (nbat > 0) {
       issue(r);
       for (int bi = 0; bi + 1 < nbat; ++bi) {
@@ -81,7 +83,7 @@ __global__ __launch_bounds__(256) void k_colmax(const uint16_t* __restrict__ x, 
       reduce(v);
       r += kSpan;
     }
-    for (; r < r1; r += 4) {
+    for (; r < r1; r += PH) {
       float f[8];
       unpack8(ld16_stream(p + r * ldx), f);
 #pragma unroll
@@ -96,7 +98,9 @@ __global__ __launch_bounds__(256) void k_colmax(const uint16_t* __restrict__ x, 
   if (ph == 0 && live) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float a = fmaxf(fmaxf(m[e], red[0][cl][e]), fmaxf(red[1][cl][e], red[2][cl][e]));
+      float a = m[e];
+#pragma unroll
+      for (int q = 0; q < PH - 1; ++q) a = fmaxf(a, red[q][cl][e]);
       atomicMax(colmax + c + e, __float_as_uint(a));
     }
   }
@@ -259,6 +263,14 @@ extern "C" int lrq_transpose_bf16(const void* src, int64_t rows, int64_t cols, v
   return LRQ_OK;
 }
 
+// k_colmax launch shape: one workgroup of 8 waves per CU (c3 shape, colmax entry: 36.1 us;
+// 4 waves x 4 per CU 39.3, 8 x 2 40.0, 16 x 1 39.5, 16 x 2 37.6)
+#ifndef LRQ_COLMAX_PH
+#define LRQ_COLMAX_PH 8
+#endif
+#ifndef LRQ_COLMAX_WPC
+#define LRQ_COLMAX_WPC 1
+#endif
 extern "C" int lrq_colmax(const void* x, int64_t ldx, int64_t rows, int64_t hidden, float* colmax,
                           void* stream) {
   if (x == nullptr || colmax == nullptr) return LRQ_ERR_NULL;
@@ -269,15 +281,16 @@ extern "C" int lrq_colmax(const void* x, int64_t ldx, int64_t rows, int64_t hidd
                      (unsigned int*)colmax, hidden));
   if (rows == 0) return LRQ_OK;
   if ((hidden % 8) == 0 && (ldx % 8) == 0 && aligned(x, 16)) {
-    // about four workgroups per CU (two measured slower, eight slower still: one atomic per
-    // column per workgroup), row groups of whole 64-row steps (4 phases x 16-row batches)
+    // about LRQ_COLMAX_WPC workgroups of LRQ_COLMAX_PH waves per CU (one atomic per column per
+    // workgroup), row groups of whole PH * 16-row steps (PH phases x 16-row batches)
+    constexpr int PH = LRQ_COLMAX_PH;
     const int64_t cgroups = (hidden + 511) / 512;
-    int64_t groups = std::max<int64_t>(1, (int64_t)cu_count() * 4 / cgroups);
+    int64_t groups = std::max<int64_t>(1, (int64_t)cu_count() * LRQ_COLMAX_WPC / cgroups);
     int64_t rows_per = (rows + groups - 1) / groups;
-    rows_per = (rows_per + 63) / 64 * 64;
+    rows_per = (rows_per + 16 * PH - 1) / (16 * PH) * (16 * PH);
     groups = (rows + rows_per - 1) / rows_per;
-    LRQ_TRY(launch(k_colmax, dim3((unsigned)cgroups, (unsigned)groups), dim3(256), 0, s, (const uint16_t*)x, ldx,
-                       rows, hidden, rows_per, (unsigned int*)colmax));
+    LRQ_TRY(launch(k_colmax<PH>, dim3((unsigned)cgroups, (unsigned)groups), dim3(PH * 64), 0, s, (const uint16_t*)x,
+                   ldx, rows, hidden, rows_per, (unsigned int*)colmax));
   } else {
     dim3 grid((unsigned)((hidden / 2 + 255) / 256), (unsigned)((rows + 63) / 64));
     LRQ_TRY(launch(k_colmax2, grid, dim3(256), 0, s, (const uint16_t*)x, ldx, rows, hidden,
