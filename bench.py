@@ -7,14 +7,15 @@ rotate over several HBM-resident buffer sets (> 512 MB of X) so the 256 MB MALL 
 serve them.  Prints ONE JSON line (driver contract).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
-                  [--config north_star|c1|c2|c3|c4|c5|c5w|lora|legacy|ref_enc|ref_dec] [--m M]
+                  [--config north_star|c1|c2|c3|c4|c5|c5w|lora|legacy|ref_enc|ref_dec|ref_mm] [--m M]
                   [--no-cpu-baseline]
 
 value       = activation GB/s = 2*rows*hidden bytes / (encode + decode time per step);
               fused-consumer configs: / (consumer time); lora: / (x A + x^T g time);
               legacy: / (encode with its outlier compaction + decode time); ref_enc / ref_dec
               (the reference's own speed tests, x [4, M, M]): / (1-bit encode + compaction) and
-              / (2-bit decode from COO)
+              / (2-bit decode from COO); ref_mm (the reference's fused dequant-matmul bench,
+              x [4, M, M] @ y [4, M, 32]): / (the fused legacy dequant-GEMM)
 timing      = exactly --warmup untimed steps, then exactly --steps timed steps between two HIP
               events on the launch stream (synchronised before and after); `settled` repeats
               the timed steps after --settle-seconds of sustained work, as a separate field
@@ -47,6 +48,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 BF16_DENSE_TFLOPS = 2500.0
+MM_COLS = 32  # ref_mm: columns of y (the reference bench's R = 32, extraction_fuse_matmul.py:427)
 METRIC = "encode+decode activation GB/s and % of HBM peak (bf16 4096-hidden, rank-16 int4)"
 
 
@@ -59,7 +61,7 @@ def parse():
     # reported as `settled` (the GPU's clocks settle over about a second of sustained work)
     ap.add_argument("--settle-seconds", type=float, default=2.0)
     ap.add_argument("--config", default="north_star")
-    ap.add_argument("--m", type=int, default=0, help="ref_enc / ref_dec: M of x [4, M, M] (the reference's sweep)")
+    ap.add_argument("--m", type=int, default=0, help="ref_enc / ref_dec / ref_mm: M of x [4, M, M] (the reference's sweep)")
     ap.add_argument("--nbuf", type=int, default=4)
     ap.add_argument("--cold-steps", type=int, default=20, help="timed launches of the last kernel with HBM-cold inputs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -122,11 +124,14 @@ def cpu_baseline(cfg, seconds: float):
     V = pkg.inputs.basis(cfg.hidden, cfg.rank, cfg.seed) if cfg.rank else None
 
     def prepare(r):
-        if cfg.consumer in ("ref_enc", "ref_dec"):
+        if cfg.consumer in ("ref_enc", "ref_dec", "ref_mm"):
             ops = pkg.inputs.ref_operands(cfg)
             g = torch.Generator().manual_seed(cfg.seed)
             d = dict(l=ops["l"][:r], r=ops["r"], s=ops["s"][:1])
-            if cfg.consumer == "ref_enc":
+            if cfg.consumer == "ref_mm":
+                d["q"] = torch.randint(0, 256, (1, r, cfg.hidden * cfg.bits // 8), generator=g, dtype=torch.uint8)
+                d["y"] = torch.randn((1, cfg.hidden, MM_COLS), generator=g).to(torch.bfloat16)
+            elif cfg.consumer == "ref_enc":
                 d["x"] = torch.randn((1, r, cfg.hidden), generator=g).to(torch.bfloat16)
             else:
                 d["q"] = torch.randint(0, 256, (1, r, cfg.hidden * cfg.bits // 8), generator=g, dtype=torch.uint8)
@@ -153,6 +158,9 @@ def cpu_baseline(cfg, seconds: float):
             T.to_coo(o)
         elif cfg.consumer == "ref_dec":
             T.legacy_decode(inp["l"], inp["r"], inp["q"], inp["o"].to_dense(), inp["s"], cfg.bits)
+        elif cfg.consumer == "ref_mm":
+            xh = T.legacy_decode(inp["l"], inp["r"], inp["q"], None, inp["s"], cfg.bits)
+            torch.matmul(xh.float(), inp["y"].float()).to(torch.bfloat16)
         elif cfg.consumer == "legacy":
             o, q = T.legacy_encode(inp["l"], inp["r"], inp["x"], inp["s"], cfg.bits, inp["tau"])
             o = T.to_coo(o)
@@ -170,7 +178,7 @@ def cpu_baseline(cfg, seconds: float):
                 {"silu": T.silu_bwd, "gelu": T.gelu_bwd, "softmax": T.softmax_bwd}[cfg.consumer](xh, inp["dy"])
         return time.perf_counter() - t0
 
-    limit = cfg.hidden if cfg.consumer in ("ref_enc", "ref_dec") else cfg.rows  # (one batch of x [B, M, M])
+    limit = cfg.hidden if cfg.consumer in ("ref_enc", "ref_dec", "ref_mm") else cfg.rows  # (one batch of x [B, M, M])
     rows = min(limit, 256)
     inp = prepare(rows)
     t = run(inp)
@@ -188,7 +196,8 @@ def cpu_baseline(cfg, seconds: float):
     what = {"decode": "encode+decode", "lora": "decode + x A + x^T g (LoRA factor gradients)",
             "legacy": "reference torch encode + to_sparse + decode",
             "ref_enc": "reference torch encode + to_sparse (one batch's rows of x [B, M, M])",
-            "ref_dec": "reference to_dense + torch decode (one batch's rows of x [B, M, M])"}.get(
+            "ref_dec": "reference to_dense + torch decode (one batch's rows of x [B, M, M])",
+            "ref_mm": "reference torch decode + matmul with y [M, 32] (one batch's rows of x [B, M, M])"}.get(
                 cfg.consumer, f"decode+{cfg.consumer} backward")
     return {"value": round(gbs, 4), "unit": "GB/s", "cores": cores, "kind": "port",
             "sample": f"PyTorch-eager fp32 {what} (oracle/lrq_torch.py) of {rows} of {cfg.rows} rows x {cfg.hidden} "
@@ -288,12 +297,19 @@ def build_plan_ref(cfg, pkg, lib, dev, nbuf):
     for i in range(nbuf):
         g = torch.Generator(device=dev)
         g.manual_seed(cfg.seed + 101 * i)
-        st = dict(idx=torch.empty((3, cap), dtype=torch.int64, device=dev),
-                  vals=torch.empty((cap,), dtype=torch.bfloat16, device=dev),
-                  nnz=torch.empty((1,), dtype=torch.int64, device=dev),
-                  ptr=torch.empty((B * M * npc + 1,), dtype=torch.int64, device=dev),
-                  ws=torch.empty(((wsb + 7) // 8,), dtype=torch.int64, device=dev))
-        if cfg.consumer == "ref_enc":
+        if cfg.consumer == "ref_mm":  # no outliers: no COO buffers
+            st = dict(nnz=torch.zeros((1,), dtype=torch.int64, device=dev))
+        else:
+            st = dict(idx=torch.empty((3, cap), dtype=torch.int64, device=dev),
+                      vals=torch.empty((cap,), dtype=torch.bfloat16, device=dev),
+                      nnz=torch.empty((1,), dtype=torch.int64, device=dev),
+                      ptr=torch.empty((B * M * npc + 1,), dtype=torch.int64, device=dev),
+                      ws=torch.empty(((wsb + 7) // 8,), dtype=torch.int64, device=dev))
+        if cfg.consumer == "ref_mm":
+            st["q"] = torch.randint(0, 256, (B, M, N * bits // 8), generator=g, device=dev, dtype=torch.uint8)
+            st["y"] = torch.randn((B, N, MM_COLS), generator=g, device=dev).to(torch.bfloat16)
+            st["out"] = torch.empty((B, M, MM_COLS), dtype=torch.bfloat16, device=dev)
+        elif cfg.consumer == "ref_enc":
             st["x"] = torch.randn((B, M, N), generator=g, device=dev).to(torch.bfloat16)
             st["o"] = torch.empty_like(st["x"])
             st["q"] = torch.empty((B, M, N * bits // 8), dtype=torch.uint8, device=dev)
@@ -325,7 +341,14 @@ def build_plan_ref(cfg, pkg, lib, dev, nbuf):
         raise RuntimeError(f"{nnz} outliers exceed the bench capacity {cap}")
     small = 2 * (M * K + N * K) + 2 * B * N
     E = B * M * N
-    if cfg.consumer == "ref_enc":
+    if cfg.consumer == "ref_mm":
+        # algorithmic: the codes, l, r, s and y read once, out written once (x_hat never stored)
+        mm = lambda k: lib.lrq_legacy_dequant_gemm(P(l), P(rt), K, P(sets[k]["q"]), P(s), B, B, M, N, bits,  # noqa: E731
+                                                   P(sets[k]["y"]), MM_COLS, MM_COLS, P(sets[k]["out"]), MM_COLS, sp)
+        mm_b = E * bits / 8 + small + 2 * B * N * MM_COLS + 2 * B * M * MM_COLS
+        entries = [("legacy_gemm", mm, mm_b, 2 * E * K + 2 * E * MM_COLS)]
+        timed = ["legacy_gemm"]
+    elif cfg.consumer == "ref_enc":
         enc_b, cmp_b = E * (2 + bits / 8 + 2) + small, E * 2 + nnz * 26 + B * M * npc * 8
         entries = [("encode_coo", enc, enc_b + cmp_b, 2 * E * K)]
         timed = ["encode_coo"]
@@ -344,7 +367,7 @@ def build_plan(cfg, pkg, lib, dev, nbuf, lora_split=False):
     import torch
     if cfg.consumer == "legacy":
         return build_plan_legacy(cfg, pkg, lib, dev, nbuf)
-    if cfg.consumer in ("ref_enc", "ref_dec"):
+    if cfg.consumer in ("ref_enc", "ref_dec", "ref_mm"):
         return build_plan_ref(cfg, pkg, lib, dev, nbuf)
     c_void_p = ctypes.c_void_p
     sp = c_void_p(torch.cuda.current_stream(dev).cuda_stream)
@@ -462,7 +485,7 @@ def main():
     lib_mod = import_module("triton-kernel-test_amd._lib")
     lib = lib_mod.load()
     cfg = pkg.inputs.CONFIGS[args.config]
-    if args.m and cfg.consumer in ("ref_enc", "ref_dec"):
+    if args.m and cfg.consumer in ("ref_enc", "ref_dec", "ref_mm"):
         import dataclasses
         cfg = dataclasses.replace(cfg, rows=cfg.batch * args.m, hidden=args.m)
     dev = torch.device("cuda", 0)
@@ -608,6 +631,9 @@ def main():
         elif cfg.consumer == "ref_dec":
             workload = (f"reference speed test, x [{cfg.batch}, {cfg.hidden}, {cfg.hidden}]: {cfg.bits}-bit decode "
                         f"from COO outliers N(0,1) * (o > 1)")
+        elif cfg.consumer == "ref_mm":
+            workload = (f"reference dequant-matmul bench, x [{cfg.batch}, {cfg.hidden}, {cfg.hidden}] {cfg.bits}-bit "
+                        f"rank {cfg.rank} @ y [{cfg.batch}, {cfg.hidden}, {MM_COLS}], one fused kernel")
     dom_name, dom_alg, dom_us = None, 0, -1.0
     for name, _, alg, _ in entries:
         if kernels[name]["mean_us"] > dom_us:
@@ -651,7 +677,7 @@ def main():
     if cfg.consumer == "legacy":
         line["legacy"] = {"outliers": _sets[0]["nnz_count"], "threshold": _sets[0]["tau"],
                           "torch_to_sparse_us": round(_sets[0]["torch_to_sparse_us"], 1)}
-    if cfg.consumer in ("ref_enc", "ref_dec"):
+    if cfg.consumer in ("ref_enc", "ref_dec", "ref_mm"):
         line["legacy"] = {"outliers": _sets[0]["nnz_count"], "threshold": _sets[0]["tau"], "batch": cfg.batch,
                           "M": cfg.hidden}
     if "alg_split" in _sets[0]:

@@ -30,7 +30,9 @@
  *                                         i*hidden/NP + u*group .. + group - 1 (the groups
  *                                         whose codes share bytes u*group .. + group - 1)
  *     side    fp16  [rows, n_outlier]     outlier channels kept dense (optional)
- *     idx     int32 [n_outlier]           their column indices, ascending (optional)
+ *     idx     int32 [n_outlier]           their column indices (optional), distinct; an entry
+ *                                         outside [0, hidden) is skipped by every kernel and
+ *                                         its side column is not written
  * where Y = X (or its blockwise 128-point Walsh-Hadamard rotation) and V[hidden, rank] is
  * an orthonormal basis supplied by the caller.
  */
@@ -56,8 +58,9 @@ extern "C" {
  * the unrotated x and rotates it as it reads (int4/g64 and int8/g128, no outlier channels,
  * hidden/NP a multiple of 128, an even number of units per row); for other shapes it returns
  * LRQ_ERR_UNSUPPORTED and the caller rotates x with lrq_wht128 into a buffer, then encodes
- * that with the flag cleared.  lrq_decode undoes the rotation.  The fused consumer entry
- * points refuse the flag (LRQ_ERR_UNSUPPORTED) rather than return unrotated values. */
+ * that with the flag cleared.  lrq_decode and the fused consumers undo the rotation;
+ * lrq_dequant_gemm_t (and its allocation-free form) and lrq_lora_grads refuse the flag
+ * (LRQ_ERR_UNSUPPORTED) rather than return unrotated values. */
 #define LRQ_FLAG_HADAMARD 1
 
 /* Descriptor of one compressed activation.  Encode writes L/codes/scale/zero/side;
@@ -96,6 +99,11 @@ int lrq_encode(const lrq_tensors* t, const void* x, int64_t ldx, void* stream);
  * Replaces low_rank_addition_fuse_decompression_dequantization
  * (low_rank_extraction_fuse_decompression_dequantization.py:116-152, kernel :13-113). */
 int lrq_decode(const lrq_tensors* t, void* out, int64_t ldo, void* stream);
+
+/* The four consumers below may write their output over their second input (dx == dy) except
+ * where they run as a decode followed by a dense pass (the rotated format in shapes without a
+ * fused rotated kernel; outlier channels or the rotated format in lrq_softmax_bwd): there the
+ * aliasing call returns LRQ_ERR_UNSUPPORTED. */
 
 /* dx = dy * s(x)(1 + x(1 - s(x))), s = sigmoid, x = decode(t), fused.
  * Replaces triton_silu_backward_fuse_extraction (extraction_fuse_silu_backward.py:192-216). */
@@ -269,6 +277,15 @@ int lrq_legacy_kth_residual(const void* l, const void* rt, int32_t K, const void
 int lrq_legacy_fused(const void* l, const void* rt, int32_t K, const void* q, const void* s,
                      int64_t s_rows, int64_t B, int64_t M, int64_t N, int32_t bits, int32_t op,
                      const void* y, void* out, void* stream);
+
+/* Fused legacy dequant-GEMM (no outliers): out[b, m, c] = bf16(sum_n x_hat[b, m, n] * y[b, n, c]),
+ * fp32 sums, x_hat the decode's value computed in registers and never stored.  y: bf16
+ * [B, N, ldy] (batch stride N * ldy), out: bf16 [B, M, ldo] (batch stride M * ldo), c < n_out.
+ * Replaces triton_matmul_decompress (extraction_fuse_matmul.py:224-249, kernel :151-221; torch
+ * form torch_matmul :5-6 of the decoded activation). */
+int lrq_legacy_dequant_gemm(const void* l, const void* rt, int32_t K, const void* q, const void* s,
+                            int64_t s_rows, int64_t B, int64_t M, int64_t N, int32_t bits, const void* y,
+                            int64_t ldy, int32_t n_out, void* out, int64_t ldo, void* stream);
 
 /* out = x + l @ r (bf16 semantics of torch_low_rank_addition).
  * Replaces low_rank_addition (low_rank_extraction_speed.py:77-103). */

@@ -209,6 +209,15 @@ def test_legacy_argument_errors(L):
     assert L.call_raw("lrq_legacy_fused", p, p, 16, p, p, 1, 1, 64, 1024, 4, 3, p, p, None) == L.LRQ_ERR_UNSUPPORTED
     assert L.call_raw("lrq_legacy_fused", p, p, 16, p, p, 1, 1, 64, 1024, 4, 1, None, p, None) == L.LRQ_ERR_NULL
     assert L.call_raw("lrq_lowrank_add", p, p, 20, p, 1, 64, 1024, p, None) == L.LRQ_ERR_UNSUPPORTED
+    mm = lambda y=p, n=32, ldy=32, ldo=32, K=16, out=p: L.call_raw(  # noqa: E731
+        "lrq_legacy_dequant_gemm", p, p, K, p, p, 1, 1, 64, 1024, 2, y, ldy, n, out, ldo, None)
+    assert mm(y=None) == L.LRQ_ERR_NULL
+    assert mm(out=None) == L.LRQ_ERR_NULL
+    assert mm(n=0) == L.LRQ_ERR_SHAPE
+    assert mm(ldy=16) == L.LRQ_ERR_SHAPE                 # ldy < n_out
+    assert mm(ldo=16) == L.LRQ_ERR_SHAPE
+    assert mm(K=8) == L.LRQ_ERR_UNSUPPORTED               # K is padded to 16 / 32 by the caller
+    assert mm(y=ctypes.c_void_p(0x10001)) == L.LRQ_ERR_ALIGN
 
 
 def test_misc_argument_errors(L):
@@ -261,3 +270,39 @@ def test_header_compiles_as_c_and_a_c_host_links(tmp_path):
     assert r.returncode == 0, r.stderr
     ver, ws, cw, msg = r.stdout.split(maxsplit=3)
     assert ver == "1" and int(ws) == 4096 * 16 * 4 and int(cw) == 16 and msg.strip()
+
+
+def test_host_outlier_indices_are_validated(pkg):
+    """Host-held outlier indices (list / numpy / CPU tensor) must be distinct and in [0, hidden)
+    (api._outlier_index, before any device work); valid ones come back as int32 unchanged."""
+    import torch
+    api = pkg.api
+    cpu = torch.device("cpu")
+    with pytest.raises(ValueError):
+        api._outlier_index([3, 4096], 4096, cpu)
+    with pytest.raises(ValueError):
+        api._outlier_index(torch.tensor([-1, 5]), 4096, cpu)
+    with pytest.raises(ValueError):
+        api._outlier_index([7, 9, 7], 4096, cpu)
+    idx, sanitized = api._outlier_index([9, 0, 4095], 4096, cpu)
+    assert not sanitized and idx.dtype == torch.int32 and idx.tolist() == [9, 0, 4095]
+
+
+def test_row_offset_clamp_stays_in_32_bits():
+    """The row clamp of the transposed dequant-GEMM and the LoRA products takes
+    min(r * ld, lim * ld) in 32-bit unsigned arithmetic, lim = the block's last present row capped
+    at 15.  With strides below 2^24 bytes every term stays below 2^28 for any number of rows,
+    so the clamp keeps rows past the end on the last row; without the cap (lim = M - 1 - r0) the
+    product wraps once (M - 1 - r0) * ld reaches 2^32 and picks a wrong row."""
+    ld = (1 << 24) - 16
+    M = 3 * (1 << 16) + 5            # (M - 1 - r0) * ld far above 2^32 at the first blocks
+    mask = (1 << 32) - 1
+    for r0 in (0, 16 * 1000, 16 * ((M - 1) // 16)):
+        for r in range(16):
+            want = min(r0 + r, M - 1) - r0   # the clamped row inside the block
+            capped = min(M - 1 - r0, 15)
+            got = min((r * ld) & mask, (capped * ld) & mask) // ld
+            assert got == want
+            wrapped = min((r * ld) & mask, ((M - 1 - r0) * ld) & mask) // ld
+            if r0 == 0 and r == 15:
+                assert wrapped != want       # the uncapped form fails here

@@ -16,7 +16,7 @@ import pytest
 import torch
 
 import oracle as O
-from parity import assert_codes, bits16, f16
+from parity import assert_codes, assert_decode_close, assert_fp_close, bits16, f16
 
 pytestmark = pytest.mark.gpu
 
@@ -175,3 +175,107 @@ def test_fullsize_legacy_outliers(pkg, dev):
     xb = pkg.low_rank_addition_fuse_decompression_dequantization(l, r, q, dense, s, quantize_bit=cfg.bits)
     torch.cuda.synchronize()
     assert torch.equal(xa, xb)
+
+
+def _row_sample(n_rows: int, k: int = 48, seed: int = 7) -> torch.Tensor:
+    return torch.randperm(n_rows, generator=torch.Generator().manual_seed(seed))[:k].sort().values
+
+
+def test_fullsize_c3_outlier_channels_gelu(pkg, dev):
+    """Config 3 at its full [16384, 4096] (the column abs-max over 32 row groups meeting in
+    atomics, the top-41 selection, the int8/g128 encode with side columns, the fused GELU
+    backward):
+      * the column abs-max equals torch's amax of |x| exactly and the top-41 set equals
+        torch.topk's (the x50 channels stand clear of the rest);
+      * the side columns are fp16(x) of those channels and the decode returns them;
+      * every other element is within half a quantisation step of x (channels zeroed);
+      * a seeded row sample: codes bit-exact to the oracle (up to ties), the decode equal to the
+        oracle's decode of the device codes, the GELU backward within the floating-point bars;
+      * the fused GELU backward equals decode followed by the dense GELU kernel on every row."""
+    cfg = pkg.inputs.CONFIGS["c3"]
+    M, N, k = cfg.rows, cfg.hidden, cfg.keep_channels
+    print(f"[full c3] {M}x{N} top-{k}", flush=True)
+    x = pkg.inputs.activation(M, N, cfg.n_outlier, cfg.outlier_scale, cfg.seed, dev)
+    dy = pkg.inputs.gradient((M, N), cfg.grad_std, cfg.seed, dev)
+    cm = pkg.column_absmax(x)
+    idx = pkg.topk_channels(cm, k)
+    torch.cuda.synchronize()
+    cm_ref = x.float().abs().amax(dim=0)
+    assert torch.equal(cm, cm_ref)
+    top = torch.sort(cm_ref, descending=True).values
+    assert float(top[k - 1]) > 5 * float(top[k])
+    assert torch.equal(idx.long(), torch.topk(cm_ref, k).indices.sort().values)
+    print("[full c3] encode + gelu", flush=True)
+    c = pkg.encode(x, None, bits=cfg.bits, group_size=cfg.group, outlier_idx=idx)
+    out = pkg.gelu_backward_compressed(c, dy)
+    xh = pkg.decode(c)
+    torch.cuda.synchronize()
+    il = idx.long()
+    assert torch.equal(c.side, x[:, il].to(torch.float16))
+    assert torch.equal(xh[:, il], c.side.to(torch.bfloat16))
+    G = cfg.group
+    r = x.float().clone()
+    r[:, il] = 0.0
+    codes = c.codes.to(torch.int32).float().view(M, -1, G)
+    d = codes * c.scale.float()[..., None] + c.zero.float()[..., None]
+    err = (d.view(M, -1) - r).abs().view(M, -1, G)
+    step = c.scale.float()[..., None]
+    bound = 0.5 * step * (1 + 2e-3) + r.abs().view(M, -1, G) * 2e-6 + 1e-6
+    frac_ok = float((err <= bound).float().mean())
+    print(f"[full c3] within half-step: {frac_ok:.7f}", flush=True)
+    assert frac_ok >= 1 - 1e-6
+    del r, codes, d, err, bound
+    assert torch.equal(out, pkg.triton_gelu_backward(xh, dy))
+    rows = _row_sample(M)
+    rd = rows.to(dev)
+    idx_np = idx.cpu().numpy()
+    ref = O.encode(bits16(x[rd]), None, cfg.bits, G, outlier_idx=idx_np)
+    assert_codes(c.codes[rd].cpu().numpy(), ref, cfg.bits, what="c3 row sample")
+    ref_xh = O.decode(None, None, c.codes[rd].cpu().numpy(), f16(c.scale[rd]), f16(c.zero[rd]), cfg.bits, G,
+                      side=f16(c.side[rd]), idx=idx_np)
+    assert np.array_equal(bits16(xh[rd]), ref_xh)
+    rep = assert_fp_close(bits16(out[rd]), O.gelu_bwd(O.bf16_to_f32(ref_xh), O.bf16_to_f32(bits16(dy[rd]))),
+                          "c3 full-size GELU row sample")
+    print(f"[full c3] row sample {rep}", flush=True)
+
+
+def test_fullsize_c5_softmax_rows(pkg, dev):
+    """Config 5 at its full 131,072 rows x 2048 (k_softmax_rows walking many row blocks per
+    workgroup):
+      * on every row, sum_i dS_i = (sum_i dP_i P_i) (1 - sum_i P_i) on the device's own decode P,
+        within the bf16 rounding of each dS_i (2^-7 sum |dS_i|) plus the fp32 row sum's
+        accumulation (2e-4 sum |dP_i P_i|); a backward missing the row-sum term misses this by
+        about sum dP_i P_i;
+      * a seeded row sample: the decode against the oracle's decode of the device codes, and dS
+        within the floating-point bars of the oracle's decompress-then-op."""
+    cfg = pkg.inputs.CONFIGS["c5"]
+    M, N = cfg.rows, cfg.hidden
+    print(f"[full c5] {M}x{N}", flush=True)
+    p = pkg.inputs.softmax_probs((M, N), seed=cfg.seed, device=dev)
+    dp = pkg.inputs.gradient((M, N), cfg.grad_std, cfg.seed, dev)
+    V = pkg.inputs.basis(N, cfg.rank, cfg.seed)
+    c = pkg.encode(p, V.to(dev), bits=cfg.bits, group_size=cfg.group)
+    ds = pkg.softmax_backward_compressed(c, dp)
+    ph = pkg.decode(c)
+    torch.cuda.synchronize()
+    worst = 0.0
+    for r0 in range(0, M, 16384):  # float64 row sums in slices of 16384 rows
+        sl = slice(r0, min(M, r0 + 16384))
+        p64, dp64, ds64 = ph[sl].double(), dp[sl].double(), ds[sl].double()
+        prod = dp64 * p64
+        s = prod.sum(-1)
+        psum = p64.sum(-1)
+        lhs = ds64.sum(-1)
+        rhs = s * (1.0 - psum)
+        bound = 2.0 ** -7 * ds64.abs().sum(-1) + 2e-4 * prod.abs().sum(-1) * psum.abs() + 1e-12
+        worst = max(worst, float(((lhs - rhs).abs() / bound).max()))
+    print(f"[full c5] row-sum identity: worst error / bound {worst:.3f}", flush=True)
+    assert worst <= 1.0
+    rows = _row_sample(M)
+    rd = rows.to(dev)
+    ref_ph = O.decode(bits16(c.L[rd]), bits16(V), c.codes[rd].cpu().numpy(), f16(c.scale[rd]), f16(c.zero[rd]),
+                      cfg.bits, cfg.group)
+    rep_d = assert_decode_close(bits16(ph[rd]), ref_ph, "c5 full-size decode row sample")
+    ref = O.softmax_bwd(O.bf16_to_f32(ref_ph), O.bf16_to_f32(bits16(dp[rd])))
+    rep = assert_fp_close(bits16(ds[rd]), ref, "c5 full-size softmax row sample", max_abs=1e-3)
+    print(f"[full c5] row sample decode {rep_d} dS {rep}", flush=True)

@@ -277,3 +277,26 @@ def test_outlier_channels_c3_shape(pkg, dev, rows):
     assert np.array_equal(bits16(xh_dev), ref_xh)
     ref_out = O.gelu_bwd(O.bf16_to_f32(ref_xh), O.bf16_to_f32(bits16(inp["dy"])))
     assert_fp_close(bits16(out), ref_out, "c3 gelu")
+
+
+def test_invalid_outlier_indices(pkg, dev):
+    """Device-held outlier indices are not read back: an entry outside [0, N) or a repeat of an
+    earlier entry becomes -1 and its side column is zero, and every other output equals the encode
+    of the valid entries alone.  Host-held indices with such entries are refused."""
+    rows, hidden = 64, 4096
+    print("[bad idx] encode", flush=True)
+    x = pkg.inputs.activation(rows, hidden, 8, 20.0, seed=77).to(dev)
+    V = pkg.inputs.basis(hidden, 16, seed=77).to(dev)
+    bad = torch.tensor([10, hidden + 3, 10, 77, -1], dtype=torch.int32, device=dev)
+    c = pkg.encode(x, V, outlier_idx=bad)
+    good = pkg.encode(x, V, outlier_idx=torch.tensor([10, 77], dtype=torch.int32, device=dev))
+    torch.cuda.synchronize()
+    assert c.idx.tolist() == [10, -1, -1, 77, -1]
+    assert torch.all(c.side[:, [1, 2, 4]] == 0)
+    assert torch.equal(c.side[:, [0, 3]], good.side)
+    assert torch.equal(c.codes, good.codes) and torch.equal(c.qparams, good.qparams) and torch.equal(c.L, good.L)
+    assert torch.equal(pkg.decode(c), pkg.decode(good))
+    with pytest.raises(ValueError):
+        pkg.encode(x, V, outlier_idx=[10, hidden])
+    with pytest.raises(ValueError):
+        pkg.encode(x, V, outlier_idx=[10, 10])

@@ -162,6 +162,52 @@ def test_legacy_fused_consumers(pkg, dev, B, M, N, K, bits):
     assert_fp_close(bits16(mm), ref, "legacy dequant matmul")
 
 
+GEMM = [
+    # (B, M, N, K, bits, n, s_rows) — the reference bench's y [B, N, 32] and 2-bit codes first
+    (2, 100, 1024, 32, 2, 32, 1),   # MFMA, ragged rows, K = 32, batch 2
+    (3, 64, 2048, 16, 1, 16, 3),    # 1-bit (8 planes), per-batch scales
+    (2, 48, 1024, 8, 4, 48, 1),     # K = 8 padded to 16; n = 48 = a 32- and a 16-column chunk
+    (1, 300, 1024, 20, 8, 20, 1),   # 8-bit, K = 20 padded to 32, n = 20 padded to 32
+    (2, 17, 96, 16, 2, 32, 2),      # scalar path (planes of 24 columns)
+    (1, 32, 32, 16, 4, 7, 1),       # scalar path, the reference smoke shape, n = 7
+]
+
+
+@pytest.mark.parametrize("B,M,N,K,bits,n,s_rows", GEMM)
+def test_legacy_dequant_gemm(pkg, dev, B, M, N, K, bits, n, s_rows):
+    """triton_matmul_decompress (R12, legacy format) in one kernel: x_hat @ y against the
+    float64 product of the oracle's decoded x_hat, at the north-star floating-point bars."""
+    l, r, x, s = _inputs(7100 + N + bits, B, M, N, K, s_rows, outlier_cols=0)
+    lb, rb, xb, sb = bits16(l), bits16(r), bits16(x), bits16(s)
+    _, q_ref = O.legacy_encode(lb, rb, xb, sb, bits, 1e9)
+    xh = O.bf16_to_f32(O.legacy_decode(lb, rb, q_ref, None, sb, bits))
+    g = torch.Generator().manual_seed(71 + n)
+    y = (torch.randn(B, N, n, generator=g) * 0.1).to(torch.bfloat16)
+    q = torch.from_numpy(q_ref).to(dev)
+    out = pkg.triton_matmul_decompress(q, l.to(dev), r.to(dev), s.to(dev), y.to(dev), quantize_bit=bits)
+    assert tuple(out.shape) == (B, M, n) and out.dtype == torch.bfloat16
+    ref = np.stack([O.gemm(xh[b], O.bf16_to_f32(bits16(y[b]))) for b in range(B)])
+    assert_fp_close(bits16(out), ref, f"legacy dequant-GEMM {bits}-bit K={K} n={n}")
+
+
+def test_legacy_dequant_gemm_strided_y_and_empty(pkg, dev):
+    """A non-contiguous y (a transposed view) gives the same bits as its contiguous copy, and
+    zero rows or zero output columns return empty results."""
+    B, M, N, K, bits = 2, 64, 1024, 16, 2
+    l, r, x, s = _inputs(7300, B, M, N, K, 1, outlier_cols=0)
+    _, q_ref = O.legacy_encode(bits16(l), bits16(r), bits16(x), bits16(s), bits, 1e9)
+    q = torch.from_numpy(q_ref).to(dev)
+    g = torch.Generator().manual_seed(73)
+    yt = (torch.randn(B, 32, N, generator=g) * 0.1).to(torch.bfloat16).to(dev)
+    a = pkg.triton_matmul_decompress(q, l.to(dev), r.to(dev), s.to(dev), yt.transpose(1, 2), quantize_bit=bits)
+    b = pkg.triton_matmul_decompress(q, l.to(dev), r.to(dev), s.to(dev), yt.transpose(1, 2).contiguous(),
+                                     quantize_bit=bits)
+    assert torch.equal(a, b)
+    e = pkg.triton_matmul_decompress(q, l.to(dev), r.to(dev), s.to(dev), yt.transpose(1, 2)[..., :0],
+                                     quantize_bit=bits)
+    assert tuple(e.shape) == (B, M, 0)
+
+
 @pytest.mark.parametrize("B,M,N,K", [(2, 100, 1024, 16), (1, 32, 32, 8), (1, 16, 96, 32)])
 def test_low_rank_addition(pkg, dev, B, M, N, K):
     l, r, x, _ = _inputs(300 + N, B, M, N, K, 1)

@@ -5,6 +5,8 @@ the plain one (codes conditional on the device's L, then end to end), and decode
 oracle's decode of the device's codes.
 """
 
+import importlib
+
 import numpy as np
 import pytest
 import torch
@@ -122,6 +124,35 @@ def test_rotated_consumers(pkg, dev, rows, n, rank, bits, group, op):
         O.bf16_to_f32(ref_xh), yf)
     rep = assert_fp_close(bits16(out), ref, f"rotated {op} vs the oracle")
     print(f"[rot consumer] {rep}", flush=True)
+
+
+@pytest.mark.parametrize("rows,n,rank,bits,group,fused", [
+    (37, 5120, 16, 4, 64, True),     # fused rotated row kernel: dx written over dy gives the same bits
+    (30, 2048, 16, 8, 128, False),   # decode then dense op: an aliasing call is refused
+])
+def test_rotated_consumer_in_place(pkg, dev, rows, n, rank, bits, group, fused):
+    """dx == dy through the C ABI on the rotated format: the fused kernel reads each dy element
+    before writing that dx element, so in place equals out of place; the decode-then-dense form
+    would overwrite dy first, so it returns LRQ_ERR_UNSUPPORTED and leaves dy untouched."""
+    import ctypes
+    L = importlib.import_module("triton-kernel-test_amd._lib")
+    lib = L.load()
+    print(f"[rot in place] rows={rows} n={n} int{bits}/g{group}", flush=True)
+    x = pkg.inputs.activation(rows, n, 8, 20.0, seed=n + 7)
+    V = pkg.inputs.basis(n, rank, seed=3)
+    c = pkg.encode(x.to(dev), V.to(dev), bits=bits, group_size=group, hadamard=True)
+    dy = pkg.inputs.gradient((rows, n), 0.02, seed=rows + 1).to(dev)
+    ref = pkg.silu_backward_compressed(c, dy)
+    buf = dy.clone()
+    d = c.descriptor()
+    sp = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    p = ctypes.c_void_p(buf.data_ptr())
+    st = lib.lrq_silu_bwd(ctypes.byref(d), p, n, p, n, sp)
+    torch.cuda.synchronize()
+    if fused:
+        assert st == 0 and torch.equal(buf, ref)
+    else:
+        assert st == L.LRQ_ERR_UNSUPPORTED and torch.equal(buf, dy)
 
 
 @pytest.mark.parametrize("rows,n,rank,n_out,out_dtype,bits,group", [

@@ -84,3 +84,35 @@ def test_noalloc_rejects_a_workspace_beyond_the_scratch(pkg):
     assert L.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(t), 32) > L.LRQ_GEMM_T_SCRATCH_BYTES
     p = ctypes.c_void_p(0x400000)
     assert L.call_raw("lrq_dequant_gemm_t_noalloc", ctypes.byref(t), p, 32, 32, p, 32, 1, None) == L.LRQ_ERR_WORKSPACE
+
+
+def test_noalloc_replays_from_a_captured_graph(pkg, dev):
+    """The entry point launches kernels only (no allocation, no memset), so a call captured in a
+    HIP graph replays correctly: three replays, each after eager calls that reuse the scratch
+    with another input and a synchronisation, each bit-identical to the workspace entry point.
+    The first call on the device (the scratch address lookup) runs eagerly before the capture."""
+    L = _lib(pkg)
+    c, g = _case(pkg, dev, 4096, 4096, 16, 4, 64, 16, seed=33)
+    other = _case(pkg, dev, 3000, 2048, 16, 4, 64, 32, seed=34)
+    ref, _ = _with_workspace(L, c, g, 16, True)
+    ref_other, _ = _with_workspace(L, *other, 32, True)
+    _no_alloc(L, c, g, 16, True)
+    torch.cuda.synchronize()
+    out = torch.full((c.hidden, 16), float("nan"), dtype=torch.float32, device=dev)
+    t = c.descriptor()
+    graph = torch.cuda.CUDAGraph()
+    print("[noalloc] capture", flush=True)
+    with torch.cuda.graph(graph):
+        stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        st = L.call_raw("lrq_dequant_gemm_t_noalloc", ctypes.byref(t), ctypes.c_void_p(g.data_ptr()), 16, 16,
+                        ctypes.c_void_p(out.data_ptr()), 16, 1, stream)
+    assert st == 0, L.status_string(st)
+    for i in range(3):
+        got_other = _no_alloc(L, *other, 32, True)
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        print(f"[noalloc] replay {i}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), f"replay {i}"
+        assert torch.equal(got_other.view(torch.int32), ref_other.view(torch.int32))

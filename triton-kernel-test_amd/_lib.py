@@ -70,6 +70,9 @@ SIGNATURES = {
                                     c_int64, c_int64, c_int64, c_int32, c_void_p, c_void_p]),
     "lrq_legacy_fused": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int64, c_int64,
                                    c_int64, c_int64, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
+    "lrq_legacy_dequant_gemm": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int64, c_int64,
+                                          c_int64, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int64,
+                                          c_void_p]),
     "lrq_coo_compact": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                   c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
     "lrq_coo_workspace": (c_int64, [c_int64, c_int64, c_int64]),

@@ -107,7 +107,7 @@ class CompressedActivation:
     L: Optional[torch.Tensor]           # bf16 [rows, r]
     basis: Optional[LowRankBasis]
     side: Optional[torch.Tensor]        # fp16 [rows, k]
-    idx: Optional[torch.Tensor]         # int32 [k], ascending
+    idx: Optional[torch.Tensor]         # int32 [k] (-1: an entry dropped as invalid, see _outlier_index)
     shape: tuple
     bits: int
     group: int
@@ -185,13 +185,42 @@ def _alloc(rows: int, n: int, bits: int, group: int, rank: int, k: int, device) 
     )
 
 
+def _outlier_index(idx, n: int, device) -> tuple[torch.Tensor, bool]:
+    """The outlier-channel index list as int32 on the device, and whether it was sanitized.
+    Indices the host holds (a list, numpy array or CPU tensor) must be distinct and in [0, n):
+    ValueError otherwise.  A device tensor (e.g. topk_channels' output) is not read back: an
+    entry outside [0, n) or a repeat of an earlier entry becomes -1, which every kernel skips,
+    and its side column is zero-filled (no host synchronisation)."""
+    if isinstance(idx, torch.Tensor) and idx.is_cuda:
+        _require_device(idx)
+        idx = idx.to(torch.int32).contiguous()
+        k = idx.numel()
+        if k == 0:
+            return idx, False
+        valid = (idx >= 0) & (idx < n)
+        vals, perm = torch.sort(idx, stable=True)
+        first = torch.ones(k, dtype=torch.bool, device=idx.device)
+        first[1:] = vals[1:] != vals[:-1]
+        first_at = torch.empty_like(first)
+        first_at[perm] = first
+        return torch.where(valid & first_at, idx, torch.full_like(idx, -1)), True
+    h = torch.as_tensor(idx).reshape(-1).to(torch.int64)
+    if h.numel() and (int(h.min()) < 0 or int(h.max()) >= n):
+        raise ValueError(f"outlier_idx entries must lie in [0, {n})")
+    if h.numel() != torch.unique(h).numel():
+        raise ValueError("outlier_idx entries must be distinct")
+    return h.to(torch.int32).to(device).contiguous(), False
+
+
 def encode(x: torch.Tensor, basis: Optional[LowRankBasis | torch.Tensor] = None, *, bits: int = 4,
            group_size: int = 64, hadamard: bool = False, outlier_idx: Optional[torch.Tensor] = None,
            _twopass: bool = False) -> CompressedActivation:
     """Compress a bf16 activation x[..., N].
 
     ``basis``: the rank-r orthonormal V[N, r] (or a ``LowRankBasis``); None for rank 0.
-    ``outlier_idx``: int32 column indices kept as fp16 side columns (see ``outlier_channels``).
+    ``outlier_idx``: column indices kept as fp16 side columns (see ``outlier_channels``);
+    host-held indices must be distinct and in range, device-held ones are sanitized on the device
+    (``_outlier_index``).
     """
     _require_device(x)
     if x.dtype != torch.bfloat16:
@@ -202,11 +231,13 @@ def encode(x: torch.Tensor, basis: Optional[LowRankBasis | torch.Tensor] = None,
     if basis is not None and basis.hidden != n:
         raise ValueError(f"basis has {basis.hidden} rows, activation hidden size is {n}")
     rank = 0 if basis is None else basis.rank
+    sanitized = False
     if outlier_idx is not None:
-        _require_device(outlier_idx)
-        outlier_idx = outlier_idx.to(torch.int32).contiguous()
+        outlier_idx, sanitized = _outlier_index(outlier_idx, n, x.device)
     k = 0 if outlier_idx is None else outlier_idx.numel()
     bufs = _alloc(rows, n, bits, group_size, rank, k, x.device)
+    if sanitized and k:
+        bufs["side"].zero_()  # the side columns of dropped indices read as zeros
     c = CompressedActivation(codes=bufs["codes"], qparams=bufs["qparams"], L=bufs["L"],
                              basis=basis, side=bufs["side"], idx=outlier_idx if k else None,
                              shape=tuple(x.shape), bits=bits, group=group_size, hadamard=hadamard)

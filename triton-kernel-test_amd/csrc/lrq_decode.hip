@@ -972,7 +972,8 @@ namespace lrq {
 // The elementwise consumers (op as lrq_dense_elementwise numbers them).  The rotated format goes
 // to the fused row kernel where it can, else decode into `out` (rotation undone) and the dense
 // op in place over it: two kernels, no scratch.  The second form needs rows of exactly `hidden`
-// elements in both tensors (the dense kernel is flat).
+// elements in both tensors (the dense kernel is flat) and `out` distinct from `in` (the decode
+// would overwrite `in` before the op reads it).
 template <class EPI>
 static int consumer(const lrq_tensors* t, const void* in, int64_t ldin, void* out, int64_t ldo, int op,
                     void* stream) {
@@ -982,7 +983,7 @@ static int consumer(const lrq_tensors* t, const void* in, int64_t ldin, void* ou
   const EPI epi{(const uint16_t*)in, ldin, (uint16_t*)out, ldo};
   if (!(t->flags & LRQ_FLAG_HADAMARD)) return decode_dispatch(t, (hipStream_t)stream, epi);
   if (consumer_rot(t, (hipStream_t)stream, epi, &st)) return st;
-  if (ldin != t->hidden || ldo != t->hidden) return LRQ_ERR_UNSUPPORTED;
+  if (ldin != t->hidden || ldo != t->hidden || in == out) return LRQ_ERR_UNSUPPORTED;
   LRQ_TRY(lrq_decode(t, out, ldo, stream));
   return lrq_dense_elementwise(op, out, in, out, t->rows * t->hidden, stream);
 }

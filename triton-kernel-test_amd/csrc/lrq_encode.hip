@@ -216,21 +216,15 @@ struct RowsEnc {
 // Direct-to-LDS slices (RowsEnc::PPL == NP): the next block's 16 row loads are issued in
 // pieces at points 0 (after the current slice is read), 1 (after the partial sums) and 2 + u
 // (after unit u is quantised); n[pt] loads at point pt.
-#ifndef LRQ_ENC_SCHED_U4
-#define LRQ_ENC_SCHED_U4 4, 8, 0, 4, 0, 0
-#endif
-#ifndef LRQ_ENC_SCHED_U2
-#define LRQ_ENC_SCHED_U2 4, 8, 0, 4
-#endif
 template <int UPW>
 struct DmaSched;
 template <>
 struct DmaSched<4> {
-  static constexpr int n[6] = {LRQ_ENC_SCHED_U4};
+  static constexpr int n[6] = {4, 8, 0, 4, 0, 0};
 };
 template <>
 struct DmaSched<2> {
-  static constexpr int n[4] = {LRQ_ENC_SCHED_U2};
+  static constexpr int n[4] = {4, 8, 0, 4};
 };
 // loads issued before point pt
 template <int UPW>

@@ -170,16 +170,12 @@ __device__ __forceinline__ void coo_bounds(const LegacyArgs& a, int64_t bm, int 
 }
 
 // Entries each lane requests per piece and pass (4 lanes per row: 4 * KL entries of a piece per pass).
-#ifndef LRQ_COO_KL
-#define LRQ_COO_KL 2
-#endif
+static constexpr int kCooEntriesPerLane = 2;
 // bf16 of padding after each row of the COO tile: rows 16 bytes apart in the LDS banks, so the
 // 16-byte accesses of 8 consecutive lanes (8 rows) fall in distinct banks.
-#ifndef LRQ_COO_PAD
-#define LRQ_COO_PAD 8
-#endif
+static constexpr int kCooRowPad = 8;
 template <int NP>
-constexpr int coo_row_stride() { return NP * 64 + LRQ_COO_PAD; }
+constexpr int coo_row_stride() { return NP * 64 + kCooRowPad; }
 template <int NP, int KL>
 __device__ __forceinline__ void coo_tile(const LegacyArgs& a, int64_t (&s0)[NP], int64_t (&s1)[NP], int u, int N,
                                          int j, int g, uint16_t* __restrict__ ot) {
@@ -355,7 +351,7 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
 #pragma unroll
     for (int e = 0; e < E; ++e) byte[e] = 0u;
     uint16_t* ot = otile + (size_t)w * 16 * coo_row_stride<NP>();
-    if constexpr (MODE == kDecode && OSRC == 3) coo_tile<NP, LRQ_COO_KL>(a, s0, s1, u, N, j, g, ot);
+    if constexpr (MODE == kDecode && OSRC == 3) coo_tile<NP, kCooEntriesPerLane>(a, s0, s1, u, N, j, g, ot);
 
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
@@ -542,6 +538,196 @@ __global__ __launch_bounds__(256) void k_legacy_scalar(LegacyArgs a, int K, int6
     }
   }
   if constexpr (MODE == kEncode) a.qout[bm * NB + c] = (uint8_t)qout;
+}
+
+// ------------------------------------------------------------------ dequant-GEMM
+// out[b, m, c] = bf16( sum_n x_hat[b, m, n] * y[b, n, c] ), the sum in fp32, with x_hat the
+// fused decode's value bf16(bf16(bf16((code - 2^(b-1)) * s) + bf16(l @ r))): the reference's
+// triton_matmul_decompress (extraction_fuse_matmul.py:224-249, kernel :151-221) on the torch form
+// of its decode.  x_hat never leaves the registers.
+struct LegacyGemmArgs {
+  const uint16_t* l;   // [M, K]
+  const uint16_t* rt;  // [N, K]
+  const uint8_t* q;    // [B, M, N/NP]
+  const uint16_t* s;   // [s_rows, N]
+  int64_t s_rows;
+  const uint16_t* y;   // [B, N, ldy]: columns c0 .. c0 + NOUT - 1 for this launch (y points at c0)
+  int64_t ldy;
+  uint16_t* out;       // [B, M, ldo] (out points at column c0)
+  int64_t ldo;
+  int64_t M, N;
+  int n_out;           // scalar path: output columns
+};
+
+// MFMA path (every plane a whole number of 64-column units).  Grid: B * ceil(row blocks / RB)
+// workgroups of 8 waves; a workgroup owns RB 16-row blocks of one batch.  Work items are
+// (unit, plane) pairs, unit-major, so the waves that run together share a unit's code rows in
+// L2; wave w takes items w, w + 8, ...  An item's operands (rt and y rows of the plane's 64
+// columns in the reconstruction layout, the lane's 16 scales, the RB blocks' code vectors) sit in
+// one of two register slots, loaded while the other item is computed.  Per item the y operands are
+// transposed once (identity MFMA); per row block the reconstruction MFMA gives bf16(l @ r) in the
+// lane's 16 columns, the decode's roundings give x_hat, and x_hat (bf16, exact) is the B operand of
+// the product MFMA.  The 8 waves' partial tiles are then summed through LDS in wave order.
+template <int BITS, int K, int NOUT, int RB>
+__global__ __launch_bounds__(512) void k_legacy_gemm(LegacyGemmArgs a) {
+  constexpr int NP = 8 / BITS, G = 64, E = 16, RT = K / 16, TO = NOUT / 16, NW = 8;
+  constexpr uint32_t kMask = BITS == 8 ? 0xffu : (1u << BITS) - 1u;
+  __shared__ f32x4 part[NW][TO][64];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int M = (int)a.M, N = (int)a.N;
+  const int nrb = (M + 15) / 16, gx = (nrb + RB - 1) / RB;
+  const int b = blockIdx.x / gx;
+  const int rb0 = (blockIdx.x - b * gx) * RB;
+  const int nu = N / NP / G, ni = nu * NP;
+  const int64_t NB = N / NP;
+  const uint16_t* srow = a.s + (a.s_rows == 1 ? 0 : (int64_t)b * N);
+  const uint16_t* yb = a.y + (int64_t)b * N * a.ldy;
+  const uint8_t* qb = a.q + (int64_t)b * M * NB;
+  const u32x2 ident = identity_bop(j, g);
+  const float zero[E] = {};
+
+  f32x4 acc[RB][TO];
+  u32x2 lop[RB][RT];
+#pragma unroll
+  for (int i = 0; i < RB; ++i) {
+    const int64_t row = min(min(rb0 + i, nrb - 1) * 16 + j, M - 1);
+#pragma unroll
+    for (int t = 0; t < TO; ++t) acc[i][t] = zero4();
+#pragma unroll
+    for (int t = 0; t < RT; ++t) lop[i][t] = ld8(a.l + row * K + 16 * t + 4 * g);
+  }
+  struct Item {
+    u32x2 vop[G / 16][RT];  // rt rows of the item's columns (reconstruction A operand)
+    u32x2 ya[G / 16][TO];   // y rows of the item's columns, same layout
+    u32x4 sc[2];            // the lane's 16 scales (bf16)
+    u32x4 cb[RB];           // the lane's 16 code bytes of each row block
+  };
+  auto load_item = [&](int it, Item& d) {
+    const int u = it / NP, p = it % NP;
+    const int base = unit_base(p, u, N, NP, G);
+    load_vops<G, K>(a.rt, base, j, g, d.vop);
+#pragma unroll
+    for (int q = 0; q < G / 16; ++q)
+#pragma unroll
+      for (int t = 0; t < TO; ++t) d.ya[q][t] = ld8(yb + (int64_t)vrow_res<G>(base, j, q) * a.ldy + 16 * t + 4 * g);
+    d.sc[0] = ld16(srow + base + E * g);
+    d.sc[1] = ld16(srow + base + E * g + 8);
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      const int64_t row = min(min(rb0 + i, nrb - 1) * 16 + j, M - 1);
+      d.cb[i] = ld16_stream(qb + row * NB + u * G + E * g);
+    }
+  };
+  auto compute_item = [&](const Item& d, int p) {
+    u32x4 yt[G / 32][TO];
+    transpose_vops<G, NOUT>(d.ya, ident, yt);
+    float sc[E];
+    unpack8(d.sc[0], sc);
+    unpack8(d.sc[1], sc + 8);
+    const int sh = BITS * p;
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      float lr[E], xh[E];
+      residual_unit<G, K>(d.vop, lop[i], zero, lr);
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const uint32_t code = (d.cb[i][e >> 2] >> (8 * (e & 3) + sh)) & kMask;
+        xh[e] = legacy_value<BITS, false>(code, sc[e], 0.f, bf16r(lr[e]));
+      }
+      u32x4 xb[G / 32];
+#pragma unroll
+      for (int k = 0; k < G / 32; ++k) {
+        const float* f = xh + 8 * k;
+        xb[k] = u32x4{pack_bf16x2_exact(f[0], f[1]), pack_bf16x2_exact(f[2], f[3]), pack_bf16x2_exact(f[4], f[5]),
+                      pack_bf16x2_exact(f[6], f[7])};
+      }
+      project_unit_vt<G, NOUT>(yt, xb, acc[i]);
+    }
+  };
+  const int nit = w < ni ? (ni - w + NW - 1) / NW : 0;
+  Item ring[2];
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl) load_item(min(w + sl * NW, ni - 1), ring[sl]);
+  for (int i0 = 0; i0 < nit; i0 += 2) {
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) {
+      if (i0 + sl < nit) compute_item(ring[sl], (w + (i0 + sl) * NW) % NP);  // wave-uniform
+      load_item(min(w + (i0 + sl + 2) * NW, ni - 1), ring[sl]);
+    }
+  }
+
+  // acc[i][t] in lane (j, g), component v: out[row j][16t + 4g + v] (partial over this wave's items)
+  constexpr int F = TO * 256 / NW, S = 64 / F, PPL = NW / S;
+  static_assert(F >= 1 && F <= 64 && 64 % F == 0 && NW % S == 0, "out reduction split");
+  const float* partf = reinterpret_cast<const float*>(&part[0][0][0]);
+  uint16_t* ob = a.out + (int64_t)b * M * a.ldo;
+#pragma unroll
+  for (int i = 0; i < RB; ++i) {
+    if (rb0 + i >= nrb) break;  // uniform
+#pragma unroll
+    for (int t = 0; t < TO; ++t) part[w][t][lane] = acc[i][t];
+    __syncthreads();
+    const int f = lane % F, pg = lane / F;
+    const int fi = w * F + f;
+    const int t = fi >> 8, src = (fi >> 2) & 63, v = fi & 3;
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < PPL; ++k) s += partf[(((pg * PPL + k) * TO + t) * 64 + src) * 4 + v];
+#pragma unroll
+    for (int m = F; m < 64; m <<= 1) s += __shfl_xor(s, m);
+    const int row = (rb0 + i) * 16 + (src & 15);
+    const int col = 16 * t + 4 * (src >> 4) + v;
+    if (pg == 0 && row < M) ob[(int64_t)row * a.ldo + col] = (uint16_t)pack_bf16x2(s, 0.f);
+    __syncthreads();
+  }
+}
+
+// Scalar path (any shape): one workgroup per row (b, m); thread t decodes columns t, t + 256, ...
+// (l @ r in fp64, exact, as k_legacy_scalar) and multiplies them into up to 32 fp32 sums; the 256
+// threads' sums are added through LDS in thread order.  Output columns in chunks of 32.
+template <int BITS>
+__global__ __launch_bounds__(256) void k_legacy_gemm_scalar(LegacyGemmArgs a, int K) {
+  constexpr int NP = 8 / BITS, OC = 32;
+  constexpr uint32_t kMask = BITS == 8 ? 0xffu : (1u << BITS) - 1u;
+  __shared__ float red[OC][257];
+  const int64_t M = a.M, N = a.N, NB = N / NP;
+  const int64_t bm = blockIdx.x, b = bm / M, m = bm - b * M;
+  const uint16_t* srow = a.s + (a.s_rows == 1 ? 0 : b * N);
+  const uint16_t* lrow = a.l + m * K;
+  const uint16_t* yb = a.y + b * N * a.ldy;
+  const int t = threadIdx.x;
+  for (int o0 = 0; o0 < a.n_out; o0 += OC) {
+    const int nc = min(OC, a.n_out - o0);
+    float acc[OC];
+#pragma unroll
+    for (int o = 0; o < OC; ++o) acc[o] = 0.f;
+    for (int64_t col = t; col < N; col += 256) {
+      const int64_t c = col % NB;
+      const int p = (int)(col / NB);
+      const uint16_t* rrow = a.rt + col * K;
+      double dot = 0.0;
+      for (int k = 0; k < K; ++k)
+        dot = __builtin_fma((double)__uint_as_float((uint32_t)lrow[k] << 16),
+                            (double)__uint_as_float((uint32_t)rrow[k] << 16), dot);
+      const uint32_t code = ((uint32_t)a.q[bm * NB + c] >> (BITS * p)) & kMask;
+      const float sc = __uint_as_float((uint32_t)srow[col] << 16);
+      const float xh = legacy_value<BITS, false>(code, sc, 0.f, bf16r((float)dot));
+      const uint16_t* yr = yb + col * a.ldy + o0;
+#pragma unroll
+      for (int o = 0; o < OC; ++o)
+        if (o < nc) acc[o] = __builtin_fmaf(xh, __uint_as_float((uint32_t)yr[o] << 16), acc[o]);
+    }
+#pragma unroll
+    for (int o = 0; o < OC; ++o) red[o][t] = acc[o];
+    __syncthreads();
+    if (t < nc) {
+      float s = 0.f;
+      for (int i = 0; i < 256; ++i) s += red[t][i];
+      a.out[bm * a.ldo + o0 + t] = (uint16_t)pack_bf16x2(s, 0.f);
+    }
+    __syncthreads();
+  }
 }
 
 // Scalar form of the hist pass: one thread per column of one row (any shape).
@@ -762,6 +948,69 @@ extern "C" int lrq_legacy_fused(const void* l, const void* rt, int32_t K, const 
     case 0: return legacy_bits<kFusedStore, 0>(a, K, B, bits, mfma_ok, hs);
     case 1: return legacy_bits<kFusedSilu, 0>(a, K, B, bits, mfma_ok, hs);
     default: return legacy_bits<kFusedMul, 0>(a, K, B, bits, mfma_ok, hs);
+  }
+}
+
+namespace lrq {
+template <int BITS, int K, int NOUT>
+static int legacy_gemm_chunk(const LegacyGemmArgs& a, int64_t B, hipStream_t st) {
+  // 16-row blocks per workgroup: 4, or 2 / 1 where 4 would leave CUs without a workgroup
+  const int64_t nrb = (a.M + 15) / 16, cu = cu_count();
+  auto launch_rb = [&](auto rb) {
+    constexpr int RB = decltype(rb)::value;
+    const int64_t nwg = B * ((nrb + RB - 1) / RB);
+    if (nwg > INT32_MAX) return (int)LRQ_ERR_SHAPE;
+    return launch((k_legacy_gemm<BITS, K, NOUT, RB>), dim3((unsigned)nwg), dim3(512), 0, st, a);
+  };
+  if (B * ((nrb + 3) / 4) >= cu) return launch_rb(std::integral_constant<int, 4>{});
+  if (B * ((nrb + 1) / 2) >= cu) return launch_rb(std::integral_constant<int, 2>{});
+  return launch_rb(std::integral_constant<int, 1>{});
+}
+
+template <int BITS>
+static int legacy_gemm_bits(LegacyGemmArgs a, int K, int64_t B, bool mfma_ok, hipStream_t st) {
+  if (!mfma_ok) {
+    if (B * a.M > INT32_MAX) return LRQ_ERR_SHAPE;
+    return launch(k_legacy_gemm_scalar<BITS>, dim3((unsigned)(B * a.M)), dim3(256), 0, st, a, K);
+  }
+  // output columns in chunks of 32 (then 16); each chunk is one pass over the codes
+  const uint16_t* y0 = a.y;
+  uint16_t* o0 = a.out;
+  for (int c0 = 0; c0 < a.n_out;) {
+    const int nc = a.n_out - c0 >= 32 ? 32 : 16;
+    a.y = y0 + c0;
+    a.out = o0 + c0;
+    int r;
+    if (K == 16) r = nc == 32 ? legacy_gemm_chunk<BITS, 16, 32>(a, B, st) : legacy_gemm_chunk<BITS, 16, 16>(a, B, st);
+    else r = nc == 32 ? legacy_gemm_chunk<BITS, 32, 32>(a, B, st) : legacy_gemm_chunk<BITS, 32, 16>(a, B, st);
+    LRQ_TRY(r);
+    c0 += nc;
+  }
+  return LRQ_OK;
+}
+}  // namespace lrq
+
+extern "C" int lrq_legacy_dequant_gemm(const void* l, const void* rt, int32_t K, const void* q, const void* s,
+                                       int64_t s_rows, int64_t B, int64_t M, int64_t N, int32_t bits, const void* y,
+                                       int64_t ldy, int32_t n_out, void* out, int64_t ldo, void* stream) {
+  int st = legacy_check(l, rt, K, B, M, N, bits, s, s_rows, true);
+  if (st) return st;
+  if (q == nullptr || y == nullptr || out == nullptr) return LRQ_ERR_NULL;
+  if (n_out < 1 || ldy < n_out || ldo < n_out) return LRQ_ERR_SHAPE;
+  if (!aligned(y, 2) || !aligned(out, 2)) return LRQ_ERR_ALIGN;
+  if (B == 0 || M == 0) return LRQ_OK;
+  LegacyGemmArgs a{};
+  a.l = (const uint16_t*)l, a.rt = (const uint16_t*)rt, a.q = (const uint8_t*)q, a.s = (const uint16_t*)s;
+  a.s_rows = s_rows, a.y = (const uint16_t*)y, a.ldy = ldy, a.out = (uint16_t*)out, a.ldo = ldo, a.M = M, a.N = N;
+  a.n_out = n_out;
+  const int64_t NB = N / (8 / bits);
+  const bool mfma_ok = vec_ok({l, rt, q, s}) && NB % 64 == 0 && n_out % 16 == 0 && aligned(y, 8) && ldy % 4 == 0;
+  hipStream_t hs = (hipStream_t)stream;
+  switch (bits) {
+    case 1: return legacy_gemm_bits<1>(a, K, B, mfma_ok, hs);
+    case 2: return legacy_gemm_bits<2>(a, K, B, mfma_ok, hs);
+    case 4: return legacy_gemm_bits<4>(a, K, B, mfma_ok, hs);
+    default: return legacy_gemm_bits<8>(a, K, B, mfma_ok, hs);
   }
 }
 

@@ -81,7 +81,8 @@ __global__ __launch_bounds__(512) void k_lora_grads(
     u32x2 gop;           // row j: g columns 4g ..
   };
   // 32-bit lane offsets from each block's wave-uniform bases; rows past the end repeat the last
-  // row (min on the offsets; row strides below 2^24 bytes, checked by the launch)
+  // row (min on the offsets against lim * ld, lim the block's last present row, at most 15: with
+  // row strides below 2^24 bytes, checked by the launch, every offset stays below 2^28)
   const uint32_t ldc1 = (uint32_t)ldc, ldq2 = (uint32_t)ldq * 2, ldl2 = (uint32_t)ldl * 2, ldg2 = (uint32_t)ldg * 2;
   uint32_t coff[4], qoff[4];
 #pragma unroll
@@ -93,7 +94,7 @@ __global__ __launch_bounds__(512) void k_lora_grads(
   const uint32_t cl = (uint32_t)(BPL * j), ql = (uint32_t)(u * NP * 4), rl = (uint32_t)(8 * g);
   auto load = [&](int rb, Blk& d) {
     const int r0 = rb * 16;
-    const uint32_t lim = (uint32_t)(M - 1 - r0);
+    const uint32_t lim = (uint32_t)min(M - 1 - r0, 15);
     const uint8_t* cbase = codes + (int64_t)r0 * ldc + u * G;
     const uint8_t* qbase = reinterpret_cast<const uint8_t*>(qparams + (int64_t)r0 * ldq);
 #pragma unroll

@@ -265,12 +265,7 @@ extern "C" int lrq_transpose_bf16(const void* src, int64_t rows, int64_t cols, v
 
 // k_colmax launch shape: one workgroup of 8 waves per CU (c3 shape, colmax entry: 36.1 us;
 // 4 waves x 4 per CU 39.3, 8 x 2 40.0, 16 x 1 39.5, 16 x 2 37.6)
-#ifndef LRQ_COLMAX_PH
-#define LRQ_COLMAX_PH 8
-#endif
-#ifndef LRQ_COLMAX_WPC
-#define LRQ_COLMAX_WPC 1
-#endif
+static constexpr int kColmaxPhases = 8, kColmaxWgPerCu = 1;
 extern "C" int lrq_colmax(const void* x, int64_t ldx, int64_t rows, int64_t hidden, float* colmax,
                           void* stream) {
   if (x == nullptr || colmax == nullptr) return LRQ_ERR_NULL;
@@ -281,11 +276,11 @@ extern "C" int lrq_colmax(const void* x, int64_t ldx, int64_t rows, int64_t hidd
                      (unsigned int*)colmax, hidden));
   if (rows == 0) return LRQ_OK;
   if ((hidden % 8) == 0 && (ldx % 8) == 0 && aligned(x, 16)) {
-    // about LRQ_COLMAX_WPC workgroups of LRQ_COLMAX_PH waves per CU (one atomic per column per
+    // about kColmaxWgPerCu workgroups of kColmaxPhases waves per CU (one atomic per column per
     // workgroup), row groups of whole PH * 16-row steps (PH phases x 16-row batches)
-    constexpr int PH = LRQ_COLMAX_PH;
+    constexpr int PH = kColmaxPhases;
     const int64_t cgroups = (hidden + 511) / 512;
-    int64_t groups = std::max<int64_t>(1, (int64_t)cu_count() * LRQ_COLMAX_WPC / cgroups);
+    int64_t groups = std::max<int64_t>(1, (int64_t)cu_count() * kColmaxWgPerCu / cgroups);
     int64_t rows_per = (rows + groups - 1) / groups;
     rows_per = (rows_per + 16 * PH - 1) / (16 * PH) * (16 * PH);
     groups = (rows + rows_per - 1) / rows_per;

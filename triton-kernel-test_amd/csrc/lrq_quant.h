@@ -12,14 +12,11 @@ namespace lrq {
 // Rank 16: x reaches fp32 through the MFMA pipe instead of VALU unpacking: an identity step
 // I * x (exact: one product of 1 per output, the rest zero) puts x[row][16g + 4q + v] in the
 // accumulator layout, and the reconstruction step adds -L V^T to it with one rounding, as above.
-#ifndef LRQ_RES_IDMFMA
-#define LRQ_RES_IDMFMA 1
-#endif
 template <int G, int R>
 __device__ __forceinline__ void residual_plane(const u32x4 (&x)[G / 32],
                                                const u32x2 (&vop)[G / 16][R > 0 ? R / 16 : 1],
                                                const u32x2* lopn, float* r) {
-  if constexpr (R == 16 && LRQ_RES_IDMFMA) {
+  if constexpr (R == 16) {
     const int l = __lane_id();
     const u32x2 ida = identity_bop(l & 15, l >> 4);  // A operand: I[i][4g + e], e < 4, for lane (i, g)
 #pragma unroll

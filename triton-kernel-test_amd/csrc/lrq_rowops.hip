@@ -1119,8 +1119,9 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t(
   };
   // A block's loads: 32-bit lane offsets from the block's wave-uniform bases.  Row clamping
   // (rows past M repeat the last row) is a min on the offsets, min(r, lim) * ld = min(r * ld,
-  // lim * ld), with the lane's r * ld computed once (row strides below 2^24 bytes, checked by the
-  // launch, keep every offset in 32 bits).
+  // lim * ld), with the lane's r * ld computed once.  lim is the last present row of the block,
+  // at most 15, so with row strides below 2^24 bytes (checked by the launch) every offset,
+  // lim * ld included, stays below 2^28.
   const uint32_t ldc1 = (uint32_t)ldc, ldq2 = (uint32_t)ldq * 2, ldl2 = (uint32_t)ldl * 2, ldg2 = (uint32_t)ldg * 2;
   uint32_t coff[4], qoff[4];
 #pragma unroll
@@ -1132,7 +1133,7 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t(
   const uint32_t cl = (uint32_t)(BPL * j), ql = (uint32_t)(ul * NP * 4), rl = (uint32_t)(8 * g);
   auto load = [&](int rb, Blk& d) {
     const int r0 = rb * 16;                  // wave-uniform
-    const uint32_t lim = (uint32_t)(M - 1 - r0);
+    const uint32_t lim = (uint32_t)min(M - 1 - r0, 15);
     const uint8_t* cbase = codes + (int64_t)r0 * ldc + u0 * G;
     const uint8_t* qbase = reinterpret_cast<const uint8_t*>(qparams + (int64_t)r0 * ldq);
 #pragma unroll
@@ -1660,8 +1661,9 @@ extern "C" int lrq_softmax_bwd(const lrq_tensors* t, const void* dp, int64_t ldd
   if (t->rows == 0) return LRQ_OK;
   if ((t->flags & LRQ_FLAG_HADAMARD) || t->n_outlier > 0) {
     // the rotated format and outlier channels: decode into ds (rotation undone, side columns
-    // substituted), then the dense backward in place over it; rows of exactly `hidden` elements
-    if (lddp != t->hidden || ldds != t->hidden) return LRQ_ERR_UNSUPPORTED;
+    // substituted), then the dense backward in place over it; rows of exactly `hidden` elements,
+    // and ds distinct from dp (the decode would overwrite dp before the backward reads it)
+    if (lddp != t->hidden || ldds != t->hidden || dp == ds) return LRQ_ERR_UNSUPPORTED;
     LRQ_TRY(lrq_decode(t, ds, ldds, stream));
     return lrq_dense_softmax_bwd(ds, dp, ds, t->rows, t->hidden, stream);
   }

@@ -39,7 +39,7 @@ class Config:
     outlier_scale: float = 1.0
     keep_channels: int = 0      # channels kept dense as fp16 side columns (top-k by abs-max)
     hadamard: bool = False
-    consumer: str = "decode"    # decode | silu | gelu | softmax | lora | legacy | ref_enc | ref_dec
+    consumer: str = "decode"    # decode | silu | gelu | softmax | lora | legacy | ref_enc | ref_dec | ref_mm
     lora_rank: int = 16         # consumer "lora": n of the LoRA factor A [hidden, n] and of g [rows, n]
     grad_std: float = 0.02
     seed: int = 0
@@ -72,6 +72,10 @@ CONFIGS = {
     # 72} there; bench.py --m picks it (default 8192).
     "ref_enc": Config("ref_enc", 4 * 8192, 8192, 16, 1, 0, consumer="ref_enc", seed=9, batch=4, tau=12.0),
     "ref_dec": Config("ref_dec", 4 * 8192, 8192, 16, 2, 0, consumer="ref_dec", seed=10, batch=4),
+    # the reference's fused dequant-matmul benchmark (extraction_fuse_matmul.py:425-436): codes
+    # q [4, M, M/4] (2-bit), l [M, 32], r [32, M], s [4, M] = N(0,1) + 2, y [4, M, 32]; out
+    # [4, M, 32].  bench.py --m picks M (default 4096).
+    "ref_mm": Config("ref_mm", 4 * 4096, 4096, 32, 2, 0, consumer="ref_mm", seed=11, batch=4),
 }
 
 REF_M = [256 * i for i in range(2, 80, 10)]  # the reference speed tests' sweep: 512 .. 18432

@@ -369,15 +369,32 @@ def triton_hadamard_add_extraction(l, r, q, s, b, quantize_bit=2):
 
 
 def triton_matmul_decompress(q, l, r, s, y, quantize_bit=2):
-    """(decode(q) ) @ y per batch: x_hat[B, M, N] @ y[B, N, n] -> bf16 [B, M, n].
-
-    The legacy per-column format is decoded by the HIP decode kernel and multiplied by the
-    library GEMM in fp32 (bf16 operands are exact in fp32), so the product is rounded to bf16
-    once, as the fused kernels round theirs; the fused dequant-GEMM kernel serves the
-    group-mode format (``api.dequant_gemm``)."""
-    a = _legacy_fused(_OP_STORE, l, r, q, s, None, quantize_bit)
-    _require_device(y)
-    return torch.matmul(a.float(), y.to(torch.bfloat16).float()).to(torch.bfloat16)
+    """decode(q) @ y per batch: x_hat[B, M, N] @ y[B, N, n] -> bf16 [B, M, n], in one kernel
+    (lrq_legacy_dequant_gemm): x_hat is rebuilt in registers and fed to the product MFMA, never
+    stored; fp32 sums rounded to bf16 once.  Output widths that are not a multiple of 16 are
+    computed on y zero-padded to one."""
+    bits = _bits(quantize_bit)
+    _require_device(q, y)
+    M, _ = l.shape
+    _, N = r.shape
+    B = q.shape[0]
+    if y.dim() != 3 or y.shape[0] != B or y.shape[1] != N:
+        raise ValueError(f"y must be [{B}, {N}, n], got {tuple(y.shape)}")
+    n = y.shape[2]
+    q = q.contiguous()
+    y = y.to(torch.bfloat16)
+    npad = (n + 15) // 16 * 16
+    if npad != n:
+        y = torch.nn.functional.pad(y, (0, npad - n))
+    y = y.contiguous()
+    with torch.cuda.device(q.device):
+        l2, rt, K = _factors(l, r)
+        s2 = _scale(s, B, N)
+        o = torch.empty((B, M, npad), device=q.device, dtype=torch.bfloat16)
+        if n > 0 and M > 0:
+            call("lrq_legacy_dequant_gemm", _p(l2), _p(rt), K, _p(q), _p(s2), s2.shape[0], B, M, N, bits, _p(y), npad,
+                 npad, _p(o), npad, _stream(q.device))
+    return o if npad == n else o[..., :n].contiguous()
 
 
 def _dense(op, x, y):
