@@ -7,7 +7,7 @@ rotate over several HBM-resident buffer sets (> 512 MB of X) so the 256 MB MALL 
 serve them.  Prints ONE JSON line (driver contract).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
-                  [--config north_star|c1|c2|c3|c4|c5|c5w|lora|legacy|ref_enc|ref_dec|ref_mm] [--m M]
+                  [--config north_star|c1|c2|c3|c4|c5|c5w|lora|legacy|ref_enc|ref_dec|ref_mm|offload] [--m M]
                   [--no-cpu-baseline]
 
 value       = activation GB/s = 2*rows*hidden bytes / (encode + decode time per step);
@@ -472,6 +472,102 @@ def build_plan(cfg, pkg, lib, dev, nbuf, lora_split=False):
     return entries, 2 * M * N, timed, sets
 
 
+def offload_bench(args, pkg, lib, dev):
+    """--config offload: the north-star compressed activation (codes, qparams, L: 37.2 MB)
+    offloaded to pinned host memory and prefetched back (offload.py, on its copy stream) while
+    the compute stream runs north-star encode + decode steps.  Times on the GPU (HIP events):
+    each copy alone, the compute alone, and both started together; the hidden fraction of a copy
+    is (copy + compute - both) / copy, 1.0 when the copy costs the compute nothing."""
+    import torch
+    OF = importlib.import_module("triton-kernel-test_amd.offload")
+    cfg = pkg.inputs.CONFIGS["north_star"]
+    entries, _, _, _ = build_plan(cfg, pkg, lib, dev, args.nbuf)
+    stream = torch.cuda.current_stream(dev)
+    x = pkg.inputs.activation(cfg.rows, cfg.hidden, cfg.n_outlier, cfg.outlier_scale, cfg.seed + 99, dev)
+    c = pkg.encode(x, pkg.LowRankBasis(pkg.inputs.basis(cfg.hidden, cfg.rank, cfg.seed).to(dev)), bits=cfg.bits,
+                   group_size=cfg.group)
+    del x
+    pool = OF.PinnedPool()
+
+    def steps(n):
+        for i in range(n):
+            for _, fn, _, _ in entries:
+                if fn(i % args.nbuf):
+                    raise RuntimeError("launch failed")
+
+    def run(copy, n):
+        """Returns (copy ms, compute ms) from a common start; copy None / n 0 leave one out."""
+        torch.cuda.synchronize()
+        torch.cuda._sleep(1 << 22)  # the host enqueues everything before the start
+        t0, tc = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        ev = copy() if copy is not None else None
+        steps(n)
+        tc.record(stream)
+        torch.cuda.synchronize()
+        return (t0.elapsed_time(ev) if ev is not None else 0.0), (t0.elapsed_time(tc) if n else 0.0)
+
+    held = []
+    # both copies run on `cs` and start after the common start (the offload makes its stream wait
+    # on the compute stream's queue; the prefetch's is made to); the prefetch's consumer is a side
+    # stream, so the compute stream does not wait for it
+    cs, side = torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)
+
+    def done_event():
+        e = torch.cuda.Event(enable_timing=True)
+        e.record(cs)
+        return e
+
+    def d2h():
+        # the previous host copies are complete (each run synchronises): back to the pool
+        for h in held:
+            h.release()
+        held.clear()
+        held.append(OF.offload(c, stream=cs, pool=pool))
+        return done_event()
+
+    def h2d():
+        cs.wait_stream(stream)
+        with torch.cuda.stream(side):
+            OF.prefetch(held[-1], dev, stream=cs)
+        return done_event()
+
+    for _ in range(3):  # warm: the pool holds the buffers after the first offload
+        run(d2h, 2)
+        run(h2d, 2)
+        for h in held:
+            h.release()
+        held.clear()
+    allocs0 = pool.allocations
+    res = {}
+    for name, fn in (("d2h", d2h), ("h2d", h2d)):
+        if name == "h2d":
+            run(d2h, 0)  # a host copy to read
+        alone = statistics.median(run(fn, 0)[0] for _ in range(5))
+        n = max(4, int(2.0 * alone / 0.062))  # about twice the copy's time of compute
+        comp = statistics.median(run(None, n)[1] for _ in range(5))
+        pairs = [run(fn, n) for _ in range(5)]
+        both = statistics.median(max(a, b) for a, b in pairs)
+        copy_in = statistics.median(a for a, _ in pairs)
+        res[name] = {"copy_alone_us": round(alone * 1e3, 1), "GBs_alone": round(c.nbytes() / (alone * 1e-3) / 1e9, 2),
+                     "copy_overlapped_us": round(copy_in * 1e3, 1), "compute_steps": n,
+                     "compute_alone_us": round(comp * 1e3, 1), "both_us": round(both * 1e3, 1),
+                     "hidden_frac": round((alone + comp - both) / alone, 4),
+                     "compute_slowdown": round(both / comp, 4)}
+        for h in held:
+            h.release()
+        held.clear()
+    line = {"metric": "offload: compressed-activation copy GB/s (device -> pinned host) and the fraction hidden "
+                      "behind encode + decode steps",
+            "value": res["d2h"]["GBs_alone"], "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+            "dtype": "u8", "data": "synthetic", "config": {"workload": "offload: north-star compressed activation, "
+                                                                       "copy stream against the step's kernels",
+                                                           "bytes": c.nbytes()},
+            "offload": res, "pool": {"allocations_after_warmup": pool.allocations - allocs0,
+                                     "cached_bytes": pool.cached_bytes}}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -484,6 +580,10 @@ def main():
     from importlib import import_module
     lib_mod = import_module("triton-kernel-test_amd._lib")
     lib = lib_mod.load()
+    if args.config == "offload":
+        dev = torch.device("cuda", 0)
+        torch.cuda.set_device(dev)
+        return offload_bench(args, pkg, lib, dev)
     cfg = pkg.inputs.CONFIGS[args.config]
     if args.m and cfg.consumer in ("ref_enc", "ref_dec", "ref_mm"):
         import dataclasses

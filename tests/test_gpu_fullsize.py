@@ -279,3 +279,32 @@ def test_fullsize_c5_softmax_rows(pkg, dev):
     ref = O.softmax_bwd(O.bf16_to_f32(ref_ph), O.bf16_to_f32(bits16(dp[rd])))
     rep = assert_fp_close(bits16(ds[rd]), ref, "c5 full-size softmax row sample", max_abs=1e-3)
     print(f"[full c5] row sample decode {rep_d} dS {rep}", flush=True)
+
+
+def test_fullsize_decode_xcd_split_equals_halves(pkg, dev):
+    """At the north-star shape the plain decode runs its XCD-weighted schedule (pairs of
+    workgroups split 32 row blocks as 18 + 14); decoding the same codes as two halves of 8192
+    rows (the kernel's loop, no split) gives the same bits, and a row sample from both kinds of
+    run matches the CPU oracle's decode."""
+    cfg = pkg.inputs.CONFIGS["north_star"]
+    M, N = cfg.rows, cfg.hidden
+    print(f"[full decode split] {M}x{N}", flush=True)
+    x = pkg.inputs.activation(M, N, cfg.n_outlier, cfg.outlier_scale, cfg.seed + 5, dev)
+    V = pkg.inputs.basis(N, cfg.rank, cfg.seed)
+    c = pkg.encode(x, V.to(dev), bits=cfg.bits, group_size=cfg.group)
+    whole = pkg.decode(c)
+    halves = []
+    for h in range(2):
+        sl = slice(h * M // 2, (h + 1) * M // 2)
+        part = pkg.CompressedActivation(codes=c.codes[sl], qparams=c.qparams[sl], L=c.L[sl], basis=c.basis,
+                                        side=None, idx=None, shape=(M // 2, N), bits=c.bits, group=c.group,
+                                        hadamard=False)
+        halves.append(pkg.decode(part))
+    torch.cuda.synchronize()
+    assert torch.equal(whole.view(torch.int16), torch.cat(halves).view(torch.int16))
+    # rows of even- and odd-XCD workgroups (each pair of workgroups covers 512 rows: the first
+    # 288 are the even one's, the rest the odd one's)
+    rows = torch.tensor([0, 287, 288, 511, 512 * 17 + 290, M - 1])
+    ref = O.decode(bits16(c.L[rows.to(dev)]), bits16(V), c.codes[rows.to(dev)].cpu().numpy(),
+                   f16(c.scale[rows.to(dev)]), f16(c.zero[rows.to(dev)]), cfg.bits, cfg.group)
+    assert_decode_close(bits16(whole[rows.to(dev)]), ref, "xcd split rows")

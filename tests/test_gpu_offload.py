@@ -27,3 +27,33 @@ def test_offload_prefetch_round_trip(pkg, dev):
     # wire format with a basis, on the device
     c3 = OF.from_state_dict(OF.to_state_dict(h), device=dev)
     assert torch.equal(pkg.decode(c3), ref)
+
+
+def test_offload_pool_reuse(pkg, dev):
+    """Offloads through one PinnedPool: after release() the next offload of the same shapes takes
+    the same pinned buffers (no new allocation), and each round trip still decodes to its own
+    activation's bits, also when the buffers are reused while a prefetch from them was queued."""
+    OF = importlib.import_module("triton-kernel-test_amd.offload")
+    pool = OF.PinnedPool()
+    V = pkg.inputs.basis(4096, 16, seed=3).to(dev)
+    acts = [pkg.encode(pkg.inputs.activation(520, 4096, 8, 20.0, seed=s).to(dev), V, bits=4, group_size=64)
+            for s in (31, 32, 33)]
+    refs = [pkg.decode(c) for c in acts]
+    h = OF.offload(acts[0], pool=pool)
+    n0 = pool.allocations
+    assert n0 == 3  # codes, qparams, L
+    back = OF.prefetch(h, dev)
+    h.release()  # the prefetch is still queued: the buffers wait for it
+    for c, ref in zip(acts[1:], refs[1:]):
+        h = OF.offload(c, pool=pool)
+        out = pkg.decode(OF.prefetch(h, dev))
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+        h.release()
+    assert torch.equal(pkg.decode(back), refs[0])
+    assert pool.allocations <= n0 + 3  # at most one more set, when the first was still in use
+    h = OF.offload(acts[0], pool=pool)
+    h.wait()
+    assert pool.allocations <= n0 + 3
+    torch.cuda.synchronize()
+    assert torch.equal(pkg.decode(OF.prefetch(h, dev)), refs[0])

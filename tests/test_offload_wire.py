@@ -38,3 +38,40 @@ def test_wire_version_refused(pkg):
     sd["meta"][0] = OF.WIRE_VERSION + 1
     with pytest.raises(ValueError):
         OF.from_state_dict(sd)
+
+
+class _Ev:
+    """Stands in for a copy's event: complete once `done` is set."""
+
+    def __init__(self, done=False):
+        self.done = done
+
+    def query(self):
+        return self.done
+
+
+def test_pinned_pool_reuses_after_the_copies_complete():
+    """PinnedPool (CPU, plain buffers in place of pinned ones): a returned buffer is handed out
+    again only once every event given with it has completed, within its size class; the cap
+    drops buffers instead of caching them."""
+    OF = importlib.import_module("triton-kernel-test_amd.offload")
+    pool = OF.PinnedPool(max_cached_bytes=3 << 16, alloc=lambda n: torch.empty(n, dtype=torch.uint8))
+    a = pool.take(1000)
+    assert a.numel() == 1 << 16 and pool.allocations == 1
+    pending, done = _Ev(False), _Ev(True)
+    pool.give(a, [done, pending])
+    b = pool.take(5000)  # same size class, but a copy still uses `a`
+    assert b.data_ptr() != a.data_ptr() and pool.allocations == 2
+    pending.done = True
+    c = pool.take(60000)
+    assert c.data_ptr() == a.data_ptr() and pool.allocations == 2
+    big = pool.take((1 << 16) + 1)  # the next size class
+    assert big.numel() == 2 << 16 and pool.allocations == 3
+    pool.give(big, [done])
+    pool.give(b, [done])
+    assert pool.cached_bytes == 3 << 16
+    pool.give(c, [done])  # over the cap: dropped
+    assert pool.cached_bytes == 3 << 16
+    assert pool.take(10).data_ptr() == b.data_ptr()
+    pool.clear()
+    assert pool.cached_bytes == 0

@@ -401,6 +401,9 @@ __global__ __launch_bounds__(NW * 64) void k_decode_staged(
 // OUTL (rank 0, at most kSideMax outlier channels): the fp16 side columns of each block are
 // staged with the codes, and reconstructed values of outlier columns are replaced by them.
 static constexpr int kSideMax = 64;
+// Row blocks the plain decode moves from each odd-XCD workgroup to its even-XCD partner (see
+// k_decode_rows): 2 of 16, for the odd XCDs' ~11 % lower decode rate after an encode.
+static constexpr int kDecodeXcdShift = 2;
 
 template <int BITS, int G, int NW>
 struct RowsOut {
@@ -426,10 +429,10 @@ struct RowsLayout {
   static constexpr size_t FIXED = 2 * (size_t)ISLOT + (IN && !INP ? 2 : 0) * (size_t)Ro::OSLOT + 2 * (size_t)Ro::OSLOT;
   static size_t bytes(int N) { return FIXED + (OUTL ? (size_t)(N / 32) * 4 + (size_t)N * 2 : 0); }
   // registers a block's prefetched inputs take per lane (drives the largest RBW)
-  static constexpr int kRegsPerBlock = 4 * Tl::CPT + 2 + (IN ? 4 * DPT : 0) + SPT;
+  static constexpr int kRegsPerBlock = 4 * Tl::CPT + 1 + (IN ? 4 * DPT : 0) + SPT;
 };
 
-template <int BITS, int G, int R, int NW, int PD, bool OUTL, bool INP, class EPI>
+template <int BITS, int G, int R, int NW, int PD, bool OUTL, bool INP, class EPI, int SLN>
 __global__ __launch_bounds__(NW * 64) void k_decode_rows(
     const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
     const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
@@ -456,9 +459,17 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
   const bool active = w < nu;
   const int vbytes = nu * G * 2;       // valid bytes of a row segment
   const int nrb = (M + 15) / 16;
-  const int rb0 = blockIdx.x * RBW;
+  // XCD-weighted runs (the plain decode's straight-line shape, an even grid that covers the rows
+  // exactly): workgroups are dealt to the 8 XCDs round robin, so with an even grid.x the odd
+  // blockIdx.x are the odd XCDs, which decode about 11 % slower than the even ones right after an
+  // encode (per-wave timestamps: every block of theirs, wherever its rows lie).  Each pair of
+  // workgroups splits its 2 RBW blocks as RBW + XS (even) and RBW - XS (odd).
+  constexpr int XS = kDecodeXcdShift;
+  const bool xsplit = SLN > XS && RBW == SLN && (gridDim.x & 1) == 0 && nrb == (int)gridDim.x * RBW;
+  const int xx = blockIdx.x;
+  const int rb0 = xsplit ? (xx / 2) * 2 * RBW + ((xx & 1) ? RBW + XS : 0) : xx * RBW;
   if (rb0 >= nrb) return;  // whole workgroup (no barrier reached)
-  const int nblk = min(RBW, nrb - rb0);
+  const int nblk = xsplit ? ((xx & 1) ? RBW - XS : RBW + XS) : min(RBW, nrb - rb0);
 
   if constexpr (OUTL) {
     for (int i = tid; i < N / 32; i += T) colmask[i] = 0u;
@@ -474,16 +485,19 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
     // made visible by the first block's barrier
   }
 
+  // V operands: requested right before the first blocks' inputs (below); unconditional (see
+  // below), waves past the last unit load the last unit's operands
   u32x2 vop[NP][G / 16][RT];
-  if constexpr (R > 0) {
-    // unconditional (see below); waves past the last unit load the last unit's operands
+  auto load_v = [&]() {
+    if constexpr (R > 0) {
 #pragma unroll
-    for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, min(u, units - 1), N, NP, G), j, g, vop[p]);
-  }
+      for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, min(u, units - 1), N, NP, G), j, g, vop[p]);
+    }
+  };
 
   struct In {
     u32x4 c[Tl::CPT];
-    u32x2 ql;
+    uint32_t ql;
     u32x4 d[IN ? Lay::DPT : 1];
     uint32_t sd[OUTL ? Lay::SPT : 1];
   };
@@ -492,13 +506,17 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
   // operations (the prefetched blocks included) before the next use of any load.  Lanes whose
   // chunk lies past the workgroup's units load a clamped (valid) address and stage the value
   // where nothing reads it; their stores are dropped by the buffer range check.
-  // qparams move as one 4-byte pair per lane (QROW / 4 per row, waves 0.. of the block), L as
-  // 8-byte chunks (the next waves); both splits are whole waves.
-  constexpr int QCH4 = 4 * Tl::QROW;
-  static_assert(QCH4 % 64 == 0 && Tl::LCH % 64 == 0 && QCH4 + Tl::LCH <= T, "qparam / L split in whole waves");
-  const int qk = tid, lk = tid - QCH4;
-  const bool has_q = qk < QCH4;
-  const bool has_l = R > 0 && lk >= 0 && lk < Tl::LCH;
+  // qparams and L move as 4-byte chunks, one per thread and block: threads 0 .. QCH4 - 1 take the
+  // qparam pairs (QROW / 4 per row), the next LCH4 threads the L row pieces, and any further
+  // threads repeat the last chunk (the same bytes to the same LDS word).  One unconditional load
+  // per thread: with a load under a per-lane branch the compiler waited for every outstanding
+  // load (vmcnt(0)) inside the prefetch, so no block could start before all had arrived.
+  constexpr int QCH4 = 4 * Tl::QROW, LCH4 = R > 0 ? 4 * Tl::LROW : 0;
+  static_assert(QCH4 + LCH4 <= T, "one qparam / L chunk per thread");
+  const int qlk = min(tid, QCH4 + LCH4 - 1);
+  const bool is_q = qlk < QCH4;  // wave-uniform except in the wave holding the q / L boundary
+  const int qr = qlk / (Tl::QROW / 4), qc4 = qlk % (Tl::QROW / 4);
+  const int lk = max(qlk - QCH4, 0), lr = lk / (R > 0 ? Tl::LROW / 4 : 1), lc4 = lk % (R > 0 ? Tl::LROW / 4 : 1);
   // tile chunk k -> (plane, row, 16-byte column chunk)
   auto chunk = [](int k, int& p, int& r, int& c16) {
     c16 = k % (Ro::OROW / 16);
@@ -520,14 +538,13 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
       const int k = tid + T * i, r = k / (Tl::CROW / 16), c16 = min(k % (Tl::CROW / 16), nu * (G / 16) - 1);
       in.c[i] = ld16_stream(cb0 + rowclamp(rb, r) * (uint32_t)ldc_b + ccol + c16 * 16);
     }
-    if (has_q) {
-      const int r = qk / (Tl::QROW / 4), c4 = min(qk % (Tl::QROW / 4), nu * NP - 1);
-      const unsigned char* qb0 = reinterpret_cast<const unsigned char*>(qparams) + (int64_t)rb * 16 * ldq_b;
-      in.ql[0] = ld4(qb0 + rowclamp(rb, r) * (uint32_t)ldq_b + (uint32_t)u0 * NP * 4 + c4 * 4);
-    } else if (has_l) {
-      const int r = lk / (Tl::LROW / 8), c8 = lk % (Tl::LROW / 8);
-      const unsigned char* lb0 = reinterpret_cast<const unsigned char*>(Lin) + (int64_t)rb * 16 * ldl_b;
-      in.ql = ld8(lb0 + rowclamp(rb, r) * (uint32_t)ldl_b + c8 * 8);
+    {
+      const unsigned char* qa = reinterpret_cast<const unsigned char*>(qparams) + (int64_t)rb * 16 * ldq_b +
+                                rowclamp(rb, qr) * (uint32_t)ldq_b + (uint32_t)u0 * NP * 4 + min(qc4, nu * NP - 1) * 4;
+      const unsigned char* la = R > 0 ? reinterpret_cast<const unsigned char*>(Lin) + (int64_t)rb * 16 * ldl_b +
+                                            rowclamp(rb, lr) * (uint32_t)ldl_b + lc4 * 4
+                                      : qa;
+      in.ql = ld4(is_q ? qa : la);
     }
     if constexpr (IN) {
       const unsigned char* ib0 = reinterpret_cast<const unsigned char*>(epi.in_row((int64_t)rb * 16));
@@ -556,13 +573,8 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
       const int k = tid + T * i, r = k / (Tl::CROW / 16), c16 = k % (Tl::CROW / 16);
       *reinterpret_cast<u32x4*>(slot + r * Tl::CROW + c16 * 16) = in.c[i];
     }
-    if (has_q) {
-      const int r = qk / (Tl::QROW / 4), c4 = qk % (Tl::QROW / 4);
-      *reinterpret_cast<uint32_t*>(slot + Tl::QOFF + r * Tl::QROW + c4 * 4) = in.ql[0];
-    } else if (has_l) {
-      const int r = lk / (Tl::LROW / 8), c8 = lk % (Tl::LROW / 8);
-      *reinterpret_cast<u32x2*>(slot + Tl::LOFF + r * Tl::LROW + c8 * 8) = in.ql;
-    }
+    *reinterpret_cast<uint32_t*>(slot + (is_q ? Tl::QOFF + qr * Tl::QROW + qc4 * 4 : Tl::LOFF + lr * Tl::LROW + lc4 * 4)) =
+        in.ql;
     if constexpr (IN) {
       unsigned char* ds = dsm + (b & 1) * Ro::OSLOT;
 #pragma unroll
@@ -617,29 +629,19 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
   const bool rot_live = (rot_q + 1) * (128 / G) <= nu;  // the block's units are all present
 
   In in[PD];
-#pragma unroll
-  for (int b = 0; b < PD; ++b)
-    if (b < nblk) load(in[b], rb0 + b);
-  __builtin_amdgcn_sched_barrier(0);
-
-#pragma unroll 1
-  for (int bb = 0; bb < nblk; bb += PD) {
-#pragma unroll
-  for (int k = 0; k < PD; ++k) {
-    const int b = bb + k;
-    if (b >= nblk) break;
-    const int rb = rb0 + b;
+  // Position b of the workgroup's sequence, row block rb, from ring slot k: stage it, store the
+  // tile of position b - 1 (row block rb_prev), then NEXT(): whatever the caller requests with the
+  // slot free (RELOAD 1: row block rb + PD if position b + PD exists; 2: always; 0: nothing), then
+  // reconstruct block b into its tile.
+  auto body_at = [&](auto kc, int b, int rb, int rb_prev, auto next) {
+    constexpr int k = decltype(kc)::value;
     stage(in[k], b);
     lds_barrier();
-    if (b > 0) store_tile(rb - 1, b - 1);
+    if (b > 0) store_tile(rb_prev, b - 1);
     // in place: block b + 1's dY goes into the tile just stored, so every wave's reads of it
     // must have returned first
     if constexpr (INP) lds_barrier();
-    if (b + PD < nblk) {
-      __builtin_amdgcn_sched_barrier(0);
-      load(in[k], rb + PD);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    next();
     if (active) {
       const unsigned char* slot = ism + (b & 1) * Lay::ISLOT;
       u32x4 cb[G / 64];
@@ -731,7 +733,55 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
         }
       }
     }
-  }
+  };
+  auto body = [&](auto kc, int b, auto reload) {
+    constexpr int k = decltype(kc)::value;
+    const int rb = rb0 + b;
+    body_at(kc, b, rb, rb - 1, [&]() {
+      if constexpr (decltype(reload)::value != 0) {
+        if (decltype(reload)::value == 2 || b + PD < nblk) {
+          __builtin_amdgcn_sched_barrier(0);
+          load(in[k], rb + PD);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    });
+  };
+  // Straight-line code for the workgroup's usual block counts (SLN, or SLN -+ XS under the XCD
+  // split): every block without conditions, so that each block waits only for its own loads (a
+  // counted vmcnt).  Under the loop below (or loads under conditions) the compiler merges the
+  // paths' pending counts and each block waited for every outstanding memory operation, the
+  // previous block's stores included.  (The V operands first: loads retire in issue order, so
+  // block 0 waits for them and its own inputs, not for the later blocks'.)
+  auto straight = [&](auto sln) {
+    constexpr int SL = decltype(sln)::value;
+    load_v();
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, (PD < SL ? PD : SL)>([&](auto kc) { load(in[decltype(kc)::value], rb0 + decltype(kc)::value); });
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, SL>([&](auto bc) {
+      constexpr int b = decltype(bc)::value;
+      body(std::integral_constant<int, b % PD>{}, b, std::integral_constant<int, (b + PD < SL) ? 2 : 0>{});
+    });
+  };
+  if (SLN > 0 && nblk == SLN) {
+    straight(std::integral_constant<int, SLN>{});
+  } else if (SLN > XS && nblk == SLN - XS) {
+    straight(std::integral_constant<int, (SLN > XS ? SLN - XS : 1)>{});
+  } else if (SLN > XS && nblk == SLN + XS) {
+    straight(std::integral_constant<int, SLN + XS>{});
+  } else {
+    load_v();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int b = 0; b < PD; ++b)
+      if (b < nblk) load(in[b], rb0 + b);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll 1
+    for (int bb = 0; bb < nblk; bb += PD)
+      static_for<0, PD>([&](auto kc) {
+        if (bb + decltype(kc)::value < nblk) body(kc, bb + decltype(kc)::value, std::integral_constant<int, 1>{});
+      });
   }
   lds_barrier();
   store_tile(rb0 + nblk - 1, nblk - 1);
@@ -748,6 +798,11 @@ constexpr int rows_nw() { return G * (8 / BITS) <= 128 ? 8 : 4; }
 // holds up to 16 blocks of staged inputs within a register budget of about 180 VGPRs (rank 32:
 // 160, its V operands are twice as large; consumers: 100, their epilogue and the streamed loop
 // need the rest).
+// Row blocks per workgroup that the plain decode runs as straight-line code (other counts, and
+// the consumers, take the kernel's loop): the count the grid below gives at 16384 rows and 4096
+// columns.  (Straight-line code for every instantiation would multiply the compile time.)
+constexpr int kDecodeRun = 16;
+
 template <int BITS, int G, int R, bool OUTL, class EPI>
 static int decode_rows_launch(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
   constexpr int NW = rows_nw<BITS, G>();
@@ -772,7 +827,8 @@ static int decode_rows_launch(const lrq_tensors* t, hipStream_t s, const EPI& ep
   const int rbw = (int)((nrb + per - 1) / per);
   const size_t shm = Lay::bytes(N);
   if (shm > 160 * 1024) return LRQ_ERR_UNSUPPORTED;
-  auto kern = k_decode_rows<BITS, G, R, NW, PD, OUTL, INP, EPI>;
+  constexpr int SLN = (!EPI::kIn && !EPI::kRot && !OUTL) ? kDecodeRun : 0;
+  auto kern = k_decode_rows<BITS, G, R, NW, PD, OUTL, INP, EPI, SLN>;
   if (shm > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
   LRQ_TRY(launch(kern, dim3((unsigned)((nrb + rbw - 1) / rbw), (unsigned)ug), dim3(NW * 64), shm, s,
                      (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp,

@@ -452,7 +452,7 @@ __global__ __launch_bounds__(NW * 64) void k_encode_rows(
       // rows), which need not complete here.  Block 0's loads are the prologue's last memory
       // operations.
       static_assert(dma_begin<UPW>(UPW + 2) == Re::NLD, "the schedule issues every load of a block once");
-      constexpr int kAfter = dma_units_after<UPW>() * (E / 16) + 1 + RT;
+      constexpr int kAfter = dma_units_after<UPW>() * quant_core_stores<G>() + 1 + RT;
       static_assert(kAfter < 16, "vmcnt immediate");
       if (b == 0)
         __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
@@ -652,12 +652,13 @@ __global__ __launch_bounds__(512) void k_encode_tiles(const uint16_t* __restrict
   const int lr = lane >> 4, lq = lane & 15;
   const uint32_t ldx2 = (uint32_t)ldx * 2u;
   auto tile_ptr = [&](int i) { return shm + (size_t)(w + NW * i) * TILE; };
+  constexpr int kTileLoads = 4;  // load instructions per tile (4 rows each)
   auto issue_tile = [&](int rb, int i) {
     const int t = w + NW * i;
     const int lim = M - 1 - rb * 16;  // last row of the block that exists (>= 0)
     const unsigned char* base = reinterpret_cast<const unsigned char*>(X + (int64_t)rb * 16 * ldx) + 256 * t;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < kTileLoads; ++k) {
       const int r = 4 * k + lr;
       ld16_to_lds(base + ((uint32_t)min(r, lim) * ldx2 + 16u * (uint32_t)(lq ^ r)), tile_ptr(i) + 1024 * k);
     }
@@ -682,12 +683,18 @@ __global__ __launch_bounds__(512) void k_encode_tiles(const uint16_t* __restrict
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  // memory operations of this wave after each tile's loads, up to its rotation (see above)
-  using C5 = std::integral_constant<int, 5>;
-  using C13 = std::integral_constant<int, 13>;
-  using C18 = std::integral_constant<int, 18>;
-  using C19 = std::integral_constant<int, 19>;
-  using C20 = std::integral_constant<int, 20>;
+  // Memory operations of this wave issued after each tile's loads, up to its rotation, from the
+  // block's schedule below (T_i = the next block's tile i, U_u = unit u's stores, Ls = the L row
+  // store): T_0 T_1 T_2 U_0 T_3 U_1 U_2 [rotate T_0] T_4 U_3 [rotate T_1] U_4 Ls [rotate T_2,
+  // T_3] ... [rotate T_4 at the next block's top].  Any change to the schedule or to the stores
+  // a unit issues changes these counts with it.
+  constexpr int TL = kTileLoads, US = quant_unit_stores<G>(), LS = 1;
+  using C_T0 = std::integral_constant<int, 2 * TL + US + TL + 2 * US>;
+  using C_T1 = std::integral_constant<int, TL + US + TL + 2 * US + TL + US>;
+  using C_T2 = std::integral_constant<int, US + TL + 2 * US + TL + 2 * US + LS>;
+  using C_T3 = std::integral_constant<int, 2 * US + TL + 2 * US + LS>;
+  using C_T4 = std::integral_constant<int, 2 * US + LS>;
+  static_assert(C_T1::value < 64 && C_T2::value < 64, "vmcnt immediate (6 bits)");
 
   // Prologue: block rb0 (HBM) first, then the V operands (L2-resident after the first
   // workgroups).
@@ -710,12 +717,12 @@ __global__ __launch_bounds__(512) void k_encode_tiles(const uint16_t* __restrict
     constexpr bool next = decltype(next_tag)::value;
     const int rb = __builtin_amdgcn_readfirstlane(rb0 + b);
     const int row = min(rb * 16 + j, M - 1);
-    // T_4 of this block: 5 operations after it (units 3, 4 and the L store of the previous
-    // block; none after the prologue)
+    // T_4 of this block: units 3, 4 and the L store of the previous block after it (none after
+    // the prologue)
     if (b == 0)
       rotate_tile(UPW - 1, std::integral_constant<int, 0>{}, true);
     else
-      rotate_tile(UPW - 1, C5{}, true);
+      rotate_tile(UPW - 1, C_T4{}, true);
     lds_barrier();  // every tile landed and rotated
     u32x4 x[UPW][NP][CPG];
 #pragma unroll
@@ -785,18 +792,18 @@ __global__ __launch_bounds__(512) void k_encode_tiles(const uint16_t* __restrict
     unit(1);
     unit(2);
     if (next) {
-      rotate_tile(0, C18{});
+      rotate_tile(0, C_T0{});
       issue_tile(rb + 1, 4);
     }
     unit(3);
-    if (next) rotate_tile(1, C20{});
+    if (next) rotate_tile(1, C_T1{});
     unit(4);
     st8_pred(Lout + (int64_t)rb * 16 * ldl, (uint32_t)(16 * ldl * 2), (uint32_t)(((row - rb * 16) * ldl + 4 * g) * 2),
              lop[0], w == 0);
     __builtin_amdgcn_sched_barrier(0);
     if (next) {
-      rotate_tile(2, C19{});
-      rotate_tile(3, C13{});
+      rotate_tile(2, C_T2{});
+      rotate_tile(3, C_T3{});
     }
   };
 #pragma unroll 1

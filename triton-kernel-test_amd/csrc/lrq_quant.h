@@ -68,6 +68,13 @@ __device__ __forceinline__ void local_minmax(const float* r, float& mn, float& m
 // stores repeat its bytes, so no store is predicated (on gfx9 a predicated store makes the
 // compiler drain all outstanding memory operations, prefetches included, at the next use
 // of a load).
+// Memory operations (stores) one call of quant_unit_core / quant_unit issues per lane: kernels
+// that wait with counted vmcnt derive their counts from these.
+template <int G>
+constexpr int quant_core_stores() { return G / 4 / 16; }
+template <int G>
+constexpr int quant_unit_stores() { return quant_core_stores<G>() + 1; }
+
 // Core of quant_unit: stores the lane's code bytes and returns the (scale, zero) pair this lane
 // computed (with two planes: plane 0's in lanes 0..31, plane 1's in lanes 32..63).
 template <int BITS, int G, int R>
@@ -77,6 +84,7 @@ __device__ __forceinline__ uint32_t quant_unit_core(const u32x4 (&x)[8 / BITS][G
                                                     int g, uint8_t* __restrict__ crow) {
   constexpr int NP = 8 / BITS, E = G / 4;
   static_assert(NP == 1 || NP == 2, "group mode packs 4- or 8-bit codes");
+  static_assert(E % 16 == 0 && E / 16 == quant_core_stores<G>(), "one 16-byte code store per 16 code bytes");
   float r[NP][E];
   float mn[NP], mx[NP];
 #pragma unroll
@@ -118,7 +126,7 @@ __device__ __forceinline__ uint32_t quant_unit_core(const u32x4 (&x)[8 / BITS][G
 #pragma unroll
   for (int i = 0; i < E / 4; ++i) word[i] = gather_bytes(byte[4 * i], byte[4 * i + 1], byte[4 * i + 2], byte[4 * i + 3]);
 #pragma unroll
-  for (int i = 0; i < E / 16; ++i)
+  for (int i = 0; i < quant_core_stores<G>(); ++i)
     st16(crow + u * G + E * g + 16 * i, u32x4{word[4 * i], word[4 * i + 1], word[4 * i + 2], word[4 * i + 3]});
   return qp;
 }
@@ -129,6 +137,7 @@ __device__ __forceinline__ void quant_unit(const u32x4 (&x)[8 / BITS][G / 32],
                                            const u32x2* lopn, const uint32_t* colmask, int u, int N, int g,
                                            uint8_t* __restrict__ crow, uint16_t* __restrict__ qrow) {
   const uint32_t qp = quant_unit_core<BITS, G, R>(x, vop, lopn, colmask, u, N, g, crow);
+  static_assert(quant_unit_stores<G>() == quant_core_stores<G>() + 1, "the core's stores and one qparams store");
   if constexpr (8 / BITS == 2)
     st4(qrow + u * 4 + (g >> 1) * 2, qp);  // lanes g, g^1 write the same pair
   else

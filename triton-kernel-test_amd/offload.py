@@ -8,7 +8,9 @@ whatever the compute stream does meanwhile.
 
 * ``offload(c)`` starts the device -> host copy of a CompressedActivation and returns a
   ``HostCompressed`` at once; the copy is ordered after the work already queued on the current
-  stream (the encode that produced ``c``).
+  stream (the encode that produced ``c``).  The host buffers come from a ``PinnedPool`` (one per
+  process by default) and go back to it with ``HostCompressed.release()``: a training loop that
+  offloads the same shapes every step allocates pinned memory in its first step only.
 * ``prefetch(h, device)`` starts the host -> device copy and returns a CompressedActivation
   whose tensors the current stream may use right away (the stream waits on the copy's event,
   on the GPU, not on the host).
@@ -19,17 +21,78 @@ whatever the compute stream does meanwhile.
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Optional
 
 import torch
 
 from .api import CompressedActivation, LowRankBasis
 
-__all__ = ["HostCompressed", "offload", "prefetch", "to_state_dict", "from_state_dict", "WIRE_VERSION"]
+__all__ = ["HostCompressed", "PinnedPool", "default_pool", "offload", "prefetch", "to_state_dict",
+           "from_state_dict", "WIRE_VERSION"]
 
 WIRE_VERSION = 1
 _FIELDS = ("codes", "qparams", "L", "side", "idx")
+
+
+class PinnedPool:
+    """Pinned host buffers reused across offloads.
+
+    ``take(n)`` hands out a flat uint8 buffer of at least ``n`` bytes: a free buffer of the same
+    size class (``n`` rounded up to 64 KiB) whose last copies have completed, else a new pinned
+    allocation.  ``give(buf, events)`` returns it together with the events of the copies that
+    still read or write it; it is handed out again only once every one of them has completed
+    (``Event.query()``), so a buffer is never overwritten under a copy in flight.  At most
+    ``max_cached_bytes`` are kept; buffers past that are dropped (freed).  Not thread-safe: use
+    one pool per thread that offloads.
+    """
+
+    GRAIN = 1 << 16
+
+    def __init__(self, max_cached_bytes: int = 16 << 30, alloc=None):
+        self.max_cached_bytes = int(max_cached_bytes)
+        self._alloc = alloc if alloc is not None else (
+            lambda n: torch.empty(n, dtype=torch.uint8, pin_memory=True))
+        self._free: dict = {}  # size class -> [(buffer, [events])]
+        self.cached_bytes = 0
+        self.allocations = 0   # pinned allocations made (pool misses)
+
+    def _cls(self, n: int) -> int:
+        return max(self.GRAIN, (int(n) + self.GRAIN - 1) // self.GRAIN * self.GRAIN)
+
+    def take(self, n: int) -> torch.Tensor:
+        cls = self._cls(n)
+        lst = self._free.get(cls, [])
+        for i, (buf, evs) in enumerate(lst):
+            if all(e.query() for e in evs):
+                del lst[i]
+                self.cached_bytes -= cls
+                return buf
+        self.allocations += 1
+        return self._alloc(cls)
+
+    def give(self, buf: torch.Tensor, events=()) -> None:
+        cls = buf.numel()
+        if cls != self._cls(cls) or self.cached_bytes + cls > self.max_cached_bytes:
+            return  # not one of ours, or over the cap: let it be freed
+        self._free.setdefault(cls, []).append((buf, [e for e in events if e is not None]))
+        self.cached_bytes += cls
+
+    def clear(self) -> None:
+        """Drop every cached buffer (each is freed once no copy uses it any more)."""
+        self._free.clear()
+        self.cached_bytes = 0
+
+
+_default_pool: Optional[PinnedPool] = None
+
+
+def default_pool() -> PinnedPool:
+    """The process-wide pool ``offload`` uses when it is given none."""
+    global _default_pool
+    if _default_pool is None:
+        _default_pool = PinnedPool()
+    return _default_pool
 
 
 @dataclass
@@ -42,6 +105,10 @@ class HostCompressed:
     group: int
     hadamard: bool
     event: Optional[torch.cuda.Event] = None
+    # pool buffers behind `tensors`, and the events of the copies that read them since (prefetch)
+    pool: Optional[PinnedPool] = None
+    buffers: list = field(default_factory=list)
+    readers: list = field(default_factory=list)
 
     def wait(self) -> "HostCompressed":
         """Block the host until the device -> host copy has landed."""
@@ -51,6 +118,14 @@ class HostCompressed:
 
     def nbytes(self) -> int:
         return sum(t.numel() * t.element_size() for t in self.tensors.values())
+
+    def release(self) -> None:
+        """Give the host buffers back to the pool.  The tensors must not be used afterwards; the
+        buffers are reused only after the offload's copy and every prefetch from them completed."""
+        if self.pool is not None:
+            for b in self.buffers:
+                self.pool.give(b, [self.event, *self.readers])
+        self.buffers, self.readers, self.tensors = [], [], {}
 
 
 _copy_streams: dict = {}
@@ -68,21 +143,31 @@ def _device_tensors(c: CompressedActivation) -> dict:
     return {k: getattr(c, k) for k in _FIELDS if getattr(c, k) is not None}
 
 
-def offload(c: CompressedActivation, stream: Optional[torch.cuda.Stream] = None) -> HostCompressed:
-    """Asynchronous device -> host copy of ``c`` into pinned buffers."""
+def _host_view(buf: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
+    n = like.numel() * like.element_size()
+    return buf[:n].view(like.dtype).view(like.shape)
+
+
+def offload(c: CompressedActivation, stream: Optional[torch.cuda.Stream] = None,
+            pool: Optional[PinnedPool] = None) -> HostCompressed:
+    """Asynchronous device -> host copy of ``c`` into pinned buffers from ``pool`` (the process's
+    default pool when None)."""
     dev = c.device
+    pool = pool if pool is not None else default_pool()
     s = stream if stream is not None else _copy_stream(dev)
     s.wait_stream(torch.cuda.current_stream(dev))  # after the producer of c
-    host = {}
+    host, bufs = {}, []
     with torch.cuda.stream(s):
         for k, t in _device_tensors(c).items():
-            h = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+            buf = pool.take(t.numel() * t.element_size())
+            bufs.append(buf)
+            h = _host_view(buf, t)
             h.copy_(t, non_blocking=True)
             t.record_stream(s)  # the device buffer stays alive until the copy is done
             host[k] = h
         ev = torch.cuda.Event()
         ev.record(s)
-    return HostCompressed(host, c.basis, tuple(c.shape), c.bits, c.group, c.hadamard, ev)
+    return HostCompressed(host, c.basis, tuple(c.shape), c.bits, c.group, c.hadamard, ev, pool, bufs)
 
 
 def prefetch(h: HostCompressed, device: torch.device, stream: Optional[torch.cuda.Stream] = None
@@ -100,6 +185,7 @@ def prefetch(h: HostCompressed, device: torch.device, stream: Optional[torch.cud
             dev[k] = d
         ev = torch.cuda.Event()
         ev.record(s)
+    h.readers.append(ev)  # the host buffers are not reused before this copy has read them
     cur = torch.cuda.current_stream(device)
     cur.wait_event(ev)
     for d in dev.values():
