@@ -7,7 +7,7 @@ rotate over several HBM-resident buffer sets (> 512 MB of X) so the 256 MB MALL 
 serve them.  Prints ONE JSON line (driver contract).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
-                  [--config north_star|c1|c2|c3|c4|c5|c5w|lora|legacy|ref_enc|ref_dec|ref_mm|offload] [--m M]
+                  [--config north_star|c1|c2|c3|c4|c5|c5w|lora|legacy|ref_enc|ref_dec|ref_mm|offload|copy] [--m M]
                   [--no-cpu-baseline]
 
 value       = activation GB/s = 2*rows*hidden bytes / (encode + decode time per step);
@@ -584,6 +584,17 @@ def main():
         dev = torch.device("cuda", 0)
         torch.cuda.set_device(dev)
         return offload_bench(args, pkg, lib, dev)
+    if args.config == "copy":
+        # counter calibration: 5 device copies of 128 MiB (the traffic summaries scale
+        # rocprofv3's FETCH_SIZE / WRITE_SIZE by what these report for a known byte count)
+        n = 128 * 1024 * 1024
+        a = torch.ones(n, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"metric": "copy: calibration copies", "bytes_each": n, "copies": 5}), flush=True)
+        return
     cfg = pkg.inputs.CONFIGS[args.config]
     if args.m and cfg.consumer in ("ref_enc", "ref_dec", "ref_mm"):
         import dataclasses
