@@ -619,43 +619,65 @@ __global__ __launch_bounds__(512) void k_legacy_gemm(LegacyGemmArgs a) {
       d.cb[i] = ld16_stream(qb + row * NB + u * G + E * g);
     }
   };
+  // x_hat = bf16(a + bf16(l @ r)) with a = bf16((code - 2^(b-1)) * s), as legacy_value, two columns
+  // at a time: (code - 2^(b-1)) * s is fma(code, s, -2^(b-1) s), exact in fp32 (an integer of at
+  // most 8 bits times a bf16), and already a bf16 value for 1 and 2 bits (|code - 2^(b-1)| <= 2);
+  // each bf16 rounding is one v_cvt_pk_bf16_f32 (round to nearest even, as bf16r) per pair, and
+  // the last one leaves the pair packed as the product's operand.
   auto compute_item = [&](const Item& d, int p) {
     u32x4 yt[G / 32][TO];
     transpose_vops<G, NOUT>(d.ya, ident, yt);
-    float sc[E];
+    float sc[E], zb[E];
     unpack8(d.sc[0], sc);
     unpack8(d.sc[1], sc + 8);
+#pragma unroll
+    for (int e = 0; e < E; ++e) zb[e] = -(float)(1 << (BITS - 1)) * sc[e];
     const int sh = BITS * p;
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
-      float lr[E], xh[E];
+      float lr[E];
       residual_unit<G, K>(d.vop, lop[i], zero, lr);
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        const uint32_t code = (d.cb[i][e >> 2] >> (8 * (e & 3) + sh)) & kMask;
-        xh[e] = legacy_value<BITS, false>(code, sc[e], 0.f, bf16r(lr[e]));
-      }
       u32x4 xb[G / 32];
 #pragma unroll
-      for (int k = 0; k < G / 32; ++k) {
-        const float* f = xh + 8 * k;
-        xb[k] = u32x4{pack_bf16x2_exact(f[0], f[1]), pack_bf16x2_exact(f[2], f[3]), pack_bf16x2_exact(f[4], f[5]),
-                      pack_bf16x2_exact(f[6], f[7])};
+      for (int e = 0; e < E; e += 2) {
+        const uint32_t lp = pack_bf16x2(lr[e], lr[e + 1]);  // bf16(l @ r) of both columns
+        float av[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t code = (d.cb[i][(e + h) >> 2] >> (8 * ((e + h) & 3) + sh)) & kMask;
+          av[h] = __builtin_fmaf((float)code, sc[e + h], zb[e + h]);
+        }
+        if constexpr (BITS > 2) {
+          const uint32_t ap = pack_bf16x2(av[0], av[1]);
+          av[0] = bf_lo(ap);
+          av[1] = bf_hi(ap);
+        }
+        xb[e / 8][(e / 2) % 4] = pack_bf16x2(av[0] + bf_lo(lp), av[1] + bf_hi(lp));
       }
       project_unit_vt<G, NOUT>(yt, xb, acc[i]);
     }
   };
-  const int nit = w < ni ? (ni - w + NW - 1) / NW : 0;
+  // Items w, w + NW, ... through the two slots.  The loop body has no condition (a compute under
+  // a branch made the compiler wait for every outstanding load, the other slot's included, at the
+  // join); an odd last item runs after the loop.  NW is a multiple of NP, so every item of a wave
+  // is in plane w % NP.
+  static_assert(NW % NP == 0, "one plane per wave");
+  const int nit = w < ni ? (ni - w + NW - 1) / NW : 0, pw = w % NP;
   Item ring[2];
 #pragma unroll
   for (int sl = 0; sl < 2; ++sl) load_item(min(w + sl * NW, ni - 1), ring[sl]);
-  for (int i0 = 0; i0 < nit; i0 += 2) {
-#pragma unroll
-    for (int sl = 0; sl < 2; ++sl) {
-      if (i0 + sl < nit) compute_item(ring[sl], (w + (i0 + sl) * NW) % NP);  // wave-uniform
-      load_item(min(w + (i0 + sl + 2) * NW, ni - 1), ring[sl]);
-    }
+  int i0 = 0;
+  for (; i0 + 1 < nit; i0 += 2) {
+    compute_item(ring[0], pw);
+    __builtin_amdgcn_sched_barrier(0);
+    load_item(min(w + (i0 + 2) * NW, ni - 1), ring[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    compute_item(ring[1], pw);
+    __builtin_amdgcn_sched_barrier(0);
+    load_item(min(w + (i0 + 3) * NW, ni - 1), ring[1]);
+    __builtin_amdgcn_sched_barrier(0);
   }
+  if (i0 < nit) compute_item(ring[0], pw);  // wave-uniform
 
   // acc[i][t] in lane (j, g), component v: out[row j][16t + 4g + v] (partial over this wave's items)
   constexpr int F = TO * 256 / NW, S = 64 / F, PPL = NW / S;
