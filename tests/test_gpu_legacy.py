@@ -396,6 +396,39 @@ def test_legacy_decode_dense_coo(pkg, dev, B, M, N, bits):
     assert _frac_mismatch(bits16(a), xh_ref) <= TIE_BUDGET
 
 
+# shapes large enough for the row-tile decode (k_legacy_rows: at least two ring rounds of 4 blocks
+# per workgroup at about two workgroups per CU): 2, 4 and 8 bits, K 16 and 32, ragged rows, a last
+# workgroup of 2 units (18 units per plane), the reference decode test's outliers
+@pytest.mark.parametrize("B,M,N,K,bits", [(4, 4096, 4096, 16, 2), (4, 4100, 4608, 16, 2), (1, 16384, 4096, 32, 4),
+                                          (2, 8192, 2048, 16, 8)])
+def test_legacy_decode_row_tiles(pkg, dev, B, M, N, K, bits):
+    """The row-tile decode, from COO outliers and without outliers, gives the bits of the decode
+    that reads dense outliers (k_legacy_mfma), and a row sample matches the oracle."""
+    print(f"[row-tile decode] B={B} M={M} N={N} K={K} bits={bits}", flush=True)
+    g = torch.Generator(device=dev)
+    g.manual_seed(5000 + N + bits)
+    l = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    r = torch.randn(K, N, generator=g, device=dev).to(torch.bfloat16)
+    s = (torch.randn(B, N, generator=g, device=dev) + 2).to(torch.bfloat16)
+    q = torch.randint(0, 256, (B, M, N * bits // 8), generator=g, device=dev, dtype=torch.uint8)
+    o = torch.randn(B, M, N, generator=g, device=dev).to(torch.bfloat16)
+    o = o * (o > 1)
+    oc = pkg.compact_outliers(o, capacity=o.numel())
+    dec = pkg.low_rank_addition_fuse_decompression_dequantization
+    a = dec(l, r, q, oc, s, quantize_bit=bits)
+    c = dec(l, r, q, o, s, quantize_bit=bits)
+    a0 = dec(l, r, q, None, s, quantize_bit=bits)
+    c0 = dec(l, r, q, torch.zeros_like(o), s, quantize_bit=bits)
+    torch.cuda.synchronize()
+    assert torch.equal(a, c), "COO row-tile decode differs from the dense-outlier decode"
+    assert torch.equal(a0, c0), "outlier-free row-tile decode differs from the decode of zero outliers"
+    rows = torch.tensor([0, 1, 15, 16, M // 2 + 3, M - 1])
+    for bb in range(B):
+        xh_ref = O.legacy_decode(bits16(l[rows]), bits16(r), q[bb][rows].cpu().numpy()[None],
+                                 bits16(o[bb][rows])[None], bits16(s[bb:bb + 1]), bits)
+        assert _frac_mismatch(bits16(a[bb][rows])[None], xh_ref) <= TIE_BUDGET
+
+
 @pytest.mark.parametrize("M,N,K", [(256, 1024, 16), (50, 100, 20), (128, 2048, 32)])
 def test_outlier_threshold_is_kthvalue(pkg, dev, M, N, K):
     """outlier_threshold = torch.kthvalue(|x[0] - l @ r|, int(numel * 0.99)) of

@@ -166,7 +166,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode(
   }
 
   using In = DecIn<BITS, G, R, EPI::kIn>;
-  auto load = [&](In& in, int rb) {
+  auto load = [&](In& in, int rb) __attribute__((always_inline)) {
     const int64_t row = min(rb * 16 + j, M - 1);
     const uint8_t* cp = codes + row * ldc + u * G + E * g;
 #pragma unroll
@@ -192,7 +192,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode(
     }
   };
 
-  auto compute = [&](const In& in, int rb) {
+  auto compute = [&](const In& in, int rb) __attribute__((always_inline)) {
     const int64_t rr = min(rb * 16 + j, M - 1);
     uint16_t* orow = epi.out_row(rr);
 #pragma unroll
@@ -297,7 +297,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_staged(
   const int qk = tid, lk = tid - Tl::QCH;
   const bool has_q = qk < Tl::QCH && (qk % (Tl::QROW / 8)) * 8 < nu * NP * 4;
   const bool has_l = R > 0 && lk >= 0 && lk < Tl::LCH;
-  auto load = [&](In& in, int rb) {
+  auto load = [&](In& in, int rb) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < Tl::CPT; ++i) {
       const int k = tid + T * i, r = k / (Tl::CROW / 16), c16 = k % (Tl::CROW / 16);
@@ -488,7 +488,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
   // V operands: requested right before the first blocks' inputs (below); unconditional (see
   // below), waves past the last unit load the last unit's operands
   u32x2 vop[NP][G / 16][RT];
-  auto load_v = [&]() {
+  auto load_v = [&]() __attribute__((always_inline)) {
     if constexpr (R > 0) {
 #pragma unroll
       for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, min(u, units - 1), N, NP, G), j, g, vop[p]);
@@ -530,8 +530,8 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
   const uint32_t ccol = (uint32_t)u0 * G;
   const int64_t ldc_b = ldc, ldq_b = ldq * 2, ldl_b = ldl * 2;
   const int64_t ldi_b = epi.in_ld() * 2, ldo_b = epi.out_ld() * 2;
-  auto rowclamp = [&](int rb, int r) { return (uint32_t)min(r, M - 1 - rb * 16); };
-  auto load = [&](In& in, int rb) {
+  auto rowclamp = [&](int rb, int r) __attribute__((always_inline)) { return (uint32_t)min(r, M - 1 - rb * 16); };
+  auto load = [&](In& in, int rb) __attribute__((always_inline)) {
     const unsigned char* cb0 = codes + (int64_t)rb * 16 * ldc_b;
 #pragma unroll
     for (int i = 0; i < Tl::CPT; ++i) {
@@ -566,7 +566,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
       }
     }
   };
-  auto stage = [&](const In& in, int b) {
+  auto stage = [&](const In& in, int b) __attribute__((always_inline)) {
     unsigned char* slot = ism + (b & 1) * Lay::ISLOT;
 #pragma unroll
     for (int i = 0; i < Tl::CPT; ++i) {
@@ -594,7 +594,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
       }
     }
   };
-  auto store_tile = [&](int rb, int b) {
+  auto store_tile = [&](int rb, int b) __attribute__((always_inline)) {
     const unsigned char* os = osm + (b & 1) * Ro::OSLOT;
     unsigned char* ob0 = reinterpret_cast<unsigned char*>(epi.out_row((int64_t)rb * 16));
 #pragma unroll
@@ -633,7 +633,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
   // tile of position b - 1 (row block rb_prev), then NEXT(): whatever the caller requests with the
   // slot free (RELOAD 1: row block rb + PD if position b + PD exists; 2: always; 0: nothing), then
   // reconstruct block b into its tile.
-  auto body_at = [&](auto kc, int b, int rb, int rb_prev, auto next) {
+  auto body_at = [&](auto kc, int b, int rb, int rb_prev, auto next) __attribute__((always_inline)) {
     constexpr int k = decltype(kc)::value;
     stage(in[k], b);
     lds_barrier();
@@ -700,7 +700,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
         const int c0 = unit_base(rot_p, u0, N, NP, G) + 128 * rot_q + 32 * g;
         const uint32_t mword = OUTL ? colmask[c0 >> 5] : 0u;
         const uint16_t* ss = reinterpret_cast<const uint16_t*>(ism + (b & 1) * Lay::ISLOT + Tl::SLOT) + j * kSideMax;
-        auto subst = [&](int k, const float* y, float* o) {
+        auto subst = [&](int k, const float* y, float* o) __attribute__((always_inline)) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) o[e] = y[e];
           if constexpr (OUTL) {
@@ -734,7 +734,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
       }
     }
   };
-  auto body = [&](auto kc, int b, auto reload) {
+  auto body = [&](auto kc, int b, auto reload) __attribute__((always_inline)) {
     constexpr int k = decltype(kc)::value;
     const int rb = rb0 + b;
     body_at(kc, b, rb, rb - 1, [&]() {
@@ -753,7 +753,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
   // paths' pending counts and each block waited for every outstanding memory operation, the
   // previous block's stores included.  (The V operands first: loads retire in issue order, so
   // block 0 waits for them and its own inputs, not for the later blocks'.)
-  auto straight = [&](auto sln) {
+  auto straight = [&](auto sln) __attribute__((always_inline)) {
     constexpr int SL = decltype(sln)::value;
     load_v();
     __builtin_amdgcn_sched_barrier(0);

@@ -272,8 +272,17 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
         ok &= rc_scale_ok(sv) ? 1 : 0;
       }
     }
-    if constexpr (MODE == kEncode) rc_ok = __syncthreads_and(ok) != 0;
-    else __syncthreads();
+    if constexpr (MODE == kEncode) {
+      // every thread's ok, as __syncthreads_and (whose device-library reduction is not inlined
+      // here): one ballot per wave, the 4 waves' results through LDS
+      __shared__ uint32_t wave_ok[4];
+      const bool all = __builtin_amdgcn_ballot_w64(ok == 0) == 0;
+      if (lane == 0) wave_ok[w] = all ? 1u : 0u;
+      __syncthreads();
+      rc_ok = (wave_ok[0] & wave_ok[1] & wave_ok[2] & wave_ok[3]) != 0;
+    } else {
+      __syncthreads();
+    }
   }
 
   // decode from the COO tile: the next row block's L operand, codes and COO piece bounds are
@@ -285,7 +294,7 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
   u32x2 nl[RT];
   u32x4 nq = u32x4{0u, 0u, 0u, 0u};
   int64_t ns0[NPB], ns1[NPB];
-  auto fetch_next = [&](int i) {  // block i of the workgroup (rows clamped to the last)
+  auto fetch_next = [&](int i) __attribute__((always_inline)) {  // block i of the workgroup (rows clamped to the last)
     const int64_t rn = min((bx * a.rb + i) * 64 + w * 16 + j, M - 1);
 #pragma unroll
     for (int t = 0; t < RT; ++t) nl[t] = ld8(a.l + rn * K + 16 * t + 4 * g);
@@ -298,7 +307,7 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
   // waves per SIMD)
   constexpr bool kPreX = MODE == kEncode && NP <= 4;
   u32x4 nx[kPreX ? NP : 1][2];
-  auto fetch_x = [&](int i) {
+  auto fetch_x = [&](int i) __attribute__((always_inline)) {
     const int64_t rn = min((bx * a.rb + i) * 64 + w * 16 + j, M - 1);
 #pragma unroll
     for (int t = 0; t < RT; ++t) nl[t] = ld8(a.l + rn * K + 16 * t + 4 * g);
@@ -540,6 +549,249 @@ __global__ __launch_bounds__(256) void k_legacy_scalar(LegacyArgs a, int K, int6
   if constexpr (MODE == kEncode) a.qout[bm * NB + c] = (uint8_t)qout;
 }
 
+// ------------------------------------------------------------------ row-tile decode
+// Decode for large shapes (2, 4 or 8 bits; no outliers, or COO outliers), staged through an LDS
+// tile so that the output leaves as whole row segments.  A workgroup of 4 waves owns 4 units
+// (wave w: unit u0 + w, i.e. 64 columns in every plane) of one batch over a run of RBW 16-row
+// blocks, with the unit's r^T operands in registers and the units' scales in LDS for the whole
+// run (in registers they pushed the 2-bit kernel past 256 VGPRs: one wave per SIMD).  The tile is
+// [16 rows][NP planes][256 columns] bf16 (rows padded by 16 bytes, so the lanes of a column
+// quarter reach different banks), two of them in turn.  Per block b:
+//   B1 | x_hat of block b: each lane reads its 16 outlier values per plane from tile b, forms
+//   x_hat (the reconstruction MFMA for l @ r, the decode's roundings two columns at a time) and
+//   writes it over them; the other tile is zeroed | B2 | tile b leaves as row segments
+//   (non-temporal 16-byte stores of whole lines); block b + 1's COO entries, requested a block
+//   earlier, go into the zeroed tile; then the requests: the entries of block b + 2, the COO
+//   bounds of block b + 4, the codes and l operand of block b + PD (PD = 2; 4 measured slower).
+// COO ranges: the entries of one (row, plane) of the workgroup's units are contiguous (row-major
+// COO, 64-column pieces in order): [piece_ptr[pc], piece_ptr[pc + units]).  Wave w takes ranges
+// w * RPW .. w * RPW + RPW - 1 (range q: row q % 16, plane q / 16), LPR = 64 / RPW lanes each;
+// lane l of range r loads its own bounds and entries start + l % LPR + LPR i, i < RPW (64 entries
+// of the range per pass); a range of more than 64 entries takes further passes right away.  An
+// entry outside the units' columns, or past the entry capacity, is not written.  Blocks are taken PD at a time
+// (ring slots by position); the positions past the run compute on the last block's inputs and
+// store nothing (a zero-length store range).
+template <int BITS>
+struct LegacyRows {
+  static constexpr int NP = 8 / BITS, NW = 4, G = 64, SEG = NW * G, PD = 2;
+  static constexpr int RSTR = NP * SEG + 8;  // bf16 per tile row
+  static constexpr int TILE = 16 * RSTR;     // bf16 per tile
+  static constexpr int NR = 16 * NP, RPW = NR / NW;
+  static constexpr size_t LDS = (2 * (size_t)TILE + 64 + NP * SEG) * 2;  // two tiles, a 64-lane dummy row, the scales
+  static_assert(BITS == 2 || BITS == 4 || BITS == 8, "2, 4 or 8 bits");
+};
+
+template <int BITS, int K, bool COO>
+__global__ __launch_bounds__(256) void k_legacy_rows(LegacyArgs a, int RBW, int ug) {
+  using Lr = LegacyRows<BITS>;
+  constexpr int NP = Lr::NP, NW = Lr::NW, G = 64, E = 16, RT = K / 16, SEG = Lr::SEG, RSTR = Lr::RSTR;
+  constexpr int TILE = Lr::TILE, RPW = Lr::RPW, PD = Lr::PD;
+  constexpr uint32_t kMask = BITS == 8 ? 0xffu : (1u << BITS) - 1u;
+  extern __shared__ __attribute__((aligned(16))) uint16_t lt[];  // [2][TILE] + dummy[64]
+  uint16_t* const dummy = lt + 2 * TILE;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int M = (int)a.M, N = (int)a.N;
+  const int64_t NB = N / NP;
+  const int nu = (int)(NB / G), nrb = (M + 15) / 16, nrun = (nrb + RBW - 1) / RBW;
+  // tile (batch, run, unit group), unit groups fastest, in XCD-aware order: the workgroups that
+  // run together on an XCD take neighbouring unit groups of the same rows (their COO ranges and
+  // code rows share L2 lines)
+  const int t = __builtin_amdgcn_readfirstlane(xcd_tile(blockIdx.x, gridDim.x));
+  const int ugi = t % ug, run = (t / ug) % nrun, b = t / (ug * nrun);
+  const int u0 = ugi * NW, nuw = min(NW, nu - u0), u = min(u0 + w, nu - 1);
+  const int rb0 = run * RBW, nblk = min(RBW, nrb - rb0);
+  const int64_t bm0 = (int64_t)b * M;  // first row of the batch in [B * M] rows
+  const uint16_t* srow = a.s + (a.s_rows == 1 ? 0 : (int64_t)b * N);
+
+  // resident: the unit's r^T operands and its 16 scales per plane (bf16 pairs)
+  u32x2 vop[NP][G / 16][RT];
+  uint16_t* const stab = lt + 2 * TILE + 64;  // [NP][SEG] scales of the workgroup's units (bf16)
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int base = unit_base(p, u, N, NP, G);
+    load_vops<G, K>(a.rt, base, j, g, vop[p]);
+  }
+  for (int i = threadIdx.x; i < NP * SEG; i += 256) {
+    const int p = i / SEG, c = min(i % SEG, nuw * G - 1);
+    stab[i] = srow[p * (int)NB + u0 * G + c];
+  }
+
+  // per block: codes (16 bytes per lane) and the l operand, PD blocks ahead
+  struct Blk {
+    u32x4 cb;
+    u32x2 lop[RT];
+  };
+  auto load_blk = [&](int i, Blk& d) __attribute__((always_inline)) {
+    const int64_t rr = min(min(rb0 + i, nrb - 1) * 16 + j, M - 1);
+    d.cb = ld16_stream(a.qin + (bm0 + rr) * NB + u * G + E * g);
+#pragma unroll
+    for (int k = 0; k < RT; ++k) d.lop[k] = ld8(a.l + rr * K + 16 * k + 4 * g);
+  };
+  // COO: this lane's range (row rq, plane pq) and its place among the range's LPR lanes
+  constexpr int LPR = 64 / RPW;
+  const int rq = (w * RPW + lane / LPR) % 16, pq = (w * RPW + lane / LPR) / 16, lr_ = lane % LPR;
+  const int cbase = pq * (int)NB + u0 * G;  // the range's first column
+  struct Bnd {
+    int64_t s0, s1;
+  };
+  auto load_bounds = [&](int i) __attribute__((always_inline)) -> Bnd {
+    const int64_t rr = min(min(rb0 + i, nrb - 1) * 16 + rq, M - 1);
+    const int64_t pc = (bm0 + rr) * a.npc + (int64_t)pq * (NB / G) + u0;
+    return Bnd{a.optr[pc], a.optr[pc + nuw]};
+  };
+  uint32_t ecol[RPW], eval[RPW];
+  // entries start + 64 pass + lr_ + LPR i of the lane's range (indices clamped to the capacity)
+  auto load_entries = [&](const Bnd& bd, int pass) __attribute__((always_inline)) {
+    const int64_t s0 = max(bd.s0, (int64_t)0) + 64 * pass + lr_;
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const int64_t k = min(s0 + LPR * i, a.ncap - 1);
+      ecol[i] = reinterpret_cast<const uint32_t*>(a.ocol)[2 * k];  // the column's low dword
+      eval[i] = a.oval[k];
+    }
+  };
+  auto scatter = [&](uint16_t* tb, const Bnd& bd, int pass) __attribute__((always_inline)) {
+    const int64_t s0 = max(bd.s0, (int64_t)0) + 64 * pass + lr_, s1 = min(bd.s1, a.ncap);
+    uint16_t* row = tb + rq * RSTR + pq * SEG;
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const int d = (int)ecol[i] - cbase;
+      const bool ok = s0 + LPR * i < s1 && d >= 0 && d < nuw * G;
+      uint16_t* dst = ok ? row + d : dummy + lane;
+      *dst = (uint16_t)eval[i];
+    }
+  };
+  // the passes after the first, for ranges of more than 64 entries (rare), loaded and written in turn
+  auto scatter_rest = [&](uint16_t* tb, const Bnd& bd) __attribute__((always_inline)) {
+    const int64_t len = min(bd.s1, a.ncap) - max(bd.s0, (int64_t)0);
+    for (int pass = 1; __builtin_amdgcn_ballot_w64(len > (int64_t)64 * pass) != 0; ++pass) {  // (uniform)
+      load_entries(bd, pass);
+      scatter(tb, bd, pass);
+    }
+  };
+  auto zero_tile = [&](uint16_t* tb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = threadIdx.x; i < TILE / 8; i += 256) *reinterpret_cast<u32x4*>(tb + 8 * i) = u32x4{0u, 0u, 0u, 0u};
+  };
+
+  const float zero[E] = {};
+  constexpr float kHalf = (float)(1 << (BITS - 1));
+  // x_hat of a block from tile tb (the lane's own 16 columns of every plane: outlier values in,
+  // x_hat out): bf16(bf16(bf16((code - 2^(b-1)) s) + o) + bf16(l @ r)), as legacy_value
+  auto compute = [&](const Blk& d, uint16_t* tb) __attribute__((always_inline)) {
+    static_for<0, NP>([&](auto pc) {
+      constexpr int p = decltype(pc)::value;
+      float lr[E];
+      residual_unit<G, K>(vop[p], d.lop, zero, lr);
+      uint16_t* tp = tb + j * RSTR + p * SEG + w * G + E * g;
+      u32x4 ov[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
+      if constexpr (COO) {
+        ov[0] = *reinterpret_cast<const u32x4*>(tp);
+        ov[1] = *reinterpret_cast<const u32x4*>(tp + 8);
+      }
+      u32x4 xo[2];
+      const uint16_t* sp = stab + p * SEG + w * G + E * g;
+      const u32x4 scp[2] = {*reinterpret_cast<const u32x4*>(sp), *reinterpret_cast<const u32x4*>(sp + 8)};
+#pragma unroll
+      for (int e = 0; e < E; e += 2) {
+        const uint32_t sw = scp[e >> 3][(e >> 1) & 3], lp = pack_bf16x2(lr[e], lr[e + 1]);
+        float av[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t code = (d.cb[(e + h) >> 2] >> (8 * ((e + h) & 3) + BITS * p)) & kMask;
+          const float s = h ? bf_hi(sw) : bf_lo(sw);
+          av[h] = __builtin_fmaf((float)code, s, -kHalf * s);  // (code - 2^(b-1)) * s, exact in fp32
+        }
+        if constexpr (BITS > 2) {  // (already a bf16 value at 1 and 2 bits)
+          const uint32_t ap = pack_bf16x2(av[0], av[1]);
+          av[0] = bf_lo(ap);
+          av[1] = bf_hi(ap);
+        }
+        if constexpr (COO) {
+          const uint32_t ow = ov[e >> 3][(e >> 1) & 3];
+          const uint32_t ap = pack_bf16x2(av[0] + bf_lo(ow), av[1] + bf_hi(ow));
+          av[0] = bf_lo(ap);
+          av[1] = bf_hi(ap);
+        }
+        xo[e >> 3][(e >> 1) & 3] = pack_bf16x2(av[0] + bf_lo(lp), av[1] + bf_hi(lp));
+      }
+      *reinterpret_cast<u32x4*>(tp) = xo[0];
+      *reinterpret_cast<u32x4*>(tp + 8) = xo[1];
+    });
+  };
+  // tile tb -> the rows of block i: 16 rows x NP planes x the units' 64 nuw columns (16 bytes a
+  // lane; rows past M and blocks past the run fall outside the store range)
+  auto store_tile = [&](const uint16_t* tb, int i) __attribute__((always_inline)) {
+    const int rb = rb0 + min(i, nblk - 1);
+    const uint32_t rows = i < nblk ? (uint32_t)min(16, M - rb * 16) : 0u;
+    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(a.out + (bm0 + (int64_t)rb * 16) * N, rows * (uint32_t)N * 2u);
+    constexpr int CH = SEG / 8;  // 16-byte chunks per (row, plane)
+    static_assert((16 * NP * CH) % 256 == 0, "whole store passes");
+#pragma unroll
+    for (int c0 = 0; c0 < 16 * NP * CH; c0 += 256) {
+      const int c = c0 + (int)threadIdx.x;
+      const int r = c / (NP * CH), rem = c % (NP * CH), p = rem / CH, k = rem % CH;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(tb + r * RSTR + p * SEG + 8 * k);
+      const uint32_t off = (uint32_t)((r * N + p * (int)NB + u0 * G + 8 * k) * 2);
+      __builtin_amdgcn_raw_buffer_store_b128(v, rs, 8 * k < nuw * G ? off : 0x7ffffff0u, 0, 2);
+    }
+  };
+
+  Blk ring[PD];
+  static_for<0, PD>([&](auto kc) { load_blk(decltype(kc)::value, ring[decltype(kc)::value]); });
+  const int npos = (nblk + PD - 1) / PD * PD;  // positions, whole ring rounds
+  if constexpr (COO) {
+    const Bnd bnd0 = load_bounds(0);
+    Bnd bnd_c = load_bounds(1), bnd_n = load_bounds(2), bnd_nn = load_bounds(3);
+    zero_tile(lt);
+    zero_tile(lt + TILE);
+    load_entries(bnd0, 0);
+    lds_barrier();  // both tiles zeroed
+    scatter(lt, bnd0, 0);
+    scatter_rest(lt, bnd0);
+    load_entries(bnd_c, 0);  // block 1's, written during block 0
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll 1
+    for (int bb = 0; bb < npos; bb += PD)
+      static_for<0, PD>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        const int bi = bb + k;
+        uint16_t* tc = lt + (bi & 1) * TILE;
+        uint16_t* tn = lt + ((bi + 1) & 1) * TILE;
+        lds_barrier();  // B1: block bi's outliers are in tc; tn's previous rows have left
+        compute(ring[k], tc);
+        zero_tile(tn);
+        lds_barrier();  // B2: x_hat of block bi in tc; tn zeroed
+        store_tile(tc, bi);
+        scatter(tn, bnd_c, 0);  // block bi + 1
+        scatter_rest(tn, bnd_c);
+        __builtin_amdgcn_sched_barrier(0);
+        load_entries(bnd_n, 0);  // block bi + 2
+        bnd_c = bnd_n;
+        bnd_n = bnd_nn;
+        bnd_nn = load_bounds(bi + 4);
+        load_blk(bi + PD, ring[k]);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+  } else {
+#pragma unroll 1
+    for (int bb = 0; bb < npos; bb += PD)
+      static_for<0, PD>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        const int bi = bb + k;
+        uint16_t* tc = lt + (bi & 1) * TILE;
+        lds_barrier();  // B1: tc's previous rows have left
+        compute(ring[k], tc);
+        lds_barrier();  // B2
+        store_tile(tc, bi);
+        __builtin_amdgcn_sched_barrier(0);
+        load_blk(bi + PD, ring[k]);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+  }
+}
+
 // ------------------------------------------------------------------ dequant-GEMM
 // out[b, m, c] = bf16( sum_n x_hat[b, m, n] * y[b, n, c] ), the sum in fp32, with x_hat the
 // fused decode's value bf16(bf16(bf16((code - 2^(b-1)) * s) + bf16(l @ r))): the reference's
@@ -603,7 +855,7 @@ __global__ __launch_bounds__(512) void k_legacy_gemm(LegacyGemmArgs a) {
     u32x4 sc[2];            // the lane's 16 scales (bf16)
     u32x4 cb[RB];           // the lane's 16 code bytes of each row block
   };
-  auto load_item = [&](int it, Item& d) {
+  auto load_item = [&](int it, Item& d) __attribute__((always_inline)) {
     const int u = it / NP, p = it % NP;
     const int base = unit_base(p, u, N, NP, G);
     load_vops<G, K>(a.rt, base, j, g, d.vop);
@@ -624,7 +876,7 @@ __global__ __launch_bounds__(512) void k_legacy_gemm(LegacyGemmArgs a) {
   // most 8 bits times a bf16), and already a bf16 value for 1 and 2 bits (|code - 2^(b-1)| <= 2);
   // each bf16 rounding is one v_cvt_pk_bf16_f32 (round to nearest even, as bf16r) per pair, and
   // the last one leaves the pair packed as the product's operand.
-  auto compute_item = [&](const Item& d, int p) {
+  auto compute_item = [&](const Item& d, int p) __attribute__((always_inline)) {
     u32x4 yt[G / 32][TO];
     transpose_vops<G, NOUT>(d.ya, ident, yt);
     float sc[E], zb[E];
@@ -825,9 +1077,50 @@ static int legacy_rows_per_wg(int64_t M, int64_t wg_cols) {
   return 1;
 }
 
+// The row-tile decode (k_legacy_rows) for decodes without dense outliers at 2, 4 and 8 bits,
+// when every workgroup of 4 units has whole units and there are enough blocks for about two
+// workgroups per CU (smaller shapes keep k_legacy_mfma, which splits rows more finely); runs of
+// whole ring rounds (PD blocks).  Returns false where it does not apply.
+template <int MODE, int BITS, int OSRC>
+static bool legacy_rows_launch(const LegacyArgs& a, int K, int64_t B, hipStream_t st, int* status) {
+  if constexpr (MODE != kDecode || OSRC == 1 || BITS == 1) {
+    return false;
+  } else {
+    using Lr = LegacyRows<BITS>;
+    const int64_t NB = a.N / Lr::NP, nu = NB / 64, nrb = (a.M + 15) / 16;
+    if (NB % 64 != 0 || nu < Lr::NW || 16 * a.N * 2 >= ((int64_t)1 << 31)) return false;
+    const int64_t ug = (nu + Lr::NW - 1) / Lr::NW, tiles = B * ug;
+    const int64_t want = 2 * (int64_t)cu_count();
+    if (tiles * nrb < want * 2 * Lr::PD) return false;  // under two ring rounds per workgroup
+    int64_t runs = std::max<int64_t>(1, want / tiles);
+    int64_t rbw = (nrb + runs - 1) / runs;
+    rbw = (rbw + Lr::PD - 1) / Lr::PD * Lr::PD;
+    runs = (nrb + rbw - 1) / rbw;
+    const int64_t nwg = tiles * runs;
+    if (nwg > INT32_MAX) return false;
+    const bool coo = OSRC != 0 && a.ncap > 0;
+    auto go = [&](auto kern) __attribute__((always_inline)) {
+      (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)Lr::LDS);
+      *status = launch(kern, dim3((unsigned)nwg), dim3(256), Lr::LDS, st, a, (int)rbw, (int)ug);
+    };
+    if (K == 16) {
+      if (coo) go(k_legacy_rows<BITS, 16, true>);
+      else go(k_legacy_rows<BITS, 16, false>);
+    } else {
+      if (coo) go(k_legacy_rows<BITS, 32, true>);
+      else go(k_legacy_rows<BITS, 32, false>);
+    }
+    return true;
+  }
+}
+
 template <int MODE, int BITS, int OSRC>
 static int legacy_launch(const LegacyArgs& a, int K, int64_t B, bool mfma_ok, hipStream_t st) {
   constexpr int NP = (MODE == kAdd) ? 1 : 8 / BITS;
+  if (mfma_ok) {
+    int status = LRQ_OK;
+    if (legacy_rows_launch<MODE, BITS, OSRC>(a, K, B, st, &status)) return status;
+  }
   const int64_t NB = a.N / NP;
   const int rb = legacy_rows_per_wg(a.M, NB / 64 * B);
   const int64_t nwg = (a.M + 64 * rb - 1) / (64 * rb) * (NB / 64) * B;
@@ -978,7 +1271,7 @@ template <int BITS, int K, int NOUT>
 static int legacy_gemm_chunk(const LegacyGemmArgs& a, int64_t B, hipStream_t st) {
   // 16-row blocks per workgroup: 4, or 2 / 1 where 4 would leave CUs without a workgroup
   const int64_t nrb = (a.M + 15) / 16, cu = cu_count();
-  auto launch_rb = [&](auto rb) {
+  auto launch_rb = [&](auto rb) __attribute__((always_inline)) {
     constexpr int RB = decltype(rb)::value;
     const int64_t nwg = B * ((nrb + RB - 1) / RB);
     if (nwg > INT32_MAX) return (int)LRQ_ERR_SHAPE;
