@@ -559,16 +559,21 @@ __global__ __launch_bounds__(256) void k_legacy_scalar(LegacyArgs a, int K, int6
 // quarter reach different banks), two of them in turn.  Per block b:
 //   B1 | x_hat of block b: each lane reads its 16 outlier values per plane from tile b, forms
 //   x_hat (the reconstruction MFMA for l @ r, the decode's roundings two columns at a time) and
-//   writes it over them; the other tile is zeroed | B2 | tile b leaves as row segments
-//   (non-temporal 16-byte stores of whole lines); block b + 1's COO entries, requested a block
-//   earlier, go into the zeroed tile; then the requests: the entries of block b + 2, the COO
-//   bounds of block b + 4, the codes and l operand of block b + PD (PD = 2; 4 measured slower).
+//   writes it over them; the workers zero the other tile | B2 | tile b leaves as row segments
+//   (non-temporal 16-byte stores of whole lines) and the codes and l operand of block b + PD are
+//   requested (PD = 2; 4 measured slower); the workers write block b + 1's COO entries, requested
+//   a block earlier, into the zeroed tile and request the entries of block b + 2 and the COO
+//   bounds of block b + 4.
 // COO ranges: the entries of one (row, plane) of the workgroup's units are contiguous (row-major
-// COO, 64-column pieces in order): [piece_ptr[pc], piece_ptr[pc + units]).  Wave w takes ranges
-// w * RPW .. w * RPW + RPW - 1 (range q: row q % 16, plane q / 16), LPR = 64 / RPW lanes each;
-// lane l of range r loads its own bounds and entries start + l % LPR + LPR i, i < RPW (64 entries
-// of the range per pass); a range of more than 64 entries takes further passes right away.  An
-// entry outside the units' columns, or past the entry capacity, is not written.  Blocks are taken PD at a time
+// COO, 64-column pieces in order): [piece_ptr[pc], piece_ptr[pc + units]).  With outliers the
+// workgroup has 4 more waves, COO workers (their loads and waits stay out of the decoding waves'
+// in-order memory queues): worker w takes ranges w * RPW .. w * RPW + RPW - 1 (range q: row q % 16,
+// plane q / 16), LPR = 64 / RPW lanes each; lane l of range r loads its own bounds and entries
+// start + l % LPR + LPR i for the i < ns the wave's longest range needs (64 entries of a range per
+// pass); a range of more than 64 entries takes further passes right away.  An entry outside the
+// units' columns, or past the entry capacity, is not written.  (Four waves per SIMD, two
+// workgroups per CU: 128 VGPRs with a small spill measured faster than 136 VGPRs and one
+// workgroup.)  Blocks are taken PD at a time
 // (ring slots by position); the positions past the run compute on the last block's inputs and
 // store nothing (a zero-length store range).
 template <int BITS>
@@ -582,10 +587,10 @@ struct LegacyRows {
 };
 
 template <int BITS, int K, bool COO>
-__global__ __launch_bounds__(256) void k_legacy_rows(LegacyArgs a, int RBW, int ug) {
+__global__ __launch_bounds__(COO ? 512 : 256) __attribute__((amdgpu_waves_per_eu(4))) void k_legacy_rows(LegacyArgs a, int RBW, int ug) {
   using Lr = LegacyRows<BITS>;
   constexpr int NP = Lr::NP, NW = Lr::NW, G = 64, E = 16, RT = K / 16, SEG = Lr::SEG, RSTR = Lr::RSTR;
-  constexpr int TILE = Lr::TILE, RPW = Lr::RPW, PD = Lr::PD;
+  constexpr int TILE = Lr::TILE, RPW = Lr::RPW, PD = Lr::PD, T = COO ? 512 : 256;
   constexpr uint32_t kMask = BITS == 8 ? 0xffu : (1u << BITS) - 1u;
   extern __shared__ __attribute__((aligned(16))) uint16_t lt[];  // [2][TILE] + dummy[64]
   uint16_t* const dummy = lt + 2 * TILE;
@@ -599,7 +604,11 @@ __global__ __launch_bounds__(256) void k_legacy_rows(LegacyArgs a, int RBW, int 
   // code rows share L2 lines)
   const int t = __builtin_amdgcn_readfirstlane(xcd_tile(blockIdx.x, gridDim.x));
   const int ugi = t % ug, run = (t / ug) % nrun, b = t / (ug * nrun);
-  const int u0 = ugi * NW, nuw = min(NW, nu - u0), u = min(u0 + w, nu - 1);
+  const int u0 = ugi * NW, nuw = min(NW, nu - u0), u = min(u0 + w % NW, nu - 1);
+  // with COO outliers, waves NW .. 2 NW - 1 are COO workers: they zero the tiles and write the
+  // entries into them, so that their loads and waits never hold up the decoding waves' block ring
+  // (memory operations retire in issue order, per wave)
+  const bool worker = COO && w >= NW;  // (uniform)
   const int rb0 = run * RBW, nblk = min(RBW, nrb - rb0);
   const int64_t bm0 = (int64_t)b * M;  // first row of the batch in [B * M] rows
   const uint16_t* srow = a.s + (a.s_rows == 1 ? 0 : (int64_t)b * N);
@@ -607,12 +616,14 @@ __global__ __launch_bounds__(256) void k_legacy_rows(LegacyArgs a, int RBW, int 
   // resident: the unit's r^T operands and its 16 scales per plane (bf16 pairs)
   u32x2 vop[NP][G / 16][RT];
   uint16_t* const stab = lt + 2 * TILE + 64;  // [NP][SEG] scales of the workgroup's units (bf16)
+  if (!worker) {
 #pragma unroll
-  for (int p = 0; p < NP; ++p) {
-    const int base = unit_base(p, u, N, NP, G);
-    load_vops<G, K>(a.rt, base, j, g, vop[p]);
+    for (int p = 0; p < NP; ++p) {
+      const int base = unit_base(p, u, N, NP, G);
+      load_vops<G, K>(a.rt, base, j, g, vop[p]);
+    }
   }
-  for (int i = threadIdx.x; i < NP * SEG; i += 256) {
+  for (int i = threadIdx.x; i < NP * SEG; i += T) {
     const int p = i / SEG, c = min(i % SEG, nuw * G - 1);
     stab[i] = srow[p * (int)NB + u0 * G + c];
   }
@@ -628,9 +639,10 @@ __global__ __launch_bounds__(256) void k_legacy_rows(LegacyArgs a, int RBW, int 
 #pragma unroll
     for (int k = 0; k < RT; ++k) d.lop[k] = ld8(a.l + rr * K + 16 * k + 4 * g);
   };
-  // COO: this lane's range (row rq, plane pq) and its place among the range's LPR lanes
+  // COO (workers): this lane's range (row rq, plane pq) and its place among the range's LPR lanes
   constexpr int LPR = 64 / RPW;
-  const int rq = (w * RPW + lane / LPR) % 16, pq = (w * RPW + lane / LPR) / 16, lr_ = lane % LPR;
+  const int wq = w % NW;
+  const int rq = (wq * RPW + lane / LPR) % 16, pq = (wq * RPW + lane / LPR) / 16, lr_ = lane % LPR;
   const int cbase = pq * (int)NB + u0 * G;  // the range's first column
   struct Bnd {
     int64_t s0, s1;
@@ -641,38 +653,50 @@ __global__ __launch_bounds__(256) void k_legacy_rows(LegacyArgs a, int RBW, int 
     return Bnd{a.optr[pc], a.optr[pc + nuw]};
   };
   uint32_t ecol[RPW], eval[RPW];
-  // entries start + 64 pass + lr_ + LPR i of the lane's range (indices clamped to the capacity)
-  auto load_entries = [&](const Bnd& bd, int pass) __attribute__((always_inline)) {
+  // the entry slots a pass needs: the wave's longest range over LPR lanes (wave-uniform)
+  auto slots = [&](const Bnd& bd, int pass) __attribute__((always_inline)) -> int {
+    int len = (int)min(min(bd.s1, a.ncap) - max(bd.s0, (int64_t)0) - (int64_t)64 * pass, (int64_t)64);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) len = max(len, __shfl_xor(len, m));
+    return __builtin_amdgcn_readfirstlane(min(max(len, 0) + LPR - 1, 64) / LPR);
+  };
+  // entries start + 64 pass + lr_ + LPR i, i < ns, of the lane's range (indices clamped to the capacity)
+  auto load_entries = [&](const Bnd& bd, int pass, int ns) __attribute__((always_inline)) {
     const int64_t s0 = max(bd.s0, (int64_t)0) + 64 * pass + lr_;
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
-      const int64_t k = min(s0 + LPR * i, a.ncap - 1);
-      ecol[i] = reinterpret_cast<const uint32_t*>(a.ocol)[2 * k];  // the column's low dword
-      eval[i] = a.oval[k];
+      if (i < ns) {  // (uniform)
+        const int64_t k = min(s0 + LPR * i, a.ncap - 1);
+        ecol[i] = reinterpret_cast<const uint32_t*>(a.ocol)[2 * k];  // the column's low dword
+        eval[i] = a.oval[k];
+      }
     }
   };
-  auto scatter = [&](uint16_t* tb, const Bnd& bd, int pass) __attribute__((always_inline)) {
+  auto scatter = [&](uint16_t* tb, const Bnd& bd, int pass, int ns) __attribute__((always_inline)) {
     const int64_t s0 = max(bd.s0, (int64_t)0) + 64 * pass + lr_, s1 = min(bd.s1, a.ncap);
     uint16_t* row = tb + rq * RSTR + pq * SEG;
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
-      const int d = (int)ecol[i] - cbase;
-      const bool ok = s0 + LPR * i < s1 && d >= 0 && d < nuw * G;
-      uint16_t* dst = ok ? row + d : dummy + lane;
-      *dst = (uint16_t)eval[i];
+      if (i < ns) {  // (uniform)
+        const int d = (int)ecol[i] - cbase;
+        const bool ok = s0 + LPR * i < s1 && d >= 0 && d < nuw * G;
+        uint16_t* dst = ok ? row + d : dummy + lane;
+        *dst = (uint16_t)eval[i];
+      }
     }
   };
   // the passes after the first, for ranges of more than 64 entries (rare), loaded and written in turn
   auto scatter_rest = [&](uint16_t* tb, const Bnd& bd) __attribute__((always_inline)) {
     const int64_t len = min(bd.s1, a.ncap) - max(bd.s0, (int64_t)0);
     for (int pass = 1; __builtin_amdgcn_ballot_w64(len > (int64_t)64 * pass) != 0; ++pass) {  // (uniform)
-      load_entries(bd, pass);
-      scatter(tb, bd, pass);
+      const int ns = slots(bd, pass);
+      load_entries(bd, pass, ns);
+      scatter(tb, bd, pass, ns);
     }
   };
+  // (the workers' 256 threads)
   auto zero_tile = [&](uint16_t* tb) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = threadIdx.x; i < TILE / 8; i += 256) *reinterpret_cast<u32x4*>(tb + 8 * i) = u32x4{0u, 0u, 0u, 0u};
+    for (int i = (int)threadIdx.x - 256; i < TILE / 8; i += 256) *reinterpret_cast<u32x4*>(tb + 8 * i) = u32x4{0u, 0u, 0u, 0u};
   };
 
   const float zero[E] = {};
@@ -739,42 +763,57 @@ __global__ __launch_bounds__(256) void k_legacy_rows(LegacyArgs a, int RBW, int 
   };
 
   Blk ring[PD];
-  static_for<0, PD>([&](auto kc) { load_blk(decltype(kc)::value, ring[decltype(kc)::value]); });
   const int npos = (nblk + PD - 1) / PD * PD;  // positions, whole ring rounds
   if constexpr (COO) {
-    const Bnd bnd0 = load_bounds(0);
-    Bnd bnd_c = load_bounds(1), bnd_n = load_bounds(2), bnd_nn = load_bounds(3);
-    zero_tile(lt);
-    zero_tile(lt + TILE);
-    load_entries(bnd0, 0);
-    lds_barrier();  // both tiles zeroed
-    scatter(lt, bnd0, 0);
-    scatter_rest(lt, bnd0);
-    load_entries(bnd_c, 0);  // block 1's, written during block 0
-    __builtin_amdgcn_sched_barrier(0);
+    if (worker) {
+      // block 0's entries into tile 0, block 1's requested; per position: zero the next tile
+      // (between the barriers), then write the next block's entries into it and request those
+      // of the block after
+      const Bnd bnd0 = load_bounds(0);
+      Bnd bnd_c = load_bounds(1), bnd_n = load_bounds(2), bnd_nn = load_bounds(3);
+      zero_tile(lt);
+      zero_tile(lt + TILE);
+      int ns = slots(bnd0, 0);
+      load_entries(bnd0, 0, ns);
+      lds_barrier();  // B0: both tiles zeroed
+      scatter(lt, bnd0, 0, ns);
+      scatter_rest(lt, bnd0);
+      int ns_c = slots(bnd_c, 0);
+      load_entries(bnd_c, 0, ns_c);  // block 1's
 #pragma unroll 1
-    for (int bb = 0; bb < npos; bb += PD)
-      static_for<0, PD>([&](auto kc) {
-        constexpr int k = decltype(kc)::value;
-        const int bi = bb + k;
-        uint16_t* tc = lt + (bi & 1) * TILE;
+      for (int bi = 0; bi < npos; ++bi) {
         uint16_t* tn = lt + ((bi + 1) & 1) * TILE;
-        lds_barrier();  // B1: block bi's outliers are in tc; tn's previous rows have left
-        compute(ring[k], tc);
+        lds_barrier();  // B1: tn's previous rows have left
         zero_tile(tn);
-        lds_barrier();  // B2: x_hat of block bi in tc; tn zeroed
-        store_tile(tc, bi);
-        scatter(tn, bnd_c, 0);  // block bi + 1
+        lds_barrier();  // B2: tn zeroed
+        scatter(tn, bnd_c, 0, ns_c);  // block bi + 1
         scatter_rest(tn, bnd_c);
-        __builtin_amdgcn_sched_barrier(0);
-        load_entries(bnd_n, 0);  // block bi + 2
         bnd_c = bnd_n;
         bnd_n = bnd_nn;
+        ns_c = slots(bnd_c, 0);
+        load_entries(bnd_c, 0, ns_c);  // block bi + 2
         bnd_nn = load_bounds(bi + 4);
-        load_blk(bi + PD, ring[k]);
-        __builtin_amdgcn_sched_barrier(0);
-      });
+      }
+    } else {
+      static_for<0, PD>([&](auto kc) { load_blk(decltype(kc)::value, ring[decltype(kc)::value]); });
+      lds_barrier();  // B0
+#pragma unroll 1
+      for (int bb = 0; bb < npos; bb += PD)
+        static_for<0, PD>([&](auto kc) {
+          constexpr int k = decltype(kc)::value;
+          const int bi = bb + k;
+          uint16_t* tc = lt + (bi & 1) * TILE;
+          lds_barrier();  // B1: block bi's outliers are in tc
+          compute(ring[k], tc);
+          lds_barrier();  // B2: x_hat of block bi in tc
+          store_tile(tc, bi);
+          __builtin_amdgcn_sched_barrier(0);
+          load_blk(bi + PD, ring[k]);
+          __builtin_amdgcn_sched_barrier(0);
+        });
+    }
   } else {
+    static_for<0, PD>([&](auto kc) { load_blk(decltype(kc)::value, ring[decltype(kc)::value]); });
 #pragma unroll 1
     for (int bb = 0; bb < npos; bb += PD)
       static_for<0, PD>([&](auto kc) {
@@ -1101,7 +1140,7 @@ static bool legacy_rows_launch(const LegacyArgs& a, int K, int64_t B, hipStream_
     const bool coo = OSRC != 0 && a.ncap > 0;
     auto go = [&](auto kern) __attribute__((always_inline)) {
       (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)Lr::LDS);
-      *status = launch(kern, dim3((unsigned)nwg), dim3(256), Lr::LDS, st, a, (int)rbw, (int)ug);
+      *status = launch(kern, dim3((unsigned)nwg), dim3(coo ? 512 : 256), Lr::LDS, st, a, (int)rbw, (int)ug);
     };
     if (K == 16) {
       if (coo) go(k_legacy_rows<BITS, 16, true>);
