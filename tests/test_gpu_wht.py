@@ -87,7 +87,8 @@ def test_rotated_format_c4_recipe(pkg, dev, rows, n):
     (37, 5120, 16, 4, 64, "silu"),    # config 4's format: fused in the row decode (EpiRot), ragged rows
     (64, 2560, 0, 4, 64, "gelu"),     # rank 0; 20 units (a workgroup with 4 of its 8 units)
     (40, 2048, 32, 4, 64, "mul"),     # rank 32 (two blocks in flight)
-    (30, 2048, 16, 8, 128, "silu"),   # int8 / g128: decode into the output, then the dense op in place
+    (30, 2048, 16, 8, 128, "silu"),   # int8 / g128: fused (4 units per workgroup)
+    (52, 4096, 0, 8, 128, "gelu"),    # int8 / g128 at rank 0, config 3's width
     (24, 2048, 16, 4, 64, "softmax"), # softmax: decode into the output, then the dense backward in place
 ])
 def test_rotated_consumers(pkg, dev, rows, n, rank, bits, group, op):
@@ -128,7 +129,8 @@ def test_rotated_consumers(pkg, dev, rows, n, rank, bits, group, op):
 
 @pytest.mark.parametrize("rows,n,rank,bits,group,fused", [
     (37, 5120, 16, 4, 64, True),     # fused rotated row kernel: dx written over dy gives the same bits
-    (30, 2048, 16, 8, 128, False),   # decode then dense op: an aliasing call is refused
+    (30, 2048, 16, 8, 128, True),    # int8 / g128: fused too (4 units per workgroup)
+    (30, 2048, 16, 4, 128, False),   # int4 / g128: decode then dense op, so an aliasing call is refused
 ])
 def test_rotated_consumer_in_place(pkg, dev, rows, n, rank, bits, group, fused):
     """dx == dy through the C ABI on the rotated format: the fused kernel reads each dy element

@@ -805,7 +805,9 @@ constexpr int kDecodeRun = 16;
 
 template <int BITS, int G, int R, bool OUTL, class EPI>
 static int decode_rows_launch(const lrq_tensors* t, hipStream_t s, const EPI& epi) {
-  constexpr int NW = rows_nw<BITS, G>();
+  // a rotated consumer of int8/g128 takes 4 units per workgroup: with 8 its dY and output tiles
+  // (four of 32 KB) and the staged inputs do not fit in LDS
+  constexpr int NW = (EPI::kIn && EPI::kRot && BITS == 8 && G == 128) ? 4 : rows_nw<BITS, G>();
   // consumers of 128-column groups stage dY in place (separate tiles would not fit in LDS; a
   // rotated consumer cannot, and is refused by the LDS check below)
   constexpr bool INP = EPI::kIn && G == 128 && !EPI::kRot;
@@ -960,7 +962,7 @@ __global__ __launch_bounds__(256) void k_scatter_side(const uint16_t* __restrict
 // planes of whole rotation blocks; returns 0 for the others.
 template <int BITS, int G, int R, class EPI>
 static int consumer_rot_fused(const lrq_tensors* t, hipStream_t s, const EPI& inner, int* status) {
-  if constexpr (!(BITS == 4 && G == 64)) {
+  if constexpr (!((BITS == 4 && G == 64) || (BITS == 8 && G == 128))) {
     return 0;
   } else {
     const int64_t plane = t->hidden / (8 / BITS);
@@ -985,6 +987,8 @@ static int consumer_rot(const lrq_tensors* t, hipStream_t s, const EPI& inner, i
     case format_key(4, 64, 0): return consumer_rot_fused<4, 64, 0>(t, s, inner, status);
     case format_key(4, 64, 16): return consumer_rot_fused<4, 64, 16>(t, s, inner, status);
     case format_key(4, 64, 32): return consumer_rot_fused<4, 64, 32>(t, s, inner, status);
+    case format_key(8, 128, 0): return consumer_rot_fused<8, 128, 0>(t, s, inner, status);
+    case format_key(8, 128, 16): return consumer_rot_fused<8, 128, 16>(t, s, inner, status);
     default: return 0;
   }
 }
