@@ -58,9 +58,10 @@ extern "C" {
  * the unrotated x and rotates it as it reads (int4/g64 and int8/g128, no outlier channels,
  * hidden/NP a multiple of 128, an even number of units per row); for other shapes it returns
  * LRQ_ERR_UNSUPPORTED and the caller rotates x with lrq_wht128 into a buffer, then encodes
- * that with the flag cleared.  lrq_decode and the fused consumers undo the rotation;
- * lrq_dequant_gemm_t (and its allocation-free form) and lrq_lora_grads refuse the flag
- * (LRQ_ERR_UNSUPPORTED) rather than return unrotated values. */
+ * that with the flag cleared.  lrq_decode, the fused consumers and the dequant-GEMMs undo the
+ * rotation (the dequant-GEMMs need planes of whole rotation blocks, hidden/NP a multiple of 128,
+ * else LRQ_ERR_UNSUPPORTED); lrq_lora_grads refuses the flag (LRQ_ERR_UNSUPPORTED: use
+ * lrq_dequant_gemm and lrq_dequant_gemm_t). */
 #define LRQ_FLAG_HADAMARD 1
 
 /* Descriptor of one compressed activation.  Encode writes L/codes/scale/zero/side;
@@ -131,8 +132,9 @@ int lrq_dequant_gemm(const lrq_tensors* t, const void* a, int32_t n_out, void* o
 
 /* out[hidden, n_out] = decode(t)^T @ g[rows, n_out] (g bf16 row-major, ld ldg a multiple of 4,
  * 8-byte aligned), fp32 accumulate, decode(t) rounded to bf16 as lrq_decode returns it; out is
- * fp32 when out_fp32 != 0, else bf16.  n_out is 16 or 32; no outlier channels, no rotated
- * format.  This is the LoRA factor gradient dA = x^T (dy B^T) of compute_lora_gradient
+ * fp32 when out_fp32 != 0, else bf16.  n_out is 16 or 32.  Outlier channels: their output rows
+ * come from the side columns, as the decode returns them.  The rotated format: decode(t) is the
+ * rotated decode's bf16 result (hidden/NP a multiple of 128).  This is the LoRA factor gradient dA = x^T (dy B^T) of compute_lora_gradient
  * (low_rank_system_profile_forward.py:14-18, `x.mT @ (dy @ b.mT)`) read from the codes: a
  * reduction over the rows.  The rows are split into groups whose fp32 partials [hidden, n_out]
  * go to `workspace` (16-byte aligned, at least lrq_dequant_gemm_t_workspace(t, n_out) bytes),

@@ -124,6 +124,9 @@ def test_dequant_gemm_t_arguments(L):
     # 32 column groups -> ceil(256 / 32) = 8 row groups, for n = 16 and n = 32 alike
     assert L.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(big), 16) == 8 * 4096 * 16 * 4
     assert L.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(big), 32) == 8 * 4096 * 32 * 4
+    # rotated: one column group per 128-column rotation block of a plane (16), ceil(256 / 16) = 16 row groups
+    assert L.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(_desc(L, rows=16384, flags=1)), 32) \
+        == 16 * 4096 * 32 * 4
     assert L.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(t), 24) == L.LRQ_ERR_UNSUPPORTED
     assert L.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(_desc(L, bits=3)), 16) == L.LRQ_ERR_UNSUPPORTED
     p, q = ctypes.c_void_p(0x10000), ctypes.c_void_p(0x20000)
@@ -137,7 +140,10 @@ def test_dequant_gemm_t_arguments(L):
     assert call(t, w=None) == L.LRQ_ERR_NULL
     assert call(t, wb=ws - 4) == L.LRQ_ERR_WORKSPACE
     assert call(t, w=ctypes.c_void_p(0x40008)) == L.LRQ_ERR_ALIGN
-    assert call(_desc(L, flags=1)) == L.LRQ_ERR_UNSUPPORTED
+    # the rotated format needs planes of whole 128-column rotation blocks (384 / 2 = 192 is not)
+    assert call(_desc(L, flags=1, hidden=384)) == L.LRQ_ERR_UNSUPPORTED
+    assert L.call_raw("lrq_dequant_gemm_t_workspace", ctypes.byref(_desc(L, flags=1, hidden=384)), 16) \
+        == L.LRQ_ERR_UNSUPPORTED
 
 
 def test_lora_grads_arguments(L):

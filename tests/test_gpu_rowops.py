@@ -158,7 +158,7 @@ def test_dequant_gemm_outlier_limit(pkg, dev):
 
 @pytest.mark.parametrize("rows,hidden,rank,bits,group,n_out,out_dtype", [
     (100, 4096, 16, 4, 64, 16, torch.float32),     # north-star width, reduced rows
-    (3000, 4096, 16, 4, 64, 16, torch.float32),    # 16 row groups, ragged last block
+    (3000, 4096, 16, 4, 64, 16, torch.float32),    # 6 row groups of 32 blocks, ragged last group and block
     (700, 4096, 32, 4, 64, 32, torch.bfloat16),    # rank 32, n = 32, bf16 out
     (300, 2048, 16, 8, 128, 16, torch.float32),    # int8 / g128, 2 units per wave
     (200, 1024, 16, 4, 128, 32, torch.float32),    # int4 / g128: one unit per wave

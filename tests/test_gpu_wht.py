@@ -260,3 +260,101 @@ def test_outliers_with_rotation(pkg, dev, rows, n, rank, bits, group, k):
         err = np.abs(out.cpu().numpy().astype(np.float64) - xd @ af)
         bound = 1e-5 * (np.abs(xd) @ np.abs(af)) + 1e-9
         assert (err <= bound).all(), float((err / bound).max())
+    # x_hat^T g: the side columns' output rows come from the side values, the rest from the
+    # rotated x_hat (any channel count)
+    gm = (torch.randn(rows, 16, generator=torch.Generator().manual_seed(k + 1)) * 0.05).to(torch.bfloat16)
+    da = pkg.dequant_gemm_t(c, gm.to(dev))
+    torch.cuda.synchronize()
+    xd = O.bf16_to_f32(bits16(xh)).astype(np.float64)
+    gf = O.bf16_to_f32(bits16(gm)).astype(np.float64)
+    err = np.abs(da.cpu().numpy().astype(np.float64) - xd.T @ gf)
+    bound = 1e-5 * (np.abs(xd).T @ np.abs(gf)) + 1e-9
+    assert (err <= bound).all(), float((err / bound).max())
+
+
+@pytest.mark.parametrize("rows,n,rank,n_out,out_dtype,bits,group", [
+    (64, 5120, 16, 16, torch.float32, 4, 64),     # config 4's format
+    (37, 2560, 0, 32, torch.bfloat16, 4, 64),     # n = 32: one plane per wave; ragged rows
+    (40, 2048, 16, 16, torch.float32, 8, 128),    # int8 / g128: one unit per rotation block
+    (300, 2048, 32, 32, torch.float32, 4, 64),    # rank 32, several blocks per wave
+    (30, 2048, 16, 32, torch.float32, 4, 128),    # int4 / g128
+    (50, 1024, 0, 16, torch.float32, 8, 64),      # int8 / g64: two units per rotation block
+    (7995, 2048, 16, 16, torch.float32, 4, 64),   # 16 row groups of 32 blocks (XCD-aware mapping), ragged ends
+    (3000, 4096, 16, 32, torch.float32, 4, 64),   # fewer blocks than whole chunks for 256 workgroups
+])
+def test_rotated_dequant_gemm_t(pkg, dev, rows, n, rank, n_out, out_dtype, bits, group):
+    """x_hat^T @ g on the rotated format, fused (the rotation's transposed MFMA form leaves x_hat
+    with the rows along the registers): against the float64 product on the device's rotated
+    decode within the fp32 accumulation bound (one bf16 rounding more for bf16 out), and against
+    the oracle's rotated decode within the floating-point bar; the allocation-free entry point
+    gives the same bits."""
+    print(f"[rot gemm_t] rows={rows} n={n} rank={rank} n_out={n_out} {out_dtype} int{bits}/g{group}", flush=True)
+    x = pkg.inputs.activation(rows, n, 8, 20.0, seed=n + n_out + 1)
+    V = pkg.inputs.basis(n, rank, seed=6) if rank else None
+    gm = (torch.randn(rows, n_out, generator=torch.Generator().manual_seed(rows)) * 0.05).to(torch.bfloat16)
+    c = pkg.encode(x.to(dev), V.to(dev) if V is not None else None, bits=bits, group_size=group, hadamard=True)
+    out = pkg.dequant_gemm_t(c, gm.to(dev), out_dtype=out_dtype)
+    out2 = torch.empty_like(out)
+    pkg.dequant_gemm_t_noalloc(c, gm.to(dev), out2)
+    xh = pkg.decode(c)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+    xd = O.bf16_to_f32(bits16(xh)).astype(np.float64)
+    gf = O.bf16_to_f32(bits16(gm)).astype(np.float64)
+    ref = xd.T @ gf
+    bound = 1e-5 * (np.abs(xd).T @ np.abs(gf)) + 1e-9
+    if out_dtype == torch.float32:
+        got = out.cpu().numpy().astype(np.float64)
+        err = np.abs(got - ref)
+        assert (err <= bound).all(), (float(err.max()), float((err / bound).max()))
+    else:
+        got = O.bf16_to_f32(bits16(out)).astype(np.float64)
+        ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))) - 7)
+        assert (np.abs(got - ref) <= ulp + bound).all()
+    ref_xh = O.decode(bits16(c.L) if rank else None, bits16(V) if rank else None, c.codes.cpu().numpy(),
+                      f16(c.scale), f16(c.zero), bits, group, hadamard=True)
+    ref_o = O.gemm_t(O.bf16_to_f32(ref_xh), O.bf16_to_f32(bits16(gm)))
+    if out_dtype == torch.float32:
+        rel = np.linalg.norm(got - ref_o) / np.linalg.norm(ref_o)
+        assert rel <= 1e-3, rel
+    else:
+        assert_fp_close(bits16(out), ref_o, "rotated dequant gemm_t bf16 vs the oracle")
+
+
+@pytest.mark.parametrize("bits,group,rank,n_out", [
+    (4, 64, 16, 16), (4, 64, 32, 32), (8, 128, 16, 16), (4, 128, 0, 32), (8, 64, 0, 32)])
+def test_rotated_dequant_gemm_t_reads_the_decoded_x_hat(pkg, dev, bits, group, rank, n_out):
+    """With g one-hot (column k selects row r_k), x_hat^T g is column k = x_hat[r_k, :] exactly
+    (one product by 1, the rest exact zeros), so the fused kernel's rotated x_hat is compared
+    bit for bit with the rotated decode's, every column of n_out rows."""
+    print(f"[rot gemm_t x_hat] int{bits}/g{group} rank={rank} n={n_out}", flush=True)
+    rows, n = 80, 2048
+    x = pkg.inputs.activation(rows, n, 8, 20.0, seed=bits + group)
+    V = pkg.inputs.basis(n, rank, seed=7) if rank else None
+    c = pkg.encode(x.to(dev), V.to(dev) if V is not None else None, bits=bits, group_size=group, hadamard=True)
+    sel = np.sort(np.random.default_rng(n_out + rank).choice(rows, n_out, replace=False))
+    gm = torch.zeros(rows, n_out, dtype=torch.bfloat16)
+    gm[torch.as_tensor(sel), torch.arange(n_out)] = 1.0
+    out = pkg.dequant_gemm_t(c, gm.to(dev))
+    xh = pkg.decode(c)
+    torch.cuda.synchronize()
+    want = O.bf16_to_f32(bits16(xh))[sel, :].T
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32)), \
+        int((got != want).sum())
+
+
+def test_rotated_lora_grads(pkg, dev):
+    """lora_grads on the rotated format (the two fused products): the same bits as dequant_gemm
+    and dequant_gemm_t called one by one."""
+    rows, n = 200, 4096
+    x = pkg.inputs.activation(rows, n, 8, 20.0, seed=9)
+    V = pkg.inputs.basis(n, 16, seed=9)
+    c = pkg.encode(x.to(dev), V.to(dev), bits=4, group_size=64, hadamard=True)
+    a = (torch.randn(n, 16, generator=torch.Generator().manual_seed(1)) / np.sqrt(n)).to(torch.bfloat16).to(dev)
+    gm = (torch.randn(rows, 16, generator=torch.Generator().manual_seed(2)) * 0.05).to(torch.bfloat16).to(dev)
+    xa, da = pkg.lora_grads(c, a, gm)
+    xa1 = pkg.dequant_gemm(c, a, out_dtype=torch.bfloat16).reshape(-1, 16)
+    da1 = pkg.dequant_gemm_t(c, gm, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(xa, xa1) and torch.equal(da, da1)

@@ -362,8 +362,6 @@ def dequant_gemm_t(c: CompressedActivation, g: torch.Tensor, out_dtype=torch.flo
         raise ValueError("g must be bf16 [rows, n] (leading dimensions those of the activation)")
     if out_dtype not in (torch.float32, torch.bfloat16):
         raise ValueError("out_dtype must be float32 or bfloat16")
-    if c.hadamard:
-        raise ValueError("dequant_gemm_t: the rotated format is not supported")
     g2 = g2.contiguous()
     n_out = g2.shape[1]
     t = c.descriptor()
@@ -382,8 +380,9 @@ def lora_grads(c: CompressedActivation, a: torch.Tensor, g: torch.Tensor, xa_dty
                da_dtype=torch.float32) -> tuple[torch.Tensor, torch.Tensor]:
     """(decode(c) @ a, decode(c)^T @ g) — the two products of compute_lora_gradient
     (low_rank_system_profile_forward.py:14-18) that read the saved x, from one pass over the codes
-    where the format allows it (int4 / g64 / rank 16, n = 16, rows of a multiple of 512 columns);
-    otherwise ``dequant_gemm`` and ``dequant_gemm_t``.  a: bf16 [N, n]; g: bf16 [rows, n]."""
+    where the format allows it (int4 / g64 / rank 16, n = 16, rows of a multiple of 512 columns,
+    not rotated); otherwise ``dequant_gemm`` and ``dequant_gemm_t``.  a: bf16 [N, n]; g: bf16
+    [rows, n]."""
     _require_device(a, g)
     g2 = g.reshape(-1, g.shape[-1]) if g.dim() >= 2 else g
     if a.dtype != torch.bfloat16 or a.dim() != 2 or a.shape[0] != c.hidden:
@@ -396,7 +395,7 @@ def lora_grads(c: CompressedActivation, a: torch.Tensor, g: torch.Tensor, xa_dty
     n_out = a.shape[1]
     t = c.descriptor()
     ws_bytes = _lib.call_raw("lrq_lora_grads_workspace", ctypes.byref(t), n_out)
-    if ws_bytes == _lib.LRQ_ERR_UNSUPPORTED or c.hadamard:
+    if ws_bytes == _lib.LRQ_ERR_UNSUPPORTED:
         xa = dequant_gemm(c, a, out_dtype=xa_dtype).reshape(-1, n_out)
         return xa, dequant_gemm_t(c, g2, out_dtype=da_dtype)
     if ws_bytes < 0:
@@ -424,8 +423,6 @@ def dequant_gemm_t_noalloc(c: CompressedActivation, g: torch.Tensor, out: torch.
     if out.dtype not in (torch.float32, torch.bfloat16) or tuple(out.shape) != (c.hidden, n_out) \
             or not out.is_contiguous():
         raise ValueError("out must be a contiguous fp32 or bf16 [N, n]")
-    if c.hadamard:
-        raise ValueError("dequant_gemm_t_noalloc: the rotated format is not supported")
     t = c.descriptor()
     with torch.cuda.device(c.device):
         call("lrq_dequant_gemm_t_noalloc", ctypes.byref(t), _p(g), n_out, n_out, _p(out), n_out,

@@ -1281,6 +1281,205 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t(
   }
 }
 
+// Transposed dequant-GEMM on the rotated format: part[rg][n][k] = sum over the rows m of row
+// group rg of x_hat[m][n] * gm[m][k], x_hat = bf16(WHT128(bf16(Y'))) blockwise as the rotated
+// decode returns it.  A workgroup takes one 128-column rotation block of each plane (the
+// 128 / G units cgi * 128 / G ..) over one row group; its waves take whole 16-row blocks each,
+// with no LDS and no barrier until the final reduction.  Per block a lane reconstructs Y' of
+// row j at 32 columns (the units' G/4-column quarters, as in the decode), which, packed to bf16,
+// is the data operand of the rotation; the rotation's MFMAs run with the data as the A operand
+// and the sign matrix as the B operand (the transposed product of the decode's wht128_lds, with
+// the same operand registers and the same sums), so their output holds, in lane (j, g), rows
+// 4g .. 4g+3 of one rotated column: K along the registers, the layout of the product with gm
+// (gm's rows transposed by an identity MFMA as in k_dequant_gemm_t), with no transpose of x_hat.
+// The rotation is the Sylvester-ordered Hadamard matrix, H[o][i] = (-1)^popcount(o & i), so
+// feeding the 32 values of a lane in another column order permutes the bits of the column
+// index and the rotated columns come out permuted the same way: rot_col gives the column of
+// output tile q in lane j for each unit width.  With two planes and large accumulators a wave
+// takes one plane (PPW = 1; waves w and w + 1 read the same code bytes).  The waves of a plane
+// are summed through LDS in wave order and leave as 16-byte rows.
+template <int G>
+__device__ __forceinline__ int rot_col(int j, int q) {
+  static_assert(G == 64 || G == 128, "64- or 128-column units");
+  // G = 128: the lane's columns 32g + 8c + e are the nominal order; G = 64: the lane holds
+  // columns 16g .. +15 of each of the two units, so nominal index bits (4; 5, 6) are column bits
+  // (6; 4, 5)
+  if constexpr (G == 128) return (j & 3) + 4 * q + 32 * (j >> 2);
+  else return (j & 3) + 4 * (q & 3) + 16 * (j >> 2) + 64 * (q >> 2);
+}
+
+template <int BITS, int G, int R, int KT, int NW, int PPW, int PD, int NBM>
+__global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t_rot(
+    const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
+    const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
+    const uint16_t* __restrict__ gm, int64_t ldg, float* __restrict__ part, int bpg, int ncg, bool xcd_map) {
+  constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, E = G / 4;
+  constexpr int U = 128 / G;                // units of one rotation block
+  constexpr int NG = NP / PPW;              // plane groups: waves w, w + NG, ... share a plane set
+  constexpr int WB = NW / NG;               // waves per plane group
+  constexpr int NACC = PPW * 8 * KT;        // f32x4 accumulators per lane
+  constexpr int CH = NACC < 8 ? NACC : 8;   // accumulators per LDS round
+  static_assert(NP % PPW == 0 && NW % NG == 0 && NACC % CH == 0, "plane groups and reduction rounds");
+  __shared__ f32x4 red[NW][CH][64];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int grp = w % NG, wb = w / NG;      // plane group; the wave's place among the group's waves
+  const int nrb = (M + 15) / 16;
+  // workgroup -> (rotation block, row group), XCD-aware as in k_dequant_gemm_t
+  const int id = blockIdx.x;
+  const int cgi = __builtin_amdgcn_readfirstlane(xcd_map ? (id >> 3) % ncg : id % ncg);
+  const int rgi = __builtin_amdgcn_readfirstlane(xcd_map ? (id & 7) + 8 * ((id >> 3) / ncg) : id / ncg);
+  const int u0 = cgi * U;
+  const int rb_lo = rgi * bpg, rb_hi = min(rb_lo + bpg, nrb);
+  const int KO = 16 * KT;
+  const u32x2 ident = identity_bop(j, g);
+  u32x4 wop[2][2];
+#pragma unroll
+  for (int q0 = 0; q0 < 2; ++q0)
+#pragma unroll
+    for (int n = 0; n < 2; ++n) wop[q0][n] = wht_base_operand(j, g, q0, n != 0);
+
+  // reconstruction operands of the wave's planes (the same for every block)
+  u32x2 vop[PPW][U][G / 16][RT];
+  if constexpr (R > 0) {
+#pragma unroll
+    for (int pi = 0; pi < PPW; ++pi)
+#pragma unroll
+      for (int ul = 0; ul < U; ++ul) load_vops<G, R>(V, unit_base(grp * PPW + pi, u0 + ul, N, NP, G), j, g, vop[pi][ul]);
+  }
+  f32x4 acc[NACC];
+#pragma unroll
+  for (int a = 0; a < NACC; ++a) acc[a] = zero4();
+
+  struct Blk {
+    u32x4 cb[U][G / 64];  // row j: the lane's G/4 code bytes of each unit
+    uint32_t qp[U][PPW];  // row j: (scale, zero) of the wave's planes of each unit
+    u32x2 lop[RT];        // row j: L ranks 4g .. (B operand of the reconstruction)
+    u32x2 gop[KT];        // row j: gm columns 16t + 4g ..
+  };
+  // 32-bit lane offsets from the block's wave-uniform bases, rows past M clamped to the last
+  // (min(r, lim) * ld = min(r * ld, lim * ld)); strides below 2^24 bytes are checked by the launch
+  const uint32_t ldc1 = (uint32_t)ldc, ldq2 = (uint32_t)ldq * 2, ldl2 = (uint32_t)ldl * 2, ldg2 = (uint32_t)ldg * 2;
+  const uint32_t coff = (uint32_t)j * ldc1, qoff = (uint32_t)j * ldq2, loff = (uint32_t)j * ldl2,
+                 goff = (uint32_t)j * ldg2;
+  const uint32_t rl = (uint32_t)(8 * g);
+  auto load = [&](int rb, Blk& d) __attribute__((always_inline)) {
+    const int r0 = rb * 16;  // wave-uniform
+    const uint32_t lim = (uint32_t)min(M - 1 - r0, 15);
+    const uint8_t* cbase = codes + (int64_t)r0 * ldc + u0 * G;
+    const uint8_t* qbase = reinterpret_cast<const uint8_t*>(qparams + (int64_t)r0 * ldq) + u0 * NP * 4;
+    const uint32_t co = min(coff, lim * ldc1) + (uint32_t)(E * g), qo = min(qoff, lim * ldq2);
+#pragma unroll
+    for (int ul = 0; ul < U; ++ul) {
+#pragma unroll
+      for (int i = 0; i < G / 64; ++i) d.cb[ul][i] = ld16_stream(cbase + (co + (uint32_t)(ul * G + 16 * i)));
+      if constexpr (PPW == 2) {
+        const u32x2 q = ld8(qbase + (qo + (uint32_t)(ul * 8)));
+        d.qp[ul][0] = q[0];
+        d.qp[ul][1] = q[1];
+      } else {
+        d.qp[ul][0] = ld4(qbase + (qo + (uint32_t)(ul * NP * 4 + grp * 4)));
+      }
+    }
+    if constexpr (R > 0) {
+      const uint8_t* lbase = reinterpret_cast<const uint8_t*>(Lin + (int64_t)r0 * ldl);
+      const uint32_t lo = min(loff, lim * ldl2) + rl;
+#pragma unroll
+      for (int t = 0; t < RT; ++t) d.lop[t] = ld8(lbase + (lo + 32 * t));
+    }
+    const uint8_t* gbase = reinterpret_cast<const uint8_t*>(gm + (int64_t)r0 * ldg);
+    const uint32_t go = min(goff, lim * ldg2) + rl;
+#pragma unroll
+    for (int t = 0; t < KT; ++t) d.gop[t] = ld8(gbase + (go + 32 * t));
+  };
+
+  const float kScale = 0.08838834764831845f;  // fp32(1/sqrt(128)), as in wht128_lds
+  auto process = [&](const Blk& cur, int rb, bool blive) __attribute__((always_inline)) {
+    // g^T operands: rows past M contribute nothing (their clamped x_hat is finite)
+    const bool live = blive && rb * 16 + j < M;
+    u32x2 a2[KT];
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      const u32x2 gv = live ? cur.gop[t] : u32x2{0u, 0u};
+      const f32x4 d = mfma_16x16x16(gv, ident, zero4());  // lane (j, g): gm[4g + v][16t + j]
+      a2[t] = u32x2{pack_bf16x2_exact(d[0], d[1]), pack_bf16x2_exact(d[2], d[3])};
+    }
+#pragma unroll
+    for (int pi = 0; pi < PPW; ++pi) {
+      const int p = grp * PPW + pi;
+      float xh[32];  // row j: Y' at the lane's E columns of each unit
+#pragma unroll
+      for (int ul = 0; ul < U; ++ul) reconstruct_plane<BITS, G, R>(cur.cb[ul], cur.qp[ul][pi], p, vop[pi][ul], cur.lop, xh + E * ul);
+      u32x4 xv[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) xv[c] = pack8(xh + 8 * c);  // bf16(Y')
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        f32x4 y = zero4();
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int flip = (((q >> 1) & c & 1) ^ ((q >> 2) & (c >> 1) & 1));
+          y = mfma_16x16x32(xv[c], wop[q & 1][flip], y);
+        }
+        // x_hat rows 4g + v of column rot_col(j, q)
+        const u32x2 xq = u32x2{pack_bf16x2(y[0] * kScale, y[1] * kScale), pack_bf16x2(y[2] * kScale, y[3] * kScale)};
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+          f32x4& c = acc[(pi * 8 + q) * KT + kt];
+          c = mfma_16x16x16(a2[kt], xq, c);
+        }
+      }
+    }
+  };
+
+  // the wave's blocks rb_lo + wb + i WB, i < nb, in straight-line chunks of NBM blocks with a
+  // ring of PD slots (as in k_dequant_gemm_t)
+  const int nb = rb_lo + wb < rb_hi ? (rb_hi - rb_lo - wb + WB - 1) / WB : 0;
+  const int last = rb_hi - 1;
+  for (int c0 = 0; c0 < nb; c0 += NBM) {  // wave-uniform
+    Blk ring[PD];
+#pragma unroll
+    for (int sl = 0; sl < PD; ++sl) load(min(rb_lo + wb + (c0 + sl) * WB, last), ring[sl]);
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, NBM>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      const int rb = rb_lo + wb + (c0 + i) * WB;
+      process(ring[i % PD], rb, c0 + i < nb);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (i + PD < NBM) load(min(rb + PD * WB, last), ring[i % PD]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  }
+
+  // acc[(pi 8 + q) KT + kt] in lane (j, g), component v: column
+  // n = p N/NP + u0 G + rot_col(j, q), k = 16 kt + 4g + v (p = grp PPW + pi)
+  float* partg = part + (int64_t)rgi * N * KO;
+#pragma unroll
+  for (int c0 = 0; c0 < NACC; c0 += CH) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) red[w][c][lane] = acc[c0 + c];
+    __syncthreads();
+    for (int e = threadIdx.x; e < NG * CH * 64; e += NW * 64) {
+      const int eg = e / (CH * 64), c = (e >> 6) % CH, ln = e & 63;
+      f32x4 s = red[eg][c][ln];
+#pragma unroll
+      for (int i = 1; i < WB; ++i) {
+        const f32x4 o = red[eg + NG * i][c][ln];
+        s[0] += o[0];
+        s[1] += o[1];
+        s[2] += o[2];
+        s[3] += o[3];
+      }
+      const int a = c0 + c, kt = a % KT, q = (a / KT) % 8, p = eg * PPW + a / (8 * KT);
+      const int jj = ln & 15, gg = ln >> 4;
+      const int n = p * (N / NP) + u0 * G + rot_col<G>(jj, q);
+      st16(partg + (int64_t)n * KO + 16 * kt + 4 * gg,
+           u32x4{__float_as_uint(s[0]), __float_as_uint(s[1]), __float_as_uint(s[2]), __float_as_uint(s[3])});
+    }
+    __syncthreads();
+  }
+}
+
 // Outlier channels in dequant_gemm_t: x_hat[:, idx[k]] = bf16(side[:, k]), so output row idx[k]
 // is sum over the rows of bf16(side[m, k]) * G[m, :].  One workgroup per channel overwrites that
 // row after the main kernels (fp32 sums, a block reduction in a fixed order).
@@ -1548,17 +1747,40 @@ struct GemmTPlan {
   int64_t ws_bytes;
 };
 
-static GemmTPlan gemm_t_plan(int64_t rows, int64_t hidden, int bits, int group, int n_out) {
+// k_dequant_gemm_t_rot: planes per wave (one where two planes' accumulators would not fit
+// beside the rest) and blocks per straight-line chunk.
+constexpr int gemm_t_rot_ppw(int bits, int n_out, int rank) {
+  return (8 / bits == 2 && (n_out == 32 || rank == 32)) ? 1 : 8 / bits;
+}
+constexpr int kGemmTRotChunk = 4;
+// k_dequant_gemm_t: accumulators alone take 128 registers (chunks of the ring's two blocks)
+constexpr bool gemm_t_big(int bits, int group, int n_out) { return (8 / bits) * (group / 16) * (n_out / 16) > 16; }
+
+// The rotated format's column groups are its rotation blocks (128 columns of each plane).  Row
+// groups hold whole chunks per wave where the rows allow (a chunk's blocks past the wave's last
+// are computed with a zero g: at 8192 x 5120 the even split gave the waves 9.25 blocks each in
+// chunks of 8, so 16 were computed): the blocks per group are the nearest multiple of (waves
+// per plane) x (chunk) to the even split.
+static GemmTPlan gemm_t_plan(int64_t rows, int64_t hidden, int bits, int group, int rank, int n_out, bool rot) {
   constexpr int NW = 8;
   GemmTPlan pl{};
   const int64_t units = hidden / ((int64_t)group * (8 / bits));
-  pl.upw = 1;
+  pl.upw = rot ? 128 / group : 1;
   pl.cg = (int)(units / pl.upw);
   const int64_t nrb = (rows + 15) / 16;
   if (nrb == 0) return pl;  // rg = 0: the sum kernel writes zeros
   const int64_t want = std::max<int64_t>(1, (256 + pl.cg - 1) / pl.cg);
-  const int64_t rg = std::min<int64_t>(want, std::max<int64_t>(1, nrb / NW));
-  pl.bpg = (int)((nrb + rg - 1) / rg);
+  if (rot) {
+    const int64_t q = (int64_t)kGemmTRotChunk * NW / ((8 / bits) / gemm_t_rot_ppw(bits, n_out, rank));
+    const int64_t even = (nrb + want - 1) / want;
+    pl.bpg = (int)std::max<int64_t>(q, (even + q / 2) / q * q);
+  } else {
+    const int64_t rg = std::min<int64_t>(want, std::max<int64_t>(1, nrb / NW));
+    const int64_t even = (nrb + rg - 1) / rg;
+    // the chunk the launch takes for this split (2, 4 or 8 blocks)
+    const int64_t q = NW * (gemm_t_big(bits, group, n_out) ? 2 : (even + NW - 1) / NW <= 4 ? 4 : 8);
+    pl.bpg = (int)std::max<int64_t>(q, (even + q / 2) / q * q);
+  }
   pl.rg = (int)((nrb + pl.bpg - 1) / pl.bpg);
   pl.ws_bytes = (int64_t)pl.rg * hidden * n_out * 4;
   return pl;
@@ -1571,10 +1793,19 @@ static int gemm_t_run(const lrq_tensors* t, const void* gmat, int64_t ldg, void*
   constexpr int UPW = 1, PD = 2;  // units per workgroup, blocks in flight per wave
   const int M = (int)t->rows, N = (int)t->hidden;
   if (!strides_fit24(t, ldg)) return LRQ_ERR_UNSUPPORTED;
-  if (pl.rg > 0) {
+  if ((t->flags & LRQ_FLAG_HADAMARD) && pl.rg > 0) {
+    constexpr int PPW = gemm_t_rot_ppw(BITS, 16 * KT, R);
+    LRQ_TRY(launch((k_dequant_gemm_t_rot<BITS, G, R, KT, NW, PPW, PD, kGemmTRotChunk>), dim3(pl.cg * pl.rg),
+                   dim3(NW * 64), 0, s,
+                   (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp, (const uint16_t*)t->L,
+                   t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)gmat, ldg, ws, pl.bpg, pl.cg,
+                   pl.rg % 8 == 0));
+  } else if (pl.rg > 0) {
     // blocks per chunk: the waves' block count ceil(bpg / NW) where it is at most 4, else 8;
-    // just the ring's PD blocks where the accumulators alone take 128 registers
-    constexpr bool kBig = (8 / BITS) * (UPW * G / 16) * KT > 16;
+    // just the ring's PD blocks where the accumulators alone take 128 registers (the plan makes
+    // bpg a multiple of NW x chunk)
+    static_assert(UPW == 1, "the plan's chunk rule assumes one unit per workgroup");
+    constexpr bool kBig = gemm_t_big(BITS, G, 16 * KT);
     auto kern = kBig ? k_dequant_gemm_t<BITS, G, R, KT, NW, UPW, PD, PD>
                 : (pl.bpg + NW - 1) / NW <= 4 ? k_dequant_gemm_t<BITS, G, R, KT, NW, UPW, PD, kBig ? PD : 4>
                                               : k_dequant_gemm_t<BITS, G, R, KT, NW, UPW, PD, kBig ? PD : 8>;
@@ -1686,11 +1917,21 @@ extern "C" int lrq_dequant_gemm(const lrq_tensors* t, const void* a, int32_t n_o
   LRQ_FORMATS(gemm_nout, t, a, n_out, out, ldo, f32, s)
 }
 
+// The rotated format needs planes of whole rotation blocks.
+static bool gemm_t_format_ok(const lrq_tensors* t) {
+  return !(t->flags & LRQ_FLAG_HADAMARD) || (t->hidden / (8 / t->bits)) % 128 == 0;
+}
+
+static GemmTPlan gemm_t_plan(const lrq_tensors* t, int n_out) {
+  return gemm_t_plan(t->rows, t->hidden, t->bits, t->group, t->rank, n_out, (t->flags & LRQ_FLAG_HADAMARD) != 0);
+}
+
 extern "C" int64_t lrq_dequant_gemm_t_workspace(const lrq_tensors* t, int32_t n_out) {
   int st = validate_tensors(t);
   if (st) return st;
   if (n_out != 16 && n_out != 32) return LRQ_ERR_UNSUPPORTED;
-  return gemm_t_plan(t->rows, t->hidden, t->bits, t->group, n_out).ws_bytes;
+  if (!gemm_t_format_ok(t)) return LRQ_ERR_UNSUPPORTED;
+  return gemm_t_plan(t, n_out).ws_bytes;
 }
 
 extern "C" int lrq_dequant_gemm_t(const lrq_tensors* t, const void* g, int64_t ldg, int32_t n_out, void* out,
@@ -1702,8 +1943,8 @@ extern "C" int lrq_dequant_gemm_t(const lrq_tensors* t, const void* g, int64_t l
   if (n_out != 16 && n_out != 32) return LRQ_ERR_UNSUPPORTED;
   if (ldg < n_out || ldo < n_out) return LRQ_ERR_SHAPE;
   if (!aligned(g, 8) || (ldg % 4) != 0 || !aligned(out, out_fp32 ? 4 : 2)) return LRQ_ERR_ALIGN;
-  if (t->flags & LRQ_FLAG_HADAMARD) return LRQ_ERR_UNSUPPORTED;
-  const GemmTPlan pl = gemm_t_plan(t->rows, t->hidden, t->bits, t->group, n_out);
+  if (!gemm_t_format_ok(t)) return LRQ_ERR_UNSUPPORTED;
+  const GemmTPlan pl = gemm_t_plan(t, n_out);
   if (pl.ws_bytes > 0) {
     if (workspace == nullptr) return LRQ_ERR_NULL;
     if (workspace_bytes < pl.ws_bytes) return LRQ_ERR_WORKSPACE;
@@ -1724,8 +1965,8 @@ extern "C" int lrq_dequant_gemm_t_noalloc(const lrq_tensors* t, const void* g, i
   if (n_out != 16 && n_out != 32) return LRQ_ERR_UNSUPPORTED;
   if (ldg < n_out || ldo < n_out) return LRQ_ERR_SHAPE;
   if (!aligned(g, 8) || (ldg % 4) != 0 || !aligned(out, out_fp32 ? 4 : 2)) return LRQ_ERR_ALIGN;
-  if (t->flags & LRQ_FLAG_HADAMARD) return LRQ_ERR_UNSUPPORTED;
-  const GemmTPlan pl = gemm_t_plan(t->rows, t->hidden, t->bits, t->group, n_out);
+  if (!gemm_t_format_ok(t)) return LRQ_ERR_UNSUPPORTED;
+  const GemmTPlan pl = gemm_t_plan(t, n_out);
   if (pl.ws_bytes > (int64_t)LRQ_GEMM_T_SCRATCH_BYTES) return LRQ_ERR_WORKSPACE;
   float* ws = nullptr;
   st = scratch_on_current_device(&ws);
