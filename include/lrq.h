@@ -103,8 +103,9 @@ int lrq_decode(const lrq_tensors* t, void* out, int64_t ldo, void* stream);
 
 /* The four consumers below may write their output over their second input (dx == dy) except
  * where they run as a decode followed by a dense pass (the rotated format in shapes without a
- * fused rotated kernel; outlier channels or the rotated format in lrq_softmax_bwd): there the
- * aliasing call returns LRQ_ERR_UNSUPPORTED. */
+ * fused rotated kernel; in lrq_softmax_bwd, outlier channels, and the rotated format with planes
+ * that are not whole 128-column rotation blocks): there the aliasing call returns
+ * LRQ_ERR_UNSUPPORTED. */
 
 /* dx = dy * s(x)(1 + x(1 - s(x))), s = sigmoid, x = decode(t), fused.
  * Replaces triton_silu_backward_fuse_extraction (extraction_fuse_silu_backward.py:192-216). */

@@ -89,12 +89,16 @@ def test_rotated_format_c4_recipe(pkg, dev, rows, n):
     (40, 2048, 32, 4, 64, "mul"),     # rank 32 (two blocks in flight)
     (30, 2048, 16, 8, 128, "silu"),   # int8 / g128: fused (4 units per workgroup)
     (52, 4096, 0, 8, 128, "gelu"),    # int8 / g128 at rank 0, config 3's width
-    (24, 2048, 16, 4, 64, "softmax"), # softmax: decode into the output, then the dense backward in place
+    (24, 2048, 16, 4, 64, "softmax"), # softmax: fused two-sweep kernel over rotation blocks
+    (40, 2048, 32, 4, 64, "softmax"), # rank 32
+    (33, 4096, 16, 8, 128, "softmax"),  # int8 / g128
+    (24, 384, 16, 4, 64, "softmax"),  # planes of 192 columns: decode, then the dense backward in place
 ])
 def test_rotated_consumers(pkg, dev, rows, n, rank, bits, group, op):
     """Consumers on the rotated format: bit-identical to the dense op on the device's own decode
-    (the same rotation code and the same elementwise formula), and within the floating-point bar
-    of the oracle's rotated decode followed by the op in float64."""
+    (the same rotation code and the same elementwise formula; the fused softmax sums its rows in
+    another order, so it is held to the floating-point bar there), and within the floating-point
+    bar of the oracle's rotated decode followed by the op in float64."""
     print(f"[rot consumer] rows={rows} n={n} rank={rank} int{bits}/g{group} {op}", flush=True)
     x = pkg.inputs.activation(rows, n, 8, 20.0, seed=n + rank)
     if op == "softmax":
@@ -115,7 +119,10 @@ def test_rotated_consumers(pkg, dev, rows, n, rank, bits, group, op):
     dense = {"silu": pkg.triton_silu_backward, "gelu": pkg.triton_gelu_backward, "mul": pkg.triton_hadamard,
              "softmax": pkg.triton_softmax_backward}[op](xh, y.to(dev))
     torch.cuda.synchronize()
-    assert np.array_equal(bits16(out), bits16(dense))
+    if op == "softmax" and (n // (8 // bits)) % 128 == 0:
+        assert_fp_close(bits16(out), O.softmax_bwd(O.bf16_to_f32(bits16(xh)), yf), "fused rotated softmax vs dense")
+    else:
+        assert np.array_equal(bits16(out), bits16(dense))
     ref_xh = O.decode(bits16(c.L) if rank else None, bits16(V) if rank else None, c.codes.cpu().numpy(),
                       f16(c.scale), f16(c.zero), bits, group, hadamard=True)
     # rank 32 reconstructs with MFMA fp32 sums that can sit a step from the oracle's, and the
@@ -125,6 +132,41 @@ def test_rotated_consumers(pkg, dev, rows, n, rank, bits, group, op):
         O.bf16_to_f32(ref_xh), yf)
     rep = assert_fp_close(bits16(out), ref, f"rotated {op} vs the oracle")
     print(f"[rot consumer] {rep}", flush=True)
+
+
+@pytest.mark.parametrize("bits,group,rank", [(4, 64, 16), (4, 64, 32), (8, 128, 16), (4, 128, 0), (8, 64, 0)])
+def test_rotated_softmax_reads_the_decoded_p(pkg, dev, bits, group, rank):
+    """The fused rotated softmax backward with dP one-hot per row (dP[r, k_r] = 1): the row sum is
+    P[r, k_r] exactly and dS[r, c] = bf16(fp32(P[r, c] (0 - P[r, k_r]))) (fp32(1 - P) at c = k_r), so
+    dS computed in float32 from the rotated decode's P must match bit for bit: the kernel's P is
+    the decode's.  In place (dS over dP) gives the same bits."""
+    import ctypes
+    L = importlib.import_module("triton-kernel-test_amd._lib")
+    lib = L.load()
+    print(f"[rot softmax P] int{bits}/g{group} rank={rank}", flush=True)
+    rows, n = 70, 2048
+    x = torch.softmax(pkg.inputs.activation(rows, n, 8, 20.0, seed=bits * group).float() / 8.0, dim=-1)
+    x = x.to(torch.bfloat16)
+    V = pkg.inputs.basis(n, rank, seed=11) if rank else None
+    c = pkg.encode(x.to(dev), V.to(dev) if V is not None else None, bits=bits, group_size=group, hadamard=True)
+    k = np.random.default_rng(rows + rank).integers(0, n, rows)
+    dp = torch.zeros(rows, n, dtype=torch.bfloat16)
+    dp[torch.arange(rows), torch.as_tensor(k)] = 1.0
+    out = pkg.softmax_backward_compressed(c, dp.to(dev))
+    xh = pkg.decode(c)
+    buf = dp.to(dev)
+    d = c.descriptor()
+    sp = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    pb = ctypes.c_void_p(buf.data_ptr())
+    st = lib.lrq_softmax_bwd(ctypes.byref(d), pb, n, pb, n, sp)
+    torch.cuda.synchronize()
+    assert st == 0 and torch.equal(buf, out)
+    P = O.bf16_to_f32(bits16(xh)).astype(np.float32)
+    pk = P[np.arange(rows), k]
+    dv = np.zeros_like(P)
+    dv[np.arange(rows), k] = 1.0
+    want = P * (dv - pk[:, None])  # float32 operations, as the kernel's
+    assert np.array_equal(bits16(out), O.round_out(want.astype(np.float64)))
 
 
 @pytest.mark.parametrize("rows,n,rank,bits,group,fused", [

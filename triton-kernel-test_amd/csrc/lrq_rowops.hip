@@ -331,6 +331,230 @@ __global__ __launch_bounds__(NW * 64) void k_softmax_2s(
   }
 }
 
+// Softmax backward on the rotated format, P = bf16(WHT128(bf16(Y'))) blockwise (the rotated
+// decode's result): the two sweeps of k_softmax_2s over the row's rotation blocks instead of
+// its units.  Wave w takes items w, w + NW, ... of the row, an item being one 128-column
+// rotation block of every plane (128/G units).  Per item and plane a lane rebuilds row j's 32
+// columns, gathers them (rot_gather_128) and rotates them in registers (wht128_regs), so P is
+// the decode's bit for bit and sits in lane group g at block columns 32g .. 32g+31, where dP is
+// read and dS written (four 16-byte pieces per lane and plane).  Sweep 1 sums P dP per row (the
+// lane's columns, the row's four lanes, then the waves in order through LDS), sweep 2 rebuilds
+// P and writes dS = P (dP - sum).  A wave reads an item's dP before writing its dS, and no other
+// wave touches those columns, so dS may overwrite dP.  Planes of whole rotation blocks
+// ((N / NP) % 128 == 0).  Rows past the end repeat the last row (identical stores).
+//   HOLD > 0 (1 .. HOLD items per wave; one workgroup per CU walking its row blocks): the
+//            items' V operands are parked in the wave's LDS slots at the start; the wave keeps
+//            its items' codes, qparams and dP of a row block for both sweeps (read once), and
+//            requests each item's inputs of the next block as soon as the second sweep has
+//            used them.
+//   HOLD = 0 (any width): each item's inputs, V operands included, are requested right before
+//            the item is computed, in both sweeps.
+// (Measured alternatives, MI355X, 16384 x 4096 int4/g64 rank 16: P kept in LDS between the
+// sweeps with V read per plane spilled registers, 122 us; without the next-block requests and
+// with a workgroup per row block, 115 us; this form 103 us.)
+template <int BITS, int G, int R, int NW, int HOLD>
+struct SmxRot {
+  static constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, U = 128 / G;
+  static constexpr int VSLOT = U * NP * (G / 16) * RT * 64 * 8;  // one item's V operands in LDS
+  static constexpr size_t LDS = (HOLD > 0 && R > 0) ? (size_t)NW * HOLD * VSLOT : 0;
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+};
+
+template <int BITS, int G, int R, int NW, int HOLD>
+__global__ __launch_bounds__(NW * 64) void k_softmax_rot(
+    const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
+    const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
+    const uint16_t* dp, int64_t lddp, uint16_t* ds, int64_t ldds, int RBW) {
+  using Sm = SmxRot<BITS, G, R, NW, HOLD>;
+  constexpr int NP = Sm::NP, RT = Sm::RT, E = G / 4, U = Sm::U;
+  __shared__ float red[NW][16];
+  extern __shared__ __attribute__((aligned(16))) unsigned char vsm[];  // HOLD, R > 0: [NW][HOLD][VSLOT]
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int nrb = (M + 15) / 16;
+  const int items = N / (NP * 128);
+  const int nmine = (items - w + NW - 1) / NW;  // items of this wave (0 when items < NW and w >= items)
+  const int PW = N / NP;                        // plane width
+  u32x4 wop[2][2];
+#pragma unroll
+  for (int q0 = 0; q0 < 2; ++q0)
+#pragma unroll
+    for (int n = 0; n < 2; ++n) wop[q0][n] = wht_base_operand(j, rot_sign_group<G>(g), q0, n != 0);
+  struct In {
+    u32x4 cb[U][G / 64];
+    uint32_t qp[U][NP];
+    u32x4 d[NP][4];
+  };
+  using Vop = u32x2[U][NP][G / 16][RT];
+  auto load = [&](In& in, int64_t row, int it) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ul = 0; ul < U; ++ul) {
+      const int u = it * U + ul;
+#pragma unroll
+      for (int i = 0; i < G / 64; ++i) in.cb[ul][i] = ld16_stream(codes + row * ldc + u * G + E * g + 16 * i);
+      if constexpr (NP == 2) {
+        const u32x2 q = ld8(qparams + row * ldq + u * 4);
+        in.qp[ul][0] = q[0];
+        in.qp[ul][1] = q[1];
+      } else {
+        in.qp[ul][0] = ld4(qparams + row * ldq + u * 2);
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint16_t* a = dp + row * lddp + p * PW + it * 128 + 32 * g + 8 * k;
+        in.d[p][k] = HOLD > 0 ? ld16_stream(a) : ld16(a);
+      }
+  };
+  auto load_v = [&](Vop& v, int it) __attribute__((always_inline)) {
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int ul = 0; ul < U; ++ul)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) load_vops<G, R>(V, unit_base(p, it * U + ul, N, NP, G), j, g, v[ul][p]);
+    }
+  };
+  // the LDS slot of held item h of this wave; operand (ul, p, q, t) is 64 lanes x 8 bytes
+  auto vslot = [&](int h) { return reinterpret_cast<u32x2*>(vsm + ((size_t)w * HOLD + h) * Sm::VSLOT); };
+  constexpr int NOPS = U * NP * (G / 16) * RT;
+  auto read_v = [&](Vop& v, int h) __attribute__((always_inline)) {
+    if constexpr (R > 0) {
+      const u32x2* sl = vslot(h);
+      u32x2* f = &v[0][0][0][0];
+#pragma unroll
+      for (int o = 0; o < NOPS; ++o) f[o] = sl[o * 64 + lane];
+    }
+  };
+  // sweep 0: part += P * dP over the lane's columns; sweep 1: dS = P (dP - sum)
+  auto work = [&](const In& in, const Vop& v, int it, int sweep, const u32x2* lop, int64_t row, float& part,
+                  float sum) __attribute__((always_inline)) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      float xh[32];
+#pragma unroll
+      for (int ul = 0; ul < U; ++ul) reconstruct_plane<BITS, G, R>(in.cb[ul], in.qp[ul][p], p, v[ul][p], lop, xh + E * ul);
+      u32x4 xv[4];
+      rot_gather_128<G>(xh, xv);
+      float y[32];
+      wht128_regs(xv, wop, y);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        float pr[8], dv[8];
+        unpack8(pack8(y + 8 * k), pr);  // P = bf16(rotated), as the decode stores it
+        unpack8(in.d[p][k], dv);
+        if (sweep == 0) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) part = __builtin_fmaf(pr[e], dv[e], part);
+        } else {
+          float o[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = pr[e] * (dv[e] - sum);
+          st16(ds + row * ldds + p * PW + it * 128 + 32 * g + 8 * k, pack8(o));
+        }
+      }
+    }
+  };
+  // the row's four lanes, then the NW waves in order (through LDS)
+  auto row_sum = [&](float part) __attribute__((always_inline)) {
+    float a = part, c = part;
+    swap32(a, c);
+    part = a + c;
+    a = part, c = part;
+    swap16(a, c);
+    part = a + c;
+    if (g == 0) red[w][j] = part;
+    lds_barrier();
+    float sum = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2) sum += red[w2][j];
+    lds_barrier();  // every wave has read red before the next row block rewrites it
+    return sum;
+  };
+  const int rb_beg = blockIdx.x * RBW, rb_end = min(nrb, rb_beg + RBW);
+  auto load_lop = [&](u32x2* lop, int64_t row) __attribute__((always_inline)) {
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t) lop[t] = ld8(Lin + row * ldl + 16 * t + 4 * g);
+    }
+  };
+  if constexpr (HOLD > 0) {
+    if constexpr (R > 0) {
+      // park this wave's V operands (the host launches this form only when 1 <= nmine <= HOLD);
+      // a wave reads back only the slots it wrote, in order, so no barrier is needed
+#pragma unroll
+      for (int h = 0; h < HOLD; ++h) {
+        if (h < nmine) {
+          Vop v;
+          load_v(v, w + h * NW);
+          u32x2* sl = vslot(h);
+          const u32x2* f = &v[0][0][0][0];
+#pragma unroll
+          for (int o = 0; o < NOPS; ++o) sl[o * 64 + lane] = f[o];
+        }
+      }
+    }
+    In in[HOLD];
+    u32x2 lop[RT], lopn[RT];
+    if (rb_beg < rb_end) {
+      const int64_t row0 = min(rb_beg * 16 + j, M - 1);
+      load_lop(lop, row0);
+#pragma unroll
+      for (int h = 0; h < HOLD; ++h) load(in[h], row0, w + min(h, nmine - 1) * NW);
+    }
+#pragma unroll 1
+    for (int rb = rb_beg; rb < rb_end; ++rb) {
+      const int64_t row = min(rb * 16 + j, M - 1);
+      const bool more = rb + 1 < rb_end;  // wave-uniform
+      const int64_t rown = min((rb + 1) * 16 + j, M - 1);
+      float part = 0.f;
+#pragma unroll
+      for (int h = 0; h < HOLD; ++h) {
+        if (h < nmine) {  // wave-uniform
+          Vop v;
+          read_v(v, h);
+          work(in[h], v, w + h * NW, 0, lop, row, part, 0.f);
+        }
+      }
+      const float sum = row_sum(part);
+      if (more) load_lop(lopn, rown);
+#pragma unroll
+      for (int h = 0; h < HOLD; ++h) {
+        if (h < nmine) {
+          Vop v;
+          read_v(v, h);
+          work(in[h], v, w + h * NW, 1, lop, row, part, sum);
+        }
+        // this item's inputs of the next block, while the rest of this block is computed
+        if (more) load(in[h], rown, w + min(h, nmine - 1) * NW);
+      }
+#pragma unroll
+      for (int t = 0; t < RT; ++t) lop[t] = lopn[t];
+    }
+  } else {
+#pragma unroll 1
+    for (int rb = rb_beg; rb < rb_end; ++rb) {
+      const int64_t row = min(rb * 16 + j, M - 1);
+      u32x2 lop[RT];
+      load_lop(lop, row);
+      float part = 0.f, sum = 0.f;
+#pragma unroll 1
+      for (int sweep = 0; sweep < 2; ++sweep) {
+#pragma unroll 1
+        for (int it = w; it < items; it += NW) {  // wave-uniform
+          In in;
+          Vop v;
+          load(in, row, it);
+          load_v(v, it);
+          work(in, v, it, sweep, lop, row, part, sum);
+        }
+        if (sweep == 0) sum = row_sum(part);
+      }
+    }
+  }
+}
+
 // Row-persistent softmax backward (one workgroup per CU; wave w owns unit w of every row, so
 // a workgroup holds whole rows).  dP moves as whole row segments straight from HBM into an LDS
 // tile (two tiles, block b in tile b&1), is read back in the MFMA layout, and dS is written
@@ -1286,27 +1510,17 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t(
 // decode returns it.  A workgroup takes one 128-column rotation block of each plane (the
 // 128 / G units cgi * 128 / G ..) over one row group; its waves take whole 16-row blocks each,
 // with no LDS and no barrier until the final reduction.  Per block a lane reconstructs Y' of
-// row j at 32 columns (the units' G/4-column quarters, as in the decode), which, packed to bf16,
-// is the data operand of the rotation; the rotation's MFMAs run with the data as the A operand
-// and the sign matrix as the B operand (the transposed product of the decode's wht128_lds, with
-// the same operand registers and the same sums), so their output holds, in lane (j, g), rows
-// 4g .. 4g+3 of one rotated column: K along the registers, the layout of the product with gm
-// (gm's rows transposed by an identity MFMA as in k_dequant_gemm_t), with no transpose of x_hat.
-// The rotation is the Sylvester-ordered Hadamard matrix, H[o][i] = (-1)^popcount(o & i), so
-// feeding the 32 values of a lane in another column order permutes the bits of the column
-// index and the rotated columns come out permuted the same way: rot_col gives the column of
-// output tile q in lane j for each unit width.  With two planes and large accumulators a wave
-// takes one plane (PPW = 1; waves w and w + 1 read the same code bytes).  The waves of a plane
-// are summed through LDS in wave order and leave as 16-byte rows.
-template <int G>
-__device__ __forceinline__ int rot_col(int j, int q) {
-  static_assert(G == 64 || G == 128, "64- or 128-column units");
-  // G = 128: the lane's columns 32g + 8c + e are the nominal order; G = 64: the lane holds
-  // columns 16g .. +15 of each of the two units, so nominal index bits (4; 5, 6) are column bits
-  // (6; 4, 5)
-  if constexpr (G == 128) return (j & 3) + 4 * q + 32 * (j >> 2);
-  else return (j & 3) + 4 * (q & 3) + 16 * (j >> 2) + 64 * (q >> 2);
-}
+// row j at 32 columns (the units' G/4-column quarters, as in the decode), gathered by
+// rot_gather_128 into the data operand of the rotation.  The rotation's MFMAs run with the data
+// as the A operand and the sign matrix as the B operand: the transposed product of the
+// decode's wht128_lds, with the same operand registers and the same sums, so x_hat is the
+// decode's bit for bit.  Their output holds, in lane (j, g), rows 4g .. 4g+3 of one rotated
+// column: K along the registers, the layout of the product with gm (gm's rows transposed by an
+// identity MFMA as in k_dequant_gemm_t), with no transpose of x_hat.  rot_col gives the column
+// of output tile q in lane j (the row index of wht128_lds's output tile).  With two planes and
+// large accumulators a wave takes one plane (PPW = 1; waves w and w + 1 read the same code
+// bytes).  The waves of a plane are summed through LDS in wave order and leave as 16-byte rows.
+__device__ __forceinline__ int rot_col(int j, int q) { return (j & 3) + 4 * q + 32 * (j >> 2); }
 
 template <int BITS, int G, int R, int KT, int NW, int PPW, int PD, int NBM>
 __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t_rot(
@@ -1337,7 +1551,7 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t_rot(
 #pragma unroll
   for (int q0 = 0; q0 < 2; ++q0)
 #pragma unroll
-    for (int n = 0; n < 2; ++n) wop[q0][n] = wht_base_operand(j, g, q0, n != 0);
+    for (int n = 0; n < 2; ++n) wop[q0][n] = wht_base_operand(j, rot_sign_group<G>(g), q0, n != 0);
 
   // reconstruction operands of the wave's planes (the same for every block)
   u32x2 vop[PPW][U][G / 16][RT];
@@ -1411,8 +1625,7 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t_rot(
 #pragma unroll
       for (int ul = 0; ul < U; ++ul) reconstruct_plane<BITS, G, R>(cur.cb[ul], cur.qp[ul][pi], p, vop[pi][ul], cur.lop, xh + E * ul);
       u32x4 xv[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) xv[c] = pack8(xh + 8 * c);  // bf16(Y')
+      rot_gather_128<G>(xh, xv);
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
         f32x4 y = zero4();
@@ -1472,7 +1685,7 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_t_rot(
       }
       const int a = c0 + c, kt = a % KT, q = (a / KT) % 8, p = eg * PPW + a / (8 * KT);
       const int jj = ln & 15, gg = ln >> 4;
-      const int n = p * (N / NP) + u0 * G + rot_col<G>(jj, q);
+      const int n = p * (N / NP) + u0 * G + rot_col(jj, q);
       st16(partg + (int64_t)n * KO + 16 * kt + 4 * gg,
            u32x4{__float_as_uint(s[0]), __float_as_uint(s[1]), __float_as_uint(s[2]), __float_as_uint(s[3])});
     }
@@ -1620,6 +1833,48 @@ static int softmax_2s_launch(const lrq_tensors* t, const void* dp, int64_t lddp,
     if (units >= NW && units <= (int64_t)NW * HOLD) return go(k_softmax_2s<BITS, G, R, NW, HOLD>, Sm::LDS);
   }
   return go(k_softmax_2s<BITS, G, R, NW, 0>, 0);
+}
+
+// Rotated format (planes of whole rotation blocks, no outlier channels): the rotated two-sweep
+// kernel, about four workgroups per CU.
+template <int BITS, int G, int R>
+static int softmax_rot_launch(const lrq_tensors* t, const void* dp, int64_t lddp, void* ds, int64_t ldds,
+                              hipStream_t s) {
+  constexpr int NW = 8;
+  // items held in registers per wave: two (rank 32: none)
+  constexpr int HOLD = R > 16 ? 0 : 2;
+  const int M = (int)t->rows, N = (int)t->hidden;
+  const int64_t items = t->hidden / ((8 / BITS) * 128);
+  const int nrb = (M + 15) / 16;
+  const int wgs = std::max(1, std::min(nrb, cu_count() * 4));
+  const int rbw = (nrb + wgs - 1) / wgs;
+  auto go = [&](auto kern, size_t shm) {
+    if (shm > 64 * 1024) {
+      const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+      if (e != hipSuccess) return (int)e;
+    }
+    return launch(kern, dim3((nrb + rbw - 1) / rbw), dim3(NW * 64), shm, s, (const uint8_t*)t->codes, t->ld_codes,
+                  (const uint16_t*)t->qparams, t->ld_qp, (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N,
+                  (const uint16_t*)dp, lddp, (uint16_t*)ds, ldds, rbw);
+  };
+  if constexpr (HOLD > 0) {
+    // one workgroup per CU (the parked V operands and the held inputs allow no second), each
+    // walking its row blocks with the next block's inputs in flight
+    if (items >= NW && items <= (int64_t)NW * HOLD) {
+      const int pw = std::max(1, std::min(nrb, cu_count()));
+      const int prbw = (nrb + pw - 1) / pw;
+      const size_t shm = SmxRot<BITS, G, R, NW, HOLD>::LDS;
+      auto kern = k_softmax_rot<BITS, G, R, NW, HOLD>;
+      if (shm > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+        if (e != hipSuccess) return (int)e;
+      }
+      return launch(kern, dim3((nrb + prbw - 1) / prbw), dim3(NW * 64), shm, s, (const uint8_t*)t->codes,
+                    t->ld_codes, (const uint16_t*)t->qparams, t->ld_qp, (const uint16_t*)t->L, t->ld_L,
+                    (const uint16_t*)t->V, M, N, (const uint16_t*)dp, lddp, (uint16_t*)ds, ldds, prbw);
+    }
+  }
+  return go(k_softmax_rot<BITS, G, R, NW, 0>, 0);
 }
 
 // One pass needs the whole row in one workgroup: 4, 8 or 16 units (one per wave).  Rows of
@@ -1890,15 +2145,19 @@ extern "C" int lrq_softmax_bwd(const lrq_tensors* t, const void* dp, int64_t ldd
   st = validate_rows16(ds, ldds, t->hidden);
   if (st) return st;
   if (t->rows == 0) return LRQ_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if ((t->flags & LRQ_FLAG_HADAMARD) && t->n_outlier == 0 && (t->hidden / (8 / t->bits)) % 128 == 0) {
+    LRQ_FORMATS(softmax_rot_launch, t, dp, lddp, ds, ldds, s)
+  }
   if ((t->flags & LRQ_FLAG_HADAMARD) || t->n_outlier > 0) {
-    // the rotated format and outlier channels: decode into ds (rotation undone, side columns
-    // substituted), then the dense backward in place over it; rows of exactly `hidden` elements,
-    // and ds distinct from dp (the decode would overwrite dp before the backward reads it)
+    // outlier channels, and the rotated format with planes that are not whole rotation blocks:
+    // decode into ds (rotation undone, side columns substituted), then the dense backward in
+    // place over it; rows of exactly `hidden` elements, and ds distinct from dp (the decode
+    // would overwrite dp before the backward reads it)
     if (lddp != t->hidden || ldds != t->hidden || dp == ds) return LRQ_ERR_UNSUPPORTED;
     LRQ_TRY(lrq_decode(t, ds, ldds, stream));
     return lrq_dense_softmax_bwd(ds, dp, ds, t->rows, t->hidden, stream);
   }
-  hipStream_t s = (hipStream_t)stream;
   LRQ_FORMATS(softmax_units, t, dp, lddp, ds, ldds, s)
 }
 

@@ -107,6 +107,55 @@ __device__ __forceinline__ void wht128_lds(unsigned char* base, const u32x4 (&op
   wht128_lds_map(base, op, [](int, const float* y) { return pack8(y); });
 }
 
+// The rotation of one 16 x 128 block held in registers, for kernels whose lanes rebuild a
+// block's columns themselves.  The decode's wht128_lds gives lane group g the block's columns
+// 32g .. 32g+31 (chunk c = columns 32g + 8c .. +7, so MFMA step c sums the 32 columns
+// {32g' + 8c + e}); a lane of the G/4-column reconstruction layout holds columns E g .. of each
+// of the block's 128/G units instead.  rot_gather_128 packs the lane's 32 values of row j to bf16
+// in the order of wht128_lds: for G = 128 they already are columns 32g + i; for G = 64 one
+// v_permlane16_swap per dword pair of the two units' quarters gives lane group g the columns
+// 32 sigma(g) .. +31, sigma(g) = (0, 2, 1, 3)[g], and the lane's sign operands are built for
+// group sigma(g) (rot_sign_group).  Each MFMA step then sums the same 32 products as the
+// decode's, so the rotated values are the decode's bit for bit.
+template <int G>
+__device__ __forceinline__ int rot_sign_group(int g) {
+  static_assert(G == 64 || G == 128, "64- or 128-column units");
+  return G == 128 ? g : ((g & 1) << 1) | (g >> 1);
+}
+template <int G>
+__device__ __forceinline__ void rot_gather_128(const float* xh, u32x4 (&xv)[4]) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) xv[c] = pack8(xh + 8 * c);  // bf16(Y')
+  if constexpr (G == 64) {
+    // xv[0..1]: unit 0, columns 16g .. +15; xv[2..3]: unit 1, columns 64 + 16g .. +15
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const auto s = __builtin_amdgcn_permlane16_swap(xv[c][d], xv[c + 2][d], false, false);
+        xv[c][d] = s[0];
+        xv[c + 2][d] = s[1];
+      }
+  }
+}
+// Rotate the gathered block: y[s] = fp32(sum) * fp32(1/sqrt(128)) of row j, column 32g + s of the
+// block (s < 32), before the bf16 rounding; op = the four wht_base_operand forms of
+// (j, rot_sign_group<G>(g)).
+__device__ __forceinline__ void wht128_regs(const u32x4 (&xv)[4], const u32x4 (&op)[2][2], float* y) {
+  const float kScale = 0.08838834764831845f;  // fp32(1/sqrt(128)), as in wht128_lds_at
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int flip = (((q >> 1) & c & 1) ^ ((q >> 2) & (c >> 1) & 1));
+      acc = mfma_16x16x32(op[q & 1][flip], xv[c], acc);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) y[4 * q + v] = acc[v] * kScale;
+  }
+}
+
 // wht128_lds on a row of a swizzled tile: the row's 16-byte chunk c (columns 8c .. 8c+7 of the
 // 128) sits at row + 16 * (c ^ sw), sw < 16; the lane's chunks are 4g .. 4g+3.
 __device__ __forceinline__ void wht128_lds_swz(unsigned char* row, int g, int sw, const u32x4 (&op)[2][2]) {
