@@ -7,7 +7,8 @@ rotate over several HBM-resident buffer sets (> 512 MB of X) so the 256 MB MALL 
 serve them.  Prints ONE JSON line (driver contract).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
-                  [--config north_star|c1|c2|c3|c4|c5|c5w|lora|legacy|ref_enc|ref_dec|ref_mm|offload|copy] [--m M]
+                  [--config north_star|c1|c2|c3|c4|c4l|c4s|c5|c5w|lora|legacy|ref_enc|ref_dec|ref_mm|offload|copy]
+                  [--m M]
                   [--no-cpu-baseline]
 
 value       = activation GB/s = 2*rows*hidden bytes / (encode + decode time per step);
@@ -455,19 +456,22 @@ def build_plan(cfg, pkg, lib, dev, nbuf, lora_split=False):
                                                                   P(lw), lw.numel() * 4, sp),
                             base + 2 * N * n + 4 * M * n + 4 * N * n, 2 * M * N * r + 4 * M * N * n))
             return entries, 2 * M * N, ["lora_grads"], sets
+        rot = 2 * M * N * 128 if cfg.hadamard else 0  # the rotation's MFMA flops, once per kernel
         entries.append(("xa", lambda k: lib.lrq_dequant_gemm(B(sets[k]["dec"]), P(sets[k]["a"]), n,
                                                              P(sets[k]["xa"]), n, 0, sp),
-                        base + 2 * N * n + 2 * M * n, 2 * M * N * r + 2 * M * N * n))
+                        base + 2 * N * n + 2 * M * n, 2 * M * N * r + 2 * M * N * n + rot))
         entries.append(("da", lambda k: lib.lrq_dequant_gemm_t(B(sets[k]["dec"]), P(sets[k]["g"]), n, n,
                                                                P(sets[k]["da"]), n, 1, P(sets[k]["ws"]),
                                                                sets[k]["ws"].numel() * 4, sp),
-                        base + 2 * M * n + 4 * N * n, 2 * M * N * r + 2 * M * N * n))
+                        base + 2 * M * n + 4 * N * n, 2 * M * N * r + 2 * M * N * n + rot))
         timed = ["xa", "da"]  # value over both gradient kernels (the encode is the producer)
     else:
         fn = {"silu": lib.lrq_silu_bwd, "gelu": lib.lrq_gelu_bwd, "softmax": lib.lrq_softmax_bwd}[cfg.consumer]
         name = f"{cfg.consumer}_bwd"
+        # (the rotated softmax rotates each block twice, once per sweep)
+        rot = (2 if cfg.consumer == "softmax" else 1) * 2 * M * N * 128 if cfg.hadamard else 0
         entries.append((name, lambda k: fn(B(sets[k]["dec"]), P(sets[k]["dy"]), N, P(sets[k]["out"]), N, sp),
-                        consumer_bytes(M, N, r, cfg.bits, cfg.group, side), 2 * M * N * r))
+                        consumer_bytes(M, N, r, cfg.bits, cfg.group, side), 2 * M * N * r + rot))
         timed = [name]  # value over the fused consumer (the encode is the producer)
     return entries, 2 * M * N, timed, sets
 

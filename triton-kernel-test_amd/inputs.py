@@ -14,6 +14,8 @@ Recipes (BASELINE.json "configs"):
   c4               X[16384, 5120] ~ N(0,1), 16 channels x30; WHT-128 rotation; V[5120, 16]; int4/g64
   c5               P = softmax(N(0,1)/sqrt(128)) over [2, 32, 2048, 2048] (rows of 2048);
                    V[2048, 16]; int4/g64 per row; dP = 0.02 N(0,1)                       (softmax bwd)
+Further workloads of the same recipes (lora, c4l, c4s, c5w, legacy, ref_*) are described at
+their CONFIGS entries.
 """
 
 from __future__ import annotations
@@ -62,6 +64,12 @@ CONFIGS = {
     "c5w": Config("c5w", 4 * 4096, 4096, 16, 4, 64, consumer="softmax", seed=8, softmax_shape=(2, 32, 4096, 4096)),
     # the LoRA layer's backward from the north-star format: x A and dA = x^T (dy B^T)
     "lora": Config("lora", 16384, 4096, 16, 4, 64, n_outlier=8, outlier_scale=20.0, consumer="lora", seed=6),
+    # the rotated format's consumers that reduce over the hidden dimension: the two LoRA products
+    # (x A and dA = x^T g, the rotation inside each) and the softmax backward, at 4096 columns
+    "c4l": Config("c4l", 16384, 4096, 16, 4, 64, n_outlier=8, outlier_scale=20.0, hadamard=True, consumer="lora",
+                  seed=12),
+    "c4s": Config("c4s", 16384, 4096, 16, 4, 64, hadamard=True, consumer="softmax", seed=13,
+                  softmax_shape=(1, 4, 4096, 4096)),
     # the reference's own format (legacy): rank-16 factors, 2-bit symmetric codes (the system
     # profile's quantize_bit=2), outliers above the 99th percentile kept as COO
     "legacy": Config("legacy", 16384, 4096, 16, 2, 0, n_outlier=8, outlier_scale=20.0, consumer="legacy", seed=7),
