@@ -208,8 +208,9 @@ def test_rotated_consumer_in_place(pkg, dev, rows, n, rank, bits, group, fused):
 ])
 def test_rotated_dequant_gemm(pkg, dev, rows, n, rank, n_out, out_dtype, bits, group):
     """x_hat @ A on the rotated format, fused: against the float64 product on the device's rotated
-    decode (the kernel rotates with the decode's routine, so the x_hat is the same) within the
-    fp32 accumulation bound, and against the oracle's rotated decode within the floating-point bar."""
+    decode (the kernel's in-register rotation sums what the decode's does, so the x_hat is the
+    same) within the fp32 accumulation bound, and against the oracle's rotated decode within the
+    floating-point bar."""
     print(f"[rot gemm] rows={rows} n={n} rank={rank} n_out={n_out} {out_dtype} int{bits}/g{group}", flush=True)
     x = pkg.inputs.activation(rows, n, 8, 20.0, seed=n + n_out)
     V = pkg.inputs.basis(n, rank, seed=5) if rank else None
@@ -239,6 +240,28 @@ def test_rotated_dequant_gemm(pkg, dev, rows, n, rank, n_out, out_dtype, bits, g
         assert rel <= 1e-3, rel
     else:
         assert_fp_close(bits16(out), ref_o, "rotated dequant gemm bf16 vs the oracle")
+
+
+@pytest.mark.parametrize("bits,group,rank,n_out", [
+    (4, 64, 16, 16), (4, 64, 32, 32), (8, 128, 16, 16), (4, 128, 0, 32), (8, 64, 0, 16)])
+def test_rotated_dequant_gemm_reads_the_decoded_x_hat(pkg, dev, bits, group, rank, n_out):
+    """With A one-hot (column k selects input column c_k), x_hat A is column k = x_hat[:, c_k]
+    exactly (one product by 1, the rest exact zeros), so the in-register rotation's x_hat is
+    compared bit for bit with the rotated decode's, n_out columns spread over planes and blocks."""
+    print(f"[rot gemm x_hat] int{bits}/g{group} rank={rank} n={n_out}", flush=True)
+    rows, n = 70, 2048
+    x = pkg.inputs.activation(rows, n, 8, 20.0, seed=bits + group + rank)
+    V = pkg.inputs.basis(n, rank, seed=8) if rank else None
+    c = pkg.encode(x.to(dev), V.to(dev) if V is not None else None, bits=bits, group_size=group, hadamard=True)
+    sel = np.sort(np.random.default_rng(n_out + bits).choice(n, n_out, replace=False))
+    a = torch.zeros(n, n_out, dtype=torch.bfloat16)
+    a[torch.as_tensor(sel), torch.arange(n_out)] = 1.0
+    out = pkg.dequant_gemm(c, a.to(dev), out_dtype=torch.float32)
+    xh = pkg.decode(c)
+    torch.cuda.synchronize()
+    want = O.bf16_to_f32(bits16(xh))[:, sel].astype(np.float32)
+    got = out.cpu().numpy().reshape(rows, n_out)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), int((got != want).sum())
 
 
 def test_rotated_dequant_gemm_straddling_planes(pkg, dev):

@@ -10,6 +10,8 @@
 //   k_dequant_gemm_t out = bf16(decode(c))^T @ G, G [M, n] bf16: the LoRA factor gradient
 //                   x^T (dy B^T) (low_rank_system_profile_forward.py:14-18), a reduction over
 //                   rows into per-row-group partials, then k_sum_parts.
+//   k_softmax_rot, k_dequant_gemm_rotr, k_dequant_gemm_t_rot: the same on the rotated format,
+//                   each rotating the 128-column blocks it rebuilds in registers (lrq_whtop.h).
 #include "lrq_common.h"
 #include "lrq_dequant.h"
 #include "lrq_host.h"
@@ -941,43 +943,38 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm(
   }
 }
 
-// Dequant-GEMM on the rotated format: x_hat = bf16(WHT128(bf16(Y'))) blockwise, the rotated
-// decode's result, times A.  Wave w takes unit s*NW + w at step s; per step and row block the
-// waves write bf16(Y') of their units into an LDS tile laid out as the rotated decode's output
-// tile (16 rows x NP planes x NW*G columns), rotate its 128-column blocks in place with the
-// decode's own routine (wht128_lds: the same bf16 x_hat, bit for bit), read their units back in
-// the B-operand layout and project as k_dequant_gemm does.  Planes must be whole rotation blocks
-// (plane % 128 == 0), so every block of a step is complete.  OUTL: the side columns replace
-// x_hat's outlier columns after the rotation, so, as in k_dequant_gemm, A's rows of those
-// columns are zeroed and the side term is added at the end.
+// Dequant-GEMM on the rotated format with the rotation in registers (no LDS tile, no barrier
+// until the final reduction).  Wave w takes the pairs (item, plane) w, w + NW, ... of the row,
+// an item being one 128-column rotation block (128/G units); per pair it walks the workgroup's
+// RBW row blocks, rebuilding row j's 32 columns of the block, gathering them (rot_gather_128)
+// and rotating them (wht128_regs), so x_hat is the decode's bit for bit and lane group g holds
+// block columns 32g .. 32g+31 as four 8-column chunks.  Chunk c is the B operand of a 16x16x32
+// step whose A operand holds A[column 32g + 8c + e][16t + i] in lane (i, g) (gathered once per
+// pair; zero for outlier columns, whose side term is added at the end as in k_dequant_gemm),
+// so the accumulator holds out[row j][16t + 4g + v] as in k_dequant_gemm.  The next row block's
+// codes and qparams are requested before the current one is computed.  The waves' partial tiles
+// are summed through LDS in wave order.  Planes of whole rotation blocks ((N / NP) % 128 == 0).
 template <int BITS, int G, int R, int NOUT, int NW, int RBW, bool OUT_F32, bool OUTL>
-__global__ __launch_bounds__(NW * 64) void k_dequant_gemm_rot(
+__global__ __launch_bounds__(NW * 64) void k_dequant_gemm_rotr(
     const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ qparams, int64_t ldq,
     const uint16_t* __restrict__ Lin, int64_t ldl, const uint16_t* __restrict__ V, int M, int N,
     const uint16_t* __restrict__ A, void* __restrict__ out, int64_t ldo, const int32_t* __restrict__ oidx, int nout,
     const uint16_t* __restrict__ side, int64_t ldside) {
-  constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, TO = NOUT / 16, E = G / 4;
-  constexpr int SEG = NW * G;           // columns of one plane per step
-  constexpr int OPAD = SEG * 2 + 16;    // LDS row pitch in bytes (spreads the 16 rows over banks)
-  constexpr int TILE = 16 * NP * OPAD;  // one row block's tile
-  constexpr int RB = SEG / 128;         // rotation blocks per plane and step
-  static_assert(SEG % 128 == 0 && OPAD % 16 == 0, "whole rotation blocks, 16-byte rows");
+  constexpr int NP = 8 / BITS, RT = R > 0 ? R / 16 : 1, TO = NOUT / 16, E = G / 4, U = 128 / G;
   __shared__ f32x4 part[NW][TO][64];
-  extern __shared__ __attribute__((aligned(16))) unsigned char tile[];  // [RBW][TILE], OUTL: + N/32 words
-  uint32_t* gmask = reinterpret_cast<uint32_t*>(tile + RBW * TILE);
+  extern __shared__ uint32_t gmask[];  // OUTL: N/32 words
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
   const int nrb = (M + 15) / 16;
   const int rb0 = blockIdx.x * RBW;
-  const int units = N / (G * NP);
-  const int steps = (units + NW - 1) / NW;
-  const u32x2 ident = identity_bop(j, g);
+  const int PW = N / NP;
+  const int pairs = (N / (NP * 128)) * NP;
   if constexpr (OUTL) build_colmask(gmask, N, oidx, nout);
   u32x4 wop[2][2];
 #pragma unroll
   for (int q0 = 0; q0 < 2; ++q0)
 #pragma unroll
-    for (int n = 0; n < 2; ++n) wop[q0][n] = wht_base_operand(j, g, q0, n != 0);
+    for (int n = 0; n < 2; ++n) wop[q0][n] = wht_base_operand(j, rot_sign_group<G>(g), q0, n != 0);
 
   f32x4 acc[RBW][TO];
 #pragma unroll
@@ -993,83 +990,99 @@ __global__ __launch_bounds__(NW * 64) void k_dequant_gemm_rot(
       for (int t = 0; t < RT; ++t) lop[b][t] = ld8(Lin + row * ldl + 16 * t + 4 * g);
     }
   }
-  struct UIn {
-    u32x2 vop[NP][G / 16][RT];
-    u32x2 va[NP][G / 16][TO];
-    u32x4 cb[RBW][G / 64];
-    uint32_t qp[RBW][NP];
+  struct Blk {
+    u32x4 cb[U][G / 64];
+    uint32_t qp[U];
   };
-  auto load_unit = [&](int u, UIn& d) {
+  // (item it, plane p) of row block b: the U units' code bytes of row j and plane p's (scale, zero)
+  auto load = [&](int it, int p, int b, Blk& d) __attribute__((always_inline)) {
+    const int64_t row = min(min(rb0 + b, nrb - 1) * 16 + j, M - 1);
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      if constexpr (R > 0) load_vops<G, R>(V, unit_base(p, u, N, NP, G), j, g, d.vop[p]);
-      load_vops<G, NOUT>(A, unit_base(p, u, N, NP, G), j, g, d.va[p]);
-      if constexpr (OUTL) mask_rows<G, TO>(d.va[p], gmask, unit_base(p, u, N, NP, G), j);
-    }
+    for (int ul = 0; ul < U; ++ul) {
+      const int u = it * U + ul;
 #pragma unroll
-    for (int b = 0; b < RBW; ++b) {
-      const int64_t row = min(min(rb0 + b, nrb - 1) * 16 + j, M - 1);
-#pragma unroll
-      for (int i = 0; i < G / 64; ++i) d.cb[b][i] = ld16_stream(codes + row * ldc + u * G + E * g + 16 * i);
-      if constexpr (NP == 2) {
-        const u32x2 q = ld8(qparams + row * ldq + u * 4);
-        d.qp[b][0] = q[0];
-        d.qp[b][1] = q[1];
-      } else {
-        d.qp[b][0] = ld4(qparams + row * ldq + u * 2);
-      }
+      for (int i = 0; i < G / 64; ++i) d.cb[ul][i] = ld16_stream(codes + row * ldc + u * G + E * g + 16 * i);
+      d.qp[ul] = ld4(qparams + row * ldq + (u * NP + p) * 2);
     }
   };
-  // the next step's inputs are loaded while this one is computed, except where a unit's
-  // registers are large (256-column units with n = 32 and rank > 0): then after its last read
-  constexpr bool PF = !(G * NP >= 256 && NOUT == 32 && R > 0);
-  UIn cur, nxt;
-  load_unit(min(w, units - 1), cur);
-  for (int s = 0; s < steps; ++s) {
-    const int u = s * NW + w;
-    const bool live = u < units;            // wave-uniform
-    const int ncols = min(NW, units - s * NW) * G;  // columns of each plane present in this step
-    if (PF && s + 1 < steps) load_unit(min(u + NW, units - 1), nxt);
-    if (live) {
+  // the pair's operands: V of the U units (reconstruction) and the gathered A chunks
+  struct Ops {
+    u32x2 vop[U][G / 16][RT];
+    u32x4 ach[4][TO];
+  };
+  auto load_ops = [&](int pi, Ops& o) __attribute__((always_inline)) {
+    const int it = pi / NP, p = pi % NP;
+    if constexpr (R > 0) {
 #pragma unroll
-      for (int b = 0; b < RBW; ++b)
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-          float xh[E];
-          reconstruct_plane<BITS, G, R>(cur.cb[b], cur.qp[b][p], p, cur.vop[p], lop[b], xh);
-#pragma unroll
-          for (int k = 0; k < E / 8; ++k)
-            *reinterpret_cast<u32x4*>(tile + b * TILE + (p * 16 + j) * OPAD + (w * G + E * g + 8 * k) * 2) =
-                pack8(xh + 8 * k);
-        }
+      for (int ul = 0; ul < U; ++ul) load_vops<G, R>(V, unit_base(p, it * U + ul, N, NP, G), j, g, o.vop[ul]);
     }
-    __syncthreads();
-    for (int k = w; k < NP * RB; k += NW) {  // wave-uniform
-      const int p = k / RB, q = k % RB;
-      if ((q + 1) * 128 <= ncols) {
+    const int c0 = p * PW + it * 128 + 32 * g;
 #pragma unroll
-        for (int b = 0; b < RBW; ++b) wht128_lds(tile + b * TILE + (p * 16 + j) * OPAD + (128 * q + 32 * g) * 2, wop);
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int t = 0; t < TO; ++t) {
+        uint32_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int col = c0 + 8 * c + e;
+          uint32_t v = A[(int64_t)col * NOUT + 16 * t + j];
+          if constexpr (OUTL) v = ((gmask[col >> 5] >> (col & 31)) & 1u) ? 0u : v;
+          h[e] = v;
+        }
+        o.ach[c][t] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
       }
+  };
+  static_assert(RBW % 2 == 0, "block b of every pair in ring slot b % 2");
+  // PF: the next pair's operands and first block are requested during the current pair's last
+  // block (a second operand set; at rank 32 it would not fit beside the rest)
+  constexpr bool PF = R <= 16;
+  const int np_mine = w < pairs ? (pairs - w + NW - 1) / NW : 0;
+  Ops ops[PF ? 2 : 1];
+  Blk ring[2];
+  auto pair = [&](auto par_tag, int k) __attribute__((always_inline)) {
+    constexpr int par = decltype(par_tag)::value;
+    Ops& o = ops[PF ? par : 0];
+    const int pi = w + k * NW, it = pi / NP, p = pi % NP;
+    const bool more = k + 1 < np_mine;  // wave-uniform
+    if constexpr (!PF) {
+      load_ops(pi, o);
+      load(it, p, 0, ring[0]);
     }
-    __syncthreads();
-    if (live) {
-#pragma unroll
-      for (int b = 0; b < RBW; ++b)
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-          u32x4 xb[G / 32];
-#pragma unroll
-          for (int k = 0; k < G / 32; ++k)
-            xb[k] = *reinterpret_cast<const u32x4*>(tile + b * TILE + (p * 16 + j) * OPAD + (w * G + E * g + 8 * k) * 2);
-          project_unit<G, NOUT>(cur.va[p], xb, ident, acc[b]);
+    static_for<0, RBW>([&](auto bc) {
+      constexpr int b = decltype(bc)::value;
+      if constexpr (b + 1 < RBW) {
+        load(it, p, b + 1, ring[(b + 1) & 1]);
+      } else if constexpr (PF) {
+        if (more) {
+          const int pn = pi + NW;
+          load_ops(pn, ops[par ^ 1]);
+          load(pn / NP, pn % NP, 0, ring[0]);
         }
-    }
-    __syncthreads();  // the tiles are rewritten by the next step
-    if constexpr (PF) {
-      cur = nxt;
-    } else {
-      if (s + 1 < steps) load_unit(min(u + NW, units - 1), cur);
-    }
+      }
+      const Blk& cur = ring[b & 1];
+      float xh[32];
+#pragma unroll
+      for (int ul = 0; ul < U; ++ul) reconstruct_plane<BITS, G, R>(cur.cb[ul], cur.qp[ul], p, o.vop[ul], lop[b], xh + E * ul);
+      u32x4 xv[4];
+      rot_gather_128<G>(xh, xv);
+      float y[32];
+      wht128_regs(xv, wop, y);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const u32x4 xc = pack8(y + 8 * c);  // x_hat of row j, block columns 32g + 8c .. +7
+#pragma unroll
+        for (int t = 0; t < TO; ++t) acc[b][t] = mfma_16x16x32(o.ach[c][t], xc, acc[b][t]);
+      }
+    });
+  };
+  if (PF && np_mine > 0) {
+    load_ops(w, ops[0]);
+    load(w / NP, w % NP, 0, ring[0]);
+  }
+#pragma unroll 1
+  for (int k = 0; k < np_mine; k += 2) {
+    pair(std::integral_constant<int, 0>{}, k);
+    if (k + 1 < np_mine) pair(std::integral_constant<int, 1>{}, k + 1);
   }
   if constexpr (OUTL) {
     if (w == 0) add_side_term<TO, RBW>(A, NOUT, N, oidx, nout, side, ldside, rb0, nrb, M, j, g, &acc[0][0]);
@@ -1940,24 +1953,19 @@ static int gemm_launch(const lrq_tensors* t, const void* a, void* out, int64_t l
   return LRQ_OK;
 }
 
-// Rotated format (no outlier channels; planes of whole rotation blocks).  Row blocks per
-// workgroup: as many as fit in about 64 KB of tiles (one to four).
+// Rotated format, rotation in registers (k_dequant_gemm_rotr): four row blocks per workgroup
+// (two at rank 32, whose V operands would otherwise spill).
 template <int BITS, int G, int R, int NOUT, bool F32, bool OUTL>
-static int gemm_rot_launch(const lrq_tensors* t, const void* a, void* out, int64_t ldo, hipStream_t s) {
-  constexpr int NP = 8 / BITS, NW = 8;
-  constexpr int TILE = 16 * NP * (NW * G * 2 + 16);
-  constexpr int RBW = 4 * TILE <= 68 * 1024 ? 4 : 2 * TILE <= 68 * 1024 ? 2 : 1;
+static int gemm_rotr_launch(const lrq_tensors* t, const void* a, void* out, int64_t ldo, hipStream_t s) {
+  constexpr int NP = 8 / BITS, NW = 8, RBW = R == 32 ? 2 : 4;
   if ((t->hidden / NP) % 128 != 0) return LRQ_ERR_UNSUPPORTED;
   const int M = (int)t->rows, N = (int)t->hidden;
   const int nrb = (M + 15) / 16;
-  const size_t shm = (size_t)RBW * TILE + (OUTL ? (size_t)(N / 32) * 4 : 0);
-  auto kern = k_dequant_gemm_rot<BITS, G, R, NOUT, NW, RBW, F32, OUTL>;
-  if (shm > 160 * 1024) return LRQ_ERR_UNSUPPORTED;
-  if (shm > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-  LRQ_TRY(launch(kern, dim3((nrb + RBW - 1) / RBW), dim3(NW * 64), shm, s, (const uint8_t*)t->codes, t->ld_codes,
-                 (const uint16_t*)t->qparams, t->ld_qp, (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N,
-                 (const uint16_t*)a, out, ldo, t->outlier_idx, (int)t->n_outlier, (const uint16_t*)t->side,
-                 t->ld_side));
+  const size_t shm = OUTL ? (size_t)(N / 32) * 4 : 0;
+  LRQ_TRY(launch((k_dequant_gemm_rotr<BITS, G, R, NOUT, NW, RBW, F32, OUTL>), dim3((nrb + RBW - 1) / RBW),
+                 dim3(NW * 64), shm, s, (const uint8_t*)t->codes, t->ld_codes, (const uint16_t*)t->qparams,
+                 t->ld_qp, (const uint16_t*)t->L, t->ld_L, (const uint16_t*)t->V, M, N, (const uint16_t*)a, out, ldo,
+                 t->outlier_idx, (int)t->n_outlier, (const uint16_t*)t->side, t->ld_side));
   return LRQ_OK;
 }
 
@@ -1966,14 +1974,14 @@ static int gemm_nout(const lrq_tensors* t, const void* a, int n_out, void* out, 
   const bool o = t->n_outlier > 0;
   if (t->flags & LRQ_FLAG_HADAMARD) {
     switch (n_out * 4 + (f32 ? 2 : 0) + (o ? 1 : 0)) {
-      case 16 * 4 + 2: return gemm_rot_launch<BITS, G, R, 16, true, false>(t, a, out, ldo, s);
-      case 16 * 4 + 3: return gemm_rot_launch<BITS, G, R, 16, true, true>(t, a, out, ldo, s);
-      case 16 * 4: return gemm_rot_launch<BITS, G, R, 16, false, false>(t, a, out, ldo, s);
-      case 16 * 4 + 1: return gemm_rot_launch<BITS, G, R, 16, false, true>(t, a, out, ldo, s);
-      case 32 * 4 + 2: return gemm_rot_launch<BITS, G, R, 32, true, false>(t, a, out, ldo, s);
-      case 32 * 4 + 3: return gemm_rot_launch<BITS, G, R, 32, true, true>(t, a, out, ldo, s);
-      case 32 * 4: return gemm_rot_launch<BITS, G, R, 32, false, false>(t, a, out, ldo, s);
-      case 32 * 4 + 1: return gemm_rot_launch<BITS, G, R, 32, false, true>(t, a, out, ldo, s);
+      case 16 * 4 + 2: return gemm_rotr_launch<BITS, G, R, 16, true, false>(t, a, out, ldo, s);
+      case 16 * 4 + 3: return gemm_rotr_launch<BITS, G, R, 16, true, true>(t, a, out, ldo, s);
+      case 16 * 4: return gemm_rotr_launch<BITS, G, R, 16, false, false>(t, a, out, ldo, s);
+      case 16 * 4 + 1: return gemm_rotr_launch<BITS, G, R, 16, false, true>(t, a, out, ldo, s);
+      case 32 * 4 + 2: return gemm_rotr_launch<BITS, G, R, 32, true, false>(t, a, out, ldo, s);
+      case 32 * 4 + 3: return gemm_rotr_launch<BITS, G, R, 32, true, true>(t, a, out, ldo, s);
+      case 32 * 4: return gemm_rotr_launch<BITS, G, R, 32, false, false>(t, a, out, ldo, s);
+      case 32 * 4 + 1: return gemm_rotr_launch<BITS, G, R, 32, false, true>(t, a, out, ldo, s);
       default: return LRQ_ERR_UNSUPPORTED;
     }
   }
