@@ -213,9 +213,25 @@ def consumer_bytes(rows, hidden, rank, bits, group, n_side=0):
     return b + 2 * rows * n_side
 
 
+def dense_pieces(ptr) -> int:
+    """64-column pieces with more entries than the legacy encode's staged record holds (2), from
+    the compacted piece pointers: the pieces whose dense values the encode writes."""
+    return int(((ptr[1:] - ptr[:-1]) > 2).sum().item())
+
+
+def staged_bytes(E, bits, npieces, nnz, ndense, small):
+    """Algorithmic bytes of lrq_legacy_encode_coo on its staged path: encode = x read, codes
+    written, each piece's 8-byte record written (and the 128 dense bytes of the pieces a record
+    cannot hold); compaction = those read once, the COO entries (3 int64 indices + bf16 value)
+    and the piece pointers written."""
+    handoff = npieces * 8 + ndense * 128
+    return E * (2 + bits / 8) + small + handoff, handoff + nnz * 26 + npieces * 8
+
+
 def build_plan_legacy(cfg, pkg, lib, dev, nbuf):
-    """The reference's own format: encode (codes + dense outliers), the GPU compaction of the
-    outliers to COO, and the decode reading the COO pieces; l / r rows sized for x[1, M, N]."""
+    """The reference's own format: encode (codes + each piece's staged outliers), the GPU
+    compaction of the outliers to COO, and the decode reading the COO pieces; l / r rows sized
+    for x[1, M, N]."""
     import torch
     c_void_p = ctypes.c_void_p
     sp = c_void_p(torch.cuda.current_stream(dev).cuda_stream)
@@ -238,8 +254,8 @@ def build_plan_legacy(cfg, pkg, lib, dev, nbuf):
                          out=torch.empty_like(x)))
     tau = float(pkg.outlier_threshold(l, r, sets[0]["x"]).item())  # 1 % outliers, as the reference calibrates
     P = lambda t: c_void_p(t.data_ptr())  # noqa: E731
-    # the encode and the outlier compaction in one call (the encode counts each piece's outliers,
-    # so the compaction reads the dense outliers once)
+    # the encode and the outlier compaction in one call (the encode stages each piece's count and
+    # first entries, so the compaction reads those instead of dense outliers)
     enc = lambda k: lib.lrq_legacy_encode_coo(P(l), P(rt), K, P(sets[k]["x"]), 1, M, N, M * N, N, P(s), 1,  # noqa: E731
                                               bits, tau, P(sets[k]["o"]), P(sets[k]["q"]), P(sets[k]["idx"]), cap,
                                               P(sets[k]["vals"]), cap, P(sets[k]["nnz"]), P(sets[k]["ptr"]),
@@ -255,17 +271,17 @@ def build_plan_legacy(cfg, pkg, lib, dev, nbuf):
     if nnz > cap:
         raise RuntimeError(f"{nnz} outliers exceed the bench capacity {cap}")
     small = 2 * (M * K + N * K) + 2 * N
-    # algorithmic: encode = x read, codes and the dense outliers written; compaction = the dense
-    # outliers read once, the COO and the piece pointers written
-    enc_b, cmp_b = M * N * (2 + bits / 8 + 2) + small, M * N * 2 + nnz * 26 + M * npc * 8
+    enc_b, cmp_b = staged_bytes(M * N, bits, M * npc, nnz, max(dense_pieces(st["ptr"]) for st in sets), small)
     entries = [
         ("encode_coo", enc, enc_b + cmp_b, 2 * M * N * K),
         ("decode", dec, M * N * (bits / 8 + 2) + nnz * 10 + M * npc * 8 + small, 2 * M * N * K),
     ]
     sets[0]["alg_split"] = {"encode": enc_b, "compact": cmp_b}
-    # the reference's sparse conversion of the same dense outliers, for comparison (it
-    # synchronises the host to size its output): mean over 20 calls
-    o0 = sets[0]["o"]
+    # the reference's sparse conversion of the same outliers, dense (lrq_legacy_encode), for
+    # comparison (it synchronises the host to size its output): mean over 20 calls
+    o0, q0 = torch.empty_like(sets[0]["x"]), torch.empty_like(sets[0]["q"])
+    if lib.lrq_legacy_encode(P(l), P(rt), K, P(sets[0]["x"]), 1, M, N, M * N, N, P(s), 1, bits, tau, P(o0), P(q0), sp):
+        raise RuntimeError("legacy encode failed")
     o0.to_sparse()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -280,7 +296,7 @@ def build_plan_legacy(cfg, pkg, lib, dev, nbuf):
 
 def build_plan_ref(cfg, pkg, lib, dev, nbuf):
     """The reference's own speed tests of its format, x [B, M, M] (see inputs.CONFIGS): ref_enc =
-    the 1-bit encode (codes + dense outliers) and the GPU compaction of the outliers to COO (the
+    the 1-bit encode (codes + staged outliers) and the GPU compaction of the outliers to COO (the
     reference's o.to_sparse(), without its host synchronisation); ref_dec = the 2-bit decode
     reading COO outliers o = N(0,1) * (o > 1) (built once by the same compaction, not timed)."""
     import torch
@@ -350,7 +366,7 @@ def build_plan_ref(cfg, pkg, lib, dev, nbuf):
         entries = [("legacy_gemm", mm, mm_b, 2 * E * K + 2 * E * MM_COLS)]
         timed = ["legacy_gemm"]
     elif cfg.consumer == "ref_enc":
-        enc_b, cmp_b = E * (2 + bits / 8 + 2) + small, E * 2 + nnz * 26 + B * M * npc * 8
+        enc_b, cmp_b = staged_bytes(E, bits, B * M * npc, nnz, max(dense_pieces(st["ptr"]) for st in sets), small)
         entries = [("encode_coo", enc, enc_b + cmp_b, 2 * E * K)]
         timed = ["encode_coo"]
         sets[0]["alg_split"] = {"encode": enc_b, "compact": cmp_b}

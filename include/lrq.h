@@ -240,12 +240,15 @@ int lrq_coo_compact(const void* o, int64_t B, int64_t M, int64_t N, int64_t* ind
 /* Workspace bytes of lrq_coo_compact (>= 0), or a negative LRQ_ERR_*.  Host only. */
 int64_t lrq_coo_workspace(int64_t B, int64_t M, int64_t N);
 
-/* lrq_legacy_encode followed by lrq_coo_compact of its outliers, with the compaction's count pass
- * done inside the encode (each 64-column piece's entries counted as they are quantised), so the
- * dense outliers o are read once, by the scatter: the reference's encode plus o.to_sparse()
- * (low_rank_extraction_fuse_compression_quantization.py:118-150), without its host
- * synchronisation.  Arguments as the two calls take them (o is still written: the scatter reads
- * it); shapes the encode's vectorised path does not take run the two calls. */
+/* lrq_legacy_encode followed by lrq_coo_compact of its outliers: the reference's encode plus
+ * o.to_sparse() (low_rank_extraction_fuse_compression_quantization.py:118-150), without its host
+ * synchronisation; codes q, indices, values, *nnz and piece_ptr as the two calls give them.  On the
+ * encode's vectorised path (bits * N % 512 == 0, 16-byte aligned operands, outlier >= 0) the encode
+ * stages each 64-column piece's count and first two entries in piece_ptr as it quantises, and
+ * writes a piece's dense values to o only when it has more entries than that; the compaction then
+ * reads the staged pieces and only those dense ones.  o [B, M, N] bf16 is therefore working memory:
+ * its contents on return are unspecified (the two calls' dense outliers come from
+ * lrq_legacy_encode).  Other shapes run the two calls. */
 int lrq_legacy_encode_coo(const void* l, const void* rt, int32_t K, const void* x, int64_t B, int64_t M,
                           int64_t N, int64_t ldx_b, int64_t ldx_m, const void* s, int64_t s_rows,
                           int32_t bits, float outlier, void* o, void* q, int64_t* indices, int64_t ld_idx,

@@ -337,19 +337,19 @@ def test_legacy_decode_coo_is_dense_decode(pkg, dev, B, M, N, K, bits, s_rows, t
 @pytest.mark.parametrize("B,M,N,K,bits,s_rows,tau", [CASES[0], CASES[1], CASES[2], CASES[5],
                                                     (2, 37, 512, 16, 1, 2, 1.5), (1, 80, 1024, 16, 2, 1, 0.5)])
 def test_legacy_encode_coo_is_encode_then_compact(pkg, dev, B, M, N, K, bits, s_rows, tau):
-    """lrq_legacy_encode_coo (the encode counting each piece's outliers, then offsets, chunk scan and
-    scatter) gives exactly what lrq_legacy_encode followed by lrq_coo_compact gives: codes, dense
-    outliers, COO indices and values, entry count and piece pointers (dense-ish outliers with a low
-    threshold included)."""
+    """lrq_legacy_encode_coo (the encode staging each piece's count and first entries, then chunk
+    totals, chunk scan and scatter) gives exactly what lrq_legacy_encode followed by
+    lrq_coo_compact gives: codes, COO indices and values, entry count and piece pointers (dense-ish
+    outliers with a low threshold included: pieces read from their dense values)."""
     print(f"[encode_coo] B={B} M={M} N={N} K={K} bits={bits} tau={tau}", flush=True)
     lib = importlib.import_module("triton-kernel-test_amd._lib").load()
     L = importlib.import_module("triton-kernel-test_amd.legacy")
     l, r, x, s = _inputs(4000 + N + bits, B, M, N, K, s_rows)
     ld, rd, xd, sd = l.to(dev), r.to(dev), x.to(dev), s.to(dev)
     cap = B * M * N
-    oc, q, o = L._encode_coo(ld, rd, xd, sd, bits, tau, cap)
+    oc, q = L._encode_coo(ld, rd, xd, sd, bits, tau, cap)
     # the two-call path on the same inputs
-    o2 = torch.empty_like(o)
+    o2 = torch.empty((B, M, N), dtype=torch.bfloat16, device=dev)
     q2 = torch.empty_like(q)
     l2, rt, KK = L._factors(ld, rd)
     s2 = L._scale(sd, B, N)
@@ -361,12 +361,90 @@ def test_legacy_encode_coo_is_encode_then_compact(pkg, dev, B, M, N, K, bits, s_
     torch.cuda.synchronize()
     n = int(oc.nnz.item())
     assert n == int(c2.nnz.item()) > 0
-    assert torch.equal(q, q2) and torch.equal(o, o2)
+    assert torch.equal(q, q2)
     assert torch.equal(oc.piece_ptr, c2.piece_ptr)
     assert torch.equal(oc.indices[:, :n], c2.indices[:, :n]) and torch.equal(oc.values[:n], c2.values[:n])
     # and the reference-named wrapper returns that sparse tensor
     o_sp, q3 = pkg.low_rank_addition_fuse_compression_quantization(ld, rd, xd, sd, quantize_bit=bits, outlier=tau)
-    assert torch.equal(q3, q) and torch.equal(o_sp.to_dense(), o.view(o_sp.shape))
+    assert torch.equal(q3, q) and torch.equal(o_sp.to_dense(), o2.view(o_sp.shape))
+
+
+def _planted(seed, B, M, N, K, counts, big=20.0):
+    """Legacy inputs whose outliers at tau = 8 are exactly planted entries: x = l @ r + small noise
+    (|residual| < 1), then +-big at a chosen number of random columns of each 64-column piece,
+    that number drawn from `counts`.  Returns l, r, x, s and the per-piece counts."""
+    g = torch.Generator().manual_seed(seed)
+    l = (torch.randn(M, K, generator=g) * 0.5).to(torch.bfloat16)
+    r = (torch.randn(K, N, generator=g) * 0.5).to(torch.bfloat16)
+    x = (l.float() @ r.float()).expand(B, M, N).clone() + 0.25 * torch.rand(B, M, N, generator=g)
+    npc = N // 64
+    pick = torch.randint(0, len(counts), (B, M, npc), generator=g)
+    n = torch.tensor(counts)[pick]
+    for idx in range(B * M * npc):
+        b, rest = divmod(idx, M * npc)
+        m, c = divmod(rest, npc)
+        k = int(n[b, m, c])
+        if k:
+            cols = 64 * c + torch.randperm(64, generator=g)[:k]
+            sign = torch.where(torch.rand(k, generator=g) < 0.5, -1.0, 1.0)
+            x[b, m, cols] = sign * (big + torch.rand(k, generator=g))
+    s = (0.05 + 0.35 * torch.rand(1, N, generator=g)).to(torch.bfloat16)
+    return l, r, x.to(torch.bfloat16), s, n
+
+
+# per-piece entry counts drawn from: many (a wave's entries exceed its LDS area of 512: written
+# where formed) or few (gathered in LDS, written coalesced); both mix pieces a record holds (0 .. 2)
+# with pieces read from their dense values
+_DENSE_COUNTS = (0, 0, 1, 1, 2, 2, 3, 4, 9, 64)
+_SPARSE_COUNTS = (0, 0, 0, 0, 0, 0, 1, 1, 2, 3)
+
+
+@pytest.mark.parametrize("B,M,N,bits,counts", [(2, 37, 1024, 1, _DENSE_COUNTS), (2, 70, 1024, 2, _DENSE_COUNTS),
+                                               (1, 100, 512, 4, _DENSE_COUNTS), (3, 20, 1024, 8, _DENSE_COUNTS),
+                                               (2, 37, 1024, 1, _SPARSE_COUNTS), (2, 70, 1024, 2, _SPARSE_COUNTS),
+                                               (1, 100, 512, 4, _SPARSE_COUNTS), (3, 20, 1024, 8, _SPARSE_COUNTS)])
+def test_legacy_encode_coo_staged_records(pkg, dev, B, M, N, bits, counts):
+    """The encode's staged records: pieces of 0, 1 and 2 entries (held by the record, entries in
+    any of the piece's four 16-column lane groups) and of more (read back from their dense values),
+    mixed across the waves, give the two-call path's COO exactly; and with fewer slots than entries
+    the first `cap` entries and the full count."""
+    print(f"[staged encode_coo] B={B} M={M} N={N} bits={bits} counts={counts}", flush=True)
+    lib = importlib.import_module("triton-kernel-test_amd._lib").load()
+    L = importlib.import_module("triton-kernel-test_amd.legacy")
+    l, r, x, s, n = _planted(7000 + N + bits + len(set(counts)), B, M, N, 16, counts)
+    tau = 8.0
+    # the planted counts are the outliers the oracle finds, and every kind of piece occurs
+    o_ref, _ = O.legacy_encode(bits16(l), bits16(r), bits16(x), bits16(s), bits, tau)
+    per_piece = ((o_ref.reshape(B, M, N // 64, 64) & 0x7FFF) != 0).sum(-1)
+    assert np.array_equal(per_piece, n.numpy())
+    for k in set(counts):
+        assert (per_piece == k).any(), k
+    # (a wave's 256 consecutive pieces: over 512 entries for the dense draw, at most 512 for the sparse)
+    waves = n.flatten()[: (n.numel() // 256) * 256].reshape(-1, 256).sum(-1)
+    assert (waves > 512).all() if counts == _DENSE_COUNTS else (waves <= 512).all()
+    ld, rd, xd, sd = l.to(dev), r.to(dev), x.to(dev), s.to(dev)
+    total = int(n.sum())
+    oc, q = L._encode_coo(ld, rd, xd, sd, bits, tau, total)
+    o2 = torch.empty((B, M, N), dtype=torch.bfloat16, device=dev)
+    q2 = torch.empty_like(q)
+    l2, rt, KK = L._factors(ld, rd)
+    s2 = L._scale(sd, B, N)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.lrq_legacy_encode(P(l2), P(rt), KK, P(xd), B, M, N, xd.stride(0), xd.stride(1), P(s2), s2.shape[0],
+                                 bits, tau, P(o2), P(q2), sp) == 0
+    c2 = pkg.compact_outliers(o2, capacity=total)
+    small, _ = L._encode_coo(ld, rd, xd, sd, bits, tau, total // 3)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits16(o2.cpu()), o_ref)
+    assert int(oc.nnz.item()) == int(c2.nnz.item()) == total
+    assert torch.equal(q, q2)
+    assert torch.equal(oc.piece_ptr, c2.piece_ptr)
+    assert torch.equal(oc.indices, c2.indices) and torch.equal(oc.values, c2.values)
+    k = total // 3
+    assert int(small.nnz.item()) == total
+    assert torch.equal(small.piece_ptr, c2.piece_ptr)
+    assert torch.equal(small.indices[:, :k], c2.indices[:, :k]) and torch.equal(small.values[:k], c2.values[:k])
 
 
 # the reference decode test's outliers (low_rank_kernel_decode_speed_test.py:38-40): o = N(0,1) *
@@ -442,3 +520,36 @@ def test_outlier_threshold_is_kthvalue(pkg, dev, M, N, K):
     assert got.item() == want, (got.item(), want)
     for k in (1, M * N // 3, M * N):
         assert pkg.residual_kthvalue(ld, rd, xd[0], k).item() == O.kth_smallest_abs(xr, k), k
+
+
+def test_legacy_encode_coo_many_chunks(pkg, dev):
+    """More than 4096 chunks of 4096 pieces (x [2, 135000, 4096], 17.3 M pieces): the staged
+    scatter takes its chunk offsets from the separate chunk scan instead of summing the totals
+    itself; the COO, count and piece pointers equal the two-call path's (generated on the GPU)."""
+    B, M, N, K, bits, tau = 2, 135000, 4096, 16, 2, 3.5
+    print(f"[staged encode_coo, many chunks] B={B} M={M} N={N}", flush=True)
+    assert B * M * (N // 64) > 4096 * 4096
+    lib = importlib.import_module("triton-kernel-test_amd._lib").load()
+    L = importlib.import_module("triton-kernel-test_amd.legacy")
+    g = torch.Generator(device=dev).manual_seed(91)
+    ld = (torch.randn(M, K, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    rd = (torch.randn(K, N, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    xd = torch.randn(B, M, N, generator=g, device=dev).to(torch.bfloat16)
+    sd = (0.05 + 0.35 * torch.rand(1, N, generator=g, device=dev)).to(torch.bfloat16)
+    cap = B * M * N // 32
+    oc, q = L._encode_coo(ld, rd, xd, sd, bits, tau, cap)
+    o2 = torch.empty((B, M, N), dtype=torch.bfloat16, device=dev)
+    q2 = torch.empty_like(q)
+    l2, rt, KK = L._factors(ld, rd)
+    s2 = L._scale(sd, B, N)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.lrq_legacy_encode(P(l2), P(rt), KK, P(xd), B, M, N, xd.stride(0), xd.stride(1), P(s2), s2.shape[0],
+                                 bits, tau, P(o2), P(q2), sp) == 0
+    c2 = pkg.compact_outliers(o2, capacity=cap)
+    torch.cuda.synchronize()
+    n = int(oc.nnz.item())
+    assert n == int(c2.nnz.item()) and 0 < n <= cap
+    assert torch.equal(q, q2)
+    assert torch.equal(oc.piece_ptr, c2.piece_ptr)
+    assert torch.equal(oc.indices[:, :n], c2.indices[:, :n]) and torch.equal(oc.values[:n], c2.values[:n])

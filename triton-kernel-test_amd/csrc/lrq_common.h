@@ -365,6 +365,21 @@ __device__ __forceinline__ float row_max4_pair(float va, float vb) {
   swap16(a, b);
   return max_nc(a, b);
 }
+// Exclusive prefix sum of `v` over the row's four lanes in lane-group order g = 0 .. 3 (lane
+// 16g + j), and the row's total.
+__device__ __forceinline__ void row_prefix4(uint32_t v, int g, uint32_t& pre, uint32_t& total) {
+  const auto h = __builtin_amdgcn_permlane16_swap(v, v, false, false);  // v of groups g & ~1, g | 1
+  const auto q = __builtin_amdgcn_permlane32_swap(h[0] + h[1], h[0] + h[1], false, false);
+  // q[0] = the sum over groups 0 and 1, q[1] = over groups 2 and 3
+  pre = ((g & 1) ? h[0] : 0u) + ((g & 2) ? q[0] : 0u);
+  total = q[0] + q[1];
+}
+// Bitwise or of `v` over the row's four lanes.
+__device__ __forceinline__ uint32_t row_or4(uint32_t v) {
+  const auto h = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  const auto q = __builtin_amdgcn_permlane32_swap(h[0] | h[1], h[0] | h[1], false, false);
+  return q[0] | q[1];
+}
 // Inverse of the pair scatter: `v` holds one value in lanes 0..31 and another in 32..63;
 // returns the first in lo and the second in hi, in every lane.
 __device__ __forceinline__ void halves_broadcast(float v, float& lo, float& hi) {

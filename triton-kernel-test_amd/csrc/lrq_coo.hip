@@ -20,6 +20,11 @@
 // (npc = ceil(N / 64) pieces per row; piece_ptr[rows * npc] = nnz): the legacy decode reads
 // the outliers of a 64-column piece from it without a dense tensor.  A value is an entry when
 // its bf16 bits are not +0 or -0 (what to_sparse keeps of a bf16 tensor).
+//
+// After the legacy encode, which stages each piece's count and first entries as a record in
+// piece_ptr (lrq_coo.h), the compaction is k_coo_totals (the chunk totals from the records) and
+// k_coo_scatter_staged (the chunk scan; the entries from the records, and from the dense values
+// only for pieces with more entries than a record holds).
 #include "lrq_common.h"
 #include "lrq_coo.h"
 #include "lrq_host.h"
@@ -30,6 +35,7 @@ constexpr int kPiece = 64;
 constexpr int kChunk = 4096;  // pieces per chunk
 constexpr int kCooThreads = 1024;
 constexpr int kStage = 8 * kPiece;  // entries one wave's 8 pieces can hold
+constexpr int kScanInline = 4096;   // chunks up to which the staged scatter sums the chunk totals itself
 
 // Exclusive prefix sum over the 1024 threads of the workgroup; returns the total in `total`.
 __device__ __forceinline__ uint32_t coo_block_scan(uint32_t v, uint32_t* wsum, uint32_t& total) {
@@ -143,31 +149,23 @@ __global__ __launch_bounds__(kCooThreads) void k_coo_count(const uint16_t* __res
   if (t == 0) chunk_total[blockIdx.x] = total;
 }
 
-// The count pass when the counts are already in piece_ptr (written by the legacy encode): per
-// chunk, the exclusive scan of its pieces' counts replaces them by chunk-local offsets, and the
-// chunk total goes to the workspace (the tail of k_coo_count, reading 8 bytes per piece instead
-// of the piece's 128 bytes of outliers).
-__global__ __launch_bounds__(kCooThreads) void k_coo_offsets(int64_t npieces, int64_t* __restrict__ piece_ptr,
-                                                             uint32_t* __restrict__ chunk_total) {
+// The chunk totals of staged records (the legacy encode's, lrq_coo.h): per chunk, the sum of its
+// pieces' counts into the workspace, 8 bytes read per piece.
+__global__ __launch_bounds__(kCooThreads) void k_coo_totals(const int64_t* __restrict__ piece_ptr, int64_t npieces,
+                                                            uint32_t* __restrict__ chunk_total) {
   __shared__ uint32_t wsum[kCooThreads / 64];
   const int t = threadIdx.x;
   const int64_t pc0 = (int64_t)blockIdx.x * kChunk;
   constexpr int PPT = kChunk / kCooThreads;
-  uint32_t c[PPT], s = 0;
+  uint32_t s = 0;
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
-    const int64_t pc = min(pc0 + t * PPT + i, npieces - 1);  // clamped: loaded, not counted
-    c[i] = pc0 + t * PPT + i < npieces ? (uint32_t)piece_ptr[pc] : 0u;
-    s += c[i];
+    const int64_t pc = pc0 + i * kCooThreads + t;
+    const uint32_t d0 = (uint32_t)piece_ptr[min(pc, npieces - 1)];  // clamped: loaded, not counted
+    s += pc < npieces ? coo_record_count(d0) : 0u;
   }
   uint32_t total;
-  uint32_t off = coo_block_scan(s, wsum, total);
-#pragma unroll
-  for (int i = 0; i < PPT; ++i) {
-    const int64_t pc = pc0 + t * PPT + i;
-    if (pc < npieces) piece_ptr[pc] = off;
-    off += c[i];
-  }
+  coo_block_scan(s, wsum, total);
   if (t == 0) chunk_total[blockIdx.x] = total;
 }
 
@@ -294,6 +292,185 @@ __global__ __launch_bounds__(kCooThreads) void k_coo_scatter(const uint16_t* __r
   }
 }
 
+// The scatter of staged records (lrq_coo.h; N % 64 == 0).  Up to kScanInline chunks it also does
+// the chunk scan: each workgroup sums the totals of the chunks before its own (at most 16 KB from
+// L2), and the last one writes nnz and piece_ptr[npieces]; above that k_coo_scan has run and
+// chunk_off holds the chunk offsets.  Thread t of a chunk's workgroup owns the chunk's pieces
+// 4t .. 4t+3, whose records it reads, scans over the workgroup (chunk-local first entries) and
+// replaces by the global first entries.  A piece's entries go to its first entry + their rank:
+// those a record holds, formed by the piece's thread; those of a piece with more entries, from its
+// 64 dense values, by the wave eight pieces at a time.  The wave's pieces are consecutive, so its
+// entries are consecutive positions: up to kStage of them are gathered in the wave's LDS area at
+// their position and written out coalesced (64 per store), more are written where they are formed.
+__global__ __launch_bounds__(kCooThreads) void k_coo_scatter_staged(const uint16_t* __restrict__ o, int64_t M,
+                                                                    int64_t N, int64_t npc, int64_t npieces,
+                                                                    int64_t nchunks, int64_t* __restrict__ piece_ptr,
+                                                                    const uint64_t* __restrict__ chunk_off,
+                                                                    const uint32_t* __restrict__ chunk_total,
+                                                                    int64_t* __restrict__ idx, int64_t ld_idx,
+                                                                    uint16_t* __restrict__ val, int64_t cap,
+                                                                    int64_t* __restrict__ nnz) {
+  constexpr int PPT = kChunk / kCooThreads;
+  __shared__ uint32_t wsum[kCooThreads / 64];
+  __shared__ uint64_t csum[kCooThreads / 64];
+  __shared__ u32x2 more_desc[kCooThreads / 64][64 * PPT];  // per wave: (first entry, piece) of each such piece
+  __shared__ u32x2 stage[kCooThreads / 64][kStage];         // per wave: (piece | column << 16, bf16 bits)
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t pc0 = (int64_t)blockIdx.x * kChunk;
+  // the records first (their loads overlap the chunk-offset sum)
+  const int64_t np = min((int64_t)kChunk, npieces - pc0);  // pieces of the chunk
+  uint32_t d0[PPT], d1[PPT];
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const uint32_t local = (uint32_t)min((int64_t)(PPT * t + i), np - 1);  // clamped: loaded, not counted
+    const uint64_t rec = (uint64_t)piece_ptr[pc0 + local];
+    d0[i] = (uint32_t)rec;
+    d1[i] = (uint32_t)(rec >> 32);
+  }
+  // coff = the totals of chunks 0 .. blockIdx.x - 1
+  const bool inline_scan = chunk_off == nullptr;
+  uint64_t part = 0;
+  if (inline_scan)
+    for (int64_t c = t; c < (int64_t)blockIdx.x; c += kCooThreads) part += chunk_total[c];
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) part += __shfl_xor(part, d);
+  if (lane == 0) csum[w] = part;
+  uint32_t c[PPT], s = 0;
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    c[i] = PPT * t + i < np ? coo_record_count(d0[i]) : 0u;
+    s += c[i];
+  }
+  uint32_t total;
+  uint32_t loc[PPT];
+  loc[0] = coo_block_scan(s, wsum, total);  // (its barriers also publish csum)
+  int64_t coff = 0;
+#pragma unroll
+  for (int i = 0; i < kCooThreads / 64; ++i) coff += (int64_t)csum[i];
+  if (!inline_scan) coff = (int64_t)chunk_off[blockIdx.x];
+#pragma unroll
+  for (int i = 1; i < PPT; ++i) loc[i] = loc[i - 1] + c[i - 1];
+  if (inline_scan && blockIdx.x == nchunks - 1 && t == 0) {
+    st8_region(piece_ptr + npieces, 8, 0, (uint64_t)(coff + total), true);
+    st8_region(nnz, 8, 0, (uint64_t)(coff + total), true);
+  }
+  const int64_t row0 = pc0 / npc;
+  const uint32_t rem0 = (uint32_t)(pc0 - row0 * npc), npc32 = (uint32_t)npc;
+  const int64_t b0 = row0 / M;
+  const uint32_t m0 = (uint32_t)(row0 - b0 * M), M32 = (uint32_t)M;
+  // the chunk's entries are positions coff .. coff + total - 1; the part below cap is written
+  const int64_t nw = max((int64_t)0, min((int64_t)total, cap - coff));
+  const uint32_t len8 = (uint32_t)(nw * 8), len2 = (uint32_t)(nw * 2);
+  int64_t* ib = idx + min(coff, cap);
+  int64_t* im = ib + ld_idx;
+  int64_t* in = im + ld_idx;
+  uint16_t* vb = val + min(coff, cap);
+  const uint32_t plen8 = (uint32_t)(np * 8);
+  // each thread rewrites only the records it read
+#pragma unroll
+  for (int i = 0; i < PPT; ++i)
+    st8_region(piece_ptr + pc0, plen8, (uint32_t)(PPT * t + i) * 8, (uint64_t)(coff + loc[i]), true);
+  // the wave's pieces are consecutive: its entries are chunk positions wbase .. wbase + wtot - 1
+  const uint32_t wbase = __builtin_amdgcn_readlane(loc[0], 0);
+  const uint32_t wtot = __builtin_amdgcn_readlane(loc[PPT - 1] + c[PPT - 1], 63) - wbase;
+  // the pieces with more entries than a record holds, listed per wave (first entry, piece)
+  uint32_t nmore = 0;
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const bool more = c[i] > (uint32_t)kCooSlots;
+    const uint64_t bal = __builtin_amdgcn_ballot_w64(more);
+    const uint32_t r = nmore + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+    if (more) more_desc[w][r] = u32x2{loc[i], (uint32_t)(PPT * t + i)};
+    nmore += (uint32_t)__builtin_popcountll(bal);
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes are done
+  __builtin_amdgcn_wave_barrier();
+  // Every entry goes through sink(chunk position, piece, column in piece, bf16 bits, keep): the
+  // entries a record holds from the piece's thread; those of the listed pieces from their dense
+  // values, eight pieces at a time (lane 8p + q: columns 8q .. 8q+7 of the round's piece p, ranks
+  // by a scan over the piece's 8 lanes).
+  auto entries = [&](auto sink) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < PPT; ++i)
+#pragma unroll
+      for (int k = 0; k < kCooSlots; ++k) {
+        const bool keep = c[i] <= (uint32_t)kCooSlots && (uint32_t)k < c[i];
+        if (__builtin_amdgcn_ballot_w64(keep) == 0) continue;  // wave-uniform
+        const uint32_t dw = k == 0 ? d0[i] : d1[i];
+        sink(loc[i] + k, (uint32_t)(PPT * t + i), dw & 63u, dw >> 16, keep);
+      }
+    const int q = lane & 7;
+    for (uint32_t r0 = 0; r0 < nmore; r0 += 8) {
+      const uint32_t r = r0 + (uint32_t)(lane >> 3);
+      const bool live = r < nmore;
+      const u32x2 desc = more_desc[w][min(r, nmore - 1)];
+      uint32_t dr, pcol;
+      piece_rc(rem0, npc32, desc[1], dr, pcol);
+      const u32x4 v = ld16(o + (row0 + dr) * N + (int64_t)pcol * kPiece + 8 * q);
+      uint32_t m = 0;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        m |= ((v[h] & 0x7fffu) != 0u ? 1u : 0u) << (2 * h);
+        m |= ((v[h] & 0x7fff0000u) != 0u ? 1u : 0u) << (2 * h + 1);
+      }
+      m = live ? m : 0u;
+      const uint32_t n = __builtin_popcount(m);
+      uint32_t incl = n;
+#pragma unroll
+      for (int d = 1; d < 8; d <<= 1) {
+        const uint32_t up = __shfl_up(incl, d, 8);
+        if (q >= d) incl += up;
+      }
+      uint32_t off = desc[0] + incl - n;
+      while (__builtin_amdgcn_ballot_w64(m != 0u) != 0) {
+        const bool keep = m != 0u;
+        const uint32_t i = __builtin_ctz(m | 0x100u) & 7u;
+        m &= m - 1u;
+        const uint32_t word = (i & 4u) ? ((i & 2u) ? v[3] : v[2]) : ((i & 2u) ? v[1] : v[0]);
+        sink(off, desc[1], 8u * q + i, (word >> (16u * (i & 1u))) & 0xffffu, keep);
+        off += keep ? 1u : 0u;
+      }
+    }
+  };
+  auto row_of = [&](uint32_t local, uint32_t& b, uint32_t& m, uint32_t& pcol) __attribute__((always_inline)) {
+    uint32_t dr;
+    piece_rc(rem0, npc32, local, dr, pcol);
+    const uint32_t mr = m0 + dr, qb = mr / M32;
+    b = (uint32_t)b0 + qb;
+    m = mr - qb * M32;
+  };
+  if (wtot <= (uint32_t)kStage) {  // wave-uniform
+    // the entries into the wave's LDS area at their position, then written out coalesced
+    entries([&](uint32_t off, uint32_t local, uint32_t col, uint32_t bits, bool keep) __attribute__((always_inline)) {
+      if (keep) stage[w][off - wbase] = u32x2{local | col << 16, bits};
+    });
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    for (uint32_t r0 = 0; r0 < wtot; r0 += 64) {
+      const uint32_t e = r0 + lane;
+      const bool keep = e < wtot;
+      const u32x2 en = stage[w][min(e, (uint32_t)kStage - 1)];
+      uint32_t b, m, pcol;
+      row_of(en[0] & 0xffffu, b, m, pcol);
+      const uint32_t off = wbase + e;
+      st8_region(ib, len8, off * 8, (uint64_t)b, keep);
+      st8_region(im, len8, off * 8, (uint64_t)m, keep);
+      st8_region(in, len8, off * 8, (uint64_t)pcol * kPiece + (en[0] >> 16), keep);
+      st2_region(vb, len2, off * 2, (uint16_t)en[1], keep);
+    }
+  } else {
+    // more entries than the area holds: each written where it is formed
+    entries([&](uint32_t off, uint32_t local, uint32_t col, uint32_t bits, bool keep) __attribute__((always_inline)) {
+      uint32_t b, m, pcol;
+      row_of(local, b, m, pcol);
+      st8_region(ib, len8, off * 8, (uint64_t)b, keep);
+      st8_region(im, len8, off * 8, (uint64_t)m, keep);
+      st8_region(in, len8, off * 8, (uint64_t)pcol * kPiece + col, keep);
+      st2_region(vb, len2, off * 2, (uint16_t)bits, keep);
+    });
+  }
+}
+
 struct CooPlan {
   int64_t npc, npieces, nchunks, ws_bytes;
 };
@@ -335,7 +512,7 @@ int lrq::coo_compact_check(const void* o, int64_t B, int64_t M, int64_t N, int64
   return LRQ_OK;
 }
 
-// The chunk scan and the scatter (after the count pass, or the encode's counts and their offsets).
+// The chunk scan and the scatter (after the count pass).
 static int coo_scan_scatter(const uint16_t* ob, int64_t M, int64_t N, const CooPlan& p, int64_t* indices,
                             int64_t ld_idx, void* values, int64_t cap, int64_t* nnz, int64_t* piece_ptr,
                             uint64_t* chunk_off, uint32_t* chunk_total, bool vec, hipStream_t s) {
@@ -352,17 +529,23 @@ static int coo_scan_scatter(const uint16_t* ob, int64_t M, int64_t N, const CooP
   return LRQ_OK;
 }
 
-int lrq::coo_compact_counted(const void* o, int64_t B, int64_t M, int64_t N, int64_t* indices, int64_t ld_idx,
-                             void* values, int64_t cap, int64_t* nnz, int64_t* piece_ptr, void* workspace,
-                             hipStream_t s) {
+int lrq::coo_compact_staged(const void* o, int64_t B, int64_t M, int64_t N, int64_t* indices, int64_t ld_idx,
+                            void* values, int64_t cap, int64_t* nnz, int64_t* piece_ptr, void* workspace,
+                            hipStream_t s) {
   const CooPlan p = coo_plan(B, M, N);
+  if (N % kPiece != 0 || p.nchunks == 0) return LRQ_ERR_SHAPE;  // whole pieces, at least one
   uint64_t* chunk_off = reinterpret_cast<uint64_t*>(workspace);
   uint32_t* chunk_total = reinterpret_cast<uint32_t*>(chunk_off + p.nchunks);
-  if (p.nchunks > 0)
-    LRQ_TRY(launch(k_coo_offsets, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, p.npieces, piece_ptr,
-                   chunk_total));
-  return coo_scan_scatter((const uint16_t*)o, M, N, p, indices, ld_idx, values, cap, nnz, piece_ptr, chunk_off,
-                          chunk_total, N % 8 == 0 && aligned(o, 16), s);
+  LRQ_TRY(launch(k_coo_totals, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, piece_ptr, p.npieces,
+                 chunk_total));
+  const bool inline_scan = p.nchunks <= kScanInline;
+  if (!inline_scan)
+    LRQ_TRY(launch(k_coo_scan, dim3(1), dim3(kCooThreads), 0, s, chunk_total, p.nchunks, chunk_off, p.npieces,
+                   piece_ptr, nnz));
+  LRQ_TRY(launch(k_coo_scatter_staged, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, (const uint16_t*)o, M, N,
+                 p.npc, p.npieces, p.nchunks, piece_ptr, inline_scan ? nullptr : chunk_off, chunk_total, indices,
+                 ld_idx, (uint16_t*)values, cap, nnz));
+  return LRQ_OK;
 }
 
 extern "C" int lrq_coo_compact(const void* o, int64_t B, int64_t M, int64_t N, int64_t* indices, int64_t ld_idx,

@@ -50,7 +50,7 @@ struct LegacyArgs {
   const int64_t* ocol;  //   [B * M * npc + 1]; the entries' column indices and bf16 values, in
   const uint16_t* oval; //   row-major order (lrq_coo_compact's output)
   int64_t npc;          // 64-column pieces per row, ceil(N / 64)
-  int64_t* pcnt;        // encode with counts: outliers per 64-column piece, [B * M * npc]
+  int64_t* pcnt;        // staged encode: each 64-column piece's record (lrq_coo.h), [B * M * npc]
   int64_t ncap;         // entries the COO arrays hold: reads are clamped to [0, ncap)
   uint32_t* hist;       // hist: 256 global bins
   const int64_t* sel;   // hist: sel[0] = the selected top-8-bit bin, or -1 in the first pass
@@ -98,6 +98,15 @@ __device__ __forceinline__ uint32_t legacy_code_rc(float x, float lr, float sc, 
   const float d = bf16r(q);
   const float c = __builtin_amdgcn_fmed3f(rintf(d), -half, half - 1.f);
   return (uint32_t)(int)(c + half);
+}
+
+// The bf16 bits of element i (0 .. 15) of the 16 packed in w0 (elements 0 .. 7) and w1: a select
+// tree, no indexed register access.
+__device__ __forceinline__ uint32_t bf16_at(const u32x4& w0, const u32x4& w1, uint32_t i) {
+  const u32x4 w = (i & 8u) ? w1 : w0;
+  const uint32_t lo = (i & 2u) ? w[1] : w[0], hi = (i & 2u) ? w[3] : w[2];
+  const uint32_t d = (i & 4u) ? hi : lo;
+  return (d >> (16u * (i & 1u))) & 0xffffu;
 }
 
 // Scales that legacy_code_rc serves exactly (NaN fails the test).
@@ -223,8 +232,8 @@ __device__ __forceinline__ void coo_tile(const LegacyArgs& a, int64_t (&s0)[NP],
 // entries (a piece's entries do not start on a line boundary), of the code rows and of the output
 // rows.  Wave w walks row blocks (bx * rb + i) * 64 + w * 16, i < rb, of unit u.  OSRC, decode: outliers
 // absent (0), dense (1) or COO pieces (2: looked up per lane, for sparse outliers; 3: gathered
-// per wave into an LDS tile, for denser ones); encode: 1 also writes each 64-column piece's
-// outlier count (a.pcnt), the compaction's first pass.
+// per wave into an LDS tile, for denser ones); encode: 1 writes each 64-column piece's staged
+// record (a.pcnt; lrq_coo.h) and the dense outliers only of the pieces it cannot hold.
 template <int MODE, int BITS, int K, int OSRC>
 __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
   constexpr int NP = (MODE == kAdd || MODE == kHist) ? 1 : 8 / BITS, G = 64, E = 16, RT = K / 16;
@@ -415,38 +424,53 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
         }
         if constexpr (MODE == kEncode) {
           float ov[E];
-          uint32_t n = 0;
+          uint32_t hm = 0;  // bit e: element e is an outlier entry
           if (rc_ok) {  // workgroup-uniform
 #pragma unroll
             for (int e = 0; e < E; ++e) {
               bool hit;
               byte[e] |= legacy_code_rc<BITS>(xv[e], lr[e], sc[e], rc[e], a.tau, ov[e], hit) << (BITS * p);
-              n += hit ? 1u : 0u;
+              hm |= hit ? 1u << e : 0u;
             }
           } else {
 #pragma unroll
             for (int e = 0; e < E; ++e) {
               bool hit;
               byte[e] |= legacy_code<BITS>(xv[e], lr[e], sc[e], a.tau, ov[e], hit) << (BITS * p);
-              n += hit ? 1u : 0u;
+              hm |= hit ? 1u << e : 0u;
             }
           }
-          st16(a.oout + erow + c0, pack8(ov));
-          st16(a.oout + erow + c0 + 8, pack8(ov + 8));
+          const u32x4 ow0 = pack8(ov), ow1 = pack8(ov + 8);
           if constexpr (OSRC == 1) {
-            // the piece's entries (counted above as the codes were formed) over the row's four
-            // lanes (two lane swaps); lane g = 0 of each row stores the count through a
-            // range-checked store (the other lanes' offsets fall outside the range: no branch)
-            float nf = __uint_as_float(n), t0 = nf, t1 = nf;
-            swap32(t0, t1);
-            nf = __uint_as_float(__float_as_uint(t0) + __float_as_uint(t1));
-            t0 = t1 = nf;
-            swap16(t0, t1);
-            n = __float_as_uint(t0) + __float_as_uint(t1);
+            // the piece's staged record (lrq_coo.h): its count and first kCooSlots entries, over
+            // the row's four lanes (lane g holds the piece's columns 16g .. 16g+15); its dense
+            // values only when the record cannot hold them
+            const uint32_t n = __builtin_popcount(hm);
+            uint32_t pre, total;
+            row_prefix4(n, g, pre, total);
+            const uint32_t i0 = __builtin_ctz(hm | 0x10000u) & 15u, h1 = hm & (hm - 1u);
+            const uint32_t i1 = __builtin_ctz(h1 | 0x10000u) & 15u;
+            const uint32_t e0 = ((uint32_t)(16 * g) + i0) | (bf16_at(ow0, ow1, i0) << 16);
+            const uint32_t e1 = ((uint32_t)(16 * g) + i1) | (bf16_at(ow0, ow1, i1) << 16);
+            static_assert(kCooSlots == 2, "two entries per record");
+            uint32_t d0 = pre == 0u && n >= 1u ? e0 : 0u;
+            uint32_t d1 = pre == 0u && n >= 2u ? e1 : pre == 1u && n >= 1u ? e0 : 0u;
+            d0 = row_or4(d0);
+            d1 = row_or4(d1);
+            // lane g = 0 of each row stores the record through a range-checked store (the other
+            // lanes' offsets fall outside the range: no branch)
             int64_t* prow = a.pcnt + ((int64_t)b * M + row0) * a.npc;  // the block's first row
             st8_pred(prow, (uint32_t)(16 * a.npc * 8),
-                     (uint32_t)(((rr - row0) * a.npc + unit_base(p, u, N, NP, G) / 64) * 8), u32x2{n, 0u},
-                     g == 0 && row < M);
+                     (uint32_t)(((rr - row0) * a.npc + unit_base(p, u, N, NP, G) / 64) * 8),
+                     u32x2{d0 | total << 8, d1}, g == 0 && row < M);
+            uint16_t* orow = a.oout + ((int64_t)b * M + row0) * N;
+            const uint32_t olen = (uint32_t)(16 * N * 2), ooff = (uint32_t)(((rr - row0) * N + c0) * 2);
+            const bool dense = total > (uint32_t)kCooSlots && row < M;
+            st16_pred(orow, olen, ooff, ow0, dense);
+            st16_pred(orow, olen, ooff + 16, ow1, dense);
+          } else {
+            st16(a.oout + erow + c0, ow0);
+            st16(a.oout + erow + c0 + 8, ow1);
           }
         } else {
           float ov[E];
@@ -1232,9 +1256,10 @@ extern "C" int lrq_legacy_encode(const void* l, const void* rt, int32_t K, const
   return legacy_bits<kEncode, 0>(a, K, B, bits, mfma_ok, (hipStream_t)stream);
 }
 
-// lrq_legacy_encode whose outlier compaction starts from the piece counts the encode writes (the
-// MFMA path), so the dense outliers are read once (by the scatter); other shapes take the encode
-// and the full compaction.
+// lrq_legacy_encode whose outlier compaction starts from the staged piece records the encode
+// writes (the MFMA path: each 64-column piece's count and first entries, its dense values only
+// when it has more entries than a record holds), so the dense outliers are neither written nor
+// read whole; other shapes take the encode and the full compaction.
 extern "C" int lrq_legacy_encode_coo(const void* l, const void* rt, int32_t K, const void* x, int64_t B, int64_t M,
                                      int64_t N, int64_t ldx_b, int64_t ldx_m, const void* s, int64_t s_rows,
                                      int32_t bits, float outlier, void* o, void* q, int64_t* indices, int64_t ld_idx,
@@ -1265,7 +1290,7 @@ extern "C" int lrq_legacy_encode_coo(const void* l, const void* rt, int32_t K, c
   a.tau = tau;
   a.npc = (N + 63) / 64, a.pcnt = piece_ptr;
   LRQ_TRY((legacy_bits<kEncode, 1>(a, K, B, bits, true, (hipStream_t)stream)));
-  return coo_compact_counted(o, B, M, N, indices, ld_idx, values, cap, nnz, piece_ptr, workspace, (hipStream_t)stream);
+  return coo_compact_staged(o, B, M, N, indices, ld_idx, values, cap, nnz, piece_ptr, workspace, (hipStream_t)stream);
 }
 
 extern "C" int lrq_legacy_decode(const void* l, const void* rt, int32_t K, const void* q, const void* o,

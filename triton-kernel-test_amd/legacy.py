@@ -202,7 +202,8 @@ def _coo_pieces(o, B: int, M: int, N: int):
 
 
 def _encode_coo(l, r, x, s, bits: int, outlier: float, capacity: Optional[int]):
-    """lrq_legacy_encode_coo: (LegacyOutliers, q, the dense outliers it compacted)."""
+    """lrq_legacy_encode_coo: (LegacyOutliers, q).  Its dense outlier buffer is working memory
+    (only pieces with more entries than the encode's staged records hold are written to it)."""
     _require_device(x)
     M, _ = l.shape
     _, N = r.shape
@@ -218,11 +219,12 @@ def _encode_coo(l, r, x, s, bits: int, outlier: float, capacity: Optional[int]):
         q = torch.empty((B, M, N // (8 // bits)), device=x.device, dtype=torch.uint8)
         cap = max(1024, o.numel() // 32) if capacity is None else int(capacity)
         bf = _coo_buffers(B, M, N, cap, x.device)
-        # the encode counts each piece's outliers as it writes them (the compaction's first pass)
+        # the encode stages each piece's count and first entries as it quantises (the
+        # compaction's first pass)
         call("lrq_legacy_encode_coo", _p(l2), _p(rt), K, _p(x), B, M, N, x.stride(0), x.stride(1), _p(s2),
              s2.shape[0], bits, float(outlier), _p(o), _p(q), _p(bf["idx"]), cap, _p(bf["vals"]), cap,
              _p(bf["nnz"]), _p(bf["ptr"]), _p(bf["ws"]), bf["ws"].numel() * 8, _stream(x.device))
-    return LegacyOutliers(bf["idx"], bf["vals"], bf["nnz"], bf["ptr"], tuple(o.shape)), q, o
+    return LegacyOutliers(bf["idx"], bf["vals"], bf["nnz"], bf["ptr"], tuple(o.shape)), q
 
 
 def low_rank_addition_fuse_compression_quantization(l, r, x, s, quantize_bit=8, outlier=5.):
@@ -232,10 +234,10 @@ def low_rank_addition_fuse_compression_quantization(l, r, x, s, quantize_bit=8, 
     assert l.is_contiguous(), "Matrix A must be contiguous"
     assert r.is_contiguous(), "Matrix B must be contiguous"
     bits = _bits(quantize_bit)
-    oc, q, o = _encode_coo(l, r, x, s, bits, outlier, None)
+    oc, q = _encode_coo(l, r, x, s, bits, outlier, None)
     n = int(oc.nnz.item())  # the host synchronisation to_sparse has too
-    if n > oc.capacity:
-        oc = compact_outliers(o, capacity=n)
+    if n > oc.capacity:  # more entries than the default buffers hold: again, with room for all
+        oc, q = _encode_coo(l, r, x, s, bits, outlier, n)
     return oc.to_sparse(), q
 
 
@@ -244,8 +246,7 @@ def legacy_encode_coo(l, r, x, s, quantize_bit=8, outlier=5., capacity: Optional
     (compacted on the GPU, the encode doing the compaction's count pass, entry count left on the
     device): no host synchronisation.  A decode of it reads at most `capacity` entries;
     ``LegacyOutliers.check()`` tells whether any were dropped."""
-    oc, q, _ = _encode_coo(l, r, x, s, _bits(quantize_bit), outlier, capacity)
-    return oc, q
+    return _encode_coo(l, r, x, s, _bits(quantize_bit), outlier, capacity)
 
 
 def low_rank_addition_fuse_decompression_dequantization(l, r, q, o, s, quantize_bit=8, outlier=5.):
