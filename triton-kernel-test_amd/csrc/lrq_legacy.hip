@@ -100,6 +100,93 @@ __device__ __forceinline__ uint32_t legacy_code_rc(float x, float lr, float sc, 
   return (uint32_t)(int)(c + half);
 }
 
+// The MFMA encode's forms of the steps above, with the same results:
+// - bf16r2 rounds two values to bf16 with one conversion;
+// - the code of a bf16 quotient d is legacy_code_biased(d) - kCodeBias + half, where
+//   legacy_code_biased(d) = bits(d + 1.5 * 2^23) clamped to [kCodeBias - half, kCodeBias + half - 1]:
+//   for |d| < 2^22 the sum lies in [2^23, 2^24), where the fp32 ulp is 1, so the add rounds d to the
+//   nearest integer, ties to even (1.5 * 2^23 is even), as rint does, and the bits are kCodeBias +
+//   rint(d); for d >= 2^22 the sum is at least 2^24 and clamps to the top code; for d <= -2^22 it is
+//   at most 2^23, +0 or negative (a negative int32) and clamps to the bottom code, as the clamp of
+//   rint(d) does (infinities included).  A byte starting from legacy_code_base (the sum of
+//   (half - kCodeBias) << BITS p over its planes, mod 2^32) and adding legacy_code_biased << BITS p
+//   per plane holds the planes' codes in its low 8 bits;
+// - at 1 bit the code is 1 exactly when bf16(q) >= -0.5, i.e. when q >= -(0.5 + 2^-9) (below
+//   -0.5 the bf16 spacing is 2^-8, and the tie at -0.5 - 2^-9 rounds to the even -0.5): one
+//   compare of the quotient, no rounding.
+// The host check tests/legacy_code_check.c compares both code forms with the reference's over
+// every fp32 quotient but NaN.
+__device__ __forceinline__ void bf16r2(float& a, float& b) {
+  const uint32_t w = pack_bf16x2(a, b);
+  a = __uint_as_float(w << 16);
+  b = __uint_as_float(w & 0xffff0000u);
+}
+constexpr uint32_t kCodeBias = 0x4B400000u;  // bits of 1.5 * 2^23
+template <int BITS>
+__device__ __forceinline__ uint32_t legacy_code_biased(float d) {
+  constexpr int half = 1 << (BITS - 1);
+  const int v = (int)__float_as_uint(d + 0x1.8p23f);
+  return (uint32_t)min(max(v, (int)kCodeBias - half), (int)kCodeBias + half - 1);
+}
+constexpr float kOneBitLow = -(0.5f + 0x1p-9f);
+template <int BITS>
+constexpr uint32_t legacy_code_base() {
+  if (BITS == 1) return 0u;  // the 1-bit codes are or-ed in
+  uint32_t k = 0;
+  for (int p = 0; p < 8 / BITS; ++p) k += ((1u << (BITS - 1)) - kCodeBias) << (BITS * p);
+  return k;
+}
+
+// legacy_code (RC false) or legacy_code_rc (RC true) for the MFMA encode, in the forms above: at 1
+// bit the code itself, at 2, 4 and 8 bits legacy_code_biased of bf16(q), which legacy_accumulate
+// adds to a byte that started from legacy_code_base.
+template <int BITS, bool RC>
+__device__ __forceinline__ uint32_t legacy_code_mfma(float x, float lr, float sc, float rc, float tau, float& o,
+                                                     bool& big) {
+  const float xr = bf16r(x - lr);
+  big = fabsf(xr) > tau;
+  o = big ? xr : 0.f;
+  const float a = xr - o;
+  float q;
+  if constexpr (RC) {
+    const float q0 = __builtin_amdgcn_fmed3f(a * rc, -0x1p20f, 0x1p20f);
+    q = __builtin_fmaf(__builtin_fmaf(-sc, q0, a), rc, q0);
+  } else {
+    q = a / sc;  // IEEE division
+  }
+  if constexpr (BITS == 1) return q >= kOneBitLow ? 1u : 0u;
+  else return legacy_code_biased<BITS>(bf16r(q));
+}
+// legacy_code_mfma of two elements with one bf16 conversion per rounding step (2, 4, 8 bits;
+// at 1 bit the extra registers of the pairs cost the kernel its second wave per SIMD).
+template <int BITS, bool RC>
+__device__ __forceinline__ void legacy_code_mfma2(const float* x, const float* lr, const float* sc, const float* rc,
+                                                  float tau, float* o, bool* big, uint32_t* code) {
+  static_assert(BITS > 1, "pairs at 2, 4 and 8 bits");
+  float xr[2] = {x[0] - lr[0], x[1] - lr[1]}, q[2];
+  bf16r2(xr[0], xr[1]);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    big[k] = fabsf(xr[k]) > tau;
+    o[k] = big[k] ? xr[k] : 0.f;
+    const float a = xr[k] - o[k];
+    if constexpr (RC) {
+      const float q0 = __builtin_amdgcn_fmed3f(a * rc[k], -0x1p20f, 0x1p20f);
+      q[k] = __builtin_fmaf(__builtin_fmaf(-sc[k], q0, a), rc[k], q0);
+    } else {
+      q[k] = a / sc[k];  // IEEE division
+    }
+  }
+  bf16r2(q[0], q[1]);
+  code[0] = legacy_code_biased<BITS>(q[0]);
+  code[1] = legacy_code_biased<BITS>(q[1]);
+}
+template <int BITS>
+__device__ __forceinline__ void legacy_accumulate(uint32_t& byte, uint32_t code, int p) {
+  if constexpr (BITS == 1) byte |= code << p;
+  else byte += code << (BITS * p);
+}
+
 // The bf16 bits of element i (0 .. 15) of the 16 packed in w0 (elements 0 .. 7) and w1: a select
 // tree, no indexed register access.
 __device__ __forceinline__ uint32_t bf16_at(const u32x4& w0, const u32x4& w1, uint32_t i) {
@@ -367,7 +454,7 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
     }
     uint32_t byte[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) byte[e] = 0u;
+    for (int e = 0; e < E; ++e) byte[e] = MODE == kEncode ? legacy_code_base<BITS>() : 0u;
     uint16_t* ot = otile + (size_t)w * 16 * coo_row_stride<NP>();
     if constexpr (MODE == kDecode && OSRC == 3) coo_tile<NP, kCooEntriesPerLane>(a, s0, s1, u, N, j, g, ot);
 
@@ -377,7 +464,7 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
       float lr[E];
       residual_unit<G, K>(vop[p], lop, zero, lr);
 #pragma unroll
-      for (int e = 0; e < E; ++e) lr[e] = bf16r(lr[e]);
+      for (int e = 0; e < E; e += 2) bf16r2(lr[e], lr[e + 1]);
       float sc[E], rc[E];
       if constexpr (MODE == kEncode) {
         const float* sp = stab + p * G + E * g;
@@ -423,21 +510,46 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
           unpack8(ld16(xp + 8), xv + 8);
         }
         if constexpr (MODE == kEncode) {
+          // legacy_code(_rc) of each element in the forms above (legacy_code_mfma)
           float ov[E];
           uint32_t hm = 0;  // bit e: element e is an outlier entry
-          if (rc_ok) {  // workgroup-uniform
+          if constexpr (BITS == 1) {
+            if (rc_ok) {  // workgroup-uniform
 #pragma unroll
-            for (int e = 0; e < E; ++e) {
-              bool hit;
-              byte[e] |= legacy_code_rc<BITS>(xv[e], lr[e], sc[e], rc[e], a.tau, ov[e], hit) << (BITS * p);
-              hm |= hit ? 1u << e : 0u;
+              for (int e = 0; e < E; ++e) {
+                bool hit;
+                legacy_accumulate<BITS>(byte[e], legacy_code_mfma<BITS, true>(xv[e], lr[e], sc[e], rc[e], a.tau, ov[e], hit), p);
+                hm |= hit ? 1u << e : 0u;
+              }
+            } else {
+#pragma unroll
+              for (int e = 0; e < E; ++e) {
+                bool hit;
+                legacy_accumulate<BITS>(byte[e], legacy_code_mfma<BITS, false>(xv[e], lr[e], sc[e], 0.f, a.tau, ov[e], hit), p);
+                hm |= hit ? 1u << e : 0u;
+              }
             }
           } else {
+            if (rc_ok) {  // workgroup-uniform
 #pragma unroll
-            for (int e = 0; e < E; ++e) {
-              bool hit;
-              byte[e] |= legacy_code<BITS>(xv[e], lr[e], sc[e], a.tau, ov[e], hit) << (BITS * p);
-              hm |= hit ? 1u << e : 0u;
+              for (int e = 0; e < E; e += 2) {
+                bool hit[2];
+                uint32_t cd[2];
+                legacy_code_mfma2<BITS, true>(xv + e, lr + e, sc + e, rc + e, a.tau, ov + e, hit, cd);
+                legacy_accumulate<BITS>(byte[e], cd[0], p);
+                legacy_accumulate<BITS>(byte[e + 1], cd[1], p);
+                hm |= (hit[0] ? 1u << e : 0u) | (hit[1] ? 2u << e : 0u);
+              }
+            } else {
+#pragma unroll
+              for (int e = 0; e < E; e += 2) {
+                bool hit[2];
+                uint32_t cd[2];
+                legacy_code_mfma2<BITS, false>(xv + e, lr + e, sc + e, rc + e, a.tau, ov + e, hit, cd);
+                legacy_accumulate<BITS>(byte[e], cd[0], p);
+                legacy_accumulate<BITS>(byte[e + 1], cd[1], p);
+                hm |= (hit[0] ? 1u << e : 0u) | (hit[1] ? 2u << e : 0u);
+              }
             }
           }
           const u32x4 ow0 = pack8(ov), ow1 = pack8(ov + 8);
