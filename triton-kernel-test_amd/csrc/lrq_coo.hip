@@ -36,8 +36,10 @@ constexpr int kChunk = 4096;  // pieces per chunk
 constexpr int kCooThreads = 1024;
 constexpr int kStage = 8 * kPiece;  // entries one wave's 8 pieces can hold
 constexpr int kScanInline = 4096;   // chunks up to which the staged scatter sums the chunk totals itself
+constexpr int kScatterThreads = 512;  // the staged scatter's workgroup (half a chunk)
 
-// Exclusive prefix sum over the 1024 threads of the workgroup; returns the total in `total`.
+// Exclusive prefix sum over the NT threads of the workgroup; returns the total in `total`.
+template <int NT = kCooThreads>
 __device__ __forceinline__ uint32_t coo_block_scan(uint32_t v, uint32_t* wsum, uint32_t& total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   uint32_t incl = v;
@@ -50,7 +52,7 @@ __device__ __forceinline__ uint32_t coo_block_scan(uint32_t v, uint32_t* wsum, u
   __syncthreads();
   uint32_t before = 0, all = 0;
 #pragma unroll
-  for (int i = 0; i < kCooThreads / 64; ++i) {
+  for (int i = 0; i < NT / 64; ++i) {
     const uint32_t t = wsum[i];
     before += i < w ? t : 0u;
     all += t;
@@ -150,23 +152,30 @@ __global__ __launch_bounds__(kCooThreads) void k_coo_count(const uint16_t* __res
 }
 
 // The chunk totals of staged records (the legacy encode's, lrq_coo.h): per chunk, the sum of its
-// pieces' counts into the workspace, 8 bytes read per piece.
+// pieces' counts, and of its first kChunk / 2 pieces' (half_total), into the workspace; 8 bytes
+// read per piece.
 __global__ __launch_bounds__(kCooThreads) void k_coo_totals(const int64_t* __restrict__ piece_ptr, int64_t npieces,
-                                                            uint32_t* __restrict__ chunk_total) {
+                                                            uint32_t* __restrict__ chunk_total,
+                                                            uint32_t* __restrict__ half_total) {
   __shared__ uint32_t wsum[kCooThreads / 64];
   const int t = threadIdx.x;
   const int64_t pc0 = (int64_t)blockIdx.x * kChunk;
   constexpr int PPT = kChunk / kCooThreads;
-  uint32_t s = 0;
+  static_assert(PPT % 2 == 0, "iterations 0 .. PPT/2 - 1 cover the first half");
+  uint32_t s[2] = {0u, 0u};
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
     const int64_t pc = pc0 + i * kCooThreads + t;
     const uint32_t d0 = (uint32_t)piece_ptr[min(pc, npieces - 1)];  // clamped: loaded, not counted
-    s += pc < npieces ? coo_record_count(d0) : 0u;
+    s[2 * i / PPT] += pc < npieces ? coo_record_count(d0) : 0u;
   }
-  uint32_t total;
-  coo_block_scan(s, wsum, total);
-  if (t == 0) chunk_total[blockIdx.x] = total;
+  uint32_t total, first;
+  coo_block_scan(s[0] + s[1], wsum, total);
+  coo_block_scan(s[0], wsum, first);
+  if (t == 0) {
+    chunk_total[blockIdx.x] = total;
+    half_total[blockIdx.x] = first;
+  }
 }
 
 // One workgroup: chunk_off[c] = sum of the totals of chunks < c; nnz and piece_ptr[npieces].
@@ -198,6 +207,14 @@ __device__ __forceinline__ void st8_region(void* base, uint32_t len, uint32_t of
 }
 __device__ __forceinline__ void st2_region(void* base, uint32_t len, uint32_t off, uint16_t v, bool keep) {
   const __amdgpu_buffer_rsrc_t r = uniform_rsrc(base, len);
+  __builtin_amdgcn_raw_buffer_store_b16(v, r, keep ? off : 0x7ffffff0u, 0, 0);
+}
+
+// The same stores through a buffer resource made once (uniform_rsrc) for several of them.
+__device__ __forceinline__ void st8_at(__amdgpu_buffer_rsrc_t r, uint32_t off, uint64_t v, bool keep) {
+  __builtin_amdgcn_raw_buffer_store_b64(u32x2{(uint32_t)v, (uint32_t)(v >> 32)}, r, keep ? off : 0x7ffffff0u, 0, 0);
+}
+__device__ __forceinline__ void st2_at(__amdgpu_buffer_rsrc_t r, uint32_t off, uint16_t v, bool keep) {
   __builtin_amdgcn_raw_buffer_store_b16(v, r, keep ? off : 0x7ffffff0u, 0, 0);
 }
 
@@ -292,33 +309,36 @@ __global__ __launch_bounds__(kCooThreads) void k_coo_scatter(const uint16_t* __r
   }
 }
 
-// The scatter of staged records (lrq_coo.h; N % 64 == 0).  Up to kScanInline chunks it also does
-// the chunk scan: each workgroup sums the totals of the chunks before its own (at most 16 KB from
-// L2), and the last one writes nnz and piece_ptr[npieces]; above that k_coo_scan has run and
-// chunk_off holds the chunk offsets.  Thread t of a chunk's workgroup owns the chunk's pieces
-// 4t .. 4t+3, whose records it reads, scans over the workgroup (chunk-local first entries) and
-// replaces by the global first entries.  A piece's entries go to its first entry + their rank:
+// The scatter of staged records (lrq_coo.h; N % 64 == 0), two workgroups of kScatterThreads per
+// chunk, each over one half (a part: kChunk / 2 pieces), so that up to three of them share a CU.
+// Up to kScanInline chunks it also does the chunk scan: each workgroup sums the totals of the
+// chunks before its own (at most 16 KB from L2), and the first part of the last chunk writes nnz
+// and piece_ptr[npieces]; above that k_coo_scan has run and chunk_off holds the chunk offsets.  The
+// second part starts after the first's half_total entries.  Thread t of a part's workgroup owns its
+// pieces 4t .. 4t+3, whose records it reads, scans over the workgroup (part-local first entries)
+// and replaces by the global first entries.  A piece's entries go to its first entry + their rank:
 // those a record holds, formed by the piece's thread; those of a piece with more entries, from its
-// 64 dense values, by the wave eight pieces at a time.  The wave's pieces are consecutive, so its
-// entries are consecutive positions: up to kStage of them are gathered in the wave's LDS area at
-// their position and written out coalesced (64 per store), more are written where they are formed.
-__global__ __launch_bounds__(kCooThreads) void k_coo_scatter_staged(const uint16_t* __restrict__ o, int64_t M,
-                                                                    int64_t N, int64_t npc, int64_t npieces,
-                                                                    int64_t nchunks, int64_t* __restrict__ piece_ptr,
-                                                                    const uint64_t* __restrict__ chunk_off,
-                                                                    const uint32_t* __restrict__ chunk_total,
-                                                                    int64_t* __restrict__ idx, int64_t ld_idx,
-                                                                    uint16_t* __restrict__ val, int64_t cap,
-                                                                    int64_t* __restrict__ nnz) {
-  constexpr int PPT = kChunk / kCooThreads;
-  __shared__ uint32_t wsum[kCooThreads / 64];
-  __shared__ uint64_t csum[kCooThreads / 64];
-  __shared__ u32x2 more_desc[kCooThreads / 64][64 * PPT];  // per wave: (first entry, piece) of each such piece
-  __shared__ u32x2 stage[kCooThreads / 64][kStage];         // per wave: (piece | column << 16, bf16 bits)
+// 64 dense values, by the wave eight pieces at a time (four such rounds' loads issued together).
+// The wave's pieces are consecutive, so its entries are consecutive positions: up to kStage of them
+// are gathered in the wave's LDS area at their position and written out coalesced (64 per store),
+// more are written where they are formed.
+__global__ __launch_bounds__(kScatterThreads) void k_coo_scatter_staged(
+    const uint16_t* __restrict__ o, int64_t M, int64_t N, int64_t npc, int64_t npieces, int64_t nchunks,
+    int64_t* __restrict__ piece_ptr, const uint64_t* __restrict__ chunk_off, const uint32_t* __restrict__ chunk_total,
+    const uint32_t* __restrict__ half_total, int64_t* __restrict__ idx, int64_t ld_idx, uint16_t* __restrict__ val,
+    int64_t cap, int64_t* __restrict__ nnz) {
+  constexpr int NW = kScatterThreads / 64, PART = kChunk / 2, PPT = PART / kScatterThreads;
+  __shared__ uint32_t wsum[NW];
+  __shared__ uint64_t csum[NW];
+  __shared__ u32x2 more_desc[NW][64 * PPT];  // per wave: (first entry, piece) of each such piece
+  __shared__ u32x2 stage[NW][kStage];         // per wave: (piece | column << 16, bf16 bits)
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int64_t pc0 = (int64_t)blockIdx.x * kChunk;
+  const int64_t chunk = blockIdx.x >> 1;
+  const int part = blockIdx.x & 1;
+  const int64_t pc0 = chunk * kChunk + part * PART;
+  const int64_t np = min((int64_t)PART, npieces - pc0);  // pieces of the part
+  if (np <= 0) return;  // the second part of a short last chunk (workgroup-uniform)
   // the records first (their loads overlap the chunk-offset sum)
-  const int64_t np = min((int64_t)kChunk, npieces - pc0);  // pieces of the chunk
   uint32_t d0[PPT], d1[PPT];
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
@@ -327,14 +347,14 @@ __global__ __launch_bounds__(kCooThreads) void k_coo_scatter_staged(const uint16
     d0[i] = (uint32_t)rec;
     d1[i] = (uint32_t)(rec >> 32);
   }
-  // coff = the totals of chunks 0 .. blockIdx.x - 1
+  // coff = the totals of chunks 0 .. chunk - 1 (+ the first part's, for the second)
   const bool inline_scan = chunk_off == nullptr;
-  uint64_t part = 0;
+  uint64_t part_sum = 0;
   if (inline_scan)
-    for (int64_t c = t; c < (int64_t)blockIdx.x; c += kCooThreads) part += chunk_total[c];
+    for (int64_t c = t; c < chunk; c += kScatterThreads) part_sum += chunk_total[c];
 #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) part += __shfl_xor(part, d);
-  if (lane == 0) csum[w] = part;
+  for (int d = 1; d < 64; d <<= 1) part_sum += __shfl_xor(part_sum, d);
+  if (lane == 0) csum[w] = part_sum;
   uint32_t c[PPT], s = 0;
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
@@ -343,16 +363,18 @@ __global__ __launch_bounds__(kCooThreads) void k_coo_scatter_staged(const uint16
   }
   uint32_t total;
   uint32_t loc[PPT];
-  loc[0] = coo_block_scan(s, wsum, total);  // (its barriers also publish csum)
-  int64_t coff = 0;
+  loc[0] = coo_block_scan<kScatterThreads>(s, wsum, total);  // (its barriers also publish csum)
+  int64_t chunk_start = 0;
 #pragma unroll
-  for (int i = 0; i < kCooThreads / 64; ++i) coff += (int64_t)csum[i];
-  if (!inline_scan) coff = (int64_t)chunk_off[blockIdx.x];
+  for (int i = 0; i < NW; ++i) chunk_start += (int64_t)csum[i];
+  if (!inline_scan) chunk_start = (int64_t)chunk_off[chunk];
+  const int64_t coff = chunk_start + (part ? (int64_t)half_total[chunk] : 0);
 #pragma unroll
   for (int i = 1; i < PPT; ++i) loc[i] = loc[i - 1] + c[i - 1];
-  if (inline_scan && blockIdx.x == nchunks - 1 && t == 0) {
-    st8_region(piece_ptr + npieces, 8, 0, (uint64_t)(coff + total), true);
-    st8_region(nnz, 8, 0, (uint64_t)(coff + total), true);
+  if (inline_scan && chunk == nchunks - 1 && part == 0 && t == 0) {
+    const uint64_t all = (uint64_t)(chunk_start + chunk_total[chunk]);
+    st8_region(piece_ptr + npieces, 8, 0, all, true);
+    st8_region(nnz, 8, 0, all, true);
   }
   const int64_t row0 = pc0 / npc;
   const uint32_t rem0 = (uint32_t)(pc0 - row0 * npc), npc32 = (uint32_t)npc;
@@ -366,11 +388,35 @@ __global__ __launch_bounds__(kCooThreads) void k_coo_scatter_staged(const uint16
   int64_t* in = im + ld_idx;
   uint16_t* vb = val + min(coff, cap);
   const uint32_t plen8 = (uint32_t)(np * 8);
+  // the regions' buffer resources, made once
+  const __amdgpu_buffer_rsrc_t r_ib = uniform_rsrc(ib, len8), r_im = uniform_rsrc(im, len8),
+                               r_in = uniform_rsrc(in, len8), r_vb = uniform_rsrc(vb, len2),
+                               r_pp = uniform_rsrc(piece_ptr + pc0, plen8);
   // each thread rewrites only the records it read
 #pragma unroll
-  for (int i = 0; i < PPT; ++i)
-    st8_region(piece_ptr + pc0, plen8, (uint32_t)(PPT * t + i) * 8, (uint64_t)(coff + loc[i]), true);
-  // the wave's pieces are consecutive: its entries are chunk positions wbase .. wbase + wtot - 1
+  for (int i = 0; i < PPT; ++i) st8_at(r_pp, (uint32_t)(PPT * t + i) * 8, (uint64_t)(coff + loc[i]), true);
+  // the row (from row0) and 64-column piece of each of the thread's pieces: one division, then steps
+  uint32_t dr[PPT], pcol[PPT];
+  piece_rc(rem0, npc32, (uint32_t)min((int64_t)(PPT * t), np - 1), dr[0], pcol[0]);
+#pragma unroll
+  for (int i = 1; i < PPT; ++i) {
+    dr[i] = dr[i - 1];
+    pcol[i] = pcol[i - 1] + 1u;
+    if (pcol[i] == npc32) {
+      pcol[i] = 0u;
+      ++dr[i];
+    }
+  }
+  // batch and row of a row offset: one batch for the whole part unless it crosses a batch end
+  uint32_t dr_last, pc_last;
+  piece_rc(rem0, npc32, (uint32_t)(np - 1), dr_last, pc_last);
+  const bool one_batch = m0 + dr_last < M32;
+  auto batch_row = [&](uint32_t d, uint64_t& b, uint64_t& m) __attribute__((always_inline)) {
+    const uint32_t mr = m0 + d, qb = one_batch ? 0u : mr / M32;
+    b = (uint64_t)(b0 + qb);
+    m = (uint64_t)(mr - qb * M32);
+  };
+  // the wave's pieces are consecutive: its entries are part positions wbase .. wbase + wtot - 1
   const uint32_t wbase = __builtin_amdgcn_readlane(loc[0], 0);
   const uint32_t wtot = __builtin_amdgcn_readlane(loc[PPT - 1] + c[PPT - 1], 63) - wbase;
   // the pieces with more entries than a record holds, listed per wave (first entry, piece)
@@ -385,10 +431,10 @@ __global__ __launch_bounds__(kCooThreads) void k_coo_scatter_staged(const uint16
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes are done
   __builtin_amdgcn_wave_barrier();
-  // Every entry goes through sink(chunk position, piece, column in piece, bf16 bits, keep): the
-  // entries a record holds from the piece's thread; those of the listed pieces from their dense
-  // values, eight pieces at a time (lane 8p + q: columns 8q .. 8q+7 of the round's piece p, ranks
-  // by a scan over the piece's 8 lanes).
+  // Every entry goes through sink(part position, row offset, column, bf16 bits, keep): the entries a
+  // record holds from the piece's thread; those of the listed pieces from their dense values, eight
+  // pieces at a time (lane 8p + q: columns 8q .. 8q+7 of the round's piece p, ranks by a scan over
+  // the piece's 8 lanes).
   auto entries = [&](auto sink) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < PPT; ++i)
@@ -397,52 +443,55 @@ __global__ __launch_bounds__(kCooThreads) void k_coo_scatter_staged(const uint16
         const bool keep = c[i] <= (uint32_t)kCooSlots && (uint32_t)k < c[i];
         if (__builtin_amdgcn_ballot_w64(keep) == 0) continue;  // wave-uniform
         const uint32_t dw = k == 0 ? d0[i] : d1[i];
-        sink(loc[i] + k, (uint32_t)(PPT * t + i), dw & 63u, dw >> 16, keep);
+        sink(loc[i] + k, dr[i], pcol[i] * kPiece + (dw & 63u), dw >> 16, keep);
       }
     const int q = lane & 7;
-    for (uint32_t r0 = 0; r0 < nmore; r0 += 8) {
-      const uint32_t r = r0 + (uint32_t)(lane >> 3);
-      const bool live = r < nmore;
-      const u32x2 desc = more_desc[w][min(r, nmore - 1)];
-      uint32_t dr, pcol;
-      piece_rc(rem0, npc32, desc[1], dr, pcol);
-      const u32x4 v = ld16(o + (row0 + dr) * N + (int64_t)pcol * kPiece + 8 * q);
-      uint32_t m = 0;
+    constexpr int RA = 4;  // rounds whose loads are in flight together
+    for (uint32_t r0 = 0; r0 < nmore; r0 += 8 * RA) {
+      u32x4 v[RA];
+      uint32_t pdr[RA], ppc[RA], first[RA];
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        m |= ((v[h] & 0x7fffu) != 0u ? 1u : 0u) << (2 * h);
-        m |= ((v[h] & 0x7fff0000u) != 0u ? 1u : 0u) << (2 * h + 1);
+      for (int j = 0; j < RA; ++j) {  // (rounds past the list load a listed piece again: unused)
+        const u32x2 desc = more_desc[w][min(r0 + 8 * j + (uint32_t)(lane >> 3), nmore - 1)];
+        first[j] = desc[0];
+        piece_rc(rem0, npc32, desc[1], pdr[j], ppc[j]);
+        v[j] = ld16(o + (row0 + pdr[j]) * N + (int64_t)ppc[j] * kPiece + 8 * q);
       }
-      m = live ? m : 0u;
-      const uint32_t n = __builtin_popcount(m);
-      uint32_t incl = n;
 #pragma unroll
-      for (int d = 1; d < 8; d <<= 1) {
-        const uint32_t up = __shfl_up(incl, d, 8);
-        if (q >= d) incl += up;
-      }
-      uint32_t off = desc[0] + incl - n;
-      while (__builtin_amdgcn_ballot_w64(m != 0u) != 0) {
-        const bool keep = m != 0u;
-        const uint32_t i = __builtin_ctz(m | 0x100u) & 7u;
-        m &= m - 1u;
-        const uint32_t word = (i & 4u) ? ((i & 2u) ? v[3] : v[2]) : ((i & 2u) ? v[1] : v[0]);
-        sink(off, desc[1], 8u * q + i, (word >> (16u * (i & 1u))) & 0xffffu, keep);
-        off += keep ? 1u : 0u;
+      for (int j = 0; j < RA; ++j) {
+        if (r0 + 8 * j >= nmore) break;  // wave-uniform
+        const bool live = r0 + 8 * j + (uint32_t)(lane >> 3) < nmore;
+        uint32_t m = 0;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          m |= ((v[j][h] & 0x7fffu) != 0u ? 1u : 0u) << (2 * h);
+          m |= ((v[j][h] & 0x7fff0000u) != 0u ? 1u : 0u) << (2 * h + 1);
+        }
+        m = live ? m : 0u;
+        const uint32_t n = __builtin_popcount(m);
+        uint32_t incl = n;
+#pragma unroll
+        for (int d = 1; d < 8; d <<= 1) {
+          const uint32_t up = __shfl_up(incl, d, 8);
+          if (q >= d) incl += up;
+        }
+        uint32_t off = first[j] + incl - n;
+        while (__builtin_amdgcn_ballot_w64(m != 0u) != 0) {
+          const bool keep = m != 0u;
+          const uint32_t i = __builtin_ctz(m | 0x100u) & 7u;
+          m &= m - 1u;
+          const u32x4 vj = v[j];
+          const uint32_t word = (i & 4u) ? ((i & 2u) ? vj[3] : vj[2]) : ((i & 2u) ? vj[1] : vj[0]);
+          sink(off, pdr[j], ppc[j] * kPiece + 8u * q + i, (word >> (16u * (i & 1u))) & 0xffffu, keep);
+          off += keep ? 1u : 0u;
+        }
       }
     }
   };
-  auto row_of = [&](uint32_t local, uint32_t& b, uint32_t& m, uint32_t& pcol) __attribute__((always_inline)) {
-    uint32_t dr;
-    piece_rc(rem0, npc32, local, dr, pcol);
-    const uint32_t mr = m0 + dr, qb = mr / M32;
-    b = (uint32_t)b0 + qb;
-    m = mr - qb * M32;
-  };
   if (wtot <= (uint32_t)kStage) {  // wave-uniform
     // the entries into the wave's LDS area at their position, then written out coalesced
-    entries([&](uint32_t off, uint32_t local, uint32_t col, uint32_t bits, bool keep) __attribute__((always_inline)) {
-      if (keep) stage[w][off - wbase] = u32x2{local | col << 16, bits};
+    entries([&](uint32_t off, uint32_t d, uint32_t col, uint32_t bits, bool keep) __attribute__((always_inline)) {
+      if (keep) stage[w][off - wbase] = u32x2{col, d | bits << 16};
     });
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
@@ -450,23 +499,23 @@ __global__ __launch_bounds__(kCooThreads) void k_coo_scatter_staged(const uint16
       const uint32_t e = r0 + lane;
       const bool keep = e < wtot;
       const u32x2 en = stage[w][min(e, (uint32_t)kStage - 1)];
-      uint32_t b, m, pcol;
-      row_of(en[0] & 0xffffu, b, m, pcol);
+      uint64_t b, m;
+      batch_row(en[1] & 0xffffu, b, m);
       const uint32_t off = wbase + e;
-      st8_region(ib, len8, off * 8, (uint64_t)b, keep);
-      st8_region(im, len8, off * 8, (uint64_t)m, keep);
-      st8_region(in, len8, off * 8, (uint64_t)pcol * kPiece + (en[0] >> 16), keep);
-      st2_region(vb, len2, off * 2, (uint16_t)en[1], keep);
+      st8_at(r_ib, off * 8, b, keep);
+      st8_at(r_im, off * 8, m, keep);
+      st8_at(r_in, off * 8, (uint64_t)en[0], keep);
+      st2_at(r_vb, off * 2, (uint16_t)(en[1] >> 16), keep);
     }
   } else {
     // more entries than the area holds: each written where it is formed
-    entries([&](uint32_t off, uint32_t local, uint32_t col, uint32_t bits, bool keep) __attribute__((always_inline)) {
-      uint32_t b, m, pcol;
-      row_of(local, b, m, pcol);
-      st8_region(ib, len8, off * 8, (uint64_t)b, keep);
-      st8_region(im, len8, off * 8, (uint64_t)m, keep);
-      st8_region(in, len8, off * 8, (uint64_t)pcol * kPiece + col, keep);
-      st2_region(vb, len2, off * 2, (uint16_t)bits, keep);
+    entries([&](uint32_t off, uint32_t d, uint32_t col, uint32_t bits, bool keep) __attribute__((always_inline)) {
+      uint64_t b, m;
+      batch_row(d, b, m);
+      st8_at(r_ib, off * 8, b, keep);
+      st8_at(r_im, off * 8, m, keep);
+      st8_at(r_in, off * 8, (uint64_t)col, keep);
+      st2_at(r_vb, off * 2, (uint16_t)bits, keep);
     });
   }
 }
@@ -480,7 +529,7 @@ static CooPlan coo_plan(int64_t B, int64_t M, int64_t N) {
   p.npc = (N + kPiece - 1) / kPiece;
   p.npieces = B * M * p.npc;
   p.nchunks = (p.npieces + kChunk - 1) / kChunk;
-  p.ws_bytes = p.nchunks * 16;  // uint32 totals (padded to 8 bytes) + uint64 offsets
+  p.ws_bytes = p.nchunks * 16;  // uint64 offsets, uint32 totals, uint32 first-half totals (staged path)
   return p;
 }
 
@@ -536,15 +585,16 @@ int lrq::coo_compact_staged(const void* o, int64_t B, int64_t M, int64_t N, int6
   if (N % kPiece != 0 || p.nchunks == 0) return LRQ_ERR_SHAPE;  // whole pieces, at least one
   uint64_t* chunk_off = reinterpret_cast<uint64_t*>(workspace);
   uint32_t* chunk_total = reinterpret_cast<uint32_t*>(chunk_off + p.nchunks);
+  uint32_t* half_total = chunk_total + p.nchunks;  // the workspace's last nchunks * 4 bytes
   LRQ_TRY(launch(k_coo_totals, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, piece_ptr, p.npieces,
-                 chunk_total));
+                 chunk_total, half_total));
   const bool inline_scan = p.nchunks <= kScanInline;
   if (!inline_scan)
     LRQ_TRY(launch(k_coo_scan, dim3(1), dim3(kCooThreads), 0, s, chunk_total, p.nchunks, chunk_off, p.npieces,
                    piece_ptr, nnz));
-  LRQ_TRY(launch(k_coo_scatter_staged, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, (const uint16_t*)o, M, N,
-                 p.npc, p.npieces, p.nchunks, piece_ptr, inline_scan ? nullptr : chunk_off, chunk_total, indices,
-                 ld_idx, (uint16_t*)values, cap, nnz));
+  LRQ_TRY(launch(k_coo_scatter_staged, dim3((unsigned)(2 * p.nchunks)), dim3(kScatterThreads), 0, s,
+                 (const uint16_t*)o, M, N, p.npc, p.npieces, p.nchunks, piece_ptr, inline_scan ? nullptr : chunk_off,
+                 chunk_total, half_total, indices, ld_idx, (uint16_t*)values, cap, nnz));
   return LRQ_OK;
 }
 
