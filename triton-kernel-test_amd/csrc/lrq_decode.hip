@@ -672,7 +672,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_rows(
           // the lane's outlier columns one by one (usually none or one): a select over the E
           // values per outlier, instead of a test, a table read and a select per value
           const int c0 = unit_base(p, u, N, NP, G) + E * g;  // E consecutive columns in one mask word
-          uint32_t mbits = (colmask[c0 >> 5] >> (c0 & 31)) & (E >= 32 ? ~0u : (1u << E) - 1u);
+          uint32_t mbits = (colmask[c0 >> 5] >> (c0 & 31)) & (uint32_t)((1ull << E) - 1ull);
           const uint16_t* ss = reinterpret_cast<const uint16_t*>(slot + Tl::SLOT) + j * kSideMax;
           while (mbits != 0u) {
             const int e0 = __builtin_ctz(mbits);
