@@ -55,6 +55,12 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
 __device__ __forceinline__ float bf16_roundtrip(float f) { return __uint_as_float(pack_bf16x2(f, 0.f) << 16); }
+// bf16_roundtrip of two values with one conversion.
+__device__ __forceinline__ void bf16_roundtrip2(float& a, float& b) {
+  const uint32_t w = pack_bf16x2(a, b);
+  a = __uint_as_float(w << 16);
+  b = __uint_as_float(w & 0xffff0000u);
+}
 // Pack two fp32 values that are already exactly representable in bf16 (no rounding): the
 // high halves of both, one v_perm_b32.
 __device__ __forceinline__ uint32_t pack_bf16x2_exact(float lo, float hi) {

@@ -64,10 +64,16 @@ struct EpiSilu {
   __host__ __device__ __forceinline__ int64_t in_ld() const { return lddy; }
   __host__ __device__ __forceinline__ int64_t out_ld() const { return lddx; }
   __device__ __forceinline__ u32x4 apply(const float* xh, u32x4 dyv) const {
-    float d[8], o[8];
+    float d[8], o[8], x[8];
     unpack8(dyv, d);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = silu_bwd_f32(bf16_roundtrip(xh[e]), d[e]);
+    for (int e = 0; e < 8; e += 2) {  // x = bf16(x_hat), two per conversion
+      x[e] = xh[e];
+      x[e + 1] = xh[e + 1];
+      bf16_roundtrip2(x[e], x[e + 1]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = silu_bwd_f32(x[e], d[e]);
     return pack8(o);
   }
 };
@@ -84,10 +90,16 @@ struct EpiGelu {
   __host__ __device__ __forceinline__ int64_t in_ld() const { return lddy; }
   __host__ __device__ __forceinline__ int64_t out_ld() const { return lddx; }
   __device__ __forceinline__ u32x4 apply(const float* xh, u32x4 dyv) const {
-    float d[8], o[8];
+    float d[8], o[8], x[8];
     unpack8(dyv, d);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = gelu_bwd_f32(bf16_roundtrip(xh[e]), d[e]);
+    for (int e = 0; e < 8; e += 2) {  // x = bf16(x_hat), two per conversion
+      x[e] = xh[e];
+      x[e + 1] = xh[e + 1];
+      bf16_roundtrip2(x[e], x[e + 1]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = gelu_bwd_f32(x[e], d[e]);
     return pack8(o);
   }
 };
@@ -104,10 +116,16 @@ struct EpiMul {
   __host__ __device__ __forceinline__ int64_t in_ld() const { return ldy; }
   __host__ __device__ __forceinline__ int64_t out_ld() const { return ldo; }
   __device__ __forceinline__ u32x4 apply(const float* xh, u32x4 yv) const {
-    float a[8], o[8];
+    float a[8], o[8], x[8];
     unpack8(yv, a);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = bf16_roundtrip(xh[e]) * a[e];
+    for (int e = 0; e < 8; e += 2) {  // x = bf16(x_hat), two per conversion
+      x[e] = xh[e];
+      x[e + 1] = xh[e + 1];
+      bf16_roundtrip2(x[e], x[e + 1]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = x[e] * a[e];
     return pack8(o);
   }
 };

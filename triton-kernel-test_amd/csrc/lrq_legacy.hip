@@ -101,7 +101,7 @@ __device__ __forceinline__ uint32_t legacy_code_rc(float x, float lr, float sc, 
 }
 
 // The MFMA encode's forms of the steps above, with the same results:
-// - bf16r2 rounds two values to bf16 with one conversion;
+// - bf16_roundtrip2 rounds two values to bf16 with one conversion;
 // - the code of a bf16 quotient d is legacy_code_biased(d) - kCodeBias + half, where
 //   legacy_code_biased(d) = bits(d + 1.5 * 2^23) clamped to [kCodeBias - half, kCodeBias + half - 1]:
 //   for |d| < 2^22 the sum lies in [2^23, 2^24), where the fp32 ulp is 1, so the add rounds d to the
@@ -116,11 +116,6 @@ __device__ __forceinline__ uint32_t legacy_code_rc(float x, float lr, float sc, 
 //   compare of the quotient, no rounding.
 // The host check tests/legacy_code_check.c compares both code forms with the reference's over
 // every fp32 quotient but NaN.
-__device__ __forceinline__ void bf16r2(float& a, float& b) {
-  const uint32_t w = pack_bf16x2(a, b);
-  a = __uint_as_float(w << 16);
-  b = __uint_as_float(w & 0xffff0000u);
-}
 constexpr uint32_t kCodeBias = 0x4B400000u;  // bits of 1.5 * 2^23
 template <int BITS>
 __device__ __forceinline__ uint32_t legacy_code_biased(float d) {
@@ -164,7 +159,7 @@ __device__ __forceinline__ void legacy_code_mfma2(const float* x, const float* l
                                                   float tau, float* o, bool* big, uint32_t* code) {
   static_assert(BITS > 1, "pairs at 2, 4 and 8 bits");
   float xr[2] = {x[0] - lr[0], x[1] - lr[1]}, q[2];
-  bf16r2(xr[0], xr[1]);
+  bf16_roundtrip2(xr[0], xr[1]);
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     big[k] = fabsf(xr[k]) > tau;
@@ -177,7 +172,7 @@ __device__ __forceinline__ void legacy_code_mfma2(const float* x, const float* l
       q[k] = a / sc[k];  // IEEE division
     }
   }
-  bf16r2(q[0], q[1]);
+  bf16_roundtrip2(q[0], q[1]);
   code[0] = legacy_code_biased<BITS>(q[0]);
   code[1] = legacy_code_biased<BITS>(q[1]);
 }
@@ -464,7 +459,7 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
       float lr[E];
       residual_unit<G, K>(vop[p], lop, zero, lr);
 #pragma unroll
-      for (int e = 0; e < E; e += 2) bf16r2(lr[e], lr[e + 1]);
+      for (int e = 0; e < E; e += 2) bf16_roundtrip2(lr[e], lr[e + 1]);
       float sc[E], rc[E];
       if constexpr (MODE == kEncode) {
         const float* sp = stab + p * G + E * g;

@@ -94,10 +94,9 @@ __global__ __launch_bounds__(NW * 64) void k_softmax_bwd(
 #pragma unroll
         for (int k = 0; k < G / 32; ++k) unpack8(in[b].d[uu][p][k], dv + 8 * k);
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-          pv[uu][p][e] = bf16_roundtrip(pv[uu][p][e]);
-          part = __builtin_fmaf(pv[uu][p][e], dv[e], part);
-        }
+        for (int e = 0; e < E; e += 2) bf16_roundtrip2(pv[uu][p][e], pv[uu][p][e + 1]);
+#pragma unroll
+        for (int e = 0; e < E; ++e) part = __builtin_fmaf(pv[uu][p][e], dv[e], part);
       }
     // the row's four lanes, then the NW waves (through LDS)
     {
@@ -218,13 +217,15 @@ __global__ __launch_bounds__(NW * 64) void k_softmax_2s(
       reconstruct_plane<BITS, G, R>(cur.cb, cur.qp[p], p, v[p], lop, pv);
 #pragma unroll
       for (int k = 0; k < G / 32; ++k) unpack8(cur.d[p][k], dv + 8 * k);
+#pragma unroll
+      for (int e = 0; e < E; e += 2) bf16_roundtrip2(pv[e], pv[e + 1]);
       if (sweep == 0) {
 #pragma unroll
-        for (int e = 0; e < E; ++e) part = __builtin_fmaf(bf16_roundtrip(pv[e]), dv[e], part);
+        for (int e = 0; e < E; ++e) part = __builtin_fmaf(pv[e], dv[e], part);
       } else {
         float o[E];
 #pragma unroll
-        for (int e = 0; e < E; ++e) o[e] = bf16_roundtrip(pv[e]) * (dv[e] - sum);
+        for (int e = 0; e < E; ++e) o[e] = pv[e] * (dv[e] - sum);
         const int c0 = unit_base(p, u, N, NP, G) + E * g;
 #pragma unroll
         for (int k = 0; k < G / 32; ++k) st16(ds + row * ldds + c0 + 8 * k, pack8(o + 8 * k));
