@@ -113,9 +113,13 @@ __device__ __forceinline__ uint32_t legacy_code_rc(float x, float lr, float sc, 
 //   per plane holds the planes' codes in its low 8 bits;
 // - at 1 bit the code is 1 exactly when bf16(q) >= -0.5, i.e. when q >= -(0.5 + 2^-9) (below
 //   -0.5 the bf16 spacing is 2^-8, and the tie at -0.5 - 2^-9 rounds to the even -0.5): one
-//   compare of the quotient, no rounding.
-// The host check tests/legacy_code_check.c compares both code forms with the reference's over
-// every fp32 quotient but NaN.
+//   compare of the quotient, no rounding;
+// - on the reciprocal path that compare can take the one-multiply estimate a * rc for the
+//   quotient: a and the scale are bf16 values, so a / sc never comes within 2^-17 of
+//   -(0.5 + 2^-9), far beyond the estimate's error, and both compares agree.
+// The host check tests/legacy_code_check.c compares the code forms with the reference's over
+// every fp32 quotient but NaN, and the estimate's compare with the IEEE quotient's over every
+// finite bf16 numerator and every scale the reciprocal path serves.
 constexpr uint32_t kCodeBias = 0x4B400000u;  // bits of 1.5 * 2^23
 template <int BITS>
 __device__ __forceinline__ uint32_t legacy_code_biased(float d) {
@@ -141,6 +145,9 @@ __device__ __forceinline__ uint32_t legacy_code_mfma(float x, float lr, float sc
   const float xr = bf16r(x - lr);
   big = fabsf(xr) > tau;
   o = big ? xr : 0.f;
+  // 1 bit, reciprocal path: an outlier leaves a = 0, whose code is 1; otherwise a = xr, and the
+  // compare of the estimate xr * rc decides as the quotient's does (see above)
+  if constexpr (BITS == 1 && RC) return (big || xr * rc >= kOneBitLow) ? 1u : 0u;
   const float a = xr - o;
   float q;
   if constexpr (RC) {
