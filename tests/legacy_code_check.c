@@ -5,12 +5,13 @@
  *   b = 1:        q >= -(0.5 + 2^-9)  (one compare, no rounding), and
  *   b = 2, 4, 8:  clamp(bits(d + 1.5 * 2^23), B - 2^(b-1), B + 2^(b-1) - 1) - B + 2^(b-1),
  *                 d = bf16(q), B = bits(1.5 * 2^23) (legacy_code_biased);
- * and, at 1 bit, for every finite bf16 numerator a and bf16 scale sc with 2^-100 <= |sc| <= 2^100
- * (the scales the reciprocal path serves), the compare of the one-multiply estimate a * RN32(1/sc)
- * with -(0.5 + 2^-9) equals the compare of the IEEE quotient RN32(a / sc): no such a / sc comes
- * within 2^-17 of the threshold, far more than the estimate's error.
- * Prints the number of quotients checked and of mismatches per bit width, then the number of
- * (a, sc) pairs checked and of mismatches of the 1-bit estimate. */
+ *   b = 2 also:   [q > -(1.5 - 2^-8)] + [q >= -(0.5 + 2^-9)] + [q > 0.5 + 2^-9] (code2_thresholds);
+ * and, at 1 and 2 bits, for every finite bf16 numerator a and bf16 scale sc with
+ * 2^-100 <= |sc| <= 2^100 (the scales the reciprocal path serves), the compares of the
+ * one-multiply estimate a * RN32(1/sc) give the codes of the IEEE quotient RN32(a / sc): no such
+ * a / sc comes within 2^-17 of a threshold, far more than the estimate's error.
+ * Prints the number of quotients checked and of mismatches per bit width (2 bits: both forms),
+ * then the number of (a, sc) pairs checked and of mismatches of the 1- and 2-bit estimates. */
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -40,6 +41,10 @@ static int code_biased(float q, int bits) {
   return v - bias + half;
 }
 
+static int code2_thresholds(float q) {
+  return (q > -(1.5f - 0x1p-8f)) + (q >= -(0.5f + 0x1p-9f)) + (q > 0.5f + 0x1p-9f);
+}
+
 int main(void) {
   long long checked = 0, bad1 = 0, bad2 = 0, bad4 = 0, bad8 = 0;
 #pragma omp parallel for schedule(dynamic, 1) reduction(+ : checked, bad1, bad2, bad4, bad8)
@@ -51,13 +56,13 @@ int main(void) {
       if (isnan(q)) continue;
       ++checked;
       bad1 += code(q, 1) != (q >= -(0.5f + 0x1p-9f) ? 1 : 0);
-      bad2 += code(q, 2) != code_biased(q, 2);
+      bad2 += (code(q, 2) != code_biased(q, 2)) + (code(q, 2) != code2_thresholds(q));
       bad4 += code(q, 4) != code_biased(q, 4);
       bad8 += code(q, 8) != code_biased(q, 8);
     }
   }
-  long long pairs = 0, bad_est = 0;
-#pragma omp parallel for schedule(dynamic, 64) reduction(+ : pairs, bad_est)
+  long long pairs = 0, bad_est = 0, bad_est2 = 0;
+#pragma omp parallel for schedule(dynamic, 64) reduction(+ : pairs, bad_est, bad_est2)
   for (int s = 0; s < 65536; ++s) {
     uint32_t us = (uint32_t)s << 16;
     float sc;
@@ -73,8 +78,9 @@ int main(void) {
       ++pairs;
       const float t = -(0.5f + 0x1p-9f);
       bad_est += (a * rc >= t) != (a / sc >= t);
+      bad_est2 += code2_thresholds(a * rc) != code2_thresholds(a / sc);
     }
   }
-  printf("%lld %lld %lld %lld %lld %lld %lld\n", checked, bad1, bad2, bad4, bad8, pairs, bad_est);
+  printf("%lld %lld %lld %lld %lld %lld %lld %lld\n", checked, bad1, bad2, bad4, bad8, pairs, bad_est, bad_est2);
   return 0;
 }

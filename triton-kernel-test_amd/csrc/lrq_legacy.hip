@@ -114,9 +114,11 @@ __device__ __forceinline__ uint32_t legacy_code_rc(float x, float lr, float sc, 
 // - at 1 bit the code is 1 exactly when bf16(q) >= -0.5, i.e. when q >= -(0.5 + 2^-9) (below
 //   -0.5 the bf16 spacing is 2^-8, and the tie at -0.5 - 2^-9 rounds to the even -0.5): one
 //   compare of the quotient, no rounding;
-// - on the reciprocal path that compare can take the one-multiply estimate a * rc for the
-//   quotient: a and the scale are bf16 values, so a / sc never comes within 2^-17 of
-//   -(0.5 + 2^-9), far beyond the estimate's error, and both compares agree.
+// - at 2 bits the code is [q > -(1.5 - 2^-8)] + [q >= -(0.5 + 2^-9)] + [q > 0.5 + 2^-9] (the
+//   bf16 ties at -1.5 and 0.5 round to the even -1.5 and 0.5, whose rint is -2 and 0);
+// - on the reciprocal path these compares can take the one-multiply estimate a * rc for the
+//   quotient: a and the scale are bf16 values, so a / sc never comes within 2^-17 of a
+//   threshold, far beyond the estimate's error, and the compares agree.
 // The host check tests/legacy_code_check.c compares the code forms with the reference's over
 // every fp32 quotient but NaN, and the estimate's compare with the IEEE quotient's over every
 // finite bf16 numerator and every scale the reciprocal path serves.
@@ -128,26 +130,27 @@ __device__ __forceinline__ uint32_t legacy_code_biased(float d) {
   return (uint32_t)min(max(v, (int)kCodeBias - half), (int)kCodeBias + half - 1);
 }
 constexpr float kOneBitLow = -(0.5f + 0x1p-9f);
+constexpr float kTwoBitLow = -(1.5f - 0x1p-8f), kTwoBitHigh = 0.5f + 0x1p-9f;
 template <int BITS>
 constexpr uint32_t legacy_code_base() {
-  if (BITS == 1) return 0u;  // the 1-bit codes are or-ed in
+  if (BITS <= 2) return 0u;  // the 1- and 2-bit codes come without the bias
   uint32_t k = 0;
   for (int p = 0; p < 8 / BITS; ++p) k += ((1u << (BITS - 1)) - kCodeBias) << (BITS * p);
   return k;
 }
 
-// legacy_code (RC false) or legacy_code_rc (RC true) for the MFMA encode, in the forms above: at 1
-// bit the code itself, at 2, 4 and 8 bits legacy_code_biased of bf16(q), which legacy_accumulate
-// adds to a byte that started from legacy_code_base.
+// legacy_code (RC false) or legacy_code_rc (RC true) of one element for the 1-bit MFMA encode, in
+// the forms above (2, 4 and 8 bits take legacy_code_mfma2, two elements at a time).
 template <int BITS, bool RC>
 __device__ __forceinline__ uint32_t legacy_code_mfma(float x, float lr, float sc, float rc, float tau, float& o,
                                                      bool& big) {
+  static_assert(BITS == 1, "the per-element form serves 1 bit");
   const float xr = bf16r(x - lr);
   big = fabsf(xr) > tau;
   o = big ? xr : 0.f;
   // 1 bit, reciprocal path: an outlier leaves a = 0, whose code is 1; otherwise a = xr, and the
   // compare of the estimate xr * rc decides as the quotient's does (see above)
-  if constexpr (BITS == 1 && RC) return (big || xr * rc >= kOneBitLow) ? 1u : 0u;
+  if constexpr (RC) return (big || xr * rc >= kOneBitLow) ? 1u : 0u;
   const float a = xr - o;
   float q;
   if constexpr (RC) {
@@ -156,17 +159,27 @@ __device__ __forceinline__ uint32_t legacy_code_mfma(float x, float lr, float sc
   } else {
     q = a / sc;  // IEEE division
   }
-  if constexpr (BITS == 1) return q >= kOneBitLow ? 1u : 0u;
-  else return legacy_code_biased<BITS>(bf16r(q));
+  return q >= kOneBitLow ? 1u : 0u;
 }
 // legacy_code_mfma of two elements with one bf16 conversion per rounding step (2, 4, 8 bits;
-// at 1 bit the extra registers of the pairs cost the kernel its second wave per SIMD).
+// at 1 bit the extra registers of the pairs cost the kernel its second wave per SIMD).  The
+// 2-bit codes come without the bias (the three compares on the reciprocal path).
 template <int BITS, bool RC>
 __device__ __forceinline__ void legacy_code_mfma2(const float* x, const float* lr, const float* sc, const float* rc,
                                                   float tau, float* o, bool* big, uint32_t* code) {
   static_assert(BITS > 1, "pairs at 2, 4 and 8 bits");
   float xr[2] = {x[0] - lr[0], x[1] - lr[1]}, q[2];
   bf16_roundtrip2(xr[0], xr[1]);
+  if constexpr (BITS == 2 && RC) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      big[k] = fabsf(xr[k]) > tau;
+      o[k] = big[k] ? xr[k] : 0.f;
+      const float e = (xr[k] - o[k]) * rc[k];  // the estimate of the quotient a / sc
+      code[k] = (e > kTwoBitLow ? 1u : 0u) + (e >= kOneBitLow ? 1u : 0u) + (e > kTwoBitHigh ? 1u : 0u);
+    }
+    return;
+  }
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     big[k] = fabsf(xr[k]) > tau;
@@ -180,8 +193,9 @@ __device__ __forceinline__ void legacy_code_mfma2(const float* x, const float* l
     }
   }
   bf16_roundtrip2(q[0], q[1]);
-  code[0] = legacy_code_biased<BITS>(q[0]);
-  code[1] = legacy_code_biased<BITS>(q[1]);
+  constexpr uint32_t unbias = BITS == 2 ? (1u << (BITS - 1)) - kCodeBias : 0u;  // legacy_code_base
+  code[0] = legacy_code_biased<BITS>(q[0]) + unbias;
+  code[1] = legacy_code_biased<BITS>(q[1]) + unbias;
 }
 template <int BITS>
 __device__ __forceinline__ void legacy_accumulate(uint32_t& byte, uint32_t code, int p) {
