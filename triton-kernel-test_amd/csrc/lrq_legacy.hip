@@ -78,29 +78,12 @@ __device__ __forceinline__ uint32_t legacy_code(float x, float lr, float sc, flo
   return (uint32_t)(int)(c + half);
 }
 
-// legacy_code with the division by the scale taken as q0 = a * rc clamped to +-2^20, then
-// q0 + rc * (a - sc * q0) (both steps fmas), rc = 1/sc rounded once: Markstein's correction of a
-// quotient within an ulp by a correctly rounded reciprocal (for a quotient of bf16 values no
-// fp32 rounding tie exists).  The clamp only touches quotients whose code saturates either way.
-// For scales with 2^-100 <= |sc| <= 2^100 the codes equal legacy_code's for every finite bf16
-// numerator and every bit width: checked exhaustively on the host (3.3e9 pairs) by the
-// repository's legacy division test.  Other scales take legacy_code.
-template <int BITS>
-__device__ __forceinline__ uint32_t legacy_code_rc(float x, float lr, float sc, float rc, float tau, float& o,
-                                                   bool& big) {
-  constexpr float half = (float)(1 << (BITS - 1));
-  const float xr = bf16r(x - lr);
-  big = fabsf(xr) > tau;
-  o = big ? xr : 0.f;
-  const float a = xr - o;
-  const float q0 = __builtin_amdgcn_fmed3f(a * rc, -0x1p20f, 0x1p20f);
-  const float q = __builtin_fmaf(__builtin_fmaf(-sc, q0, a), rc, q0);
-  const float d = bf16r(q);
-  const float c = __builtin_amdgcn_fmed3f(rintf(d), -half, half - 1.f);
-  return (uint32_t)(int)(c + half);
-}
-
-// The MFMA encode's forms of the steps above, with the same results:
+// The MFMA encode's forms of legacy_code, with the same codes:
+// - the quotient: for scales with 2^-100 <= |sc| <= 2^100 (rc_scale_ok) the one-multiply
+//   estimate a * rc, rc = 1/sc rounded once, instead of the IEEE division: its code equals the
+//   IEEE quotient's at every bit width for every finite bf16 numerator a (a and sc are bf16
+//   values, so a / sc never comes near a code boundary within the estimate's error); other
+//   scales take the IEEE division;
 // - bf16_roundtrip2 rounds two values to bf16 with one conversion;
 // - the code of a bf16 quotient d is legacy_code_biased(d) - kCodeBias + half, where
 //   legacy_code_biased(d) = bits(d + 1.5 * 2^23) clamped to [kCodeBias - half, kCodeBias + half - 1]:
@@ -113,15 +96,10 @@ __device__ __forceinline__ uint32_t legacy_code_rc(float x, float lr, float sc, 
 //   per plane holds the planes' codes in its low 8 bits;
 // - at 1 bit the code is 1 exactly when bf16(q) >= -0.5, i.e. when q >= -(0.5 + 2^-9) (below
 //   -0.5 the bf16 spacing is 2^-8, and the tie at -0.5 - 2^-9 rounds to the even -0.5): one
-//   compare of the quotient, no rounding;
-// - at 2 bits the code is [q > -(1.5 - 2^-8)] + [q >= -(0.5 + 2^-9)] + [q > 0.5 + 2^-9] (the
-//   bf16 ties at -1.5 and 0.5 round to the even -1.5 and 0.5, whose rint is -2 and 0);
-// - on the reciprocal path these compares can take the one-multiply estimate a * rc for the
-//   quotient: a and the scale are bf16 values, so a / sc never comes within 2^-17 of a
-//   threshold, far beyond the estimate's error, and the compares agree.
+//   compare of the quotient, no rounding.
 // The host check tests/legacy_code_check.c compares the code forms with the reference's over
-// every fp32 quotient but NaN, and the estimate's compare with the IEEE quotient's over every
-// finite bf16 numerator and every scale the reciprocal path serves.
+// every fp32 quotient but NaN, and the estimate's codes with the IEEE quotient's at 1, 2, 4 and
+// 8 bits over every finite bf16 numerator and every scale the estimate serves.
 constexpr uint32_t kCodeBias = 0x4B400000u;  // bits of 1.5 * 2^23
 template <int BITS>
 __device__ __forceinline__ uint32_t legacy_code_biased(float d) {
@@ -130,17 +108,17 @@ __device__ __forceinline__ uint32_t legacy_code_biased(float d) {
   return (uint32_t)min(max(v, (int)kCodeBias - half), (int)kCodeBias + half - 1);
 }
 constexpr float kOneBitLow = -(0.5f + 0x1p-9f);
-constexpr float kTwoBitLow = -(1.5f - 0x1p-8f), kTwoBitHigh = 0.5f + 0x1p-9f;
 template <int BITS>
 constexpr uint32_t legacy_code_base() {
-  if (BITS <= 2) return 0u;  // the 1- and 2-bit codes come without the bias
+  if (BITS == 1) return 0u;  // the 1-bit codes are or-ed in
   uint32_t k = 0;
   for (int p = 0; p < 8 / BITS; ++p) k += ((1u << (BITS - 1)) - kCodeBias) << (BITS * p);
   return k;
 }
 
-// legacy_code (RC false) or legacy_code_rc (RC true) of one element for the 1-bit MFMA encode, in
-// the forms above (2, 4 and 8 bits take legacy_code_mfma2, two elements at a time).
+// legacy_code of one element for the 1-bit MFMA encode, in the forms above (RC: the estimate of
+// the quotient; 2, 4 and 8 bits take legacy_code_mfma2, two elements at a time).  An outlier
+// leaves a = 0, whose code is 1; otherwise a = xr.
 template <int BITS, bool RC>
 __device__ __forceinline__ uint32_t legacy_code_mfma(float x, float lr, float sc, float rc, float tau, float& o,
                                                      bool& big) {
@@ -148,54 +126,28 @@ __device__ __forceinline__ uint32_t legacy_code_mfma(float x, float lr, float sc
   const float xr = bf16r(x - lr);
   big = fabsf(xr) > tau;
   o = big ? xr : 0.f;
-  // 1 bit, reciprocal path: an outlier leaves a = 0, whose code is 1; otherwise a = xr, and the
-  // compare of the estimate xr * rc decides as the quotient's does (see above)
-  if constexpr (RC) return (big || xr * rc >= kOneBitLow) ? 1u : 0u;
-  const float a = xr - o;
-  float q;
-  if constexpr (RC) {
-    const float q0 = __builtin_amdgcn_fmed3f(a * rc, -0x1p20f, 0x1p20f);
-    q = __builtin_fmaf(__builtin_fmaf(-sc, q0, a), rc, q0);
-  } else {
-    q = a / sc;  // IEEE division
-  }
-  return q >= kOneBitLow ? 1u : 0u;
+  const float q = RC ? xr * rc : xr / sc;  // (IEEE division when !RC)
+  return (big || q >= kOneBitLow) ? 1u : 0u;
 }
 // legacy_code_mfma of two elements with one bf16 conversion per rounding step (2, 4, 8 bits;
-// at 1 bit the extra registers of the pairs cost the kernel its second wave per SIMD).  The
-// 2-bit codes come without the bias (the three compares on the reciprocal path).
+// at 1 bit the extra registers of the pairs cost the kernel its second wave per SIMD); the codes
+// biased (legacy_code_biased).
 template <int BITS, bool RC>
 __device__ __forceinline__ void legacy_code_mfma2(const float* x, const float* lr, const float* sc, const float* rc,
                                                   float tau, float* o, bool* big, uint32_t* code) {
   static_assert(BITS > 1, "pairs at 2, 4 and 8 bits");
   float xr[2] = {x[0] - lr[0], x[1] - lr[1]}, q[2];
   bf16_roundtrip2(xr[0], xr[1]);
-  if constexpr (BITS == 2 && RC) {
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      big[k] = fabsf(xr[k]) > tau;
-      o[k] = big[k] ? xr[k] : 0.f;
-      const float e = (xr[k] - o[k]) * rc[k];  // the estimate of the quotient a / sc
-      code[k] = (e > kTwoBitLow ? 1u : 0u) + (e >= kOneBitLow ? 1u : 0u) + (e > kTwoBitHigh ? 1u : 0u);
-    }
-    return;
-  }
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     big[k] = fabsf(xr[k]) > tau;
     o[k] = big[k] ? xr[k] : 0.f;
     const float a = xr[k] - o[k];
-    if constexpr (RC) {
-      const float q0 = __builtin_amdgcn_fmed3f(a * rc[k], -0x1p20f, 0x1p20f);
-      q[k] = __builtin_fmaf(__builtin_fmaf(-sc[k], q0, a), rc[k], q0);
-    } else {
-      q[k] = a / sc[k];  // IEEE division
-    }
+    q[k] = RC ? a * rc[k] : a / sc[k];  // (IEEE division when !RC)
   }
   bf16_roundtrip2(q[0], q[1]);
-  constexpr uint32_t unbias = BITS == 2 ? (1u << (BITS - 1)) - kCodeBias : 0u;  // legacy_code_base
-  code[0] = legacy_code_biased<BITS>(q[0]) + unbias;
-  code[1] = legacy_code_biased<BITS>(q[1]) + unbias;
+  code[0] = legacy_code_biased<BITS>(q[0]);
+  code[1] = legacy_code_biased<BITS>(q[1]);
 }
 template <int BITS>
 __device__ __forceinline__ void legacy_accumulate(uint32_t& byte, uint32_t code, int p) {
@@ -212,7 +164,7 @@ __device__ __forceinline__ uint32_t bf16_at(const u32x4& w0, const u32x4& w1, ui
   return (d >> (16u * (i & 1u))) & 0xffffu;
 }
 
-// Scales that legacy_code_rc serves exactly (NaN fails the test).
+// Scales whose reciprocal estimate gives legacy_code's codes (NaN fails the test).
 __device__ __forceinline__ bool rc_scale_ok(float sc) {
   const float m = fabsf(sc);
   return m >= 0x1p-100f && m <= 0x1p100f;
@@ -369,7 +321,7 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
 
   // the unit's scales in LDS for every row block of the workgroup (the same columns throughout),
   // and for the encode their reciprocals (one IEEE division per column); rc_ok: every scale is
-  // one legacy_code_rc serves exactly
+  // the reciprocal estimate serves exactly
   constexpr bool kScales = MODE != kAdd && MODE != kHist;
   __shared__ __attribute__((aligned(16))) float stab[MODE == kEncode ? 2 * NP * G : (kScales ? NP * G : 4)];
   bool rc_ok = false;
