@@ -153,26 +153,47 @@ __global__ __launch_bounds__(kCooThreads) void k_coo_count(const uint16_t* __res
 
 // The chunk totals of staged records (the legacy encode's, lrq_coo.h): per chunk, the sum of its
 // pieces' counts, and of its first kChunk / 2 pieces' (half_total), into the workspace; 8 bytes
-// read per piece.
-__global__ __launch_bounds__(kCooThreads) void k_coo_totals(const int64_t* __restrict__ piece_ptr, int64_t npieces,
-                                                            uint32_t* __restrict__ chunk_total,
-                                                            uint32_t* __restrict__ half_total) {
-  __shared__ uint32_t wsum[kCooThreads / 64];
-  const int t = threadIdx.x;
-  const int64_t pc0 = (int64_t)blockIdx.x * kChunk;
-  constexpr int PPT = kChunk / kCooThreads;
-  static_assert(PPT % 2 == 0, "iterations 0 .. PPT/2 - 1 cover the first half");
-  uint32_t s[2] = {0u, 0u};
+// read per piece.  A workgroup of kTotalsThreads per chunk, thread t summing pieces
+// t + kTotalsThreads i, i < 16 (16 coalesced loads in flight), so that several chunks'
+// workgroups share a CU.
+constexpr int kTotalsThreads = 256;
+__global__ __launch_bounds__(kTotalsThreads) void k_coo_totals(const int64_t* __restrict__ piece_ptr, int64_t npieces,
+                                                               uint32_t* __restrict__ chunk_total,
+                                                               uint32_t* __restrict__ half_total) {
+  constexpr int PPT = kChunk / kTotalsThreads, NW = kTotalsThreads / 64;
+  static_assert(PPT % 2 == 0, "whole iterations per half");
+  __shared__ uint32_t wsum[2][NW];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t pc0 = (int64_t)blockIdx.x * kChunk + t;
+  uint32_t d0[PPT];
+#pragma unroll
+  for (int i = 0; i < PPT; ++i)  // clamped: loaded, not counted
+    d0[i] = (uint32_t)piece_ptr[min(pc0 + (int64_t)kTotalsThreads * i, npieces - 1)];
+  // the first half is iterations 0 .. PPT / 2 - 1
+  uint32_t s = 0, f = 0;
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
-    const int64_t pc = pc0 + i * kCooThreads + t;
-    const uint32_t d0 = (uint32_t)piece_ptr[min(pc, npieces - 1)];  // clamped: loaded, not counted
-    s[2 * i / PPT] += pc < npieces ? coo_record_count(d0) : 0u;
+    const uint32_t c = pc0 + (int64_t)kTotalsThreads * i < npieces ? coo_record_count(d0[i]) : 0u;
+    s += c;
+    f += i < PPT / 2 ? c : 0u;
   }
-  uint32_t total, first;
-  coo_block_scan(s[0] + s[1], wsum, total);
-  coo_block_scan(s[0], wsum, first);
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    s += __shfl_xor(s, d);
+    f += __shfl_xor(f, d);
+  }
+  if (lane == 0) {
+    wsum[0][w] = s;
+    wsum[1][w] = f;
+  }
+  __syncthreads();
   if (t == 0) {
+    uint32_t total = 0, first = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      total += wsum[0][i];
+      first += wsum[1][i];
+    }
     chunk_total[blockIdx.x] = total;
     half_total[blockIdx.x] = first;
   }
@@ -586,7 +607,7 @@ int lrq::coo_compact_staged(const void* o, int64_t B, int64_t M, int64_t N, int6
   uint64_t* chunk_off = reinterpret_cast<uint64_t*>(workspace);
   uint32_t* chunk_total = reinterpret_cast<uint32_t*>(chunk_off + p.nchunks);
   uint32_t* half_total = chunk_total + p.nchunks;  // the workspace's last nchunks * 4 bytes
-  LRQ_TRY(launch(k_coo_totals, dim3((unsigned)p.nchunks), dim3(kCooThreads), 0, s, piece_ptr, p.npieces,
+  LRQ_TRY(launch(k_coo_totals, dim3((unsigned)p.nchunks), dim3(kTotalsThreads), 0, s, piece_ptr, p.npieces,
                  chunk_total, half_total));
   const bool inline_scan = p.nchunks <= kScanInline;
   if (!inline_scan)
