@@ -116,28 +116,25 @@ constexpr uint32_t legacy_code_base() {
   return k;
 }
 
-// legacy_code of one element for the 1-bit MFMA encode, in the forms above (RC: the estimate of
-// the quotient; 2, 4 and 8 bits take legacy_code_mfma2, two elements at a time).  An outlier
-// leaves a = 0, whose code is 1; otherwise a = xr.
-template <int BITS, bool RC>
-__device__ __forceinline__ uint32_t legacy_code_mfma(float x, float lr, float sc, float rc, float tau, float& o,
-                                                     bool& big) {
-  static_assert(BITS == 1, "the per-element form serves 1 bit");
-  const float xr = bf16r(x - lr);
-  big = fabsf(xr) > tau;
-  o = big ? xr : 0.f;
-  const float q = RC ? xr * rc : xr / sc;  // (IEEE division when !RC)
-  return (big || q >= kOneBitLow) ? 1u : 0u;
-}
-// legacy_code_mfma of two elements with one bf16 conversion per rounding step (2, 4, 8 bits;
-// at 1 bit the extra registers of the pairs cost the kernel its second wave per SIMD); the codes
-// biased (legacy_code_biased).
+// legacy_code of two elements for the MFMA encode, in the forms above (RC: the estimate of the
+// quotient, else the IEEE division), with one bf16 conversion per rounding step of the pair: at
+// 1 bit the code itself (an outlier leaves a = 0, whose code is 1; otherwise a = xr), at 2, 4
+// and 8 bits biased (legacy_code_biased).
 template <int BITS, bool RC>
 __device__ __forceinline__ void legacy_code_mfma2(const float* x, const float* lr, const float* sc, const float* rc,
                                                   float tau, float* o, bool* big, uint32_t* code) {
-  static_assert(BITS > 1, "pairs at 2, 4 and 8 bits");
   float xr[2] = {x[0] - lr[0], x[1] - lr[1]}, q[2];
   bf16_roundtrip2(xr[0], xr[1]);
+  if constexpr (BITS == 1) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      big[k] = fabsf(xr[k]) > tau;
+      o[k] = big[k] ? xr[k] : 0.f;
+      const float qk = RC ? xr[k] * rc[k] : xr[k] / sc[k];  // (IEEE division when !RC)
+      code[k] = (big[k] || qk >= kOneBitLow) ? 1u : 0u;
+    }
+    return;
+  }
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     big[k] = fabsf(xr[k]) > tau;
@@ -478,46 +475,28 @@ __global__ __launch_bounds__(256) void k_legacy_mfma(LegacyArgs a) {
           unpack8(ld16(xp + 8), xv + 8);
         }
         if constexpr (MODE == kEncode) {
-          // legacy_code(_rc) of each element in the forms above (legacy_code_mfma)
+          // legacy_code of each element in the forms above, two at a time (legacy_code_mfma2)
           float ov[E];
           uint32_t hm = 0;  // bit e: element e is an outlier entry
-          if constexpr (BITS == 1) {
-            if (rc_ok) {  // workgroup-uniform
+          if (rc_ok) {  // workgroup-uniform
 #pragma unroll
-              for (int e = 0; e < E; ++e) {
-                bool hit;
-                legacy_accumulate<BITS>(byte[e], legacy_code_mfma<BITS, true>(xv[e], lr[e], sc[e], rc[e], a.tau, ov[e], hit), p);
-                hm |= hit ? 1u << e : 0u;
-              }
-            } else {
-#pragma unroll
-              for (int e = 0; e < E; ++e) {
-                bool hit;
-                legacy_accumulate<BITS>(byte[e], legacy_code_mfma<BITS, false>(xv[e], lr[e], sc[e], 0.f, a.tau, ov[e], hit), p);
-                hm |= hit ? 1u << e : 0u;
-              }
+            for (int e = 0; e < E; e += 2) {
+              bool hit[2];
+              uint32_t cd[2];
+              legacy_code_mfma2<BITS, true>(xv + e, lr + e, sc + e, rc + e, a.tau, ov + e, hit, cd);
+              legacy_accumulate<BITS>(byte[e], cd[0], p);
+              legacy_accumulate<BITS>(byte[e + 1], cd[1], p);
+              hm |= (hit[0] ? 1u << e : 0u) | (hit[1] ? 2u << e : 0u);
             }
           } else {
-            if (rc_ok) {  // workgroup-uniform
 #pragma unroll
-              for (int e = 0; e < E; e += 2) {
-                bool hit[2];
-                uint32_t cd[2];
-                legacy_code_mfma2<BITS, true>(xv + e, lr + e, sc + e, rc + e, a.tau, ov + e, hit, cd);
-                legacy_accumulate<BITS>(byte[e], cd[0], p);
-                legacy_accumulate<BITS>(byte[e + 1], cd[1], p);
-                hm |= (hit[0] ? 1u << e : 0u) | (hit[1] ? 2u << e : 0u);
-              }
-            } else {
-#pragma unroll
-              for (int e = 0; e < E; e += 2) {
-                bool hit[2];
-                uint32_t cd[2];
-                legacy_code_mfma2<BITS, false>(xv + e, lr + e, sc + e, rc + e, a.tau, ov + e, hit, cd);
-                legacy_accumulate<BITS>(byte[e], cd[0], p);
-                legacy_accumulate<BITS>(byte[e + 1], cd[1], p);
-                hm |= (hit[0] ? 1u << e : 0u) | (hit[1] ? 2u << e : 0u);
-              }
+            for (int e = 0; e < E; e += 2) {
+              bool hit[2];
+              uint32_t cd[2];
+              legacy_code_mfma2<BITS, false>(xv + e, lr + e, sc + e, rc + e, a.tau, ov + e, hit, cd);
+              legacy_accumulate<BITS>(byte[e], cd[0], p);
+              legacy_accumulate<BITS>(byte[e + 1], cd[1], p);
+              hm |= (hit[0] ? 1u << e : 0u) | (hit[1] ? 2u << e : 0u);
             }
           }
           const u32x4 ow0 = pack8(ov), ow1 = pack8(ov + 8);
