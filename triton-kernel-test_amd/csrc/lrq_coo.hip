@@ -23,8 +23,9 @@
 //
 // After the legacy encode, which stages each piece's count and first entries as a record in
 // piece_ptr (lrq_coo.h), the compaction is k_coo_totals (the chunk totals from the records) and
-// k_coo_scatter_staged (the chunk scan; the entries from the records, and from the dense values
-// only for pieces with more entries than a record holds).
+// k_coo_scatter_staged (the chunk scan, or k_coo_scan before it above kScanInline chunks; the
+// entries from the records, and from the dense values only for pieces with more entries than a
+// record holds).
 #include "lrq_common.h"
 #include "lrq_coo.h"
 #include "lrq_host.h"
@@ -34,7 +35,7 @@ namespace lrq {
 constexpr int kPiece = 64;
 constexpr int kChunk = 4096;  // pieces per chunk
 constexpr int kCooThreads = 1024;
-constexpr int kStage = 8 * kPiece;  // entries one wave's 8 pieces can hold
+constexpr int kStage = 8 * kPiece;  // entries a wave gathers in LDS (k_coo_scatter: its 8 pieces' worst case)
 constexpr int kScanInline = 4096;   // chunks up to which the staged scatter sums the chunk totals itself
 constexpr int kScatterThreads = 512;  // the staged scatter's workgroup (half a chunk)
 
@@ -352,7 +353,7 @@ __global__ __launch_bounds__(kScatterThreads) void k_coo_scatter_staged(
   __shared__ uint32_t wsum[NW];
   __shared__ uint64_t csum[NW];
   __shared__ u32x2 more_desc[NW][64 * PPT];  // per wave: (first entry, piece) of each such piece
-  __shared__ u32x2 stage[NW][kStage];         // per wave: (piece | column << 16, bf16 bits)
+  __shared__ u32x2 stage[NW][kStage];         // per wave: (column, row offset | bf16 bits << 16)
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int64_t chunk = blockIdx.x >> 1;
   const int part = blockIdx.x & 1;
